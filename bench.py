@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode matmul path on one MI355X.
+
+Headline (default): batch-1 Q4_0 GEMV over every linear layer of Llama-3-8B
+decode - 32 layers x {q, k, v, o, gate, up, down}, K x N = 4096x4096,
+4096x1024 (k, v), 4096x14336 (gate, up), 14336x4096 (down) - with 32
+distinct weight copies resident in HBM (3.9 GB, 15x the 256 MB Infinity
+Cache, so every weight byte comes from HBM).  One step = one decode token
+through all 224 GEMVs, replayed as a HIP graph.  value = algorithmic bytes
+(weights + scales + x + y) / step time, in GB/s.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (Q4_0 GEMV at 14336 x 4096, the gate/up
+                shape) timed with HIP events around graph replays of
+                back-to-back launches over rotating weight copies;
+  cpu_baseline  the C restatement of the reference CPU engine's Q4_0 GEMV
+                (GemmF32Q4NT, internal/xblas/gemm_quant.go:81-157) on the
+                host cores, over one layer's seven matrices.
+
+`python bench.py --suite` instead prints one line per benchmark
+configuration (W4A16, Q4_0, Q8_0, ternary, IQ4_NL) with us per matmul and
+effective GB/s; those are supporting numbers, not the headline line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "quant GEMV effective HBM GB/s (% of peak) at Llama-3-8B decode shapes, batch 1"
+PEAK_GBS = 8000.0
+LLAMA3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+             ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]  # (name, rows=N_out, K)
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------ device setup
+
+class Q4Matrix:
+    """One Q4_0 weight matrix uploaded in the RawBytesGPU layout."""
+
+    def __init__(self, torch, lib, rows: int, K: int, seed: int, copies: int):
+        from ztensor_amd import synth
+
+        self.rows, self.K = rows, K
+        w = synth.q4_0(rows, K, seed)
+        self.raw = w.raw
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_q4_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+        base = torch.from_numpy(host).cuda()
+        self.copies = [base] + [base.clone() for _ in range(copies - 1)]
+        self.off = lib.zt_q4_gpu_data_offset(nblk)
+        self.x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
+        self.y = [torch.empty(rows, dtype=torch.float32, device="cuda") for _ in range(copies)]
+        from ztensor_amd.synth import algorithmic_bytes
+
+        self.bytes = algorithmic_bytes("q4_0", rows, K)
+
+    def launch(self, lib, i: int, stream: int) -> None:
+        rc = lib.zt_gemm_q4_f32(self.copies[i].data_ptr(), self.x.data_ptr(), self.y[i].data_ptr(), self.rows,
+                                self.K, 1, self.off, stream)
+        if rc != 0:
+            raise RuntimeError(f"zt_gemm_q4_f32 returned {rc}")
+
+
+def graph_of(torch, fn):
+    """Captures fn() (which launches on torch's current stream) into a graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up launch outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps: int) -> float:
+    """Average ms per replay, HIP events on the replay stream."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+# ------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(mats, budget_s: float = 12.0) -> dict:
+    from oracle import oracle
+
+    threads = min(16, oracle.nthreads())
+    total_bytes, t_total, reps = 0, 0.0, 0
+    xs = {m.K: m.x.cpu().numpy() for m in mats}
+    while t_total < budget_s and reps < 50:
+        for m in mats:
+            t0 = time.perf_counter()
+            oracle.gemm_f32_q4_nt(xs[m.K], m.raw, 1, m.rows, m.K, threads=threads)
+            t_total += time.perf_counter() - t0
+            total_bytes += m.bytes
+        reps += 1
+    try:
+        cpu = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu = "unknown"
+    return {
+        "value": round(total_bytes / t_total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} passes over one Llama-3-8B layer's 7 Q4_0 GEMVs (batch 1) with the C restatement of "
+                  f"GemmF32Q4NT (scalar q4DotRow, N split over min(threads, N/4) workers); {t_total:.1f} s on {cpu}",
+    }
+
+
+# ------------------------------------------------------------ headline run
+
+def run_headline(args) -> dict:
+    import torch
+
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    layers = args.layers
+    log(f"bench: generating Llama-3-8B Q4_0 weights, {layers} layer copies")
+    mats = [Q4Matrix(torch, lib, rows, K, 0x5EED0020 + i, layers) for i, (_, rows, K) in enumerate(LLAMA3_8B)]
+    step_bytes = layers * sum(m.bytes for m in mats)
+    resident = layers * sum(m.copies[0].numel() for m in mats)
+    log(f"bench: {resident / 1e9:.2f} GB of weights resident; {step_bytes / 1e6:.1f} MB per step")
+
+    def step():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            for m in mats:
+                m.launch(lib, layer, s)
+
+    g = graph_of(torch, step)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = time_graph(torch, g, args.steps)
+    wall = time.perf_counter() - t0
+    value = step_bytes / (ms * 1e-3) / 1e9
+    log(f"bench: {ms * 1e3:.1f} us/step, {value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}% of peak), wall {wall:.2f}s")
+
+    # Per-shape and dominant-kernel timings: graphs of back-to-back launches
+    # rotating over the layer copies.
+    per_shape = {}
+    dom = None
+    for (name, rows, K), m in zip(LLAMA3_8B, mats):
+        if name in ("k", "up"):
+            continue  # same shapes as v / gate
+        n = 4 * layers
+
+        def loop(m=m, n=n):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                m.launch(lib, i % layers, s)
+
+        gl = graph_of(torch, loop)
+        gl.replay()
+        us = time_graph(torch, gl, max(3, args.steps // 20)) * 1e3 / n
+        gbs = m.bytes / (us * 1e-6) / 1e9
+        per_shape[f"{name} {K}x{rows}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                           "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": m.bytes}
+        if name == "gate":
+            dom = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                   "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                   "kernel": "gemv_blk18_kernel<Q4_0> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
+                   "bytes_per_launch": m.bytes, "us_per_launch": round(us, 3)}
+        log(f"bench: {name:5s} K={K:5d} N={rows:5d}: {us:7.2f} us  {gbs:7.1f} GB/s")
+
+    # Parity spot check of the last replayed outputs against the oracle.
+    from oracle import oracle
+
+    m = mats[0]
+    ref = oracle.gemm_f32_q4_nt(m.x.cpu().numpy(), m.raw, 1, m.rows, m.K, threads=8)
+    err = float(np.max(np.abs(m.y[0].cpu().numpy() - ref)) / np.max(np.abs(ref)))
+    if err > 1e-3:
+        raise SystemExit(f"bench: parity check failed (rel err {err:.2e})")
+
+    cpu = cpu_baseline(mats[:7]) if args.cpu_baseline else None
+    return {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_0 nibbles U[0,15], fp16 scales |N(0,1)|*0.02, fp32 x ~ N(0,1))",
+        "config": {
+            "workload": f"Llama-3-8B decode, {layers} layers x {{q,k,v,o,gate,up,down}} Q4_0 GEMV, batch 1, "
+                        "weights resident in HBM (distinct copy per layer)",
+            "format": "Q4_0 (RawBytesGPU layout)",
+            "batch": 1,
+            "layers": layers,
+            "shapes_KxN": [f"{K}x{rows}" for _, rows, K in LLAMA3_8B],
+            "bytes_per_step": step_bytes,
+            "pct_of_peak": round(100 * value / PEAK_GBS, 1),
+            "parity_rel_err": err,
+        },
+        "per_shape": per_shape,
+        "roofline": dom,
+        "cpu_baseline": cpu,
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build "
+              "(see the sharding note in DESIGN.md)", file=sys.stderr)
+        raise SystemExit(2)
+    if args.suite:
+        from ztensor_amd import bench_suite
+
+        bench_suite.run(args)
+        return
+    print(json.dumps(run_headline(args)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

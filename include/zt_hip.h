@@ -1,0 +1,155 @@
+/*
+ * zt_hip.h -- C ABI of libzt_hip.so, the MI355X (gfx950) quantized-weight
+ * GEMV / small-batch GEMM library for ztensor's decode matmul path.
+ *
+ * Every entry point takes plain pointers and integers (floats only by device
+ * pointer), allocates nothing, launches asynchronously on `stream` and
+ * returns a hipError_t as int: 0 on success, 1 (hipErrorInvalidValue) for a
+ * shape, alignment or null-pointer violation (nothing is launched then), or
+ * the launch error.  This is the contract of the reference's CUDA launchers
+ * (internal/cuda/kernels/gemm_q4.cu:163-201) and of the purego layer that
+ * calls them (internal/cuda/kernels/gemm_q4_purego.go:15-28: integer /
+ * pointer arguments only, nonzero -> Go error -> CPU fallback).
+ *
+ * Matrix convention (the one GemmQ4F32 / GemmQ8F32 use,
+ * internal/gpuapi/kernels.go:45-48,79-81): C[M,N] = dequant(A)[M,K] * B[K,N],
+ * A is the weight with M output rows and blocks/groups along K, B is the
+ * activation with element (k,n) at B[k*N+n], C is fp32 with element (m,n) at
+ * C[m*N+n].  N is the batch (1 for decode GEMV).
+ *
+ * Device layouts (built once at upload, see the zt_*_raw_to_gpu helpers):
+ *   Q4_0 / IQ4_NL: [scales nblk*2 B][pad to 16][data nblk*16 B]
+ *                  (tensor/quantized.go:158-198 RawBytesGPU)
+ *   Q8_0 raw:      36-byte blocks [fp32 scale][32 x int8] (tensor/quantized.go:425-438)
+ *   Q8_0 sep:      [scales nblk*4 B][pad to 16][data nblk*32 B]
+ *   W4 (GPTQ/AWQ): packed nibbles [M, K/2] + fp16 scales/zeros [M, K/group]
+ *                  (tensor/quantized_gptq.go:217-277, tensor/quantized_awq.go:23-39)
+ *   Ternary:       row-aligned 2-bit codes [M, ceil(K/4)]
+ *                  (compute/ternary_gemv_gpu.go:52-67)
+ */
+#ifndef ZT_HIP_H
+#define ZT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* zt_stream_t; /* == hipStream_t; NULL = default stream */
+
+/* ---- library ---------------------------------------------------------- */
+
+/* ABI version of this header (major*100 + minor). */
+int zt_abi_version(void);
+
+/* ---- Q4_0 -------------------------------------------------------------- */
+
+/* Replaces gemm_q4_f32 (internal/cuda/kernels/gemm_q4.cu:163-201) behind
+ * KernelRunner.GemmQ4F32 (internal/gpuapi/kernels.go:45-48), whose ROCm
+ * implementation is a "not implemented" stub
+ * (internal/gpuapi/rocm_kernels.go:109-111).  A_q4 is the RawBytesGPU
+ * layout, data_offset = Q4GPUDataOffset(M*K/32) (tensor/quantized.go:195-198).
+ * K % 32 != 0 -> InvalidValue (gemm_q4.cu:169-171).  fp32 activations. */
+int zt_gemm_q4_f32(const void* A_q4, const float* B, float* C, int M, int K, int N, int data_offset,
+                   zt_stream_t stream);
+
+/* Q4_0 weights x fp16 activations (the Q4Storage case of
+ * compute.detectW4A16, compute/w4a16.go:50-54), fp32 output. */
+int zt_gemm_q4_f16(const void* A_q4, const uint16_t* B, float* C, int M, int K, int N, int data_offset,
+                   zt_stream_t stream);
+
+/* Device dequantizer, bit-exact with Q4Storage.Dequantize
+ * (tensor/quantized.go:96-114) over the RawBytesGPU layout. */
+int zt_dequant_q4_f32(const void* A_q4, float* out, long nelem, int data_offset, zt_stream_t stream);
+
+/* Host: RawBytes (18-byte blocks, tensor/quantized.go:146-156) ->
+ * RawBytesGPU (tensor/quantized.go:158-187).  out holds
+ * zt_q4_gpu_bytes(nblk) bytes. */
+long zt_q4_gpu_data_offset(long nblk); /* tensor/quantized.go:195-198 */
+long zt_q4_gpu_bytes(long nblk);
+void zt_q4_raw_to_gpu(const void* raw, long nblk, void* out);
+
+/* ---- IQ4_NL ------------------------------------------------------------ */
+
+/* IQ4_NL GEMV/GEMM.  The reference has no IQ4_NL kernel or upload path
+ * (IQ4NLStorage is only dequantized, tensor/iq4_storage.go:74-95, and
+ * CPUEngine.MatMul falls back to Data() + SGEMM); the device layout is the
+ * Q4_0 RawBytesGPU layout applied to IQ4_NL's 18-byte blocks
+ * (tensor/iq4_storage.go:12-23).  Decode follows DequantizeIQ4NL
+ * (tensor/iq4_storage.go:36-46): interleaved nibbles, float IQ4NLTable. */
+int zt_gemm_iq4nl_f32(const void* A_iq4, const float* B, float* C, int M, int K, int N, int data_offset,
+                      zt_stream_t stream);
+int zt_gemm_iq4nl_f16(const void* A_iq4, const uint16_t* B, float* C, int M, int K, int N, int data_offset,
+                      zt_stream_t stream);
+/* Bit-exact with IQ4NLStorage.Dequantize (tensor/iq4_storage.go:75-89). */
+int zt_dequant_iq4nl_f32(const void* A_iq4, float* out, long nelem, int data_offset, zt_stream_t stream);
+/* Host: IQ4NLStorage.RawBytes (tensor/iq4_storage.go:104) -> separated layout. */
+void zt_iq4nl_raw_to_gpu(const void* raw, long nblk, void* out);
+
+/* ---- Q8_0 -------------------------------------------------------------- */
+
+/* Replaces gemm_q8_f32 (internal/cuda/kernels/gemm_q8.cu:156-182) behind
+ * KernelRunner.GemmQ8F32 (internal/gpuapi/kernels.go:79-81; ROCm stub
+ * internal/gpuapi/rocm_kernels.go:133-135).  A_q8 is Q8Storage.RawBytes()
+ * (36-byte blocks, fp32 scale), 4-byte aligned. */
+int zt_gemm_q8_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, zt_stream_t stream);
+
+/* Same product over the separated Q8_0 layout (aligned 32-byte payloads;
+ * the Q8 counterpart of Q4's RawBytesGPU).  data_offset =
+ * zt_q8_gpu_data_offset(M*K/32). */
+int zt_gemm_q8sep_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, long data_offset,
+                      zt_stream_t stream);
+/* Bit-exact with Q8Storage.Dequantize (tensor/quantized.go:344-355). */
+int zt_dequant_q8_f32(const void* A_q8, float* out, long nelem, zt_stream_t stream);
+int zt_dequant_q8sep_f32(const void* A_q8, float* out, long nelem, long data_offset, zt_stream_t stream);
+/* Raw 36-byte blocks -> separated layout, on the device (raw 4-byte
+ * aligned, out 16-byte aligned and zt_q8_gpu_bytes(nblk) long) or host. */
+int zt_q8_repack(const void* raw, void* out, long nblk, zt_stream_t stream);
+long zt_q8_gpu_data_offset(long nblk);
+long zt_q8_gpu_bytes(long nblk);
+void zt_q8_raw_to_gpu(const void* raw, long nblk, void* out);
+
+/* ---- W4A16 (GPTQ / AWQ 4-bit, fp16 activations) ----------------------- */
+
+/* Backs W4A16MatMuler.MatMulW4A16 (compute/w4a16.go:137-143), which no
+ * reference engine implements; the CPU fallback it replaces is
+ * MatMulW4A16 (compute/w4a16.go:71-119: dequantize + fp32 GEMM, fp32
+ * result).  W_packed: [M, K/2] nibbles (GPTQ bits=4 / AWQ byte order),
+ * 16-byte aligned; scales, zeros: fp16 [M, K/group_size] (zeros NULL ->
+ * zero-point 8); B: fp16 [K, N]; C: fp32 [M, N].  group_size % 32 == 0 and
+ * K % group_size == 0, else InvalidValue. */
+int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, const uint16_t* B,
+                      float* C, int M, int K, int N, int group_size, zt_stream_t stream);
+/* Bit-exact with GPTQStorage.Dequantize (tensor/quantized_gptq.go:134-163)
+ * and AWQStorage.Dequantize (tensor/quantized_awq.go:118-136). */
+int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,
+                      int group_size, zt_stream_t stream);
+
+/* ---- Ternary ----------------------------------------------------------- */
+
+/* Replaces ternary_gemv_f32 (internal/cuda/kernels/ternary_gemv.cu:85-99),
+ * the device half of TernaryGEMVGPU (compute/ternary_gemv_gpu.go:18-91):
+ * y[M] = W[M,K] x[K], W row-aligned 2-bit codes, fp32 x and y. */
+int zt_ternary_gemv_f32(const void* W_ternary, const float* x, float* y, int M, int K, zt_stream_t stream);
+
+/* BitNet decode variant: int8 activations with a per-token fp32 scale and
+ * one per-tensor fp32 weight scale, both by device pointer:
+ *   y = float(sum_j w_j q_j) * (w_scale * x_scale).
+ * No reference counterpart (TernaryGEMV takes fp32 x, TernaryStorage has no
+ * scale: compute/ternary_gemv.go:12, tensor/ternary_storage.go:7-10); the
+ * result equals TernaryGEMV(W, float(q)) * (w_scale * x_scale) bit for bit. */
+int zt_ternary_gemv_i8(const void* W_ternary, const int8_t* x_q, const float* x_scale, const float* w_scale,
+                       float* y, int M, int K, zt_stream_t stream);
+/* Codes -> fp32 {-1,0,+1} (TernaryStorage.Get, tensor/ternary_storage.go:39-47). */
+int zt_dequant_ternary_f32(const void* W_ternary, float* out, int M, int K, zt_stream_t stream);
+/* Host: flat TernaryStorage.RawBytes (tensor/ternary_storage.go:91-92) ->
+ * row-aligned layout, the repack of compute/ternary_gemv_gpu.go:55-67.
+ * out holds M*ceil(K/4) bytes. */
+void zt_ternary_repack_rows(const void* raw, long M, long K, void* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZT_HIP_H */

@@ -1,0 +1,484 @@
+/*
+ * zt_oracle.c -- CPU restatement of zerfoo/ztensor's quantized-weight
+ * dequantizers and CPU GEMV/GEMM loops (the decode matmul path).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker and the
+ * CPU baseline of bench.py; it is never linked into, loaded by or called
+ * from the product library (libzt_hip.so) or the ztensor_amd package.
+ *
+ * Every function follows one reference function; the citation is given as
+ * path:line relative to the reference repository root.  Loop order, the
+ * position of each rounding and the skip conditions are kept as the
+ * reference has them, so results are bit-identical to the reference where
+ * the reference's arithmetic is deterministic.  The file is compiled with
+ * -ffp-contract=off because the reference is Go on amd64 (GOAMD64=v1), which
+ * does not fuse x*y+z into an FMA in the scalar loops, while its AVX2 axpy
+ * (gemm_simd_amd64.s) does use VFMADD231PS; orc_sgemm_simd reproduces that
+ * by calling fmaf explicitly on the vector part and mul-then-add on the
+ * scalar tail.
+ *
+ * Pinning (what checks each function besides restating it) is documented in
+ * tests/test_oracle.py next to each test.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ fp16 */
+
+/* IEEE binary16 -> binary32 widening (exact).  Stands for
+ * github.com/zerfoo/float16 v0.2.0 Float16.ToFloat32, which the reference
+ * calls at tensor/quantized.go:99, tensor/iq4_storage.go:37,
+ * tensor/quantized_gptq.go:136-137, tensor/fp16_storage.go:60. */
+EXPORT float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t frac = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (frac == 0) {
+            bits = sign;
+        } else { /* subnormal: normalise */
+            int e = -1;
+            do { frac <<= 1; e++; } while ((frac & 0x400) == 0);
+            frac &= 0x3ff;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (frac << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (frac << 13);
+    } else {
+        bits = sign | ((exp - 15 + 127) << 23) | (frac << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* internal/xblas/q4dot.go:53-78 float16BitsToFloat32: same as IEEE for
+ * finite values, but Inf/NaN map to 0 and subnormals are computed as
+ * (frac/1024) * 2^-14 in two fp32 steps. */
+EXPORT float orc_f16_bits_to_f32_xblas(uint16_t bits) {
+    uint32_t sign = (bits >> 15) & 1;
+    uint32_t exp = (bits >> 10) & 0x1f;
+    uint32_t frac = bits & 0x3ff;
+    if (exp == 0) {
+        if (frac == 0) return 0.0f;
+        float f = (float)frac / 1024.0f;
+        f *= 1.0f / 16384.0f;
+        return sign ? -f : f;
+    }
+    if (exp == 31) return 0.0f;
+    uint32_t b32 = (sign << 31) | ((exp - 15 + 127) << 23) | (frac << 13);
+    float f;
+    memcpy(&f, &b32, 4);
+    return f;
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline uint32_t rd32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* ------------------------------------------------------------------ Q4_0 */
+
+/* tensor/quantized.go:96-114 Q4Storage.Dequantize over the RawBytes layout
+ * (tensor/quantized.go:148-156): 18-byte blocks, fp16 scale LE then 16
+ * bytes; low nibble -> element j, high nibble -> element j+16. */
+EXPORT void orc_q4_dequant(const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 31) / 32;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        const uint8_t* b = raw + bi * 18;
+        float scale = orc_f16_to_f32(rd16(b));
+        int64_t off = bi * 32;
+        for (int j = 0; j < 16; j++) {
+            uint8_t packed = b[2 + j];
+            int q0 = (int)(packed & 0x0f) - 8;
+            int q1 = (int)(packed >> 4) - 8;
+            if (off + j < nelem) dst[off + j] = (float)q0 * scale;
+            if (off + j + 16 < nelem) dst[off + j + 16] = (float)q1 * scale;
+        }
+    }
+}
+
+/* tensor/quantized.go:195-198 Q4GPUDataOffset. */
+EXPORT int64_t orc_q4_gpu_data_offset(int64_t nblk) { return (nblk * 2 + 15) & ~(int64_t)15; }
+
+/* tensor/quantized.go:168-187 RawBytesGPU: [scales nblk*2][pad to 16][data nblk*16]. */
+EXPORT void orc_q4_raw_to_gpu(const uint8_t* raw, int64_t nblk, uint8_t* out) {
+    int64_t doff = orc_q4_gpu_data_offset(nblk);
+    memset(out, 0, (size_t)doff);
+    for (int64_t i = 0; i < nblk; i++) {
+        out[i * 2] = raw[i * 18];
+        out[i * 2 + 1] = raw[i * 18 + 1];
+        memcpy(out + doff + i * 16, raw + i * 18 + 2, 16);
+    }
+}
+
+/* internal/xblas/q4dot.go:10-31 q4DotBlockScalar. */
+EXPORT float orc_q4_dot_block(const uint8_t* packed, float scale, const float* x, int n) {
+    if (n > 32) n = 32;
+    float sum = 0.0f;
+    for (int p = 0; p < 16; p++) {
+        if (p >= n) break;
+        uint8_t bv = packed[p];
+        float lo = (float)((int)(bv & 0x0f) - 8);
+        float hi = (float)((int)(bv >> 4) - 8);
+        sum += lo * x[p];
+        if (p + 16 < n) sum += hi * x[p + 16];
+    }
+    return sum * scale;
+}
+
+/* internal/xblas/q4dot.go:36-50 q4DotRowScalar (the amd64 q4DotRow,
+ * internal/xblas/q4dot_generic.go:13-15). */
+EXPORT float orc_q4_dot_row(const uint8_t* blocks, const float* x, int nblocks) {
+    float total = 0.0f;
+    for (int bi = 0; bi < nblocks; bi++) {
+        const uint8_t* b = blocks + (int64_t)bi * 18;
+        float scale = orc_f16_bits_to_f32_xblas(rd16(b));
+        total += orc_q4_dot_block(b + 2, scale, x + (int64_t)bi * 32, 32);
+    }
+    return total;
+}
+
+/* ------------------------------------------------------- threading helper */
+
+typedef void (*orc_range_fn)(void* ctx, int64_t j0, int64_t j1);
+typedef struct { orc_range_fn fn; void* ctx; int64_t j0, j1; } orc_task;
+static void* orc_task_run(void* p) {
+    orc_task* t = (orc_task*)p;
+    t->fn(t->ctx, t->j0, t->j1);
+    return NULL;
+}
+/* Splits [0,n) into nthreads chunks of ceil(n/nthreads), the split of
+ * gemmF32Q4NTParallel (internal/xblas/gemm_quant.go:122-157). */
+static void orc_parallel_rows(int64_t n, int nthreads, orc_range_fn fn, void* ctx) {
+    if (nthreads <= 1) { fn(ctx, 0, n); return; }
+    int64_t chunk = (n + nthreads - 1) / nthreads;
+    pthread_t th[256];
+    orc_task tk[256];
+    int nt = 0;
+    for (int t = 0; t < nthreads && t < 256; t++) {
+        int64_t j0 = (int64_t)t * chunk, j1 = j0 + chunk < n ? j0 + chunk : n;
+        if (j0 >= n) break;
+        tk[nt] = (orc_task){fn, ctx, j0, j1};
+        pthread_create(&th[nt], NULL, orc_task_run, &tk[nt]);
+        nt++;
+    }
+    for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
+}
+
+/* ----------------------------------------------------------- SgemmSimd */
+
+/* internal/xblas/gemm_simd_amd64.s:8-75 sgemmAccRow: c[j] += a*b[j];
+ * 16- then 8- then 4-wide VFMADD231PS blocks, scalar tail MULSS+ADDSS. */
+static void orc_sgemm_acc_row(float* c, const float* b, float a, int64_t n) {
+    int64_t j = 0;
+    for (; j + 16 <= n; j += 16)
+        for (int l = 0; l < 16; l++) c[j + l] = fmaf(a, b[j + l], c[j + l]);
+    if (j + 8 <= n) { for (int l = 0; l < 8; l++) c[j + l] = fmaf(a, b[j + l], c[j + l]); j += 8; }
+    if (j + 4 <= n) { for (int l = 0; l < 4; l++) c[j + l] = fmaf(a, b[j + l], c[j + l]); j += 4; }
+    for (; j < n; j++) { float t = b[j] * a; c[j] = t + c[j]; }
+}
+
+/* internal/xblas/gemm_simd_amd64.go:19-37 SgemmSimd: C += A*B, K tiled by
+ * 256, zero elements of A skipped.  The caller zeroes C (xblas.GemmF32 is
+ * called on a fresh result tensor, compute/cpu_engine.go:1219-1237). */
+EXPORT void orc_sgemm_simd(int64_t m, int64_t n, int64_t k, const float* a, const float* b, float* c) {
+    if (m == 0 || n == 0 || k == 0) return;
+    for (int64_t p0 = 0; p0 < k; p0 += 256) {
+        int64_t p1 = p0 + 256 < k ? p0 + 256 : k;
+        for (int64_t i = 0; i < m; i++) {
+            float* crow = c + i * n;
+            for (int64_t p = p0; p < p1; p++) {
+                float av = a[i * k + p];
+                if (av != 0.0f) orc_sgemm_acc_row(crow, b + p * n, av, n);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------ GemmF32Q4NT */
+
+typedef struct { const float* a; const uint8_t* raw; float* c; int bpr; } q4nt_ctx;
+static void q4nt_range(void* p, int64_t j0, int64_t j1) {
+    q4nt_ctx* t = (q4nt_ctx*)p;
+    for (int64_t j = j0; j < j1; j++)
+        t->c[j] = orc_q4_dot_row(t->raw + j * t->bpr * 18, t->a, t->bpr);
+}
+
+/* internal/xblas/gemm_quant.go:81-157 GemmF32Q4NT: C[M,N] = A[M,K] * B^T,
+ * B = Q4_0 [N,K] in RawBytes layout.  K%32 must be 0 (the reference's
+ * k%32!=0 branch dequantizes and calls SgemmSimd; callers here use
+ * orc_q4_dequant + orc_sgemm_simd for that).  For M=1 and N*K>=65536 the
+ * reference splits N over min(NumCPU, N/4) workers; nthreads stands for
+ * NumCPU.  Each output is one q4DotRow, so the split does not change bits. */
+EXPORT void orc_gemm_f32_q4_nt(int64_t m, int64_t n, int64_t k, const float* a, const uint8_t* raw,
+                               float* c, int nthreads) {
+    int bpr = (int)(k / 32);
+    if (m == 1 && n * k >= 256 * 256) {
+        int nc = nthreads;
+        if (nc > n / 4) nc = (int)(n / 4);
+        if (nc > 1) {
+            q4nt_ctx ctx = {a, raw, c, bpr};
+            orc_parallel_rows(n, nc, q4nt_range, &ctx);
+            return;
+        }
+    }
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t j = 0; j < n; j++)
+            c[i * n + j] = orc_q4_dot_row(raw + j * bpr * 18, a + i * k, bpr);
+}
+
+/* ------------------------------------------------------------------ Q8_0 */
+
+/* tensor/quantized.go:344-355 Q8Storage.Dequantize over the RawBytes layout
+ * (tensor/quantized.go:427-438): 36-byte blocks, fp32 scale LE + 32 int8. */
+EXPORT void orc_q8_dequant(const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 31) / 32;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        const uint8_t* b = raw + bi * 36;
+        uint32_t sb = rd32(b);
+        float scale;
+        memcpy(&scale, &sb, 4);
+        for (int j = 0; j < 32; j++) {
+            int64_t idx = bi * 32 + j;
+            if (idx >= nelem) break;
+            dst[idx] = (float)(int8_t)b[4 + j] * scale;
+        }
+    }
+}
+
+typedef struct { const float* a; const uint8_t* raw; float* c; int bpr; } q8nt_ctx;
+/* One output of GemmF32Q8NT: DequantizeBlock (tensor/quantized.go:358-363)
+ * into a 32-float buffer, then sum += a*buf in element order
+ * (internal/xblas/gemm_quant.go:193-203). */
+static float q8_dot_row(const uint8_t* row, const float* a, int bpr) {
+    float buf[32];
+    float sum = 0.0f;
+    for (int bi = 0; bi < bpr; bi++) {
+        const uint8_t* b = row + (int64_t)bi * 36;
+        uint32_t sb = rd32(b);
+        float scale;
+        memcpy(&scale, &sb, 4);
+        for (int j = 0; j < 32; j++) buf[j] = (float)(int8_t)b[4 + j] * scale;
+        const float* ab = a + (int64_t)bi * 32;
+        for (int p = 0; p < 32; p++) sum += ab[p] * buf[p];
+    }
+    return sum;
+}
+static void q8nt_range(void* p, int64_t j0, int64_t j1) {
+    q8nt_ctx* t = (q8nt_ctx*)p;
+    for (int64_t j = j0; j < j1; j++) t->c[j] = q8_dot_row(t->raw + j * t->bpr * 36, t->a, t->bpr);
+}
+
+/* internal/xblas/gemm_quant.go:163-264 GemmF32Q8NT (+ gemmF32Q8NTParallel). */
+EXPORT void orc_gemm_f32_q8_nt(int64_t m, int64_t n, int64_t k, const float* a, const uint8_t* raw,
+                               float* c, int nthreads) {
+    int bpr = (int)(k / 32);
+    if (m == 1 && n * k >= 256 * 256) {
+        int nc = nthreads;
+        if (nc > n / 4) nc = (int)(n / 4);
+        if (nc > 1) {
+            q8nt_ctx ctx = {a, raw, c, bpr};
+            orc_parallel_rows(n, nc, q8nt_range, &ctx);
+            return;
+        }
+    }
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t j = 0; j < n; j++) c[i * n + j] = q8_dot_row(raw + j * bpr * 36, a + i * k, bpr);
+}
+
+/* --------------------------------------------------------------- IQ4_NL */
+
+/* tensor/iq4_storage.go:28-33 IQ4NLTable. */
+static const float orc_iq4nl_table[16] = {
+    -1.0f, -0.6961928f, -0.5250730f, -0.3947555f, -0.2831612f, -0.1790887f, -0.0805542f, 0.0f,
+    0.0805542f, 0.1790887f, 0.2831612f, 0.3947555f, 0.5250730f, 0.6961928f, 1.0f, 1.3312578f};
+
+EXPORT void orc_iq4nl_table_copy(float* dst) { memcpy(dst, orc_iq4nl_table, sizeof orc_iq4nl_table); }
+
+/* tensor/iq4_storage.go:36-46 DequantizeIQ4NL (one block: dst[2i] = d*T[lo],
+ * dst[2i+1] = d*T[hi]) and :75-89 IQ4NLStorage.Dequantize (partial last
+ * block copied through a temporary). */
+EXPORT void orc_iq4nl_dequant(const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 31) / 32;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        const uint8_t* b = raw + bi * 18;
+        float d = orc_f16_to_f32(rd16(b));
+        float tmp[32];
+        for (int i = 0; i < 16; i++) {
+            uint8_t lo = b[2 + i] & 0x0f, hi = b[2 + i] >> 4;
+            tmp[2 * i] = d * orc_iq4nl_table[lo];
+            tmp[2 * i + 1] = d * orc_iq4nl_table[hi];
+        }
+        int64_t off = bi * 32, rem = nelem - off;
+        memcpy(dst + off, tmp, sizeof(float) * (size_t)(rem >= 32 ? 32 : rem));
+    }
+}
+
+/* ------------------------------------------------------------ GPTQ / AWQ */
+
+/* tensor/quantized_gptq.go:134-163 GPTQStorage.Dequantize.  data is the
+ * concatenation of every group's packed bytes (the layout that
+ * NewGPTQStorageFromRaw, tensor/quantized_gptq.go:217-277, accepts); for
+ * bits=4 element j of a group is the low nibble of byte j/2 when j is even
+ * and the high nibble when odd. */
+EXPORT void orc_gptq_dequant(const uint8_t* data, const uint16_t* scales, const uint16_t* zeros,
+                             int64_t nelem, int64_t group, int bits, float* dst) {
+    int64_t ngroups = (nelem + group - 1) / group;
+    const uint8_t* g = data;
+    for (int64_t gi = 0; gi < ngroups; gi++) {
+        float scale = orc_f16_to_f32(scales[gi]);
+        float zero = orc_f16_to_f32(zeros[gi]);
+        int64_t off = gi * group, end = off + group < nelem ? off + group : nelem;
+        int64_t count = end - off;
+        if (bits == 4) {
+            for (int64_t j = 0; j < count; j++) {
+                int q = (j % 2 == 0) ? (g[j / 2] & 0x0f) : (g[j / 2] >> 4);
+                dst[off + j] = ((float)q - zero) * scale;
+            }
+            g += (count + 1) / 2;
+        } else {
+            for (int64_t j = 0; j < count; j++) dst[off + j] = ((float)g[j] - zero) * scale;
+            g += count;
+        }
+    }
+}
+
+/* tensor/quantized_awq.go:118-136 AWQStorage.Dequantize: 8 nibbles per
+ * little-endian uint32, element j of a group at bits 4*(j%8) of word j/8. */
+EXPORT void orc_awq_dequant(const uint32_t* words, const uint16_t* scales, const uint16_t* zeros,
+                            int64_t nelem, int64_t group, float* dst) {
+    int64_t ngroups = (nelem + group - 1) / group;
+    const uint32_t* w = words;
+    for (int64_t gi = 0; gi < ngroups; gi++) {
+        float scale = orc_f16_to_f32(scales[gi]);
+        float zero = orc_f16_to_f32(zeros[gi]);
+        int64_t off = gi * group, end = off + group < nelem ? off + group : nelem;
+        int64_t count = end - off;
+        for (int64_t j = 0; j < count; j++) {
+            int q = (int)((w[j / 8] >> ((j % 8) * 4)) & 0xf);
+            dst[off + j] = ((float)q - zero) * scale;
+        }
+        w += (count + 7) / 8;
+    }
+}
+
+/* ----------------------------------------- dequant + SgemmSimd matmuls */
+
+/* tensor/fp16_storage.go:53-63 Float16Storage.Slice. */
+EXPORT void orc_f16_slice(const uint16_t* h, int64_t n, float* dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = orc_f16_to_f32(h[i]);
+}
+
+/* compute/w4a16.go:71-105 MatMulW4A16 with the weights on the A side:
+ * w4.Slice() (GPTQ dequant), fp16Act.Slice(), then eng.MatMul on float32,
+ * which is xblas.GemmF32 -> SgemmSimd (compute/cpu_engine.go:1219-1237,
+ * internal/xblas/gemm.go:12-14) into a zeroed result.
+ * W is [M,K] (groups along K), X is fp16 [K,N], C is fp32 [M,N].
+ * wtmp must hold M*K floats and xtmp K*N floats (the reference allocates
+ * both on every call; the caller passes them so timing can include or
+ * exclude allocation). */
+EXPORT void orc_w4a16_matmul_gptq(const uint8_t* data, const uint16_t* scales, const uint16_t* zeros,
+                                  const uint16_t* x16, float* c, int64_t m, int64_t k, int64_t n,
+                                  int64_t group, float* wtmp, float* xtmp) {
+    orc_gptq_dequant(data, scales, zeros, m * k, group, 4, wtmp);
+    orc_f16_slice(x16, k * n, xtmp);
+    memset(c, 0, sizeof(float) * (size_t)(m * n));
+    orc_sgemm_simd(m, n, k, wtmp, xtmp, c);
+}
+
+/* IQ4_NL has no quantized GEMV in the reference: CPUEngine.MatMul falls
+ * through to Data() (tensor/tensor.go:216-219) -> IQ4NLStorage.Slice
+ * (tensor/iq4_storage.go:95) -> GemmF32 -> SgemmSimd
+ * (compute/cpu_engine.go:1215-1245).  Activations arrive as fp16 and are
+ * widened first (tensor/fp16_storage.go:53-63).  W [M,K], X [K,N], C [M,N]. */
+EXPORT void orc_iq4nl_matmul(const uint8_t* raw, const uint16_t* x16, float* c, int64_t m, int64_t k,
+                             int64_t n, float* wtmp, float* xtmp) {
+    orc_iq4nl_dequant(raw, m * k, wtmp);
+    orc_f16_slice(x16, k * n, xtmp);
+    memset(c, 0, sizeof(float) * (size_t)(m * n));
+    orc_sgemm_simd(m, n, k, wtmp, xtmp, c);
+}
+
+/* --------------------------------------------------------------- Ternary */
+
+/* tensor/ternary_storage.go:39-47 TernaryStorage.Get: 2 bits per value,
+ * element i at bits 2*(i%4) of byte i/4, value = code - 1. */
+EXPORT int orc_ternary_get(const uint8_t* raw, int64_t i) {
+    return (int)((raw[i / 4] >> ((i % 4) * 2)) & 3) - 1;
+}
+
+/* compute/ternary_gemv.go:68-77 ternaryLUT. */
+static float orc_ternary_lut[256][4];
+static int orc_ternary_lut_ready = 0;
+static void orc_ternary_lut_init(void) {
+    if (orc_ternary_lut_ready) return;
+    for (int b = 0; b < 256; b++)
+        for (int k = 0; k < 4; k++) orc_ternary_lut[b][k] = (float)((int8_t)((b >> (k * 2)) & 3) - 1);
+    orc_ternary_lut_ready = 1;
+}
+
+/* compute/ternary_gemv.go:12-64 TernaryGEMV: weights packed flat across rows
+ * (element i*cols+j), fp32 x, sequential fp32 sum per row; byte-aligned rows
+ * use the 4-entry LUT per byte, the rest per-element extraction. */
+EXPORT void orc_ternary_gemv(const uint8_t* raw, const float* x, int64_t rows, int64_t cols, float* y) {
+    orc_ternary_lut_init();
+    for (int64_t i = 0; i < rows; i++) {
+        float sum = 0.0f;
+        int64_t base = i * cols, j = 0;
+        int64_t byteStart = base / 4;
+        if (base % 4 == 0) {
+            int64_t fullBytes = cols / 4;
+            for (int64_t bi = 0; bi < fullBytes; bi++) {
+                const float* l = orc_ternary_lut[raw[byteStart + bi]];
+                sum += l[0] * x[j];
+                sum += l[1] * x[j + 1];
+                sum += l[2] * x[j + 2];
+                sum += l[3] * x[j + 3];
+                j += 4;
+            }
+        }
+        for (; j < cols; j++) {
+            int64_t idx = base + j;
+            int bits = (raw[idx / 4] >> ((idx % 4) * 2)) & 3;
+            if (bits == 0) sum -= x[j];
+            else if (bits == 2) sum += x[j];
+        }
+        y[i] = sum;
+    }
+}
+
+/* compute/ternary_gemv_gpu.go:55-67: repack flat-packed ternary weights into
+ * one byte-aligned row of ceil(cols/4) bytes per output row (the layout the
+ * GPU kernel reads).  out must be zeroed and hold rows*ceil(cols/4) bytes. */
+EXPORT void orc_ternary_repack_rows(const uint8_t* raw, int64_t rows, int64_t cols, uint8_t* out) {
+    int64_t bpr = (cols + 3) / 4;
+    for (int64_t i = 0; i < rows; i++)
+        for (int64_t j = 0; j < cols; j++) {
+            int64_t s = i * cols + j;
+            uint8_t bits = (raw[s / 4] >> ((s % 4) * 2)) & 3;
+            out[i * bpr + j / 4] |= (uint8_t)(bits << ((j % 4) * 2));
+        }
+}
+
+/* BitNet-style int8-activation ternary GEMV (the decode configuration of
+ * this path).  The reference has no int8 activation path: TernaryGEMV takes
+ * fp32 x (compute/ternary_gemv.go:12) and TernaryStorage has no scale
+ * (tensor/ternary_storage.go:7-10).  The reduction is therefore defined as
+ *   y = TernaryGEMV(W, float(q_x)) * (w_scale * x_scale)
+ * in fp32, with the scale product rounded first.  Every partial sum is an
+ * integer of magnitude <= cols*127 < 2^24, so the fp32 sums are exact and
+ * the result is independent of summation order. */
+EXPORT void orc_ternary_gemv_i8(const uint8_t* raw, const int8_t* qx, float x_scale, float w_scale,
+                                int64_t rows, int64_t cols, float* y, float* xtmp) {
+    for (int64_t j = 0; j < cols; j++) xtmp[j] = (float)qx[j];
+    orc_ternary_gemv(raw, xtmp, rows, cols, y);
+    float s = w_scale * x_scale;
+    for (int64_t i = 0; i < rows; i++) y[i] = y[i] * s;
+}

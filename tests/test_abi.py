@@ -1,0 +1,83 @@
+"""CPU checks of the drop-in boundary: libzt_hip.so loads, exports every
+entry point include/zt_hip.h declares with the ctypes table matching the
+header, and its host-side layout converters produce the reference's device
+layouts (checked against the oracle).  No GPU compute is called."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from ztensor_amd import _lib, synth
+from ztensor_amd.storage import IQ4NLStorage, Q4Storage, Q8Storage, TernaryStorage
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    text = (ROOT / "include" / "zt_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:int|long|void)\s+(zt_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert len(declared) >= 20
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib.cdll, name)
+    assert lib.zt_abi_version() == 100
+
+
+def test_header_arity_matches_binding():
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "zt_hip.h").read_text(), flags=re.S)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), name
+
+
+def test_q4_and_iq4_gpu_layout_match_oracle(orc):
+    for rows, K in [(1, 32), (3, 96), (16, 4096)]:
+        w = synth.q4_0(rows, K, 1)
+        s = Q4Storage.from_raw(w.raw, rows * K)
+        nblk = rows * K // 32
+        assert np.array_equal(s.raw_bytes_gpu(), orc.q4_raw_to_gpu(w.raw, nblk))
+        assert s.gpu_data_offset() == orc.lib().orc_q4_gpu_data_offset(nblk)
+        iq = IQ4NLStorage.from_raw(w.raw, rows * K)
+        assert np.array_equal(iq.raw_bytes_gpu(), s.raw_bytes_gpu())
+
+
+def test_q8_separated_layout():
+    w = synth.q8_0(5, 64, 2)
+    s = Q8Storage(w.raw, 5 * 64)
+    g = s.raw_bytes_gpu()
+    nblk = 10
+    off = s.gpu_data_offset()
+    assert off == 48 and g.size == off + 32 * nblk
+    blocks = w.raw.reshape(nblk, 36)
+    assert np.array_equal(g[: 4 * nblk].reshape(nblk, 4), blocks[:, :4])
+    assert np.array_equal(g[off:].reshape(nblk, 32), blocks[:, 4:])
+
+
+def test_ternary_repack_matches_oracle(orc):
+    rng = np.random.default_rng(0)
+    for rows, cols in [(3, 5), (4, 8), (33, 33), (2, 2560)]:
+        w = rng.integers(-1, 2, rows * cols).astype(np.int8)
+        raw = synth.pack_ternary(w)
+        assert np.array_equal(TernaryStorage(raw, w.size).row_aligned(rows, cols),
+                              orc.ternary_repack_rows(raw, rows, cols))
+
+
+def test_storage_constructors_validate_like_reference():
+    with pytest.raises(ValueError):
+        Q4Storage.from_raw(np.zeros(10, np.uint8), 32)  # short raw
+    with pytest.raises(ValueError):
+        Q4Storage.from_raw(np.zeros(18, np.uint8), 0)
+    with pytest.raises(ValueError):
+        IQ4NLStorage.from_raw(np.zeros(10, np.uint8), 32)  # tensor/iq4_storage_test.go:137-142
+    with pytest.raises(ValueError):
+        IQ4NLStorage.from_raw(np.zeros(0, np.uint8), -1)
+    with pytest.raises(ValueError):
+        Q8Storage.from_blocks(np.zeros(1, np.float32), np.zeros(31, np.int8), 32)

@@ -1,0 +1,96 @@
+"""ctypes binding of libzt_hip.so.
+
+This is the Python twin of the reference's purego layer
+(internal/cuda/kernels/purego.go:230-260, internal/hip/kernels/purego.go:44-107):
+the library is opened once, every symbol is resolved once into a table, and
+every call passes only integers and pointers.  A nonzero return is a
+hipError_t and becomes ZTError, which is what the reference's checkKernel
+turns into a Go error (internal/cuda/kernels/elementwise_purego.go:11-16).
+
+There is no fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libzt_hip.so"
+
+P = C.c_void_p
+I = C.c_int
+L = C.c_long
+
+# name -> (restype, argtypes); mirrors include/zt_hip.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "zt_abi_version": (I, []),
+    "zt_gemm_q4_f32": (I, [P, P, P, I, I, I, I, P]),
+    "zt_gemm_q4_f16": (I, [P, P, P, I, I, I, I, P]),
+    "zt_dequant_q4_f32": (I, [P, P, L, I, P]),
+    "zt_q4_gpu_data_offset": (L, [L]),
+    "zt_q4_gpu_bytes": (L, [L]),
+    "zt_q4_raw_to_gpu": (None, [P, L, P]),
+    "zt_gemm_iq4nl_f32": (I, [P, P, P, I, I, I, I, P]),
+    "zt_gemm_iq4nl_f16": (I, [P, P, P, I, I, I, I, P]),
+    "zt_dequant_iq4nl_f32": (I, [P, P, L, I, P]),
+    "zt_iq4nl_raw_to_gpu": (None, [P, L, P]),
+    "zt_gemm_q8_f32": (I, [P, P, P, I, I, I, P]),
+    "zt_gemm_q8sep_f32": (I, [P, P, P, I, I, I, L, P]),
+    "zt_dequant_q8_f32": (I, [P, P, L, P]),
+    "zt_dequant_q8sep_f32": (I, [P, P, L, L, P]),
+    "zt_q8_repack": (I, [P, P, L, P]),
+    "zt_q8_gpu_data_offset": (L, [L]),
+    "zt_q8_gpu_bytes": (L, [L]),
+    "zt_q8_raw_to_gpu": (None, [P, L, P]),
+    "zt_gemm_w4a16_f32": (I, [P, P, P, P, P, I, I, I, I, P]),
+    "zt_dequant_w4_f32": (I, [P, P, P, P, L, I, P]),
+    "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),
+    "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
+    "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),
+    "zt_ternary_repack_rows": (None, [P, L, L, P]),
+}
+
+HIP_ERROR_INVALID_VALUE = 1
+
+
+class ZTError(RuntimeError):
+    """A libzt_hip entry point returned a nonzero hipError_t."""
+
+    def __init__(self, name: str, code: int):
+        super().__init__(f"{name} failed: hipError_t {code}")
+        self.name = name
+        self.code = code
+
+
+class _Lib:
+    def __init__(self, path: Path):
+        if not path.exists():
+            raise FileNotFoundError(
+                f"{path} is not built; run `python -m ztensor_amd.build` (no CPU fallback exists)"
+            )
+        self.path = path
+        self.cdll = C.CDLL(str(path))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(self.cdll, name)
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, fn)
+
+    def call(self, name: str, *args) -> None:
+        """Calls an int-returning entry point and raises ZTError on failure."""
+        rc = getattr(self, name)(*args)
+        if rc != 0:
+            raise ZTError(name, rc)
+
+
+_once = threading.Lock()
+_lib: _Lib | None = None
+
+
+def load() -> _Lib:
+    """Opens the library once (the sync.Once of the reference loader)."""
+    global _lib
+    with _once:
+        if _lib is None:
+            _lib = _Lib(LIB_PATH)
+    return _lib

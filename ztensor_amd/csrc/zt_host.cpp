@@ -1,0 +1,67 @@
+// Host-side (CPU) half of libzt_hip.so: load-time layout conversions that
+// turn the reference's serialised weight formats into the device layouts the
+// kernels read.  They run once per weight at upload, like
+// Q4Storage.RawBytesGPU (tensor/quantized.go:158-187) does for the CUDA
+// engine, so no conversion happens inside a matmul call.
+#include <string.h>
+
+#include "zt_hip.h"
+
+extern "C" {
+
+int zt_abi_version(void) { return 100; }
+
+long zt_q4_gpu_data_offset(long nblk) { return (nblk * 2 + 15) & ~15L; }
+
+long zt_q4_gpu_bytes(long nblk) { return zt_q4_gpu_data_offset(nblk) + nblk * 16; }
+
+// tensor/quantized.go:168-187: scales first (LE fp16), zero padding to a
+// 16-byte boundary, then every block's 16 nibble bytes.
+void zt_q4_raw_to_gpu(const void* raw, long nblk, void* out) {
+    const unsigned char* src = static_cast<const unsigned char*>(raw);
+    unsigned char* dst = static_cast<unsigned char*>(out);
+    const long doff = zt_q4_gpu_data_offset(nblk);
+    memset(dst + nblk * 2, 0, (size_t)(doff - nblk * 2));
+    for (long i = 0; i < nblk; i++) {
+        dst[2 * i] = src[18 * i];
+        dst[2 * i + 1] = src[18 * i + 1];
+        memcpy(dst + doff + 16 * i, src + 18 * i + 2, 16);
+    }
+}
+
+// IQ4_NL blocks have the same 18-byte shape (tensor/iq4_storage.go:12-23).
+void zt_iq4nl_raw_to_gpu(const void* raw, long nblk, void* out) { zt_q4_raw_to_gpu(raw, nblk, out); }
+
+// 36-byte Q8_0 blocks (tensor/quantized.go:425-438) -> [fp32 scales][pad][32-byte payloads].
+void zt_q8_raw_to_gpu(const void* raw, long nblk, void* out) {
+    const unsigned char* src = static_cast<const unsigned char*>(raw);
+    unsigned char* dst = static_cast<unsigned char*>(out);
+    const long doff = zt_q8_gpu_data_offset(nblk);
+    memset(dst + nblk * 4, 0, (size_t)(doff - nblk * 4));
+    for (long i = 0; i < nblk; i++) {
+        memcpy(dst + 4 * i, src + 36 * i, 4);
+        memcpy(dst + doff + 32 * i, src + 36 * i + 4, 32);
+    }
+}
+
+// compute/ternary_gemv_gpu.go:55-67: element (i, j) of the flat 2-bit
+// packing (bit offset 2*(i*K+j)) moves to byte i*ceil(K/4) + j/4, bits
+// 2*(j%4); the pad bits of each row stay zero.
+void zt_ternary_repack_rows(const void* raw, long M, long K, void* out) {
+    const unsigned char* src = static_cast<const unsigned char*>(raw);
+    unsigned char* dst = static_cast<unsigned char*>(out);
+    const long bpr = (K + 3) / 4;
+    memset(dst, 0, (size_t)(M * bpr));
+    if (K % 4 == 0) {  // rows are already byte-aligned: a plain copy
+        memcpy(dst, src, (size_t)(M * bpr));
+        return;
+    }
+    for (long i = 0; i < M; i++)
+        for (long j = 0; j < K; j++) {
+            const long s = i * K + j;
+            const unsigned bits = (src[s / 4] >> (2 * (s % 4))) & 3u;
+            dst[i * bpr + j / 4] |= (unsigned char)(bits << (2 * (j % 4)));
+        }
+}
+
+}  // extern "C"

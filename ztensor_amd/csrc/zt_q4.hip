@@ -1,0 +1,256 @@
+// Q4_0 and IQ4_NL GEMV / small-batch GEMM and dequantization for gfx950.
+//
+// Both formats use 32-weight blocks with one fp16 scale and 16 bytes of
+// nibbles, uploaded in the separated layout
+//     [scales: nblk * 2 bytes][pad to 16 bytes][data: nblk * 16 bytes]
+// (tensor/quantized.go:158-198 RawBytesGPU / Q4GPUDataOffset).  Block i of
+// the [rows, K] matrix is block (row * K/32 + kb).  They differ only in how
+// a block decodes:
+//   Q4_0   w[j] = (lo_j - 8) * d, w[j+16] = (hi_j - 8) * d   (byte j, GGML split order;
+//          tensor/quantized.go:96-114)
+//   IQ4_NL w[2i] = d * T[lo_i], w[2i+1] = d * T[hi_i]       (interleaved order, float table;
+//          tensor/iq4_storage.go:28-46)
+//
+// GEMV design (HBM-bound; every weight byte is read once):
+//  * lane <-> one 32-weight block column; its 16 data bytes are one 128-bit
+//    load, and the 64 lanes of a wave read 1 KiB of a row contiguously;
+//  * each wave walks R rows with the same block column, so the lane's 32
+//    activations are loaded once (registers) and reused R times;
+//  * the waves of a workgroup split K (split-K) and combine through LDS;
+//  * Q4_0: sum_j (q_j - 8) x_j = sum_j q_j x_j - 8 * sum_j x_j, with q_j
+//    converted by v_cvt_f32_ubyte{0..3} straight from the masked dword, and
+//    the per-block activation sum computed once per lane;
+//  * IQ4_NL: the 16-entry fp32 table sits in LDS; a lookup is one
+//    conflict-free ds_read_b32 (at most 16 distinct addresses per wave);
+//  * the block scale multiplies the block's partial sum once.
+#include "zt_common.h"
+
+namespace zt {
+
+enum class Fmt { Q4_0, IQ4NL };
+
+// tensor/iq4_storage.go:28-33 IQ4NLTable.
+__constant__ float kIQ4NLTable[16] = {
+    -1.0f, -0.6961928f, -0.5250730f, -0.3947555f, -0.2831612f, -0.1790887f, -0.0805542f, 0.0f,
+    0.0805542f, 0.1790887f, 0.2831612f, 0.3947555f, 0.5250730f, 0.6961928f, 1.0f, 1.3312578f};
+
+template <class XT>
+__device__ __forceinline__ float to_f32(XT v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return h2f(v); }
+
+// Loads the 32 activations of block column b into registers.
+template <class XT, bool CONTIG>
+__device__ __forceinline__ void load_x32(const XT* __restrict__ x, long x_stride, int b, float (&xv)[32]) {
+    if constexpr (CONTIG && sizeof(XT) == 4) {
+        const float4* p = reinterpret_cast<const float4*>(x + (long)b * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 t = p[i];
+            xv[4 * i] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
+        }
+    } else if constexpr (CONTIG && sizeof(XT) == 2) {
+        const uint4* p = reinterpret_cast<const uint4*>(x + (long)b * 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint4 t = p[i];
+            uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                xv[8 * i + 2 * j] = h2f((uint16_t)(w[j] & 0xffff));
+                xv[8 * i + 2 * j + 1] = h2f((uint16_t)(w[j] >> 16));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) xv[i] = to_f32<XT>(x[((long)b * 32 + i) * x_stride]);
+    }
+}
+
+// sum_j w_j x_j over one block, without the block scale.
+template <Fmt F>
+__device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32], float xsum, const float* tbl) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (F == Fmt::Q4_0) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = d[i] & 0x0f0f0f0fu;         // elements 4i .. 4i+3
+            const uint32_t hi = (d[i] >> 4) & 0x0f0f0f0fu;  // elements 16+4i .. 16+4i+3
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                s0 = fmaf((float)((lo >> (8 * j)) & 0xffu), xv[4 * i + j], s0);
+                s1 = fmaf((float)((hi >> (8 * j)) & 0xffu), xv[16 + 4 * i + j], s1);
+            }
+        }
+        return (s0 + s1) - 8.0f * xsum;
+    } else {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int m = 0; m < 8; m += 2) {  // nibble m of dword i is element 8i+m
+                s0 = fmaf(tbl[(d[i] >> (4 * m)) & 0xfu], xv[8 * i + m], s0);
+                s1 = fmaf(tbl[(d[i] >> (4 * m + 4)) & 0xfu], xv[8 * i + m + 1], s1);
+            }
+        }
+        return s0 + s1;
+    }
+}
+
+template <Fmt F, int R, class XT, bool CONTIG>
+__global__ void __launch_bounds__(512) gemv_blk18_kernel(const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ data,
+                                                         const XT* __restrict__ x, float* __restrict__ y,
+                                                         long xy_stride, int rows, int kb) {
+    __shared__ float red[8 * R];
+    __shared__ float tbl[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    if constexpr (F == Fmt::IQ4NL) {
+        if (threadIdx.x < 16) tbl[threadIdx.x] = kIQ4NLTable[threadIdx.x];
+        __syncthreads();
+    }
+    x += blockIdx.y;
+    y += blockIdx.y;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int b = wave * kWave + lane; b < kb; b += nwaves * kWave) {
+        uint4 w[R];
+        uint16_t s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = ld_stream(&data[rbase[r] + b]);
+            s[r] = scales[rbase[r] + b];
+        }
+        float xv[32];
+        load_x32<XT, CONTIG>(x, xy_stride, b, xv);
+        float xsum = 0.0f;
+        if constexpr (F == Fmt::Q4_0) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) xsum += xv[i];
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(s[r]), block_dot<F>(w[r], xv, xsum, tbl), acc[r]);
+    }
+    block_reduce_store<R>(acc, red, y, xy_stride, row0, rows);
+}
+
+template <Fmt F, class XT, bool CONTIG>
+static void launch_gemv_r(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint4* dt,
+                          const XT* x, float* y, long stride, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_blk18_kernel<F, 8, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
+        case 4: gemv_blk18_kernel<F, 4, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
+        case 2: gemv_blk18_kernel<F, 2, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
+        default: gemv_blk18_kernel<F, 1, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
+    }
+}
+
+template <Fmt F, class XT>
+static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N, int data_offset, hipStream_t st) {
+    if (M < 0 || N < 0 || K < 0 || K % 32 != 0 || data_offset < 0 || N > 65535) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(A);
+    const uint8_t* data = base + data_offset;
+    if (((uintptr_t)base & 1) || ((uintptr_t)data & 15)) return (int)hipErrorInvalidValue;
+    if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
+    const int kb = K / 32;
+    const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
+    const int R = pick_rows_per_wave(M, nwaves, N, 2048);
+    dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base);
+    const uint4* dt = reinterpret_cast<const uint4*>(data);
+    if (N == 1)
+        launch_gemv_r<F, XT, true>(R, grid, block, st, sc, dt, B, C, 1, M, kb);
+    else
+        launch_gemv_r<F, XT, false>(R, grid, block, st, sc, dt, B, C, N, M, kb);
+    return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------ dequantize
+
+template <Fmt F>
+__global__ void dequant_blk18_kernel(const uint16_t* __restrict__ scales, const uint4* __restrict__ data,
+                                     float* __restrict__ out, long nelem) {
+    const long blk = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long nblk = (nelem + 31) / 32;
+    if (blk >= nblk) return;
+    const float d = h2f(scales[blk]);
+    const uint4 w = data[blk];
+    const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t byte = (dw[i / 4] >> (8 * (i % 4))) & 0xffu;
+        if constexpr (F == Fmt::Q4_0) {
+            v[i] = (float)((int)(byte & 0x0f) - 8) * d;
+            v[i + 16] = (float)((int)(byte >> 4) - 8) * d;
+        } else {
+            v[2 * i] = d * kIQ4NLTable[byte & 0x0f];
+            v[2 * i + 1] = d * kIQ4NLTable[byte >> 4];
+        }
+    }
+    float* o = out + blk * 32;
+    const long rem = nelem - blk * 32;
+    if (rem >= 32) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) o[i] = v[i];
+    } else {
+        for (int i = 0; i < rem; i++) o[i] = v[i];
+    }
+}
+
+template <Fmt F>
+static int dequant_blk18(const void* A, float* out, long nelem, int data_offset, hipStream_t st) {
+    if (nelem < 0 || data_offset < 0) return (int)hipErrorInvalidValue;
+    if (nelem == 0) return (int)hipSuccess;
+    const uint8_t* base = static_cast<const uint8_t*>(A);
+    if (((uintptr_t)base & 1) || ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
+    const long nblk = (nelem + 31) / 32;
+    dequant_blk18_kernel<F><<<ceil_div(nblk, 256), 256, 0, st>>>(
+        reinterpret_cast<const uint16_t*>(base), reinterpret_cast<const uint4*>(base + data_offset), out, nelem);
+    return (int)hipGetLastError();
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+ZT_EXPORT int zt_gemm_q4_f32(const void* A_q4, const float* B, float* C, int M, int K, int N, int data_offset,
+                             hipStream_t stream) {
+    return gemm_blk18<Fmt::Q4_0, float>(A_q4, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_gemm_q4_f16(const void* A_q4, const uint16_t* B, float* C, int M, int K, int N,
+                             int data_offset, hipStream_t stream) {
+    return gemm_blk18<Fmt::Q4_0, uint16_t>(A_q4, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_gemm_iq4nl_f32(const void* A_iq4, const float* B, float* C, int M, int K, int N,
+                                int data_offset, hipStream_t stream) {
+    return gemm_blk18<Fmt::IQ4NL, float>(A_iq4, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_gemm_iq4nl_f16(const void* A_iq4, const uint16_t* B, float* C, int M, int K, int N,
+                                int data_offset, hipStream_t stream) {
+    return gemm_blk18<Fmt::IQ4NL, uint16_t>(A_iq4, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_q4_f32(const void* A_q4, float* out, long nelem, int data_offset, hipStream_t stream) {
+    return dequant_blk18<Fmt::Q4_0>(A_q4, out, nelem, data_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_iq4nl_f32(const void* A_iq4, float* out, long nelem, int data_offset,
+                                   hipStream_t stream) {
+    return dequant_blk18<Fmt::IQ4NL>(A_iq4, out, nelem, data_offset, stream);
+}

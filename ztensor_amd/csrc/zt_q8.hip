@@ -1,0 +1,214 @@
+// Q8_0 GEMV / small-batch GEMM and dequantization for gfx950.
+//
+// Q8_0 here is the Q8Storage format: 32 int8 weights and one fp32 scale per
+// block, w = float(q) * scale (tensor/quantized.go:278-363).  Its raw
+// serialisation is 36-byte blocks [fp32 scale LE][32 x int8]
+// (tensor/quantized.go:425-438), which leaves the int8 payload only 4-byte
+// aligned.  Two device layouts are accepted:
+//   * raw:       the 36-byte blocks as RawBytes() produces them (the layout
+//                gemm_q8_f32 takes, internal/cuda/kernels/gemm_q8.cu:3-6);
+//   * separated: [scales: nblk * 4 bytes][pad to 16 bytes][data: nblk * 32 bytes],
+//                the Q8 counterpart of Q4's RawBytesGPU, built once at
+//                upload (zt_q8_raw_to_gpu on the host or zt_q8_repack on the
+//                device).  Every block's 32 bytes are two aligned 128-bit
+//                loads, so a wave reads 2 KiB of a row contiguously.
+//
+// Kernel structure as for Q4_0 (zt_q4.hip): lane <-> block column, R rows
+// per wave with the 32 activations held in registers, split-K across the
+// waves of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
+// which v_cvt_f32_ubyte converts directly; sum (q+128) x - 128 sum x
+// recovers the signed dot product.
+#include "zt_common.h"
+
+namespace zt {
+
+__device__ __forceinline__ float q8_dot_dwords(const uint32_t* d, const float (&xv)[32], float xsum) {
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t u = d[i] ^ 0x80808080u;  // bytes q+128
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            s0 = fmaf((float)((u >> (8 * j)) & 0xffu), xv[4 * i + j], s0);
+            s1 = fmaf((float)((u >> (8 * j + 8)) & 0xffu), xv[4 * i + j + 1], s1);
+        }
+    }
+    return (s0 + s1) - 128.0f * xsum;
+}
+
+template <class XT, bool CONTIG>
+__device__ __forceinline__ void load_x32f(const XT* __restrict__ x, long x_stride, int b, float (&xv)[32]) {
+    if constexpr (CONTIG) {
+        const float4* p = reinterpret_cast<const float4*>(x + (long)b * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 t = p[i];
+            xv[4 * i] = t.x; xv[4 * i + 1] = t.y; xv[4 * i + 2] = t.z; xv[4 * i + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) xv[i] = x[((long)b * 32 + i) * x_stride];
+    }
+}
+
+// SEP = separated layout, else raw 36-byte blocks.
+template <bool SEP, int R, bool CONTIG>
+__global__ void __launch_bounds__(512) gemv_q8_kernel(const uint8_t* __restrict__ base, long data_offset,
+                                                      const float* __restrict__ x, float* __restrict__ y,
+                                                      long xy_stride, int rows, int kb) {
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    x += blockIdx.y;
+    y += blockIdx.y;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
+    const float* scales = reinterpret_cast<const float*>(base);
+    const uint4* data = reinterpret_cast<const uint4*>(base + data_offset);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int b = wave * kWave + lane; b < kb; b += nwaves * kWave) {
+        uint32_t d[R][8];
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const long blk = rbase[r] + b;
+            if constexpr (SEP) {
+                const uint4 a = ld_stream(&data[2 * blk]);
+                const uint4 c = ld_stream(&data[2 * blk + 1]);
+                d[r][0] = a.x; d[r][1] = a.y; d[r][2] = a.z; d[r][3] = a.w;
+                d[r][4] = c.x; d[r][5] = c.y; d[r][6] = c.z; d[r][7] = c.w;
+                s[r] = scales[blk];
+            } else {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(base + blk * 36);
+                s[r] = __uint_as_float(__builtin_nontemporal_load(p));
+#pragma unroll
+                for (int i = 0; i < 8; i++) d[r][i] = __builtin_nontemporal_load(p + 1 + i);
+            }
+        }
+        float xv[32];
+        load_x32f<float, CONTIG>(x, xy_stride, b, xv);
+        float xsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xsum += xv[i];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = fmaf(s[r], q8_dot_dwords(d[r], xv, xsum), acc[r]);
+    }
+    block_reduce_store<R>(acc, red, y, xy_stride, row0, rows);
+}
+
+template <bool SEP, bool CONTIG>
+static void launch_q8(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
+                      float* y, long stride, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_q8_kernel<SEP, 8, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        case 4: gemv_q8_kernel<SEP, 4, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        case 2: gemv_q8_kernel<SEP, 2, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        default: gemv_q8_kernel<SEP, 1, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+    }
+}
+
+template <bool SEP>
+static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N, long data_offset, hipStream_t st) {
+    if (M < 0 || N < 0 || K < 0 || K % 32 != 0 || data_offset < 0 || N > 65535) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(A);
+    if ((uintptr_t)base & 3) return (int)hipErrorInvalidValue;
+    if (SEP && ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
+    if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
+    const int kb = K / 32;
+    const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
+    const int R = pick_rows_per_wave(M, nwaves, N, 2048);
+    dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
+    if (N == 1)
+        launch_q8<SEP, true>(R, grid, block, st, base, data_offset, B, C, 1, M, kb);
+    else
+        launch_q8<SEP, false>(R, grid, block, st, base, data_offset, B, C, N, M, kb);
+    return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------ dequantize
+
+template <bool SEP>
+__global__ void dequant_q8_kernel(const uint8_t* __restrict__ base, long data_offset, float* __restrict__ out,
+                                  long nelem) {
+    const long blk = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long nblk = (nelem + 31) / 32;
+    if (blk >= nblk) return;
+    float scale;
+    const uint8_t* q;
+    if constexpr (SEP) {
+        scale = reinterpret_cast<const float*>(base)[blk];
+        q = base + data_offset + blk * 32;
+    } else {
+        scale = *reinterpret_cast<const float*>(base + blk * 36);
+        q = base + blk * 36 + 4;
+    }
+    const long rem = nelem - blk * 32;
+    const int n = rem >= 32 ? 32 : (int)rem;
+    float* o = out + blk * 32;
+    for (int j = 0; j < n; j++) o[j] = (float)(int8_t)q[j] * scale;
+}
+
+template <bool SEP>
+static int dequant_q8(const void* A, float* out, long nelem, long data_offset, hipStream_t st) {
+    if (nelem < 0 || data_offset < 0) return (int)hipErrorInvalidValue;
+    if (nelem == 0) return (int)hipSuccess;
+    if ((uintptr_t)A & 3) return (int)hipErrorInvalidValue;
+    const long nblk = (nelem + 31) / 32;
+    dequant_q8_kernel<SEP><<<ceil_div(nblk, 256), 256, 0, st>>>(static_cast<const uint8_t*>(A), data_offset, out,
+                                                                 nelem);
+    return (int)hipGetLastError();
+}
+
+// Raw 36-byte blocks -> separated layout, one thread per block.
+__global__ void q8_repack_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, long nblk,
+                                 long data_offset) {
+    const long blk = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= nblk) return;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(raw + blk * 36);
+    reinterpret_cast<uint32_t*>(out)[blk] = src[0];
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + data_offset + blk * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) dst[i] = src[1 + i];
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+// Byte offset of the data region in the separated Q8_0 layout.
+ZT_EXPORT long zt_q8_gpu_data_offset(long nblk) { return (nblk * 4 + 15) & ~15L; }
+
+ZT_EXPORT long zt_q8_gpu_bytes(long nblk) { return zt_q8_gpu_data_offset(nblk) + nblk * 32; }
+
+ZT_EXPORT int zt_gemm_q8_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, hipStream_t stream) {
+    return gemm_q8<false>(A_q8, B, C, M, K, N, 0, stream);
+}
+
+ZT_EXPORT int zt_gemm_q8sep_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, long data_offset,
+                                hipStream_t stream) {
+    return gemm_q8<true>(A_q8, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_q8_f32(const void* A_q8, float* out, long nelem, hipStream_t stream) {
+    return dequant_q8<false>(A_q8, out, nelem, 0, stream);
+}
+
+ZT_EXPORT int zt_dequant_q8sep_f32(const void* A_q8, float* out, long nelem, long data_offset, hipStream_t stream) {
+    return dequant_q8<true>(A_q8, out, nelem, data_offset, stream);
+}
+
+ZT_EXPORT int zt_q8_repack(const void* raw, void* out, long nblk, hipStream_t stream) {
+    if (nblk < 0 || ((uintptr_t)raw & 3) || ((uintptr_t)out & 15)) return (int)hipErrorInvalidValue;
+    if (nblk == 0) return (int)hipSuccess;
+    q8_repack_kernel<<<ceil_div(nblk, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(raw),
+                                                              static_cast<uint8_t*>(out), nblk,
+                                                              zt_q8_gpu_data_offset(nblk));
+    return (int)hipGetLastError();
+}

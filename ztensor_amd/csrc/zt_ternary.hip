@@ -1,0 +1,291 @@
+// Ternary {-1, 0, +1} GEMV for gfx950.
+//
+// Weight format: 2 bits per weight, code 00 = -1, 01 = 0, 10 = +1, element
+// j of a byte at bits 2*(j%4) (tensor/ternary_storage.go:5-62).  The device
+// layout is the row-aligned one the GPU path uploads
+// (compute/ternary_gemv_gpu.go:52-67): row r occupies bytes
+// [r*bpr, (r+1)*bpr) with bpr = ceil(K/4); pad bits of a row's last byte
+// are zero (code 00), so activations past K are treated as 0.
+//
+// Two kernels:
+//  * f32 activations (the reference's TernaryGEMV / ternary_gemv_f32
+//    contract, compute/ternary_gemv.go:12-64): each 2-bit code c is
+//    converted with v_cvt_f32_ubyte and sum (c-1) x = sum c x - sum x;
+//  * int8 activations with a per-tensor weight scale and a per-token
+//    activation scale (BitNet decode): integer dot products with
+//    v_dot4_i32_i8 on the codes, y = float(sum c q - sum q) * (w_scale *
+//    x_scale).  The integer sum is exact, so the result is bit-identical to
+//    the fp32 reference reduction (whose partial sums are exact integers).
+//
+// Work split: a lane owns CB consecutive bytes of a row (4*CB weights);
+// CB = 16 when bpr % 16 == 0 (one 128-bit load), 4 when bpr % 4 == 0, else
+// 1.  Its activations stay in registers while the wave walks R rows; waves of
+// a workgroup split K and combine through LDS.
+#include "zt_common.h"
+
+namespace zt {
+
+template <int CB>
+__device__ __forceinline__ void load_codes(const uint8_t* __restrict__ p, uint32_t (&w)[(CB + 3) / 4]) {
+    if constexpr (CB == 16) {
+        const uint4 v = ld_stream(reinterpret_cast<const uint4*>(p));
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (CB == 4) {
+        w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    } else {
+        w[0] = *p;
+    }
+}
+
+// ----------------------------------------------------------- int8 x
+
+template <int CB, int R>
+__global__ void __launch_bounds__(512) ternary_i8_kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                         const float* __restrict__ x_scale,
+                                                         const float* __restrict__ w_scale, float* __restrict__ y,
+                                                         int rows, int K, int bpr) {
+    constexpr int ND = (CB + 3) / 4;  // weight dwords per lane
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int nchunk = bpr / CB;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * bpr;
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int c = wave * kWave + lane; c < nchunk; c += nwaves * kWave) {
+        uint32_t w[R][ND];
+#pragma unroll
+        for (int r = 0; r < R; r++) load_codes<CB>(W + rbase[r] + (long)c * CB, w[r]);
+        // xd[i][t] holds activations 16i+4t .. 16i+4t+3 (zero past K);
+        // xp[i][s] packs activations 16i+s, 16i+4+s, 16i+8+s, 16i+12+s: the
+        // order in which (w >> 2s) & 0x03030303 lays out the codes of dword i.
+        const int k0 = c * CB * 4;
+        uint32_t xd[ND][4];
+        if (k0 + 4 * CB <= K && (CB == 1 || ((uintptr_t)(xq + k0) & 15) == 0)) {
+            if constexpr (CB == 16) {
+#pragma unroll
+                for (int i = 0; i < ND; i++) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(xq + k0 + 16 * i);
+                    xd[i][0] = v.x; xd[i][1] = v.y; xd[i][2] = v.z; xd[i][3] = v.w;
+                }
+            } else if constexpr (CB == 4) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xq + k0);
+                xd[0][0] = v.x; xd[0][1] = v.y; xd[0][2] = v.z; xd[0][3] = v.w;
+            } else {
+                xd[0][0] = (uint32_t)(uint8_t)xq[k0] | ((uint32_t)(uint8_t)xq[k0 + 1] << 8) |
+                           ((uint32_t)(uint8_t)xq[k0 + 2] << 16) | ((uint32_t)(uint8_t)xq[k0 + 3] << 24);
+                xd[0][1] = xd[0][2] = xd[0][3] = 0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < ND; i++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    uint32_t v = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const int e = 16 * i + 4 * t + b, k = k0 + e;
+                        if (e < 4 * CB && k < K) v |= (uint32_t)(uint8_t)xq[k] << (8 * b);
+                    }
+                    xd[i][t] = v;
+                }
+        }
+        int xp[ND][4];
+        int xsum = 0;
+#pragma unroll
+        for (int i = 0; i < ND; i++) {
+            // 4x4 byte transpose with v_perm_b32.
+            const uint32_t t0 = __builtin_amdgcn_perm(xd[i][1], xd[i][0], 0x05010400u);
+            const uint32_t t1 = __builtin_amdgcn_perm(xd[i][3], xd[i][2], 0x05010400u);
+            const uint32_t t2 = __builtin_amdgcn_perm(xd[i][1], xd[i][0], 0x07030602u);
+            const uint32_t t3 = __builtin_amdgcn_perm(xd[i][3], xd[i][2], 0x07030602u);
+            xp[i][0] = (int)__builtin_amdgcn_perm(t1, t0, 0x05040100u);
+            xp[i][1] = (int)__builtin_amdgcn_perm(t1, t0, 0x07060302u);
+            xp[i][2] = (int)__builtin_amdgcn_perm(t3, t2, 0x05040100u);
+            xp[i][3] = (int)__builtin_amdgcn_perm(t3, t2, 0x07060302u);
+#pragma unroll
+            for (int s2 = 0; s2 < 4; s2++) xsum = __builtin_amdgcn_sdot4((int)xd[i][s2], 0x01010101, xsum, false);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int s32 = 0;
+#pragma unroll
+            for (int i = 0; i < ND; i++)
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+                    s32 = __builtin_amdgcn_sdot4((int)((w[r][i] >> (2 * s)) & 0x03030303u), xp[i][s], s32, false);
+            acc[r] += (float)(s32 - xsum);  // |partial| <= K*127 < 2^24: exact in fp32
+        }
+    }
+    // Every partial sum is an integer below 2^24, so the float reduction is exact.
+    float tot[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) tot[r] = acc[r];
+    wave_reduce_rows<R>(tot);
+    const float scale = w_scale[0] * x_scale[0];
+    if (nwaves == 1) {
+        if (is_row_writer<R>(lane)) {
+            const int r = row0 + row_of_lane<R>(lane);
+            if (r < rows) y[r] = tot[0] * scale;
+        }
+        return;
+    }
+    if (is_row_writer<R>(lane)) red[wave * R + row_of_lane<R>(lane)] = tot[0];
+    __syncthreads();
+    if ((int)threadIdx.x < R) {
+        float s = 0.0f;
+        for (int w2 = 0; w2 < nwaves; w2++) s += red[w2 * R + threadIdx.x];
+        const int r = row0 + threadIdx.x;
+        if (r < rows) y[r] = s * scale;
+    }
+}
+
+// ----------------------------------------------------------- fp32 x
+
+template <int CB, int R>
+__global__ void __launch_bounds__(512) ternary_f32_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                          float* __restrict__ y, int rows, int K, int bpr) {
+    constexpr int ND = (CB + 3) / 4;
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int nchunk = bpr / CB;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * bpr;
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int c = wave * kWave + lane; c < nchunk; c += nwaves * kWave) {
+        uint32_t w[R][ND];
+#pragma unroll
+        for (int r = 0; r < R; r++) load_codes<CB>(W + rbase[r] + (long)c * CB, w[r]);
+        const int k0 = c * CB * 4;
+        float xv[ND][16];
+        if (k0 + 4 * CB <= K && (((uintptr_t)(x + k0)) & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < ND; i++)
+#pragma unroll
+                for (int q = 0; q < (CB == 1 ? 1 : 4); q++) {
+                    const float4 v = *reinterpret_cast<const float4*>(x + k0 + 16 * i + 4 * q);
+                    xv[i][4 * q] = v.x; xv[i][4 * q + 1] = v.y; xv[i][4 * q + 2] = v.z; xv[i][4 * q + 3] = v.w;
+                }
+            if constexpr (CB == 1) {
+#pragma unroll
+                for (int e = 4; e < 16; e++) xv[0][e] = 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < ND; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int k = k0 + 16 * i + e;
+                    xv[i][e] = (e < 4 * CB && k < K) ? x[k] : 0.0f;
+                }
+        }
+        float xsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) xsum += xv[i][e];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ND; i++)
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const uint32_t cds = (w[r][i] >> (2 * s)) & 0x03030303u;  // codes of elements 4j+s
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        s0 = fmaf((float)((cds >> (8 * j)) & 0xffu), xv[i][4 * j + s], s0);
+                        s1 = fmaf((float)((cds >> (8 * j + 8)) & 0xffu), xv[i][4 * j + 4 + s], s1);
+                    }
+                }
+            acc[r] += (s0 + s1) - xsum;
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int CB>
+static void launch_ternary(bool i8, int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* W, const void* x,
+                           const float* xs, const float* ws, float* y, int rows, int K, int bpr) {
+#define ZT_TERN_CASE(RR)                                                                                     \
+    case RR:                                                                                                 \
+        if (i8)                                                                                              \
+            ternary_i8_kernel<CB, RR><<<g, b, 0, st>>>(W, (const int8_t*)x, xs, ws, y, rows, K, bpr);       \
+        else                                                                                                 \
+            ternary_f32_kernel<CB, RR><<<g, b, 0, st>>>(W, (const float*)x, y, rows, K, bpr);               \
+        break;
+    switch (R) {
+        ZT_TERN_CASE(8)
+        ZT_TERN_CASE(4)
+        ZT_TERN_CASE(2)
+        default:
+        ZT_TERN_CASE(1)
+    }
+#undef ZT_TERN_CASE
+}
+
+static int ternary_gemv(bool i8, const void* Wv, const void* x, const float* xs, const float* ws, float* y, int M,
+                        int K, hipStream_t st) {
+    if (M < 0 || K < 0) return (int)hipErrorInvalidValue;
+    if (M == 0) return (int)hipSuccess;
+    if (Wv == nullptr || y == nullptr || (K > 0 && x == nullptr)) return (int)hipErrorInvalidValue;
+    if (i8 && (xs == nullptr || ws == nullptr)) return (int)hipErrorInvalidValue;
+    const uint8_t* W = static_cast<const uint8_t*>(Wv);
+    const int bpr = (K + 3) / 4;
+    int CB = 1;
+    if (bpr % 16 == 0 && ((uintptr_t)W & 15) == 0) CB = 16;
+    else if (bpr % 4 == 0 && ((uintptr_t)W & 3) == 0) CB = 4;
+    const int nchunk = bpr / CB;
+    const int nwaves = nchunk <= 64 ? 1 : (nchunk >= 8 * 64 ? 8 : ceil_div(nchunk, 64));
+    const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
+    dim3 grid(ceil_div(M, R)), block(nwaves * kWave);
+    if (CB == 16) launch_ternary<16>(i8, R, grid, block, st, W, x, xs, ws, y, M, K, bpr);
+    else if (CB == 4) launch_ternary<4>(i8, R, grid, block, st, W, x, xs, ws, y, M, K, bpr);
+    else launch_ternary<1>(i8, R, grid, block, st, W, x, xs, ws, y, M, K, bpr);
+    return (int)hipGetLastError();
+}
+
+// Row-aligned codes -> fp32 {-1, 0, +1} (TernaryStorage.Slice semantics,
+// tensor/ternary_storage.go:65-71, over the row-aligned layout).
+__global__ void ternary_dequant_kernel(const uint8_t* __restrict__ W, float* __restrict__ out, int rows, int K,
+                                       int bpr) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * K) return;
+    const long r = i / K, j = i % K;
+    const int code = (W[r * bpr + j / 4] >> (2 * (j % 4))) & 3;
+    out[i] = (float)(code - 1);
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+ZT_EXPORT int zt_ternary_gemv_f32(const void* W_ternary, const float* x, float* y, int M, int K,
+                                  hipStream_t stream) {
+    return ternary_gemv(false, W_ternary, x, nullptr, nullptr, y, M, K, stream);
+}
+
+ZT_EXPORT int zt_ternary_gemv_i8(const void* W_ternary, const int8_t* x_q, const float* x_scale,
+                                 const float* w_scale, float* y, int M, int K, hipStream_t stream) {
+    return ternary_gemv(true, W_ternary, x_q, x_scale, w_scale, y, M, K, stream);
+}
+
+ZT_EXPORT int zt_dequant_ternary_f32(const void* W_ternary, float* out, int M, int K, hipStream_t stream) {
+    if (M < 0 || K < 0) return (int)hipErrorInvalidValue;
+    const long n = (long)M * K;
+    if (n == 0) return (int)hipSuccess;
+    ternary_dequant_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(W_ternary), out, M, K,
+                                                                  (K + 3) / 4);
+    return (int)hipGetLastError();
+}

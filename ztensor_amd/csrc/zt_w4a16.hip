@@ -1,0 +1,195 @@
+// W4A16 GEMV / small-batch GEMM for gfx950: 4-bit group-quantized weights
+// (GPTQ / AWQ) times fp16 activations, fp32 accumulation and fp32 output
+// (the result type of compute.MatMulW4A16, compute/w4a16.go:64-119).
+//
+// Weight layout ([rows, K], groups of `group` consecutive weights along K):
+//   packed: rows*K/2 bytes, element j at the low nibble of byte j/2 when j is
+//           even and the high nibble when odd.  This is GPTQStorage's packing
+//           (tensor/quantized_gptq.go:110-116, 145-155) with all groups
+//           concatenated (NewGPTQStorageFromRaw, :217-277), and byte for byte
+//           the same as AWQStorage's little-endian uint32 words with 8
+//           nibbles each (tensor/quantized_awq.go:97-105, 118-136).
+//   scales, zeros: fp16, one per group, [rows, K/group].  zeros may be
+//           NULL, meaning the symmetric zero-point 8.
+// Dequantization: w = (float(q) - zero) * scale (quantized_gptq.go:154).
+//
+// GEMV (VALU): lane <-> 32 consecutive weights (16 bytes, one 128-bit load),
+// R rows per wave with the lane's activations held in registers, split-K
+// over the waves of a workgroup.  Inside a chunk (one group, since group is
+// a multiple of 32):
+//     sum_j (q_j - z) x_j * s = s * (sum_j q_j x_j - z * sum_j x_j)
+// q_j becomes an exact fp16 by OR-ing the nibble into the mantissa of 1024.0
+// (0x6400 | q == 1024 + q) and subtracting 1024 with one packed fp16 add for
+// two weights; v_dot2_f32_f16 then multiplies two exact fp16 products and
+// accumulates them in fp32.  Nibble pairs are taken as (w >> 4t) &
+// 0x000F000F, which pairs element e with e+4 inside each dword; the
+// activations are pre-permuted into the same pairs once per lane.
+//
+// Small-batch GEMM (N >= 4): v_mfma_f32_16x16x32_f16 with the dequantized
+// weights as the A operand (16 rows x 32 K) and the activations as the B
+// operand (32 K x 16 batch columns, zero-padded past N); see the MFMA section.
+#include "zt_common.h"
+
+namespace zt {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+// Two nibbles (bits 0-3 and 16-19 of v after the mask) -> exact fp16 pair.
+__device__ __forceinline__ half2v nib_pair(uint32_t v) {
+    const half2v biased = as_h2((v & 0x000F000Fu) | 0x64006400u);  // 1024 + q
+    return biased - (half2v){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// fp16 activations of one 32-weight chunk, permuted into the nibble-pair
+// order: xp[i][t] = (x[8i+t], x[8i+t+4]).
+__device__ __forceinline__ void permute_x(const uint32_t (&xr)[16], uint32_t (&xp)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t X0 = xr[4 * i], X1 = xr[4 * i + 1], X2 = xr[4 * i + 2], X3 = xr[4 * i + 3];
+        xp[i][0] = __builtin_amdgcn_perm(X2, X0, 0x05040100u);  // (x0, x4)
+        xp[i][1] = __builtin_amdgcn_perm(X2, X0, 0x07060302u);  // (x1, x5)
+        xp[i][2] = __builtin_amdgcn_perm(X3, X1, 0x05040100u);  // (x2, x6)
+        xp[i][3] = __builtin_amdgcn_perm(X3, X1, 0x07060302u);  // (x3, x7)
+    }
+}
+
+template <int R, bool CONTIG>
+__global__ void __launch_bounds__(512) w4a16_gemv_kernel(const uint4* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ zeros,
+                                                         const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                         long xy_stride, int rows, int nchunk, int chunks_per_group) {
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    x += blockIdx.y;
+    y += blockIdx.y;
+    const int ngroups = nchunk / chunks_per_group;
+    const int row0 = blockIdx.x * R;
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rr[r] = min(row0 + r, rows - 1);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int c = wave * kWave + lane; c < nchunk; c += nwaves * kWave) {
+        const int g = c / chunks_per_group;
+        uint4 w[R];
+        uint16_t s[R], z[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = ld_stream(&packed[(long)rr[r] * nchunk + c]);
+            s[r] = scales[(long)rr[r] * ngroups + g];
+            z[r] = zeros ? zeros[(long)rr[r] * ngroups + g] : (uint16_t)0x4800;  // fp16 8.0
+        }
+        uint32_t xr[16];
+        if constexpr (CONTIG) {
+            const uint4* p = reinterpret_cast<const uint4*>(x + (long)c * 32);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 t = p[i];
+                xr[4 * i] = t.x; xr[4 * i + 1] = t.y; xr[4 * i + 2] = t.z; xr[4 * i + 3] = t.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                xr[i] = (uint32_t)x[((long)c * 32 + 2 * i) * xy_stride] |
+                        ((uint32_t)x[((long)c * 32 + 2 * i + 1) * xy_stride] << 16);
+        }
+        uint32_t xp[4][4];
+        permute_x(xr, xp);
+        float xsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) xsum = __builtin_amdgcn_fdot2(as_h2(xr[i]), as_h2(0x3c003c00u), xsum, false);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                s0 = __builtin_amdgcn_fdot2(nib_pair(d[i]), as_h2(xp[i][0]), s0, false);
+                s1 = __builtin_amdgcn_fdot2(nib_pair(d[i] >> 4), as_h2(xp[i][1]), s1, false);
+                s0 = __builtin_amdgcn_fdot2(nib_pair(d[i] >> 8), as_h2(xp[i][2]), s0, false);
+                s1 = __builtin_amdgcn_fdot2(nib_pair(d[i] >> 12), as_h2(xp[i][3]), s1, false);
+            }
+            acc[r] = fmaf(h2f(s[r]), (s0 + s1) - h2f(z[r]) * xsum, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, xy_stride, row0, rows);
+}
+
+template <bool CONTIG>
+static void launch_w4a16_gemv(int R, dim3 g, dim3 b, hipStream_t st, const uint4* w, const uint16_t* s,
+                              const uint16_t* z, const uint16_t* x, float* y, long stride, int rows, int nchunk,
+                              int cpg) {
+    switch (R) {
+        case 8: w4a16_gemv_kernel<8, CONTIG><<<g, b, 0, st>>>(w, s, z, x, y, stride, rows, nchunk, cpg); break;
+        case 4: w4a16_gemv_kernel<4, CONTIG><<<g, b, 0, st>>>(w, s, z, x, y, stride, rows, nchunk, cpg); break;
+        case 2: w4a16_gemv_kernel<2, CONTIG><<<g, b, 0, st>>>(w, s, z, x, y, stride, rows, nchunk, cpg); break;
+        default: w4a16_gemv_kernel<1, CONTIG><<<g, b, 0, st>>>(w, s, z, x, y, stride, rows, nchunk, cpg); break;
+    }
+}
+
+// ------------------------------------------------------------ dequantize
+
+// One thread per 32-weight chunk; bit-exact with GPTQStorage.Dequantize.
+__global__ void w4_dequant_kernel(const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
+                                  const uint16_t* __restrict__ zeros, float* __restrict__ out, long nchunk,
+                                  int chunks_per_group) {
+    const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= nchunk) return;
+    const long g = c / chunks_per_group;
+    const float s = h2f(scales[g]);
+    const float z = zeros ? h2f(zeros[g]) : 8.0f;
+    const uint4 w = packed[c];
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    float* o = out + c * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int q = (int)((d[i / 8] >> (4 * (i % 8))) & 0xfu);
+        o[i] = ((float)q - z) * s;
+    }
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros,
+                                const uint16_t* B, float* C, int M, int K, int N, int group_size,
+                                hipStream_t stream) {
+    if (M < 0 || N < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0 || N > 65535)
+        return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    if (W_packed == nullptr || scales == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_packed & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1))
+        return (int)hipErrorInvalidValue;
+    if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
+    const int nchunk = K / 32;
+    const int nwaves = nchunk <= 64 ? 1 : (nchunk >= 8 * 64 ? 8 : ceil_div(nchunk, 64));
+    const int R = pick_rows_per_wave(M, nwaves, N, 2048);
+    dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
+    const uint4* w = static_cast<const uint4*>(W_packed);
+    if (N == 1)
+        launch_w4a16_gemv<true>(R, grid, block, stream, w, scales, zeros, B, C, 1, M, nchunk, group_size / 32);
+    else
+        launch_w4a16_gemv<false>(R, grid, block, stream, w, scales, zeros, B, C, N, M, nchunk, group_size / 32);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out,
+                                long nelem, int group_size, hipStream_t stream) {
+    if (nelem < 0 || group_size <= 0 || group_size % 32 != 0 || nelem % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    if (nelem == 0) return (int)hipSuccess;
+    if ((uintptr_t)W_packed & 15) return (int)hipErrorInvalidValue;
+    const long nchunk = nelem / 32;
+    w4_dequant_kernel<<<ceil_div(nchunk, 256), 256, 0, stream>>>(static_cast<const uint4*>(W_packed), scales, zeros,
+                                                                  out, nchunk, group_size / 32);
+    return (int)hipGetLastError();
+}

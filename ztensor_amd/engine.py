@@ -1,0 +1,217 @@
+"""ROCmEngine: the quantized-matmul surface of ztensor's compute engine on MI355X.
+
+Two levels, as in the reference:
+
+* KernelRunner level (internal/gpuapi/kernels.go:45-81): gemm_q4_f32,
+  gemm_q8_f32, ... take raw device pointers and integers and call the C ABI
+  of libzt_hip.so on the engine's stream.  These replace the ROCm stubs
+  that return "not implemented" (internal/gpuapi/rocm_kernels.go:109-135).
+* Engine level: upload_weights (WeightUploader.UploadWeights,
+  compute/engine.go:36-38; compute/gpu_engine.go:778-1050), matmul with the
+  storage-type dispatch of GPUEngine.MatMul (compute/gpu_engine.go:1409-1470,
+  2115-2200) and CPUEngine.tryQuantizedMatMul (compute/cpu_engine.go:2277-2523),
+  matmul_w4a16 (W4A16MatMuler, compute/w4a16.go:137-168) and ternary_gemv
+  (TernaryGEMVGPU, compute/ternary_gemv_gpu.go:18-25).
+
+Device memory and the stream come from PyTorch; every byte of arithmetic on
+the path runs in libzt_hip.so.  There is no CPU fallback: a kernel error
+raises ZTError (the reference falls back to its CPU engine; here the caller
+decides).
+"""
+from __future__ import annotations
+
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import _lib
+from .storage import (
+    AWQStorage,
+    Float16Storage,
+    GPTQStorage,
+    GPUBuffer,
+    IQ4NLStorage,
+    Q4Storage,
+    Q8Storage,
+    Tensor,
+    TernaryStorage,
+)
+
+
+def _p(t: torch.Tensor | None) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+class ROCmEngine:
+    def __init__(self, device: int = 0, stream: torch.cuda.Stream | None = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("ROCmEngine needs a ROCm GPU (torch.cuda.is_available() is False)")
+        self.device = torch.device("cuda", device)
+        self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
+        self.lib = _lib.load()
+
+    @property
+    def _s(self) -> int:
+        return self.stream.cuda_stream
+
+    # ------------------------------------------------------ KernelRunner level
+
+    def gemm_q4_f32(self, a_q4: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
+        self.lib.call("zt_gemm_q4_f32", a_q4, b, c, m, k, n, data_offset, self._s)
+
+    def gemm_q4_f16(self, a_q4: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
+        self.lib.call("zt_gemm_q4_f16", a_q4, b, c, m, k, n, data_offset, self._s)
+
+    def gemm_iq4nl_f32(self, a: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
+        self.lib.call("zt_gemm_iq4nl_f32", a, b, c, m, k, n, data_offset, self._s)
+
+    def gemm_iq4nl_f16(self, a: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
+        self.lib.call("zt_gemm_iq4nl_f16", a, b, c, m, k, n, data_offset, self._s)
+
+    def gemm_q8_f32(self, a_q8: int, b: int, c: int, m: int, k: int, n: int) -> None:
+        self.lib.call("zt_gemm_q8_f32", a_q8, b, c, m, k, n, self._s)
+
+    def gemm_q8sep_f32(self, a_q8: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
+        self.lib.call("zt_gemm_q8sep_f32", a_q8, b, c, m, k, n, data_offset, self._s)
+
+    def gemm_w4a16_f32(self, w: int, scales: int, zeros: int, b: int, c: int, m: int, k: int, n: int,
+                       group_size: int) -> None:
+        self.lib.call("zt_gemm_w4a16_f32", w, scales, zeros, b, c, m, k, n, group_size, self._s)
+
+    def ternary_gemv_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
+        self.lib.call("zt_ternary_gemv_f32", w, x, y, m, k, self._s)
+
+    def ternary_gemv_i8(self, w: int, xq: int, x_scale: int, w_scale: int, y: int, m: int, k: int) -> None:
+        self.lib.call("zt_ternary_gemv_i8", w, xq, x_scale, w_scale, y, m, k, self._s)
+
+    # ------------------------------------------------------------ residency
+
+    def _to_dev(self, host: np.ndarray) -> torch.Tensor:
+        t = torch.from_numpy(np.ascontiguousarray(host).view(np.uint8).reshape(-1))
+        return t.to(self.device, non_blocking=False)
+
+    def upload_weights(self, storages: list[Any]) -> int:
+        """Copies each quantized storage to the device once, in its GPU layout,
+        and records the buffer with set_gpu_ptr (compute/gpu_engine.go:778-818).
+        Returns the number of storages uploaded."""
+        n = 0
+        for s in storages:
+            if isinstance(s, (Q4Storage, IQ4NLStorage, Q8Storage)):
+                if s.gpu_ptr() is None:
+                    buf = s.raw_bytes_gpu()
+                    s.set_gpu_ptr(GPUBuffer(self._to_dev(buf), buf.size, self.device.index or 0,
+                                            s.gpu_data_offset()))
+                    n += 1
+            elif isinstance(s, (GPTQStorage, AWQStorage)):
+                if s.gpu_ptr() is None:
+                    packed = s.data if isinstance(s, GPTQStorage) else s.packed_bytes()
+                    if isinstance(s, GPTQStorage) and s.bits != 4:
+                        raise ValueError("only 4-bit GPTQ weights are on the W4A16 path")
+                    t = self._to_dev(packed)
+                    sc = self._to_dev(s.scales).view(torch.int16)
+                    zr = self._to_dev(s.zeros).view(torch.int16)
+                    s.set_gpu_ptr(GPUBuffer(t, packed.size, self.device.index or 0))
+                    s._gpu_scales, s._gpu_zeros = sc, zr  # type: ignore[attr-defined]
+                    n += 1
+        return n
+
+    # ---------------------------------------------------------------- matmul
+
+    def matmul(self, a: Tensor | torch.Tensor, b: Tensor | torch.Tensor) -> torch.Tensor:
+        """C = A @ B where one operand is a quantized weight Tensor and the
+        other an fp32 (or fp16, for the W4A16 formats) device tensor.
+
+        A-side weight: A is [M, K] (blocks along K), B is [K, N] -> C [M, N].
+        B-side weight: B is the virtually transposed weight, logical [K, N],
+        physical [N, K] (compute/cpu_engine.go:1378-1390); A is [M, K];
+        C [M, N] is computed as (W[N,K] @ A^T)^T, as matMulQ4BWeight does
+        (compute/gpu_engine.go:2115-2200)."""
+        if isinstance(a, Tensor):
+            rows, k = a.shape[-2], a.shape[-1]
+            x = b
+            if x.shape[0] != k:
+                raise ValueError(f"matmul: A is [{rows},{k}] but B has {x.shape[0]} rows")
+            return self._weight_times(a.storage, rows, k, x.contiguous())
+        if isinstance(b, Tensor):
+            k, nout = b.shape[-2], b.shape[-1]
+            if a.shape[-1] != k:
+                raise ValueError(f"matmul: A has {a.shape[-1]} columns but B is [{k},{nout}]")
+            m = a.numel() // k
+            xt = a.reshape(m, k).t().contiguous()  # [K, M]
+            ct = self._weight_times(b.storage, nout, k, xt)  # [Nout, M]
+            return ct.t().contiguous().reshape(*a.shape[:-1], nout)
+        raise TypeError("matmul: neither operand is a quantized weight Tensor")
+
+    def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
+        """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
+        n = 1 if x.dim() == 1 else x.shape[1]
+        if x.device != self.device:
+            raise ValueError("activations must be on the engine's device")
+        self.upload_weights([s])
+        c = torch.empty((rows, n), dtype=torch.float32, device=self.device)
+        buf = s.gpu_ptr()
+        if isinstance(s, Q4Storage):
+            if x.dtype == torch.float32:
+                self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype == torch.float16:
+                self.gemm_q4_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            else:
+                raise TypeError(f"Q4_0 matmul: unsupported activation dtype {x.dtype}")
+        elif isinstance(s, IQ4NLStorage):
+            if x.dtype == torch.float32:
+                self.gemm_iq4nl_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype == torch.float16:
+                self.gemm_iq4nl_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            else:
+                raise TypeError(f"IQ4_NL matmul: unsupported activation dtype {x.dtype}")
+        elif isinstance(s, Q8Storage):
+            if x.dtype != torch.float32:
+                raise TypeError("Q8_0 matmul takes fp32 activations")
+            self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+        elif isinstance(s, (GPTQStorage, AWQStorage)):
+            if x.dtype != torch.float16:
+                raise TypeError("W4A16 matmul takes fp16 activations")
+            self.gemm_w4a16_f32(_p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(x), _p(c), rows, k, n,
+                                s.group_size)
+        else:
+            raise TypeError(f"matmul: {type(s).__name__} is not a quantized weight storage")
+        return c
+
+    def matmul_w4a16(self, a: Tensor, b: Tensor) -> torch.Tensor:
+        """W4A16MatMuler.MatMulW4A16 (compute/w4a16.go:137-143): one operand
+        holds 4-bit weights (Q4_0, GPTQ bits=4 or AWQ), the other a
+        Float16Storage; the result is fp32 (compute/w4a16.go:64-119)."""
+        w, act, side = _detect_w4a16(a, b)
+        if w is None:
+            raise ValueError("MatMulW4A16: inputs are not W4A16 - need 4-bit weights and FP16 activations")
+        x = torch.from_numpy(act.storage.data.view(np.float16)).to(self.device)
+        if side == "A":
+            return self.matmul(w, x.reshape(act.shape))
+        return self.matmul(x.reshape(act.shape), w)
+
+    # ---------------------------------------------------------------- ternary
+
+    def ternary_gemv(self, weights: TernaryStorage, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        """TernaryGEMVGPU (compute/ternary_gemv_gpu.go:18-91): host weights and
+        x in, host y out; the weights are repacked to row-aligned bytes and
+        uploaded for the call (the reference does the same per call)."""
+        w = self._to_dev(weights.row_aligned(rows, cols))
+        xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device)
+        y = torch.empty(rows, dtype=torch.float32, device=self.device)
+        self.ternary_gemv_f32(_p(w), _p(xd), _p(y), rows, cols)
+        return y.cpu().numpy()
+
+
+def _detect_w4a16(a: Tensor, b: Tensor):
+    """detectW4A16 (compute/w4a16.go:27-62)."""
+
+    def w4(s):
+        return isinstance(s, (Q4Storage, AWQStorage)) or (isinstance(s, GPTQStorage) and s.bits == 4)
+
+    if isinstance(a, Tensor) and isinstance(b, Tensor):
+        if w4(a.storage) and isinstance(b.storage, Float16Storage):
+            return a, b, "A"
+        if w4(b.storage) and isinstance(a.storage, Float16Storage):
+            return b, a, "B"
+    return None, None, ""

@@ -1,0 +1,261 @@
+"""Host-side quantized storage types, mirroring the reference's tensor package.
+
+Each class holds the reference's serialised bytes on the host (numpy) and
+knows its device upload layout.  Names and semantics follow the Go types so a
+caller of tensor.Q4Storage & co. finds the same surface:
+
+  Q4Storage      tensor/quantized.go:22-274   (RawBytes, RawBytesGPU, NumBlocks, SetGPUPtr/GPUPtr)
+  Q8Storage      tensor/quantized.go:288-478  (36-byte blocks, fp32 scale)
+  IQ4NLStorage   tensor/iq4_storage.go:48-142
+  GPTQStorage    tensor/quantized_gptq.go:30-280 (bits = 4 for W4A16)
+  AWQStorage     tensor/quantized_awq.go:30-321
+  TernaryStorage tensor/ternary_storage.go:7-95
+  Float16Storage tensor/fp16_storage.go:14-122
+
+Dequantization on the host is not offered here on purpose: the product path
+dequantizes on the GPU (zt_dequant_*), and the CPU restatement used to check
+it lives in the test-only oracle.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
+
+from . import _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data_as(C.c_void_p).value or 0
+
+
+@dataclass
+class GPUBuffer:
+    """A device copy set by the engine's upload (SetGPUPtr); the caller (the
+    engine) owns the memory, as in tensor/quantized.go:200-212."""
+
+    tensor: Any  # torch.Tensor (uint8, on the device)
+    nbytes: int
+    device_id: int
+    data_offset: int = 0
+
+
+class _GPUPtrMixin:
+    _gpu: GPUBuffer | None
+
+    def set_gpu_ptr(self, buf: GPUBuffer | None) -> None:
+        self._gpu = buf
+
+    def gpu_ptr(self) -> GPUBuffer | None:
+        return self._gpu
+
+
+@dataclass
+class Q4Storage(_GPUPtrMixin):
+    raw: np.ndarray  # 18-byte blocks
+    len: int
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    @staticmethod
+    def from_raw(raw: np.ndarray, num_elements: int) -> "Q4Storage":
+        """NewQ4StorageFromRaw (tensor/quantized.go:247-264)."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        nblk = (num_elements + 31) // 32
+        raw = np.asarray(raw, np.uint8).reshape(-1)
+        if raw.size < nblk * 18:
+            raise ValueError(f"Q4_0 raw data too short: need {nblk * 18} bytes for {nblk} blocks, got {raw.size}")
+        return Q4Storage(raw[: nblk * 18].copy(), num_elements)
+
+    def num_blocks(self) -> int:
+        return (self.len + 31) // 32
+
+    def byte_size(self) -> int:
+        return self.num_blocks() * 18
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.raw
+
+    def raw_bytes_gpu(self) -> np.ndarray:
+        """RawBytesGPU (tensor/quantized.go:168-187), built by the library."""
+        lib = _lib.load()
+        nblk = self.num_blocks()
+        out = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_q4_raw_to_gpu(_ptr(self.raw), nblk, _ptr(out))
+        return out
+
+    def gpu_data_offset(self) -> int:
+        """Q4GPUDataOffset (tensor/quantized.go:195-198)."""
+        return _lib.load().zt_q4_gpu_data_offset(self.num_blocks())
+
+
+@dataclass
+class IQ4NLStorage(_GPUPtrMixin):
+    raw: np.ndarray
+    len: int
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    @staticmethod
+    def from_raw(raw: np.ndarray, num_elements: int) -> "IQ4NLStorage":
+        """NewIQ4NLStorageFromRaw (tensor/iq4_storage.go:60-72)."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        nblk = (num_elements + 31) // 32
+        raw = np.asarray(raw, np.uint8).reshape(-1)
+        if raw.size < nblk * 18:
+            raise ValueError(f"IQ4_NL raw data too short: need {nblk * 18} bytes for {nblk} blocks, got {raw.size}")
+        return IQ4NLStorage(raw[: nblk * 18].copy(), num_elements)
+
+    def num_blocks(self) -> int:
+        return (self.len + 31) // 32
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.raw
+
+    def raw_bytes_gpu(self) -> np.ndarray:
+        lib = _lib.load()
+        nblk = self.num_blocks()
+        out = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_iq4nl_raw_to_gpu(_ptr(self.raw), nblk, _ptr(out))
+        return out
+
+    def gpu_data_offset(self) -> int:
+        return _lib.load().zt_q4_gpu_data_offset(self.num_blocks())
+
+
+@dataclass
+class Q8Storage(_GPUPtrMixin):
+    raw: np.ndarray  # 36-byte blocks
+    len: int
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    @staticmethod
+    def from_blocks(scales: np.ndarray, quants: np.ndarray, num_elements: int) -> "Q8Storage":
+        """NewQ8StorageFromBlocks (tensor/quantized.go:457-475)."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        nblk = (num_elements + 31) // 32
+        scales = np.asarray(scales, np.float32).reshape(-1)
+        quants = np.asarray(quants, np.int8).reshape(-1)
+        if scales.size != nblk:
+            raise ValueError(f"expected {nblk} scales for {num_elements} elements, got {scales.size}")
+        if quants.size != nblk * 32:
+            raise ValueError(f"expected {nblk * 32} quants for {nblk} blocks, got {quants.size}")
+        raw = np.empty((nblk, 36), np.uint8)
+        raw[:, :4] = scales.astype("<f4").reshape(nblk, 1).view(np.uint8)
+        raw[:, 4:] = quants.reshape(nblk, 32).view(np.uint8)
+        return Q8Storage(raw.reshape(-1), num_elements)
+
+    def num_blocks(self) -> int:
+        return (self.len + 31) // 32
+
+    def byte_size(self) -> int:
+        return self.num_blocks() * 36
+
+    def raw_bytes(self) -> np.ndarray:
+        """RawBytes (tensor/quantized.go:427-438)."""
+        return self.raw
+
+    def raw_bytes_gpu(self) -> np.ndarray:
+        lib = _lib.load()
+        nblk = self.num_blocks()
+        out = np.empty(lib.zt_q8_gpu_bytes(nblk), np.uint8)
+        lib.zt_q8_raw_to_gpu(_ptr(self.raw), nblk, _ptr(out))
+        return out
+
+    def gpu_data_offset(self) -> int:
+        return _lib.load().zt_q8_gpu_data_offset(self.num_blocks())
+
+
+@dataclass
+class GPTQStorage(_GPUPtrMixin):
+    data: np.ndarray  # packed groups, concatenated
+    scales: np.ndarray  # uint16 fp16 bits, one per group
+    zeros: np.ndarray  # uint16 fp16 bits, one per group
+    len: int
+    group_size: int
+    bits: int = 4
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    @staticmethod
+    def from_raw(data, scales, zeros, num_elements: int, group_size: int, bits: int) -> "GPTQStorage":
+        """NewGPTQStorageFromRaw (tensor/quantized_gptq.go:217-277)."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        if bits not in (4, 8):
+            raise ValueError(f"bits must be 4 or 8, got {bits}")
+        ng = (num_elements + group_size - 1) // group_size
+        scales = np.asarray(scales, np.uint16).reshape(-1)
+        zeros = np.asarray(zeros, np.uint16).reshape(-1)
+        if scales.size != ng:
+            raise ValueError(f"expected {ng} scales for {ng} groups, got {scales.size}")
+        if zeros.size != ng:
+            raise ValueError(f"expected {ng} zeros for {ng} groups, got {zeros.size}")
+        total = 0
+        for gi in range(ng):
+            cnt = min(group_size, num_elements - gi * group_size)
+            total += (cnt + 1) // 2 if bits == 4 else cnt
+        data = np.asarray(data, np.uint8).reshape(-1)
+        if data.size < total:
+            raise ValueError(f"GPTQ data too short: need {total} bytes, got {data.size}")
+        return GPTQStorage(data[:total].copy(), scales.copy(), zeros.copy(), num_elements, group_size, bits)
+
+    def num_groups(self) -> int:
+        return self.scales.size
+
+    def byte_size(self) -> int:
+        return self.data.size + 4 * self.num_groups()
+
+
+@dataclass
+class AWQStorage(_GPUPtrMixin):
+    words: np.ndarray  # uint32, 8 nibbles each, groups concatenated
+    scales: np.ndarray
+    zeros: np.ndarray
+    len: int
+    group_size: int
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    def packed_bytes(self) -> np.ndarray:
+        """The words' little-endian bytes: identical to GPTQ 4-bit packing when
+        the group size is a multiple of 8 (tensor/quantized_awq.go:97-105)."""
+        return self.words.astype("<u4").view(np.uint8)
+
+
+@dataclass
+class TernaryStorage:
+    data: np.ndarray  # flat 2-bit packing
+    len: int
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.data
+
+    def row_aligned(self, rows: int, cols: int) -> np.ndarray:
+        """The per-row byte-aligned layout of compute/ternary_gemv_gpu.go:55-67."""
+        lib = _lib.load()
+        out = np.empty(rows * ((cols + 3) // 4), np.uint8)
+        lib.zt_ternary_repack_rows(_ptr(self.data), rows, cols, _ptr(out))
+        return out
+
+
+@dataclass
+class Float16Storage(_GPUPtrMixin):
+    data: np.ndarray  # uint16 fp16 bits
+    len: int
+    _gpu: GPUBuffer | None = field(default=None, repr=False)
+
+    @staticmethod
+    def from_raw(raw: np.ndarray, num_elems: int) -> "Float16Storage":
+        """NewFloat16StorageFromRaw (tensor/fp16_storage.go:42-46)."""
+        return Float16Storage(np.asarray(raw).view(np.uint16).reshape(-1)[:num_elems].copy(), num_elems)
+
+
+@dataclass
+class Tensor:
+    """A shaped view over a storage (the subset of tensor.TensorNumeric the
+    matmul dispatch reads: shape and storage type)."""
+
+    shape: tuple[int, ...]
+    storage: Any

@@ -1,0 +1,213 @@
+"""Seeded synthetic weights and activations for the decode-path workloads.
+
+Every generator returns the reference's own serialised format (the bytes
+RawBytes()/NewXStorageFromRaw use), so the same arrays feed the oracle and,
+after the load-time repack, the GPU.  Distributions follow the benchmark
+configurations of this path:
+
+  Q4_0     nibbles U[0,15], fp16 block scale |N(0,1)|*0.02, fp32 x ~ N(0,1)
+  Q8_0     int8 U[-127,127], fp32 block scale |N(0,1)|*0.02
+  W4A16    uint4 U[0,15], group 128, fp16 scales |N(0,1)|*0.02, zero-point 8,
+           fp16 x ~ N(0,1)
+  IQ4_NL   nibbles U[0,15], fp16 block scale |N(0,1)|*0.01, fp16 x ~ N(0,1)
+  Ternary  w in {-1,0,+1} with p = {.25,.5,.25}, one fp32 weight scale,
+           int8 x = clip(round(N(0,1)*32), -127, 127) with an fp32 scale
+
+Seeds are 0x5EED0000 + 16*config + shape (numpy PCG64), so any host
+regenerates identical inputs.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+SEED_BASE = 0x5EED0000
+
+
+def seed_for(config: int, shape: int = 0) -> int:
+    return SEED_BASE + 16 * config + shape
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def f16_bits(a: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 bits (round to nearest even) as uint16."""
+    return np.asarray(a, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+# --------------------------------------------------------------- packers
+
+
+def pack_q4_0(nib: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """Nibbles [nblk,32] (0..15) and fp16 scale bits [nblk] -> 18-byte Q4_0
+    blocks (tensor/quantized.go:146-156): low nibble = element j, high
+    nibble = element j+16."""
+    nib = nib.reshape(-1, 32).astype(np.uint8)
+    nblk = nib.shape[0]
+    out = np.empty((nblk, 18), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").reshape(nblk, 1).view(np.uint8)
+    out[:, 2:] = nib[:, :16] | (nib[:, 16:] << 4)
+    return out.reshape(-1)
+
+
+def pack_iq4nl(nib: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """Nibbles [nblk,32] -> 18-byte IQ4_NL blocks, interleaved order
+    (tensor/iq4_storage.go:36-46): byte i = element 2i | element 2i+1 << 4."""
+    nib = nib.reshape(-1, 32).astype(np.uint8)
+    nblk = nib.shape[0]
+    out = np.empty((nblk, 18), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").reshape(nblk, 1).view(np.uint8)
+    out[:, 2:] = nib[:, 0::2] | (nib[:, 1::2] << 4)
+    return out.reshape(-1)
+
+
+def pack_q8_0(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """int8 [nblk,32] and fp32 scales [nblk] -> 36-byte Q8_0 blocks
+    (tensor/quantized.go:425-438)."""
+    q = q.reshape(-1, 32).astype(np.int8)
+    nblk = q.shape[0]
+    out = np.empty((nblk, 36), np.uint8)
+    out[:, 0:4] = scale.astype("<f4").reshape(nblk, 1).view(np.uint8)
+    out[:, 4:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def pack_nibbles_interleaved(q: np.ndarray) -> np.ndarray:
+    """uint4 values [.., K] -> bytes [.., K/2], element j at the low nibble
+    of byte j/2 when even, high when odd (GPTQ bits=4,
+    tensor/quantized_gptq.go:110-116; AWQ words, tensor/quantized_awq.go:97-105)."""
+    q = q.astype(np.uint8)
+    return q[..., 0::2] | (q[..., 1::2] << 4)
+
+
+def pack_ternary(w: np.ndarray) -> np.ndarray:
+    """{-1,0,1} values (flat, row-major) -> 2-bit codes, 4 per byte, element
+    i at bits 2*(i%4) of byte i/4 (tensor/ternary_storage.go:49-62)."""
+    codes = (w.reshape(-1).astype(np.int16) + 1).astype(np.uint8)
+    pad = (-codes.size) % 4
+    # NewTernaryStorage zero-fills its bytes, so unused codes of the last byte are 00.
+    codes = np.concatenate([codes, np.zeros(pad, np.uint8)])
+    c = codes.reshape(-1, 4)
+    out = c[:, 0] | (c[:, 1] << 2) | (c[:, 2] << 4) | (c[:, 3] << 6)
+    return out.astype(np.uint8)
+
+
+# ------------------------------------------------------------ workloads
+
+
+@dataclass
+class Q4Weights:
+    rows: int
+    K: int
+    raw: np.ndarray  # 18-byte blocks
+
+
+@dataclass
+class Q8Weights:
+    rows: int
+    K: int
+    raw: np.ndarray  # 36-byte blocks
+
+
+@dataclass
+class IQ4Weights:
+    rows: int
+    K: int
+    raw: np.ndarray  # 18-byte blocks
+
+
+@dataclass
+class W4Weights:
+    rows: int
+    K: int
+    group: int
+    packed: np.ndarray  # uint8 [rows, K/2]
+    scales: np.ndarray  # uint16 fp16 bits [rows, K/group]
+    zeros: np.ndarray  # uint16 fp16 bits [rows, K/group]
+
+
+@dataclass
+class TernaryWeights:
+    rows: int
+    K: int
+    raw: np.ndarray  # flat 2-bit packing, ceil(rows*K/4) bytes
+    w_scale: np.float32 = field(default_factory=lambda: np.float32(1.0))
+
+
+def q4_0(rows: int, K: int, seed: int) -> Q4Weights:
+    g = rng(seed)
+    nblk = rows * K // 32
+    nib = g.integers(0, 16, size=(nblk, 32), dtype=np.uint8)
+    d = f16_bits(np.abs(g.standard_normal(nblk, dtype=np.float32)) * np.float32(0.02))
+    return Q4Weights(rows, K, pack_q4_0(nib, d))
+
+
+def q8_0(rows: int, K: int, seed: int) -> Q8Weights:
+    g = rng(seed)
+    nblk = rows * K // 32
+    q = g.integers(-127, 128, size=(nblk, 32), dtype=np.int16).astype(np.int8)
+    s = (np.abs(g.standard_normal(nblk, dtype=np.float32)) * np.float32(0.02)).astype(np.float32)
+    return Q8Weights(rows, K, pack_q8_0(q, s))
+
+
+def iq4nl(rows: int, K: int, seed: int) -> IQ4Weights:
+    g = rng(seed)
+    nblk = rows * K // 32
+    nib = g.integers(0, 16, size=(nblk, 32), dtype=np.uint8)
+    d = f16_bits(np.abs(g.standard_normal(nblk, dtype=np.float32)) * np.float32(0.01))
+    return IQ4Weights(rows, K, pack_iq4nl(nib, d))
+
+
+def w4a16(rows: int, K: int, seed: int, group: int = 128, zero_point: float = 8.0) -> W4Weights:
+    g = rng(seed)
+    q = g.integers(0, 16, size=(rows, K), dtype=np.uint8)
+    ng = K // group
+    s = f16_bits(np.abs(g.standard_normal((rows, ng), dtype=np.float32)) * np.float32(0.02))
+    z = np.full((rows, ng), f16_bits(np.float32(zero_point)), np.uint16)
+    return W4Weights(rows, K, group, pack_nibbles_interleaved(q), s, z)
+
+
+def ternary(rows: int, K: int, seed: int) -> TernaryWeights:
+    g = rng(seed)
+    w = g.choice(np.array([-1, 0, 1], np.int8), size=rows * K, p=[0.25, 0.5, 0.25])
+    w_scale = np.float32(np.abs(g.standard_normal(dtype=np.float32)) * np.float32(0.02) + np.float32(0.01))
+    return TernaryWeights(rows, K, pack_ternary(w), w_scale)
+
+
+def x_f32(n: int, seed: int) -> np.ndarray:
+    return rng(seed ^ 0xA5A5).standard_normal(n, dtype=np.float32)
+
+
+def x_f16(n: int, seed: int) -> np.ndarray:
+    """fp16 activation bits (uint16)."""
+    return f16_bits(rng(seed ^ 0xA5A5).standard_normal(n, dtype=np.float32))
+
+
+def x_i8(n: int, seed: int) -> tuple[np.ndarray, np.float32]:
+    g = rng(seed ^ 0xA5A5)
+    q = np.clip(np.rint(g.standard_normal(n, dtype=np.float32) * np.float32(32.0)), -127, 127).astype(np.int8)
+    x_scale = np.float32(np.float32(1.0) / np.float32(32.0))
+    return q, x_scale
+
+
+# ---------------------------------------------------------- byte counts
+
+def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128, zeros: bool = True) -> int:
+    """Bytes one call must move at minimum: weights + scales (+zeros) +
+    activations + output, each read or written once."""
+    nblk = rows * K // 32
+    if fmt == "q4_0":
+        return nblk * 18 + 4 * K * N + 4 * rows * N
+    if fmt == "q8_0":
+        return nblk * 36 + 4 * K * N + 4 * rows * N
+    if fmt == "iq4nl":
+        return nblk * 18 + 2 * K * N + 4 * rows * N
+    if fmt == "w4a16":
+        ng = rows * K // group
+        return rows * K // 2 + 2 * ng * (2 if zeros else 1) + 2 * K * N + 4 * rows * N
+    if fmt == "ternary_i8":
+        return rows * ((K + 3) // 4) + K * N + 4 * rows * N + 8
+    raise ValueError(fmt)
