@@ -231,6 +231,117 @@ def run_headline(args) -> dict:
     }
 
 
+# ------------------------------------------------------------ suite mode
+
+SUITE = {
+    # name: (format, [(rows = N_out, K)], batches)
+    "w4a16_c1": ("w4a16", [(4096, 4096)], [1]),
+    "q4_0": ("q4_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q4_0_merged": ("q4_0", [(6144, 4096), (28672, 4096)], [1]),
+    "q8_0": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q8_0_raw": ("q8_0_raw", [(4096, 4096), (14336, 4096)], [1]),
+    "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
+    "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
+    "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
+}
+
+
+def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> dict:
+    from ztensor_amd import synth
+
+    s = torch.cuda.current_stream().cuda_stream
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+    if fmt == "q4_0" or fmt == "iq4nl":
+        w = synth.q4_0(rows, K, seed) if fmt == "q4_0" else synth.iq4nl(rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_q4_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+        wbufs = [dev(host)]
+        off = lib.zt_q4_gpu_data_offset(nblk)
+        if fmt == "q4_0":
+            x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+            fn = lambda wb, y: lib.zt_gemm_q4_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
+        else:
+            x = dev(synth.x_f16(K * N, seed))
+            fn = lambda wb, y: lib.zt_gemm_iq4nl_f16(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off,
+                                                     s)
+        nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
+    elif fmt in ("q8_0", "q8_0_raw"):
+        w = synth.q8_0(rows, K, seed)
+        nblk = rows * K // 32
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        if fmt == "q8_0":
+            host = np.empty(lib.zt_q8_gpu_bytes(nblk), np.uint8)
+            lib.zt_q8_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+            off = lib.zt_q8_gpu_data_offset(nblk)
+            wbufs = [dev(host)]
+            fn = lambda wb, y: lib.zt_gemm_q8sep_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
+        else:
+            wbufs = [dev(w.raw)]
+            fn = lambda wb, y: lib.zt_gemm_q8_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, s)
+        nbytes = synth.algorithmic_bytes("q8_0", rows, K, N)
+    elif fmt == "w4a16":
+        w = synth.w4a16(rows, K, seed)
+        wbufs = [dev(w.packed), dev(w.scales), dev(w.zeros)]
+        x = dev(synth.x_f16(K * N, seed))
+        fn = lambda wb, y: lib.zt_gemm_w4a16_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
+                                                 y.data_ptr(), rows, K, N, 128, s)
+        nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
+    elif fmt == "ternary_i8":
+        t = synth.ternary(rows, K, seed)
+        from ztensor_amd.storage import TernaryStorage
+
+        wbufs = [dev(TernaryStorage(t.raw, rows * K).row_aligned(rows, K))]
+        q, xs = synth.x_i8(K, seed)
+        x = dev(q)
+        sc = torch.tensor([xs, t.w_scale], dtype=torch.float32, device="cuda")
+        fn = lambda wb, y: lib.zt_ternary_gemv_i8(wb[0].data_ptr(), x.data_ptr(), sc.data_ptr(), sc.data_ptr() + 4,
+                                                  y.data_ptr(), rows, K, s)
+        nbytes = synth.algorithmic_bytes("ternary_i8", rows, K, N)
+    else:
+        raise ValueError(fmt)
+    wbytes = sum(b.numel() for b in wbufs)
+    copies = int(min(64, max(2, -(-2 * MALL_BYTES // wbytes) + 1)))
+    sets = [wbufs] + [[b.clone() for b in wbufs] for _ in range(copies - 1)]
+    ys = [torch.empty(rows * N, dtype=torch.float32, device="cuda") for _ in range(copies)]
+    n = copies * max(1, 64 // copies)
+
+    def loop():
+        nonlocal s
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(n):
+            rc = fn(sets[i % copies], ys[i % copies])
+            if rc != 0:
+                raise RuntimeError(f"{fmt} launch returned {rc}")
+
+    g = graph_of(torch, loop)
+    g.replay()
+    us = time_graph(torch, g, 5) * 1e3 / n
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
+            "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
+
+
+def run_suite(args) -> None:
+    import torch
+
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    only = set(args.only.split(",")) if args.only else None
+    for ci, (name, (fmt, shapes, batches)) in enumerate(SUITE.items()):
+        if only and name not in only:
+            continue
+        for si, (rows, K) in enumerate(shapes):
+            for N in batches:
+                r = _suite_case(torch, lib, fmt, rows, K, N, 0x5EED0000 + 16 * ci + si)
+                r["config"] = name
+                print(json.dumps(r), flush=True)
+                log(f"suite: {name:10s} K={K:5d} N={rows:5d} batch={N:2d}: {r['us']:8.2f} us {r['GB/s']:8.1f} GB/s "
+                    f"({r['pct_peak']:.1f}%)")
+                torch.cuda.empty_cache()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,15 +350,14 @@ def main() -> None:
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
+    ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build "
               "(see the sharding note in DESIGN.md)", file=sys.stderr)
         raise SystemExit(2)
     if args.suite:
-        from ztensor_amd import bench_suite
-
-        bench_suite.run(args)
+        run_suite(args)
         return
     print(json.dumps(run_headline(args)), flush=True)
 
