@@ -37,26 +37,69 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Sum R per-lane values across a wave64.  After the call, lane l holds the
-// full sum of value index row_of_lane<R>(l) in v[0].  The first log2(R)
-// exchange steps halve the number of live values per lane (each lane keeps
-// one half and ships the other to its partner), so the whole reduction costs
-// R-1 + log2(64/R) shuffles instead of 6*R.
+// Cross-lane exchange steps of wave_reduce_rows.  For a pair (a, b) of
+// per-lane values, pair_step<OFF> returns, in lanes whose bit OFF is clear,
+// a + a(partner) and, in lanes whose bit OFF is set, b + b(partner), where
+// the partner lane differs from the caller in bit OFF.
+//  * OFF 32 / 16: v_permlane32_swap / v_permlane16_swap exchange the upper
+//    half of `a` with the lower half of `b`, so a' + b' is exactly that sum
+//    with no per-lane select;
+//  * OFF 8 / 4 / 2 / 1: a DPP row_mirror / row_half_mirror / quad_perm move
+//    (partners 15-l, 7-l, l^2, l^1 inside a 16-lane row; each flips bit OFF)
+//    fused into the add, with two mask selects choosing what is kept and sent.
+template <int OFF>
+__device__ __forceinline__ float pair_step(float a, float b) {
+    if constexpr (OFF == 32 || OFF == 16) {
+        const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+        auto r = (OFF == 32) ? __builtin_amdgcn_permlane32_swap(ua, ub, false, false)
+                             : __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        constexpr uint64_t m = OFF == 8 ? 0xFF00FF00FF00FF00ull
+                             : OFF == 4 ? 0xF0F0F0F0F0F0F0F0ull
+                             : OFF == 2 ? 0xCCCCCCCCCCCCCCCCull : 0xAAAAAAAAAAAAAAAAull;
+        constexpr int ctrl = OFF == 8 ? 0x140 : OFF == 4 ? 0x141 : OFF == 2 ? 0x4E : 0xB1;
+        float keep, send;
+        asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(keep) : "v"(a), "v"(b), "s"(m));
+        asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(send) : "v"(b), "v"(a), "s"(m));
+        return keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), ctrl, 0xF, 0xF, false));
+    }
+}
+
+// One value: v + v(partner) in every lane.
+template <int OFF>
+__device__ __forceinline__ float single_step(float v) {
+    if constexpr (OFF == 32 || OFF == 16) {
+        return pair_step<OFF>(v, v);
+    } else {
+        constexpr int ctrl = OFF == 8 ? 0x140 : OFF == 4 ? 0x141 : OFF == 2 ? 0x4E : 0xB1;
+        return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+    }
+}
+
+template <int R, int OFF>
+__device__ __forceinline__ void reduce_level(float (&v)[R]) {
+    if constexpr (OFF >= 1) {
+        constexpr int c = R * OFF / 32 > 1 ? R * OFF / 32 : 1;  // live values per lane at this level
+        if constexpr (c > 1) {
+#pragma unroll
+            for (int i = 0; i < c / 2; i++) v[i] = pair_step<OFF>(v[i], v[c / 2 + i]);
+        } else {
+            v[0] = single_step<OFF>(v[0]);
+        }
+        reduce_level<R, OFF / 2>(v);
+    }
+}
+
+// Sum R per-lane values across a wave64.  After the call, every lane l holds
+// the full sum of value index row_of_lane<R>(l) in v[0].  The first log2(R)
+// steps halve the number of live values per lane (each lane keeps one half
+// and trades the other with its partner), so the reduction costs R-1 +
+// log2(64/R) exchange-and-add steps instead of 6*R.
 template <int R>
 __device__ __forceinline__ void wave_reduce_rows(float (&v)[R]) {
-    const int lane = threadIdx.x & 63;
-    int off = 32;
-#pragma unroll
-    for (int c = R; c > 1; c >>= 1, off >>= 1) {
-        const bool upper = (lane & off) != 0;
-#pragma unroll
-        for (int i = 0; i < c / 2; i++) {
-            float keep = upper ? v[c / 2 + i] : v[i];
-            float send = upper ? v[i] : v[c / 2 + i];
-            v[i] = keep + __shfl_xor(send, off, 64);
-        }
-    }
-    for (; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
+    static_assert(R >= 1 && R <= 32 && (R & (R - 1)) == 0, "R must be a power of two <= 32");
+    reduce_level<R, 32>(v);
 }
 
 // Which value index lane l holds after wave_reduce_rows<R>.

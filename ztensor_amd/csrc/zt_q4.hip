@@ -11,18 +11,24 @@
 //   IQ4_NL w[2i] = d * T[lo_i], w[2i+1] = d * T[hi_i]       (interleaved order, float table;
 //          tensor/iq4_storage.go:28-46)
 //
-// GEMV design (HBM-bound; every weight byte is read once):
-//  * lane <-> one 32-weight block column; its 16 data bytes are one 128-bit
-//    load, and the 64 lanes of a wave read 1 KiB of a row contiguously;
-//  * each wave walks R rows with the same block column, so the lane's 32
-//    activations are loaded once (registers) and reused R times;
+// Batch-1 GEMV design (HBM-bound; every weight byte is read once):
+//  * four lanes share one 32-weight block: lane q of the quad loads dword q
+//    of the block's 16 data bytes, so a wave covers 16 blocks per row and
+//    its activation loads are 64 (Q4_0: two 16-byte halves) or 128
+//    (IQ4_NL) contiguous bytes per block instead of a 128-byte stride per
+//    lane, which is what keeps the load pipe streaming;
+//  * each wave walks R rows with the same block columns, so the lane's 8
+//    activations are loaded once and reused R times;
 //  * the waves of a workgroup split K (split-K) and combine through LDS;
-//  * Q4_0: sum_j (q_j - 8) x_j = sum_j q_j x_j - 8 * sum_j x_j, with q_j
-//    converted by v_cvt_f32_ubyte{0..3} straight from the masked dword, and
-//    the per-block activation sum computed once per lane;
+//  * Q4_0: a nibble masked into the low bits of an fp16 half is the
+//    subnormal q * 2^-24 (exact), which v_fma_mix_f32 multiplies straight
+//    into an fp32 accumulator: 5 integer ops + 8 FMAs per 8 weights with no
+//    conversions; sum_j (q_j - 8) x_j = sum_j q_j x_j - 8 * sum_j x_j;
 //  * IQ4_NL: the 16-entry fp32 table sits in LDS; a lookup is one
 //    conflict-free ds_read_b32 (at most 16 distinct addresses per wave);
 //  * the block scale multiplies the block's partial sum once.
+// Batched calls (N > 1, column-strided activations) use the
+// block-per-lane kernel with one grid row per batch column.
 #include "zt_common.h"
 
 namespace zt {
@@ -100,6 +106,111 @@ __device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32],
     }
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+// The 8 activations lane q of a quad needs for block b: Q4_0 elements
+// 4q..4q+3 and 16+4q..16+4q+3 (GGML split order), IQ4_NL elements 8q..8q+7.
+template <Fmt F, class XT>
+__device__ __forceinline__ void load_x8(const XT* __restrict__ x, int b, int q, float (&xv)[8]) {
+    if constexpr (sizeof(XT) == 4) {
+        const float* p = reinterpret_cast<const float*>(x) + (long)b * 32;
+        const float4 a = *reinterpret_cast<const float4*>(p + (F == Fmt::Q4_0 ? 4 * q : 8 * q));
+        const float4 c = *reinterpret_cast<const float4*>(p + (F == Fmt::Q4_0 ? 16 + 4 * q : 8 * q + 4));
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = c.x; xv[5] = c.y; xv[6] = c.z; xv[7] = c.w;
+    } else {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(x) + (long)b * 32;
+        const uint2 a = *reinterpret_cast<const uint2*>(p + (F == Fmt::Q4_0 ? 4 * q : 8 * q));
+        const uint2 c = *reinterpret_cast<const uint2*>(p + (F == Fmt::Q4_0 ? 16 + 4 * q : 8 * q + 4));
+        xv[0] = h2f(a.x & 0xffff); xv[1] = h2f(a.x >> 16); xv[2] = h2f(a.y & 0xffff); xv[3] = h2f(a.y >> 16);
+        xv[4] = h2f(c.x & 0xffff); xv[5] = h2f(c.x >> 16); xv[6] = h2f(c.y & 0xffff); xv[7] = h2f(c.y >> 16);
+    }
+}
+
+// sum_j w_j x_j over the 8 weights of one data dword (without the block
+// scale).  Q4_0: byte j of the dword holds element 4q+j (low nibble,
+// activation xv[j]) and 16+4q+j (high nibble, xv[4+j]).  IQ4_NL: nibble m
+// is element 8q+m (activation xv[m]).
+template <Fmt F>
+__device__ __forceinline__ float dword_dot(uint32_t d, const float (&xv)[8], float xsum, const float* tbl) {
+    if constexpr (F == Fmt::Q4_0) {
+        const uint32_t d8 = d >> 8;
+        const half2v m0 = as_half2(d & 0x000F000Fu);   // bytes 0,2 low nibbles  (q * 2^-24)
+        const half2v m1 = as_half2(d & 0x00F000F0u);   // bytes 0,2 high nibbles (q * 2^-20)
+        const half2v m2 = as_half2(d8 & 0x000F000Fu);  // bytes 1,3 low nibbles
+        const half2v m3 = as_half2(d8 & 0x00F000F0u);  // bytes 1,3 high nibbles
+        float sa = (float)m0.x * xv[0];
+        float sb = (float)m1.x * xv[4];
+        sa = __builtin_fmaf((float)m2.x, xv[1], sa);
+        sb = __builtin_fmaf((float)m3.x, xv[5], sb);
+        sa = __builtin_fmaf((float)m0.y, xv[2], sa);
+        sb = __builtin_fmaf((float)m1.y, xv[6], sb);
+        sa = __builtin_fmaf((float)m2.y, xv[3], sa);
+        sb = __builtin_fmaf((float)m3.y, xv[7], sb);
+        return __builtin_fmaf(sa, 16777216.0f, __builtin_fmaf(sb, 1048576.0f, -8.0f * xsum));
+    } else {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 8; m += 2) {
+            s0 = fmaf(tbl[(d >> (4 * m)) & 0xfu], xv[m], s0);
+            s1 = fmaf(tbl[(d >> (4 * m + 4)) & 0xfu], xv[m + 1], s1);
+        }
+        return s0 + s1;
+    }
+}
+
+template <Fmt F, int R, class XT>
+__global__ void __launch_bounds__(512) gemv_quad_kernel(const uint16_t* __restrict__ scales,
+                                                        const uint32_t* __restrict__ data,
+                                                        const XT* __restrict__ x, float* __restrict__ y,
+                                                        int rows, int kb) {
+    __shared__ float red[8 * R];
+    __shared__ float tbl[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    if constexpr (F == Fmt::IQ4NL) {
+        if (threadIdx.x < 16) tbl[threadIdx.x] = kIQ4NLTable[threadIdx.x];
+        __syncthreads();
+    }
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int b = wave * 16 + (lane >> 2); b < kb; b += nwaves * 16) {
+        uint32_t w[R];
+        uint16_t s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = __builtin_nontemporal_load(&data[(rbase[r] + b) * 4 + q]);
+            s[r] = scales[rbase[r] + b];
+        }
+        float xv[8];
+        load_x8<F, XT>(x, b, q, xv);
+        float xsum = 0.0f;
+        if constexpr (F == Fmt::Q4_0) xsum = ((xv[0] + xv[1]) + (xv[2] + xv[3])) + ((xv[4] + xv[5]) + (xv[6] + xv[7]));
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(s[r]), dword_dot<F>(w[r], xv, xsum, tbl), acc[r]);
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <Fmt F, class XT>
+static void launch_quad(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
+                        const XT* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_quad_kernel<F, 8, XT><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 4: gemv_quad_kernel<F, 4, XT><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 2: gemv_quad_kernel<F, 2, XT><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        default: gemv_quad_kernel<F, 1, XT><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+    }
+}
+
 template <Fmt F, int R, class XT, bool CONTIG>
 __global__ void __launch_bounds__(512) gemv_blk18_kernel(const uint16_t* __restrict__ scales,
                                                          const uint4* __restrict__ data,
@@ -165,15 +276,18 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
     if (((uintptr_t)base & 1) || ((uintptr_t)data & 15)) return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base);
+    if (N == 1) {
+        const int nwaves = min(8, ceil_div(kb, 16));
+        const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
+        launch_quad<F, XT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, sc,
+                           reinterpret_cast<const uint32_t*>(data), B, C, M, kb);
+        return (int)hipGetLastError();
+    }
     const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
     const int R = pick_rows_per_wave(M, nwaves, N, 2048);
     dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base);
-    const uint4* dt = reinterpret_cast<const uint4*>(data);
-    if (N == 1)
-        launch_gemv_r<F, XT, true>(R, grid, block, st, sc, dt, B, C, 1, M, kb);
-    else
-        launch_gemv_r<F, XT, false>(R, grid, block, st, sc, dt, B, C, N, M, kb);
+    launch_gemv_r<F, XT, false>(R, grid, block, st, sc, reinterpret_cast<const uint4*>(data), B, C, N, M, kb);
     return (int)hipGetLastError();
 }
 
