@@ -104,15 +104,46 @@ def time_graph(torch, g, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+# ------------------------------------------------------------ HBM traffic
+
+TRAFFIC_FILE = ROOT / "profiles" / "q4_0_gemv_14336x4096_traffic.md"
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (a line starting with
+    'traffic_json: '), or None when it is absent or was taken on another
+    kernel build."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_json: "):
+                t = json.loads(line[len("traffic_json: "):])
+                if t.get("kernel") == kernel:
+                    return t["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        pass
+    return None
+
+
+def calibration_copy(torch) -> None:
+    """Device-to-device copies of 64 MiB, the known-size reference kernel that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    src = torch.ones(64 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 # ------------------------------------------------------------ CPU baseline
 
-def cpu_baseline(mats, budget_s: float = 12.0) -> dict:
+def cpu_baseline(mats, budget_s: float = 15.0) -> dict:
     from oracle import oracle
 
     threads = min(16, oracle.nthreads())
     total_bytes, t_total, reps = 0, 0.0, 0
     xs = {m.K: m.x.cpu().numpy() for m in mats}
-    while t_total < budget_s and reps < 50:
+    while t_total < budget_s:
         for m in mats:
             t0 = time.perf_counter()
             oracle.gemm_f32_q4_nt(xs[m.K], m.raw, 1, m.rows, m.K, threads=threads)
@@ -141,6 +172,8 @@ def run_headline(args) -> dict:
     from ztensor_amd import _lib
 
     lib = _lib.load()
+    if args.calibration_copy:
+        calibration_copy(torch)
     layers = args.layers
     log(f"bench: generating Llama-3-8B Q4_0 weights, {layers} layer copies")
     mats = [Q4Matrix(torch, lib, rows, K, 0x5EED0020 + i, layers) for i, (_, rows, K) in enumerate(LLAMA3_8B)]
@@ -187,9 +220,12 @@ def run_headline(args) -> dict:
         if name == "gate":
             dom = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                    "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
-                   "kernel": "gemv_blk18_kernel<Q4_0> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
+                   "kernel": "gemv_quad_kernel<Q4_0, R=8, float> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
                    "bytes_per_launch": m.bytes, "us_per_launch": round(us, 3)}
         log(f"bench: {name:5s} K={K:5d} N={rows:5d}: {us:7.2f} us  {gbs:7.1f} GB/s")
+
+    if dom is not None:
+        dom["traffic"] = measured_traffic(dom["kernel"])
 
     # Parity spot check of the last replayed outputs against the oracle.
     from oracle import oracle
@@ -351,6 +387,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build "
