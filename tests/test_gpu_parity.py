@@ -355,6 +355,31 @@ def test_w4a16_ragged(lib, orc, rows, K, g, N):
     assert rel_err(run_w4a16(lib, w, x16, rows, K, N), ref) <= TOL
 
 
+@pytest.mark.parametrize("rows,K,g,N", [(65, 384, 128, 4), (33, 2176, 128, 8), (17, 4096, 256, 12), (1, 128, 128, 16),
+                                        (100, 2048, 128, 16)])
+def test_w4a16_mfma_ragged(lib, orc, rows, K, g, N):
+    """Batched shapes on the MFMA path: partial row tiles, a partial last K
+    chunk (2176 = 2048 + 128), group 256, N = 12 and one-row matrices."""
+    say(f"w4a16 mfma rows={rows} K={K} g={g} N={N}")
+    w = synth.w4a16(rows, K, 9, group=g)
+    x16 = synth.x_f16(K * N, 9)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, g)
+    assert rel_err(run_w4a16(lib, w, x16, rows, K, N), ref) <= TOL
+
+
+def test_w4a16_mfma_non_integer_zero(lib, orc):
+    """Zero points that are not integers (GPTQ allows any fp16): the MFMA
+    path subtracts z * sum(x) exactly instead of folding z into the weights."""
+    rows, K, N = 64, 1024, 8
+    w = synth.w4a16(rows, K, 10)
+    rng = np.random.default_rng(10)
+    zeros = synth.f16_bits((rng.random(w.zeros.shape, dtype=np.float32) * 15).astype(np.float32))
+    w = synth.W4Weights(rows, K, w.group, w.packed, w.scales, zeros)
+    x16 = synth.x_f16(K * N, 10)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    assert rel_err(run_w4a16(lib, w, x16, rows, K, N), ref) <= TOL
+
+
 def test_w4a16_invalid_group(lib):
     t = torch.zeros(4096, dtype=torch.uint8, device="cuda")
     assert lib.zt_gemm_w4a16_f32(t.data_ptr(), t.data_ptr(), 0, t.data_ptr(), t.data_ptr(), 2, 128, 1, 48,
