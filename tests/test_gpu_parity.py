@@ -276,6 +276,23 @@ def test_iq4nl_gemm_matches_oracle(lib, orc, rows, K, N):
     assert rel_err(c.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("rows,K,N", [(33, 2176, 4), (1, 128, 16), (100, 3584, 12), (64, 384, 8)])
+def test_iq4nl_mfma_ragged(lib, orc, rows, K, N):
+    """Batched IQ4_NL on the MFMA path: partial row tiles, a partial last K
+    chunk (2176 = 2048 + 128), a single row, N = 4, 8, 12, 16."""
+    say(f"iq4nl mfma rows={rows} K={K} N={N}")
+    w = synth.iq4nl(rows, K, 21)
+    x16 = synth.x_f16(K * N, 21)
+    nblk = rows * K // 32
+    a = dev(synth_gpu_q4(w.raw, nblk))
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    xd = dev(x16)
+    lib.call("zt_gemm_iq4nl_f16", a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             lib.zt_q4_gpu_data_offset(nblk), stream())
+    ref = orc.iq4nl_matmul(w.raw, x16, rows, K, N)
+    assert rel_err(c.cpu().numpy(), ref) <= TOL
+
+
 def test_iq4nl_fp32_activations(lib, orc):
     rows, K = 64, 1024
     w = synth.iq4nl(rows, K, 3)
@@ -356,10 +373,12 @@ def test_w4a16_ragged(lib, orc, rows, K, g, N):
 
 
 @pytest.mark.parametrize("rows,K,g,N", [(65, 384, 128, 4), (33, 2176, 128, 8), (17, 4096, 256, 12), (1, 128, 128, 16),
-                                        (100, 2048, 128, 16)])
+                                        (100, 2048, 128, 16), (100, 4096, 128, 8), (40, 12288, 256, 4)])
 def test_w4a16_mfma_ragged(lib, orc, rows, K, g, N):
     """Batched shapes on the MFMA path: partial row tiles, a partial last K
-    chunk (2176 = 2048 + 128), group 256, N = 12 and one-row matrices."""
+    chunk (2176 = 2048 + 128), group 256, N = 12, one-row matrices, and
+    few-row matrices whose K is split across workgroups (100 x 4096: four
+    splits of 8 units; 40 x 12288: eight splits of 12 units)."""
     say(f"w4a16 mfma rows={rows} K={K} g={g} N={N}")
     w = synth.w4a16(rows, K, 9, group=g)
     x16 = synth.x_f16(K * N, 9)

@@ -1,0 +1,143 @@
+// Shared pieces of the small-batch MFMA GEMMs (W4A16, IQ4_NL) for gfx950.
+//
+// Common structure (C[rows, N] = W[rows, K] x X[K, N], 4 <= N <= 16, N % 4 == 0,
+// K % 128 == 0, X fp16 row-major with N columns):
+//  * a workgroup of kMfmaWaves waves owns kMfmaRows rows (two 16-row MFMA
+//    tiles) and walks K in chunks of kMfmaKC;
+//  * each chunk's X rows are copied (16 bytes a lane, coalesced) into LDS
+//    with two padding rows after every 32, which puts the four 16-lane
+//    groups of a transposing read on distinct banks;
+//  * the B operand of v_mfma_f32_16x16x32_f16 (32 K x 16 columns) is read
+//    with two ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b
+//    addresses X row r(a) and columns 4b .. 4b+3, and the read hands lane n
+//    the four values X[r(0..3)][n]; columns >= N address a zero word;
+//  * the waves' partial output tiles are summed through LDS at the end;
+//  * when the matrix has too few rows to fill the GPU, blockIdx.y splits K
+//    into contiguous unit ranges; the caller zeroes C first (mfma_zero, a
+//    plain kernel so that it can sit in a captured graph) and each split
+//    adds its partial tile with a hardware fp32 atomic.  The summation order
+//    of the splits, and so the last bits of C, then vary from run to run.
+#pragma once
+
+#include "zt_common.h"
+
+namespace zt {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+typedef __attribute__((address_space(3))) char lds_char;
+
+constexpr int kMfmaRows = 32;                         // rows per workgroup (two 16-row tiles)
+constexpr int kMfmaTiles = kMfmaRows / 16;
+constexpr int kMfmaWaves = 8;                         // waves per workgroup
+constexpr int kMfmaUPW = 2;                           // 128-K units per wave per chunk
+constexpr int kMfmaKC = 128 * kMfmaWaves * kMfmaUPW;  // K per chunk
+constexpr int kMfmaUC = kMfmaKC / 128;                // units per chunk
+
+__device__ __forceinline__ short4v tr_read_b64(char* lds, int byte_off) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)((lds_char*)lds + byte_off));
+}
+
+// Bytes of one staged X chunk: kMfmaKC rows of 2N bytes plus 2 pad rows per 32.
+__host__ __device__ __forceinline__ int mfma_xbytes(int N) { return (kMfmaKC + kMfmaKC / 16) * 2 * N; }
+
+// LDS byte offset of chunk-relative X row k (row stride 2N, 2 pad rows per 32).
+__device__ __forceinline__ int mfma_xrow(int k, int N) { return (k + 2 * (k >> 5)) * 2 * N; }
+
+// Copies X rows [c0*128, min(c0*128 + kMfmaKC, kend)) into the padded LDS chunk.
+__device__ __forceinline__ void mfma_stage_x(char* smem, const uint16_t* __restrict__ x, int c0, int kend, int N) {
+    const int npieces = min(kMfmaKC, kend - c0 * 128) * 2 * N / 16;
+    const uint4* xg = reinterpret_cast<const uint4*>(x + (long)c0 * 128 * N);
+    for (int p = threadIdx.x; p < npieces; p += blockDim.x) {
+        const uint4 v = xg[p];
+        const int off = p * 16;  // a 16-byte piece never straddles a 32-row segment (64N bytes)
+        *reinterpret_cast<uint4*>(smem + off + (off / (64 * N)) * (4 * N)) = v;
+    }
+}
+
+// Per-lane roles of the transposing reads (li = lane % 16).
+struct MfmaBRole {
+    int jq, qq;
+    bool colok;
+    __device__ __forceinline__ MfmaBRole(int li, int N) : jq(li >> 2), qq(li & 3), colok(4 * (li & 3) < N) {}
+};
+
+// B operand for the 8 chunk-relative X rows k0 + ord[0..7] (ord given as the
+// two row-offset quadruples of the two reads), column li.
+__device__ __forceinline__ half8v mfma_b_operand(char* smem, const MfmaBRole& ro, int k0, int offa, int offb, int N,
+                                                 int zero_off) {
+    const int ra = k0 + offa, rb = k0 + offb;
+    const int adda = ro.colok ? mfma_xrow(ra, N) + 8 * ro.qq : zero_off;
+    const int addb = ro.colok ? mfma_xrow(rb, N) + 8 * ro.qq : zero_off;
+    const short4v ba = tr_read_b64(smem, adda), bb = tr_read_b64(smem, addb);
+    return __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
+}
+
+// Sums the waves' partial tiles and stores C rows row0 .. row0+31, columns < N.
+// acc[t][i] of lane l holds row 16t + 4*(l/16) + i, column l%16 (the MFMA
+// D layout).  Uses smem as scratch; the caller has passed a barrier after
+// its last read of the staged chunk.
+__device__ __forceinline__ void mfma_reduce_store(float4v (&acc)[kMfmaTiles], char* smem, float* __restrict__ y,
+                                                  int row0, int rows, int N, bool split) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int t = 0; t < kMfmaTiles; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[((wave * kMfmaTiles + t) * 4 + i) * 64 + lane] = acc[t][i];
+    __syncthreads();
+    for (int o = tid; o < kMfmaTiles * 256; o += blockDim.x) {
+        const int t = o >> 8, r = (o >> 4) & 15, n = o & 15;
+        const int ln = (r >> 2) * 16 + n, i = r & 3;
+        float sum = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < kMfmaWaves; wv++) sum += red[((wv * kMfmaTiles + t) * 4 + i) * 64 + ln];
+        const int row = row0 + 16 * t + r;
+        if (n < N && row < rows) {
+            if (split)
+                unsafeAtomicAdd(&y[(long)row * N + n], sum);
+            else
+                y[(long)row * N + n] = sum;
+        }
+    }
+}
+
+// The unit range [ub, ue) of K-split blockIdx.y out of gridDim.y.
+__device__ __forceinline__ void mfma_split_range(int nunits, int& ub, int& ue) {
+    const int per = (nunits + gridDim.y - 1) / gridDim.y;
+    ub = min(nunits, (int)blockIdx.y * per);
+    ue = min(nunits, ub + per);
+}
+
+// Number of K splits: enough workgroups for ~2 per CU, each split keeping
+// at least one 128-K unit per wave.
+__host__ __forceinline__ int mfma_splits(int rows, int K) {
+    const int wgs = (rows + kMfmaRows - 1) / kMfmaRows;
+    const int nunits = K / 128;
+    int s = 1;
+    while (s < 16 && wgs * s < 512 && nunits / (2 * s) >= kMfmaWaves) s *= 2;
+    return s;
+}
+
+static __global__ void mfma_zero_kernel(float* __restrict__ y, long n) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = 0.0f;
+}
+
+// Zeroes C before a split-K launch on the same stream.
+__host__ __forceinline__ void mfma_zero(float* y, long n, hipStream_t st) {
+    mfma_zero_kernel<<<(int)((n + 255) / 256), 256, 0, st>>>(y, n);
+}
+
+__host__ __forceinline__ size_t mfma_reduce_bytes() { return (size_t)kMfmaWaves * kMfmaTiles * 4 * 64 * sizeof(float); }
+
+// Host-side eligibility of a call for the MFMA path.
+__host__ __forceinline__ bool mfma_shape_ok(int N, int K, const void* x) {
+    return N >= 4 && N <= 16 && N % 4 == 0 && K % 128 == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+}  // namespace zt

@@ -29,7 +29,7 @@
 //  * the block scale multiplies the block's partial sum once.
 // Batched calls (N > 1, column-strided activations) use the
 // block-per-lane kernel with one grid row per batch column.
-#include "zt_common.h"
+#include "zt_mfma.h"
 
 namespace zt {
 
@@ -105,8 +105,6 @@ __device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32],
         return s0 + s1;
     }
 }
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
@@ -211,6 +209,123 @@ static void launch_quad(int R, dim3 grid, dim3 block, hipStream_t st, const uint
     }
 }
 
+// ------------------------------------------------------------ IQ4_NL MFMA GEMM
+//
+// Batched IQ4_NL (fp16 activations, 4 <= N <= 16, N % 4 == 0, K % 128 == 0):
+// the workgroup structure, X staging and transposing B reads of zt_mfma.h.
+//  * For a 128-K unit, lane (i = lane%16, g = lane/16) loads the 16 data
+//    bytes of block 4u+g of row i.  Two v_permlane32_swap and two
+//    v_permlane16_swap transpose the four lanes' dwords so that register c
+//    holds dword g of block 4u+c: MFMA step c then covers exactly one block
+//    (lane group g supplies its elements 8g .. 8g+7), and the block's fp16
+//    scale multiplies the step's result.
+//  * The fp32 codebook value T[q] enters the MFMA as two exact fp16 parts,
+//    T_hi = fp16(T) and T_lo = fp16(T - T_hi) (|T - T_hi - T_lo| <= 2^-23 |T|),
+//    looked up together as one dword from a 16-entry LDS table; two MFMAs
+//    per step accumulate both parts.
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+__global__ void __launch_bounds__(512) iq4nl_mfma_kernel(const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ data,
+                                                         const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                         int rows, int K, int N) {
+    constexpr int NT = kMfmaTiles;
+    constexpr int BPC = kMfmaUC * 4;  // blocks per chunk
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int xbytes = mfma_xbytes(N);
+    char* zero_area = smem + xbytes;
+    uint32_t* tbl = reinterpret_cast<uint32_t*>(zero_area + 16);  // 16 x (T_hi | T_lo << 16)
+    uint16_t* ss = reinterpret_cast<uint16_t*>(tbl + 16);         // [block in chunk][row]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int row0 = blockIdx.x * kMfmaRows;
+    const int nunits = K / 128, kb = K / 32;
+    if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
+    if (tid < 16) {
+        const float t = kIQ4NLTable[tid];
+        const _Float16 hi = (_Float16)t;
+        const _Float16 lo = (_Float16)(t - (float)hi);
+        tbl[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    }
+
+    float4v acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = (float4v){0.f, 0.f, 0.f, 0.f};
+    long abase[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) abase[t] = (long)min(row0 + 16 * t + li, rows - 1) * kb;
+    const MfmaBRole ro(li, N);
+
+    int ub, ue;
+    mfma_split_range(nunits, ub, ue);
+    for (int c0 = ub; c0 < ue; c0 += kMfmaUC) {
+        uint4 w[kMfmaUPW][NT];
+#pragma unroll
+        for (int u = 0; u < kMfmaUPW; u++) {
+            const int unit = min(c0 + wave + kMfmaWaves * u, ue - 1);
+#pragma unroll
+            for (int t = 0; t < NT; t++) w[u][t] = ld_stream(&data[abase[t] + unit * 4 + lg]);
+        }
+        mfma_stage_x(smem, x, c0, ue * 128, N);
+        for (int e = tid; e < BPC * kMfmaRows; e += blockDim.x) {
+            const int bb = e / kMfmaRows, r = e % kMfmaRows;
+            const int blk = c0 * 4 + bb;
+            if (blk < kb) ss[e] = scales[(long)min(row0 + r, rows - 1) * kb + blk];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kMfmaUPW; u++) {
+            const int uu = wave + kMfmaWaves * u;
+            if (c0 + uu < ue) {
+                uint32_t r[NT][4];
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    // 4x4 transpose across the lane groups: r[t][c] = dword g of block 4u+c.
+                    auto p02 = __builtin_amdgcn_permlane32_swap(w[u][t].x, w[u][t].z, false, false);
+                    auto p13 = __builtin_amdgcn_permlane32_swap(w[u][t].y, w[u][t].w, false, false);
+                    auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+                    auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+                    r[t][0] = q01[0]; r[t][1] = q01[1]; r[t][2] = q23[0]; r[t][3] = q23[1];
+                }
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const half8v bv = mfma_b_operand(smem, ro, uu * 128 + 32 * c + 8 * lg, ro.jq, ro.jq + 4, N, xbytes);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        uint32_t e[8];
+#pragma unroll
+                        for (int m = 0; m < 8; m++) e[m] = tbl[(r[t][c] >> (4 * m)) & 0xfu];
+                        const uint32_t ah[4] = {pack_lo16(e[0], e[1]), pack_lo16(e[2], e[3]), pack_lo16(e[4], e[5]),
+                                                pack_lo16(e[6], e[7])};
+                        const uint32_t al[4] = {pack_hi16(e[0], e[1]), pack_hi16(e[2], e[3]), pack_hi16(e[4], e[5]),
+                                                pack_hi16(e[6], e[7])};
+                        float4v dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8v, (u32x4){ah[0], ah[1], ah[2], ah[3]}), bv,
+                            (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8v, (u32x4){al[0], al[1], al[2], al[3]}), bv, dd, 0, 0, 0);
+                        const int rb0 = (uu * 4 + c) * kMfmaRows + 16 * t + 4 * lg;
+                        const uint2 s4 = *reinterpret_cast<const uint2*>(ss + rb0);
+                        acc[t][0] = fmaf(h2f(s4.x & 0xffff), dd[0], acc[t][0]);
+                        acc[t][1] = fmaf(h2f(s4.x >> 16), dd[1], acc[t][1]);
+                        acc[t][2] = fmaf(h2f(s4.y & 0xffff), dd[2], acc[t][2]);
+                        acc[t][3] = fmaf(h2f(s4.y >> 16), dd[3], acc[t][3]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    mfma_reduce_store(acc, smem, y, row0, rows, N, gridDim.y > 1);
+}
+
+static size_t iq4_mfma_lds_bytes(int N) {
+    const size_t stage = (size_t)mfma_xbytes(N) + 16 + 16 * 4 + kMfmaUC * 4 * kMfmaRows * sizeof(uint16_t);
+    return stage > mfma_reduce_bytes() ? stage : mfma_reduce_bytes();
+}
+
 template <Fmt F, int R, class XT, bool CONTIG>
 __global__ void __launch_bounds__(512) gemv_blk18_kernel(const uint16_t* __restrict__ scales,
                                                          const uint4* __restrict__ data,
@@ -283,6 +398,15 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         launch_quad<F, XT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, sc,
                            reinterpret_cast<const uint32_t*>(data), B, C, M, kb);
         return (int)hipGetLastError();
+    }
+    if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
+        if (mfma_shape_ok(N, K, B)) {
+            const int splits = mfma_splits(M, K);
+            if (splits > 1) mfma_zero(C, (long)M * N, st);
+            iq4nl_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), splits), kMfmaWaves * kWave, iq4_mfma_lds_bytes(N), st>>>(
+                sc, reinterpret_cast<const uint4*>(data), reinterpret_cast<const uint16_t*>(B), C, M, K, N);
+            return (int)hipGetLastError();
+        }
     }
     const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
     const int R = pick_rows_per_wave(M, nwaves, N, 2048);

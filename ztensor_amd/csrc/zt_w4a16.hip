@@ -27,13 +27,10 @@
 //
 // Small-batch GEMM (N = 4, 8, 12, 16): v_mfma_f32_16x16x32_f16, see the
 // MFMA section below.
-#include "zt_common.h"
+#include "zt_mfma.h"
 
 namespace zt {
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
@@ -137,41 +134,17 @@ static void launch_w4a16_gemv(int R, dim3 g, dim3 b, hipStream_t st, const uint4
 // ------------------------------------------------------------ MFMA GEMM
 //
 // C[rows, N] = W[rows, K] x X[K, N] for 4 <= N <= 16, N % 4 == 0, K and the
-// group size multiples of 128.
-//  * A workgroup of 8 waves owns 32 rows (two 16-row MFMA tiles) and walks
-//    K in chunks of 2048.  Each chunk's X rows are copied (coalesced, 16
-//    bytes a lane) into LDS, two padding rows per 32 so that the transposed
-//    reads below hit distinct banks; the chunk's scales and zeros go along.
-//  * Wave w of the workgroup takes the 128-K units w and w+8 of the chunk.
+// group size multiples of 128 (workgroup structure, X staging and the
+// transposing B reads: zt_mfma.h).
+//  * Wave w of the workgroup takes the 128-K units w and w+8 of each chunk.
 //    For a unit, lane (i = lane%16, g = lane/16) loads 16 bytes of row i:
 //    the 32 weights 32g .. 32g+31 of the unit.  Dword s of that load feeds
 //    MFMA step s: its nibble pairs (m, m+4) become exact fp16 with
-//    (0x6400 | q) - 1024, ordered [e0,e4,e1,e5,e2,e6,e3,e7].
-//  * The B operand (32 K x 16 columns, columns >= N read a zero word) comes
-//    from two ds_read_b64_tr_b16 per step: within each 16-lane group, lane
-//    j' = 4a + b addresses X row (k0 + {0,4,1,5}[a]) (then {2,6,3,7}),
-//    columns 4b..4b+3, and the transposing read hands lane n the column n of
-//    those four rows -- the same k order as the A halves.
+//    (0x6400 | q) - 1024, ordered [e0,e4,e1,e5,e2,e6,e3,e7], and the B
+//    reads take X rows k0 + {0,4,1,5} and k0 + {2,6,3,7} to match.
 //  * A third MFMA per step with an all-ones A gives sum_k x[k][n] for the
-//    unit, so y += s * (sum_k q x - z * sum_k x) is exact for any fp16 zero.
-//  * The eight waves' partial tiles are summed through LDS at the end.
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
-typedef short short4v __attribute__((ext_vector_type(4)));
-typedef short short8v __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) short4v lds_short4v;
-typedef __attribute__((address_space(3))) char lds_char;
-
-constexpr int kMfmaRows = 32;     // rows per workgroup (two 16-row tiles)
-constexpr int kMfmaWaves = 8;     // waves per workgroup
-constexpr int kMfmaUPW = 2;       // 128-K units per wave per chunk
-constexpr int kMfmaKC = 128 * kMfmaWaves * kMfmaUPW;  // K per chunk
-constexpr int kMfmaUC = kMfmaKC / 128;                // units per chunk
-
-__device__ __forceinline__ short4v tr_read_b64(char* lds, int byte_off) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)((lds_char*)lds + byte_off));
-}
-
+//    unit, so y += s * (sum_k q x - z * sum_k x) is exact for any fp16 zero
+//    (one scale and zero per unit since the group size is a multiple of 128).
 __device__ __forceinline__ half8v w4_a_operand(uint32_t d) {
     half8v a;
 #pragma unroll
@@ -183,18 +156,14 @@ __device__ __forceinline__ half8v w4_a_operand(uint32_t d) {
     return a;
 }
 
-// Bytes of one staged X chunk: KC rows of 2N bytes plus 2 pad rows per 32.
-__host__ __device__ __forceinline__ int w4_mfma_xbytes(int N) { return (kMfmaKC + kMfmaKC / 16) * 2 * N; }
-
 __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restrict__ packed,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ zeros,
                                                          const uint16_t* __restrict__ x, float* __restrict__ y,
                                                          int rows, int K, int N, int gs) {
-    constexpr int NT = 2;
+    constexpr int NT = kMfmaTiles;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    const int rowb = 2 * N;
-    const int xbytes = w4_mfma_xbytes(N);
+    const int xbytes = mfma_xbytes(N);
     char* zero_area = smem + xbytes;
     uint16_t* ss = reinterpret_cast<uint16_t*>(zero_area + 16);
     uint16_t* zs = ss + kMfmaUC * kMfmaRows;
@@ -213,31 +182,26 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
     int arow[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) arow[t] = min(row0 + 16 * t + li, rows - 1);
-    const int jq = li >> 2, qq = li & 3;
-    const int roffa = (jq == 0) ? 0 : (jq == 1) ? 4 : (jq == 2) ? 1 : 5;
-    const int roffb = roffa + 2;
-    const bool colok = 4 * qq < N;
+    const MfmaBRole ro(li, N);
+    const int offa = (ro.jq == 0) ? 0 : (ro.jq == 1) ? 4 : (ro.jq == 2) ? 1 : 5;  // rows {0,4,1,5}
+    const int offb = offa + 2;                                                      // rows {2,6,3,7}
     const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
 
-    for (int c0 = 0; c0 < nunits; c0 += kMfmaUC) {
+    int ub, ue;
+    mfma_split_range(nunits, ub, ue);
+    for (int c0 = ub; c0 < ue; c0 += kMfmaUC) {
         uint4 w[kMfmaUPW][NT];
 #pragma unroll
         for (int u = 0; u < kMfmaUPW; u++) {
-            const int unit = min(c0 + wave + kMfmaWaves * u, nunits - 1);
+            const int unit = min(c0 + wave + kMfmaWaves * u, ue - 1);
 #pragma unroll
             for (int t = 0; t < NT; t++)
                 w[u][t] = ld_stream(reinterpret_cast<const uint4*>(packed + (long)arow[t] * rowbytes + unit * 64 + 16 * lg));
         }
-        const int npieces = min(kMfmaKC, K - c0 * 128) * rowb / 16;
-        const uint4* xg = reinterpret_cast<const uint4*>(x + (long)c0 * 128 * N);
-        for (int p = tid; p < npieces; p += blockDim.x) {
-            const uint4 v = xg[p];
-            const int off = p * 16;
-            *reinterpret_cast<uint4*>(smem + off + (off / (64 * N)) * (4 * N)) = v;
-        }
+        mfma_stage_x(smem, x, c0, ue * 128, N);
         for (int e = tid; e < kMfmaUC * kMfmaRows; e += blockDim.x) {
             const int uu = e / kMfmaRows, r = e % kMfmaRows;
-            if (c0 + uu < nunits) {
+            if (c0 + uu < ue) {
                 const long gi = (long)min(row0 + r, rows - 1) * ngroups + ((c0 + uu) * 128) / gs;
                 ss[e] = scales[gi];
                 zs[e] = zeros ? zeros[gi] : (uint16_t)0x4800;  // fp16 8.0
@@ -247,19 +211,13 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
 #pragma unroll
         for (int u = 0; u < kMfmaUPW; u++) {
             const int uu = wave + kMfmaWaves * u;
-            if (c0 + uu < nunits) {
+            if (c0 + uu < ue) {
                 float4v d[NT], dn = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int t = 0; t < NT; t++) d[t] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 4; s++) {
-                    const int k0 = uu * 128 + 32 * lg + 8 * s;
-                    const int ra = k0 + roffa, rb = k0 + roffb;
-                    const int adda = colok ? (ra + 2 * (ra >> 5)) * rowb + 8 * qq : xbytes;
-                    const int addb = colok ? (rb + 2 * (rb >> 5)) * rowb + 8 * qq : xbytes;
-                    const short4v ba = tr_read_b64(smem, adda), bb = tr_read_b64(smem, addb);
-                    const half8v bv = __builtin_bit_cast(
-                        half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
+                    const half8v bv = mfma_b_operand(smem, ro, uu * 128 + 32 * lg + 8 * s, offa, offb, N, xbytes);
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
@@ -267,7 +225,6 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
                     }
                     dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, bv, dn, 0, 0, 0);
                 }
-                // D lane layout: rows 4*lg + i of the tile, column li.
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const int rb0 = uu * kMfmaRows + 16 * t + 4 * lg;
@@ -285,27 +242,12 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
         }
         __syncthreads();
     }
-    float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) red[((wave * NT + t) * 4 + i) * 64 + lane] = acc[t][i];
-    __syncthreads();
-    {
-        const int t = tid >> 8, r = (tid >> 4) & 15, n = tid & 15;
-        const int ln = (r >> 2) * 16 + n, i = r & 3;
-        float sum = 0.f;
-#pragma unroll
-        for (int wv = 0; wv < kMfmaWaves; wv++) sum += red[((wv * NT + t) * 4 + i) * 64 + ln];
-        const int row = row0 + 16 * t + r;
-        if (n < N && row < rows) y[(long)row * N + n] = sum;
-    }
+    mfma_reduce_store(acc, smem, y, row0, rows, N, gridDim.y > 1);
 }
 
 static size_t w4_mfma_lds_bytes(int N) {
-    const size_t stage = (size_t)w4_mfma_xbytes(N) + 16 + 2 * kMfmaUC * kMfmaRows * sizeof(uint16_t);
-    const size_t red = (size_t)kMfmaWaves * 2 * 4 * 64 * sizeof(float);
-    return stage > red ? stage : red;
+    const size_t stage = (size_t)mfma_xbytes(N) + 16 + 2 * kMfmaUC * kMfmaRows * sizeof(uint16_t);
+    return stage > mfma_reduce_bytes() ? stage : mfma_reduce_bytes();
 }
 
 // ------------------------------------------------------------ dequantize
@@ -343,8 +285,10 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     if (((uintptr_t)W_packed & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1))
         return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
-    if (N >= 4 && N <= 16 && N % 4 == 0 && K % 128 == 0 && group_size % 128 == 0 && ((uintptr_t)B & 15) == 0) {
-        w4a16_mfma_kernel<<<ceil_div(M, kMfmaRows), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
+    if (mfma_shape_ok(N, K, B) && group_size % 128 == 0) {
+        const int splits = mfma_splits(M, K);
+        if (splits > 1) mfma_zero(C, (long)M * N, stream);
+        w4a16_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), splits), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
             static_cast<const uint8_t*>(W_packed), scales, zeros, B, C, M, K, N, group_size);
         return (int)hipGetLastError();
     }
