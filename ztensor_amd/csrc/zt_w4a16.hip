@@ -131,6 +131,92 @@ static void launch_w4a16_gemv(int R, dim3 g, dim3 b, hipStream_t st, const uint4
     }
 }
 
+// Batch-1 GEMV: four lanes share one 32-weight chunk.  Lane q of a quad
+// loads dword q of the chunk (weights 8q .. 8q+7; nibble m of the dword is
+// weight 8q+m) and the 8 matching fp16 activations as one 16-byte load, so a
+// wave reads 256 contiguous weight bytes per row and 16 contiguous chunks of
+// activations.  A nibble masked into an fp16 half is the subnormal q * 2^-24
+// (or q * 2^-20 for the upper nibble of a byte); v_fma_mix_f32 multiplies it
+// by the fp16 activation into an fp32 accumulator exactly.  Per chunk and row:
+// y += s * (2^24 sum_lo + 2^20 sum_hi - z * sum x).  The workgroup's scale
+// and zero pairs are staged in LDS once (one dword per row and group), so a
+// step issues one global load per row.
+template <int R>
+__global__ void __launch_bounds__(512) w4a16_quad_kernel(const uint32_t* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ zeros,
+                                                         const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                         int rows, int nchunk, int chunks_per_group) {
+    __shared__ float red[8 * R];
+    extern __shared__ uint32_t sz[];  // [group][R]: scale | zero << 16
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int ngroups = nchunk / chunks_per_group;
+    const int row0 = blockIdx.x * R;
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rr[r] = min(row0 + r, rows - 1);
+    for (int e = threadIdx.x; e < R * ngroups; e += blockDim.x) {
+        const int r = e / ngroups, g = e - r * ngroups;  // row-major walk: coalesced global reads
+        const long gi = (long)min(row0 + r, rows - 1) * ngroups + g;
+        sz[g * R + r] = (uint32_t)scales[gi] | ((uint32_t)(zeros ? zeros[gi] : (uint16_t)0x4800) << 16);  // zero 8.0
+    }
+    __syncthreads();
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int c = wave * 16 + (lane >> 2); c < nchunk; c += nwaves * 16) {
+        const int g = c / chunks_per_group;
+        uint32_t w[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) w[r] = __builtin_nontemporal_load(&packed[((long)rr[r] * nchunk + c) * 4 + q]);
+        const uint4 xv = *reinterpret_cast<const uint4*>(x + (long)c * 32 + 8 * q);
+        const half2v x01 = as_h2(xv.x), x23 = as_h2(xv.y), x45 = as_h2(xv.z), x67 = as_h2(xv.w);
+        float xsum = __builtin_amdgcn_fdot2(x01, as_h2(0x3c003c00u), 0.0f, false);
+        xsum = __builtin_amdgcn_fdot2(x23, as_h2(0x3c003c00u), xsum, false);
+        xsum = __builtin_amdgcn_fdot2(x45, as_h2(0x3c003c00u), xsum, false);
+        xsum = __builtin_amdgcn_fdot2(x67, as_h2(0x3c003c00u), xsum, false);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[r], d8 = d >> 8;
+            const half2v m0 = as_h2(d & 0x000F000Fu);   // weights 0, 4  (q * 2^-24)
+            const half2v m1 = as_h2(d & 0x00F000F0u);   // weights 1, 5  (q * 2^-20)
+            const half2v m2 = as_h2(d8 & 0x000F000Fu);  // weights 2, 6
+            const half2v m3 = as_h2(d8 & 0x00F000F0u);  // weights 3, 7
+            float sa = (float)m0.x * (float)x01.x;
+            float sb = (float)m1.x * (float)x01.y;
+            sa = __builtin_fmaf((float)m0.y, (float)x45.x, sa);
+            sb = __builtin_fmaf((float)m1.y, (float)x45.y, sb);
+            sa = __builtin_fmaf((float)m2.x, (float)x23.x, sa);
+            sb = __builtin_fmaf((float)m3.x, (float)x23.y, sb);
+            sa = __builtin_fmaf((float)m2.y, (float)x67.x, sa);
+            sb = __builtin_fmaf((float)m3.y, (float)x67.y, sb);
+            const uint32_t szr = sz[g * R + r];
+            const float t = __builtin_fmaf(sa, 16777216.0f, __builtin_fmaf(sb, 1048576.0f, -h2f(szr >> 16) * xsum));
+            acc[r] = fmaf(h2f(szr & 0xffff), t, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int R>
+static void launch_w4a16_quad_r(dim3 g, dim3 b, hipStream_t st, const uint32_t* w, const uint16_t* s,
+                                const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+    const size_t lds = (size_t)R * (nchunk / cpg) * sizeof(uint32_t);
+    w4a16_quad_kernel<R><<<g, b, lds, st>>>(w, s, z, x, y, rows, nchunk, cpg);
+}
+
+static void launch_w4a16_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint32_t* w, const uint16_t* s,
+                              const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+    switch (R) {
+        case 8: launch_w4a16_quad_r<8>(g, b, st, w, s, z, x, y, rows, nchunk, cpg); break;
+        case 4: launch_w4a16_quad_r<4>(g, b, st, w, s, z, x, y, rows, nchunk, cpg); break;
+        case 2: launch_w4a16_quad_r<2>(g, b, st, w, s, z, x, y, rows, nchunk, cpg); break;
+        default: launch_w4a16_quad_r<1>(g, b, st, w, s, z, x, y, rows, nchunk, cpg); break;
+    }
+}
+
 // ------------------------------------------------------------ MFMA GEMM
 //
 // C[rows, N] = W[rows, K] x X[K, N] for 4 <= N <= 16, N % 4 == 0, K and the
@@ -293,14 +379,18 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
         return (int)hipGetLastError();
     }
     const int nchunk = K / 32;
+    if (N == 1) {
+        const int nw = min(8, ceil_div(nchunk, 16));
+        const int R = pick_rows_per_wave(M, nw, 1, 2048);
+        launch_w4a16_quad(R, dim3(ceil_div(M, R)), dim3(nw * kWave), stream, static_cast<const uint32_t*>(W_packed),
+                          scales, zeros, B, C, M, nchunk, group_size / 32);
+        return (int)hipGetLastError();
+    }
     const int nwaves = nchunk <= 64 ? 1 : (nchunk >= 8 * 64 ? 8 : ceil_div(nchunk, 64));
     const int R = pick_rows_per_wave(M, nwaves, N, 2048);
     dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
-    const uint4* w = static_cast<const uint4*>(W_packed);
-    if (N == 1)
-        launch_w4a16_gemv<true>(R, grid, block, stream, w, scales, zeros, B, C, 1, M, nchunk, group_size / 32);
-    else
-        launch_w4a16_gemv<false>(R, grid, block, stream, w, scales, zeros, B, C, N, M, nchunk, group_size / 32);
+    launch_w4a16_gemv<false>(R, grid, block, stream, static_cast<const uint4*>(W_packed), scales, zeros, B, C, N, M,
+                             nchunk, group_size / 32);
     return (int)hipGetLastError();
 }
 
