@@ -27,8 +27,9 @@
 //  * IQ4_NL: the 16-entry fp32 table sits in LDS; a lookup is one
 //    conflict-free ds_read_b32 (at most 16 distinct addresses per wave);
 //  * the block scale multiplies the block's partial sum once.
-// Batched calls (N > 1, column-strided activations) use the
-// block-per-lane kernel with one grid row per batch column.
+// Batched IQ4_NL calls with fp16 activations and 4 <= N <= 16 use the MFMA
+// GEMM further down; other batched calls (N > 1, column-strided
+// activations) use the block-per-lane kernel with one grid row per column.
 #include "zt_mfma.h"
 
 namespace zt {
