@@ -13,9 +13,10 @@
 //                device).  Every block's 32 bytes are two aligned 128-bit
 //                loads, so a wave reads 2 KiB of a row contiguously.
 //
-// Kernel structure as for Q4_0 (zt_q4.hip): lane <-> block column, R rows
-// per wave with the 32 activations held in registers, split-K across the
-// waves of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
+// Batch 1 uses the quad mapping of zt_q4.hip (four lanes per block, see
+// gemv_q8_quad_kernel); batched calls use lane <-> block column, R rows per
+// wave with the 32 activations held in registers, split-K across the waves
+// of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
 // which v_cvt_f32_ubyte converts directly; sum (q+128) x - 128 sum x
 // recovers the signed dot product.
 #include "zt_common.h"
@@ -112,6 +113,79 @@ static void launch_q8(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base
     }
 }
 
+// Batch-1 GEMV: four lanes share one block.  Lane q of a quad takes bytes
+// 8q .. 8q+7 of the block's 32 int8 weights (one 8-byte load in the
+// separated layout, two dwords in the raw 36-byte blocks) and the matching 8
+// activations as two 16-byte loads, so a quad reads its block's 128 bytes of
+// activations contiguously.  R rows per wave, split-K over the waves.
+template <bool SEP, int R>
+__global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __restrict__ base, long data_offset,
+                                                           const float* __restrict__ x, float* __restrict__ y,
+                                                           int rows, int kb) {
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
+    const float* scales = reinterpret_cast<const float*>(base);
+    const uint2* data = reinterpret_cast<const uint2*>(base + data_offset);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int b = wave * 16 + (lane >> 2); b < kb; b += nwaves * 16) {
+        uint32_t d[R][2];
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const long blk = rbase[r] + b;
+            if constexpr (SEP) {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(&data[blk * 4 + q]));
+                d[r][0] = v.x;
+                d[r][1] = v.y;
+                s[r] = scales[blk];
+            } else {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(base + blk * 36);
+                s[r] = __uint_as_float(p[0]);
+                d[r][0] = __builtin_nontemporal_load(p + 1 + 2 * q);
+                d[r][1] = __builtin_nontemporal_load(p + 2 + 2 * q);
+            }
+        }
+        const float4 xa = *reinterpret_cast<const float4*>(x + (long)b * 32 + 8 * q);
+        const float4 xb = *reinterpret_cast<const float4*>(x + (long)b * 32 + 8 * q + 4);
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const float xsum = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t u = d[r][i] ^ 0x80808080u;  // bytes q+128
+                s0 = fmaf((float)(u & 0xffu), xv[4 * i], s0);
+                s1 = fmaf((float)((u >> 8) & 0xffu), xv[4 * i + 1], s1);
+                s0 = fmaf((float)((u >> 16) & 0xffu), xv[4 * i + 2], s0);
+                s1 = fmaf((float)(u >> 24), xv[4 * i + 3], s1);
+            }
+            acc[r] = fmaf(s[r], (s0 + s1) - 128.0f * xsum, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <bool SEP>
+static void launch_q8_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
+                           float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_q8_quad_kernel<SEP, 8><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 4: gemv_q8_quad_kernel<SEP, 4><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 2: gemv_q8_quad_kernel<SEP, 2><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        default: gemv_q8_quad_kernel<SEP, 1><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+    }
+}
+
 template <bool SEP>
 static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N, long data_offset, hipStream_t st) {
     if (M < 0 || N < 0 || K < 0 || K % 32 != 0 || data_offset < 0 || N > 65535) return (int)hipErrorInvalidValue;
@@ -122,13 +196,16 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
     if (SEP && ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
+    if (N == 1) {
+        const int nw = min(8, ceil_div(kb, 16));
+        const int R = pick_rows_per_wave(M, nw, 1, 2048);
+        launch_q8_quad<SEP>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
+        return (int)hipGetLastError();
+    }
     const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
     const int R = pick_rows_per_wave(M, nwaves, N, 2048);
     dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
-    if (N == 1)
-        launch_q8<SEP, true>(R, grid, block, st, base, data_offset, B, C, 1, M, kb);
-    else
-        launch_q8<SEP, false>(R, grid, block, st, base, data_offset, B, C, N, M, kb);
+    launch_q8<SEP, false>(R, grid, block, st, base, data_offset, B, C, N, M, kb);
     return (int)hipGetLastError();
 }
 
