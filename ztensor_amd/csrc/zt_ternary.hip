@@ -49,6 +49,7 @@ __global__ void __launch_bounds__(512) ternary_i8_kernel(const uint8_t* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int nchunk = bpr / CB;
     const int row0 = blockIdx.x * R;
+    const float scale = w_scale[0] * x_scale[0];  // issued first: its latency overlaps the weight stream
     long rbase[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * bpr;
@@ -127,7 +128,6 @@ __global__ void __launch_bounds__(512) ternary_i8_kernel(const uint8_t* __restri
 #pragma unroll
     for (int r = 0; r < R; r++) tot[r] = acc[r];
     wave_reduce_rows<R>(tot);
-    const float scale = w_scale[0] * x_scale[0];
     if (nwaves == 1) {
         if (is_row_writer<R>(lane)) {
             const int r = row0 + row_of_lane<R>(lane);
