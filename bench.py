@@ -358,6 +358,25 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
             "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
 
 
+def run_pmc_case(args) -> None:
+    """A short, fixed workload for rocprofv3 counter passes: the 64 MiB
+    calibration copies, then 40 launches of the dominant Q4_0 GEMV (14336 x
+    4096, batch 1) rotating over 20 weight copies (660 MB, beyond the
+    Infinity Cache)."""
+    import torch
+
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    calibration_copy(torch)
+    m = Q4Matrix(torch, lib, 14336, 4096, 0x5EED0024, 20)
+    s = torch.cuda.current_stream().cuda_stream
+    for i in range(40):
+        m.launch(lib, i % 20, s)
+    torch.cuda.synchronize()
+    log("bench: pmc case done")
+
+
 def run_suite(args) -> None:
     import torch
 
@@ -387,6 +406,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
+    ap.add_argument("--pmc-case", action="store_true",
+                    help="short fixed workload for rocprofv3 counter passes (copies + 40 dominant-kernel launches)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -396,6 +417,9 @@ def main() -> None:
         raise SystemExit(2)
     if args.suite:
         run_suite(args)
+        return
+    if args.pmc_case:
+        run_pmc_case(args)
         return
     print(json.dumps(run_headline(args)), flush=True)
 
