@@ -275,15 +275,24 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
 
     int ub, ue;
     mfma_split_range(nunits, ub, ue);
-    for (int c0 = ub; c0 < ue; c0 += kMfmaUC) {
-        uint4 w[kMfmaUPW][NT];
+    // Weights of the next chunk are loaded while the current chunk computes.
+    uint4 wn[kMfmaUPW][NT];
+    auto load_w = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < kMfmaUPW; u++) {
             const int unit = min(c0 + wave + kMfmaWaves * u, ue - 1);
 #pragma unroll
             for (int t = 0; t < NT; t++)
-                w[u][t] = ld_stream(reinterpret_cast<const uint4*>(packed + (long)arow[t] * rowbytes + unit * 64 + 16 * lg));
+                wn[u][t] = ld_stream(reinterpret_cast<const uint4*>(packed + (long)arow[t] * rowbytes + unit * 64 + 16 * lg));
         }
+    };
+    if (ub < ue) load_w(ub);
+    for (int c0 = ub; c0 < ue; c0 += kMfmaUC) {
+        uint4 w[kMfmaUPW][NT];
+#pragma unroll
+        for (int u = 0; u < kMfmaUPW; u++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) w[u][t] = wn[u][t];
         mfma_stage_x(smem, x, c0, ue * 128, N);
         for (int e = tid; e < kMfmaUC * kMfmaRows; e += blockDim.x) {
             const int uu = e / kMfmaRows, r = e % kMfmaRows;
@@ -294,6 +303,7 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
             }
         }
         __syncthreads();
+        if (c0 + kMfmaUC < ue) load_w(c0 + kMfmaUC);
 #pragma unroll
         for (int u = 0; u < kMfmaUPW; u++) {
             const int uu = wave + kMfmaWaves * u;
