@@ -24,8 +24,8 @@
 //    subnormal q * 2^-24 (exact), which v_fma_mix_f32 multiplies straight
 //    into an fp32 accumulator: 5 integer ops + 8 FMAs per 8 weights with no
 //    conversions; sum_j (q_j - 8) x_j = sum_j q_j x_j - 8 * sum_j x_j;
-//  * IQ4_NL: the 16-entry fp32 table sits in LDS; a lookup is one
-//    conflict-free ds_read_b32 (at most 16 distinct addresses per wave);
+//  * IQ4_NL: a 256-entry LDS table maps a data byte to the fp32 codebook
+//    values of its two nibbles, one ds_read_b64 per two weights;
 //  * the block scale multiplies the block's partial sum once.
 // Batched IQ4_NL calls with fp16 activations and 4 <= N <= 16 use the MFMA
 // GEMM further down; other batched calls (N > 1, column-strided
@@ -78,7 +78,7 @@ __device__ __forceinline__ void load_x32(const XT* __restrict__ x, long x_stride
 
 // sum_j w_j x_j over one block, without the block scale.
 template <Fmt F>
-__device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32], float xsum, const float* tbl) {
+__device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32], float xsum, const float2* tbl) {
     const uint32_t d[4] = {w.x, w.y, w.z, w.w};
     if constexpr (F == Fmt::Q4_0) {
         float s0 = 0.0f, s1 = 0.0f;
@@ -98,9 +98,10 @@ __device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32],
 #pragma unroll
         for (int i = 0; i < 4; i++) {
 #pragma unroll
-            for (int m = 0; m < 8; m += 2) {  // nibble m of dword i is element 8i+m
-                s0 = fmaf(tbl[(d[i] >> (4 * m)) & 0xfu], xv[8 * i + m], s0);
-                s1 = fmaf(tbl[(d[i] >> (4 * m + 4)) & 0xfu], xv[8 * i + m + 1], s1);
+            for (int j = 0; j < 4; j++) {  // byte j of dword i holds elements 8i+2j (low), 8i+2j+1 (high)
+                const float2 t = tbl[(d[i] >> (8 * j)) & 0xffu];
+                s0 = fmaf(t.x, xv[8 * i + 2 * j], s0);
+                s1 = fmaf(t.y, xv[8 * i + 2 * j + 1], s1);
             }
         }
         return s0 + s1;
@@ -133,7 +134,7 @@ __device__ __forceinline__ void load_x8(const XT* __restrict__ x, int b, int q, 
 // activation xv[j]) and 16+4q+j (high nibble, xv[4+j]).  IQ4_NL: nibble m
 // is element 8q+m (activation xv[m]).
 template <Fmt F>
-__device__ __forceinline__ float dword_dot(uint32_t d, const float (&xv)[8], float xsum, const float* tbl) {
+__device__ __forceinline__ float dword_dot(uint32_t d, const float (&xv)[8], float xsum, const float2* tbl) {
     if constexpr (F == Fmt::Q4_0) {
         const uint32_t d8 = d >> 8;
         const half2v m0 = as_half2(d & 0x000F000Fu);   // bytes 0,2 low nibbles  (q * 2^-24)
@@ -152,9 +153,10 @@ __device__ __forceinline__ float dword_dot(uint32_t d, const float (&xv)[8], flo
     } else {
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 8; m += 2) {
-            s0 = fmaf(tbl[(d >> (4 * m)) & 0xfu], xv[m], s0);
-            s1 = fmaf(tbl[(d >> (4 * m + 4)) & 0xfu], xv[m + 1], s1);
+        for (int j = 0; j < 4; j++) {  // byte j: elements 8q+2j (low nibble), 8q+2j+1 (high nibble)
+            const float2 t = tbl[(d >> (8 * j)) & 0xffu];
+            s0 = fmaf(t.x, xv[2 * j], s0);
+            s1 = fmaf(t.y, xv[2 * j + 1], s1);
         }
         return s0 + s1;
     }
@@ -166,11 +168,11 @@ __global__ void __launch_bounds__(512) gemv_quad_kernel(const uint16_t* __restri
                                                         const XT* __restrict__ x, float* __restrict__ y,
                                                         int rows, int kb) {
     __shared__ float red[8 * R];
-    __shared__ float tbl[16];
+    __shared__ float2 tbl[256];  // IQ4_NL: byte value -> (T[low nibble], T[high nibble])
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int q = lane & 3;
     if constexpr (F == Fmt::IQ4NL) {
-        if (threadIdx.x < 16) tbl[threadIdx.x] = kIQ4NLTable[threadIdx.x];
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = make_float2(kIQ4NLTable[i & 0xf], kIQ4NLTable[i >> 4]);
         __syncthreads();
     }
     const int row0 = blockIdx.x * R;
@@ -333,10 +335,10 @@ __global__ void __launch_bounds__(512) gemv_blk18_kernel(const uint16_t* __restr
                                                          const XT* __restrict__ x, float* __restrict__ y,
                                                          long xy_stride, int rows, int kb) {
     __shared__ float red[8 * R];
-    __shared__ float tbl[16];
+    __shared__ float2 tbl[256];  // IQ4_NL: byte value -> (T[low nibble], T[high nibble])
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     if constexpr (F == Fmt::IQ4NL) {
-        if (threadIdx.x < 16) tbl[threadIdx.x] = kIQ4NLTable[threadIdx.x];
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = make_float2(kIQ4NLTable[i & 0xf], kIQ4NLTable[i >> 4]);
         __syncthreads();
     }
     x += blockIdx.y;
