@@ -227,6 +227,8 @@ def run_headline(args) -> dict:
     if dom is not None:
         dom["traffic"] = measured_traffic(dom["kernel"])
 
+    merged = run_merged_step(torch, lib, args) if args.merged else None
+
     # Parity spot check of the last replayed outputs against the oracle.
     from oracle import oracle
 
@@ -262,9 +264,40 @@ def run_headline(args) -> dict:
             "parity_rel_err": err,
         },
         "per_shape": per_shape,
+        "merged_projections": merged,
         "roofline": dom,
         "cpu_baseline": cpu,
     }
+
+
+def run_merged_step(torch, lib, args) -> dict:
+    """The same 32-layer decode step with Q/K/V and Gate/Up merged row-wise
+    (MergeQ4Storage, tensor/quantized.go:224-242): 4 GEMVs per layer
+    (6144x4096, 4096x4096, 28672x4096, 4096x14336 as rows x K) moving the
+    same bytes as the 7 separate ones.  Reported beside the headline, which
+    keeps one GEMV per projection."""
+    layers = args.layers
+    shapes = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+    mats = [Q4Matrix(torch, lib, rows, K, 0x5EED0040 + i, layers) for i, (_, rows, K) in enumerate(shapes)]
+    step_bytes = layers * sum(m.bytes for m in mats)
+
+    def step():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            for m in mats:
+                m.launch(lib, layer, s)
+
+    g = graph_of(torch, step)
+    for _ in range(args.warmup):
+        g.replay()
+    ms = time_graph(torch, g, args.steps)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    log(f"bench: merged Q/K/V and Gate/Up: {ms * 1e3:.1f} us/step, {value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}%)")
+    del mats
+    torch.cuda.empty_cache()
+    return {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "bytes_per_step": step_bytes,
+            "pct_of_peak": round(100 * value / PEAK_GBS, 1),
+            "shapes_rows_x_K": [f"{rows}x{K}" for _, rows, K in shapes]}
 
 
 # ------------------------------------------------------------ suite mode
@@ -404,6 +437,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--no-merged", dest="merged", action="store_false",
+                    help="skip the merged Q/K/V + Gate/Up variant reported beside the headline")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
     ap.add_argument("--pmc-case", action="store_true",

@@ -81,3 +81,26 @@ def test_storage_constructors_validate_like_reference():
         IQ4NLStorage.from_raw(np.zeros(0, np.uint8), -1)
     with pytest.raises(ValueError):
         Q8Storage.from_blocks(np.zeros(1, np.float32), np.zeros(31, np.int8), 32)
+
+
+def test_merge_storages_concatenate_blocks_like_reference(orc):
+    """MergeQ4Storage / MergeIQ4NLStorage (tensor/quantized.go:224-242,
+    tensor/iq4_storage.go:124-140): blocks in order, lengths summed; the
+    merged Q/K/V storage dequantizes to the three matrices stacked row-wise
+    and uploads to the RawBytesGPU layout of the concatenated blocks."""
+    from ztensor_amd import synth
+    from ztensor_amd.storage import IQ4NLStorage, Q4Storage, merge_iq4nl_storage, merge_q4_storage
+
+    parts = [synth.q4_0(rows, 256, 40 + i) for i, rows in enumerate((64, 16, 16))]
+    st = [Q4Storage.from_raw(p.raw, p.rows * p.K) for p in parts]
+    m = merge_q4_storage(*st)
+    assert m.len == 96 * 256 and m.num_blocks() == sum(s.num_blocks() for s in st)
+    want = np.concatenate([orc.q4_dequant(p.raw, p.rows * p.K) for p in parts])
+    assert np.array_equal(orc.q4_dequant(m.raw_bytes(), m.len).view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(m.raw_bytes_gpu(), orc.q4_raw_to_gpu(np.concatenate([p.raw for p in parts]), m.num_blocks()))
+    iparts = [synth.iq4nl(rows, 128, 50 + i) for i, rows in enumerate((8, 4))]
+    mi = merge_iq4nl_storage(*[IQ4NLStorage.from_raw(p.raw, p.rows * p.K) for p in iparts])
+    want = np.concatenate([orc.iq4nl_dequant(p.raw, p.rows * p.K) for p in iparts])
+    assert np.array_equal(orc.iq4nl_dequant(mi.raw_bytes(), mi.len).view(np.uint32), want.view(np.uint32))
+    with pytest.raises(ValueError):
+        merge_q4_storage()

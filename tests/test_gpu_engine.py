@@ -165,3 +165,19 @@ def test_ternary_gemv_matches_oracle(eng, orc):
     x = synth.x_f32(cols, 19)
     y = eng.ternary_gemv(TernaryStorage(t.raw, rows * cols), x, rows, cols)
     assert rel_err(y, orc.ternary_gemv(t.raw, x, rows, cols)) <= TOL
+
+
+def test_merged_qkv_storage_equals_separate_gemvs(eng, orc):
+    """A merged Q/K/V storage (MergeQ4Storage) gives, in one GEMV, the three
+    projections stacked: rows 0..4095 = Q, then K, then V."""
+    from ztensor_amd.storage import merge_q4_storage
+
+    K = 4096
+    parts = [synth.q4_0(rows, K, 60 + i) for i, rows in enumerate((4096, 1024, 1024))]
+    st = [Q4Storage.from_raw(p.raw, p.rows * K) for p in parts]
+    x = torch.from_numpy(synth.x_f32(K, 60)).cuda()
+    merged = eng.matmul(Tensor((6144, K), merge_q4_storage(*st)), x).cpu().numpy().reshape(-1)
+    sep = np.concatenate([eng.matmul(Tensor((p.rows, K), s), x).cpu().numpy().reshape(-1) for p, s in zip(parts, st)])
+    assert rel_err(merged, sep) <= 1e-6  # same kernel, row reduction order may differ with the row-tile size
+    ref = np.concatenate([orc.gemm_f32_q4_nt(x.cpu().numpy(), p.raw, 1, p.rows, K) for p in parts])
+    assert rel_err(merged, ref) <= TOL

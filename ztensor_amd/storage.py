@@ -4,9 +4,10 @@ Each class holds the reference's serialised bytes on the host (numpy) and
 knows its device upload layout.  Names and semantics follow the Go types so a
 caller of tensor.Q4Storage & co. finds the same surface:
 
-  Q4Storage      tensor/quantized.go:22-274   (RawBytes, RawBytesGPU, NumBlocks, SetGPUPtr/GPUPtr)
+  Q4Storage      tensor/quantized.go:22-274   (RawBytes, RawBytesGPU, NumBlocks, SetGPUPtr/GPUPtr,
+                                               MergeQ4Storage -> merge_q4_storage)
   Q8Storage      tensor/quantized.go:288-478  (36-byte blocks, fp32 scale)
-  IQ4NLStorage   tensor/iq4_storage.go:48-142
+  IQ4NLStorage   tensor/iq4_storage.go:48-142 (MergeIQ4NLStorage -> merge_iq4nl_storage)
   GPTQStorage    tensor/quantized_gptq.go:30-280 (bits = 4 for W4A16)
   AWQStorage     tensor/quantized_awq.go:30-321
   TernaryStorage tensor/ternary_storage.go:7-95
@@ -91,6 +92,17 @@ class Q4Storage(_GPUPtrMixin):
         return _lib.load().zt_q4_gpu_data_offset(self.num_blocks())
 
 
+def merge_q4_storage(*storages: "Q4Storage") -> "Q4Storage":
+    """MergeQ4Storage (tensor/quantized.go:224-242): the blocks of every
+    storage, in order, as one storage whose length is the sum of the lengths.
+    Merging the row-major Q, K and V (or Gate and Up) weights this way gives
+    one [sum(rows), K] matrix, so a decode step runs one GEMV instead of
+    three (or two)."""
+    if not storages:
+        raise ValueError("merge_q4_storage: no storages")
+    return Q4Storage(np.concatenate([st.raw for st in storages]), sum(st.len for st in storages))
+
+
 @dataclass
 class IQ4NLStorage(_GPUPtrMixin):
     raw: np.ndarray
@@ -123,6 +135,14 @@ class IQ4NLStorage(_GPUPtrMixin):
 
     def gpu_data_offset(self) -> int:
         return _lib.load().zt_q4_gpu_data_offset(self.num_blocks())
+
+
+def merge_iq4nl_storage(*storages: "IQ4NLStorage") -> "IQ4NLStorage":
+    """MergeIQ4NLStorage (tensor/iq4_storage.go:124-140): raw blocks
+    concatenated in order, lengths summed."""
+    if not storages:
+        raise ValueError("merge_iq4nl_storage: no storages")
+    return IQ4NLStorage(np.concatenate([st.raw for st in storages]), sum(st.len for st in storages))
 
 
 @dataclass
