@@ -26,6 +26,11 @@
  *                  (tensor/quantized_gptq.go:217-277, tensor/quantized_awq.go:23-39)
  *   Ternary:       row-aligned 2-bit codes [M, ceil(K/4)]
  *                  (compute/ternary_gemv_gpu.go:52-67)
+ *   Q4_K/Q5_K/Q6_K: the raw contiguous super-blocks (144/176/210 bytes per
+ *                  256 values) RawBytes() holds, uploaded unchanged as the
+ *                  reference does (compute/gpu_engine.go:817-874)
+ *   Q5_0:          [fp16 d nblk*2][pad 16][uint32 qh nblk*4][pad 16][qs nblk*16]
+ *                  (tensor/quantized_q5_0.go:118-165 RawBytesGPU)
  */
 #ifndef ZT_HIP_H
 #define ZT_HIP_H
@@ -147,6 +152,51 @@ int zt_dequant_ternary_f32(const void* W_ternary, float* out, int M, int K, zt_s
  * row-aligned layout, the repack of compute/ternary_gemv_gpu.go:55-67.
  * out holds M*ceil(K/4) bytes. */
 void zt_ternary_repack_rows(const void* raw, long M, long K, void* out);
+
+/* ---- K-quants (Q4_K, Q5_K, Q6_K) and Q5_0 ------------------------------- */
+
+/* Batch-1 GEMV y[M] = dequant(W)[M,K] x[K], fp32 x and y, W the raw
+ * super-blocks [M, K/256] as uploaded by GPUEngine.UploadWeights
+ * (compute/gpu_engine.go:817-874).  They replace gemv_q4k_f32 /
+ * gemv_q5k_f32 / gemv_q6k_f32 (internal/cuda/kernels/gemv_q4k.cu:146-160,
+ * gemv_q5k.cu:160-170, gemv_q6k.cu:135-145) behind KernelRunner.GemvQ4KF32 /
+ * GemvQ5KF32 / GemvQ6KF32 (internal/gpuapi/kernels.go:50-63), whose ROCm
+ * implementations return "not implemented"
+ * (internal/gpuapi/rocm_kernels.go:113-123).  K % 256 != 0 -> InvalidValue,
+ * as the reference launchers.  W: 16-byte aligned (Q6_K: 2-byte), x 16-byte. */
+int zt_gemv_q4k_f32(const void* W, const float* x, float* y, int M, int K, zt_stream_t stream);
+int zt_gemv_q5k_f32(const void* W, const float* x, float* y, int M, int K, zt_stream_t stream);
+int zt_gemv_q6k_f32(const void* W, const float* x, float* y, int M, int K, zt_stream_t stream);
+
+/* Replaces gemv_q5_0_f32 (internal/cuda/kernels/gemv_q5_0.cu:108-125) behind
+ * KernelRunner.GemvQ5_0F32 (internal/gpuapi/kernels.go:65-69; ROCm stub
+ * internal/gpuapi/rocm_kernels.go:125-127).  W is the RawBytesGPU layout,
+ * qh_offset / qs_offset = Q5_0GPUQhOffset / Q5_0GPUQsOffset(M*K/32)
+ * (tensor/quantized_q5_0.go:151-165).  K % 32 != 0 -> InvalidValue. */
+int zt_gemv_q5_0_f32(const void* W, const float* x, float* y, int M, int K, int qh_offset, int qs_offset,
+                     zt_stream_t stream);
+
+/* Device dequantizers, bit-exact with Q4KStorage / Q5KStorage / Q6KStorage
+ * .Dequantize (tensor/quantized_kquant.go:263-277, 579-593, 412-426); they
+ * replace dequant_q4k_f32 etc. behind KernelRunner.DequantQ4KF32 /
+ * DequantQ5KF32 / DequantQ6KF32 (internal/gpuapi/kernels.go:71-76).  W is
+ * [rows, K] raw super-blocks, out rows*K floats, K % 256 == 0. */
+int zt_dequant_q4k_f32(const void* W, float* out, int rows, int K, zt_stream_t stream);
+int zt_dequant_q5k_f32(const void* W, float* out, int rows, int K, zt_stream_t stream);
+int zt_dequant_q6k_f32(const void* W, float* out, int rows, int K, zt_stream_t stream);
+/* Bit-exact with Q5_0Storage.Dequantize (tensor/quantized_q5_0.go:26-45,
+ * 75-90) over the raw 22-byte blocks, the layout dequant_q5_0_f32 reads
+ * (internal/cuda/kernels/dequant_q5_0.cu:18-67; KernelRunner.DequantQ5_0F32,
+ * internal/gpuapi/kernels.go:77).  K % 32 == 0. */
+int zt_dequant_q5_0_f32(const void* W, float* out, int rows, int K, zt_stream_t stream);
+
+/* Host: Q5_0Storage.RawBytes (22-byte blocks) -> RawBytesGPU
+ * (tensor/quantized_q5_0.go:118-147); offsets as Q5_0GPUQhOffset /
+ * Q5_0GPUQsOffset (:151-165); out holds zt_q5_0_gpu_bytes(nblk) bytes. */
+long zt_q5_0_gpu_qh_offset(long nblk);
+long zt_q5_0_gpu_qs_offset(long nblk);
+long zt_q5_0_gpu_bytes(long nblk);
+void zt_q5_0_raw_to_gpu(const void* raw, long nblk, void* out);
 
 #ifdef __cplusplus
 }

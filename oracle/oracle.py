@@ -40,6 +40,16 @@ _SIG = {
     "orc_ternary_gemv": (None, [P, P, L, L, P]),
     "orc_ternary_repack_rows": (None, [P, L, L, P]),
     "orc_ternary_gemv_i8": (None, [P, P, F, F, L, L, P, P]),
+    "orc_kq_scales_mins": (None, [P, P, P]),
+    "orc_q4k_dequant": (None, [P, L, P]),
+    "orc_q5k_dequant": (None, [P, L, P]),
+    "orc_q6k_dequant": (None, [P, L, P]),
+    "orc_gemm_f32_kq_nt": (None, [I, L, L, L, P, P, P, I]),
+    "orc_q5_0_dequant": (None, [P, L, P]),
+    "orc_q5_0_gpu_qh_offset": (L, [L]),
+    "orc_q5_0_gpu_qs_offset": (L, [L]),
+    "orc_q5_0_raw_to_gpu": (None, [P, L, P]),
+    "orc_gemm_f32_q5_0_nt": (None, [L, L, L, P, P, P, P, P]),
 }
 
 _lib = None
@@ -196,3 +206,55 @@ def ternary_gemv_i8(raw, qx, x_scale, w_scale, rows: int, cols: int) -> np.ndarr
 
 def ternary_get(raw: np.ndarray, i: int) -> int:
     return lib().orc_ternary_get(_p(raw), i)
+
+
+# ---- K-quants and Q5_0 ----------------------------------------------------
+
+KQ_FMT = {"q4_k": 4, "q5_k": 5, "q6_k": 6}
+
+
+def kq_scales_mins(block: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    block = np.ascontiguousarray(block, np.uint8)
+    sc = np.empty(8, np.uint8)
+    mn = np.empty(8, np.uint8)
+    lib().orc_kq_scales_mins(_p(block), _p(sc), _p(mn))
+    return sc, mn
+
+
+def kq_dequant(fmt: str, raw: np.ndarray, nelem: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.empty(nelem, np.float32)
+    getattr(lib(), f"orc_{fmt.replace('_', '')}_dequant")(_p(raw), nelem, _p(out))
+    return out
+
+
+def gemm_f32_kq_nt(fmt: str, a: np.ndarray, raw: np.ndarray, m: int, n: int, k: int, threads: int = 1) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    raw = np.ascontiguousarray(raw, np.uint8)
+    c = np.empty(m * n, np.float32)
+    lib().orc_gemm_f32_kq_nt(KQ_FMT[fmt], m, n, k, _p(a), _p(raw), _p(c), threads)
+    return c
+
+
+def q5_0_dequant(raw: np.ndarray, nelem: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.empty(nelem, np.float32)
+    lib().orc_q5_0_dequant(_p(raw), nelem, _p(out))
+    return out
+
+
+def q5_0_raw_to_gpu(raw: np.ndarray, nblk: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.empty(lib().orc_q5_0_gpu_qs_offset(nblk) + 16 * nblk, np.uint8)
+    lib().orc_q5_0_raw_to_gpu(_p(raw), nblk, _p(out))
+    return out
+
+
+def gemm_f32_q5_0_nt(a: np.ndarray, raw: np.ndarray, m: int, n: int, k: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    raw = np.ascontiguousarray(raw, np.uint8)
+    c = np.empty(m * n, np.float32)
+    wt = np.empty(n * k, np.float32)
+    tt = np.empty(n * k, np.float32)
+    lib().orc_gemm_f32_q5_0_nt(m, n, k, _p(a), _p(raw), _p(c), _p(wt), _p(tt))
+    return c

@@ -482,3 +482,228 @@ EXPORT void orc_ternary_gemv_i8(const uint8_t* raw, const int8_t* qx, float x_sc
     float s = w_scale * x_scale;
     for (int64_t i = 0; i < rows; i++) y[i] = y[i] * s;
 }
+
+/* ------------------------------------------------------------- K-quants */
+
+/* tensor/quantized_kquant.go:34-51 decodeQ4KScalesMins: the 6-bit scales and
+ * mins of the eight 32-value sub-blocks, packed in bytes 4..15 of a Q4_K or
+ * Q5_K super-block (Q5_K reuses it, :513). */
+EXPORT void orc_kq_scales_mins(const uint8_t* blk, uint8_t* scales, uint8_t* mins) {
+    const uint8_t* sc = blk + 4;
+    for (int i = 0; i < 4; i++) {
+        scales[i] = sc[i] & 63;
+        mins[i] = sc[4 + i] & 63;
+    }
+    for (int i = 0; i < 4; i++) {
+        scales[4 + i] = (uint8_t)((sc[8 + i] & 0xF) | ((sc[i] >> 6) << 4));
+        mins[4 + i] = (uint8_t)((sc[8 + i] >> 4) | ((sc[4 + i] >> 6) << 4));
+    }
+}
+
+/* tensor/quantized_kquant.go:54-79 DequantizeQ4K: one 144-byte super-block
+ * [fp16 d][fp16 dmin][12 bytes scales/mins][128 bytes nibbles] -> 256 values.
+ * Group g (64 values) reads bytes 32g..32g+31: low nibble of byte l ->
+ * value 64g+l (sub-block 2g), high nibble -> 64g+32+l (sub-block 2g+1);
+ * value = (d*sc)*q - dmin*mn, each product and the difference rounded. */
+static void q4k_block(const uint8_t* b, float* dst) {
+    float d = orc_f16_to_f32(rd16(b)), dmin = orc_f16_to_f32(rd16(b + 2));
+    uint8_t scales[8], mins[8];
+    orc_kq_scales_mins(b, scales, mins);
+    const uint8_t* q = b + 16;
+    for (int g = 0; g < 4; g++) {
+        float sc0 = d * (float)scales[2 * g], mn0 = dmin * (float)mins[2 * g];
+        float sc1 = d * (float)scales[2 * g + 1], mn1 = dmin * (float)mins[2 * g + 1];
+        for (int l = 0; l < 32; l++) {
+            uint8_t v = q[32 * g + l];
+            dst[64 * g + l] = sc0 * (float)(v & 0xF) - mn0;
+            dst[64 * g + l + 32] = sc1 * (float)(v >> 4) - mn1;
+        }
+    }
+}
+
+/* Partial last super-block through a 256-value temporary, as every
+ * K-quant Dequantize does (tensor/quantized_kquant.go:263-277, 412-426,
+ * 579-593). */
+typedef void (*orc_kq_block_fn)(const uint8_t*, float*);
+static void kq_dequant(orc_kq_block_fn fn, int bytes, const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 255) / 256;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        int64_t off = bi * 256, rem = nelem - off;
+        if (rem >= 256) {
+            fn(raw + bi * bytes, dst + off);
+        } else {
+            float tmp[256];
+            fn(raw + bi * bytes, tmp);
+            memcpy(dst + off, tmp, sizeof(float) * (size_t)rem);
+        }
+    }
+}
+
+/* tensor/quantized_kquant.go:263-277 Q4KStorage.Dequantize. */
+EXPORT void orc_q4k_dequant(const uint8_t* raw, int64_t nelem, float* dst) { kq_dequant(q4k_block, 144, raw, nelem, dst); }
+
+/* tensor/quantized_kquant.go:355-382 DequantizeQ6K: one 210-byte super-block
+ * [128 ql][64 qh][16 int8 scales][fp16 d].  Half h (128 values) uses ql
+ * bytes 64h.., qh bytes 32h.. and scales 8h..; for l < 32 (is = l/16):
+ *   q1 = (ql[l] & 15 | (qh[l] & 3) << 4) - 32           -> value l,      scale is
+ *   q2 = (ql[32+l] & 15 | (qh[l] >> 2 & 3) << 4) - 32   -> value 32+l,   scale is+2
+ *   q3 = (ql[l] >> 4 | (qh[l] >> 4 & 3) << 4) - 32      -> value 64+l,   scale is+4
+ *   q4 = (ql[32+l] >> 4 | (qh[l] >> 6 & 3) << 4) - 32   -> value 96+l,   scale is+6
+ * value = (d * scale) * q, two roundings left to right. */
+static void q6k_block(const uint8_t* b, float* dst) {
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    const int8_t* sc = (const int8_t*)(b + 192);
+    float d = orc_f16_to_f32(rd16(b + 208));
+    for (int h = 0; h < 2; h++) {
+        const uint8_t* l0 = ql + 64 * h;
+        const uint8_t* h0 = qh + 32 * h;
+        const int8_t* s0 = sc + 8 * h;
+        float* o = dst + 128 * h;
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (int)(int8_t)((l0[l] & 0xF) | ((h0[l] & 3) << 4)) - 32;
+            int q2 = (int)(int8_t)((l0[32 + l] & 0xF) | (((h0[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)(int8_t)((l0[l] >> 4) | (((h0[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)(int8_t)((l0[32 + l] >> 4) | (((h0[l] >> 6) & 3) << 4)) - 32;
+            o[l] = d * (float)s0[is + 0] * (float)q1;
+            o[32 + l] = d * (float)s0[is + 2] * (float)q2;
+            o[64 + l] = d * (float)s0[is + 4] * (float)q3;
+            o[96 + l] = d * (float)s0[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* tensor/quantized_kquant.go:412-426 Q6KStorage.Dequantize. */
+EXPORT void orc_q6k_dequant(const uint8_t* raw, int64_t nelem, float* dst) { kq_dequant(q6k_block, 210, raw, nelem, dst); }
+
+/* tensor/quantized_kquant.go:509-549 DequantizeQ5K: one 176-byte super-block
+ * [fp16 d][fp16 dmin][12 bytes scales/mins][128 ql][32 qh].  As Q4_K, plus
+ * a fifth bit: for group g, bit 2g of qh[l] adds 16 to the low-nibble value
+ * 64g+l and bit 2g+1 adds 16 to the high-nibble value 64g+32+l. */
+static void q5k_block(const uint8_t* b, float* dst) {
+    float d = orc_f16_to_f32(rd16(b)), dmin = orc_f16_to_f32(rd16(b + 2));
+    uint8_t scales[8], mins[8];
+    orc_kq_scales_mins(b, scales, mins);
+    const uint8_t* ql = b + 16;
+    const uint8_t* qh = b + 144;
+    uint8_t u1 = 1, u2 = 2;
+    for (int g = 0; g < 4; g++) {
+        float sc0 = d * (float)scales[2 * g], mn0 = dmin * (float)mins[2 * g];
+        float sc1 = d * (float)scales[2 * g + 1], mn1 = dmin * (float)mins[2 * g + 1];
+        for (int l = 0; l < 32; l++) {
+            uint8_t q = ql[32 * g + l], hb = qh[l];
+            uint8_t hi0 = (hb & u1) ? 16 : 0, hi1 = (hb & u2) ? 16 : 0;
+            dst[64 * g + l] = sc0 * (float)((q & 0xF) | hi0) - mn0;
+            dst[64 * g + l + 32] = sc1 * (float)((q >> 4) | hi1) - mn1;
+        }
+        u1 = (uint8_t)(u1 << 2);
+        u2 = (uint8_t)(u2 << 2);
+    }
+}
+
+/* tensor/quantized_kquant.go:579-593 Q5KStorage.Dequantize. */
+EXPORT void orc_q5k_dequant(const uint8_t* raw, int64_t nelem, float* dst) { kq_dequant(q5k_block, 176, raw, nelem, dst); }
+
+/* One output of the K-quant GEMV-NTs: the row's super-blocks dequantized in
+ * order and sum += a[p] * w[p] over all K values in element order.
+ * GemmF32Q4KNT (internal/xblas/gemm_q4k.go:54-103) dequantizes per 32-value
+ * sub-block with DequantizeSubBlock (tensor/quantized_kquant.go:82-106),
+ * whose values equal DequantizeQ4K's (same d*sc, dmin*mn and formula);
+ * GemmF32Q5KNT / GemmF32Q6KNT (internal/xblas/gemm_quant.go:273-317,
+ * 384-428) dequantize whole super-blocks.  Either way the summation order is
+ * p = 0 .. K-1 into one fp32 accumulator. */
+typedef struct { const float* a; const uint8_t* raw; float* c; int64_t bpr; orc_kq_block_fn fn; int bytes; } kqnt_ctx;
+static float kq_dot_row(const kqnt_ctx* t, const uint8_t* row) {
+    float buf[256], sum = 0.0f;
+    for (int64_t bi = 0; bi < t->bpr; bi++) {
+        t->fn(row + bi * t->bytes, buf);
+        const float* ab = t->a + bi * 256;
+        for (int p = 0; p < 256; p++) sum += ab[p] * buf[p];
+    }
+    return sum;
+}
+static void kqnt_range(void* p, int64_t j0, int64_t j1) {
+    kqnt_ctx* t = (kqnt_ctx*)p;
+    for (int64_t j = j0; j < j1; j++) t->c[j] = kq_dot_row(t, t->raw + j * t->bpr * t->bytes);
+}
+
+/* fmt: 4 = Q4_K, 5 = Q5_K, 6 = Q6_K.  C[M,N] = A[M,K] * B^T, B = [N,K] in
+ * contiguous super-blocks, K % 256 == 0 (the reference's other branch
+ * dequantizes fully and calls SgemmSimd).  M = 1 with N*K >= 65536 splits N
+ * over min(NumCPU, N/4) workers (gemm_q4k.go:72-79, gemm_quant.go:286-293,
+ * 397-404); every output is computed whole by one worker, so the split does
+ * not change any bit. */
+EXPORT void orc_gemm_f32_kq_nt(int fmt, int64_t m, int64_t n, int64_t k, const float* a, const uint8_t* raw,
+                               float* c, int nthreads) {
+    kqnt_ctx ctx = {a, raw, c, k / 256, fmt == 4 ? q4k_block : fmt == 5 ? q5k_block : q6k_block,
+                    fmt == 4 ? 144 : fmt == 5 ? 176 : 210};
+    if (m == 1 && n * k >= 256 * 256) {
+        int nc = nthreads;
+        if (nc > n / 4) nc = (int)(n / 4);
+        if (nc > 1) {
+            orc_parallel_rows(n, nc, kqnt_range, &ctx);
+            return;
+        }
+    }
+    for (int64_t i = 0; i < m; i++) {
+        ctx.a = a + i * k;
+        ctx.c = c + i * n;
+        kqnt_range(&ctx, 0, n);
+    }
+}
+
+/* ------------------------------------------------------------------ Q5_0 */
+
+/* tensor/quantized_q5_0.go:26-45 DequantizeQ5_0: 22-byte block [fp16 d]
+ * [uint32 qh LE][16 bytes qs]; value j = d*((qs[j] & 15 | bit j of qh << 4) - 16),
+ * value j+16 = d*((qs[j] >> 4 | bit j+16 of qh << 4) - 16).  :75-90
+ * Q5_0Storage.Dequantize handles the partial last block. */
+EXPORT void orc_q5_0_dequant(const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 31) / 32;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        const uint8_t* b = raw + bi * 22;
+        float d = orc_f16_to_f32(rd16(b));
+        uint32_t qh = rd32(b + 2);
+        float tmp[32];
+        for (int j = 0; j < 16; j++) {
+            uint8_t packed = b[6 + j];
+            int x0 = (int)((packed & 0x0F) | (((qh >> j) & 1) << 4)) - 16;
+            int x1 = (int)((packed >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+            tmp[j] = d * (float)x0;
+            tmp[j + 16] = d * (float)x1;
+        }
+        int64_t off = bi * 32, rem = nelem - off;
+        memcpy(dst + off, tmp, sizeof(float) * (size_t)(rem >= 32 ? 32 : rem));
+    }
+}
+
+/* tensor/quantized_q5_0.go:151-165 Q5_0GPUQhOffset / Q5_0GPUQsOffset. */
+EXPORT int64_t orc_q5_0_gpu_qh_offset(int64_t nblk) { return (nblk * 2 + 15) & ~(int64_t)15; }
+EXPORT int64_t orc_q5_0_gpu_qs_offset(int64_t nblk) {
+    return orc_q5_0_gpu_qh_offset(nblk) + ((nblk * 4 + 15) & ~(int64_t)15);
+}
+
+/* tensor/quantized_q5_0.go:118-147 RawBytesGPU: [fp16 d, nblk*2][pad 16]
+ * [uint32 qh, nblk*4][pad 16][qs, nblk*16]. */
+EXPORT void orc_q5_0_raw_to_gpu(const uint8_t* raw, int64_t nblk, uint8_t* out) {
+    int64_t qh = orc_q5_0_gpu_qh_offset(nblk), qs = orc_q5_0_gpu_qs_offset(nblk);
+    memset(out, 0, (size_t)qs);
+    for (int64_t i = 0; i < nblk; i++) {
+        memcpy(out + i * 2, raw + i * 22, 2);
+        memcpy(out + qh + i * 4, raw + i * 22 + 2, 4);
+        memcpy(out + qs + i * 16, raw + i * 22 + 6, 16);
+    }
+}
+
+/* compute/cpu_engine.go:2450-2473, Q5_0 weights on the B side: dequantize
+ * the [N,K] weights, transpose to [K,N], SgemmSimd into a zeroed C[M,N].
+ * wtmp and ttmp each hold N*K floats. */
+EXPORT void orc_gemm_f32_q5_0_nt(int64_t m, int64_t n, int64_t k, const float* a, const uint8_t* raw, float* c,
+                                 float* wtmp, float* ttmp) {
+    orc_q5_0_dequant(raw, n * k, wtmp);
+    for (int64_t r = 0; r < n; r++)
+        for (int64_t col = 0; col < k; col++) ttmp[col * n + r] = wtmp[r * k + col];
+    memset(c, 0, sizeof(float) * (size_t)(m * n));
+    orc_sgemm_simd(m, n, k, a, ttmp, c);
+}

@@ -104,3 +104,31 @@ def test_merge_storages_concatenate_blocks_like_reference(orc):
     assert np.array_equal(orc.iq4nl_dequant(mi.raw_bytes(), mi.len).view(np.uint32), want.view(np.uint32))
     with pytest.raises(ValueError):
         merge_q4_storage()
+
+
+def test_q5_0_gpu_layout_matches_oracle(orc):
+    from ztensor_amd.storage import Q5_0Storage
+
+    for rows, K in [(1, 32), (3, 96), (16, 4096)]:
+        w = synth.kquant("q5_0", rows, K, 5)
+        s = Q5_0Storage.from_raw(w.raw, rows * K)
+        nblk = rows * K // 32
+        assert np.array_equal(s.raw_bytes_gpu(), orc.q5_0_raw_to_gpu(w.raw, nblk))
+        assert s.gpu_qh_offset() == orc.lib().orc_q5_0_gpu_qh_offset(nblk)
+        assert s.gpu_qs_offset() == orc.lib().orc_q5_0_gpu_qs_offset(nblk)
+
+
+def test_kquant_storage_constructors_validate_like_the_reference():
+    from ztensor_amd.storage import Q4KStorage, Q5KStorage, Q6KStorage, merge_q4k_storage
+
+    # NewQ4KStorageFromRaw_InvalidSize (tensor/quantized_kquant_test.go:208-213)
+    with pytest.raises(ValueError):
+        Q4KStorage.from_raw(np.zeros(10, np.uint8), 256)
+    with pytest.raises(ValueError):
+        Q6KStorage.from_raw(np.zeros(210, np.uint8), 0)
+    s = Q5KStorage.from_raw(np.zeros(3 * 176 + 5, np.uint8), 700)
+    assert s.num_blocks() == 3 and s.raw_bytes().size == 3 * 176
+    a = Q4KStorage.from_raw(synth.kquant("q4_k", 2, 256, 1).raw, 512)
+    b = Q4KStorage.from_raw(synth.kquant("q4_k", 1, 256, 2).raw, 256)
+    m = merge_q4k_storage(a, b)  # TestMergeQ4KStorage (tensor/quantized_kquant_test.go:496-543)
+    assert m.len == 768 and np.array_equal(m.raw, np.concatenate([a.raw, b.raw]))

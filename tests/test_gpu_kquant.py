@@ -1,0 +1,213 @@
+"""GPU parity of the K-quant (Q4_K, Q5_K, Q6_K) and Q5_0 entry points against
+the CPU oracle, through the C ABI and the engine.
+
+Bars: dequantizers bit-exact (uint32 view equality); GEMVs
+max|y - y_ref| / max|y_ref| <= 1e-3 with fp32 accumulation, y_ref = the
+reference CPU engine's GemmF32Q4KNT / Q5KNT / Q6KNT and its Q5_0 B-side
+matmul as restated by the oracle.  Shapes: the Llama-3-8B decode layers,
+plus ragged cases (one super-block, partial wave steps, odd super-block
+counts that leave Q6_K blocks 2-byte aligned, a 2-byte offset base).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from ztensor_amd import _lib, synth  # noqa: E402
+from ztensor_amd.storage import Q4KStorage, Q5_0Storage, Q6KStorage, Tensor  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+KQ = ["q4_k", "q5_k", "q6_k"]
+LLAMA8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+RAGGED = [(1, 256), (17, 768), (65, 2560), (5, 6912), (130, 1792)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return _lib.load()
+
+
+def dev(a: np.ndarray, pad: int = 0) -> "torch.Tensor":
+    b = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+    t = torch.zeros(b.size + pad, dtype=torch.uint8)
+    t[pad:] = torch.from_numpy(b.copy())
+    return t.cuda()
+
+
+def devf(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rel_err(y, ref) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def kq_gemv(lib, fmt, w_dev_ptr, x, rows, K):
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = devf(x)
+    lib.call(f"zt_gemv_{fmt.replace('_', '')}_f32", w_dev_ptr, xd.data_ptr(), y.data_ptr(), rows, K, stream())
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("rows,K", [(1, 256), (3, 768), (64, 4096), (7, 6912)])
+def test_kquant_dequant_bit_exact(lib, orc, fmt, rows, K):
+    say(f"dequant {fmt} {rows}x{K}")
+    w = synth.kquant(fmt, rows, K, synth.seed_for(6, rows % 16))
+    d = dev(w.raw)
+    out = torch.empty(rows * K, dtype=torch.float32, device="cuda")
+    lib.call(f"zt_dequant_{fmt.replace('_', '')}_f32", d.data_ptr(), out.data_ptr(), rows, K, stream())
+    torch.cuda.synchronize()
+    want = orc.kq_dequant(fmt, w.raw, rows * K)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED)
+def test_kquant_gemv_matches_oracle(lib, orc, fmt, rows, K):
+    say(f"gemv {fmt} {rows}x{K}")
+    w = synth.kquant(fmt, rows, K, synth.seed_for(6, K % 16))
+    x = synth.x_f32(K, synth.seed_for(6, K % 16))
+    d = dev(w.raw)
+    y = kq_gemv(lib, fmt, d.data_ptr(), x, rows, K)
+    ref = orc.gemm_f32_kq_nt(fmt, x, w.raw, 1, rows, K, threads=orc.nthreads())
+    err = rel_err(y, ref)
+    say(f"  rel err {err:.2e}")
+    assert err <= TOL
+
+
+def test_q6k_gemv_on_a_2_byte_aligned_base(lib, orc):
+    # Q6_K super-blocks are 210 bytes: a weight slice can start at any even
+    # address, which the kernel's aligned-dword reads must handle.
+    rows, K = 33, 2560
+    w = synth.kquant("q6_k", rows, K, 77)
+    x = synth.x_f32(K, 77)
+    d = dev(w.raw, pad=2)
+    y = kq_gemv(lib, "q6_k", d.data_ptr() + 2, x, rows, K)
+    assert rel_err(y, orc.gemm_f32_kq_nt("q6_k", x, w.raw, 1, rows, K)) <= TOL
+    out = torch.empty(rows * K, dtype=torch.float32, device="cuda")
+    lib.call("zt_dequant_q6k_f32", d.data_ptr() + 2, out.data_ptr(), rows, K, stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.kq_dequant("q6_k", w.raw, rows * K).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", KQ)
+def test_kquant_zero_superblocks_give_zero(lib, fmt):
+    nbytes = {"q4_k": 144, "q5_k": 176, "q6_k": 210}[fmt]
+    d = dev(np.zeros(8 * 2 * nbytes, np.uint8))
+    y = kq_gemv(lib, fmt, d.data_ptr(), synth.x_f32(512, 3), 8, 512)
+    assert np.all(y == 0)
+
+
+@pytest.mark.parametrize("fmt", KQ)
+def test_kquant_invalid_arguments_rejected(lib, fmt):
+    name = f"zt_gemv_{fmt.replace('_', '')}_f32"
+    fn = getattr(lib, name)
+    w = dev(np.zeros(4096, np.uint8))
+    x = devf(np.zeros(512, np.float32))
+    y = torch.empty(8, dtype=torch.float32, device="cuda")
+    assert fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), 8, 300, stream()) == _lib.HIP_ERROR_INVALID_VALUE  # K % 256
+    assert fn(0, x.data_ptr(), y.data_ptr(), 8, 256, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+    assert fn(w.data_ptr(), x.data_ptr() + 4, y.data_ptr(), 8, 256, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+    assert fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), 0, 256, stream()) == 0
+    assert fn(w.data_ptr(), x.data_ptr(), y.data_ptr(), -1, 256, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+    deq = getattr(lib, f"zt_dequant_{fmt.replace('_', '')}_f32")
+    assert deq(w.data_ptr(), y.data_ptr(), 1, 100, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+
+
+# ------------------------------------------------------------------ Q5_0
+
+
+def q5_0_dev(lib, w):
+    nblk = w.rows * w.K // 32
+    host = np.empty(lib.zt_q5_0_gpu_bytes(nblk), np.uint8)
+    lib.zt_q5_0_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+    return dev(host), lib.zt_q5_0_gpu_qh_offset(nblk), lib.zt_q5_0_gpu_qs_offset(nblk)
+
+
+@pytest.mark.parametrize("rows,K", [(1, 32), (3, 96), (64, 4096)])
+def test_q5_0_dequant_bit_exact(lib, orc, rows, K):
+    w = synth.kquant("q5_0", rows, K, synth.seed_for(7, rows % 16))
+    d = dev(w.raw)
+    out = torch.empty(rows * K, dtype=torch.float32, device="cuda")
+    lib.call("zt_dequant_q5_0_f32", d.data_ptr(), out.data_ptr(), rows, K, stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.q5_0_dequant(w.raw, rows * K).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,K", LLAMA8B + [(1, 32), (3, 96), (17, 4128), (65, 2080)])
+def test_q5_0_gemv_matches_oracle(lib, orc, rows, K):
+    say(f"gemv q5_0 {rows}x{K}")
+    w = synth.kquant("q5_0", rows, K, synth.seed_for(7, K % 16))
+    x = synth.x_f32(K, synth.seed_for(7, K % 16))
+    d, qh, qs = q5_0_dev(lib, w)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = devf(x)
+    lib.call("zt_gemv_q5_0_f32", d.data_ptr(), xd.data_ptr(), y.data_ptr(), rows, K, qh, qs, stream())
+    torch.cuda.synchronize()
+    ref = orc.gemm_f32_q5_0_nt(x, w.raw, 1, rows, K)
+    err = rel_err(y.cpu().numpy(), ref)
+    say(f"  rel err {err:.2e}")
+    assert err <= TOL
+
+
+def test_q5_0_invalid_arguments_rejected(lib):
+    w = dev(np.zeros(4096, np.uint8))
+    x = devf(np.zeros(64, np.float32))
+    y = torch.empty(4, dtype=torch.float32, device="cuda")
+    f = lib.zt_gemv_q5_0_f32
+    assert f(w.data_ptr(), x.data_ptr(), y.data_ptr(), 4, 40, 16, 32, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+    assert f(w.data_ptr(), x.data_ptr(), y.data_ptr(), 4, 64, 16, 40, stream()) == _lib.HIP_ERROR_INVALID_VALUE
+    assert f(w.data_ptr(), x.data_ptr(), y.data_ptr(), 0, 64, 16, 32, stream()) == 0
+
+
+# ------------------------------------------------------------------ engine
+
+
+@pytest.mark.parametrize("n", [1, 3])
+def test_engine_q4k_both_operand_sides(orc, n):
+    from ztensor_amd.engine import ROCmEngine
+
+    eng = ROCmEngine()
+    rows, K = 96, 1024
+    w = synth.kquant("q4_k", rows, K, 88)
+    x = synth.x_f32(K * n, 88).reshape(K, n)
+    W = orc.kq_dequant("q4_k", w.raw, rows * K).reshape(rows, K).astype(np.float64)
+    # A side: W [rows, K] @ x [K, n]
+    a = Tensor((rows, K), Q4KStorage.from_raw(w.raw, rows * K))
+    got = eng.matmul(a, devf(x)).cpu().numpy()
+    assert rel_err(got, W @ x.astype(np.float64)) <= TOL
+    # B side: act [n, K] @ W^T (virtually transposed weight, logical [K, rows])
+    b = Tensor((K, rows), Q4KStorage.from_raw(w.raw, rows * K))
+    got = eng.matmul(devf(x.T.copy()), b).cpu().numpy()
+    assert rel_err(got, x.T.astype(np.float64) @ W.T) <= TOL
+
+
+def test_engine_q6k_and_q5_0(orc):
+    from ztensor_amd.engine import ROCmEngine
+
+    eng = ROCmEngine()
+    rows, K = 40, 768
+    w6 = synth.kquant("q6_k", rows, K, 89)
+    x = synth.x_f32(K, 89)
+    got = eng.matmul(Tensor((rows, K), Q6KStorage.from_raw(w6.raw, rows * K)), devf(x)).cpu().numpy()
+    assert rel_err(got.reshape(-1), orc.gemm_f32_kq_nt("q6_k", x, w6.raw, 1, rows, K)) <= TOL
+    w5 = synth.kquant("q5_0", rows, K, 90)
+    x2 = synth.x_f32(2 * K, 90).reshape(K, 2)
+    got = eng.matmul(Tensor((rows, K), Q5_0Storage.from_raw(w5.raw, rows * K)), devf(x2)).cpu().numpy()
+    W5 = orc.q5_0_dequant(w5.raw, rows * K).reshape(rows, K).astype(np.float64)
+    assert rel_err(got, W5 @ x2.astype(np.float64)) <= TOL

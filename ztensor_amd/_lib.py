@@ -48,6 +48,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
     "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),
     "zt_ternary_repack_rows": (None, [P, L, L, P]),
+    "zt_gemv_q4k_f32": (I, [P, P, P, I, I, P]),
+    "zt_gemv_q5k_f32": (I, [P, P, P, I, I, P]),
+    "zt_gemv_q6k_f32": (I, [P, P, P, I, I, P]),
+    "zt_gemv_q5_0_f32": (I, [P, P, P, I, I, I, I, P]),
+    "zt_dequant_q4k_f32": (I, [P, P, I, I, P]),
+    "zt_dequant_q5k_f32": (I, [P, P, I, I, P]),
+    "zt_dequant_q6k_f32": (I, [P, P, I, I, P]),
+    "zt_dequant_q5_0_f32": (I, [P, P, I, I, P]),
+    "zt_q5_0_gpu_qh_offset": (L, [L]),
+    "zt_q5_0_gpu_qs_offset": (L, [L]),
+    "zt_q5_0_gpu_bytes": (L, [L]),
+    "zt_q5_0_raw_to_gpu": (None, [P, L, P]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1

@@ -64,4 +64,23 @@ void zt_ternary_repack_rows(const void* raw, long M, long K, void* out) {
         }
 }
 
+// tensor/quantized_q5_0.go:118-165 RawBytesGPU and its offsets: fp16 scales,
+// zero padding to 16, the uint32 qh words, padding to 16, then every
+// block's 16 nibble bytes.
+long zt_q5_0_gpu_qh_offset(long nblk) { return (nblk * 2 + 15) & ~15L; }
+long zt_q5_0_gpu_qs_offset(long nblk) { return zt_q5_0_gpu_qh_offset(nblk) + ((nblk * 4 + 15) & ~15L); }
+long zt_q5_0_gpu_bytes(long nblk) { return zt_q5_0_gpu_qs_offset(nblk) + nblk * 16; }
+
+void zt_q5_0_raw_to_gpu(const void* raw, long nblk, void* out) {
+    const unsigned char* src = static_cast<const unsigned char*>(raw);
+    unsigned char* dst = static_cast<unsigned char*>(out);
+    const long qh = zt_q5_0_gpu_qh_offset(nblk), qs = zt_q5_0_gpu_qs_offset(nblk);
+    memset(dst, 0, (size_t)qs);
+    for (long i = 0; i < nblk; i++) {
+        memcpy(dst + 2 * i, src + 22 * i, 2);
+        memcpy(dst + qh + 4 * i, src + 22 * i + 2, 4);
+        memcpy(dst + qs + 16 * i, src + 22 * i + 6, 16);
+    }
+}
+
 }  // extern "C"

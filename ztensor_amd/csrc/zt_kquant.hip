@@ -1,0 +1,447 @@
+// K-quant (Q4_K, Q5_K, Q6_K) and Q5_0 batch-1 GEMV and dequantization for gfx950.
+//
+// Formats (value v of a 256-value super-block; each stored in the raw
+// contiguous layout RawBytes() holds and the reference uploads as is,
+// compute/gpu_engine.go:817-874):
+//   Q4_K 144 B [fp16 d][fp16 dmin][12 B 6-bit scales/mins][128 B nibbles]:
+//        group g = v/64 reads bytes 32g..32g+31; low nibble of byte l is
+//        v = 64g+l (sub-block 2g), high nibble v = 64g+32+l (sub-block 2g+1);
+//        w = (d*sc)*q - dmin*mn            (tensor/quantized_kquant.go:34-79)
+//   Q5_K 176 B: Q4_K plus qh[32]: bit 2g / 2g+1 of qh[l] is the fifth bit of
+//        the low / high nibble value                    (:509-549)
+//   Q6_K 210 B [128 ql][64 qh][16 int8 scales][fp16 d]: value v uses scale
+//        v/16; w = (d*sc)*(q-32)                        (:355-382)
+//   Q5_0 22 B blocks of 32 [fp16 d][uint32 qh][16 B qs], uploaded in the
+//        separated layout [d, nblk*2][pad 16][qh, nblk*4][pad 16][qs, nblk*16]
+//        (tensor/quantized_q5_0.go:118-165); w = d*((nib | qh bit << 4) - 16).
+//
+// Batch-1 GEMV design (HBM-bound, every weight byte read once):
+//  * K-quants: 16 lanes per super-block, each taking 8 bytes of the
+//    low-bit array (16 weights), so a wave covers 4 super-blocks of R rows
+//    per step and the waves of a workgroup split K;
+//  * the nibbles (with the fifth / sixth bit OR-ed in by masks) are read as
+//    fp16 subnormals q*2^-24 (low nibble) or q*2^-20 (high nibble, in place)
+//    and v_fma_mix_f32 multiplies them into fp32 accumulators against
+//    activations pre-scaled by 2^24 / 2^20, one chain per sub-block;
+//  * the per-sub-block scale and min enter once per chain:
+//    sum_v w_v x_v = d*(sc0*S0 + sc1*S1) - dmin*(mn0*X0 + mn1*X1)
+//    (S = sum q x, X = sum x over the lane's values of that sub-block);
+//  * Q6_K's 210-byte blocks are only 2-byte aligned: fields are read as
+//    aligned dwords and joined with v_alignbit;
+//  * Q5_0 uses the quad mapping of the Q4_0 kernel (four lanes per 32-value
+//    block, one dword of nibbles each) with the qh bits spread into the
+//    nibble bytes.
+// The reference's CPU GEMVs apply each weight's dequantized value to x and
+// sum in element order; the factored sums here reorder that fp32 sum, so
+// GEMV results agree within rounding (the dequantizers are bit-exact).
+#include "zt_mfma.h"
+
+namespace zt {
+
+// 8 bytes at a 2-byte aligned address, from three aligned dwords.
+__device__ __forceinline__ uint2 ld_u64_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+    const uint32_t s = (uint32_t)(a & 3) * 8u;
+    const uint32_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1);
+    // the third dword only when misaligned: an aligned field ends at the
+    // second, and reading further could pass the end of the last block
+    const uint32_t w2 = s ? __builtin_nontemporal_load(q + 2) : 0u;
+    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, s), __builtin_amdgcn_alignbit(w2, w1, s));
+}
+
+// Sum of the 8 masked fp16 subnormals of two dwords (lo: values 0..3 of the
+// first dword and 0..3 of the second) against pre-scaled activations.
+// m0/m2 hold the values of bytes (0,2)/(1,3) of dword j in their two halves.
+__device__ __forceinline__ float chain8(const uint32_t (&m)[2][2], const float (&xp)[8], float acc) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const half2v a = as_half2(m[j][0]), b = as_half2(m[j][1]);
+        acc = __builtin_fmaf((float)a.x, xp[4 * j + 0], acc);
+        acc = __builtin_fmaf((float)b.x, xp[4 * j + 1], acc);
+        acc = __builtin_fmaf((float)a.y, xp[4 * j + 2], acc);
+        acc = __builtin_fmaf((float)b.y, xp[4 * j + 3], acc);
+    }
+    return acc;
+}
+
+// x pieces of one lane: 8 values starting at lo and 8 at hi (16-byte aligned).
+struct KqX {
+    float lo[8], hi[8];  // pre-scaled by 2^24 / 2^20
+    float slo, shi;      // plain sums
+};
+
+__device__ __forceinline__ void kq_load_x(const float* __restrict__ x, long lo, long hi, bool valid, KqX& o) {
+    float a[8], b[8];
+    if (valid) {
+        const float4 a0 = *reinterpret_cast<const float4*>(x + lo), a1 = *reinterpret_cast<const float4*>(x + lo + 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(x + hi), b1 = *reinterpret_cast<const float4*>(x + hi + 4);
+        a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+        b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[i] = b[i] = 0.0f;
+    }
+    o.slo = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+    o.shi = ((b[0] + b[1]) + (b[2] + b[3])) + ((b[4] + b[5]) + (b[6] + b[7]));
+    // chain8 order: dword j -> bytes 0, 1, 2, 3 = values 4j .. 4j+3 as (a.x, b.x, a.y, b.y)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        o.lo[i] = a[i] * 16777216.0f;
+        o.hi[i] = b[i] * 1048576.0f;
+    }
+}
+
+// Scale and min pairs (sub-blocks 2g, 2g+1) of a Q4_K/Q5_K header, as two
+// bytes each (byte 0 = sub-block 2g).  hi_grp = g >= 2, sh = 16*(g&1).
+__device__ __forceinline__ void kq_sc_mn(const uint4 h, bool hi_grp, uint32_t sh, uint32_t& scp, uint32_t& mnp) {
+    const uint32_t A = h.y >> sh, B = h.z >> sh, C = h.w >> sh;
+    const uint32_t s_lo = A & 0x3F3Fu, m_lo = B & 0x3F3Fu;
+    const uint32_t s_hi = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);
+    const uint32_t m_hi = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
+    scp = hi_grp ? s_hi : s_lo;
+    mnp = hi_grp ? m_hi : m_lo;
+}
+
+// ------------------------------------------------------------ K-quant GEMV
+
+template <int FMT>
+struct KqFmt;
+template <>
+struct KqFmt<4> { static constexpr int bytes = 144; };
+template <>
+struct KqFmt<5> { static constexpr int bytes = 176; };
+template <>
+struct KqFmt<6> { static constexpr int bytes = 210; };
+
+template <int FMT, int R>
+__global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                      float* __restrict__ y, int rows, int nsb) {
+    constexpr int BB = KqFmt<FMT>::bytes;
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int slot = lane >> 4, t = lane & 15;
+    const int row0 = blockIdx.x * R;
+    // Lane roles.  Q4_K/Q5_K: g = t/4 (group), u = t%4 -> bytes 32g+8u of the
+    // nibbles: values 64g+8u+i (sub-block 2g) and 64g+32+8u+i (2g+1).
+    // Q6_K: h = t/8 (half), u = t%8 -> ql bytes 64h+8u: values
+    // vlo = 128h + 32*(u>=4) + 8*(u%4) + i (scale vlo/16) and vlo+64.
+    const int g = t >> 2, u4 = t & 3;
+    const int h6 = t >> 3, u8 = t & 7;
+    const bool hi_grp = g >= 2;
+    const uint32_t sh = 16u * (uint32_t)(g & 1);
+    const int vlo = FMT == 6 ? 128 * h6 + 32 * (u8 >= 4) + 8 * (u8 & 3) : 64 * g + 8 * u4;
+    const int vhi = FMT == 6 ? vlo + 64 : vlo + 32;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * nsb;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    for (int base = wave * 4; base < nsb; base += nwaves * 4) {
+        const int sb = base + slot;
+        const bool valid = sb < nsb;
+        const int sbc = valid ? sb : nsb - 1;
+        KqX xs;
+        kq_load_x(x, (long)sbc * 256 + vlo, (long)sbc * 256 + vhi, valid, xs);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t* blk = W + (rbase[r] + sbc) * BB;
+            uint32_t m[2][2][2];  // [lo/hi][dword][pair]
+            if constexpr (FMT == 4 || FMT == 5) {
+                const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+                const uint2 q = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + 8 * u4);
+                uint2 qh = make_uint2(0, 0);
+                if constexpr (FMT == 5) qh = *reinterpret_cast<const uint2*>(blk + 144 + 8 * u4);
+                const uint32_t qd[2] = {q.x, q.y}, hd[2] = {qh.x, qh.y};
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t d = qd[j], d8 = d >> 8;
+                    uint32_t l0 = d & 0x000F000Fu, l2 = d8 & 0x000F000Fu, h0 = d & 0x00F000F0u, h2 = d8 & 0x00F000F0u;
+                    if constexpr (FMT == 5) {
+                        const uint32_t L = hd[j] >> (2 * g), H = hd[j] >> (2 * g + 1);
+                        l0 |= (L << 4) & 0x00100010u;  // byte 0 / 2 fifth bit -> bit 4 / 20
+                        l2 |= (L >> 4) & 0x00100010u;  // byte 1 / 3 -> bit 4 / 20
+                        h0 |= (H << 8) & 0x01000100u;  // (q<<4) fifth bit -> bit 8 / 24
+                        h2 |= H & 0x01000100u;
+                    }
+                    m[0][j][0] = l0; m[0][j][1] = l2; m[1][j][0] = h0; m[1][j][1] = h2;
+                }
+                const float S0 = chain8(m[0], xs.lo, 0.0f);
+                const float S1 = chain8(m[1], xs.hi, 0.0f);
+                uint32_t scp, mnp;
+                kq_sc_mn(hdr, hi_grp, sh, scp, mnp);
+                const float sc0 = (float)(scp & 0xFFu), sc1 = (float)((scp >> 8) & 0xFFu);  // v_cvt_f32_ubyte0/1
+                const float mn0 = (float)(mnp & 0xFFu), mn1 = (float)((mnp >> 8) & 0xFFu);
+                const float tq = __builtin_fmaf(sc1, S1, sc0 * S0);
+                const float tm = __builtin_fmaf(mn1, xs.shi, mn0 * xs.slo);
+                const half2v dd = as_half2(hdr.x);  // (d, dmin)
+                acc[r] = __builtin_fmaf((float)dd.x, tq, acc[r]);
+                acc[r] = __builtin_fmaf(-(float)dd.y, tm, acc[r]);
+            } else {
+                const uint2 ql = ld_u64_a2(blk + 64 * h6 + 8 * u8);
+                const uint2 qh = ld_u64_a2(blk + 128 + 32 * h6 + 8 * (u8 & 3));
+                const uint2 scw = ld_u64_a2(blk + 192 + 8 * h6);   // scales 8h .. 8h+7
+                const uint32_t dw = *reinterpret_cast<const uint16_t*>(blk + 208);
+                const uint32_t qsh = (u8 >= 4) ? 2u : 0u;           // lo uses qh bits 0-1 (2-3), hi bits 4-5 (6-7)
+                const uint32_t qd[2] = {ql.x, ql.y}, hd[2] = {qh.x, qh.y};
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t d = qd[j], d8 = d >> 8;
+                    const uint32_t L = hd[j] >> qsh, H = hd[j] >> (qsh + 4);
+                    m[0][j][0] = (d & 0x000F000Fu) | ((L << 4) & 0x00300030u);
+                    m[0][j][1] = (d8 & 0x000F000Fu) | ((L >> 4) & 0x00300030u);
+                    m[1][j][0] = (d & 0x00F000F0u) | ((H << 8) & 0x03000300u);
+                    m[1][j][1] = (d8 & 0x00F000F0u) | (H & 0x03000300u);
+                }
+                const float S0 = chain8(m[0], xs.lo, -32.0f * xs.slo);
+                const float S1 = chain8(m[1], xs.hi, -32.0f * xs.shi);
+                // scale index of vlo is 8h + 2*(u>=4) + (u%4)/2; of vhi that + 4.
+                const int si = 2 * (u8 >= 4) + ((u8 & 3) >> 1);
+                const int sc0 = __builtin_amdgcn_sbfe((int)scw.x, 8 * si, 8);
+                const int sc1 = __builtin_amdgcn_sbfe((int)scw.y, 8 * si, 8);
+                const float tq = __builtin_fmaf((float)sc1, S1, (float)sc0 * S0);
+                const half2v dd = as_half2(dw);
+                acc[r] = __builtin_fmaf((float)dd.x, tq, acc[r]);
+            }
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int FMT>
+static void launch_kq(int R, dim3 grid, dim3 block, hipStream_t st, const uint8_t* W, const float* x, float* y,
+                      int rows, int nsb) {
+    switch (R) {
+        case 8: kq_gemv_kernel<FMT, 8><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 4: kq_gemv_kernel<FMT, 4><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 2: kq_gemv_kernel<FMT, 2><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        default: kq_gemv_kernel<FMT, 1><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+    }
+}
+
+template <int FMT>
+static int gemv_kq(const void* W, const float* x, float* y, int M, int K, hipStream_t st) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) {
+        if (M > 0 && K == 0 && y) {  // empty sum
+            mfma_zero(y, M, st);
+            return (int)hipGetLastError();
+        }
+        return (int)hipSuccess;
+    }
+    if (W == nullptr || x == nullptr || y == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)x & 15) || ((uintptr_t)W & (FMT == 6 ? 1 : 15))) return (int)hipErrorInvalidValue;
+    const int nsb = K / 256;
+    const int nwaves = min(8, ceil_div(nsb, 4));
+    const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
+    launch_kq<FMT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, static_cast<const uint8_t*>(W), x, y, M, nsb);
+    return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------ Q5_0 GEMV
+
+// Spreads bits 0..3 of v into bit 0 of bytes 0..3 (distinct partial
+// products of v * 0x00204081 land on distinct bits, so nothing carries).
+__device__ __forceinline__ uint32_t spread4(uint32_t v) { return ((v & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+template <int R>
+__global__ void __launch_bounds__(512) q5_0_gemv_kernel(const uint16_t* __restrict__ scales,
+                                                        const uint32_t* __restrict__ qh,
+                                                        const uint32_t* __restrict__ qs, const float* __restrict__ x,
+                                                        float* __restrict__ y, int rows, int kb) {
+    __shared__ float red[8 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    long rbase[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int b = wave * 16 + (lane >> 2); b < kb; b += nwaves * 16) {
+        uint32_t w[R], hb[R];
+        uint16_t s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = __builtin_nontemporal_load(&qs[(rbase[r] + b) * 4 + q]);
+            hb[r] = qh[rbase[r] + b];
+            s[r] = scales[rbase[r] + b];
+        }
+        // lane q: values 4q..4q+3 (low nibbles, qh bits 4q..) and 16+4q.. (high nibbles, qh bits 16+4q..)
+        const float* p = x + (long)b * 32;
+        const float4 a = *reinterpret_cast<const float4*>(p + 4 * q);
+        const float4 c = *reinterpret_cast<const float4*>(p + 16 + 4 * q);
+        const float xsum = ((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w));
+        const float xl[4] = {a.x * 16777216.0f, a.y * 16777216.0f, a.z * 16777216.0f, a.w * 16777216.0f};
+        const float xh[4] = {c.x * 1048576.0f, c.y * 1048576.0f, c.z * 1048576.0f, c.w * 1048576.0f};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[r], d8 = d >> 8;
+            const uint32_t el = spread4(hb[r] >> (4 * q)), eh = spread4(hb[r] >> (16 + 4 * q));
+            const half2v m0 = as_half2((d & 0x000F000Fu) | ((el << 4) & 0x00100010u));
+            const half2v m2 = as_half2((d8 & 0x000F000Fu) | ((el >> 4) & 0x00100010u));
+            const half2v m1 = as_half2((d & 0x00F000F0u) | ((eh << 8) & 0x01000100u));
+            const half2v m3 = as_half2((d8 & 0x00F000F0u) | (eh & 0x01000100u));
+            float v = __builtin_fmaf((float)m0.x, xl[0], -16.0f * xsum);
+            v = __builtin_fmaf((float)m1.x, xh[0], v);
+            v = __builtin_fmaf((float)m2.x, xl[1], v);
+            v = __builtin_fmaf((float)m3.x, xh[1], v);
+            v = __builtin_fmaf((float)m0.y, xl[2], v);
+            v = __builtin_fmaf((float)m1.y, xh[2], v);
+            v = __builtin_fmaf((float)m2.y, xl[3], v);
+            v = __builtin_fmaf((float)m3.y, xh[3], v);
+            acc[r] = __builtin_fmaf(h2f(s[r]), v, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+static int gemv_q5_0(const void* W, const float* x, float* y, int M, int K, int qh_off, int qs_off, hipStream_t st) {
+    if (M < 0 || K < 0 || K % 32 != 0 || qh_off < 0 || qs_off < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) {
+        if (M > 0 && K == 0 && y) {
+            mfma_zero(y, M, st);
+            return (int)hipGetLastError();
+        }
+        return (int)hipSuccess;
+    }
+    if (W == nullptr || x == nullptr || y == nullptr) return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(W);
+    if (((uintptr_t)base & 3) || ((uintptr_t)(base + qh_off) & 3) || ((uintptr_t)(base + qs_off) & 15) ||
+        ((uintptr_t)x & 15))
+        return (int)hipErrorInvalidValue;
+    const int kb = K / 32;
+    const int nwaves = min(8, ceil_div(kb, 16));
+    const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(base + qh_off);
+    const uint32_t* qs = reinterpret_cast<const uint32_t*>(base + qs_off);
+    const dim3 grid(ceil_div(M, R)), block(nwaves * kWave);
+    switch (R) {
+        case 8: q5_0_gemv_kernel<8><<<grid, block, 0, st>>>(sc, qh, qs, x, y, M, kb); break;
+        case 4: q5_0_gemv_kernel<4><<<grid, block, 0, st>>>(sc, qh, qs, x, y, M, kb); break;
+        case 2: q5_0_gemv_kernel<2><<<grid, block, 0, st>>>(sc, qh, qs, x, y, M, kb); break;
+        default: q5_0_gemv_kernel<1><<<grid, block, 0, st>>>(sc, qh, qs, x, y, M, kb); break;
+    }
+    return (int)hipGetLastError();
+}
+
+// ------------------------------------------------------------ dequantizers
+
+// One thread per 32-value piece of a super-block (piece p = 0..7: values
+// 32p .. 32p+31), each value computed with the reference's operations and
+// rounding order, so the output is bit-identical to the CPU dequantizers.
+template <int FMT>
+__global__ void kq_dequant_kernel(const uint8_t* __restrict__ W, float* __restrict__ out, long npieces) {
+    constexpr int BB = KqFmt<FMT>::bytes;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npieces) return;
+    const long sbi = i >> 3;
+    const int p = (int)(i & 7);
+    const uint8_t* b = W + sbi * BB;
+    float* o = out + i * 32;
+    if constexpr (FMT == 4 || FMT == 5) {
+        // piece p is sub-block p: group g = p/2, low nibbles (p even) or high (p odd)
+        const int g = p >> 1, hi = p & 1;
+        const float d = h2f((uint16_t)(b[0] | (b[1] << 8))), dmin = h2f((uint16_t)(b[2] | (b[3] << 8)));
+        const uint8_t* sc = b + 4;
+        uint32_t scale, mn;
+        if (p < 4) {
+            scale = sc[p] & 63;
+            mn = sc[4 + p] & 63;
+        } else {
+            scale = (sc[8 + p - 4] & 0xF) | ((sc[p - 4] >> 6) << 4);
+            mn = (sc[8 + p - 4] >> 4) | ((sc[4 + p - 4] >> 6) << 4);
+        }
+        const float s = d * (float)scale, m = dmin * (float)mn;
+#pragma unroll 4
+        for (int l = 0; l < 32; l++) {
+            const uint8_t v = b[16 + 32 * g + l];
+            uint32_t qv = hi ? (v >> 4) : (v & 0xF);
+            if constexpr (FMT == 5) qv |= ((b[144 + l] >> (2 * g + hi)) & 1) << 4;
+            o[l] = __fsub_rn(__fmul_rn(s, (float)qv), m);
+        }
+    } else {
+        // piece p = half h = p/4, quarter j = p%4 (values 128h + 32j + l)
+        const int h = p >> 2, j = p & 3;
+        const float d = h2f((uint16_t)(b[208] | (b[209] << 8)));
+        const uint8_t* ql = b + 64 * h + (j & 1) * 32;
+        const uint8_t* qh = b + 128 + 32 * h;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + 8 * h);
+#pragma unroll 4
+        for (int l = 0; l < 32; l++) {
+            const uint32_t nib = (j < 2) ? (ql[l] & 0xF) : (ql[l] >> 4);
+            const uint32_t top = (qh[l] >> (2 * j)) & 3;
+            const int q = (int)(nib | (top << 4)) - 32;
+            o[l] = __fmul_rn(__fmul_rn(d, (float)sc[l / 16 + 2 * j]), (float)q);
+        }
+    }
+}
+
+template <int FMT>
+static int dequant_kq(const void* W, float* out, int rows, int K, hipStream_t st) {
+    if (rows < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (rows == 0 || K == 0) return (int)hipSuccess;
+    if (W == nullptr || out == nullptr) return (int)hipErrorInvalidValue;
+    const long npieces = (long)rows * (K / 256) * 8;
+    kq_dequant_kernel<FMT><<<ceil_div(npieces, 256), 256, 0, st>>>(static_cast<const uint8_t*>(W), out, npieces);
+    return (int)hipGetLastError();
+}
+
+// Q5_0 over the raw 22-byte blocks (the layout dequant_q5_0_f32 reads,
+// internal/cuda/kernels/dequant_q5_0.cu:18-67): one thread per block.
+__global__ void q5_0_dequant_kernel(const uint8_t* __restrict__ raw, float* __restrict__ out, long nblk) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint8_t* b = raw + i * 22;
+    const float d = h2f((uint16_t)(b[0] | (b[1] << 8)));
+    const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    float* o = out + i * 32;
+#pragma unroll 4
+    for (int j = 0; j < 16; j++) {
+        const uint8_t v = b[6 + j];
+        const int x0 = (int)((v & 0xF) | (((qh >> j) & 1) << 4)) - 16;
+        const int x1 = (int)((v >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+        o[j] = __fmul_rn(d, (float)x0);
+        o[j + 16] = __fmul_rn(d, (float)x1);
+    }
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+ZT_EXPORT int zt_gemv_q4k_f32(const void* W, const float* x, float* y, int M, int K, hipStream_t stream) {
+    return gemv_kq<4>(W, x, y, M, K, stream);
+}
+ZT_EXPORT int zt_gemv_q5k_f32(const void* W, const float* x, float* y, int M, int K, hipStream_t stream) {
+    return gemv_kq<5>(W, x, y, M, K, stream);
+}
+ZT_EXPORT int zt_gemv_q6k_f32(const void* W, const float* x, float* y, int M, int K, hipStream_t stream) {
+    return gemv_kq<6>(W, x, y, M, K, stream);
+}
+ZT_EXPORT int zt_gemv_q5_0_f32(const void* W, const float* x, float* y, int M, int K, int qh_offset, int qs_offset,
+                               hipStream_t stream) {
+    return gemv_q5_0(W, x, y, M, K, qh_offset, qs_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_q4k_f32(const void* W, float* out, int rows, int K, hipStream_t stream) {
+    return dequant_kq<4>(W, out, rows, K, stream);
+}
+ZT_EXPORT int zt_dequant_q5k_f32(const void* W, float* out, int rows, int K, hipStream_t stream) {
+    return dequant_kq<5>(W, out, rows, K, stream);
+}
+ZT_EXPORT int zt_dequant_q6k_f32(const void* W, float* out, int rows, int K, hipStream_t stream) {
+    return dequant_kq<6>(W, out, rows, K, stream);
+}
+ZT_EXPORT int zt_dequant_q5_0_f32(const void* W, float* out, int rows, int K, hipStream_t stream) {
+    if (rows < 0 || K < 0 || K % 32 != 0) return (int)hipErrorInvalidValue;
+    if (rows == 0 || K == 0) return (int)hipSuccess;
+    if (W == nullptr || out == nullptr) return (int)hipErrorInvalidValue;
+    const long nblk = (long)rows * (K / 32);
+    q5_0_dequant_kernel<<<ceil_div(nblk, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(W), out, nblk);
+    return (int)hipGetLastError();
+}

@@ -31,6 +31,9 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 typedef __attribute__((address_space(3))) char lds_char;
 
+// A dword viewed as two fp16 halves (x = bits 0-15).
+__device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
 constexpr int kMfmaRows = 32;                         // rows per workgroup (two 16-row tiles)
 constexpr int kMfmaTiles = kMfmaRows / 16;
 constexpr int kMfmaWaves = 8;                         // waves per workgroup

@@ -108,8 +108,6 @@ __device__ __forceinline__ float block_dot(const uint4 w, const float (&xv)[32],
     }
 }
 
-__device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
-
 // The 8 activations lane q of a quad needs for block b: Q4_0 elements
 // 4q..4q+3 and 16+4q..16+4q+3 (GGML split order), IQ4_NL elements 8q..8q+7.
 template <Fmt F, class XT>

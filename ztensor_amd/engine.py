@@ -32,11 +32,18 @@ from .storage import (
     GPTQStorage,
     GPUBuffer,
     IQ4NLStorage,
+    Q4KStorage,
     Q4Storage,
+    Q5_0Storage,
+    Q5KStorage,
+    Q6KStorage,
     Q8Storage,
     Tensor,
     TernaryStorage,
 )
+
+_KQ_GEMV = {Q4KStorage: "zt_gemv_q4k_f32", Q5KStorage: "zt_gemv_q5k_f32", Q6KStorage: "zt_gemv_q6k_f32"}
+_KQ_DEQUANT = {Q4KStorage: "zt_dequant_q4k_f32", Q5KStorage: "zt_dequant_q5k_f32", Q6KStorage: "zt_dequant_q6k_f32"}
 
 
 def _p(t: torch.Tensor | None) -> int:
@@ -79,6 +86,30 @@ class ROCmEngine:
                        group_size: int) -> None:
         self.lib.call("zt_gemm_w4a16_f32", w, scales, zeros, b, c, m, k, n, group_size, self._s)
 
+    def gemv_q4k_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
+        self.lib.call("zt_gemv_q4k_f32", w, x, y, m, k, self._s)
+
+    def gemv_q5k_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
+        self.lib.call("zt_gemv_q5k_f32", w, x, y, m, k, self._s)
+
+    def gemv_q6k_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
+        self.lib.call("zt_gemv_q6k_f32", w, x, y, m, k, self._s)
+
+    def gemv_q5_0_f32(self, w: int, x: int, y: int, m: int, k: int, qh_offset: int, qs_offset: int) -> None:
+        self.lib.call("zt_gemv_q5_0_f32", w, x, y, m, k, qh_offset, qs_offset, self._s)
+
+    def dequant_q4k_f32(self, src: int, dst: int, rows: int, k: int) -> None:
+        self.lib.call("zt_dequant_q4k_f32", src, dst, rows, k, self._s)
+
+    def dequant_q5k_f32(self, src: int, dst: int, rows: int, k: int) -> None:
+        self.lib.call("zt_dequant_q5k_f32", src, dst, rows, k, self._s)
+
+    def dequant_q6k_f32(self, src: int, dst: int, rows: int, k: int) -> None:
+        self.lib.call("zt_dequant_q6k_f32", src, dst, rows, k, self._s)
+
+    def dequant_q5_0_f32(self, src: int, dst: int, rows: int, k: int) -> None:
+        self.lib.call("zt_dequant_q5_0_f32", src, dst, rows, k, self._s)
+
     def ternary_gemv_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
         self.lib.call("zt_ternary_gemv_f32", w, x, y, m, k, self._s)
 
@@ -102,6 +133,15 @@ class ROCmEngine:
                     buf = s.raw_bytes_gpu()
                     s.set_gpu_ptr(GPUBuffer(self._to_dev(buf), buf.size, self.device.index or 0,
                                             s.gpu_data_offset()))
+                    n += 1
+            elif isinstance(s, (Q4KStorage, Q5KStorage, Q6KStorage)):
+                if s.gpu_ptr() is None:  # raw super-blocks, as compute/gpu_engine.go:817-874
+                    s.set_gpu_ptr(GPUBuffer(self._to_dev(s.raw), s.raw.size, self.device.index or 0))
+                    n += 1
+            elif isinstance(s, Q5_0Storage):
+                if s.gpu_ptr() is None:  # RawBytesGPU, as compute/gpu_engine.go:876-893
+                    buf = s.raw_bytes_gpu()
+                    s.set_gpu_ptr(GPUBuffer(self._to_dev(buf), buf.size, self.device.index or 0))
                     n += 1
             elif isinstance(s, (GPTQStorage, AWQStorage)):
                 if s.gpu_ptr() is None:
@@ -174,6 +214,35 @@ class ROCmEngine:
                 raise TypeError("W4A16 matmul takes fp16 activations")
             self.gemm_w4a16_f32(_p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(x), _p(c), rows, k, n,
                                 s.group_size)
+        elif isinstance(s, (Q4KStorage, Q5KStorage, Q6KStorage, Q5_0Storage)):
+            if x.dtype != torch.float32:
+                raise TypeError(f"{type(s).__name__} matmul takes fp32 activations")
+            q50 = isinstance(s, Q5_0Storage)
+            if n == 1 and k % (32 if q50 else 256) == 0:
+                # fused dequant-GEMV (compute/gpu_engine.go:2224-2238, 2505-2510)
+                if q50:
+                    self.gemv_q5_0_f32(_p(buf.tensor), _p(x), _p(c), rows, k, s.gpu_qh_offset(), s.gpu_qs_offset())
+                else:
+                    self.lib.call(_KQ_GEMV[type(s)], _p(buf.tensor), _p(x), _p(c), rows, k, self._s)
+            else:
+                # batched: dequantize on the device, then a dense fp32 GEMM, the
+                # reference's dequantSgemm (compute/gpu_engine.go:2240-2255);
+                # rocBLAS via torch stands in for its cuBLAS Sgemm
+                if q50:
+                    # the upload holds RawBytesGPU, which the raw-block dequantizer
+                    # does not read: one fused GEMV per activation column
+                    xt = x.reshape(k, n).t().contiguous()
+                    ct = torch.empty((n, rows), dtype=torch.float32, device=self.device)
+                    for j in range(n):
+                        self.gemv_q5_0_f32(_p(buf.tensor), _p(xt[j]), _p(ct[j]), rows, k, s.gpu_qh_offset(),
+                                           s.gpu_qs_offset())
+                    c.copy_(ct.t())
+                    return c
+                if k % 256 != 0:
+                    raise ValueError(f"{type(s).__name__} matmul needs K % 256 == 0")
+                w = torch.empty((rows, k), dtype=torch.float32, device=self.device)
+                self.lib.call(_KQ_DEQUANT[type(s)], _p(buf.tensor), _p(w), rows, k, self._s)
+                torch.matmul(w, x.reshape(k, n), out=c)
         else:
             raise TypeError(f"matmul: {type(s).__name__} is not a quantized weight storage")
         return c

@@ -12,6 +12,10 @@ caller of tensor.Q4Storage & co. finds the same surface:
   AWQStorage     tensor/quantized_awq.go:30-321
   TernaryStorage tensor/ternary_storage.go:7-95
   Float16Storage tensor/fp16_storage.go:14-122
+  Q4KStorage     tensor/quantized_kquant.go:236-339 (MergeQ4KStorage -> merge_q4k_storage)
+  Q5KStorage     tensor/quantized_kquant.go:552-636
+  Q6KStorage     tensor/quantized_kquant.go:385-505 (MergeQ6KStorage -> merge_q6k_storage)
+  Q5_0Storage    tensor/quantized_q5_0.go:47-184 (RawBytesGPU, Q5_0GPUQhOffset/QsOffset)
 
 Dequantization on the host is not offered here on purpose: the product path
 dequantizes on the GPU (zt_dequant_*), and the CPU restatement used to check
@@ -270,6 +274,124 @@ class Float16Storage(_GPUPtrMixin):
     def from_raw(raw: np.ndarray, num_elems: int) -> "Float16Storage":
         """NewFloat16StorageFromRaw (tensor/fp16_storage.go:42-46)."""
         return Float16Storage(np.asarray(raw).view(np.uint16).reshape(-1)[:num_elems].copy(), num_elems)
+
+
+class _KQuantBase(_GPUPtrMixin):
+    """Shared body of the K-quant storages: contiguous super-blocks of 256
+    values, uploaded to the device unchanged (compute/gpu_engine.go:817-874)."""
+
+    BLOCK_VALUES = 256
+    BLOCK_BYTES = 0
+    NAME = ""
+
+    def __init__(self, raw: np.ndarray, length: int):
+        self.raw = raw
+        self.len = length
+        self._gpu = None
+
+    @classmethod
+    def from_raw(cls, raw: np.ndarray, num_elements: int):
+        """NewQ4KStorageFromRaw / NewQ5KStorageFromRaw / NewQ6KStorageFromRaw
+        (tensor/quantized_kquant.go:248-261, 564-577, 397-410): the first
+        ceil(n/256) super-blocks are copied; shorter data is an error."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        nb = (num_elements + cls.BLOCK_VALUES - 1) // cls.BLOCK_VALUES
+        need = nb * cls.BLOCK_BYTES
+        raw = np.asarray(raw, np.uint8).reshape(-1)
+        if raw.size < need:
+            raise ValueError(f"{cls.NAME} raw data too short: need {need} bytes for {nb} blocks, got {raw.size}")
+        return cls(raw[:need].copy(), num_elements)
+
+    def num_blocks(self) -> int:
+        return (self.len + self.BLOCK_VALUES - 1) // self.BLOCK_VALUES
+
+    def byte_size(self) -> int:
+        return self.num_blocks() * self.BLOCK_BYTES
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.raw
+
+    def block_raw(self, i: int) -> np.ndarray:
+        """BlockRaw (tensor/quantized_kquant.go:450-454, 618-622)."""
+        return self.raw[i * self.BLOCK_BYTES:(i + 1) * self.BLOCK_BYTES]
+
+
+class Q4KStorage(_KQuantBase):
+    """Q4_K: 144-byte super-blocks [fp16 d][fp16 dmin][12 B scales/mins][128 B nibbles]."""
+
+    BLOCK_BYTES = 144
+    NAME = "Q4_K"
+
+
+class Q5KStorage(_KQuantBase):
+    """Q5_K: 176-byte super-blocks (Q4_K plus 32 bytes of fifth bits)."""
+
+    BLOCK_BYTES = 176
+    NAME = "Q5_K"
+
+
+class Q6KStorage(_KQuantBase):
+    """Q6_K: 210-byte super-blocks [128 ql][64 qh][16 int8 scales][fp16 d]."""
+
+    BLOCK_BYTES = 210
+    NAME = "Q6_K"
+
+
+def merge_q4k_storage(*storages: Q4KStorage) -> Q4KStorage:
+    """MergeQ4KStorage (tensor/quantized_kquant.go:316-336)."""
+    if not storages:
+        raise ValueError("merge_q4k_storage: no storages")
+    return Q4KStorage(np.concatenate([st.raw for st in storages]), sum(st.len for st in storages))
+
+
+def merge_q6k_storage(*storages: Q6KStorage) -> Q6KStorage:
+    """MergeQ6KStorage (tensor/quantized_kquant.go:470-490)."""
+    if not storages:
+        raise ValueError("merge_q6k_storage: no storages")
+    return Q6KStorage(np.concatenate([st.raw for st in storages]), sum(st.len for st in storages))
+
+
+class Q5_0Storage(_GPUPtrMixin):
+    """Q5_0: 22-byte blocks of 32 values [fp16 d][uint32 qh][16 B nibbles]."""
+
+    def __init__(self, raw: np.ndarray, length: int):
+        self.raw = raw
+        self.len = length
+        self._gpu = None
+
+    @staticmethod
+    def from_raw(raw: np.ndarray, num_elements: int) -> "Q5_0Storage":
+        """NewQ5_0StorageFromRaw (tensor/quantized_q5_0.go:60-73)."""
+        if num_elements <= 0:
+            raise ValueError(f"numElements must be positive, got {num_elements}")
+        nb = (num_elements + 31) // 32
+        raw = np.asarray(raw, np.uint8).reshape(-1)
+        if raw.size < nb * 22:
+            raise ValueError(f"Q5_0 raw data too short: need {nb * 22} bytes for {nb} blocks, got {raw.size}")
+        return Q5_0Storage(raw[: nb * 22].copy(), num_elements)
+
+    def num_blocks(self) -> int:
+        return (self.len + 31) // 32
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.raw
+
+    def raw_bytes_gpu(self) -> np.ndarray:
+        """RawBytesGPU (tensor/quantized_q5_0.go:118-147), built by the library."""
+        lib = _lib.load()
+        nb = self.num_blocks()
+        out = np.empty(lib.zt_q5_0_gpu_bytes(nb), np.uint8)
+        lib.zt_q5_0_raw_to_gpu(_ptr(self.raw), nb, _ptr(out))
+        return out
+
+    def gpu_qh_offset(self) -> int:
+        """Q5_0GPUQhOffset (tensor/quantized_q5_0.go:151-156)."""
+        return _lib.load().zt_q5_0_gpu_qh_offset(self.num_blocks())
+
+    def gpu_qs_offset(self) -> int:
+        """Q5_0GPUQsOffset (tensor/quantized_q5_0.go:158-165)."""
+        return _lib.load().zt_q5_0_gpu_qs_offset(self.num_blocks())
 
 
 @dataclass

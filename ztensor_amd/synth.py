@@ -12,6 +12,12 @@ configurations of this path:
   IQ4_NL   nibbles U[0,15], fp16 block scale |N(0,1)|*0.01, fp16 x ~ N(0,1)
   Ternary  w in {-1,0,+1} with p = {.25,.5,.25}, one fp32 weight scale,
            int8 x = clip(round(N(0,1)*32), -127, 127) with an fp32 scale
+  Q4_K/Q5_K codes U[0,15] / U[0,31], 6-bit sub-block scales and mins
+           U[0,63], fp16 d |N(0,1)|*0.002 and dmin |N(0,1)|*0.001
+  Q6_K     codes U[0,63], int8 sub-block scales U[-64,63], fp16 d
+           |N(0,1)|*0.0005
+  Q5_0     codes U[0,31], fp16 block scale |N(0,1)|*0.02
+  (the K-quant and Q5_0 configurations take fp32 x ~ N(0,1))
 
 Seeds are 0x5EED0000 + 16*config + shape (numpy PCG64), so any host
 regenerates identical inputs.
@@ -93,6 +99,90 @@ def pack_ternary(w: np.ndarray) -> np.ndarray:
     c = codes.reshape(-1, 4)
     out = c[:, 0] | (c[:, 1] << 2) | (c[:, 2] << 4) | (c[:, 3] << 6)
     return out.astype(np.uint8)
+
+
+def pack_kq_scales_mins(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """6-bit scales and mins [nsb, 8] -> the 12 packed bytes [nsb, 12] of a
+    Q4_K / Q5_K super-block, written as the reference's test builders write
+    them (tensor/quantized_kquant_test.go:87-94): bytes 0-3 hold scales 0-3
+    with the top two bits of scales 4-7, bytes 4-7 the same for the mins,
+    bytes 8-11 the low nibbles of scales 4-7 and (high nibble) mins 4-7."""
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    out = np.empty((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = (mn[:, 0:4] & 63) | ((mn[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 0xF) | ((mn[:, 4:8] & 0xF) << 4)
+    return out
+
+
+def pack_q4_k(q: np.ndarray, sc: np.ndarray, mn: np.ndarray, d_bits: np.ndarray, dmin_bits: np.ndarray) -> np.ndarray:
+    """Codes [nsb, 256] (0..15) -> 144-byte Q4_K super-blocks
+    (tensor/quantized_kquant_test.go:80-128): group g's 32 bytes hold value
+    64g+l in the low nibble of byte l and 64g+32+l in the high nibble."""
+    q = q.reshape(-1, 256).astype(np.uint8)
+    nsb = q.shape[0]
+    out = np.empty((nsb, 144), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").reshape(nsb, 1).view(np.uint8)
+    out[:, 2:4] = dmin_bits.astype("<u2").reshape(nsb, 1).view(np.uint8)
+    out[:, 4:16] = pack_kq_scales_mins(sc, mn)
+    g = q.reshape(nsb, 4, 64)
+    out[:, 16:] = (g[:, :, :32] | (g[:, :, 32:] << 4)).reshape(nsb, 128)
+    return out.reshape(-1)
+
+
+def pack_q5_k(q: np.ndarray, sc: np.ndarray, mn: np.ndarray, d_bits: np.ndarray, dmin_bits: np.ndarray) -> np.ndarray:
+    """Codes [nsb, 256] (0..31) -> 176-byte Q5_K super-blocks
+    (tensor/quantized_kquant_test.go:414-468): the low four bits as Q4_K,
+    the fifth bit of value 64g+l at bit 2g of qh byte l and of value
+    64g+32+l at bit 2g+1."""
+    q = q.reshape(-1, 256).astype(np.uint8)
+    nsb = q.shape[0]
+    out = np.empty((nsb, 176), np.uint8)
+    out[:, 0:144] = pack_q4_k(q & 0xF, sc, mn, d_bits, dmin_bits).reshape(nsb, 144)
+    g = (q >> 4).reshape(nsb, 4, 2, 32)  # [sb, group, half, l]
+    qh = np.zeros((nsb, 32), np.uint8)
+    for grp in range(4):
+        for half in range(2):
+            qh |= g[:, grp, half, :] << (2 * grp + half)
+    out[:, 144:176] = qh
+    return out.reshape(-1)
+
+
+def pack_q6_k(q: np.ndarray, sc: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """Codes [nsb, 256] (0..63, value q-32) and int8 scales [nsb, 16] ->
+    210-byte Q6_K super-blocks (tensor/quantized_kquant_test.go:263-292):
+    half h, l < 32: ql[64h+l] = q1 & 15 | (q3 & 15) << 4,
+    ql[64h+32+l] = q2 & 15 | (q4 & 15) << 4, qh[32h+l] = the top two bits of
+    q1, q2, q3, q4 at bits 0, 2, 4, 6, with q1..q4 the values 128h + l,
+    +32, +64, +96."""
+    q = q.reshape(-1, 2, 4, 32).astype(np.uint8)  # [sb, half, quarter, l]
+    nsb = q.shape[0]
+    out = np.empty((nsb, 210), np.uint8)
+    q1, q2, q3, q4 = q[:, :, 0], q[:, :, 1], q[:, :, 2], q[:, :, 3]
+    ql = np.empty((nsb, 2, 64), np.uint8)
+    ql[:, :, :32] = (q1 & 0xF) | ((q3 & 0xF) << 4)
+    ql[:, :, 32:] = (q2 & 0xF) | ((q4 & 0xF) << 4)
+    qh = ((q1 >> 4) & 3) | (((q2 >> 4) & 3) << 2) | (((q3 >> 4) & 3) << 4) | (((q4 >> 4) & 3) << 6)
+    out[:, 0:128] = ql.reshape(nsb, 128)
+    out[:, 128:192] = qh.reshape(nsb, 64)
+    out[:, 192:208] = sc.reshape(nsb, 16).astype(np.int8).view(np.uint8)
+    out[:, 208:210] = d_bits.astype("<u2").reshape(nsb, 1).view(np.uint8)
+    return out.reshape(-1)
+
+
+def pack_q5_0(q: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """Codes [nblk, 32] (0..31, value q-16) -> 22-byte Q5_0 blocks
+    (tensor/quantized_q5_0.go:14-45): [fp16 d][uint32 qh: bit j = fifth bit
+    of value j][16 bytes: value j low nibble | value j+16 low nibble << 4]."""
+    q = q.reshape(-1, 32).astype(np.uint32)
+    nblk = q.shape[0]
+    out = np.empty((nblk, 22), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").reshape(nblk, 1).view(np.uint8)
+    qh = (((q >> 4) & 1) << np.arange(32, dtype=np.uint32)).sum(axis=1).astype("<u4")
+    out[:, 2:6] = qh.reshape(nblk, 1).view(np.uint8)
+    out[:, 6:22] = ((q[:, :16] & 0xF) | ((q[:, 16:] & 0xF) << 4)).astype(np.uint8)
+    return out.reshape(-1)
 
 
 # ------------------------------------------------------------ workloads
@@ -177,6 +267,41 @@ def ternary(rows: int, K: int, seed: int) -> TernaryWeights:
     return TernaryWeights(rows, K, pack_ternary(w), w_scale)
 
 
+@dataclass
+class KQWeights:
+    fmt: str  # "q4_k", "q5_k", "q6_k" or "q5_0"
+    rows: int
+    K: int
+    raw: np.ndarray  # contiguous super-blocks / blocks as RawBytes() holds them
+
+
+KQ_BLOCK = {"q4_k": (256, 144), "q5_k": (256, 176), "q6_k": (256, 210), "q5_0": (32, 22)}
+
+
+def kquant(fmt: str, rows: int, K: int, seed: int) -> KQWeights:
+    """Seeded K-quant / Q5_0 weights of shape [rows, K] (blocks along K)."""
+    g = rng(seed)
+    vals, _ = KQ_BLOCK[fmt]
+    nb = rows * K // vals
+    if fmt in ("q4_k", "q5_k"):
+        q = g.integers(0, 16 if fmt == "q4_k" else 32, size=(nb, 256), dtype=np.uint8)
+        sc = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        mn = g.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        d = f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.002))
+        dmin = f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.001))
+        raw = (pack_q4_k if fmt == "q4_k" else pack_q5_k)(q, sc, mn, d, dmin)
+    elif fmt == "q6_k":
+        q = g.integers(0, 64, size=(nb, 256), dtype=np.uint8)
+        sc = g.integers(-64, 64, size=(nb, 16), dtype=np.int16).astype(np.int8)
+        d = f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.0005))
+        raw = pack_q6_k(q, sc, d)
+    else:
+        q = g.integers(0, 32, size=(nb, 32), dtype=np.uint8)
+        d = f16_bits(np.abs(g.standard_normal(nb, dtype=np.float32)) * np.float32(0.02))
+        raw = pack_q5_0(q, d)
+    return KQWeights(fmt, rows, K, raw)
+
+
 def x_f32(n: int, seed: int) -> np.ndarray:
     return rng(seed ^ 0xA5A5).standard_normal(n, dtype=np.float32)
 
@@ -208,6 +333,9 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
     if fmt == "w4a16":
         ng = rows * K // group
         return rows * K // 2 + 2 * ng * (2 if zeros else 1) + 2 * K * N + 4 * rows * N
+    if fmt in KQ_BLOCK:
+        vals, nbytes = KQ_BLOCK[fmt]
+        return rows * K // vals * nbytes + 4 * K * N + 4 * rows * N
     if fmt == "ternary_i8":
         return rows * ((K + 3) // 4) + K * N + 4 * rows * N + 8
     raise ValueError(fmt)
