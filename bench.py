@@ -18,8 +18,9 @@ Also reported on the same JSON line:
                 host cores, over one layer's seven matrices.
 
 `python bench.py --suite` instead prints one line per benchmark
-configuration (W4A16, Q4_0, Q8_0, ternary, IQ4_NL) with us per matmul and
-effective GB/s; those are supporting numbers, not the headline line.
+configuration (W4A16, Q4_0, Q8_0, ternary, IQ4_NL, and the K-quant / Q5_0
+formats at the Llama-3-8B shapes) with us per matmul and effective GB/s;
+those are supporting numbers, not the headline line.
 """
 from __future__ import annotations
 
@@ -312,6 +313,10 @@ SUITE = {
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
+    "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
 }
 
 
@@ -367,6 +372,23 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: lib.zt_ternary_gemv_i8(wb[0].data_ptr(), x.data_ptr(), sc.data_ptr(), sc.data_ptr() + 4,
                                                   y.data_ptr(), rows, K, s)
         nbytes = synth.algorithmic_bytes("ternary_i8", rows, K, N)
+    elif fmt in ("q4_k", "q5_k", "q6_k"):
+        w = synth.kquant(fmt, rows, K, seed)
+        wbufs = [dev(w.raw)]
+        x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
+        name = f"zt_gemv_{fmt.replace('_', '')}_f32"
+        fn = lambda wb, y: getattr(lib, name)(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, s)
+        nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
+    elif fmt == "q5_0":
+        w = synth.kquant(fmt, rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q5_0_gpu_bytes(nblk), np.uint8)
+        lib.zt_q5_0_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+        wbufs = [dev(host)]
+        qh, qs = lib.zt_q5_0_gpu_qh_offset(nblk), lib.zt_q5_0_gpu_qs_offset(nblk)
+        x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
+        fn = lambda wb, y: lib.zt_gemv_q5_0_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, qh, qs, s)
+        nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
     else:
         raise ValueError(fmt)
     wbytes = sum(b.numel() for b in wbufs)
