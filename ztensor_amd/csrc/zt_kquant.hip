@@ -38,24 +38,42 @@
 
 namespace zt {
 
-// 8 bytes at a 2-byte aligned address, from three aligned dwords.
-__device__ __forceinline__ uint2 ld_u64_a2(const uint8_t* p) {
+// NW dwords at a 2-byte aligned address, from aligned dwords joined with
+// v_alignbit.  The extra dword is read only when the address is misaligned:
+// an aligned field ends at its last dword, and reading further could pass
+// the end of the last block.
+template <int NW>
+__device__ __forceinline__ void ld_a2(const uint8_t* p, uint32_t (&out)[NW]) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
     const uint32_t s = (uint32_t)(a & 3) * 8u;
-    const uint32_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1);
-    // the third dword only when misaligned: an aligned field ends at the
-    // second, and reading further could pass the end of the last block
-    const uint32_t w2 = s ? __builtin_nontemporal_load(q + 2) : 0u;
-    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, s), __builtin_amdgcn_alignbit(w2, w1, s));
+    uint32_t w[NW + 1];
+#pragma unroll
+    for (int i = 0; i < NW; i++) w[i] = __builtin_nontemporal_load(q + i);
+    w[NW] = s ? __builtin_nontemporal_load(q + NW) : 0u;
+#pragma unroll
+    for (int i = 0; i < NW; i++) out[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], s);
 }
 
-// Sum of the 8 masked fp16 subnormals of two dwords (lo: values 0..3 of the
-// first dword and 0..3 of the second) against pre-scaled activations.
-// m0/m2 hold the values of bytes (0,2)/(1,3) of dword j in their two halves.
-__device__ __forceinline__ float chain8(const uint32_t (&m)[2][2], const float (&xp)[8], float acc) {
+// NW dwords at a 4*NW-byte aligned address.
+template <int NW>
+__device__ __forceinline__ void ld_vec(const uint8_t* p, uint32_t (&out)[NW]) {
+    if constexpr (NW == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        out[0] = v.x; out[1] = v.y;
+    }
+}
+
+// Sum of the masked fp16 subnormals of NW dwords against pre-scaled
+// activations.  m[j][0] / m[j][1] hold the values of bytes (0,2) / (1,3) of
+// dword j in their two halves, i.e. values 4j+0, 4j+2 / 4j+1, 4j+3.
+template <int NW>
+__device__ __forceinline__ float chainw(const uint32_t (&m)[NW][2], const float (&xp)[4 * NW], float acc) {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NW; j++) {
         const half2v a = as_half2(m[j][0]), b = as_half2(m[j][1]);
         acc = __builtin_fmaf((float)a.x, xp[4 * j + 0], acc);
         acc = __builtin_fmaf((float)b.x, xp[4 * j + 1], acc);
@@ -65,31 +83,37 @@ __device__ __forceinline__ float chain8(const uint32_t (&m)[2][2], const float (
     return acc;
 }
 
-// x pieces of one lane: 8 values starting at lo and 8 at hi (16-byte aligned).
+// The lane's activations: 4*NW values at lo and 4*NW at hi (16-byte aligned),
+// pre-scaled by 2^24 / 2^20 for the low / high nibble chains, plus their sums.
+template <int NW>
 struct KqX {
-    float lo[8], hi[8];  // pre-scaled by 2^24 / 2^20
-    float slo, shi;      // plain sums
+    float lo[4 * NW], hi[4 * NW];
+    float slo, shi;
 };
 
-__device__ __forceinline__ void kq_load_x(const float* __restrict__ x, long lo, long hi, bool valid, KqX& o) {
-    float a[8], b[8];
-    if (valid) {
-        const float4 a0 = *reinterpret_cast<const float4*>(x + lo), a1 = *reinterpret_cast<const float4*>(x + lo + 4);
-        const float4 b0 = *reinterpret_cast<const float4*>(x + hi), b1 = *reinterpret_cast<const float4*>(x + hi + 4);
-        a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
-        b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
-    } else {
+template <int NW>
+__device__ __forceinline__ void kq_load_x(const float* __restrict__ x, long lo, long hi, bool valid, KqX<NW>& o) {
+    float a[4 * NW], b[4 * NW];
 #pragma unroll
-        for (int i = 0; i < 8; i++) a[i] = b[i] = 0.0f;
+    for (int i = 0; i < NW; i++) {
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), v = u;
+        if (valid) {
+            u = *reinterpret_cast<const float4*>(x + lo + 4 * i);
+            v = *reinterpret_cast<const float4*>(x + hi + 4 * i);
+        }
+        a[4 * i] = u.x; a[4 * i + 1] = u.y; a[4 * i + 2] = u.z; a[4 * i + 3] = u.w;
+        b[4 * i] = v.x; b[4 * i + 1] = v.y; b[4 * i + 2] = v.z; b[4 * i + 3] = v.w;
     }
-    o.slo = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-    o.shi = ((b[0] + b[1]) + (b[2] + b[3])) + ((b[4] + b[5]) + (b[6] + b[7]));
-    // chain8 order: dword j -> bytes 0, 1, 2, 3 = values 4j .. 4j+3 as (a.x, b.x, a.y, b.y)
+    float sa = 0.0f, sb = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < 4 * NW; i++) {
+        sa += a[i];
+        sb += b[i];
         o.lo[i] = a[i] * 16777216.0f;
         o.hi[i] = b[i] * 1048576.0f;
     }
+    o.slo = sa;
+    o.shi = sb;
 }
 
 // Scale and min pairs (sub-blocks 2g, 2g+1) of a Q4_K/Q5_K header, as two
@@ -114,23 +138,31 @@ struct KqFmt<5> { static constexpr int bytes = 176; };
 template <>
 struct KqFmt<6> { static constexpr int bytes = 210; };
 
-template <int FMT, int R>
+// NW = dwords of the low-bit array per lane (2 or 4): 128 / (4*NW) lanes
+// share a super-block and a wave covers NW super-blocks per step.
+template <int FMT, int NW, int R>
 __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                       float* __restrict__ y, int rows, int nsb) {
     constexpr int BB = KqFmt<FMT>::bytes;
+    constexpr int NB = 4 * NW;        // low-bit bytes per lane
+    constexpr int LPS = 128 / NB;     // lanes per super-block
+    constexpr int SPW = 64 / LPS;     // super-blocks per wave step
     __shared__ float red[8 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int slot = lane >> 4, t = lane & 15;
+    const int slot = lane / LPS, t = lane % LPS;
     const int row0 = blockIdx.x * R;
-    // Lane roles.  Q4_K/Q5_K: g = t/4 (group), u = t%4 -> bytes 32g+8u of the
-    // nibbles: values 64g+8u+i (sub-block 2g) and 64g+32+8u+i (2g+1).
-    // Q6_K: h = t/8 (half), u = t%8 -> ql bytes 64h+8u: values
-    // vlo = 128h + 32*(u>=4) + 8*(u%4) + i (scale vlo/16) and vlo+64.
-    const int g = t >> 2, u4 = t & 3;
-    const int h6 = t >> 3, u8 = t & 7;
+    // Lane roles.  Q4_K/Q5_K: bytes t*NB .. of the 128 nibble bytes: group
+    // g = t*NB/32, offset o = t*NB%32 -> values 64g+o+i (sub-block 2g) and
+    // 64g+32+o+i (2g+1); Q5_K's fifth bits are qh bytes o .. o+NB-1.
+    // Q6_K: half h = t*NB/64, w = t*NB%64: ql bytes 64h+w .. are values
+    // vlo = 128h + 32*(w>=32) + w%32 + i (scale vlo/16, qh bits 0-1 / 2-3)
+    // and vlo+64 (scale +4, qh bits 4-5 / 6-7); qh bytes 32h + w%32 ...
+    const int byte0 = t * NB;
+    const int g = byte0 >> 5, o = byte0 & 31;
+    const int h6 = byte0 >> 6, w6 = byte0 & 63;
     const bool hi_grp = g >= 2;
     const uint32_t sh = 16u * (uint32_t)(g & 1);
-    const int vlo = FMT == 6 ? 128 * h6 + 32 * (u8 >= 4) + 8 * (u8 & 3) : 64 * g + 8 * u4;
+    const int vlo = FMT == 6 ? 128 * h6 + 32 * (w6 >= 32) + (w6 & 31) : 64 * g + o;
     const int vhi = FMT == 6 ? vlo + 64 : vlo + 32;
     long rbase[R];
 #pragma unroll
@@ -139,24 +171,23 @@ __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
 
-    for (int base = wave * 4; base < nsb; base += nwaves * 4) {
+    for (int base = wave * SPW; base < nsb; base += nwaves * SPW) {
         const int sb = base + slot;
         const bool valid = sb < nsb;
         const int sbc = valid ? sb : nsb - 1;
-        KqX xs;
-        kq_load_x(x, (long)sbc * 256 + vlo, (long)sbc * 256 + vhi, valid, xs);
+        KqX<NW> xs;
+        kq_load_x<NW>(x, (long)sbc * 256 + vlo, (long)sbc * 256 + vhi, valid, xs);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint8_t* blk = W + (rbase[r] + sbc) * BB;
-            uint32_t m[2][2][2];  // [lo/hi][dword][pair]
+            uint32_t ml[NW][2], mh[NW][2];
+            uint32_t qd[NW], hd[NW];
             if constexpr (FMT == 4 || FMT == 5) {
                 const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
-                const uint2 q = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + 8 * u4);
-                uint2 qh = make_uint2(0, 0);
-                if constexpr (FMT == 5) qh = *reinterpret_cast<const uint2*>(blk + 144 + 8 * u4);
-                const uint32_t qd[2] = {q.x, q.y}, hd[2] = {qh.x, qh.y};
+                ld_vec<NW>(blk + 16 + byte0, qd);
+                if constexpr (FMT == 5) ld_vec<NW>(blk + 144 + o, hd);
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < NW; j++) {
                     const uint32_t d = qd[j], d8 = d >> 8;
                     uint32_t l0 = d & 0x000F000Fu, l2 = d8 & 0x000F000Fu, h0 = d & 0x00F000F0u, h2 = d8 & 0x00F000F0u;
                     if constexpr (FMT == 5) {
@@ -166,10 +197,10 @@ __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict_
                         h0 |= (H << 8) & 0x01000100u;  // (q<<4) fifth bit -> bit 8 / 24
                         h2 |= H & 0x01000100u;
                     }
-                    m[0][j][0] = l0; m[0][j][1] = l2; m[1][j][0] = h0; m[1][j][1] = h2;
+                    ml[j][0] = l0; ml[j][1] = l2; mh[j][0] = h0; mh[j][1] = h2;
                 }
-                const float S0 = chain8(m[0], xs.lo, 0.0f);
-                const float S1 = chain8(m[1], xs.hi, 0.0f);
+                const float S0 = chainw<NW>(ml, xs.lo, 0.0f);
+                const float S1 = chainw<NW>(mh, xs.hi, 0.0f);
                 uint32_t scp, mnp;
                 kq_sc_mn(hdr, hi_grp, sh, scp, mnp);
                 const float sc0 = (float)(scp & 0xFFu), sc1 = (float)((scp >> 8) & 0xFFu);  // v_cvt_f32_ubyte0/1
@@ -180,27 +211,27 @@ __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict_
                 acc[r] = __builtin_fmaf((float)dd.x, tq, acc[r]);
                 acc[r] = __builtin_fmaf(-(float)dd.y, tm, acc[r]);
             } else {
-                const uint2 ql = ld_u64_a2(blk + 64 * h6 + 8 * u8);
-                const uint2 qh = ld_u64_a2(blk + 128 + 32 * h6 + 8 * (u8 & 3));
-                const uint2 scw = ld_u64_a2(blk + 192 + 8 * h6);   // scales 8h .. 8h+7
+                ld_a2<NW>(blk + byte0, qd);
+                ld_a2<NW>(blk + 128 + 32 * h6 + (w6 & 31), hd);
+                uint32_t scw[2];
+                ld_a2<2>(blk + 192 + 8 * h6, scw);  // scales 8h .. 8h+7
                 const uint32_t dw = *reinterpret_cast<const uint16_t*>(blk + 208);
-                const uint32_t qsh = (u8 >= 4) ? 2u : 0u;           // lo uses qh bits 0-1 (2-3), hi bits 4-5 (6-7)
-                const uint32_t qd[2] = {ql.x, ql.y}, hd[2] = {qh.x, qh.y};
+                const uint32_t qsh = (w6 >= 32) ? 2u : 0u;  // lo uses qh bits 0-1 (2-3), hi bits 4-5 (6-7)
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < NW; j++) {
                     const uint32_t d = qd[j], d8 = d >> 8;
                     const uint32_t L = hd[j] >> qsh, H = hd[j] >> (qsh + 4);
-                    m[0][j][0] = (d & 0x000F000Fu) | ((L << 4) & 0x00300030u);
-                    m[0][j][1] = (d8 & 0x000F000Fu) | ((L >> 4) & 0x00300030u);
-                    m[1][j][0] = (d & 0x00F000F0u) | ((H << 8) & 0x03000300u);
-                    m[1][j][1] = (d8 & 0x00F000F0u) | (H & 0x03000300u);
+                    ml[j][0] = (d & 0x000F000Fu) | ((L << 4) & 0x00300030u);
+                    ml[j][1] = (d8 & 0x000F000Fu) | ((L >> 4) & 0x00300030u);
+                    mh[j][0] = (d & 0x00F000F0u) | ((H << 8) & 0x03000300u);
+                    mh[j][1] = (d8 & 0x00F000F0u) | (H & 0x03000300u);
                 }
-                const float S0 = chain8(m[0], xs.lo, -32.0f * xs.slo);
-                const float S1 = chain8(m[1], xs.hi, -32.0f * xs.shi);
-                // scale index of vlo is 8h + 2*(u>=4) + (u%4)/2; of vhi that + 4.
-                const int si = 2 * (u8 >= 4) + ((u8 & 3) >> 1);
-                const int sc0 = __builtin_amdgcn_sbfe((int)scw.x, 8 * si, 8);
-                const int sc1 = __builtin_amdgcn_sbfe((int)scw.y, 8 * si, 8);
+                const float S0 = chainw<NW>(ml, xs.lo, -32.0f * xs.slo);
+                const float S1 = chainw<NW>(mh, xs.hi, -32.0f * xs.shi);
+                // scale index of vlo relative to 8h: 2*(w>=32) + (w%32)/16; of vhi that + 4
+                const int si = 2 * (w6 >= 32) + ((w6 & 31) >> 4);
+                const int sc0 = __builtin_amdgcn_sbfe((int)scw[0], 8 * si, 8);
+                const int sc1 = __builtin_amdgcn_sbfe((int)scw[1], 8 * si, 8);
                 const float tq = __builtin_fmaf((float)sc1, S1, (float)sc0 * S0);
                 const half2v dd = as_half2(dw);
                 acc[r] = __builtin_fmaf((float)dd.x, tq, acc[r]);
@@ -210,14 +241,14 @@ __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict_
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
-template <int FMT>
+template <int FMT, int NW>
 static void launch_kq(int R, dim3 grid, dim3 block, hipStream_t st, const uint8_t* W, const float* x, float* y,
                       int rows, int nsb) {
     switch (R) {
-        case 8: kq_gemv_kernel<FMT, 8><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
-        case 4: kq_gemv_kernel<FMT, 4><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
-        case 2: kq_gemv_kernel<FMT, 2><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
-        default: kq_gemv_kernel<FMT, 1><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 8: kq_gemv_kernel<FMT, NW, 8><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 4: kq_gemv_kernel<FMT, NW, 4><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 2: kq_gemv_kernel<FMT, NW, 2><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        default: kq_gemv_kernel<FMT, NW, 1><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
     }
 }
 
@@ -234,9 +265,13 @@ static int gemv_kq(const void* W, const float* x, float* y, int M, int K, hipStr
     if (W == nullptr || x == nullptr || y == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)x & 15) || ((uintptr_t)W & (FMT == 6 ? 1 : 15))) return (int)hipErrorInvalidValue;
     const int nsb = K / 256;
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    // 8 bytes of the low-bit array per lane (NW = 2): measured on the
+    // Llama-3-8B shapes, 16 bytes per lane (NW = 4) was no faster for
+    // Q4_K / Q5_K and 10-15% slower for Q6_K.
     const int nwaves = min(8, ceil_div(nsb, 4));
     const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
-    launch_kq<FMT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, static_cast<const uint8_t*>(W), x, y, M, nsb);
+    launch_kq<FMT, 2>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, w, x, y, M, nsb);
     return (int)hipGetLastError();
 }
 
