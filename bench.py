@@ -317,6 +317,7 @@ SUITE = {
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q8_0_gguf": ("q8_0_gguf", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
 }
 
 
@@ -378,6 +379,16 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
         name = f"zt_gemv_{fmt.replace('_', '')}_f32"
         fn = lambda wb, y: getattr(lib, name)(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, s)
+        nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
+    elif fmt == "q8_0_gguf":
+        raw = synth.gguf_q8_0(rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q8gguf_gpu_bytes(nblk), np.uint8)
+        lib.zt_q8gguf_raw_to_gpu(raw.ctypes.data, nblk, host.ctypes.data)
+        wbufs = [dev(host)]
+        off = lib.zt_q8gguf_gpu_data_offset(nblk)
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        fn = lambda wb, y: lib.zt_gemm_q8gguf_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
         nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
     elif fmt == "q5_0":
         w = synth.kquant(fmt, rows, K, seed)

@@ -22,6 +22,7 @@
  *                  (tensor/quantized.go:158-198 RawBytesGPU)
  *   Q8_0 raw:      36-byte blocks [fp32 scale][32 x int8] (tensor/quantized.go:425-438)
  *   Q8_0 sep:      [scales nblk*4 B][pad to 16][data nblk*32 B]
+ *   GGUF Q8_0:     [fp16 scales nblk*2 B][pad to 16][data nblk*32 B]
  *   W4 (GPTQ/AWQ): packed nibbles [M, K/2] + fp16 scales/zeros [M, K/group]
  *                  (tensor/quantized_gptq.go:217-277, tensor/quantized_awq.go:23-39)
  *   Ternary:       row-aligned 2-bit codes [M, ceil(K/4)]
@@ -114,6 +115,21 @@ int zt_q8_repack(const void* raw, void* out, long nblk, zt_stream_t stream);
 long zt_q8_gpu_data_offset(long nblk);
 long zt_q8_gpu_bytes(long nblk);
 void zt_q8_raw_to_gpu(const void* raw, long nblk, void* out);
+
+/* GGUF Q8_0: the 34-byte [fp16 d][32 x int8] blocks of an mmap'd GGUF tensor
+ * (MmapStorage, tensor/mmap_storage.go:94-96, 265-284).  The reference's GPU
+ * engine hands these bytes to the 36-byte gemm_q8_f32
+ * (compute/gpu_engine.go:2865-2870), which misreads them; here they are
+ * repacked once at upload into [fp16 d, nblk*2][pad 16][int8, nblk*32]
+ * (zt_q8gguf_raw_to_gpu; data_offset = zt_q8gguf_gpu_data_offset(nblk)) and
+ * multiplied with the Q8_0 kernels.  Dequantization is bit-exact with
+ * MmapStorage.dequantizeQ8_0. */
+int zt_gemm_q8gguf_f32(const void* A, const float* B, float* C, int M, int K, int N, long data_offset,
+                       zt_stream_t stream);
+int zt_dequant_q8gguf_f32(const void* A, float* out, long nelem, long data_offset, zt_stream_t stream);
+long zt_q8gguf_gpu_data_offset(long nblk);
+long zt_q8gguf_gpu_bytes(long nblk);
+void zt_q8gguf_raw_to_gpu(const void* raw, long nblk, void* out);
 
 /* ---- W4A16 (GPTQ / AWQ 4-bit, fp16 activations) ----------------------- */
 

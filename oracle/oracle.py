@@ -50,6 +50,8 @@ _SIG = {
     "orc_q5_0_gpu_qs_offset": (L, [L]),
     "orc_q5_0_raw_to_gpu": (None, [P, L, P]),
     "orc_gemm_f32_q5_0_nt": (None, [L, L, L, P, P, P, P, P]),
+    "orc_gguf_q8_0_dequant": (None, [P, L, P]),
+    "orc_gemm_f32_mmap_nt": (I, [I, L, L, L, P, P, P, I, P]),
 }
 
 _lib = None
@@ -257,4 +259,24 @@ def gemm_f32_q5_0_nt(a: np.ndarray, raw: np.ndarray, m: int, n: int, k: int) -> 
     wt = np.empty(n * k, np.float32)
     tt = np.empty(n * k, np.float32)
     lib().orc_gemm_f32_q5_0_nt(m, n, k, _p(a), _p(raw), _p(c), _p(wt), _p(tt))
+    return c
+
+
+# ---- GGUF mmap --------------------------------------------------------------
+
+def gguf_q8_0_dequant(raw: np.ndarray, nelem: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.empty(nelem, np.float32)
+    lib().orc_gguf_q8_0_dequant(_p(raw), nelem, _p(out))
+    return out
+
+
+def gemm_f32_mmap_nt(qtype: int, a: np.ndarray, raw: np.ndarray, m: int, n: int, k: int, threads: int = 1) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    raw = np.ascontiguousarray(raw, np.uint8)
+    c = np.empty(m * n, np.float32)
+    wt = np.empty(n * k if qtype in (2, 6, 8) else 1, np.float32)
+    rc = lib().orc_gemm_f32_mmap_nt(qtype, m, n, k, _p(a), _p(raw), _p(c), threads, _p(wt))
+    if rc != 0:
+        raise ValueError(f"GGML type {qtype} has no quantized GEMV here")
     return c

@@ -707,3 +707,47 @@ EXPORT void orc_gemm_f32_q5_0_nt(int64_t m, int64_t n, int64_t k, const float* a
     memset(c, 0, sizeof(float) * (size_t)(m * n));
     orc_sgemm_simd(m, n, k, a, ttmp, c);
 }
+
+/* ------------------------------------------------------------ GGUF mmap */
+
+/* tensor/mmap_storage.go:265-284 MmapStorage.dequantizeQ8_0: GGUF Q8_0,
+ * 34-byte blocks [fp16 d][32 x int8], value = float32(int8) * d. */
+EXPORT void orc_gguf_q8_0_dequant(const uint8_t* raw, int64_t nelem, float* dst) {
+    int64_t nblk = (nelem + 31) / 32;
+    for (int64_t bi = 0; bi < nblk; bi++) {
+        const uint8_t* b = raw + bi * 34;
+        float scale = orc_f16_to_f32(rd16(b));
+        for (int j = 0; j < 32; j++) {
+            int64_t idx = bi * 32 + j;
+            if (idx >= nelem) break;
+            dst[idx] = (float)(int8_t)b[2 + j] * scale;
+        }
+    }
+}
+
+/* internal/xblas/gemm_mmap.go:18-40 GemmF32MmapNT: C[M,N] = A[M,K] * B^T,
+ * B an MmapStorage [N,K] of GGML type qtype (tensor/mmap_storage.go:18-30).
+ * Q4_K / Q5_K / Q6_K stream super-blocks (gemm_mmap.go:56-195; the same
+ * element-order sums as the storage GEMVs above); every other type is
+ * dequantized whole (Slice, tensor/mmap_storage.go:127-134, 191-216) and
+ * summed in element order.  Q4_0 (:239-263) dequantizes like Q4Storage,
+ * Q5_0 (:368-400) like DequantizeQ5_0 (float32(q-16) * d).  wtmp holds N*K
+ * floats for the dequantizing types. */
+EXPORT int orc_gemm_f32_mmap_nt(int qtype, int64_t m, int64_t n, int64_t k, const float* a, const uint8_t* raw,
+                                float* c, int nthreads, float* wtmp) {
+    if (qtype == 12 || qtype == 13 || qtype == 14) {
+        orc_gemm_f32_kq_nt(qtype == 12 ? 4 : qtype == 13 ? 5 : 6, m, n, k, a, raw, c, nthreads);
+        return 0;
+    }
+    if (qtype == 2) orc_q4_dequant(raw, n * k, wtmp);
+    else if (qtype == 8) orc_gguf_q8_0_dequant(raw, n * k, wtmp);
+    else if (qtype == 6) orc_q5_0_dequant(raw, n * k, wtmp);
+    else return -1;
+    for (int64_t i = 0; i < m; i++)
+        for (int64_t j = 0; j < n; j++) {
+            float sum = 0.0f;
+            for (int64_t p = 0; p < k; p++) sum += a[i * k + p] * wtmp[j * k + p];
+            c[i * n + j] = sum;
+        }
+    return 0;
+}

@@ -132,3 +132,40 @@ def test_kquant_storage_constructors_validate_like_the_reference():
     b = Q4KStorage.from_raw(synth.kquant("q4_k", 1, 256, 2).raw, 256)
     m = merge_q4k_storage(a, b)  # TestMergeQ4KStorage (tensor/quantized_kquant_test.go:496-543)
     assert m.len == 768 and np.array_equal(m.raw, np.concatenate([a.raw, b.raw]))
+
+
+def test_gguf_q8_0_device_layout():
+    from ztensor_amd.storage import GGMLType, MmapStorage
+
+    rows, K = 5, 64
+    raw = synth.gguf_q8_0(rows, K, 7)
+    s = MmapStorage(raw, rows * K, GGMLType.Q8_0)
+    buf, offs = s.device_layout()
+    nblk = rows * K // 32
+    off = offs["data_offset"]
+    assert off == 32 and buf.size == off + 32 * nblk  # (10*2 + 15) & ~15
+    blocks = raw.reshape(nblk, 34)
+    assert np.array_equal(buf[: 2 * nblk].reshape(nblk, 2), blocks[:, :2])
+    assert not buf[2 * nblk:off].any()
+    assert np.array_equal(buf[off:].reshape(nblk, 32), blocks[:, 2:])
+
+
+def test_mmap_storage_validates_like_the_reference():
+    from ztensor_amd.storage import GGMLType, MmapStorage, Q4Storage, mmap_byte_size
+
+    # mmapByteSize (tensor/mmap_storage.go:85-119)
+    assert mmap_byte_size(GGMLType.Q8_0, 64) == 68 and mmap_byte_size(GGMLType.Q4_K, 300) == 288
+    assert mmap_byte_size(GGMLType.Q5_1, 33) == 48 and mmap_byte_size(GGMLType.BF16, 3) == 6
+    with pytest.raises(ValueError):
+        mmap_byte_size(99, 32)
+    with pytest.raises(ValueError):
+        MmapStorage(np.zeros(10, np.uint8), 32, GGMLType.Q8_0)  # too short
+    with pytest.raises(ValueError):
+        MmapStorage(np.zeros(0, np.uint8), 32, GGMLType.Q4_0)
+    w = synth.q4_0(3, 64, 8)
+    m = MmapStorage(np.concatenate([w.raw, np.zeros(9, np.uint8)]), 192, GGMLType.Q4_0)
+    assert m.raw_bytes().size == 6 * 18
+    # RawBytesGPU (tensor/mmap_storage.go:170-189) is Q4Storage's for Q4_0
+    assert np.array_equal(m.raw_bytes_gpu(), Q4Storage.from_raw(w.raw, 192).raw_bytes_gpu())
+    with pytest.raises(TypeError):
+        MmapStorage(np.zeros(40, np.uint8), 32, GGMLType.Q4_1).device_layout()

@@ -211,3 +211,64 @@ def test_engine_q6k_and_q5_0(orc):
     got = eng.matmul(Tensor((rows, K), Q5_0Storage.from_raw(w5.raw, rows * K)), devf(x2)).cpu().numpy()
     W5 = orc.q5_0_dequant(w5.raw, rows * K).reshape(rows, K).astype(np.float64)
     assert rel_err(got, W5 @ x2.astype(np.float64)) <= TOL
+
+
+# ------------------------------------------------------------------ GGUF mmap
+
+
+def q8gguf_dev(lib, raw, nblk):
+    host = np.empty(lib.zt_q8gguf_gpu_bytes(nblk), np.uint8)
+    lib.zt_q8gguf_raw_to_gpu(raw.ctypes.data, nblk, host.ctypes.data)
+    return dev(host), lib.zt_q8gguf_gpu_data_offset(nblk)
+
+
+@pytest.mark.parametrize("rows,K", [(1, 32), (5, 96), (64, 4096)])
+def test_gguf_q8_0_dequant_bit_exact(lib, orc, rows, K):
+    raw = synth.gguf_q8_0(rows, K, 91)
+    nblk = rows * K // 32
+    d, off = q8gguf_dev(lib, raw, nblk)
+    out = torch.empty(rows * K, dtype=torch.float32, device="cuda")
+    lib.call("zt_dequant_q8gguf_f32", d.data_ptr(), out.data_ptr(), rows * K, off, stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.gguf_q8_0_dequant(raw, rows * K).view(np.uint32))
+
+
+@pytest.mark.parametrize("N", [1, 3])
+@pytest.mark.parametrize("rows,K", LLAMA8B + [(3, 32), (65, 2080)])
+def test_gguf_q8_0_gemm_matches_oracle(lib, orc, rows, K, N):
+    say(f"gguf q8_0 {rows}x{K} N={N}")
+    raw = synth.gguf_q8_0(rows, K, 92)
+    d, off = q8gguf_dev(lib, raw, rows * K // 32)
+    x = synth.x_f32(K * N, 92)
+    xd = devf(x)
+    y = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_q8gguf_f32", d.data_ptr(), xd.data_ptr(), y.data_ptr(), rows, K, N, off, stream())
+    torch.cuda.synchronize()
+    # reference CPU engine on the same weights: GemmF32MmapNT with A = x^T [N, K]
+    ref = orc.gemm_f32_mmap_nt(8, x.reshape(K, N).T.copy(), raw, N, rows, K).reshape(N, rows).T
+    err = rel_err(y.cpu().numpy().reshape(rows, N), ref)
+    say(f"  rel err {err:.2e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("qtype", [2, 6, 8, 12, 13, 14])
+def test_engine_mmap_dispatch_by_ggml_type(orc, qtype):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import GGMLType, MmapStorage
+
+    eng = ROCmEngine()
+    rows, K = 48, 1024
+    raw = {2: lambda: synth.q4_0(rows, K, 93).raw, 6: lambda: synth.kquant("q5_0", rows, K, 93).raw,
+           8: lambda: synth.gguf_q8_0(rows, K, 93), 12: lambda: synth.kquant("q4_k", rows, K, 93).raw,
+           13: lambda: synth.kquant("q5_k", rows, K, 93).raw, 14: lambda: synth.kquant("q6_k", rows, K, 93).raw}[qtype]()
+    for n in (1, 2):
+        x = synth.x_f32(K * n, 93 + n)
+        ref = orc.gemm_f32_mmap_nt(qtype, x.reshape(K, n).T.copy(), raw, n, rows, K)  # [n, rows]
+        # B side (virtually transposed weight): act [n, K] @ W^T
+        b = Tensor((K, rows), MmapStorage(raw, rows * K, GGMLType(qtype)))
+        got = eng.matmul(devf(x.reshape(K, n).T.copy()), b).cpu().numpy()
+        assert rel_err(got.reshape(n, rows), ref.reshape(n, rows)) <= TOL
+        # A side: W [rows, K] @ x [K, n]
+        a = Tensor((rows, K), MmapStorage(raw, rows * K, GGMLType(qtype)))
+        got = eng.matmul(a, devf(x.reshape(K, n))).cpu().numpy()
+        assert rel_err(got.reshape(rows, n), ref.reshape(n, rows).T) <= TOL

@@ -231,3 +231,52 @@ def test_q5_0_matmul_matches_fp64_bruteforce(orc):
     W = orc.q5_0_dequant(w.raw, rows * K).reshape(rows, K).astype(np.float64)
     ref = W @ x.astype(np.float64)
     assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ---- GGUF mmap ---------------------------------------------------------------
+
+def test_gguf_q8_0_dequant_from_known_codes_is_bit_exact(orc):
+    g = np.random.default_rng(41)
+    q = g.integers(-128, 128, size=(50, 32), dtype=np.int16).astype(np.int8)
+    d = synth.f16_bits(g.standard_normal(50).astype(F) * F(0.02))
+    raw = synth.pack_gguf_q8_0(q, d)
+    assert raw.size == 50 * 34
+    got = orc.gguf_q8_0_dequant(raw, 50 * 32)
+    want = (q.astype(F) * d.view(np.float16).astype(F)[:, None]).astype(F).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # partial last block
+    assert np.array_equal(orc.gguf_q8_0_dequant(raw, 50 * 32 - 7), got[:-7])
+
+
+@pytest.mark.parametrize("qtype,fmt", [(12, "q4_k"), (13, "q5_k"), (14, "q6_k")])
+def test_mmap_gemv_kquants_equal_the_storage_gemvs(orc, qtype, fmt):
+    # GemmF32MmapNT streams super-blocks exactly as GemmF32Q{4,5,6}KNT do.
+    rows, K = 20, 768
+    w = synth.kquant(fmt, rows, K, 42)
+    x = synth.x_f32(K, 42)
+    a = orc.gemm_f32_mmap_nt(qtype, x, w.raw, 1, rows, K)
+    b = orc.gemm_f32_kq_nt(fmt, x, w.raw, 1, rows, K)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [2, 6, 8])
+def test_mmap_gemv_dequantizing_types_match_fp64(orc, qtype):
+    rows, K = 24, 512
+    if qtype == 2:
+        raw = synth.q4_0(rows, K, 43).raw
+        W = orc.q4_dequant(raw, rows * K)
+    elif qtype == 6:
+        raw = synth.kquant("q5_0", rows, K, 43).raw
+        W = orc.q5_0_dequant(raw, rows * K)
+    else:
+        raw = synth.gguf_q8_0(rows, K, 43)
+        W = orc.gguf_q8_0_dequant(raw, rows * K)
+    x = synth.x_f32(2 * K, 43)
+    y = orc.gemm_f32_mmap_nt(qtype, x, raw, 2, rows, K)
+    ref = x.reshape(2, K).astype(np.float64) @ W.reshape(rows, K).astype(np.float64).T
+    assert np.abs(y.reshape(2, rows) - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_mmap_gemv_rejects_types_without_a_kernel(orc):
+    with pytest.raises(ValueError):
+        orc.gemm_f32_mmap_nt(3, np.zeros(32, np.float32), np.zeros(20, np.uint8), 1, 1, 32)

@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q8_gpu_data_offset": (L, [L]),
     "zt_q8_gpu_bytes": (L, [L]),
     "zt_q8_raw_to_gpu": (None, [P, L, P]),
+    "zt_gemm_q8gguf_f32": (I, [P, P, P, I, I, I, L, P]),
+    "zt_dequant_q8gguf_f32": (I, [P, P, L, L, P]),
+    "zt_q8gguf_gpu_data_offset": (L, [L]),
+    "zt_q8gguf_gpu_bytes": (L, [L]),
+    "zt_q8gguf_raw_to_gpu": (None, [P, L, P]),
     "zt_gemm_w4a16_f32": (I, [P, P, P, P, P, I, I, I, I, P]),
     "zt_dequant_w4_f32": (I, [P, P, P, P, L, I, P]),
     "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),

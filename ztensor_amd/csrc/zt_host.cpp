@@ -83,4 +83,21 @@ void zt_q5_0_raw_to_gpu(const void* raw, long nblk, void* out) {
     }
 }
 
+// GGUF Q8_0 (34-byte blocks [fp16 d][32 x int8], tensor/mmap_storage.go:94-96,
+// 265-284) -> [fp16 scales, nblk*2][pad to 16][int8 payloads, nblk*32]: every
+// payload lands 16-byte aligned and the fp16 scales keep 34 bytes per block.
+long zt_q8gguf_gpu_data_offset(long nblk) { return (nblk * 2 + 15) & ~15L; }
+long zt_q8gguf_gpu_bytes(long nblk) { return zt_q8gguf_gpu_data_offset(nblk) + nblk * 32; }
+
+void zt_q8gguf_raw_to_gpu(const void* raw, long nblk, void* out) {
+    const unsigned char* src = static_cast<const unsigned char*>(raw);
+    unsigned char* dst = static_cast<unsigned char*>(out);
+    const long doff = zt_q8gguf_gpu_data_offset(nblk);
+    memset(dst + nblk * 2, 0, (size_t)(doff - nblk * 2));
+    for (long i = 0; i < nblk; i++) {
+        memcpy(dst + 2 * i, src + 34 * i, 2);
+        memcpy(dst + doff + 32 * i, src + 34 * i + 2, 32);
+    }
+}
+
 }  // extern "C"

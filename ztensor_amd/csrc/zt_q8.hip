@@ -23,6 +23,15 @@
 
 namespace zt {
 
+constexpr int kRaw36 = 0, kSep32 = 1, kSep16 = 2;
+
+// Scale of block blk in a separated layout (fp16 scales widen exactly).
+template <int L>
+__device__ __forceinline__ float sep_scale(const uint8_t* base, long blk) {
+    if constexpr (L == kSep16) return h2f(reinterpret_cast<const uint16_t*>(base)[blk]);
+    else return reinterpret_cast<const float*>(base)[blk];
+}
+
 __device__ __forceinline__ float q8_dot_dwords(const uint32_t* d, const float (&xv)[32], float xsum) {
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
@@ -52,8 +61,9 @@ __device__ __forceinline__ void load_x32f(const XT* __restrict__ x, long x_strid
     }
 }
 
-// SEP = separated layout, else raw 36-byte blocks.
-template <bool SEP, int R, bool CONTIG>
+// Layout L: kRaw36 = raw 36-byte blocks; kSep32 = separated, fp32 scales;
+// kSep16 = separated, fp16 scales (GGUF Q8_0 after its upload repack).
+template <int L, int R, bool CONTIG>
 __global__ void __launch_bounds__(512) gemv_q8_kernel(const uint8_t* __restrict__ base, long data_offset,
                                                       const float* __restrict__ x, float* __restrict__ y,
                                                       long xy_stride, int rows, int kb) {
@@ -65,7 +75,6 @@ __global__ void __launch_bounds__(512) gemv_q8_kernel(const uint8_t* __restrict_
     long rbase[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
-    const float* scales = reinterpret_cast<const float*>(base);
     const uint4* data = reinterpret_cast<const uint4*>(base + data_offset);
 
     float acc[R];
@@ -78,12 +87,12 @@ __global__ void __launch_bounds__(512) gemv_q8_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const long blk = rbase[r] + b;
-            if constexpr (SEP) {
+            if constexpr (L != kRaw36) {
                 const uint4 a = ld_stream(&data[2 * blk]);
                 const uint4 c = ld_stream(&data[2 * blk + 1]);
                 d[r][0] = a.x; d[r][1] = a.y; d[r][2] = a.z; d[r][3] = a.w;
                 d[r][4] = c.x; d[r][5] = c.y; d[r][6] = c.z; d[r][7] = c.w;
-                s[r] = scales[blk];
+                s[r] = sep_scale<L>(base, blk);
             } else {
                 const uint32_t* p = reinterpret_cast<const uint32_t*>(base + blk * 36);
                 s[r] = __uint_as_float(__builtin_nontemporal_load(p));
@@ -102,14 +111,14 @@ __global__ void __launch_bounds__(512) gemv_q8_kernel(const uint8_t* __restrict_
     block_reduce_store<R>(acc, red, y, xy_stride, row0, rows);
 }
 
-template <bool SEP, bool CONTIG>
+template <int L, bool CONTIG>
 static void launch_q8(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
                       float* y, long stride, int rows, int kb) {
     switch (R) {
-        case 8: gemv_q8_kernel<SEP, 8, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
-        case 4: gemv_q8_kernel<SEP, 4, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
-        case 2: gemv_q8_kernel<SEP, 2, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
-        default: gemv_q8_kernel<SEP, 1, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        case 8: gemv_q8_kernel<L, 8, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        case 4: gemv_q8_kernel<L, 4, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        case 2: gemv_q8_kernel<L, 2, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
+        default: gemv_q8_kernel<L, 1, CONTIG><<<g, b, 0, st>>>(base, off, x, y, stride, rows, kb); break;
     }
 }
 
@@ -118,7 +127,7 @@ static void launch_q8(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base
 // separated layout, two dwords in the raw 36-byte blocks) and the matching 8
 // activations as two 16-byte loads, so a quad reads its block's 128 bytes of
 // activations contiguously.  R rows per wave, split-K over the waves.
-template <bool SEP, int R>
+template <int L, int R>
 __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __restrict__ base, long data_offset,
                                                            const float* __restrict__ x, float* __restrict__ y,
                                                            int rows, int kb) {
@@ -129,7 +138,6 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
     long rbase[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rbase[r] = (long)min(row0 + r, rows - 1) * kb;
-    const float* scales = reinterpret_cast<const float*>(base);
     const uint2* data = reinterpret_cast<const uint2*>(base + data_offset);
     float acc[R];
 #pragma unroll
@@ -141,12 +149,12 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const long blk = rbase[r] + b;
-            if constexpr (SEP) {
+            if constexpr (L != kRaw36) {
                 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
                 const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(&data[blk * 4 + q]));
                 d[r][0] = v.x;
                 d[r][1] = v.y;
-                s[r] = scales[blk];
+                s[r] = sep_scale<L>(base, blk);
             } else {
                 const uint32_t* p = reinterpret_cast<const uint32_t*>(base + blk * 36);
                 s[r] = __uint_as_float(p[0]);
@@ -175,43 +183,43 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
-template <bool SEP>
+template <int L>
 static void launch_q8_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
                            float* y, int rows, int kb) {
     switch (R) {
-        case 8: gemv_q8_quad_kernel<SEP, 8><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
-        case 4: gemv_q8_quad_kernel<SEP, 4><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
-        case 2: gemv_q8_quad_kernel<SEP, 2><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
-        default: gemv_q8_quad_kernel<SEP, 1><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 8: gemv_q8_quad_kernel<L, 8><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 4: gemv_q8_quad_kernel<L, 4><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 2: gemv_q8_quad_kernel<L, 2><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        default: gemv_q8_quad_kernel<L, 1><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
     }
 }
 
-template <bool SEP>
+template <int L>
 static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N, long data_offset, hipStream_t st) {
     if (M < 0 || N < 0 || K < 0 || K % 32 != 0 || data_offset < 0 || N > 65535) return (int)hipErrorInvalidValue;
     if (M == 0 || N == 0) return (int)hipSuccess;
     if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     const uint8_t* base = static_cast<const uint8_t*>(A);
     if ((uintptr_t)base & 3) return (int)hipErrorInvalidValue;
-    if (SEP && ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
+    if (L != kRaw36 && ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
     if (N == 1) {
         const int nw = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
-        launch_q8_quad<SEP>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
+        launch_q8_quad<L>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
         return (int)hipGetLastError();
     }
     const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));
     const int R = pick_rows_per_wave(M, nwaves, N, 2048);
     dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
-    launch_q8<SEP, false>(R, grid, block, st, base, data_offset, B, C, N, M, kb);
+    launch_q8<L, false>(R, grid, block, st, base, data_offset, B, C, N, M, kb);
     return (int)hipGetLastError();
 }
 
 // ------------------------------------------------------------ dequantize
 
-template <bool SEP>
+template <int L>
 __global__ void dequant_q8_kernel(const uint8_t* __restrict__ base, long data_offset, float* __restrict__ out,
                                   long nelem) {
     const long blk = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -219,8 +227,8 @@ __global__ void dequant_q8_kernel(const uint8_t* __restrict__ base, long data_of
     if (blk >= nblk) return;
     float scale;
     const uint8_t* q;
-    if constexpr (SEP) {
-        scale = reinterpret_cast<const float*>(base)[blk];
+    if constexpr (L != kRaw36) {
+        scale = sep_scale<L>(base, blk);
         q = base + data_offset + blk * 32;
     } else {
         scale = *reinterpret_cast<const float*>(base + blk * 36);
@@ -232,13 +240,13 @@ __global__ void dequant_q8_kernel(const uint8_t* __restrict__ base, long data_of
     for (int j = 0; j < n; j++) o[j] = (float)(int8_t)q[j] * scale;
 }
 
-template <bool SEP>
+template <int L>
 static int dequant_q8(const void* A, float* out, long nelem, long data_offset, hipStream_t st) {
     if (nelem < 0 || data_offset < 0) return (int)hipErrorInvalidValue;
     if (nelem == 0) return (int)hipSuccess;
     if ((uintptr_t)A & 3) return (int)hipErrorInvalidValue;
     const long nblk = (nelem + 31) / 32;
-    dequant_q8_kernel<SEP><<<ceil_div(nblk, 256), 256, 0, st>>>(static_cast<const uint8_t*>(A), data_offset, out,
+    dequant_q8_kernel<L><<<ceil_div(nblk, 256), 256, 0, st>>>(static_cast<const uint8_t*>(A), data_offset, out,
                                                                  nelem);
     return (int)hipGetLastError();
 }
@@ -265,20 +273,20 @@ ZT_EXPORT long zt_q8_gpu_data_offset(long nblk) { return (nblk * 4 + 15) & ~15L;
 ZT_EXPORT long zt_q8_gpu_bytes(long nblk) { return zt_q8_gpu_data_offset(nblk) + nblk * 32; }
 
 ZT_EXPORT int zt_gemm_q8_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, hipStream_t stream) {
-    return gemm_q8<false>(A_q8, B, C, M, K, N, 0, stream);
+    return gemm_q8<kRaw36>(A_q8, B, C, M, K, N, 0, stream);
 }
 
 ZT_EXPORT int zt_gemm_q8sep_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, long data_offset,
                                 hipStream_t stream) {
-    return gemm_q8<true>(A_q8, B, C, M, K, N, data_offset, stream);
+    return gemm_q8<kSep32>(A_q8, B, C, M, K, N, data_offset, stream);
 }
 
 ZT_EXPORT int zt_dequant_q8_f32(const void* A_q8, float* out, long nelem, hipStream_t stream) {
-    return dequant_q8<false>(A_q8, out, nelem, 0, stream);
+    return dequant_q8<kRaw36>(A_q8, out, nelem, 0, stream);
 }
 
 ZT_EXPORT int zt_dequant_q8sep_f32(const void* A_q8, float* out, long nelem, long data_offset, hipStream_t stream) {
-    return dequant_q8<true>(A_q8, out, nelem, data_offset, stream);
+    return dequant_q8<kSep32>(A_q8, out, nelem, data_offset, stream);
 }
 
 ZT_EXPORT int zt_q8_repack(const void* raw, void* out, long nblk, hipStream_t stream) {
@@ -288,4 +296,16 @@ ZT_EXPORT int zt_q8_repack(const void* raw, void* out, long nblk, hipStream_t st
                                                               static_cast<uint8_t*>(out), nblk,
                                                               zt_q8_gpu_data_offset(nblk));
     return (int)hipGetLastError();
+}
+
+// GGUF Q8_0 (tensor/mmap_storage.go:265-284: 34-byte blocks [fp16 d][32 x
+// int8]) over its separated upload layout [fp16 d, nblk*2][pad 16][int8,
+// nblk*32]: data_offset = zt_q8gguf_gpu_data_offset(nblk).
+ZT_EXPORT int zt_gemm_q8gguf_f32(const void* A, const float* B, float* C, int M, int K, int N, long data_offset,
+                                 hipStream_t stream) {
+    return gemm_q8<kSep16>(A, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_q8gguf_f32(const void* A, float* out, long nelem, long data_offset, hipStream_t stream) {
+    return dequant_q8<kSep16>(A, out, nelem, data_offset, stream);
 }

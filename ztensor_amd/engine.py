@@ -32,6 +32,8 @@ from .storage import (
     GPTQStorage,
     GPUBuffer,
     IQ4NLStorage,
+    MmapStorage,
+    GGMLType,
     Q4KStorage,
     Q4Storage,
     Q5_0Storage,
@@ -138,6 +140,13 @@ class ROCmEngine:
                 if s.gpu_ptr() is None:  # raw super-blocks, as compute/gpu_engine.go:817-874
                     s.set_gpu_ptr(GPUBuffer(self._to_dev(s.raw), s.raw.size, self.device.index or 0))
                     n += 1
+            elif isinstance(s, MmapStorage):
+                if s.gpu_ptr() is None:  # compute/gpu_engine.go:3072-3100 mmapDevicePtr, plus the repacks
+                    buf, offs = s.device_layout()
+                    s.set_gpu_ptr(GPUBuffer(self._to_dev(buf), buf.size, self.device.index or 0,
+                                            offs.get("data_offset", 0)))
+                    s._gpu_offsets = offs  # type: ignore[attr-defined]
+                    n += 1
             elif isinstance(s, Q5_0Storage):
                 if s.gpu_ptr() is None:  # RawBytesGPU, as compute/gpu_engine.go:876-893
                     buf = s.raw_bytes_gpu()
@@ -191,6 +200,8 @@ class ROCmEngine:
         self.upload_weights([s])
         c = torch.empty((rows, n), dtype=torch.float32, device=self.device)
         buf = s.gpu_ptr()
+        if isinstance(s, MmapStorage):
+            return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
             if x.dtype == torch.float32:
                 self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
@@ -245,6 +256,41 @@ class ROCmEngine:
                 torch.matmul(w, x.reshape(k, n), out=c)
         else:
             raise TypeError(f"matmul: {type(s).__name__} is not a quantized weight storage")
+        return c
+
+    def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
+                    c: torch.Tensor) -> torch.Tensor:
+        """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
+        the GGML type picks the kernel.  Q8_0 runs on its own repacked layout
+        (the reference passes the 34-byte blocks to the 36-byte kernel,
+        compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
+        its CPU engine, runs on the Q5_0 GEMV; types without a quantized
+        kernel (F32, F16, BF16, Q4_1, Q5_1) raise."""
+        if x.dtype != torch.float32:
+            raise TypeError("MmapStorage matmul takes fp32 activations")
+        q, p, offs = s.qtype, _p(buf.tensor), s._gpu_offsets
+        if q == GGMLType.Q4_0:
+            self.gemm_q4_f32(p, _p(x), _p(c), rows, k, n, offs["data_offset"])
+        elif q == GGMLType.Q8_0:
+            self.lib.call("zt_gemm_q8gguf_f32", p, _p(x), _p(c), rows, k, n, offs["data_offset"], self._s)
+        elif q == GGMLType.Q5_0:
+            xt = x.reshape(k, n).t().contiguous()
+            ct = torch.empty((n, rows), dtype=torch.float32, device=self.device)
+            for j in range(n):
+                self.gemv_q5_0_f32(p, _p(xt[j]), _p(ct[j]), rows, k, offs["qh_offset"], offs["qs_offset"])
+            c.copy_(ct.t())
+        elif q in (GGMLType.Q4_K, GGMLType.Q5_K, GGMLType.Q6_K):
+            kind = {GGMLType.Q4_K: Q4KStorage, GGMLType.Q5_K: Q5KStorage, GGMLType.Q6_K: Q6KStorage}[q]
+            if k % 256 != 0:
+                raise ValueError(f"{q.name} matmul needs K % 256 == 0")
+            if n == 1:
+                self.lib.call(_KQ_GEMV[kind], p, _p(x), _p(c), rows, k, self._s)
+            else:
+                w = torch.empty((rows, k), dtype=torch.float32, device=self.device)
+                self.lib.call(_KQ_DEQUANT[kind], p, _p(w), rows, k, self._s)
+                torch.matmul(w, x.reshape(k, n), out=c)
+        else:
+            raise TypeError(f"GGML type {q.name} has no quantized GEMV on this path")
         return c
 
     def matmul_w4a16(self, a: Tensor, b: Tensor) -> torch.Tensor:

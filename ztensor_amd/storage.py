@@ -16,6 +16,8 @@ caller of tensor.Q4Storage & co. finds the same surface:
   Q5KStorage     tensor/quantized_kquant.go:552-636
   Q6KStorage     tensor/quantized_kquant.go:385-505 (MergeQ6KStorage -> merge_q6k_storage)
   Q5_0Storage    tensor/quantized_q5_0.go:47-184 (RawBytesGPU, Q5_0GPUQhOffset/QsOffset)
+  MmapStorage    tensor/mmap_storage.go:16-189 (GGUF tensors by GGML type; device_layout adds the
+                 repacks the engine uploads)
 
 Dequantization on the host is not offered here on purpose: the product path
 dequantizes on the GPU (zt_dequant_*), and the CPU restatement used to check
@@ -25,6 +27,7 @@ from __future__ import annotations
 
 import ctypes as C
 from dataclasses import dataclass, field
+from enum import IntEnum
 from typing import Any
 
 import numpy as np
@@ -392,6 +395,104 @@ class Q5_0Storage(_GPUPtrMixin):
     def gpu_qs_offset(self) -> int:
         """Q5_0GPUQsOffset (tensor/quantized_q5_0.go:158-165)."""
         return _lib.load().zt_q5_0_gpu_qs_offset(self.num_blocks())
+
+
+class GGMLType(IntEnum):
+    """tensor/mmap_storage.go:16-30."""
+
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
+    Q8_0 = 8
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+    BF16 = 30
+
+
+# (values per block, bytes per block), tensor/mmap_storage.go:85-119 mmapByteSize
+_GGML_BLOCK = {
+    GGMLType.F32: (1, 4), GGMLType.F16: (1, 2), GGMLType.BF16: (1, 2),
+    GGMLType.Q4_0: (32, 18), GGMLType.Q8_0: (32, 34), GGMLType.Q4_1: (32, 20),
+    GGMLType.Q5_0: (32, 22), GGMLType.Q5_1: (32, 24),
+    GGMLType.Q4_K: (256, 144), GGMLType.Q5_K: (256, 176), GGMLType.Q6_K: (256, 210),
+}
+
+
+def mmap_byte_size(qtype: int, num_elements: int) -> int:
+    """mmapByteSize (tensor/mmap_storage.go:85-119)."""
+    try:
+        vals, nbytes = _GGML_BLOCK[GGMLType(qtype)]
+    except (ValueError, KeyError):
+        raise ValueError(f"unsupported GGML type {qtype}") from None
+    return (num_elements + vals - 1) // vals * nbytes
+
+
+class MmapStorage(_GPUPtrMixin):
+    """A GGUF tensor's raw bytes (a view of the mmap'd file) with its GGML type."""
+
+    def __init__(self, data: np.ndarray, length: int, qtype: int):
+        """NewMmapStorage (tensor/mmap_storage.go:59-83): length > 0, data
+        non-empty and at least mmapByteSize long; the storage keeps exactly
+        that many bytes."""
+        if length <= 0:
+            raise ValueError(f"mmap storage: length must be positive, got {length}")
+        data = np.asarray(data, np.uint8).reshape(-1)
+        if data.size == 0:
+            raise ValueError("mmap storage: data must not be empty")
+        need = mmap_byte_size(qtype, length)
+        if data.size < need:
+            raise ValueError(f"mmap storage: data too short for {length} elements of type {int(qtype)}: "
+                             f"need {need} bytes, got {data.size}")
+        self.data = data[:need]
+        self.len = length
+        self.qtype = GGMLType(qtype)
+        self._gpu = None
+
+    def byte_size(self) -> int:
+        return self.data.size
+
+    def raw_bytes(self) -> np.ndarray:
+        return self.data
+
+    def num_blocks(self) -> int:
+        vals, _ = _GGML_BLOCK[self.qtype]
+        return (self.len + vals - 1) // vals
+
+    def raw_bytes_gpu(self) -> np.ndarray:
+        """RawBytesGPU (tensor/mmap_storage.go:170-189): Q4_0 in the separated
+        layout, every other type unchanged."""
+        if self.qtype != GGMLType.Q4_0:
+            return self.data
+        lib = _lib.load()
+        nb = self.data.size // 18
+        out = np.empty(lib.zt_q4_gpu_bytes(nb), np.uint8)
+        lib.zt_q4_raw_to_gpu(_ptr(self.data), nb, _ptr(out))
+        return out
+
+    def device_layout(self) -> tuple[np.ndarray, dict]:
+        """The bytes this library's kernels read and their offsets: Q4_0 as
+        RawBytesGPU; Q8_0 repacked to [fp16 scales][pad][int8 payloads]
+        (zt_q8gguf_raw_to_gpu); Q5_0 as Q5_0Storage.RawBytesGPU; the K-quants
+        unchanged."""
+        lib = _lib.load()
+        nb = self.num_blocks()
+        if self.qtype == GGMLType.Q4_0:
+            return self.raw_bytes_gpu(), {"data_offset": lib.zt_q4_gpu_data_offset(nb)}
+        if self.qtype == GGMLType.Q8_0:
+            out = np.empty(lib.zt_q8gguf_gpu_bytes(nb), np.uint8)
+            lib.zt_q8gguf_raw_to_gpu(_ptr(self.data), nb, _ptr(out))
+            return out, {"data_offset": lib.zt_q8gguf_gpu_data_offset(nb)}
+        if self.qtype == GGMLType.Q5_0:
+            out = np.empty(lib.zt_q5_0_gpu_bytes(nb), np.uint8)
+            lib.zt_q5_0_raw_to_gpu(_ptr(self.data), nb, _ptr(out))
+            return out, {"qh_offset": lib.zt_q5_0_gpu_qh_offset(nb), "qs_offset": lib.zt_q5_0_gpu_qs_offset(nb)}
+        if self.qtype in (GGMLType.Q4_K, GGMLType.Q5_K, GGMLType.Q6_K):
+            return self.data, {}
+        raise TypeError(f"GGML type {self.qtype.name} has no quantized GEMV on this path")
 
 
 @dataclass

@@ -185,6 +185,26 @@ def pack_q5_0(q: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def pack_gguf_q8_0(q: np.ndarray, d_bits: np.ndarray) -> np.ndarray:
+    """int8 [nblk, 32] and fp16 scale bits [nblk] -> 34-byte GGUF Q8_0 blocks
+    (tensor/mmap_storage.go:94-96, 265-284): [fp16 d LE][32 x int8]."""
+    q = q.reshape(-1, 32).astype(np.int8)
+    nblk = q.shape[0]
+    out = np.empty((nblk, 34), np.uint8)
+    out[:, 0:2] = d_bits.astype("<u2").reshape(nblk, 1).view(np.uint8)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def gguf_q8_0(rows: int, K: int, seed: int) -> np.ndarray:
+    """GGUF Q8_0 weights [rows, K]: int8 U[-127,127], fp16 d |N(0,1)|*0.02."""
+    g = rng(seed)
+    nblk = rows * K // 32
+    q = g.integers(-127, 128, size=(nblk, 32), dtype=np.int16).astype(np.int8)
+    d = f16_bits(np.abs(g.standard_normal(nblk, dtype=np.float32)) * np.float32(0.02))
+    return pack_gguf_q8_0(q, d)
+
+
 # ------------------------------------------------------------ workloads
 
 
@@ -333,6 +353,8 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
     if fmt == "w4a16":
         ng = rows * K // group
         return rows * K // 2 + 2 * ng * (2 if zeros else 1) + 2 * K * N + 4 * rows * N
+    if fmt == "q8_0_gguf":
+        return nblk * 34 + 4 * K * N + 4 * rows * N
     if fmt in KQ_BLOCK:
         vals, nbytes = KQ_BLOCK[fmt]
         return rows * K // vals * nbytes + 4 * K * N + 4 * rows * N
