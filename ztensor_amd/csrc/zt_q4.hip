@@ -199,6 +199,97 @@ __global__ void __launch_bounds__(512) gemv_quad_kernel(const uint16_t* __restri
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+
+// Q4_0 batch-1 GEMV where every wave does a fixed number S of 16-block
+// steps per row (the quad mapping of gemv_quad_kernel), with every load of
+// all S steps issued before any arithmetic.  Leaner per wave, which is what
+// matters when waves are this short:
+//  * buffer loads: the row offsets are wave-uniform and go in the scalar
+//    offset, so no per-lane 64-bit address arithmetic; lanes past the last
+//    block get an out-of-range offset and read zeros;
+//  * the activations are pre-scaled once by 2^24 / 2^20, so each row is one
+//    v_fma_mix chain started at -8*sum(x), and the fp16 block scale enters
+//    v_fma_mix directly.
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __restrict__ scales,
+                                                             const uint32_t* __restrict__ data,
+                                                             const float* __restrict__ x, float* __restrict__ y,
+                                                             int rows, int kb) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
+    uint32_t w[S][R], s[S][R];
+    u32x4 xa[S], xb[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+        const uint32_t voff = ok ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, row * (uint32_t)kb * 16u, 2);  // nontemporal
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t soff = b < kb ? (uint32_t)(b * 2) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            s[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, row * (uint32_t)kb * 2u, 0);
+        }
+        const uint32_t xo = b < kb ? (uint32_t)(b * 128 + q * 16) : 0x80000000u;
+        xa[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);       // values 4q .. 4q+3
+        xb[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 64, 0, 0);  // values 16+4q ..
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const float l0 = __uint_as_float(xa[t].x), l1 = __uint_as_float(xa[t].y), l2 = __uint_as_float(xa[t].z),
+                    l3 = __uint_as_float(xa[t].w);
+        const float h0 = __uint_as_float(xb[t].x), h1 = __uint_as_float(xb[t].y), h2 = __uint_as_float(xb[t].z),
+                    h3 = __uint_as_float(xb[t].w);
+        const float c0 = -8.0f * (((l0 + l1) + (l2 + l3)) + ((h0 + h1) + (h2 + h3)));
+        const float pl0 = l0 * 16777216.0f, pl1 = l1 * 16777216.0f, pl2 = l2 * 16777216.0f, pl3 = l3 * 16777216.0f;
+        const float ph0 = h0 * 1048576.0f, ph1 = h1 * 1048576.0f, ph2 = h2 * 1048576.0f, ph3 = h3 * 1048576.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[t][r], d8 = d >> 8;
+            const half2v m0 = as_half2(d & 0x000F000Fu), m1 = as_half2(d & 0x00F000F0u);
+            const half2v m2 = as_half2(d8 & 0x000F000Fu), m3 = as_half2(d8 & 0x00F000F0u);
+            float v = __builtin_fmaf((float)m0.x, pl0, c0);
+            v = __builtin_fmaf((float)m1.x, ph0, v);
+            v = __builtin_fmaf((float)m2.x, pl1, v);
+            v = __builtin_fmaf((float)m3.x, ph1, v);
+            v = __builtin_fmaf((float)m0.y, pl2, v);
+            v = __builtin_fmaf((float)m1.y, ph2, v);
+            v = __builtin_fmaf((float)m2.y, pl3, v);
+            v = __builtin_fmaf((float)m3.y, ph3, v);
+            acc[r] = __builtin_fmaf((float)as_half2(s[t][r]).x, v, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S>
+static void launch_q4_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
+                            const float* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_q4_steps_kernel<S, 8><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 4: gemv_q4_steps_kernel<S, 4><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 2: gemv_q4_steps_kernel<S, 2><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        default: gemv_q4_steps_kernel<S, 1><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+    }
+}
+
 template <Fmt F, class XT>
 static void launch_quad(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
                         const XT* x, float* y, int rows, int kb) {
@@ -396,6 +487,22 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
     if (N == 1) {
         const int nwaves = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
+        if constexpr (F == Fmt::Q4_0 && sizeof(XT) == 4) {
+            // A fixed S steps per wave with all loads up front: S = 1 for K <= 4096,
+            // S = 2 with up to 16 waves for K <= 16384 (measured best at K = 8192 and
+            // 14336); longer rows loop.  Buffer offsets are 32-bit (data region < 2 GiB).
+            const uint32_t* dt = reinterpret_cast<const uint32_t*>(data);
+            if ((long)M * kb * 16 < 0x7fffffffL && kb <= 512) {
+                const int S = kb <= 128 ? 1 : 2;
+                const int nw = ceil_div(kb, 16 * S);
+                const int Rs = pick_rows_per_wave(M, nw, 1, 2048);
+                if (S == 1)
+                    launch_q4_steps<1>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
+                else
+                    launch_q4_steps<2>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
+                return (int)hipGetLastError();
+            }
+        }
         launch_quad<F, XT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, sc,
                            reinterpret_cast<const uint32_t*>(data), B, C, M, kb);
         return (int)hipGetLastError();
