@@ -217,6 +217,100 @@ static void launch_w4a16_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint3
     }
 }
 
+
+// Batch-1 W4A16 with a fixed S steps of 16 chunks per wave (the quad
+// mapping of w4a16_quad_kernel) for K <= 16384.  Every load of all S steps -
+// weights, the rows' (scale, zero) pairs of each step's group and the
+// activations - is issued before any arithmetic, so a wave waits for one
+// memory round trip.  Buffer loads take the wave-uniform row offsets as
+// scalar offsets; lanes past the last chunk read zeros through out-of-range
+// offsets.
+template <int S, int R>
+__global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __restrict__ packed,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint16_t* __restrict__ zeros,
+                                                           const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                           int rows, int nchunk, int chunks_per_group) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int ngroups = nchunk / chunks_per_group;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)packed, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, zeros ? 0x7fffffff : 0,
+                                                                        0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nchunk * 64, 0x00020000);
+    uint32_t w[S][R], sc[S][R], zr[S][R];
+    u32x4 xv[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = c < nchunk;
+        const uint32_t voff = ok ? (uint32_t)(c * 16 + q * 4) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rw, voff, row * (uint32_t)nchunk * 16u, 2);  // nontemporal
+        }
+        xv[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (uint32_t)(c * 64 + q * 16) : 0x80000000u, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t goff = c < nchunk ? (uint32_t)((c / chunks_per_group) * 2) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t rowg = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)ngroups * 2u;
+            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, goff, rowg, 0);
+            // no zeros array: the buffer has no records and reads 0; zero-point 8 is applied below
+            zr[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rz, goff, rowg, 0);
+        }
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const half2v x01 = as_h2(xv[t].x), x23 = as_h2(xv[t].y), x45 = as_h2(xv[t].z), x67 = as_h2(xv[t].w);
+        float xsum = __builtin_amdgcn_fdot2(x01, as_h2(0x3c003c00u), 0.0f, false);
+        xsum = __builtin_amdgcn_fdot2(x23, as_h2(0x3c003c00u), xsum, false);
+        xsum = __builtin_amdgcn_fdot2(x45, as_h2(0x3c003c00u), xsum, false);
+        xsum = __builtin_amdgcn_fdot2(x67, as_h2(0x3c003c00u), xsum, false);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[t][r], d8 = d >> 8;
+            const half2v m0 = as_h2(d & 0x000F000Fu);   // weights 0, 4  (q * 2^-24)
+            const half2v m1 = as_h2(d & 0x00F000F0u);   // weights 1, 5  (q * 2^-20)
+            const half2v m2 = as_h2(d8 & 0x000F000Fu);  // weights 2, 6
+            const half2v m3 = as_h2(d8 & 0x00F000F0u);  // weights 3, 7
+            float sa = (float)m0.x * (float)x01.x;
+            float sb = (float)m1.x * (float)x01.y;
+            sa = __builtin_fmaf((float)m0.y, (float)x45.x, sa);
+            sb = __builtin_fmaf((float)m1.y, (float)x45.y, sb);
+            sa = __builtin_fmaf((float)m2.x, (float)x23.x, sa);
+            sb = __builtin_fmaf((float)m3.x, (float)x23.y, sb);
+            sa = __builtin_fmaf((float)m2.y, (float)x67.x, sa);
+            sb = __builtin_fmaf((float)m3.y, (float)x67.y, sb);
+            const float z = zeros ? (float)as_h2(zr[t][r]).x : 8.0f;
+            const float tq = __builtin_fmaf(sa, 16777216.0f, __builtin_fmaf(sb, 1048576.0f, -z * xsum));
+            acc[r] = __builtin_fmaf((float)as_h2(sc[t][r]).x, tq, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S>
+static void launch_w4a16_steps(int R, dim3 g, dim3 b, hipStream_t st, const uint32_t* w, const uint16_t* s,
+                               const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+    switch (R) {
+        case 8: w4a16_steps_kernel<S, 8><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
+        case 4: w4a16_steps_kernel<S, 4><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
+        case 2: w4a16_steps_kernel<S, 2><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
+        default: w4a16_steps_kernel<S, 1><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
+    }
+}
+
 // ------------------------------------------------------------ MFMA GEMM
 //
 // C[rows, N] = W[rows, K] x X[K, N] for 4 <= N <= 16, N % 4 == 0, K and the
@@ -390,6 +484,19 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     }
     const int nchunk = K / 32;
     if (N == 1) {
+        if ((long)M * nchunk * 16 < 0x7fffffffL && nchunk <= 512) {
+            // fixed steps: S = 1 for K <= 4096, else 2 with up to 16 waves
+            const int S = nchunk <= 128 ? 1 : 2;
+            const int nw = ceil_div(nchunk, 16 * S);
+            const int R = pick_rows_per_wave(M, nw, 1, 2048);
+            const dim3 g(ceil_div(M, R)), b(nw * kWave);
+            const uint32_t* w = static_cast<const uint32_t*>(W_packed);
+            if (S == 1)
+                launch_w4a16_steps<1>(R, g, b, stream, w, scales, zeros, B, C, M, nchunk, group_size / 32);
+            else
+                launch_w4a16_steps<2>(R, g, b, stream, w, scales, zeros, B, C, M, nchunk, group_size / 32);
+            return (int)hipGetLastError();
+        }
         const int nw = min(8, ceil_div(nchunk, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
         launch_w4a16_quad(R, dim3(ceil_div(M, R)), dim3(nw * kWave), stream, static_cast<const uint32_t*>(W_packed),
