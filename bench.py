@@ -221,7 +221,7 @@ def run_headline(args) -> dict:
         if name == "gate":
             dom = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
                    "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
-                   "kernel": "gemv_quad_kernel<Q4_0, R=8, float> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
+                   "kernel": "gemv_q4_steps_kernel<S=1, R=8> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
                    "bytes_per_launch": m.bytes, "us_per_launch": round(us, 3)}
         log(f"bench: {name:5s} K={K:5d} N={rows:5d}: {us:7.2f} us  {gbs:7.1f} GB/s")
 
