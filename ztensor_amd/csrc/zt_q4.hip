@@ -279,6 +279,73 @@ __global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __r
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// IQ4_NL batch-1 GEMV with fp16 activations.  The quad mapping of
+// gemv_quad_kernel (lane q of a quad holds dword q of a block: elements
+// 8q .. 8q+7, byte j = elements 8q+2j (low nibble) and 8q+2j+1 (high)),
+// with a 1 KB LDS table from a data byte to the fp16 pair (T[low], T[high]).
+// The codebook values are integers |T| <= 127, exact in fp16, and the pair
+// lines up with the activation dword (x[8q+2j], x[8q+2j+1]), so each byte is
+// one ds_read_b32 and one v_dot2_f32_f16 (products exact in fp32, fp32 sums).
+// Buffer loads take the wave-uniform row offsets as scalar offsets; lanes
+// past the last block read zeros through out-of-range offsets.
+template <int R>
+__global__ void __launch_bounds__(1024) gemv_iq4nl_h16_kernel(const uint16_t* __restrict__ scales,
+                                                              const uint32_t* __restrict__ data,
+                                                              const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                              int rows, int kb) {
+    __shared__ float red[16 * R];
+    __shared__ uint32_t tbl[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 64, 0x00020000);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
+        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    __syncthreads();
+    uint32_t rofs[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rofs[r] = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)kb;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int b0 = wave * 16; b0 < kb; b0 += nwaves * 16) {
+        const int b = b0 + (lane >> 2);
+        const bool ok = b < kb;
+        const uint32_t voff = ok ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+        const uint32_t soff = ok ? (uint32_t)(b * 2) : 0x80000000u;
+        uint32_t w[R], s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) w[r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, rofs[r] * 16u, 2);  // nontemporal
+#pragma unroll
+        for (int r = 0; r < R; r++) s[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, rofs[r] * 2u, 0);
+        const u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (uint32_t)(b * 64 + q * 16) : 0x80000000u, 0, 0);
+        const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v = __builtin_amdgcn_fdot2(as_half2(tbl[(w[r] >> (8 * j)) & 0xffu]), as_half2(xx[j]), v, false);
+            acc[r] = __builtin_fmaf(h2f(s[r]), v, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+static void launch_iq4nl_h16(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
+                             const uint16_t* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_iq4nl_h16_kernel<8><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 4: gemv_iq4nl_h16_kernel<4><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 2: gemv_iq4nl_h16_kernel<2><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        default: gemv_iq4nl_h16_kernel<1><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+    }
+}
+
 template <int S>
 static void launch_q4_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
                             const float* x, float* y, int rows, int kb) {
@@ -500,6 +567,18 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
                     launch_q4_steps<1>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
                 else
                     launch_q4_steps<2>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
+                return (int)hipGetLastError();
+            }
+        }
+        if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
+            // Waves per workgroup chosen so the grid holds about 8192 waves
+            // (4 .. 16, at most one per 16 blocks of a row).
+            if ((long)M * kb * 16 < 0x7fffffffL) {
+                const int Ri = pick_rows_per_wave(M, 16, 1, 2048);
+                const int groups = ceil_div(M, Ri);
+                const int nw = min(min(16, max(4, ceil_div(8192, groups))), ceil_div(kb, 16));
+                launch_iq4nl_h16(Ri, dim3(groups), dim3(nw * kWave), st, sc, reinterpret_cast<const uint32_t*>(data),
+                                 reinterpret_cast<const uint16_t*>(B), C, M, kb);
                 return (int)hipGetLastError();
             }
         }
