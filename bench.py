@@ -312,6 +312,7 @@ SUITE = {
     "q8_0_raw": ("q8_0_raw", [(4096, 4096), (14336, 4096)], [1]),
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
+    "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
@@ -361,6 +362,21 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         x = dev(synth.x_f16(K * N, seed))
         fn = lambda wb, y: lib.zt_gemm_w4a16_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
                                                  y.data_ptr(), rows, K, N, 128, s)
+        nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
+    elif fmt == "w4a16t":
+        # the tiled upload layout (zt_w4a16_tile), built once outside the timing
+        w = synth.w4a16(rows, K, seed)
+        p, sc, zr = dev(w.packed), dev(w.scales), dev(w.zeros)
+        wt = torch.empty(lib.zt_w4a16_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        sz = torch.empty(lib.zt_w4a16_sz_bytes(rows, K, 128), dtype=torch.uint8, device="cuda")
+        if lib.zt_w4a16_tile(p.data_ptr(), sc.data_ptr(), zr.data_ptr(), rows, K, 128, wt.data_ptr(), sz.data_ptr(),
+                             s) != 0:
+            raise RuntimeError("zt_w4a16_tile failed")
+        del p, sc, zr
+        wbufs = [wt, sz]
+        x = dev(synth.x_f16(K * N, seed))
+        fn = lambda wb, y: lib.zt_gemm_w4a16t_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows,
+                                                  K, N, 128, s)
         nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
     elif fmt == "ternary_i8":
         t = synth.ternary(rows, K, seed)

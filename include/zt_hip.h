@@ -147,6 +147,33 @@ int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, const uint16
 int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,
                       int group_size, zt_stream_t stream);
 
+/* Tiled upload layout for the small-batch path of the same MatMulW4A16
+ * (compute/w4a16.go:137-143).  The reference uploads W4A16 weights as
+ * they are stored; this layout is built once at upload, like the separated
+ * Q8_0 layout, and serves N in {4, 8, 12, 16}:
+ *   W_tiled: each 16-row x 128-K tile is 1 KB, tile (rt, u) at byte
+ *   (rt * K/128 + u) * 1024; 16-byte piece l = 16 g + i holds row 16 rt + i,
+ *   K 128 u + 32 g .. +32, the same bytes as in W_packed; rows past M, to
+ *   the next multiple of 16, are zero (zt_w4a16_tiled_bytes bytes);
+ *   sz: uint32 [K/group_size][M], fp16 scale in the low half and fp16 zero
+ *   (8.0 when zeros is NULL) in the high half (zt_w4a16_sz_bytes bytes).
+ * zt_w4a16_tile builds both on the device from the zt_gemm_w4a16_f32
+ * operands: K % 128 == 0, group_size % 32 == 0, K % group_size == 0,
+ * W_packed and W_tiled 16-byte aligned, else InvalidValue.  The size
+ * helpers return -1 for shapes the layout does not take. */
+long zt_w4a16_tiled_bytes(int M, int K);
+long zt_w4a16_sz_bytes(int M, int K, int group_size);
+int zt_w4a16_tile(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, int M, int K, int group_size,
+                  void* W_tiled, uint32_t* sz, zt_stream_t stream);
+/* C[M, N] = dequant(W) B on the tiled layout, the result of
+ * zt_gemm_w4a16_f32 within the fp32 tolerance: N in {4, 8, 12, 16},
+ * K % 128 == 0, group_size % 128 == 0, B fp16 [K, N] 16-byte aligned,
+ * M * K/group_size < 2^29, else InvalidValue.  Writes C with a zero fill
+ * and fp32 atomic adds when K is split across workgroups, so the last bits
+ * of C can vary from run to run. */
+int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* B, float* C, int M, int K, int N,
+                       int group_size, zt_stream_t stream);
+
 /* ---- Ternary ----------------------------------------------------------- */
 
 /* Replaces ternary_gemv_f32 (internal/cuda/kernels/ternary_gemv.cu:85-99),

@@ -169,3 +169,19 @@ def test_mmap_storage_validates_like_the_reference():
     assert np.array_equal(m.raw_bytes_gpu(), Q4Storage.from_raw(w.raw, 192).raw_bytes_gpu())
     with pytest.raises(TypeError):
         MmapStorage(np.zeros(40, np.uint8), 32, GGMLType.Q4_1).device_layout()
+
+
+def test_w4a16_tiled_layout_sizes():
+    """The tiled W4A16 layout's byte counts (host helpers, no GPU): rows
+    padded to a multiple of 16, K a multiple of 128, one dword per
+    (group, row); shapes the layout does not take return -1."""
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    assert lib.zt_w4a16_tiled_bytes(8192, 8192) == 8192 * 4096
+    assert lib.zt_w4a16_tiled_bytes(17, 256) == 32 * 128
+    assert lib.zt_w4a16_tiled_bytes(1, 128) == 16 * 64
+    assert lib.zt_w4a16_tiled_bytes(4, 96) == -1
+    assert lib.zt_w4a16_sz_bytes(8192, 8192, 128) == 8192 * 64 * 4
+    assert lib.zt_w4a16_sz_bytes(17, 256, 64) == 17 * 4 * 4
+    assert lib.zt_w4a16_sz_bytes(4, 96, 64) == -1

@@ -49,6 +49,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q8gguf_raw_to_gpu": (None, [P, L, P]),
     "zt_gemm_w4a16_f32": (I, [P, P, P, P, P, I, I, I, I, P]),
     "zt_dequant_w4_f32": (I, [P, P, P, P, L, I, P]),
+    "zt_w4a16_tiled_bytes": (L, [I, I]),
+    "zt_w4a16_sz_bytes": (L, [I, I, I]),
+    "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),
+    "zt_gemm_w4a16t_f32": (I, [P, P, P, P, I, I, I, I, P]),
     "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),
     "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
     "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),

@@ -522,3 +522,255 @@ ZT_EXPORT int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, co
                                                                   out, nchunk, group_size / 32);
     return (int)hipGetLastError();
 }
+
+// ------------------------------------------------------------ tiled layout
+//
+// An upload-time repack of the W4A16 weights for the small-batch MFMA GEMM.
+// The row-major packed layout puts the 16 rows of an MFMA tile 0.5 K bytes
+// apart, so a load instruction in the A-operand lane order (lane = row) reads
+// 16 rows x 64 bytes; the tiled layout stores each 16-row x 128-K tile as one
+// contiguous 1 KB block in exactly that lane order:
+//   tile (rt, u) at byte ((rt * K/128) + u) * 1024; lane l = 16 g + i holds the
+//   16 packed bytes of row 16 rt + i, K range 128 u + 32 g .. +32 (the same
+//   bytes, in the same nibble order, as the row-major layout);
+// rows past M (to the next multiple of 16) are zero.  The group scale and
+// zero of (row, group) are packed as one dword, fp16 scale in the low half
+// and fp16 zero in the high half (8.0 without a zeros array), laid out
+// [group][row] so that a tile's 16 rows are 64 contiguous bytes.  A wave's
+// weight load is then one contiguous 1 KB block.
+
+__global__ void w4t_tile_kernel(const uint4* __restrict__ packed, uint4* __restrict__ tiled, int rows, int nunits,
+                                long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63);
+    const long tu = p >> 6;
+    const int u = (int)(tu % nunits);
+    const long rt = tu / nunits;
+    const long row = rt * 16 + (lane & 15);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) v = packed[(row * nunits + u) * 4 + (lane >> 4)];
+    tiled[p] = v;
+}
+
+__global__ void w4t_sz_kernel(const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+                              uint32_t* __restrict__ sz, int rows, int ngroups) {
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;  // e = group * rows + row
+    if (e >= (long)rows * ngroups) return;
+    const long g = e / rows, r = e % rows;
+    const uint16_t s = scales[r * ngroups + g];
+    const uint16_t z = zeros ? zeros[r * ngroups + g] : (uint16_t)0x4800;  // fp16 8.0
+    sz[e] = (uint32_t)s | ((uint32_t)z << 16);
+}
+
+// X rows [k0, k1) of the staged chunk: row stride 2N bytes, two pad rows per 32.
+__host__ __device__ constexpr int w4t_xbytes(int KC, int N) { return (KC + KC / 16) * 2 * N; }
+
+// Small-batch W4A16 GEMM on the tiled layout (N in {4, 8, 12, 16}, K % 128 == 0,
+// group size % 128 == 0).  A workgroup of W waves owns 32 W rows (two 16-row
+// tiles a wave) and a K range of UPW 128-K units; K ranges are split across
+// workgroups (blockIdx.y) and add into C with fp32 atomics after a zero fill.
+//  * The X chunk and the workgroup's (scale, zero) dwords are loaded first
+//    (coalesced buffer loads), the weights next (each tile one contiguous
+//    1 KB load), and X / scales are written to LDS while the weights stream;
+//    the barrier waits for LDS only, so each unit computes as soon as its own
+//    weights arrive.
+//  * A operand: the nibble pairs (e_m, e_m+4) of a dword, (d >> 4m) &
+//    0x000F000F, are the fp16 subnormals e * 2^-24 exactly (7 VALU per 8
+//    weights), so a unit's MFMA sum is 2^-24 * sum(q x) with the products
+//    exact in fp32.  A sum-of-x MFMA with an all-ones A gives sum(x), and
+//    y += (s 2^24) * D - (s z) * sum(x), with s 2^24 and s z formed once per
+//    (row, unit) in fp32.
+//  * Workgroups are mapped XCD-aware: workgroup id mod 8 selects the XCD,
+//    and every K range of a row block runs on one XCD, whose L2 then holds
+//    the row block's scale lines.
+template <int UPW, int W, int N>
+__global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __restrict__ wt,
+                                                             const uint32_t* __restrict__ szp,
+                                                             const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                             int rows, int K, int gs) {
+    constexpr int KC = 128 * UPW;
+    constexpr int RW = 32 * W;
+    constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
+    constexpr int SP = (UPW * RW + W * 64 - 1) / (W * 64);
+    constexpr int XB = w4t_xbytes(KC, N);
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* zero_area = smem + XB;
+    float2* szs = reinterpret_cast<float2*>(zero_area + 16);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int nunits = K / 128;
+    int byi = blockIdx.y, bxi = blockIdx.x;
+    if ((gridDim.x & 7) == 0) {
+        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
+        byi = j % gridDim.y;
+        bxi = (id & 7) + 8 * (j / gridDim.y);
+    }
+    const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
+    const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
+    const int ntiles = (rows + 15) / 16;
+    const int npieces = (u1 - u0) * 128 * 2 * N / 16;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsz = __builtin_amdgcn_make_buffer_rsrc((void*)szp, (short)0, 0x7fffffff, 0x00020000);
+    u32x4 xr[XP];
+#pragma unroll
+    for (int i = 0; i < XP; i++) xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    uint32_t sr[SP];
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64, u = e / RW, r = e % RW;
+        const bool ok = e < UPW * RW && u0 + u < u1;
+        const uint32_t off = ok ? (uint32_t)(((u0 + u) * 128 / gs) * rows + min(rw0 + r, rows - 1)) * 4u : 0x80000000u;
+        sr[i] = __builtin_amdgcn_raw_buffer_load_b32(rsz, off, 0, 0);
+    }
+    uint4 w[UPW][2];
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        const int unit = min(u0 + u, u1 - 1);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = min(row0 / 16 + t, ntiles - 1);
+            w[u][t] = ld_stream(wt + ((long)rt * nunits + unit) * 64 + lane);
+        }
+    }
+    if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+        const int p = tid + i * W * 64;
+        if (p < npieces) {
+            const int off = p * 16;
+            *reinterpret_cast<u32x4*>(smem + off + (off / (64 * N)) * (4 * N)) = xr[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64;
+        if (e < UPW * RW && u0 + e / RW < u1) {
+            const float sc = h2f(sr[i] & 0xffff), zz = h2f(sr[i] >> 16);
+            szs[e] = make_float2(sc * 16777216.0f, sc * zz);
+        }
+    }
+    // LDS writes visible to the workgroup; the weight loads stay in flight.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const MfmaBRole ro(li, N);
+    const int offa = (ro.jq == 0) ? 0 : (ro.jq == 1) ? 4 : (ro.jq == 2) ? 1 : 5;  // rows {0,4,1,5}
+    const int offb = offa + 2;                                                      // rows {2,6,3,7}
+    const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
+    float4v acc[2];
+    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        if (u0 + u < u1) {
+            float4v d[2], dn = (float4v){0.f, 0.f, 0.f, 0.f};
+            d[0] = d[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const half8v bv = mfma_b_operand(smem, ro, u * 128 + 32 * lg + 8 * s, offa, offb, N, XB);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
+                    const u32x4 av = {dw & 0x000F000Fu, (dw >> 4) & 0x000F000Fu, (dw >> 8) & 0x000F000Fu,
+                                      (dw >> 12) & 0x000F000Fu};
+                    d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv, d[t], 0, 0, 0);
+                }
+                dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, bv, dn, 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const float* q = reinterpret_cast<const float*>(szs + u * RW + 32 * wave + 16 * t + 4 * lg);
+                const float4 qa = *reinterpret_cast<const float4*>(q), qb = *reinterpret_cast<const float4*>(q + 4);
+                const float sv[4] = {qa.x, qa.z, qb.x, qb.z}, zv[4] = {qa.y, qa.w, qb.y, qb.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][i] = fmaf(sv[i], d[t][i], fmaf(-zv[i], dn[i], acc[t][i]));
+            }
+        }
+    }
+    if (li < N) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = row0 + 16 * t + 4 * lg + i;
+                if (row < rows) {
+                    if (gridDim.y > 1)
+                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
+                    else
+                        y[(long)row * N + li] = acc[t][i];
+                }
+            }
+    }
+}
+
+template <int UPW, int N>
+static void launch_w4t(dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz, const uint16_t* x, float* y,
+                       int M, int K, int gs) {
+    constexpr int W = 4;
+    const size_t lds = (size_t)w4t_xbytes(128 * UPW, N) + 16 + 8 * UPW * 32 * W;
+    w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, y, M, K, gs);
+}
+
+template <int N>
+static void launch_w4t_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz, const uint16_t* x,
+                         float* y, int M, int K, int gs) {
+    if (upw == 8)
+        launch_w4t<8, N>(g, st, wt, sz, x, y, M, K, gs);
+    else if (upw == 4)
+        launch_w4t<4, N>(g, st, wt, sz, x, y, M, K, gs);
+    else
+        launch_w4t<2, N>(g, st, wt, sz, x, y, M, K, gs);
+}
+
+ZT_EXPORT long zt_w4a16_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 2);
+}
+
+ZT_EXPORT long zt_w4a16_sz_bytes(int M, int K, int group_size) {
+    if (M < 0 || K < 0 || group_size <= 0 || K % group_size != 0) return -1;
+    return (long)M * (K / group_size) * 4;
+}
+
+ZT_EXPORT int zt_w4a16_tile(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, int M, int K,
+                            int group_size, void* W_tiled, uint32_t* sz, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_packed == nullptr || scales == nullptr || W_tiled == nullptr || sz == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_packed & 15) || ((uintptr_t)W_tiled & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1) ||
+        ((uintptr_t)sz & 3))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128, ngroups = K / group_size;
+    const long npieces = (long)((M + 15) / 16) * nunits * 64;
+    w4t_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(static_cast<const uint4*>(W_packed),
+                                                               static_cast<uint4*>(W_tiled), M, nunits, npieces);
+    w4t_sz_kernel<<<ceil_div((long)M * ngroups, 256), 256, 0, stream>>>(scales, zeros, sz, M, ngroups);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* B, float* C, int M, int K,
+                                 int N, int group_size, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0 || group_size <= 0 || group_size % 128 != 0 || K % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_tiled == nullptr || sz == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_tiled & 15) || ((uintptr_t)sz & 3) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
+        return (int)hipErrorInvalidValue;
+    if ((long)M * (K / group_size) >= (1L << 29)) return (int)hipErrorInvalidValue;  // 32-bit sz offsets
+    const int nunits = K / 128;
+    const int gx = ceil_div(M, 128);
+    // the largest K range per workgroup that still gives >= 256 workgroups
+    int upw = 8;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    const dim3 g(gx, ceil_div(nunits, upw));
+    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    const uint4* wt = static_cast<const uint4*>(W_tiled);
+    switch (N) {
+        case 4: launch_w4t_n<4>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
+        case 8: launch_w4t_n<8>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
+        case 12: launch_w4t_n<12>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
+        default: launch_w4t_n<16>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
+    }
+    return (int)hipGetLastError();
+}

@@ -88,6 +88,13 @@ class ROCmEngine:
                        group_size: int) -> None:
         self.lib.call("zt_gemm_w4a16_f32", w, scales, zeros, b, c, m, k, n, group_size, self._s)
 
+    def w4a16_tile(self, w: int, scales: int, zeros: int, m: int, k: int, group_size: int, w_tiled: int,
+                   sz: int) -> None:
+        self.lib.call("zt_w4a16_tile", w, scales, zeros, m, k, group_size, w_tiled, sz, self._s)
+
+    def gemm_w4a16t_f32(self, w_tiled: int, sz: int, b: int, c: int, m: int, k: int, n: int, group_size: int) -> None:
+        self.lib.call("zt_gemm_w4a16t_f32", w_tiled, sz, b, c, m, k, n, group_size, self._s)
+
     def gemv_q4k_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
         self.lib.call("zt_gemv_q4k_f32", w, x, y, m, k, self._s)
 
@@ -192,6 +199,24 @@ class ROCmEngine:
             return ct.t().contiguous().reshape(*a.shape[:-1], nout)
         raise TypeError("matmul: neither operand is a quantized weight Tensor")
 
+    def _w4a16_tiled(self, s: Any, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The tiled copy of uploaded W4A16 weights for batches of 4-16
+        columns, built on the device on the first batched call and kept
+        beside the row-major upload (which batch 1 reads)."""
+        cached = getattr(s, "_gpu_tiled", None)
+        if cached is not None and cached[0] == (rows, k):
+            return cached[1], cached[2]
+        nbytes = self.lib.zt_w4a16_tiled_bytes(rows, k)
+        szbytes = self.lib.zt_w4a16_sz_bytes(rows, k, s.group_size)
+        if nbytes < 0 or szbytes < 0:
+            raise ValueError(f"W4A16 tiled layout: unsupported shape [{rows}, {k}] (group {s.group_size})")
+        wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        sz = torch.empty(szbytes // 4, dtype=torch.int32, device=self.device)
+        zeros = _p(s._gpu_zeros) if s._gpu_zeros is not None else 0
+        self.w4a16_tile(_p(s.gpu_ptr().tensor), _p(s._gpu_scales), zeros, rows, k, s.group_size, _p(wt), _p(sz))
+        s._gpu_tiled = ((rows, k), wt, sz)  # type: ignore[attr-defined]
+        return wt, sz
+
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
         n = 1 if x.dim() == 1 else x.shape[1]
@@ -223,8 +248,12 @@ class ROCmEngine:
         elif isinstance(s, (GPTQStorage, AWQStorage)):
             if x.dtype != torch.float16:
                 raise TypeError("W4A16 matmul takes fp16 activations")
-            self.gemm_w4a16_f32(_p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(x), _p(c), rows, k, n,
-                                s.group_size)
+            if n in _W4T_BATCHES and k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29:
+                wt, sz = self._w4a16_tiled(s, rows, k)
+                self.gemm_w4a16t_f32(_p(wt), _p(sz), _p(x), _p(c), rows, k, n, s.group_size)
+            else:
+                self.gemm_w4a16_f32(_p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(x), _p(c), rows, k, n,
+                                    s.group_size)
         elif isinstance(s, (Q4KStorage, Q5KStorage, Q6KStorage, Q5_0Storage)):
             if x.dtype != torch.float32:
                 raise TypeError(f"{type(s).__name__} matmul takes fp32 activations")
@@ -316,6 +345,9 @@ class ROCmEngine:
         y = torch.empty(rows, dtype=torch.float32, device=self.device)
         self.ternary_gemv_f32(_p(w), _p(xd), _p(y), rows, cols)
         return y.cpu().numpy()
+
+
+_W4T_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 layout
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
