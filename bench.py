@@ -451,8 +451,8 @@ def run_pmc_case(args) -> None:
 
     lib = _lib.load()
     calibration_copy(torch)
-    if args.pmc_case == "w4a16_b8":
-        run_pmc_case_w4a16(torch, lib)
+    if args.pmc_case in ("w4a16_b8", "w4a16t_b8"):
+        run_pmc_case_w4a16(torch, lib, tiled=args.pmc_case == "w4a16t_b8")
         return
     m = Q4Matrix(torch, lib, 14336, 4096, 0x5EED0024, 20)
     s = torch.cuda.current_stream().cuda_stream
@@ -462,29 +462,42 @@ def run_pmc_case(args) -> None:
     log("bench: pmc case done")
 
 
-def run_pmc_case_w4a16(torch, lib) -> None:
+def run_pmc_case_w4a16(torch, lib, tiled: bool) -> None:
     """40 launches of the batch-8 W4A16 MFMA GEMM at the Llama-3-70B down
     projection (28672 rows, K = 8192, group 128), rotating over 3 weight
-    copies (352 MB, beyond the Infinity Cache)."""
+    copies (352 MB, beyond the Infinity Cache), on the row-major layout or
+    on the tiled layout (built before the launches)."""
     from ztensor_amd import synth
 
     rows, K, N = 28672, 8192, 8
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+    s = torch.cuda.current_stream().cuda_stream
     copies = []
     for c in range(3):
         w = synth.w4a16(rows, K, 0x5EED0040 + c)
-        copies.append((dev(w.packed), dev(w.scales), dev(w.zeros)))
+        bufs = (dev(w.packed), dev(w.scales), dev(w.zeros))
+        if tiled:
+            wt = torch.empty(lib.zt_w4a16_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+            sz = torch.empty(lib.zt_w4a16_sz_bytes(rows, K, 128), dtype=torch.uint8, device="cuda")
+            if lib.zt_w4a16_tile(*(b.data_ptr() for b in bufs), rows, K, 128, wt.data_ptr(), sz.data_ptr(), s) != 0:
+                raise SystemExit("bench: zt_w4a16_tile failed")
+            bufs = (wt, sz)
+        copies.append(bufs)
     x = dev(synth.x_f16(K * N, 0x5EED0043))
     y = torch.empty(rows * N, dtype=torch.float32, device="cuda")
-    s = torch.cuda.current_stream().cuda_stream
-    for i in range(40):
-        wp, sc, zr = copies[i % 3]
-        rc = lib.zt_gemm_w4a16_f32(wp.data_ptr(), sc.data_ptr(), zr.data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N,
-                                   128, s)
-        if rc != 0:
-            raise SystemExit(f"bench: zt_gemm_w4a16_f32 returned {rc}")
     torch.cuda.synchronize()
-    log("bench: pmc case w4a16_b8 done")
+    for i in range(40):
+        b = copies[i % 3]
+        if tiled:
+            rc = lib.zt_gemm_w4a16t_f32(b[0].data_ptr(), b[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, 128,
+                                        s)
+        else:
+            rc = lib.zt_gemm_w4a16_f32(b[0].data_ptr(), b[1].data_ptr(), b[2].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                       rows, K, N, 128, s)
+        if rc != 0:
+            raise SystemExit(f"bench: W4A16 GEMM returned {rc}")
+    torch.cuda.synchronize()
+    log(f"bench: pmc case {'w4a16t_b8' if tiled else 'w4a16_b8'} done")
 
 
 def run_suite(args) -> None:
@@ -518,9 +531,10 @@ def main() -> None:
                     help="skip the merged Q/K/V + Gate/Up variant reported beside the headline")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
-    ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8"],
+    ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8", "w4a16t_b8"],
                     help="short fixed workload for rocprofv3 counter passes: copies + 40 launches of the dominant "
-                         "Q4_0 GEMV (default), or of the W4A16 batch-8 MFMA GEMM at 28672 x 8192")
+                         "Q4_0 GEMV (default), or of the W4A16 batch-8 MFMA GEMM at 28672 x 8192 on the row-major "
+                         "(w4a16_b8) or tiled (w4a16t_b8) layout")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()

@@ -131,9 +131,18 @@ static __global__ void mfma_zero_kernel(float* __restrict__ y, long n) {
     if (i < n) y[i] = 0.0f;
 }
 
-// Zeroes C before a split-K launch on the same stream.
+static __global__ void mfma_zero4_kernel(float4* __restrict__ y, long n4) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n4) y[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+// Zeroes C before a split-K launch on the same stream (16-byte stores when
+// C is 16-byte aligned and a multiple of 4 floats).
 __host__ __forceinline__ void mfma_zero(float* y, long n, hipStream_t st) {
-    mfma_zero_kernel<<<(int)((n + 255) / 256), 256, 0, st>>>(y, n);
+    if (((uintptr_t)y & 15) == 0 && n % 4 == 0)
+        mfma_zero4_kernel<<<(int)((n / 4 + 255) / 256), 256, 0, st>>>(reinterpret_cast<float4*>(y), n / 4);
+    else
+        mfma_zero_kernel<<<(int)((n + 255) / 256), 256, 0, st>>>(y, n);
 }
 
 __host__ __forceinline__ size_t mfma_reduce_bytes() { return (size_t)kMfmaWaves * kMfmaTiles * 4 * 64 * sizeof(float); }
