@@ -293,6 +293,29 @@ def test_iq4nl_mfma_ragged(lib, orc, rows, K, N):
     assert rel_err(c.cpu().numpy(), ref) <= TOL
 
 
+def test_iq4nl_fp16_codebook_worst_case(lib, orc):
+    """The fp16-activation GEMV rounds the fp32 codebook to fp16 (relative
+    error at most 2^-11; 3.25e-4 for T = -0.5250730, the worst entry).
+    With every weight on that entry and every activation positive the
+    per-weight errors cannot cancel, so the output error is that bound: it
+    must stay under the 1e-3 bar (and within 4e-4)."""
+    rows, K = 256, 4096
+    nblk = rows * K // 32
+    rng = np.random.default_rng(5)
+    nib = np.full((nblk, 32), 2, np.uint8)
+    scales = synth.f16_bits(np.abs(rng.standard_normal(nblk).astype(np.float32)) * np.float32(0.01) + np.float32(0.001))
+    raw = synth.pack_iq4nl(nib, scales)
+    x16 = synth.f16_bits(rng.uniform(0.5, 1.5, K).astype(np.float32))
+    a = dev(synth_gpu_q4(raw, nblk))
+    c = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = dev(x16)
+    lib.call("zt_gemm_iq4nl_f16", a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, 1,
+             lib.zt_q4_gpu_data_offset(nblk), stream())
+    ref = orc.iq4nl_matmul(raw, x16, rows, K, 1)
+    err = rel_err(c.cpu().numpy(), ref)
+    assert err <= 4e-4 and err <= TOL
+
+
 def test_iq4nl_fp32_activations(lib, orc):
     rows, K = 64, 1024
     w = synth.iq4nl(rows, K, 3)
