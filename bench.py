@@ -314,6 +314,7 @@ SUITE = {
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
+    "iq4nlt": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [8]),
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
@@ -363,6 +364,25 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: lib.zt_gemm_w4a16_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
                                                  y.data_ptr(), rows, K, N, 128, s)
         nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
+    elif fmt == "iq4nlt":
+        # the tiled upload layout (zt_iq4nl_tile), built once outside the timing
+        w = synth.iq4nl(rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_iq4nl_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+        sep = dev(host)
+        wt = torch.empty(lib.zt_iq4nl_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        st = torch.empty(lib.zt_iq4nl_tiled_scale_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        if lib.zt_iq4nl_tile(sep.data_ptr(), rows, K, lib.zt_q4_gpu_data_offset(nblk), wt.data_ptr(), st.data_ptr(),
+                             s) != 0:
+            raise RuntimeError("zt_iq4nl_tile failed")
+        torch.cuda.synchronize()
+        del sep
+        wbufs = [wt, st]
+        x = dev(synth.x_f16(K * N, seed))
+        fn = lambda wb, y: lib.zt_gemm_iq4nlt_f16(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows,
+                                                  K, N, s)
+        nbytes = synth.algorithmic_bytes("iq4nl", rows, K, N)
     elif fmt == "w4a16t":
         # the tiled upload layout (zt_w4a16_tile), built once outside the timing
         w = synth.w4a16(rows, K, seed)

@@ -92,6 +92,26 @@ int zt_gemm_iq4nl_f16(const void* A_iq4, const uint16_t* B, float* C, int M, int
 int zt_dequant_iq4nl_f32(const void* A_iq4, float* out, long nelem, int data_offset, zt_stream_t stream);
 /* Host: IQ4NLStorage.RawBytes (tensor/iq4_storage.go:104) -> separated layout. */
 void zt_iq4nl_raw_to_gpu(const void* raw, long nblk, void* out);
+/* Tiled upload layout for batched fp16 activations on the same IQ4_NL
+ * matmul (the engine's CPU fallback, compute/cpu_engine.go:1215-1245); the
+ * reference has no GPU IQ4_NL kernel.  Built once from the separated layout:
+ *   W_tiled: tile (rt, u) = rows 16 rt .. +16, blocks 4u .. 4u+3, 1 KB at
+ *   ((rt * K/128) + u) * 1024; 16-byte piece l = 16 g + i holds dword g of
+ *   blocks 4u .. 4u+3 of row 16 rt + i (zt_iq4nl_tiled_bytes bytes);
+ *   S_tiled: fp16 block scales, 128 bytes a tile at ((rt * K/128) + u) * 128,
+ *   [16 rows][4 blocks] (zt_iq4nl_tiled_scale_bytes bytes);
+ * rows past M, to the next multiple of 16, are zero.  K % 128 == 0, the
+ * separated layout's base 2-byte and data 16-byte aligned, W_tiled and
+ * S_tiled 16-byte aligned, else InvalidValue. */
+long zt_iq4nl_tiled_bytes(int M, int K);
+long zt_iq4nl_tiled_scale_bytes(int M, int K);
+int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+/* C[M, N] = dequant(W) B on the tiled layout, B fp16 [K, N] 16-byte
+ * aligned, N in {4, 8, 12, 16}, K % 128 == 0, else InvalidValue.  The
+ * codebook enters the MFMAs rounded to fp16 (relative error at most 2^-11
+ * per entry); split K ranges add into C with fp32 atomics after a zero fill. */
+int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t* B, float* C, int M, int K, int N,
+                       zt_stream_t stream);
 
 /* ---- Q8_0 -------------------------------------------------------------- */
 

@@ -185,3 +185,14 @@ def test_w4a16_tiled_layout_sizes():
     assert lib.zt_w4a16_sz_bytes(8192, 8192, 128) == 8192 * 64 * 4
     assert lib.zt_w4a16_sz_bytes(17, 256, 64) == 17 * 4 * 4
     assert lib.zt_w4a16_sz_bytes(4, 96, 64) == -1
+
+
+def test_iq4nl_tiled_layout_sizes():
+    """The tiled IQ4_NL layout's byte counts (host helpers, no GPU)."""
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    assert lib.zt_iq4nl_tiled_bytes(3584, 3584) == 3584 * 1792
+    assert lib.zt_iq4nl_tiled_bytes(17, 256) == 32 * 128
+    assert lib.zt_iq4nl_tiled_scale_bytes(17, 256) == 32 * 8 * 2
+    assert lib.zt_iq4nl_tiled_bytes(4, 96) == -1 and lib.zt_iq4nl_tiled_scale_bytes(4, 96) == -1

@@ -33,6 +33,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_gemm_iq4nl_f32": (I, [P, P, P, I, I, I, I, P]),
     "zt_gemm_iq4nl_f16": (I, [P, P, P, I, I, I, I, P]),
     "zt_dequant_iq4nl_f32": (I, [P, P, L, I, P]),
+    "zt_iq4nl_tiled_bytes": (L, [I, I]),
+    "zt_iq4nl_tiled_scale_bytes": (L, [I, I]),
+    "zt_iq4nl_tile": (I, [P, I, I, I, P, P, P]),
+    "zt_gemm_iq4nlt_f16": (I, [P, P, P, P, I, I, I, P]),
     "zt_iq4nl_raw_to_gpu": (None, [P, L, P]),
     "zt_gemm_q8_f32": (I, [P, P, P, I, I, I, P]),
     "zt_gemm_q8sep_f32": (I, [P, P, P, I, I, I, L, P]),

@@ -48,6 +48,9 @@ __device__ __forceinline__ short4v tr_read_b64(char* lds, int byte_off) {
 // Bytes of one staged X chunk: kMfmaKC rows of 2N bytes plus 2 pad rows per 32.
 __host__ __device__ __forceinline__ int mfma_xbytes(int N) { return (kMfmaKC + kMfmaKC / 16) * 2 * N; }
 
+// Bytes of a staged X chunk of KC rows (row stride 2N bytes, two pad rows per 32).
+__host__ __device__ constexpr int mfma_chunk_xbytes(int KC, int N) { return (KC + KC / 16) * 2 * N; }
+
 // LDS byte offset of chunk-relative X row k (row stride 2N, 2 pad rows per 32).
 __device__ __forceinline__ int mfma_xrow(int k, int N) { return (k + 2 * (k >> 5)) * 2 * N; }
 

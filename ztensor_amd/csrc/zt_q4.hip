@@ -683,3 +683,228 @@ ZT_EXPORT int zt_dequant_iq4nl_f32(const void* A_iq4, float* out, long nelem, in
                                    hipStream_t stream) {
     return dequant_blk18<Fmt::IQ4NL>(A_iq4, out, nelem, data_offset, stream);
 }
+
+// ------------------------------------------------------------ IQ4_NL tiled layout
+//
+// An upload-time repack of the IQ4_NL separated layout for batched fp16
+// activations (N in {4, 8, 12, 16}), the IQ4_NL counterpart of the tiled
+// W4A16 layout.  For tile (rt, u) = rows 16 rt .. +16, blocks 4u .. 4u+3:
+//   data: 1 KB at byte ((rt * K/128) + u) * 1024; the 16 bytes of lane
+//     l = 16 g + i are dword g of blocks 4u, 4u+1, 4u+2, 4u+3 of row 16 rt + i
+//     (elements 8g .. 8g+7 of each block, interleaved nibble order), so MFMA
+//     step s takes component s of every lane and covers exactly block 4u+s;
+//   scales: 128 bytes at ((rt * K/128) + u) * 128, fp16 [16 rows][4 blocks].
+// Rows past M (to the next multiple of 16) are zero.
+
+__global__ void iq4t_tile_kernel(const uint32_t* __restrict__ data, const uint16_t* __restrict__ scales,
+                                 u32x4* __restrict__ wt, uint16_t* __restrict__ st, int rows, int nunits, long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63), i = lane & 15, g = lane >> 4;
+    const long tu = p >> 6;
+    const int u = (int)(tu % nunits);
+    const long row = (tu / nunits) * 16 + i;
+    const long kb = (long)nunits * 4;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    uint16_t sc = 0;
+    if (row < rows) {
+        const long b0 = row * kb + 4L * u;
+        v = (u32x4){data[b0 * 4 + g], data[(b0 + 1) * 4 + g], data[(b0 + 2) * 4 + g], data[(b0 + 3) * 4 + g]};
+        sc = scales[b0 + g];  // lane (i, g) also moves the scale of row i, block 4u + g
+    }
+    wt[p] = v;
+    st[tu * 64 + i * 4 + g] = sc;
+}
+
+// Batched IQ4_NL on the tiled layout: the W4A16 tiled kernel's structure
+// (4 waves x 32 rows a workgroup, UPW 128-K units, XCD-aware mapping, X and
+// scales staged in LDS behind an LDS-only barrier while the 1 KB weight
+// loads stream).  A operand: one ds_read_b32 per data byte from a 1 KB LDS
+// table byte -> fp16 pair (T[low], T[high]), the codebook rounded to fp16
+// (relative error at most 2^-11 per entry, as in the fp16 GEMV); the pairs
+// are in element order, so the B rows of a lane group are read in natural
+// order.  Each step's result is scaled by its block's fp16 scale in fp32.
+template <int UPW, int W, int N>
+__global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __restrict__ wt,
+                                                             const uint16_t* __restrict__ stl,
+                                                             const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                             int rows, int K) {
+    constexpr int KC = 128 * UPW;
+    constexpr int RW = 32 * W;
+    constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
+    constexpr int SPC = RW / 16 * UPW * 128 / 16;  // 16-byte scale pieces of the workgroup
+    constexpr int SP = (SPC + W * 64 - 1) / (W * 64);
+    constexpr int XB = mfma_chunk_xbytes(KC, N);
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* zero_area = smem + XB;
+    uint32_t* tbl = reinterpret_cast<uint32_t*>(zero_area + 16);   // 256 fp16 pairs
+    uint16_t* ssm = reinterpret_cast<uint16_t*>(tbl + 256);        // [tile in WG][unit][16 rows][4 blocks]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int nunits = K / 128;
+    int byi = blockIdx.y, bxi = blockIdx.x;
+    if ((gridDim.x & 7) == 0) {
+        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
+        byi = j % gridDim.y;
+        bxi = (id & 7) + 8 * (j / gridDim.y);
+    }
+    const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
+    const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
+    const int ntiles = (rows + 15) / 16;
+    const int npieces = (u1 - u0) * 128 * 2 * N / 16;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)stl, (short)0, 0x7fffffff, 0x00020000);
+    u32x4 xr[XP];
+#pragma unroll
+    for (int i = 0; i < XP; i++) xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    // scales: piece e = (tile in WG) * UPW * 8 + unit * 8 + q (8 pieces of 16 bytes a tile-unit)
+    u32x4 sr[SP];
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64, tw = e / (UPW * 8), u = (e / 8) % UPW, q = e % 8;
+        const int rt = rw0 / 16 + tw;
+        const bool ok = e < SPC && rt < ntiles && u0 + u < u1;
+        const uint32_t off = ok ? (uint32_t)(((rt * nunits + u0 + u) * 8 + q) * 16) : 0x80000000u;
+        sr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    }
+    uint4 w[UPW][2];
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        const int unit = min(u0 + u, u1 - 1);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = min(row0 / 16 + t, ntiles - 1);
+            w[u][t] = ld_stream(wt + ((long)rt * nunits + unit) * 64 + lane);
+        }
+    }
+    if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
+    for (int i = tid; i < 256; i += W * 64) {
+        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
+        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+        const int p = tid + i * W * 64;
+        if (p < npieces) {
+            const int off = p * 16;
+            *reinterpret_cast<u32x4*>(smem + off + (off / (64 * N)) * (4 * N)) = xr[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64;
+        if (e < SPC) *reinterpret_cast<u32x4*>(ssm + e * 8) = sr[i];
+    }
+    // LDS writes visible to the workgroup; the weight loads stay in flight.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const MfmaBRole ro(li, N);
+    float4v acc[2];
+    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        if (u0 + u < u1) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const half8v bv = mfma_b_operand(smem, ro, u * 128 + 32 * s + 8 * lg, ro.jq, ro.jq + 4, N, XB);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
+                    const u32x4 av = {tbl[dw & 0xffu], tbl[(dw >> 8) & 0xffu], tbl[(dw >> 16) & 0xffu], tbl[dw >> 24]};
+                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv,
+                                                                            (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    // scales of rows 4 lg + i of this tile, block 4u + s
+                    const uint16_t* sp = ssm + ((2 * wave + t) * UPW + u) * 64 + 16 * lg + s;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(h2f(sp[4 * i]), d[i], acc[t][i]);
+                }
+            }
+        }
+    }
+    if (li < N) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = row0 + 16 * t + 4 * lg + i;
+                if (row < rows) {
+                    if (gridDim.y > 1)
+                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
+                    else
+                        y[(long)row * N + li] = acc[t][i];
+                }
+            }
+    }
+}
+
+template <int UPW, int N>
+static void launch_iq4t(dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc, const uint16_t* x, float* y,
+                        int M, int K) {
+    constexpr int W = 4;
+    const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 1024 + (size_t)2 * W * UPW * 64 * 2;
+    iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, y, M, K);
+}
+
+template <int N>
+static void launch_iq4t_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc, const uint16_t* x,
+                          float* y, int M, int K) {
+    if (upw == 8)
+        launch_iq4t<8, N>(g, st, wt, sc, x, y, M, K);
+    else if (upw == 4)
+        launch_iq4t<4, N>(g, st, wt, sc, x, y, M, K);
+    else
+        launch_iq4t<2, N>(g, st, wt, sc, x, y, M, K);
+}
+
+ZT_EXPORT long zt_iq4nl_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 2);
+}
+
+ZT_EXPORT long zt_iq4nl_tiled_scale_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 32) * 2;
+}
+
+ZT_EXPORT int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, void* W_tiled, void* S_tiled,
+                            hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0 || data_offset < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (A_iq4 == nullptr || W_tiled == nullptr || S_tiled == nullptr) return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(A_iq4);
+    if (((uintptr_t)base & 1) || ((uintptr_t)(base + data_offset) & 15) || ((uintptr_t)W_tiled & 15) ||
+        ((uintptr_t)S_tiled & 15))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 64;
+    iq4t_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        reinterpret_cast<const uint32_t*>(base + data_offset), reinterpret_cast<const uint16_t*>(base),
+        static_cast<u32x4*>(W_tiled), static_cast<uint16_t*>(S_tiled), M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t* B, float* C, int M, int K,
+                                 int N, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0) return (int)hipErrorInvalidValue;
+    if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
+        return (int)hipErrorInvalidValue;
+    if ((long)((M + 15) / 16) * (K / 128) * 128 >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
+    const int nunits = K / 128;
+    const int gx = ceil_div(M, 128);
+    int upw = 8;  // the largest K range per workgroup that still gives >= 256 workgroups
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    const dim3 g(gx, ceil_div(nunits, upw));
+    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    const uint4* wt = static_cast<const uint4*>(W_tiled);
+    const uint16_t* sc = static_cast<const uint16_t*>(S_tiled);
+    switch (N) {
+        case 4: launch_iq4t_n<4>(upw, g, stream, wt, sc, B, C, M, K); break;
+        case 8: launch_iq4t_n<8>(upw, g, stream, wt, sc, B, C, M, K); break;
+        case 12: launch_iq4t_n<12>(upw, g, stream, wt, sc, B, C, M, K); break;
+        default: launch_iq4t_n<16>(upw, g, stream, wt, sc, B, C, M, K); break;
+    }
+    return (int)hipGetLastError();
+}

@@ -563,9 +563,6 @@ __global__ void w4t_sz_kernel(const uint16_t* __restrict__ scales, const uint16_
     sz[e] = (uint32_t)s | ((uint32_t)z << 16);
 }
 
-// X rows [k0, k1) of the staged chunk: row stride 2N bytes, two pad rows per 32.
-__host__ __device__ constexpr int w4t_xbytes(int KC, int N) { return (KC + KC / 16) * 2 * N; }
-
 // Small-batch W4A16 GEMM on the tiled layout (N in {4, 8, 12, 16}, K % 128 == 0,
 // group size % 128 == 0).  A workgroup of W waves owns 32 W rows (two 16-row
 // tiles a wave) and a K range of UPW 128-K units; K ranges are split across
@@ -593,7 +590,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     constexpr int RW = 32 * W;
     constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
     constexpr int SP = (UPW * RW + W * 64 - 1) / (W * 64);
-    constexpr int XB = w4t_xbytes(KC, N);
+    constexpr int XB = mfma_chunk_xbytes(KC, N);
     extern __shared__ __attribute__((aligned(16))) char smem[];
     char* zero_area = smem + XB;
     float2* szs = reinterpret_cast<float2*>(zero_area + 16);
@@ -706,7 +703,7 @@ template <int UPW, int N>
 static void launch_w4t(dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz, const uint16_t* x, float* y,
                        int M, int K, int gs) {
     constexpr int W = 4;
-    const size_t lds = (size_t)w4t_xbytes(128 * UPW, N) + 16 + 8 * UPW * 32 * W;
+    const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 8 * UPW * 32 * W;
     w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, y, M, K, gs);
 }
 

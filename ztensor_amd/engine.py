@@ -217,6 +217,21 @@ class ROCmEngine:
         s._gpu_tiled = ((rows, k), wt, sz)  # type: ignore[attr-defined]
         return wt, sz
 
+    def _iq4nl_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The tiled copy of uploaded IQ4_NL weights for batches of 4-16
+        fp16 columns, built on the device on first use."""
+        cached = getattr(s, "_gpu_tiled", None)
+        if cached is not None and cached[0] == (rows, k):
+            return cached[1], cached[2]
+        nbytes, sbytes = self.lib.zt_iq4nl_tiled_bytes(rows, k), self.lib.zt_iq4nl_tiled_scale_bytes(rows, k)
+        if nbytes < 0 or sbytes < 0:
+            raise ValueError(f"IQ4_NL tiled layout: unsupported shape [{rows}, {k}]")
+        wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        st = torch.empty(sbytes, dtype=torch.uint8, device=self.device)
+        self.lib.call("zt_iq4nl_tile", _p(buf.tensor), rows, k, buf.data_offset, _p(wt), _p(st), self._s)
+        s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
+        return wt, st
+
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
         n = 1 if x.dim() == 1 else x.shape[1]
@@ -237,6 +252,9 @@ class ROCmEngine:
         elif isinstance(s, IQ4NLStorage):
             if x.dtype == torch.float32:
                 self.gemm_iq4nl_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype == torch.float16 and n in _TILED_BATCHES and k % 128 == 0:
+                wt, st = self._iq4nl_tiled(s, buf, rows, k)
+                self.lib.call("zt_gemm_iq4nlt_f16", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
             elif x.dtype == torch.float16:
                 self.gemm_iq4nl_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             else:
@@ -248,7 +266,7 @@ class ROCmEngine:
         elif isinstance(s, (GPTQStorage, AWQStorage)):
             if x.dtype != torch.float16:
                 raise TypeError("W4A16 matmul takes fp16 activations")
-            if n in _W4T_BATCHES and k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29:
+            if n in _TILED_BATCHES and k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29:
                 wt, sz = self._w4a16_tiled(s, rows, k)
                 self.gemm_w4a16t_f32(_p(wt), _p(sz), _p(x), _p(c), rows, k, n, s.group_size)
             else:
@@ -347,7 +365,7 @@ class ROCmEngine:
         return y.cpu().numpy()
 
 
-_W4T_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 layout
+_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL layouts
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
