@@ -167,6 +167,29 @@ def test_ternary_gemv_matches_oracle(eng, orc):
     assert rel_err(y, orc.ternary_gemv(t.raw, x, rows, cols)) <= TOL
 
 
+def test_ternary_weights_stay_resident(eng, orc):
+    """The row-aligned ternary upload is made once per storage and shape
+    (the reference repacks and uploads on every TernaryGEMVGPU call) and is
+    reused by both ternary_gemv and matmul, including several activation
+    columns."""
+    rows, cols = 256, 1000
+    t = synth.ternary(rows, cols, 23)
+    st = TernaryStorage(t.raw, rows * cols)
+    x = synth.x_f32(cols, 23)
+    y1 = eng.ternary_gemv(st, x, rows, cols)
+    first = st._gpu_rows[1]
+    y2 = eng.ternary_gemv(st, x, rows, cols)
+    assert st._gpu_rows[1] is first and np.array_equal(y1, y2)
+    assert rel_err(y1, orc.ternary_gemv(t.raw, x, rows, cols)) <= TOL
+    xs = np.stack([synth.x_f32(cols, 30 + j) for j in range(3)], axis=1)  # [cols, 3]
+    c = eng.matmul(Tensor((rows, cols), st), torch.from_numpy(np.ascontiguousarray(xs)).cuda()).cpu().numpy()
+    assert st._gpu_rows[1] is first
+    for j in range(3):
+        assert rel_err(c[:, j], orc.ternary_gemv(t.raw, np.ascontiguousarray(xs[:, j]), rows, cols)) <= TOL
+    with pytest.raises(ValueError):
+        eng.ternary_gemv(st, x, rows + 1, cols)
+
+
 def test_merged_qkv_storage_equals_separate_gemvs(eng, orc):
     """A merged Q/K/V storage (MergeQ4Storage) gives, in one GEMV, the three
     projections stacked: rows 0..4095 = Q, then K, then V."""

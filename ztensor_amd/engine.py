@@ -239,7 +239,7 @@ class ROCmEngine:
             raise ValueError("activations must be on the engine's device")
         self.upload_weights([s])
         c = torch.empty((rows, n), dtype=torch.float32, device=self.device)
-        buf = s.gpu_ptr()
+        buf = s.gpu_ptr() if hasattr(s, "gpu_ptr") else None  # ternary: resident per shape, below
         if isinstance(s, MmapStorage):
             return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
@@ -272,6 +272,17 @@ class ROCmEngine:
             else:
                 self.gemm_w4a16_f32(_p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(x), _p(c), rows, k, n,
                                     s.group_size)
+        elif isinstance(s, TernaryStorage):
+            if x.dtype != torch.float32:
+                raise TypeError("ternary matmul takes fp32 activations")
+            w = self._ternary_resident(s, rows, k)
+            xs = x.reshape(k, n)
+            cols = [xs[:, j].contiguous() for j in range(n)] if n > 1 else [xs.reshape(k)]
+            outs = [c] if n == 1 else [torch.empty(rows, dtype=torch.float32, device=self.device) for _ in range(n)]
+            for xj, yj in zip(cols, outs):  # TernaryGEMV per column (compute/ternary_gemv.go:12)
+                self.ternary_gemv_f32(_p(w), _p(xj), _p(yj), rows, k)
+            if n > 1:
+                c.copy_(torch.stack(outs, dim=1))
         elif isinstance(s, (Q4KStorage, Q5KStorage, Q6KStorage, Q5_0Storage)):
             if x.dtype != torch.float32:
                 raise TypeError(f"{type(s).__name__} matmul takes fp32 activations")
@@ -355,14 +366,27 @@ class ROCmEngine:
     # ---------------------------------------------------------------- ternary
 
     def ternary_gemv(self, weights: TernaryStorage, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
-        """TernaryGEMVGPU (compute/ternary_gemv_gpu.go:18-91): host weights and
-        x in, host y out; the weights are repacked to row-aligned bytes and
-        uploaded for the call (the reference does the same per call)."""
-        w = self._to_dev(weights.row_aligned(rows, cols))
+        """TernaryGEMVGPU (compute/ternary_gemv_gpu.go:18-91): host x in, host
+        y out.  The reference repacks and uploads the weights on every call
+        (:34-67); here the row-aligned upload is made once per storage and
+        shape and kept resident (_ternary_resident)."""
+        w = self._ternary_resident(weights, rows, cols)
         xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device)
         y = torch.empty(rows, dtype=torch.float32, device=self.device)
         self.ternary_gemv_f32(_p(w), _p(xd), _p(y), rows, cols)
         return y.cpu().numpy()
+
+    def _ternary_resident(self, s: TernaryStorage, rows: int, cols: int) -> torch.Tensor:
+        """The row-aligned device copy of ternary weights (the layout of
+        compute/ternary_gemv_gpu.go:52-67), uploaded on first use."""
+        cached = getattr(s, "_gpu_rows", None)
+        if cached is not None and cached[0] == (rows, cols):
+            return cached[1]
+        if s.len != rows * cols:
+            raise ValueError(f"ternary weights hold {s.len} values, not [{rows}, {cols}]")
+        w = self._to_dev(s.row_aligned(rows, cols))
+        s._gpu_rows = ((rows, cols), w)  # type: ignore[attr-defined]
+        return w
 
 
 _TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL layouts
