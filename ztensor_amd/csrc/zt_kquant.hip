@@ -241,6 +241,112 @@ __global__ void __launch_bounds__(512) kq_gemv_kernel(const uint8_t* __restrict_
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// Q4_K / Q5_K batch-1 GEMV with one fixed step of 4 super-blocks per wave
+// (16 lanes x 8 bytes of the nibble array a super-block, the lane roles of
+// kq_gemv_kernel with NW = 2), for K <= 64 super-blocks per wave group.
+// Every load - nibbles, Q5_K fifth bits, the 16-byte headers and the
+// activations - is issued before any arithmetic, as buffer loads whose
+// wave-uniform row offset is the scalar offset; lanes past the last
+// super-block read zeros through out-of-range offsets.
+template <int FMT, int R>
+__global__ void __launch_bounds__(1024) kq_steps_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                        float* __restrict__ y, int rows, int nsb) {
+    constexpr int BB = KqFmt<FMT>::bytes;
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int slot = lane >> 4, t = lane & 15;
+    const int byte0 = t * 8, g = byte0 >> 5, o = byte0 & 31;
+    const bool hi_grp = g >= 2;
+    const uint32_t sh = 16u * (uint32_t)(g & 1);
+    const int vlo = 64 * g + o;
+    const int row0 = blockIdx.x * R;
+    const int sb = wave * 4 + slot;
+    const bool ok = sb < nsb;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nsb * 1024, 0x00020000);
+    const uint32_t vq = ok ? (uint32_t)(sb * BB + 16 + byte0) : 0x80000000u;
+    const uint32_t vqh = ok ? (uint32_t)(sb * BB + 144 + o) : 0x80000000u;
+    const uint32_t vh = ok ? (uint32_t)(sb * BB) : 0x80000000u;
+    uint32_t q0[R], q1[R], h0[R], h1[R];
+    u32x4 hdr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t ro = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)(nsb * BB);
+        q0[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vq, ro, 2);  // nontemporal
+        q1[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vq + 4, ro, 2);
+        if constexpr (FMT == 5) {
+            h0[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vqh, ro, 2);
+            h1[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vqh + 4, ro, 2);
+        }
+        hdr[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vh, ro, 0);
+    }
+    const uint32_t xo = ok ? (uint32_t)((sb * 256 + vlo) * 4) : 0x80000000u;
+    const u32x4 xl0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0), xl1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    const u32x4 xh0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 128, 0, 0);
+    const u32x4 xh1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 144, 0, 0);
+    const uint32_t lw[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+    const uint32_t hw[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+    float lo[8], hi[8], slo = 0.f, shi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float a = __uint_as_float(lw[i]), b = __uint_as_float(hw[i]);
+        slo += a;
+        shi += b;
+        lo[i] = a * 16777216.0f;  // low-nibble chain: q * 2^-24
+        hi[i] = b * 1048576.0f;   // high-nibble chain: q * 2^-20
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t dq[2] = {q0[r], q1[r]};
+        float S0 = 0.f, S1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t d = dq[j], d8 = d >> 8;
+            uint32_t l0 = d & 0x000F000Fu, l2 = d8 & 0x000F000Fu, m0 = d & 0x00F000F0u, m2 = d8 & 0x00F000F0u;
+            if constexpr (FMT == 5) {
+                const uint32_t hq = j == 0 ? h0[r] : h1[r];
+                const uint32_t L = hq >> (2 * g), H = hq >> (2 * g + 1);
+                l0 |= (L << 4) & 0x00100010u;  // fifth bits of bytes 0 / 2 -> bit 4 / 20
+                l2 |= (L >> 4) & 0x00100010u;  // bytes 1 / 3
+                m0 |= (H << 8) & 0x01000100u;  // (q << 4) fifth bit -> bit 8 / 24
+                m2 |= H & 0x01000100u;
+            }
+            const half2v a = as_half2(l0), b = as_half2(l2), c = as_half2(m0), e = as_half2(m2);
+            S0 = __builtin_fmaf((float)a.x, lo[4 * j + 0], S0);
+            S0 = __builtin_fmaf((float)b.x, lo[4 * j + 1], S0);
+            S0 = __builtin_fmaf((float)a.y, lo[4 * j + 2], S0);
+            S0 = __builtin_fmaf((float)b.y, lo[4 * j + 3], S0);
+            S1 = __builtin_fmaf((float)c.x, hi[4 * j + 0], S1);
+            S1 = __builtin_fmaf((float)e.x, hi[4 * j + 1], S1);
+            S1 = __builtin_fmaf((float)c.y, hi[4 * j + 2], S1);
+            S1 = __builtin_fmaf((float)e.y, hi[4 * j + 3], S1);
+        }
+        const uint4 h = make_uint4(hdr[r].x, hdr[r].y, hdr[r].z, hdr[r].w);
+        uint32_t scp, mnp;
+        kq_sc_mn(h, hi_grp, sh, scp, mnp);
+        const float sc0 = (float)(scp & 0xFFu), sc1 = (float)((scp >> 8) & 0xFFu);
+        const float mn0 = (float)(mnp & 0xFFu), mn1 = (float)((mnp >> 8) & 0xFFu);
+        const float tq = __builtin_fmaf(sc1, S1, sc0 * S0);
+        const float tm = __builtin_fmaf(mn1, shi, mn0 * slo);
+        const half2v dd = as_half2(h.x);  // (d, dmin)
+        acc[r] = __builtin_fmaf(-(float)dd.y, tm, (float)dd.x * tq);
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int FMT>
+static void launch_kq_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint8_t* W, const float* x, float* y,
+                            int rows, int nsb) {
+    switch (R) {
+        case 16: kq_steps_kernel<FMT, 16><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 8: kq_steps_kernel<FMT, 8><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 4: kq_steps_kernel<FMT, 4><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 2: kq_steps_kernel<FMT, 2><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        default: kq_steps_kernel<FMT, 1><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+    }
+}
+
 template <int FMT, int NW>
 static void launch_kq(int R, dim3 grid, dim3 block, hipStream_t st, const uint8_t* W, const float* x, float* y,
                       int rows, int nsb) {
@@ -266,6 +372,17 @@ static int gemv_kq(const void* W, const float* x, float* y, int M, int K, hipStr
     if (((uintptr_t)x & 15) || ((uintptr_t)W & (FMT == 6 ? 1 : 15))) return (int)hipErrorInvalidValue;
     const int nsb = K / 256;
     const uint8_t* w = static_cast<const uint8_t*>(W);
+    if constexpr (FMT != 6) {
+        // One fixed step per wave for K <= 16384 (32-bit buffer offsets) and
+        // M >= 2048 (below, the loop kernel measured faster): 16 rows a wave
+        // when more than 8 waves split K (measured best at K = 14336), else 8.
+        if (nsb <= 64 && M >= 2048 && (long)M * nsb * KqFmt<FMT>::bytes < 0x7fffffffL) {
+            const int nw = ceil_div(nsb, 4);
+            const int Rs = nw > 8 && (long)ceil_div(M, 16) * nw >= 2048 ? 16 : pick_rows_per_wave(M, nw, 1, 2048);
+            launch_kq_steps<FMT>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, w, x, y, M, nsb);
+            return (int)hipGetLastError();
+        }
+    }
     // 8 bytes of the low-bit array per lane (NW = 2): measured on the
     // Llama-3-8B shapes, 16 bytes per lane (NW = 4) was no faster for
     // Q4_K / Q5_K and 10-15% slower for Q6_K.
