@@ -451,6 +451,95 @@ __global__ void __launch_bounds__(512) q5_0_gemv_kernel(const uint16_t* __restri
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// Q5_0 batch-1 GEMV in the fixed-step form of the Q4_0 kernel: each wave
+// does S steps of 16 blocks (the quad mapping above), all loads issued
+// before any arithmetic as buffer loads with the wave-uniform row offsets
+// as scalar offsets; lanes past the last block read zeros.
+template <int S, int R>
+__global__ void __launch_bounds__(1024) q5_0_steps_kernel(const uint16_t* __restrict__ scales,
+                                                          const uint32_t* __restrict__ qh,
+                                                          const uint32_t* __restrict__ qs, const float* __restrict__ x,
+                                                          float* __restrict__ y, int rows, int kb) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)qs, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)qh, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
+    uint32_t w[S][R], hb[S][R], sc[S][R];
+    u32x4 xa[S], xc[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rq, ok ? (uint32_t)(b * 16 + q * 4) : 0x80000000u,
+                                                           row * (uint32_t)kb * 16u, 2);  // nontemporal
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            hb[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rh, ok ? (uint32_t)(b * 4) : 0x80000000u, row * (uint32_t)kb * 4u, 0);
+            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (uint32_t)(b * 2) : 0x80000000u, row * (uint32_t)kb * 2u, 0);
+        }
+        const uint32_t xo = ok ? (uint32_t)(b * 128 + q * 16) : 0x80000000u;
+        xa[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);       // values 4q .. 4q+3
+        xc[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 64, 0, 0);  // values 16+4q ..
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const float a0 = __uint_as_float(xa[t].x), a1 = __uint_as_float(xa[t].y), a2 = __uint_as_float(xa[t].z),
+                    a3 = __uint_as_float(xa[t].w);
+        const float c0 = __uint_as_float(xc[t].x), c1 = __uint_as_float(xc[t].y), c2 = __uint_as_float(xc[t].z),
+                    c3 = __uint_as_float(xc[t].w);
+        const float base = -16.0f * (((a0 + a1) + (a2 + a3)) + ((c0 + c1) + (c2 + c3)));
+        const float xl[4] = {a0 * 16777216.0f, a1 * 16777216.0f, a2 * 16777216.0f, a3 * 16777216.0f};
+        const float xh[4] = {c0 * 1048576.0f, c1 * 1048576.0f, c2 * 1048576.0f, c3 * 1048576.0f};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[t][r], d8 = d >> 8;
+            const uint32_t el = spread4(hb[t][r] >> (4 * q)), eh = spread4(hb[t][r] >> (16 + 4 * q));
+            const half2v m0 = as_half2((d & 0x000F000Fu) | ((el << 4) & 0x00100010u));
+            const half2v m2 = as_half2((d8 & 0x000F000Fu) | ((el >> 4) & 0x00100010u));
+            const half2v m1 = as_half2((d & 0x00F000F0u) | ((eh << 8) & 0x01000100u));
+            const half2v m3 = as_half2((d8 & 0x00F000F0u) | (eh & 0x01000100u));
+            float v = __builtin_fmaf((float)m0.x, xl[0], base);
+            v = __builtin_fmaf((float)m1.x, xh[0], v);
+            v = __builtin_fmaf((float)m2.x, xl[1], v);
+            v = __builtin_fmaf((float)m3.x, xh[1], v);
+            v = __builtin_fmaf((float)m0.y, xl[2], v);
+            v = __builtin_fmaf((float)m1.y, xh[2], v);
+            v = __builtin_fmaf((float)m2.y, xl[3], v);
+            v = __builtin_fmaf((float)m3.y, xh[3], v);
+            acc[r] = __builtin_fmaf((float)as_half2(sc[t][r]).x, v, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S>
+static void launch_q5_0_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* qh,
+                              const uint32_t* qs, const float* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: q5_0_steps_kernel<S, 8><<<grid, block, 0, st>>>(sc, qh, qs, x, y, rows, kb); break;
+        case 4: q5_0_steps_kernel<S, 4><<<grid, block, 0, st>>>(sc, qh, qs, x, y, rows, kb); break;
+        case 2: q5_0_steps_kernel<S, 2><<<grid, block, 0, st>>>(sc, qh, qs, x, y, rows, kb); break;
+        default: q5_0_steps_kernel<S, 1><<<grid, block, 0, st>>>(sc, qh, qs, x, y, rows, kb); break;
+    }
+}
+
 static int gemv_q5_0(const void* W, const float* x, float* y, int M, int K, int qh_off, int qs_off, hipStream_t st) {
     if (M < 0 || K < 0 || K % 32 != 0 || qh_off < 0 || qs_off < 0) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) {
@@ -466,10 +555,22 @@ static int gemv_q5_0(const void* W, const float* x, float* y, int M, int K, int 
         ((uintptr_t)x & 15))
         return (int)hipErrorInvalidValue;
     const int kb = K / 32;
-    const int nwaves = min(8, ceil_div(kb, 16));
-    const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base);
     const uint32_t* qh = reinterpret_cast<const uint32_t*>(base + qh_off);
+    if ((long)M * kb * 16 < 0x7fffffffL && kb <= 512) {
+        // fixed steps, as for Q4_0: S = 1 for K <= 4096, else 2 with up to 16 waves
+        const int S = kb <= 128 ? 1 : 2;
+        const int nw = ceil_div(kb, 16 * S);
+        const int Rs = pick_rows_per_wave(M, nw, 1, 2048);
+        const uint32_t* qsp = reinterpret_cast<const uint32_t*>(base + qs_off);
+        if (S == 1)
+            launch_q5_0_steps<1>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, qh, qsp, x, y, M, kb);
+        else
+            launch_q5_0_steps<2>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, qh, qsp, x, y, M, kb);
+        return (int)hipGetLastError();
+    }
+    const int nwaves = min(8, ceil_div(kb, 16));
+    const int R = pick_rows_per_wave(M, nwaves, 1, 2048);
     const uint32_t* qs = reinterpret_cast<const uint32_t*>(base + qs_off);
     const dim3 grid(ceil_div(M, R)), block(nwaves * kWave);
     switch (R) {
