@@ -183,6 +183,94 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// The same quad mapping in the fixed-step form of the Q4_0 kernel, for the
+// separated layouts: each wave does S steps of 16 blocks, every load issued
+// before any arithmetic as buffer loads with the wave-uniform row offsets as
+// scalar offsets; lanes past the last block read zeros.
+template <int L, int S, int R>
+__global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __restrict__ base, long data_offset,
+                                                             const float* __restrict__ x, float* __restrict__ y,
+                                                             int rows, int kb) {
+    static_assert(L != kRaw36, "separated layouts only");
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    constexpr uint32_t SB = L == kSep16 ? 2u : 4u;  // bytes per scale
+    const __amdgpu_buffer_rsrc_t rd =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + data_offset), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 d[S][R];
+    uint32_t sc[S][R];
+    u32x4 xa[S], xb[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rd, ok ? (uint32_t)(b * 32 + q * 8) : 0x80000000u,
+                                                           row * (uint32_t)kb * 32u, 2);  // nontemporal
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            const uint32_t so = ok ? (uint32_t)b * SB : 0x80000000u;
+            if constexpr (L == kSep16)
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, row * (uint32_t)kb * SB, 0);
+            else
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, row * (uint32_t)kb * SB, 0);
+        }
+        const uint32_t xo = ok ? (uint32_t)(b * 128 + q * 32) : 0x80000000u;
+        xa[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        xb[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const float xv[8] = {__uint_as_float(xa[t].x), __uint_as_float(xa[t].y), __uint_as_float(xa[t].z),
+                             __uint_as_float(xa[t].w), __uint_as_float(xb[t].x), __uint_as_float(xb[t].y),
+                             __uint_as_float(xb[t].z), __uint_as_float(xb[t].w)};
+        const float m128 = -128.0f * (((xv[0] + xv[1]) + (xv[2] + xv[3])) + ((xv[4] + xv[5]) + (xv[6] + xv[7])));
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s0 = m128, s1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t u = d[t][r][i] ^ 0x80808080u;  // bytes q+128
+                s0 = fmaf((float)(u & 0xffu), xv[4 * i], s0);
+                s1 = fmaf((float)((u >> 8) & 0xffu), xv[4 * i + 1], s1);
+                s0 = fmaf((float)((u >> 16) & 0xffu), xv[4 * i + 2], s0);
+                s1 = fmaf((float)(u >> 24), xv[4 * i + 3], s1);
+            }
+            const float scale = L == kSep16 ? h2f(sc[t][r] & 0xffffu) : __uint_as_float(sc[t][r]);
+            acc[r] = fmaf(scale, s0 + s1, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int L, int S>
+static void launch_q8_steps(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
+                            float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_q8_steps_kernel<L, S, 8><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 4: gemv_q8_steps_kernel<L, S, 4><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        case 2: gemv_q8_steps_kernel<L, S, 2><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+        default: gemv_q8_steps_kernel<L, S, 1><<<g, b, 0, st>>>(base, off, x, y, rows, kb); break;
+    }
+}
+
 template <int L>
 static void launch_q8_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base, long off, const float* x,
                            float* y, int rows, int kb) {
@@ -205,6 +293,21 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
     if (N == 1) {
+        if constexpr (L != kRaw36) {
+            // fixed steps: S = 1 for K <= 4096, 2 for K <= 8192; longer rows
+            // (K = 14336 measured) stay on the loop kernel
+            if ((long)M * kb * 32 < 0x7fffffffL && data_offset < 0x7fffffffL && kb <= 256) {
+                const int S = kb <= 128 ? 1 : 2;
+                const int nws = ceil_div(kb, 16 * S);
+                const int Rs = pick_rows_per_wave(M, nws, 1, 2048);
+                const dim3 g(ceil_div(M, Rs)), blk(nws * kWave);
+                if (S == 1)
+                    launch_q8_steps<L, 1>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
+                else
+                    launch_q8_steps<L, 2>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
+                return (int)hipGetLastError();
+            }
+        }
         const int nw = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
         launch_q8_quad<L>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
