@@ -15,7 +15,11 @@ Also reported on the same JSON line:
                 back-to-back launches over rotating weight copies;
   cpu_baseline  the C restatement of the reference CPU engine's Q4_0 GEMV
                 (GemmF32Q4NT, internal/xblas/gemm_quant.go:81-157) on the
-                host cores, over one layer's seven matrices.
+                host cores, over one layer's seven matrices;
+  configs       every benchmark configuration's shapes and batches as the
+                engine runs them (batched W4A16 / IQ4_NL on their tiled
+                layouts): [format, "KxN", batch, us per matmul, % of peak]
+                (skipped with --no-configs).
 
 `python bench.py --suite` instead prints one line per benchmark
 configuration (W4A16, Q4_0, Q8_0, ternary, IQ4_NL, and the K-quant / Q5_0
@@ -540,6 +544,40 @@ def run_suite(args) -> None:
                 torch.cuda.empty_cache()
 
 
+# The BASELINE configurations as run by the engine's dispatch (batched W4A16
+# and IQ4_NL on their tiled layouts), reported beside the headline.
+CONFIGS = {
+    "1_w4a16_gemv": ["w4a16_c1"],
+    "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
+    "3_ternary_bitnet": ["ternary"],
+    "4_w4a16_llama3_70b": [("w4a16_70b", [1]), "w4a16t_70b"],
+    "5_iq4nl_qwen2_7b": [("iq4nl", [1]), "iq4nlt"],
+}
+
+
+def run_configs(torch, lib) -> dict:
+    """Per-configuration timings (graph replays over rotating weight copies,
+    as --suite): {config: [[format, "KxN", batch, us, pct_of_peak], ...]}."""
+    out = {}
+    names = list(SUITE)
+    for cfg, entries in CONFIGS.items():
+        rows_out = []
+        for e in entries:
+            name, only_batches = (e if isinstance(e, tuple) else (e, None))
+            fmt, shapes, batches = SUITE[name]
+            ci = names.index(name)
+            for si, (rows, K) in enumerate(shapes):
+                for N in batches:
+                    if only_batches is not None and N not in only_batches:
+                        continue
+                    r = _suite_case(torch, lib, fmt, rows, K, N, 0x5EED0000 + 16 * ci + si)
+                    rows_out.append([fmt, f"{K}x{rows}", N, r["us"], r["pct_peak"]])
+                    torch.cuda.empty_cache()
+        out[cfg] = rows_out
+        log(f"bench: config {cfg}: " + ", ".join(f"{f} {s} b{n} {us:.2f}us {p:.1f}%" for f, s, n, us, p in rows_out))
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -549,6 +587,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--no-merged", dest="merged", action="store_false",
                     help="skip the merged Q/K/V + Gate/Up variant reported beside the headline")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="skip the per-configuration timings reported beside the headline")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
     ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8", "w4a16t_b8"],
@@ -568,7 +608,14 @@ def main() -> None:
     if args.pmc_case:
         run_pmc_case(args)
         return
-    print(json.dumps(run_headline(args)), flush=True)
+    result = run_headline(args)
+    if args.configs:
+        import torch
+
+        from ztensor_amd import _lib
+
+        result["configs"] = run_configs(torch, _lib.load())
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":
