@@ -105,6 +105,22 @@ def test_q6k_gemv_on_a_2_byte_aligned_base(lib, orc):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.kq_dequant("q6_k", w.raw, rows * K).view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt,K,off", [("q4_k", 768, 0), ("q5_k", 4352, 0), ("q6_k", 768, 0), ("q6_k", 768, 2),
+                                        ("q6_k", 4352, 2), ("q6_k", 4096, 2)])
+def test_kquant_fixed_step_kernel_odd_superblocks_and_offset_base(lib, orc, fmt, K, off):
+    """2048-row matrices (the Q4_K / Q5_K fixed-step kernel; the Q6_K loop
+    kernel): an odd number of super-blocks per row (3; 17 with a partial
+    last wave), and for Q6_K a base 2 bytes past a 4-byte boundary, so
+    blocks alternate between both misalignments."""
+    rows = 2048
+    say(f"{fmt} steps rows={rows} K={K} off={off}")
+    w = synth.kquant(fmt, rows, K, 78)
+    x = synth.x_f32(K, 78)
+    d = dev(w.raw, pad=off)
+    y = kq_gemv(lib, fmt, d.data_ptr() + off, x, rows, K)
+    assert rel_err(y, orc.gemm_f32_kq_nt(fmt, x, w.raw, 1, rows, K, threads=orc.nthreads())) <= TOL
+
+
 @pytest.mark.parametrize("fmt", KQ)
 def test_kquant_zero_superblocks_give_zero(lib, fmt):
     nbytes = {"q4_k": 144, "q5_k": 176, "q6_k": 210}[fmt]
