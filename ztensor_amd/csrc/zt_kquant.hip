@@ -281,7 +281,8 @@ __global__ void __launch_bounds__(1024) kq_steps_kernel(const uint8_t* __restric
         hdr[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vh, ro, 0);
     }
     const uint32_t xo = ok ? (uint32_t)((sb * 256 + vlo) * 4) : 0x80000000u;
-    const u32x4 xl0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0), xl1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    const u32x4 xl0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+    const u32x4 xl1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
     const u32x4 xh0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 128, 0, 0);
     const u32x4 xh1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 144, 0, 0);
     const uint32_t lw[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
@@ -488,8 +489,9 @@ __global__ void __launch_bounds__(1024) q5_0_steps_kernel(const uint16_t* __rest
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
-            hb[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rh, ok ? (uint32_t)(b * 4) : 0x80000000u, row * (uint32_t)kb * 4u, 0);
-            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (uint32_t)(b * 2) : 0x80000000u, row * (uint32_t)kb * 2u, 0);
+            const uint32_t blk4 = ok ? (uint32_t)(b * 4) : 0x80000000u, blk2 = ok ? (uint32_t)(b * 2) : 0x80000000u;
+            hb[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rh, blk4, row * (uint32_t)kb * 4u, 0);
+            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, blk2, row * (uint32_t)kb * 2u, 0);
         }
         const uint32_t xo = ok ? (uint32_t)(b * 128 + q * 16) : 0x80000000u;
         xa[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);       // values 4q .. 4q+3

@@ -757,7 +757,8 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)stl, (short)0, 0x7fffffff, 0x00020000);
     u32x4 xr[XP];
 #pragma unroll
-    for (int i = 0; i < XP; i++) xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    for (int i = 0; i < XP; i++)
+        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
     // scales: piece e = (tile in WG) * UPW * 8 + unit * 8 + q (8 pieces of 16 bytes a tile-unit)
     u32x4 sr[SP];
 #pragma unroll

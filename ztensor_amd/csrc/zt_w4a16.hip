@@ -377,7 +377,8 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
             const int unit = min(c0 + wave + kMfmaWaves * u, ue - 1);
 #pragma unroll
             for (int t = 0; t < NT; t++)
-                wn[u][t] = ld_stream(reinterpret_cast<const uint4*>(packed + (long)arow[t] * rowbytes + unit * 64 + 16 * lg));
+                wn[u][t] =
+                    ld_stream(reinterpret_cast<const uint4*>(packed + (long)arow[t] * rowbytes + unit * 64 + 16 * lg));
         }
     };
     if (ub < ue) load_w(ub);
@@ -615,7 +616,8 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     const __amdgpu_buffer_rsrc_t rsz = __builtin_amdgcn_make_buffer_rsrc((void*)szp, (short)0, 0x7fffffff, 0x00020000);
     u32x4 xr[XP];
 #pragma unroll
-    for (int i = 0; i < XP; i++) xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    for (int i = 0; i < XP; i++)
+        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
     uint32_t sr[SP];
 #pragma unroll
     for (int i = 0; i < SP; i++) {

@@ -266,7 +266,8 @@ class ROCmEngine:
         elif isinstance(s, (GPTQStorage, AWQStorage)):
             if x.dtype != torch.float16:
                 raise TypeError("W4A16 matmul takes fp16 activations")
-            if n in _TILED_BATCHES and k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29:
+            tiled_ok = k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29
+            if n in _TILED_BATCHES and tiled_ok:
                 wt, sz = self._w4a16_tiled(s, rows, k)
                 self.gemm_w4a16t_f32(_p(wt), _p(sz), _p(x), _p(c), rows, k, n, s.group_size)
             else:
