@@ -19,7 +19,10 @@ Also reported on the same JSON line:
   configs       every benchmark configuration's shapes and batches as the
                 engine runs them (batched W4A16 / IQ4_NL on their tiled
                 layouts): [format, "KxN", batch, us per matmul, % of peak]
-                (skipped with --no-configs).
+                (skipped with --no-configs);
+  configs_cpu   the CPU restatement of each configuration's reference CPU
+                path on one representative shape, about 2 s each (skipped
+                with --no-configs or --no-cpu-baseline).
 
 `python bench.py --suite` instead prints one line per benchmark
 configuration (W4A16, Q4_0, Q8_0, ternary, IQ4_NL, and the K-quant / Q5_0
@@ -578,6 +581,58 @@ def run_configs(torch, lib) -> dict:
     return out
 
 
+def cpu_configs(budget_s: float = 2.0) -> dict:
+    """The CPU restatement of each configuration's reference CPU path on one
+    representative shape, timed on the host (about budget_s each):
+    W4A16 and IQ4_NL dequantize then SgemmSimd (compute/w4a16.go:71-119,
+    compute/cpu_engine.go:1215-1245), Q8_0 GemmF32Q8NT
+    (internal/xblas/gemm_quant.go:163-264), ternary TernaryGEMV
+    (compute/ternary_gemv.go:12-77)."""
+    from oracle import oracle
+    from ztensor_amd import synth
+
+    th = min(16, oracle.nthreads())
+    w1 = synth.w4a16(4096, 4096, 0x5EED0011)
+    x1 = synth.x_f16(4096, 0x5EED0011)
+    q8 = synth.q8_0(14336, 4096, 0x5EED0012)
+    x2 = synth.x_f32(4096, 0x5EED0012)
+    t3 = synth.ternary(6912, 2560, 0x5EED0013)
+    x3 = synth.x_f32(2560, 0x5EED0013)
+    w4 = synth.w4a16(8192, 8192, 0x5EED0014)
+    x4 = synth.x_f16(8192 * 8, 0x5EED0014)
+    i5 = synth.iq4nl(18944, 3584, 0x5EED0015)
+    x5 = synth.x_f16(3584 * 8, 0x5EED0015)
+    cases = {
+        "1_w4a16_gemv": ("w4a16 4096x4096 batch 1, dequantize + SgemmSimd", 1,
+                         synth.algorithmic_bytes("w4a16", 4096, 4096, 1),
+                         lambda: oracle.w4a16_matmul(w1.packed, w1.scales, w1.zeros, x1, 4096, 4096, 1, 128)),
+        "2_q4_0_q8_0_llama3_8b": ("q8_0 4096x14336 batch 1, GemmF32Q8NT", th,
+                                  synth.algorithmic_bytes("q8_0", 14336, 4096, 1),
+                                  lambda: oracle.gemm_f32_q8_nt(x2, q8.raw, 1, 14336, 4096, threads=th)),
+        "3_ternary_bitnet": ("ternary 2560x6912 batch 1, TernaryGEMV", 1, 6912 * 640 + 4 * 2560 + 4 * 6912,
+                             lambda: oracle.ternary_gemv(t3.raw, x3, 6912, 2560)),
+        "4_w4a16_llama3_70b": ("w4a16 8192x8192 batch 8, dequantize + SgemmSimd", 1,
+                               synth.algorithmic_bytes("w4a16", 8192, 8192, 8),
+                               lambda: oracle.w4a16_matmul(w4.packed, w4.scales, w4.zeros, x4, 8192, 8192, 8, 128)),
+        "5_iq4nl_qwen2_7b": ("iq4nl 3584x18944 batch 8, dequantize + SgemmSimd", 1,
+                             synth.algorithmic_bytes("iq4nl", 18944, 3584, 8),
+                             lambda: oracle.iq4nl_matmul(i5.raw, x5, 18944, 3584, 8)),
+    }
+    out = {}
+    for cfg, (case, threads, nbytes, fn) in cases.items():
+        reps, t = 0, 0.0
+        while t < budget_s or reps == 0:
+            t0 = time.perf_counter()
+            fn()
+            t += time.perf_counter() - t0
+            reps += 1
+        us = t / reps * 1e6
+        out[cfg] = {"case": case, "us": round(us, 1), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 3), "threads": threads,
+                    "kind": "port", "calls": reps}
+        log(f"bench: cpu {cfg}: {case}: {us:.0f} us/call on {threads} thread(s)")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -615,6 +670,8 @@ def main() -> None:
         from ztensor_amd import _lib
 
         result["configs"] = run_configs(torch, _lib.load())
+        if args.cpu_baseline:
+            result["configs_cpu"] = cpu_configs()
     print(json.dumps(result), flush=True)
 
 
