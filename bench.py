@@ -313,12 +313,15 @@ def run_merged_step(torch, lib, args) -> dict:
 SUITE = {
     # name: (format, [(rows = N_out, K)], batches)
     "w4a16_c1": ("w4a16", [(4096, 4096)], [1]),
+    "w4a16sz_c1": ("w4a16sz", [(4096, 4096)], [1]),
     "q4_0": ("q4_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q4_0_merged": ("q4_0", [(6144, 4096), (28672, 4096)], [1]),
     "q8_0": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_raw": ("q8_0_raw", [(4096, 4096), (14336, 4096)], [1]),
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
+    "w4a16sz_70b": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [1]),
+    "w4a16_70b_k28672": ("w4a16", [(8192, 28672)], [1]),
     "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
     "iq4nlt": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [8]),
@@ -390,6 +393,18 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: lib.zt_gemm_iq4nlt_f16(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows,
                                                   K, N, s)
         nbytes = synth.algorithmic_bytes("iq4nl", rows, K, N)
+    elif fmt == "w4a16sz":
+        # batch 1 on the packed (scale, zero) dwords (zt_w4a16_pack_szr), built outside the timing
+        w = synth.w4a16(rows, K, seed)
+        sc, zr = dev(w.scales), dev(w.zeros)
+        szr = torch.empty(w.scales.size, dtype=torch.int32, device="cuda")
+        if lib.zt_w4a16_pack_szr(sc.data_ptr(), zr.data_ptr(), rows, K, 128, szr.data_ptr(), s) != 0:
+            raise RuntimeError("zt_w4a16_pack_szr failed")
+        wbufs = [dev(w.packed), szr]
+        x = dev(synth.x_f16(K, seed))
+        fn = lambda wb, y: lib.zt_gemv_w4a16sz_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                   rows, K, 128, s)
+        nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
     elif fmt == "w4a16t":
         # the tiled upload layout (zt_w4a16_tile), built once outside the timing
         w = synth.w4a16(rows, K, seed)
@@ -547,13 +562,14 @@ def run_suite(args) -> None:
                 torch.cuda.empty_cache()
 
 
-# The BASELINE configurations as run by the engine's dispatch (batched W4A16
+# The BASELINE configurations as run by the engine's dispatch (batch-1 W4A16 on
+# packed (scale, zero) dwords, batched W4A16
 # and IQ4_NL on their tiled layouts), reported beside the headline.
 CONFIGS = {
     "1_w4a16_gemv": ["w4a16_c1"],
     "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
     "3_ternary_bitnet": ["ternary"],
-    "4_w4a16_llama3_70b": [("w4a16_70b", [1]), "w4a16t_70b"],
+    "4_w4a16_llama3_70b": ["w4a16sz_70b", "w4a16_70b_k28672", "w4a16t_70b"],
     "5_iq4nl_qwen2_7b": [("iq4nl", [1]), "iq4nlt"],
 }
 

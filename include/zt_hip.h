@@ -162,6 +162,19 @@ void zt_q8gguf_raw_to_gpu(const void* raw, long nblk, void* out);
  * K % group_size == 0, else InvalidValue. */
 int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, const uint16_t* B,
                       float* C, int M, int K, int N, int group_size, zt_stream_t stream);
+/* Batch-1 form of the same MatMulW4A16 (compute/w4a16.go:137-143) on a
+ * packed (scale, zero) array built once at upload: szr is uint32
+ * [M][K/group_size], fp16 scale in the low half and fp16 zero (8.0 when
+ * zeros is NULL) in the high half (zt_w4a16_sz_bytes bytes), built by
+ * zt_w4a16_pack_szr from the zt_gemm_w4a16_f32 scales and zeros.  One
+ * load per row and group instead of two; y[M] = dequant(W) x, the result of
+ * zt_gemm_w4a16_f32 with N = 1.  group_size % 32 == 0, K % group_size == 0,
+ * K <= 32768, M * K / 2 < 2^31, W_packed and x 16-byte aligned, else
+ * InvalidValue.  K == 0 writes zeros. */
+int zt_w4a16_pack_szr(const uint16_t* scales, const uint16_t* zeros, int M, int K, int group_size, uint32_t* szr,
+                      zt_stream_t stream);
+int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* x, float* y, int M, int K,
+                        int group_size, zt_stream_t stream);
 /* Bit-exact with GPTQStorage.Dequantize (tensor/quantized_gptq.go:134-163)
  * and AWQStorage.Dequantize (tensor/quantized_awq.go:118-136). */
 int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,

@@ -209,3 +209,66 @@ def test_engine_batched_w4a16_uses_tiled_layout(lib, orc, side):
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
     assert getattr(st, "_gpu_tiled", None) is not None
+
+
+def _w4t_call(lib, wt, sz, xd, c, rows, K, N, s):
+    lib.call("zt_gemm_w4a16t_f32", wt.data_ptr(), sz.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, 128, s)
+
+
+def test_w4t_split_combine_graph_replays(lib, orc):
+    """A split-K call (zero fill, then atomic adds) captured in a HIP graph:
+    every replay, with eager calls of the same kernel on other operands in
+    between, matches the oracle."""
+    rows, K, N = 4096, 4096, 8
+    w = synth.w4a16(rows, K, 67)
+    x16 = synth.x_f16(K * N, 67)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    wt, sz = tile_dev(lib, w)
+    xd = dev(x16)
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    w2 = synth.w4a16(rows, K, 68)
+    x2 = synth.x_f16(K * N, 68)
+    ref2 = orc.w4a16_matmul(w2.packed, w2.scales, w2.zeros, x2, rows, K, N, 128)
+    wt2, sz2 = tile_dev(lib, w2)
+    xd2 = dev(x2)
+    c2 = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        _w4t_call(lib, wt, sz, xd, c, rows, K, N, cs.cuda_stream)
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _w4t_call(lib, wt, sz, xd, c, rows, K, N, torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        c.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert rel_err(c.cpu().numpy(), ref) <= TOL, rep
+        _w4t_call(lib, wt2, sz2, xd2, c2, rows, K, N, stream())
+        torch.cuda.synchronize()
+        assert rel_err(c2.cpu().numpy(), ref2) <= TOL, rep
+
+
+def test_w4t_split_combine_two_streams(lib, orc):
+    """Split-K calls on two streams at once, repeated, both against the
+    oracle."""
+    rows, K, N = 8192, 8192, 16
+    cases = []
+    for seed in (69, 70):
+        w = synth.w4a16(rows, K, seed)
+        x16 = synth.x_f16(K * N, seed)
+        wt, sz = tile_dev(lib, w)
+        cases.append((wt, sz, dev(x16), torch.empty(rows * N, dtype=torch.float32, device="cuda"),
+                      orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (wt, sz, xd, c, _), s in zip(cases, streams):
+            for _ in range(3):
+                _w4t_call(lib, wt, sz, xd, c, rows, K, N, s.cuda_stream)
+        torch.cuda.synchronize()
+        for i, (_, _, _, c, ref) in enumerate(cases):
+            assert rel_err(c.cpu().numpy(), ref) <= TOL, (rep, i)
+

@@ -219,16 +219,22 @@ static void launch_w4a16_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint3
 
 
 // Batch-1 W4A16 with a fixed S steps of 16 chunks per wave (the quad
-// mapping of w4a16_quad_kernel) for K <= 16384.  Every load of all S steps -
-// weights, the rows' (scale, zero) pairs of each step's group and the
-// activations - is issued before any arithmetic, so a wave waits for one
-// memory round trip.  Buffer loads take the wave-uniform row offsets as
-// scalar offsets; lanes past the last chunk read zeros through out-of-range
-// offsets.
-template <int S, int R>
+// mapping of w4a16_quad_kernel) for K <= 16384 (SZ = false) or K <= 32768
+// (SZ = true).  Every load of all S steps - weights, the rows' (scale, zero)
+// pairs of each step's group and the activations - is issued before any
+// arithmetic, so a wave waits for one memory round trip.  Buffer loads take
+// the wave-uniform row offsets as scalar offsets; lanes past the last chunk
+// read zeros through out-of-range offsets.
+//  * SZ = false: scales and zeros are the stored fp16 arrays, two 2-byte
+//    loads per row and step (zeros == NULL: no records, zero-point 8);
+//  * SZ = true: szr holds one dword per (row, group), scale | zero << 16,
+//    row-major (zt_w4a16_pack_szr): one load per row and step.  At
+//    28672 x 8192 this measured 23.4 us against 27.6 us for the two loads.
+template <int S, int R, bool SZ>
 __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __restrict__ packed,
                                                            const uint16_t* __restrict__ scales,
                                                            const uint16_t* __restrict__ zeros,
+                                                           const uint32_t* __restrict__ szr,
                                                            const uint16_t* __restrict__ x, float* __restrict__ y,
                                                            int rows, int nchunk, int chunks_per_group) {
     __shared__ float red[16 * R];
@@ -237,7 +243,8 @@ __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __res
     const int ngroups = nchunk / chunks_per_group;
     const int row0 = blockIdx.x * R;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)packed, (short)0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(SZ ? (void*)szr : (void*)scales, (short)0,
+                                                                        0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, zeros ? 0x7fffffff : 0,
                                                                         0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nchunk * 64, 0x00020000);
@@ -258,13 +265,18 @@ __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __res
 #pragma unroll
     for (int t = 0; t < S; t++) {
         const int c = (wave * S + t) * 16 + (lane >> 2);
-        const uint32_t goff = c < nchunk ? (uint32_t)((c / chunks_per_group) * 2) : 0x80000000u;
+        const uint32_t g = (uint32_t)(c / chunks_per_group);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t rowg = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)ngroups * 2u;
-            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, goff, rowg, 0);
-            // no zeros array: the buffer has no records and reads 0; zero-point 8 is applied below
-            zr[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rz, goff, rowg, 0);
+            const uint32_t rowg = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)ngroups;
+            if (SZ) {
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, c < nchunk ? g * 4u : 0x80000000u, rowg * 4u, 0);
+            } else {
+                const uint32_t goff = c < nchunk ? g * 2u : 0x80000000u;
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, goff, rowg * 2u, 0);
+                // no zeros array: the buffer has no records and reads 0; zero-point 8 is applied below
+                zr[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rz, goff, rowg * 2u, 0);
+            }
         }
     }
     float acc[R];
@@ -292,23 +304,43 @@ __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __res
             sb = __builtin_fmaf((float)m3.x, (float)x23.y, sb);
             sa = __builtin_fmaf((float)m2.y, (float)x67.x, sa);
             sb = __builtin_fmaf((float)m3.y, (float)x67.y, sb);
-            const float z = zeros ? (float)as_h2(zr[t][r]).x : 8.0f;
+            const half2v szh = as_h2(sc[t][r]);
+            const float z = SZ ? (float)szh.y : zeros ? (float)as_h2(zr[t][r]).x : 8.0f;
             const float tq = __builtin_fmaf(sa, 16777216.0f, __builtin_fmaf(sb, 1048576.0f, -z * xsum));
-            acc[r] = __builtin_fmaf((float)as_h2(sc[t][r]).x, tq, acc[r]);
+            acc[r] = __builtin_fmaf((float)szh.x, tq, acc[r]);
         }
     }
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
-template <int S>
+template <int S, bool SZ>
 static void launch_w4a16_steps(int R, dim3 g, dim3 b, hipStream_t st, const uint32_t* w, const uint16_t* s,
-                               const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+                               const uint16_t* z, const uint32_t* szr, const uint16_t* x, float* y, int rows,
+                               int nchunk, int cpg) {
     switch (R) {
-        case 8: w4a16_steps_kernel<S, 8><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
-        case 4: w4a16_steps_kernel<S, 4><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
-        case 2: w4a16_steps_kernel<S, 2><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
-        default: w4a16_steps_kernel<S, 1><<<g, b, 0, st>>>(w, s, z, x, y, rows, nchunk, cpg); break;
+        case 8: w4a16_steps_kernel<S, 8, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
+        case 4: w4a16_steps_kernel<S, 4, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
+        case 2: w4a16_steps_kernel<S, 2, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
+        default: w4a16_steps_kernel<S, 1, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
     }
+}
+
+// Rows per wave of the batch-1 steps kernel: about 8192 waves (4 at
+// 4096 x 4096 measured 10% faster than 8), but not below 4 where 2048 waves
+// allow it.
+static int w4a16_steps_rows(int M, int nw) {
+    int R = pick_rows_per_wave(M, nw, 1, 8192);
+    if (R < 4) R = min(4, pick_rows_per_wave(M, nw, 1, 2048));
+    return R;
+}
+
+// Packs (scale, zero) into one dword per (row, group), row-major.
+__global__ void w4_szr_kernel(const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+                              uint32_t* __restrict__ szr, long n) {
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const uint16_t z = zeros ? zeros[e] : (uint16_t)0x4800;  // fp16 8.0
+    szr[e] = (uint32_t)scales[e] | ((uint32_t)z << 16);
 }
 
 // ------------------------------------------------------------ MFMA GEMM
@@ -472,7 +504,12 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     if (M < 0 || N < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0 || N > 65535)
         return (int)hipErrorInvalidValue;
     if (M == 0 || N == 0) return (int)hipSuccess;
-    if (W_packed == nullptr || scales == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (C == nullptr) return (int)hipErrorInvalidValue;
+    if (K == 0) {  // empty sums
+        mfma_zero(C, (long)M * N, stream);
+        return (int)hipGetLastError();
+    }
+    if (W_packed == nullptr || scales == nullptr || B == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)W_packed & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1))
         return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
@@ -489,16 +526,15 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
             // fixed steps: S = 1 for K <= 4096, else 2 with up to 16 waves
             const int S = nchunk <= 128 ? 1 : 2;
             const int nw = ceil_div(nchunk, 16 * S);
-            // rows per wave for ~8192 waves (4 at 4096 x 4096 measured 10% faster
-            // than 8), but not below 4 where 2048 waves allow it
-            int R = pick_rows_per_wave(M, nw, 1, 8192);
-            if (R < 4) R = min(4, pick_rows_per_wave(M, nw, 1, 2048));
+            const int R = w4a16_steps_rows(M, nw);
             const dim3 g(ceil_div(M, R)), b(nw * kWave);
             const uint32_t* w = static_cast<const uint32_t*>(W_packed);
             if (S == 1)
-                launch_w4a16_steps<1>(R, g, b, stream, w, scales, zeros, B, C, M, nchunk, group_size / 32);
+                launch_w4a16_steps<1, false>(R, g, b, stream, w, scales, zeros, nullptr, B, C, M, nchunk,
+                                             group_size / 32);
             else
-                launch_w4a16_steps<2>(R, g, b, stream, w, scales, zeros, B, C, M, nchunk, group_size / 32);
+                launch_w4a16_steps<2, false>(R, g, b, stream, w, scales, zeros, nullptr, B, C, M, nchunk,
+                                             group_size / 32);
             return (int)hipGetLastError();
         }
         const int nw = min(8, ceil_div(nchunk, 16));
@@ -512,6 +548,49 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     dim3 grid(ceil_div(M, R), N), block(nwaves * kWave);
     launch_w4a16_gemv<false>(R, grid, block, stream, static_cast<const uint4*>(W_packed), scales, zeros, B, C, N, M,
                              nchunk, group_size / 32);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_w4a16_pack_szr(const uint16_t* scales, const uint16_t* zeros, int M, int K, int group_size,
+                                uint32_t* szr, hipStream_t stream) {
+    if (M < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (scales == nullptr || szr == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1) || ((uintptr_t)szr & 3)) return (int)hipErrorInvalidValue;
+    const long n = (long)M * (K / group_size);
+    w4_szr_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(scales, zeros, szr, n);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* x, float* y, int M,
+                                  int K, int group_size, hipStream_t stream) {
+    if (M < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    if (M == 0) return (int)hipSuccess;
+    if (y == nullptr) return (int)hipErrorInvalidValue;
+    if (K == 0) {  // empty sums (a fill kernel, not a memset node, so the call can be graph-captured)
+        mfma_zero(y, M, stream);
+        return (int)hipGetLastError();
+    }
+    if (W_packed == nullptr || szr == nullptr || x == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_packed & 15) || ((uintptr_t)szr & 3) || ((uintptr_t)x & 15)) return (int)hipErrorInvalidValue;
+    const int nchunk = K / 32;
+    // 32-bit buffer offsets; at most 16 waves of 4 steps
+    if ((long)M * nchunk * 16 >= 0x7fffffffL || nchunk > 1024) return (int)hipErrorInvalidValue;
+    const int S = nchunk <= 128 ? 1 : nchunk <= 256 ? 2 : 4;
+    int nw = ceil_div(nchunk, 16 * S);
+    if (S == 4) nw = (nw + 3) & ~3;  // 14 waves measured 30% slower than 16 at K = 28672
+    const int R = w4a16_steps_rows(M, nw);
+    const dim3 g(ceil_div(M, R)), b(nw * kWave);
+    const uint32_t* w = static_cast<const uint32_t*>(W_packed);
+    const int cpg = group_size / 32;
+    if (S == 1)
+        launch_w4a16_steps<1, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
+    else if (S == 2)
+        launch_w4a16_steps<2, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
+    else
+        launch_w4a16_steps<4, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
     return (int)hipGetLastError();
 }
 
