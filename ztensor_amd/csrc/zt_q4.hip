@@ -565,7 +565,8 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
             const uint32_t* dt = reinterpret_cast<const uint32_t*>(data);
             if ((long)M * kb * 16 < 0x7fffffffL && kb <= 512) {
                 const int S = kb <= 128 ? 1 : 2;
-                const int nw = ceil_div(kb, 16 * S);
+                int nw = ceil_div(kb, 16 * S);
+                if (nw > 12) nw = 16;  // K = 14336: 16 waves measured 3% faster than 14
                 const int Rs = pick_rows_per_wave(M, nw, 1, 2048);
                 if (S == 1)
                     launch_q4_steps<1>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);

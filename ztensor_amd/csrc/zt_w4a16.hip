@@ -525,7 +525,8 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
         if ((long)M * nchunk * 16 < 0x7fffffffL && nchunk <= 512) {
             // fixed steps: S = 1 for K <= 4096, else 2 with up to 16 waves
             const int S = nchunk <= 128 ? 1 : 2;
-            const int nw = ceil_div(nchunk, 16 * S);
+            int nw = ceil_div(nchunk, 16 * S);
+            if (nw > 12) nw = 16;  // whole SIMD sets: 14 waves measured slower than 16
             const int R = w4a16_steps_rows(M, nw);
             const dim3 g(ceil_div(M, R)), b(nw * kWave);
             const uint32_t* w = static_cast<const uint32_t*>(W_packed);
@@ -580,7 +581,11 @@ ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, con
     if ((long)M * nchunk * 16 >= 0x7fffffffL || nchunk > 1024) return (int)hipErrorInvalidValue;
     const int S = nchunk <= 128 ? 1 : nchunk <= 256 ? 2 : 4;
     int nw = ceil_div(nchunk, 16 * S);
-    if (S == 4) nw = (nw + 3) & ~3;  // 14 waves measured 30% slower than 16 at K = 28672
+    // whole SIMD sets: 14 waves measured 3% (K = 14336) to 30% (K = 28672) slower than 16
+    if (nw > 12)
+        nw = 16;
+    else if (S == 4)
+        nw = (nw + 3) & ~3;
     const int R = w4a16_steps_rows(M, nw);
     const dim3 g(ceil_div(M, R)), b(nw * kWave);
     const uint32_t* w = static_cast<const uint32_t*>(W_packed);
