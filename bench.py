@@ -212,7 +212,7 @@ def run_headline(args) -> dict:
     for (name, rows, K), m in zip(LLAMA3_8B, mats):
         if name in ("k", "up"):
             continue  # same shapes as v / gate
-        n = 4 * layers
+        n = 8 * layers
 
         def loop(m=m, n=n):
             s = torch.cuda.current_stream().cuda_stream
@@ -464,7 +464,9 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
     copies = int(min(64, max(2, -(-2 * MALL_BYTES // wbytes) + 1)))
     sets = [wbufs] + [[b.clone() for b in wbufs] for _ in range(copies - 1)]
     ys = [torch.empty(rows * N, dtype=torch.float32, device="cuda") for _ in range(copies)]
-    n = copies * max(1, -(-128 // copies))  # at least 128 launches: shorter graphs measured 5-10% slower per launch
+    # at least 256 launches a graph, two untimed replays, then 10 timed: 60-128-launch
+    # graphs measured 5-10% slower per launch and varied more between runs
+    n = copies * max(1, -(-256 // copies))
 
     def loop():
         nonlocal s
@@ -476,7 +478,8 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
 
     g = graph_of(torch, loop)
     g.replay()
-    us = time_graph(torch, g, 5) * 1e3 / n
+    g.replay()
+    us = time_graph(torch, g, 10) * 1e3 / n
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
             "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}

@@ -276,6 +276,25 @@ def test_iq4nl_gemm_matches_oracle(lib, orc, rows, K, N):
     assert rel_err(c.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("rows,K", [(8193, 4096), (9001, 3616), (8200, 128), (7, 2048), (1, 32), (4099, 3584),
+                                    (3, 4128)])
+def test_iq4nl_f16_gemv_ragged(lib, orc, rows, K):
+    """Batch-1 fp16 IQ4_NL on the fixed-step kernel (K <= 4096: two steps
+    from 8192 rows, one below; a partial last step at K = 3616) and on the
+    loop kernel above 4096 (4128), with row counts that are not a multiple
+    of the rows per wave."""
+    say(f"iq4nl f16 gemv rows={rows} K={K}")
+    w = synth.iq4nl(rows, K, 23)
+    x16 = synth.x_f16(K, 23)
+    nblk = rows * K // 32
+    a = dev(synth_gpu_q4(w.raw, nblk))
+    c = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = dev(x16)
+    lib.call("zt_gemm_iq4nl_f16", a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, 1,
+             lib.zt_q4_gpu_data_offset(nblk), stream())
+    assert rel_err(c.cpu().numpy(), orc.iq4nl_matmul(w.raw, x16, rows, K, 1)) <= TOL
+
+
 @pytest.mark.parametrize("rows,K,N", [(33, 2176, 4), (1, 128, 16), (100, 3584, 12), (64, 384, 8)])
 def test_iq4nl_mfma_ragged(lib, orc, rows, K, N):
     """Batched IQ4_NL on the MFMA path: partial row tiles, a partial last K

@@ -340,6 +340,83 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_kernel(const uint16_t* __
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// The same computation with a fixed S steps of 16 blocks per wave for
+// K <= 4096 (the form of gemv_q4_steps_kernel): every weight, scale and
+// activation load of all steps is issued before the table is built and any
+// product is formed, so a wave waits for one memory round trip where the
+// loop above waits for one per iteration.  Two steps of 4 rows on 4 waves
+// measured 15-17% faster than the loop at 14336-18944 x 3584.
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_iq4nl_h16_steps_kernel(const uint16_t* __restrict__ scales,
+                                                                    const uint32_t* __restrict__ data,
+                                                                    const uint16_t* __restrict__ x,
+                                                                    float* __restrict__ y, int rows, int kb) {
+    __shared__ float red[16 * R];
+    __shared__ uint32_t tbl[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 64, 0x00020000);
+    uint32_t w[S][R], s[S][R];
+    u32x4 xv[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t voff = b < kb ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, row * (uint32_t)kb * 16u, 2);  // nontemporal
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t soff = b < kb ? (uint32_t)(b * 2) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            s[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, row * (uint32_t)kb * 2u, 0);
+        }
+        xv[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, b < kb ? (uint32_t)(b * 64 + q * 16) : 0x80000000u, 0, 0);
+    }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
+        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    // the table is visible to the workgroup; the loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const uint32_t xx[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v = __builtin_amdgcn_fdot2(as_half2(tbl[(w[t][r] >> (8 * j)) & 0xffu]), as_half2(xx[j]), v, false);
+            acc[r] = __builtin_fmaf(h2f(s[t][r]), v, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S>
+static void launch_iq4nl_h16_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc,
+                                   const uint32_t* dt, const uint16_t* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_iq4nl_h16_steps_kernel<S, 8><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 4: gemv_iq4nl_h16_steps_kernel<S, 4><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 2: gemv_iq4nl_h16_steps_kernel<S, 2><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        default: gemv_iq4nl_h16_steps_kernel<S, 1><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+    }
+}
+
 static void launch_iq4nl_h16(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
                              const uint16_t* x, float* y, int rows, int kb) {
     switch (R) {
@@ -578,6 +655,21 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
             // Waves per workgroup chosen so the grid holds about 8192 waves
             // (4 .. 16, at most one per 16 blocks of a row).
+            if ((long)M * kb * 16 < 0x7fffffffL && kb <= 128) {
+                // K <= 4096: fixed steps, 2 steps on 4 waves for M >= 8192, else 1
+                const int S = M >= 8192 ? 2 : 1;
+                int nw = ceil_div(kb, 16 * S);
+                if (nw > 4) nw = (nw + 3) & ~3;  // whole SIMD sets: 8 waves measured 3% faster than 7
+                const int Rs = (long)ceil_div(M, 4) * nw >= 2048 ? 4 : pick_rows_per_wave(M, nw, 1, 2048);
+                const dim3 g(ceil_div(M, Rs)), b(nw * kWave);
+                const uint32_t* dt = reinterpret_cast<const uint32_t*>(data);
+                const uint16_t* xh = reinterpret_cast<const uint16_t*>(B);
+                if (S == 2)
+                    launch_iq4nl_h16_steps<2>(Rs, g, b, st, sc, dt, xh, C, M, kb);
+                else
+                    launch_iq4nl_h16_steps<1>(Rs, g, b, st, sc, dt, xh, C, M, kb);
+                return (int)hipGetLastError();
+            }
             if ((long)M * kb * 16 < 0x7fffffffL) {
                 const int Ri = pick_rows_per_wave(M, 16, 1, 2048);
                 const int groups = ceil_div(M, Ri);
