@@ -330,6 +330,10 @@ SUITE = {
     "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_gguf": ("q8_0_gguf", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q4_0_batched": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q8_0_batched": ("q8_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
 }
 
 
@@ -367,6 +371,25 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
             wbufs = [dev(w.raw)]
             fn = lambda wb, y: lib.zt_gemm_q8_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, s)
         nbytes = synth.algorithmic_bytes("q8_0", rows, K, N)
+    elif fmt in ("q4_0t", "q8_0t"):
+        # the tiled upload layouts (zt_q4_tile / zt_q8_tile), built once outside the timing
+        f = fmt[:2]
+        w = synth.q4_0(rows, K, seed) if f == "q4" else synth.q8_0(rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(getattr(lib, f"zt_{f}_gpu_bytes")(nblk), np.uint8)
+        getattr(lib, f"zt_{f}_raw_to_gpu")(w.raw.ctypes.data, nblk, host.ctypes.data)
+        sep = dev(host)
+        wt = torch.empty(getattr(lib, f"zt_{f}_tiled_bytes")(rows, K), dtype=torch.uint8, device="cuda")
+        st = torch.empty(getattr(lib, f"zt_{f}_tiled_scale_bytes")(rows, K), dtype=torch.uint8, device="cuda")
+        lib.call(f"zt_{f}_tile", sep.data_ptr(), rows, K, getattr(lib, f"zt_{f}_gpu_data_offset")(nblk), wt.data_ptr(),
+                 st.data_ptr(), s)
+        torch.cuda.synchronize()
+        del sep
+        wbufs = [wt, st]
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        gemm = getattr(lib, f"zt_gemm_{f}t_f32")
+        fn = lambda wb, y: gemm(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, s)
+        nbytes = synth.algorithmic_bytes(fmt[:4], rows, K, N)
     elif fmt == "w4a16":
         w = synth.w4a16(rows, K, seed)
         wbufs = [dev(w.packed), dev(w.scales), dev(w.zeros)]

@@ -207,6 +207,38 @@ int zt_w4a16_tile(const void* W_packed, const uint16_t* scales, const uint16_t* 
 int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* B, float* C, int M, int K, int N,
                        int group_size, zt_stream_t stream);
 
+/* ---- Batched Q4_0 / Q8_0 on tiled layouts (MFMA) ------------------------- */
+
+/* The batched products behind KernelRunner.GemmQ4F32 / GemmQ8F32
+ * (internal/gpuapi/kernels.go:45-48, 79-81; CUDA gemm_q4_f32 / gemm_q8_f32,
+ * internal/cuda/kernels/gemm_q4.cu:163-201, gemm_q8.cu:156-182) for batches
+ * of 4, 8, 12 or 16 fp32 activation columns, on upload-time tiled layouts:
+ *   Q4_0: zt_q4_tile builds the IQ4_NL tiled layout (above) from Q4_0's
+ *   separated layout (RawBytesGPU, tensor/quantized.go:168-198), which has
+ *   the same 18-byte block shape: W_tiled zt_q4_tiled_bytes, S_tiled (fp16
+ *   scales) zt_q4_tiled_scale_bytes;
+ *   Q8_0: zt_q8_tile builds it from the separated Q8_0 layout (data_offset =
+ *   zt_q8_gpu_data_offset): tile (rt, u) = rows 16 rt .. +16, blocks
+ *   4u .. 4u+3, 2 KB at ((rt * K/128) + u) * 2048; in half h (1 KB) piece
+ *   l = 16 g + i holds bytes 8g .. 8g+7 of block 4u+2h, then of block
+ *   4u+2h+1, of row 16 rt + i; S_tiled fp32 scales, 256 bytes a tile
+ *   [16 rows][4 blocks].  Rows past M, to the next multiple of 16, are zero.
+ * K % 128 == 0, W_tiled / S_tiled / B 16-byte aligned, N in {4, 8, 12, 16},
+ * else InvalidValue.  Activations are split into two fp16 parts after a
+ * power-of-two normalisation (about 2^-22 relative precision each); split
+ * K ranges add into C with fp32 atomics after a zero fill, so the last bits
+ * of C can vary from run to run. */
+long zt_q4_tiled_bytes(int M, int K);
+long zt_q4_tiled_scale_bytes(int M, int K);
+int zt_q4_tile(const void* A_q4, int M, int K, int data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                    zt_stream_t stream);
+long zt_q8_tiled_bytes(int M, int K);
+long zt_q8_tiled_scale_bytes(int M, int K);
+int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                    zt_stream_t stream);
+
 /* ---- Ternary ----------------------------------------------------------- */
 
 /* Replaces ternary_gemv_f32 (internal/cuda/kernels/ternary_gemv.cu:85-99),

@@ -1,0 +1,281 @@
+"""GPU parity of the batched Q4_0 / Q8_0 MFMA GEMMs on tiled layouts
+(zt_q4_tile / zt_gemm_q4t_f32, zt_q8_tile / zt_gemm_q8t_f32).
+
+The products are the reference's batched Q4_0 / Q8_0 matmuls with fp32
+activations (xblas.GemmF32Q4NT / GemmF32Q8NT, internal/xblas/gemm_quant.go:
+81-264, run here by the oracle's C restatement).  Bars:
+  * the repacks: byte-identical with the layouts restated here in numpy;
+  * the GEMMs: max|y - y_ref| / max|y_ref| <= 1e-3 with fp32 accumulation
+    (measured about 1e-7: the activations are carried as two fp16 parts
+    after a power-of-two normalisation), also for activations far outside
+    the fp16 range, tiny activations and columns of very different scale.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from ztensor_amd import _lib, synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+LLAMA = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return _lib.load()
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rel_err(y, ref) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def weights(fmt: str, rows: int, K: int, seed: int):
+    return synth.q4_0(rows, K, seed) if fmt == "q4" else synth.q8_0(rows, K, seed)
+
+
+def separated(lib, fmt: str, raw: np.ndarray, nblk: int):
+    if fmt == "q4":
+        out = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+        lib.zt_q4_raw_to_gpu(raw.ctypes.data, nblk, out.ctypes.data)
+        return out, lib.zt_q4_gpu_data_offset(nblk)
+    out = np.empty(lib.zt_q8_gpu_bytes(nblk), np.uint8)
+    lib.zt_q8_raw_to_gpu(raw.ctypes.data, nblk, out.ctypes.data)
+    return out, lib.zt_q8_gpu_data_offset(nblk)
+
+
+def tile_ref(fmt: str, raw: np.ndarray, rows: int, K: int):
+    """Q4_0: piece 16 g + i of tile (rt, u) = dword g of blocks 4u .. 4u+3 of
+    row 16 rt + i, fp16 scales [rt][u][16 rows][4 blocks].  Q8_0: half h,
+    piece 16 g + i = bytes 8g .. 8g+7 of blocks 4u+2h and 4u+2h+1 of row
+    16 rt + i, fp32 scales [rt][u][16 rows][4 blocks]."""
+    nt, nu, kb = (rows + 15) // 16, K // 128, K // 32
+    if fmt == "q4":
+        blk = raw.reshape(rows * kb, 18)
+        d = np.zeros((nt * 16, kb, 16), np.uint8)
+        d[:rows] = blk[:, 2:].reshape(rows, kb, 16)
+        sc = np.zeros((nt * 16, kb), np.uint16)
+        sc[:rows] = blk[:, :2].copy().view("<u2").reshape(rows, kb)
+        dt = d.reshape(nt, 16, nu, 4, 4, 4).transpose(0, 2, 4, 1, 3, 5).reshape(-1)
+    else:
+        blk = raw.reshape(rows * kb, 36)
+        d = np.zeros((nt * 16, kb, 32), np.uint8)
+        d[:rows] = blk[:, 4:].reshape(rows, kb, 32)
+        sc = np.zeros((nt * 16, kb), np.float32)
+        sc[:rows] = blk[:, :4].copy().view("<f4").reshape(rows, kb)
+        # d: [rt, i, u, h, b2, g, 8] -> [rt, u, h, g, i, b2, 8]
+        dt = d.reshape(nt, 16, nu, 2, 2, 4, 8).transpose(0, 2, 3, 5, 1, 4, 6).reshape(-1)
+    st = sc.reshape(nt, 16, nu, 4).transpose(0, 2, 1, 3).reshape(-1)
+    return dt, st
+
+
+def tile_dev(lib, fmt, raw, rows, K):
+    nblk = rows * K // 32
+    sep, off = separated(lib, fmt, raw, nblk)
+    a = dev(sep)
+    wt = torch.empty(getattr(lib, f"zt_{fmt}_tiled_bytes")(rows, K), dtype=torch.uint8, device="cuda")
+    st = torch.empty(getattr(lib, f"zt_{fmt}_tiled_scale_bytes")(rows, K), dtype=torch.uint8, device="cuda")
+    lib.call(f"zt_{fmt}_tile", a.data_ptr(), rows, K, off, wt.data_ptr(), st.data_ptr(), stream())
+    torch.cuda.synchronize()
+    return wt, st
+
+
+def run_t(lib, fmt, wt, st, x, rows, K, N):
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, stream())
+    return c.cpu().numpy().reshape(rows, N)
+
+
+def oracle(orc, fmt, raw, x, rows, K, N):
+    """The reference CPU GEMM on x [K, N]: C^T = X^T W^T (GemmF32Q{4,8}NT)."""
+    xt = np.ascontiguousarray(np.asarray(x, np.float32).reshape(K, N).T)
+    f = orc.gemm_f32_q4_nt if fmt == "q4" else orc.gemm_f32_q8_nt
+    return f(xt, raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+@pytest.mark.parametrize("rows,K", [(16, 128), (17, 256), (100, 1024), (1, 384)])
+def test_tile_layout_bytes(lib, fmt, rows, K):
+    w = weights(fmt, rows, K, 81)
+    wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+    dref, sref = tile_ref(fmt, w.raw, rows, K)
+    assert np.array_equal(wt.cpu().numpy(), dref)
+    got = st.cpu().numpy().view("<u2" if fmt == "q4" else "<f4")
+    assert np.array_equal(got.view(np.uint8), sref.view(np.uint8))
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+@pytest.mark.parametrize("rows,K,N", [(16, 128, 4), (17, 256, 8), (33, 2176, 12), (65, 384, 16), (100, 4096, 8),
+                                      (40, 12288, 4), (1, 128, 16), (300, 1024, 16), (129, 640, 12)])
+def test_blockt_ragged(lib, orc, fmt, rows, K, N):
+    print(f"{fmt}t rows={rows} K={K} N={N}", flush=True)
+    w = weights(fmt, rows, K, 82)
+    x = synth.x_f32(K * N, 82).reshape(K, N)
+    wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+    assert rel_err(run_t(lib, fmt, wt, st, x, rows, K, N), oracle(orc, fmt, w.raw, x, rows, K, N)) <= TOL
+
+
+@pytest.mark.parametrize("N", [4, 8, 16])
+@pytest.mark.parametrize("rows,K", LLAMA)
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+def test_blockt_llama3_shapes(lib, orc, fmt, rows, K, N):
+    """The Llama-3-8B shapes at full size against the oracle, and against
+    the VALU batched kernel on the separated layout."""
+    print(f"{fmt}t rows={rows} K={K} N={N}", flush=True)
+    seed = synth.seed_for(2, LLAMA.index((rows, K)))
+    w = weights(fmt, rows, K, seed)
+    x = synth.x_f32(K * N, seed + N).reshape(K, N)
+    wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+    y = run_t(lib, fmt, wt, st, x, rows, K, N)
+    err = rel_err(y, oracle(orc, fmt, w.raw, x, rows, K, N))
+    assert err <= 1e-5, err  # fp32-level: two fp16 parts carry each activation
+    nblk = rows * K // 32
+    sep, off = separated(lib, fmt, w.raw, nblk)
+    a, xd = dev(sep), torch.from_numpy(np.ascontiguousarray(x).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    name = "zt_gemm_q4_f32" if fmt == "q4" else "zt_gemm_q8sep_f32"
+    lib.call(name, a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, off, stream())
+    assert rel_err(y, c.cpu().numpy().reshape(rows, N)) <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+@pytest.mark.parametrize("case", ["huge", "tiny", "mixed_columns", "zero", "one_hot"])
+def test_blockt_activation_ranges(lib, orc, fmt, case):
+    """Activations outside fp16's range (|x| up to 1e7), far below its normal
+    range (1e-7), columns 1e4 apart in scale, all zero, and a single
+    nonzero activation (the result is one weight column times x)."""
+    rows, K, N = 96, 1024, 8
+    w = weights(fmt, rows, K, 83)
+    x = synth.x_f32(K * N, 83).reshape(K, N)
+    if case == "huge":
+        x = x * np.float32(1e7)
+    elif case == "tiny":
+        x = x * np.float32(1e-7)
+    elif case == "mixed_columns":
+        x = x * np.float32(1e4) ** (np.arange(N) % 2).astype(np.float32)
+    elif case == "zero":
+        x = np.zeros_like(x)
+    else:
+        x = np.zeros_like(x)
+        x[517, 3] = np.float32(3.25)
+    x = np.ascontiguousarray(x, np.float32)
+    wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+    y = run_t(lib, fmt, wt, st, x, rows, K, N)
+    ref = oracle(orc, fmt, w.raw, x, rows, K, N)
+    assert np.all(np.isfinite(y))
+    if case == "zero":
+        assert np.array_equal(y, np.zeros_like(y))
+    elif case == "one_hot" and fmt == "q4":
+        assert np.array_equal(y, ref)  # scale * ((q - 8) x): one rounding both ways
+    elif case == "one_hot":
+        # the reference rounds q * scale, then x * that (gemm_quant.go:199-201): one ulp apart at most
+        assert rel_err(y, ref) <= 2.0 ** -22
+    elif case == "mixed_columns":
+        for n in range(N):  # each column on its own scale
+            assert rel_err(y[:, n], ref[:, n]) <= TOL, n
+    else:
+        assert rel_err(y, ref) <= 1e-5
+
+
+def test_blockt_invalid_arguments(lib):
+    t = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    p = t.data_ptr()
+    for fmt in ("q4", "q8"):
+        g = getattr(lib, f"zt_gemm_{fmt}t_f32")
+        for rows, K, N in [(2, 128, 3), (2, 128, 1), (2, 96, 4), (2, 160, 8), (-1, 128, 4)]:
+            assert g(p, p, p, p, rows, K, N, stream()) == 1, (fmt, rows, K, N)
+        assert g(p + 4, p, p, p, 2, 128, 4, stream()) == 1
+        assert g(p, p, p + 4, p, 2, 128, 4, stream()) == 1  # B not 16-byte aligned
+        assert g(p, p, p, p, 0, 128, 4, stream()) == 0  # empty: nothing to do
+        assert getattr(lib, f"zt_{fmt}_tiled_bytes")(2, 96) == -1
+    assert lib.zt_q4_tile(p, 2, 96, 16, p, p, stream()) == 1  # K % 128
+    assert lib.zt_q8_tile(p, 2, 96, 16, p, p, stream()) == 1
+    assert lib.zt_q8_tile(p, 2, 128, 8, p, p, stream()) == 1  # data not 16-byte aligned
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+@pytest.mark.parametrize("side", ["A", "B"])
+def test_engine_batched_uses_tiled_layout(lib, orc, fmt, side):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import Q4Storage, Q8Storage, Tensor
+
+    rows, K, N = 512, 1024, 8
+    w = weights(fmt, rows, K, 84)
+    if fmt == "q4":
+        s = Q4Storage.from_raw(w.raw, rows * K)
+    else:
+        q = w.raw.reshape(-1, 36)
+        s = Q8Storage.from_blocks(q[:, :4].copy().view("<f4").reshape(-1), q[:, 4:].copy().view(np.int8), rows * K)
+    eng = ROCmEngine()
+    x = synth.x_f32(K * N, 84).reshape(K, N)
+    ref = oracle(orc, fmt, w.raw, x, rows, K, N)
+    xk = torch.from_numpy(x).cuda()
+    if side == "A":
+        y = eng.matmul(Tensor((rows, K), s), xk).cpu().numpy()
+        want = ref
+    else:
+        y = eng.matmul(xk.t().contiguous(), Tensor((K, rows), s)).cpu().numpy()
+        want = ref.T
+    assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+def test_blockt_split_graph_replays_and_two_streams(lib, orc, fmt):
+    """Split-K calls (zero fill, then atomic adds) captured in a HIP graph and
+    replayed with eager calls in between, then run on two streams at once:
+    every result matches the oracle."""
+    rows, K, N = 4096, 4096, 8
+    cases = []
+    for seed in (85, 86):
+        w = weights(fmt, rows, K, seed)
+        x = synth.x_f32(K * N, seed).reshape(K, N)
+        wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+        cases.append((wt, st, torch.from_numpy(np.ascontiguousarray(x).reshape(-1)).cuda(),
+                      torch.empty(rows * N, dtype=torch.float32, device="cuda"),
+                      oracle(orc, fmt, w.raw, x, rows, K, N).reshape(-1)))
+
+    def call(case, s):
+        wt, st, xd, c, _ = case
+        lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, s)
+
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        call(cases[0], cs.cuda_stream)
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(cases[0], torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        cases[0][3].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert rel_err(cases[0][3].cpu().numpy(), cases[0][4]) <= TOL, rep
+        call(cases[1], stream())
+        torch.cuda.synchronize()
+        assert rel_err(cases[1][3].cpu().numpy(), cases[1][4]) <= TOL, rep
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for case, s in zip(cases, streams):
+            for _ in range(3):
+                call(case, s.cuda_stream)
+        torch.cuda.synchronize()
+        for i, case in enumerate(cases):
+            assert rel_err(case[3].cpu().numpy(), case[4]) <= TOL, (rep, i)

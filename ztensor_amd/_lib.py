@@ -59,6 +59,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_w4a16_sz_bytes": (L, [I, I, I]),
     "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),
     "zt_gemm_w4a16t_f32": (I, [P, P, P, P, I, I, I, I, P]),
+    "zt_q4_tiled_bytes": (L, [I, I]),
+    "zt_q4_tiled_scale_bytes": (L, [I, I]),
+    "zt_q4_tile": (I, [P, I, I, I, P, P, P]),
+    "zt_gemm_q4t_f32": (I, [P, P, P, P, I, I, I, P]),
+    "zt_q8_tiled_bytes": (L, [I, I]),
+    "zt_q8_tiled_scale_bytes": (L, [I, I]),
+    "zt_q8_tile": (I, [P, I, I, L, P, P, P]),
+    "zt_gemm_q8t_f32": (I, [P, P, P, P, I, I, I, P]),
     "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),
     "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
     "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),

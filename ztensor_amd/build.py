@@ -31,13 +31,20 @@ COMMON = [
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# Per-source device flags.  The tiled block MFMA kernels consume every MFMA
+# result in VALU right away; the VGPR form of the MFMAs avoids copying each
+# result out of the accumulation registers first.
+EXTRA = {"zt_blockt.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *COMMON, *(DEVICE if src.suffix == ".hip" else []), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *(DEVICE if src.suffix == ".hip" else []), *EXTRA.get(src.name, []), "-c", str(src),
+           "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)

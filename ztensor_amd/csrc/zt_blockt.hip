@@ -1,0 +1,411 @@
+// Small-batch Q4_0 / Q8_0 GEMM on tiled upload layouts with MFMA, fp32
+// activations (N in {4, 8, 12, 16}, K % 128 == 0), for gfx950.
+//
+// The reference computes these products with fp32 activations on its CPU
+// engine (xblas.GemmF32Q4NT / GemmF32Q8NT, internal/xblas/gemm_quant.go:81-264)
+// and with the per-row CUDA kernels gemm_q4_f32 / gemm_q8_f32
+// (internal/cuda/kernels/gemm_q4.cu:117-201, gemm_q8.cu:121-182).  Here the
+// batched product runs on v_mfma_f32_16x16x32_f16 instead:
+//  * Weights are exact small integers in fp16: a Q4_0 nibble q or a Q8_0
+//    byte q + 128 becomes the fp16 subnormal q * 2^-24 with masks (Q4_0) or
+//    byte permutes (Q8_0), and the products are exact in fp32.  The offset
+//    (8 for Q4_0, 128 for Q8_0) is one more MFMA a step, with every A element
+//    -off * 2^-24 (an fp16 subnormal), whose result is the C input of the
+//    weight MFMAs of both tiles: each step's D is 2^-24 sum((q - off) x), and
+//    one v_fma_mix per output takes the block's fp16 scale straight from LDS.
+//  * fp32 activations are split into two fp16 parts, x = hi + lo, after a
+//    power-of-two normalisation per workgroup (max |x| of the workgroup's K
+//    range maps into [2^14, 2^15)), so each activation is carried to about
+//    2^-22 relative precision over the whole fp32 range; the normalisation
+//    is undone exactly at the end.  For N <= 8 the hi parts sit in B columns
+//    0..N-1 and the lo parts in columns 8..8+N-1 of the same MFMA, and the
+//    two column halves are added once at the end; for N > 8 hi and lo are
+//    two MFMAs into one accumulator.
+//  * Each 16-row x 128-K tile is one contiguous block in MFMA lane order
+//    (1 KB for Q4_0, 2 KB for Q8_0), so a wave's weight load is contiguous;
+//    the workgroup structure (4 waves x 32 rows, UPW 128-K units, XCD-aware
+//    K split with fp32 atomics after a zero fill, X and scales staged behind
+//    an LDS-only barrier while the weights stream) follows the tiled W4A16
+//    and IQ4_NL kernels.
+//
+// Tiled layouts (ntiles = ceil(M / 16), nunits = K / 128, tile-unit tu =
+// rt * nunits + u; rows past M are zero):
+//  * Q4_0 (zt_q4_tile): the IQ4_NL tiled layout applied to Q4_0's separated
+//    layout, which has the same 18-byte block structure: data 1 KB at
+//    tu * 1024, lane l = 16 g + i holds dword g of blocks 4u .. 4u+3 of row
+//    16 rt + i; scales fp16 [16 rows][4 blocks] at tu * 128.
+//  * Q8_0 (zt_q8_tile): data 2 KB at tu * 2048; half h (1 KB) lane
+//    l = 16 g + i holds bytes 8g .. 8g+7 of block 4u + 2h, then of block
+//    4u + 2h + 1, of row 16 rt + i; scales fp32 [16 rows][4 blocks] at tu * 256.
+#include <type_traits>
+
+#include "zt_mfma.h"
+
+namespace zt {
+
+enum class BlkFmt { Q4_0, Q8_0 };
+
+__global__ void q8t_tile_kernel(const uint2* __restrict__ data, const float* __restrict__ scales,
+                                u32x4* __restrict__ wt, float* __restrict__ st, int rows, int nunits, long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63), h = (int)((p >> 6) & 1), i = lane & 15, g = lane >> 4;
+    const long tu = p >> 7;
+    const int u = (int)(tu % nunits);
+    const long row = (tu / nunits) * 16 + i;
+    const long nb = (long)nunits * 4;  // blocks per row
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < rows) {
+        const long b0 = row * nb + 4L * u + 2 * h;
+        const uint2 a = data[b0 * 4 + g], b = data[(b0 + 1) * 4 + g];
+        v = (u32x4){a.x, a.y, b.x, b.y};
+    }
+    wt[p] = v;
+    if (h == 0) st[tu * 64 + i * 4 + g] = row < rows ? scales[row * nb + 4L * u + g] : 0.0f;
+}
+
+// LDS row of chunk-relative activation row r (K index within the
+// workgroup's range).  Within each 128-K unit, the 8 activations that lane
+// group g of MFMA step s multiplies sit in rows 32 g + 8 s .. +7, in the
+// order of the A operand's halves, so the two transposing reads of a step
+// address 8 consecutive rows and the four lane groups are 32 rows apart.
+template <BlkFmt F>
+__device__ __forceinline__ int blkt_lds_row(int r) {
+    const int u = r >> 7, b = (r >> 5) & 3, e = r & 31;
+    int g, j;
+    if constexpr (F == BlkFmt::Q4_0) {
+        // A halves of lane group g: elements 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3, 4g+17, 4g+19
+        const int i4 = e & 3;
+        g = (e & 15) >> 2;
+        j = (i4 & 1) * 4 + (i4 >> 1) + ((e >> 4) << 1);
+    } else {
+        g = e >> 3;  // elements 8g .. 8g+7 in order
+        j = e & 7;
+    }
+    return (u << 7) + (g << 5) + (b << 3) + j;
+}
+
+template <BlkFmt F, int UPW, int N>
+__global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict__ wt, const void* __restrict__ stl,
+                                                        const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                        int K) {
+    constexpr int W = 4;
+    constexpr int KC = 128 * UPW;
+    constexpr int RW = 32 * W;
+    constexpr int NPL = N <= 8 ? 1 : 2;                 // staged fp16 planes (hi/lo in columns, or two planes)
+    constexpr int XPB = mfma_chunk_xbytes(KC, 16);      // one plane: 16 fp16 columns, 2 pad rows per 32
+    constexpr int PPR = N / 4;                          // 16-byte pieces per fp32 activation row
+    constexpr int XP = (KC * PPR + W * 64 - 1) / (W * 64);
+    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : 4;       // scale bytes
+    constexpr int PPT = 4 * SB;                         // 16-byte scale pieces per tile-unit
+    constexpr int SPC = (RW / 16) * UPW * PPT;
+    constexpr int SP = (SPC + W * 64 - 1) / (W * 64);
+    constexpr int WL = F == BlkFmt::Q4_0 ? 1 : 2;       // 16-byte weight loads per lane per tile-unit
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    float* wmax = reinterpret_cast<float*>(smem + NPL * XPB);  // per-wave max |x|
+    char* ssm = smem + NPL * XPB + 16;                            // block scales
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int nunits = K / 128;
+    int byi = blockIdx.y, bxi = blockIdx.x;
+    if ((gridDim.x & 7) == 0) {
+        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
+        byi = j % gridDim.y;
+        bxi = (id & 7) + 8 * (j / gridDim.y);
+    }
+    const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
+    const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
+    const int ntiles = (rows + 15) / 16;
+    const int npieces = (u1 - u0) * 128 * PPR;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)stl, (short)0, 0x7fffffff, 0x00020000);
+    u32x4 xr[XP];
+#pragma unroll
+    for (int i = 0; i < XP; i++)
+        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    u32x4 sr[SP];
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64, tw = e / (UPW * PPT), u = (e / PPT) % UPW, q = e % PPT;
+        const int rt = rw0 / 16 + tw;
+        const bool ok = e < SPC && rt < ntiles && u0 + u < u1;
+        const uint32_t off = ok ? (uint32_t)(((rt * nunits + u0 + u) * PPT + q) * 16) : 0x80000000u;
+        sr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    }
+    uint4 w[UPW][2][WL];
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        const int unit = min(u0 + u, u1 - 1);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = min(row0 / 16 + t, ntiles - 1);
+#pragma unroll
+            for (int h = 0; h < WL; h++) w[u][t][h] = ld_stream(wt + (((long)rt * nunits + unit) * WL + h) * 64 + lane);
+        }
+    }
+    // workgroup max |x| -> power-of-two normalisation c = 2^sh
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XP; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) m = fmaxf(m, fabsf(__uint_as_float(xr[i][c])));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) wmax[wave] = m;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int sh = 0;
+    if (m > 0.0f && m <= 3.402823466e38f) {
+        int e2;
+        (void)frexpf(m, &e2);  // m = f 2^e2, f in [0.5, 1)
+        sh = min(127, 15 - e2);
+    }
+    const float cs = ldexpf(1.0f, sh);
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+        const int p = tid + i * W * 64;
+        if (p < npieces) {
+            const int r = p / PPR, c4 = (p % PPR) * 4;
+            // Q4_0: the activations of high-nibble elements (16..31 of a block)
+            // are staged at 1/16, as their A halves are q * 2^-20
+            const float cr = (F == BlkFmt::Q4_0 && (r & 16)) ? cs * 0.0625f : cs;
+            const int base = mfma_xrow(blkt_lds_row<F>(r), 16);
+            uint32_t hv[2], lv[2];
+#pragma unroll
+            for (int c = 0; c < 4; c += 2) {
+                const float v0 = __uint_as_float(xr[i][c]) * cr, v1 = __uint_as_float(xr[i][c + 1]) * cr;
+                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+                const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+                hv[c / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lv[c / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            const int lo_off = NPL == 1 ? 16 : XPB;
+            if (N % 8 != 0 && c4 == N - 4) {
+                // last piece of a row: it also zeroes the unused columns up to the
+                // next multiple of 8, so every lane of a transposing read reads data
+                *reinterpret_cast<uint4*>(smem + base + 2 * c4) = make_uint4(hv[0], hv[1], 0u, 0u);
+                *reinterpret_cast<uint4*>(smem + lo_off + base + 2 * c4) = make_uint4(lv[0], lv[1], 0u, 0u);
+            } else {
+                *reinterpret_cast<uint2*>(smem + base + 2 * c4) = make_uint2(hv[0], hv[1]);
+                *reinterpret_cast<uint2*>(smem + lo_off + base + 2 * c4) = make_uint2(lv[0], lv[1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < SP; i++) {
+        const int e = tid + i * W * 64;
+        if (e < SPC) *reinterpret_cast<u32x4*>(ssm + e * 16) = sr[i];
+    }
+    // LDS writes visible to the workgroup; the weight loads stay in flight.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // transposing-read address of this lane for unit u, step s: X row
+    // 128u + 32 lg + 8s + jq (and + 4 for the second read), columns 4 qq ..
+    // 4 qq + 3; mfma_xrow of that row is this lane base plus (136u + 8s) * 32.
+    const int jq = li >> 2, qq = li & 3;
+    const int lbase = (34 * lg + jq) * 32 + 8 * qq;
+    // -off * 2^-24 in every A element (fp16 subnormal bits 0x8008 / 0x8080):
+    // one MFMA a step gives -off * 2^-24 * sum(x), the C input of both
+    // tiles' weight MFMAs, so each step's D is 2^-24 * sum((q - off) x)
+    // (Q4_0: -8 * 2^-20 in the halves of high-nibble elements, whose
+    // activations are staged at 1/16)
+    const _Float16 ol = __builtin_bit_cast(_Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : 0x8080u));
+    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)0x8080u);
+    const half8v aoff = F == BlkFmt::Q4_0 ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
+                                          : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
+    float4v acc[2];
+    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+        if (u0 + u < u1) {
+            // the 4 block scales of rows 4 lg + i of each tile for this unit
+            using SV = typename std::conditional<F == BlkFmt::Q4_0, uint2, float4>::type;
+            SV sc[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    sc[t][i] = reinterpret_cast<const SV*>(ssm)[((2 * wave + t) * UPW + u) * 16 + 4 * lg + i];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                half8v bv[NPL];
+#pragma unroll
+                for (int pl = 0; pl < NPL; pl++) {
+                    const int o = pl * XPB + (136 * u + 8 * s) * 32;
+                    const short4v ba = tr_read_b64(smem, lbase + o), bb = tr_read_b64(smem, lbase + o + 128);
+                    bv[pl] = __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
+                }
+                float4v dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bv[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (NPL == 2) dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bv[1], dn, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    u32x4 av;
+                    if constexpr (F == BlkFmt::Q4_0) {
+                        const uint4 q = w[u][t][0];
+                        const uint32_t dw = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
+                        const uint32_t d8 = dw >> 8;  // halves: q 2^-24 (low nibbles), q 2^-20 (high)
+                        av = (u32x4){dw & 0x000F000Fu, dw & 0x00F000F0u, d8 & 0x000F000Fu, d8 & 0x00F000F0u};
+                    } else {
+                        const uint4 q = w[u][t][s >> 1];
+                        const uint32_t da = ((s & 1) ? q.z : q.x) ^ 0x80808080u;
+                        const uint32_t db = ((s & 1) ? q.w : q.y) ^ 0x80808080u;
+                        av = (u32x4){__builtin_amdgcn_perm(da, da, 0x0C010C00u), __builtin_amdgcn_perm(da, da, 0x0C030C02u),
+                                     __builtin_amdgcn_perm(db, db, 0x0C010C00u), __builtin_amdgcn_perm(db, db, 0x0C030C02u)};
+                    }
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[0], dn, 0, 0, 0);
+                    if constexpr (NPL == 2)
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[1], d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float sv;
+                        if constexpr (F == BlkFmt::Q4_0) {
+                            const uint32_t h2 = (s < 2) ? sc[t][i].x : sc[t][i].y;
+                            sv = h2f((s & 1) ? (uint16_t)(h2 >> 16) : (uint16_t)(h2 & 0xffffu));
+                        } else {
+                            sv = s == 0 ? sc[t][i].x : s == 1 ? sc[t][i].y : s == 2 ? sc[t][i].z : sc[t][i].w;
+                        }
+                        acc[t][i] = fmaf(sv, d[i], acc[t][i]);
+                    }
+                }
+            }
+        }
+    }
+    // y = 2^24 * acc / c: the 2^-24 of the weight encoding and the
+    // activation normalisation undone in one exact power-of-two scaling
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v = acc[t][i];
+            if constexpr (NPL == 1) v += __shfl_xor(v, 8);  // hi columns n + lo columns 8 + n
+            acc[t][i] = ldexpf(v, 24 - sh);
+        }
+    if (li < N) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = row0 + 16 * t + 4 * lg + i;
+                if (row < rows) {
+                    if (gridDim.y > 1)
+                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
+                    else
+                        y[(long)row * N + li] = acc[t][i];
+                }
+            }
+    }
+}
+
+template <BlkFmt F, int UPW, int N>
+static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y, int M,
+                        int K) {
+    constexpr int NPL = N <= 8 ? 1 : 2;
+    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : 4;
+    const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
+    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, x, y, M, K);
+}
+
+template <BlkFmt F, int N>
+static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y,
+                          int M, int K) {
+    if constexpr (F == BlkFmt::Q4_0) {
+        if (upw == 8) {
+            launch_blkt<F, 8, N>(g, st, wt, sc, x, y, M, K);
+            return;
+        }
+    }
+    if (upw >= 4)
+        launch_blkt<F, 4, N>(g, st, wt, sc, x, y, M, K);
+    else
+        launch_blkt<F, 2, N>(g, st, wt, sc, x, y, M, K);
+}
+
+template <BlkFmt F>
+static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                     hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0) return (int)hipErrorInvalidValue;
+    if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
+        return (int)hipErrorInvalidValue;
+    constexpr long SB = F == BlkFmt::Q4_0 ? 2 : 4;
+    if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
+    const int nunits = K / 128;
+    const int gx = ceil_div(M, 128);
+    // the largest K range per workgroup that still gives >= 256 workgroups
+    // (Q8_0 at most 4 units: its weights take twice the registers)
+    int upw = F == BlkFmt::Q4_0 ? 8 : 4;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    const dim3 g(gx, ceil_div(nunits, upw));
+    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    const uint4* wt = static_cast<const uint4*>(W_tiled);
+    switch (N) {
+        case 4: launch_blkt_n<F, 4>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
+        case 8: launch_blkt_n<F, 8>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
+        case 12: launch_blkt_n<F, 12>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
+        default: launch_blkt_n<F, 16>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+// The IQ4_NL tile repack (zt_q4.hip) moves bytes and scales only, so it
+// serves Q4_0's separated layout, which has the same 18-byte block shape.
+extern "C" int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, void* W_tiled, void* S_tiled,
+                             hipStream_t stream);
+
+ZT_EXPORT long zt_q4_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 2);
+}
+
+ZT_EXPORT long zt_q4_tiled_scale_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 32) * 2;
+}
+
+ZT_EXPORT int zt_q4_tile(const void* A_q4, int M, int K, int data_offset, void* W_tiled, void* S_tiled,
+                         hipStream_t stream) {
+    return zt_iq4nl_tile(A_q4, M, K, data_offset, W_tiled, S_tiled, stream);
+}
+
+ZT_EXPORT int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                              hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, stream);
+}
+
+ZT_EXPORT long zt_q8_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * K;
+}
+
+ZT_EXPORT long zt_q8_tiled_scale_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 32) * 4;
+}
+
+ZT_EXPORT int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled,
+                         hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0 || data_offset < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (A_q8 == nullptr || W_tiled == nullptr || S_tiled == nullptr) return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(A_q8);
+    if (((uintptr_t)base & 3) || ((uintptr_t)(base + data_offset) & 15) || ((uintptr_t)W_tiled & 15) ||
+        ((uintptr_t)S_tiled & 15))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 128;
+    q8t_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        reinterpret_cast<const uint2*>(base + data_offset), reinterpret_cast<const float*>(base),
+        static_cast<u32x4*>(W_tiled), static_cast<float*>(S_tiled), M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                              hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q8_0>(W_tiled, S_tiled, B, C, M, K, N, stream);
+}

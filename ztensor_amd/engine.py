@@ -240,6 +240,24 @@ class ROCmEngine:
         s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
         return wt, st
 
+    def _block_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, fmt: str) -> tuple[torch.Tensor, torch.Tensor]:
+        """The tiled copy of uploaded Q4_0 ("q4") or Q8_0 ("q8") weights for
+        batches of 4-16 fp32 columns, built on the device from the separated
+        upload on the first batched call and kept beside it (batch 1 reads
+        the separated layout)."""
+        cached = getattr(s, "_gpu_tiled", None)
+        if cached is not None and cached[0] == (rows, k):
+            return cached[1], cached[2]
+        nbytes = getattr(self.lib, f"zt_{fmt}_tiled_bytes")(rows, k)
+        sbytes = getattr(self.lib, f"zt_{fmt}_tiled_scale_bytes")(rows, k)
+        if nbytes < 0 or sbytes < 0:
+            raise ValueError(f"{fmt} tiled layout: unsupported shape [{rows}, {k}]")
+        wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        st = torch.empty(sbytes, dtype=torch.uint8, device=self.device)
+        self.lib.call(f"zt_{fmt}_tile", _p(buf.tensor), rows, k, buf.data_offset, _p(wt), _p(st), self._s)
+        s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
+        return wt, st
+
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
         n = 1 if x.dim() == 1 else x.shape[1]
@@ -251,7 +269,10 @@ class ROCmEngine:
         if isinstance(s, MmapStorage):
             return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
-            if x.dtype == torch.float32:
+            if x.dtype == torch.float32 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
+                wt, st = self._block_tiled(s, buf, rows, k, "q4")
+                self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
+            elif x.dtype == torch.float32:
                 self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             elif x.dtype == torch.float16:
                 self.gemm_q4_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
@@ -270,6 +291,10 @@ class ROCmEngine:
         elif isinstance(s, Q8Storage):
             if x.dtype != torch.float32:
                 raise TypeError("Q8_0 matmul takes fp32 activations")
+            if n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
+                wt, st = self._block_tiled(s, buf, rows, k, "q8")
+                self.lib.call("zt_gemm_q8t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
+                return c
             self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
         elif isinstance(s, (GPTQStorage, AWQStorage)):
             if x.dtype != torch.float16:
@@ -404,7 +429,7 @@ class ROCmEngine:
         return w
 
 
-_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL layouts
+_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL / Q4_0 / Q8_0 layouts
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
