@@ -31,10 +31,11 @@ COMMON = [
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-# Per-source device flags.  The tiled block MFMA kernels consume every MFMA
-# result in VALU right away; the VGPR form of the MFMAs avoids copying each
-# result out of the accumulation registers first.
-EXTRA = {"zt_blockt.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Per-source device flags.  The tiled MFMA kernels consume MFMA results in
+# VALU right away; the VGPR form of the MFMAs avoids copying each result out
+# of the accumulation registers first.
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+EXTRA = {"zt_blockt.hip": _VGPR_MFMA, "zt_q4.hip": _VGPR_MFMA, "zt_w4a16.hip": _VGPR_MFMA}
 
 
 def sources() -> list[Path]:

@@ -308,12 +308,6 @@ static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc,
 template <BlkFmt F, int N>
 static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y,
                           int M, int K) {
-    if constexpr (F == BlkFmt::Q4_0) {
-        if (upw == 8) {
-            launch_blkt<F, 8, N>(g, st, wt, sc, x, y, M, K);
-            return;
-        }
-    }
     if (upw >= 4)
         launch_blkt<F, 4, N>(g, st, wt, sc, x, y, M, K);
     else
@@ -333,10 +327,13 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     const int nunits = K / 128;
     const int gx = ceil_div(M, 128);
-    // the largest K range per workgroup that still gives >= 256 workgroups
-    // (Q8_0 at most 4 units: its weights take twice the registers)
-    int upw = F == BlkFmt::Q4_0 ? 8 : 4;
-    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    // the largest K range per workgroup, up to 4 units, that still gives
+    // >= 256 (Q4_0) or >= 512 (Q8_0) workgroups; measured at the Llama-3-8B
+    // shapes, batches 8 and 16: 8 units were 3-14% slower for Q4_0 and 8-40%
+    // for Q8_0, and 8 waves a workgroup were slower at every unit count
+    int upw = 4;
+    const long minwg = F == BlkFmt::Q4_0 ? 256 : 512;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < minwg) upw >>= 1;
     const dim3 g(gx, ceil_div(nunits, upw));
     if (g.y > 1) mfma_zero(C, (long)M * N, stream);
     const uint4* wt = static_cast<const uint4*>(W_tiled);

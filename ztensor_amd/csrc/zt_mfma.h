@@ -83,6 +83,17 @@ __device__ __forceinline__ half8v mfma_b_operand(char* smem, const MfmaBRole& ro
     return __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
 }
 
+// B operand from two transposing reads at LDS byte offsets a and a + db.
+// The tiled kernels pass a = (lane part) + (compile-time part): every row a
+// step reads lies in one 32-row segment of the padded chunk, so the pad term
+// of mfma_xrow is a per-unit constant and the whole offset folds into the
+// instructions' immediate field.  Columns >= N read neighbouring LDS bytes;
+// they only reach D columns >= N, which are never stored.
+__device__ __forceinline__ half8v mfma_b_pair(char* smem, int a, int db) {
+    const short4v ba = tr_read_b64(smem, a), bb = tr_read_b64(smem, a + db);
+    return __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
+}
+
 // Sums the waves' partial tiles and stores C rows row0 .. row0+31, columns < N.
 // acc[t][i] of lane l holds row 16t + 4*(l/16) + i, column l%16 (the MFMA
 // D layout).  Uses smem as scratch; the caller has passed a barrier after

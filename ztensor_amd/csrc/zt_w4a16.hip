@@ -739,9 +739,11 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     }
     // LDS writes visible to the workgroup; the weight loads stay in flight.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const MfmaBRole ro(li, N);
-    const int offa = (ro.jq == 0) ? 0 : (ro.jq == 1) ? 4 : (ro.jq == 2) ? 1 : 5;  // rows {0,4,1,5}
-    const int offb = offa + 2;                                                      // rows {2,6,3,7}
+    const int jq = li >> 2;
+    const int offa = (jq == 0) ? 0 : (jq == 1) ? 4 : (jq == 2) ? 1 : 5;  // rows {0,4,1,5}, then + 2: {2,6,3,7}
+    // step s of unit u reads X rows 128u + 32lg + 8s + offa (+ 2), whose
+    // padded LDS offset is (34lg + offa) 2N + (136u + 8s) 2N
+    const int lbase = (34 * lg + offa) * 2 * N + 8 * (li & 3);
     const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
     float4v acc[2];
     acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
@@ -752,7 +754,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
             d[0] = d[1] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                const half8v bv = mfma_b_operand(smem, ro, u * 128 + 32 * lg + 8 * s, offa, offb, N, XB);
+                const half8v bv = mfma_b_pair(smem, lbase + (136 * u + 8 * s) * 2 * N, 4 * N);
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
