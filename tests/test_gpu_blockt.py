@@ -279,3 +279,42 @@ def test_blockt_split_graph_replays_and_two_streams(lib, orc, fmt):
         torch.cuda.synchronize()
         for i, case in enumerate(cases):
             assert rel_err(case[3].cpu().numpy(), case[4]) <= TOL, (rep, i)
+
+
+@pytest.mark.parametrize("n", [2, 3, 5, 20])
+@pytest.mark.parametrize("fmt", ["q4", "q8", "iq4nl", "w4a16"])
+def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
+    """Batches outside {4, 8, 12, 16}: ROCmEngine runs them on the tiled
+    kernels in column chunks of 16, zero-padded to a multiple of 4, and the
+    result matches the reference CPU product."""
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import GPTQStorage, IQ4NLStorage, Q4Storage, Q8Storage, Tensor
+
+    rows, K = 200, 1024
+    eng = ROCmEngine()
+    if fmt in ("q4", "q8"):
+        w = weights(fmt, rows, K, 87)
+        if fmt == "q4":
+            s = Q4Storage.from_raw(w.raw, rows * K)
+        else:
+            q = w.raw.reshape(-1, 36)
+            s = Q8Storage.from_blocks(q[:, :4].copy().view("<f4").reshape(-1), q[:, 4:].copy().view(np.int8), rows * K)
+        x = synth.x_f32(K * n, 87).reshape(K, n)
+        ref = oracle(orc, fmt, w.raw, x, rows, K, n)
+        xd = torch.from_numpy(x).cuda()
+    elif fmt == "iq4nl":
+        w = synth.iq4nl(rows, K, 87)
+        s = IQ4NLStorage.from_raw(w.raw, rows * K)
+        x16 = synth.x_f16(K * n, 87)
+        ref = np.asarray(orc.iq4nl_matmul(w.raw, x16, rows, K, n)).reshape(rows, n)
+        xd = torch.from_numpy(x16.view(np.float16).reshape(K, n)).cuda()
+    else:
+        w = synth.w4a16(rows, K, 87)
+        s = GPTQStorage.from_raw(w.packed.reshape(-1), w.scales.reshape(-1), w.zeros.reshape(-1), rows * K, 128, 4)
+        x16 = synth.x_f16(K * n, 87)
+        ref = np.asarray(orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, n, 128)).reshape(rows, n)
+        xd = torch.from_numpy(x16.view(np.float16).reshape(K, n)).cuda()
+    y = eng.matmul(Tensor((rows, K), s), xd).cpu().numpy()
+    assert y.shape == (rows, n)
+    assert rel_err(y, ref) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None

@@ -258,11 +258,37 @@ class ROCmEngine:
         s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
         return wt, st
 
+    @staticmethod
+    def _tiled_ok(s: Any, rows: int, k: int, x: torch.Tensor) -> bool:
+        """Whether this weight and activation dtype have a tiled MFMA path."""
+        if k % 128 != 0 or isinstance(s, MmapStorage):
+            return False
+        if isinstance(s, (Q4Storage, Q8Storage)):
+            return x.dtype == torch.float32
+        if isinstance(s, IQ4NLStorage):
+            return x.dtype == torch.float16
+        if isinstance(s, (GPTQStorage, AWQStorage)):
+            return (x.dtype == torch.float16 and s.group_size % 128 == 0 and
+                    rows * (k // s.group_size) < 1 << 29)
+        return False
+
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
         n = 1 if x.dim() == 1 else x.shape[1]
         if x.device != self.device:
             raise ValueError("activations must be on the engine's device")
+        if n > 1 and n not in _TILED_BATCHES and self._tiled_ok(s, rows, k, x):
+            # other batch sizes on the tiled MFMA kernels: columns in chunks of
+            # 16, the last one zero-padded to a multiple of 4
+            xs = x.reshape(k, n)
+            outs = []
+            for j0 in range(0, n, 16):
+                m = min(16, n - j0)
+                mp = -(-m // 4) * 4
+                xp = torch.zeros((k, mp), dtype=x.dtype, device=self.device)
+                xp[:, :m] = xs[:, j0:j0 + m]
+                outs.append(self._weight_times(s, rows, k, xp)[:, :m])
+            return torch.cat(outs, dim=1)
         self.upload_weights([s])
         c = torch.empty((rows, n), dtype=torch.float32, device=self.device)
         buf = s.gpu_ptr() if hasattr(s, "gpu_ptr") else None  # ternary: resident per shape, below
