@@ -388,7 +388,10 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         wbufs = [wt, st]
         x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
         gemm = getattr(lib, f"zt_gemm_{f}t_f32")
-        fn = lambda wb, y: gemm(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, s)
+        wsb = getattr(lib, f"zt_gemm_{f}t_workspace_bytes")(rows, K, N)
+        wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")  # launches run in order on one stream
+        fn = lambda wb, y: gemm(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N,
+                                wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes(fmt[:4], rows, K, N)
     elif fmt == "w4a16":
         w = synth.w4a16(rows, K, seed)

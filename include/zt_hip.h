@@ -225,19 +225,25 @@ int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* 
  *   [16 rows][4 blocks].  Rows past M, to the next multiple of 16, are zero.
  * K % 128 == 0, W_tiled / S_tiled / B 16-byte aligned, N in {4, 8, 12, 16},
  * else InvalidValue.  Activations are split into two fp16 parts after a
- * power-of-two normalisation (about 2^-22 relative precision each); split
- * K ranges add into C with fp32 atomics after a zero fill, so the last bits
- * of C can vary from run to run. */
+ * power-of-two normalisation (about 2^-22 relative precision each).  When
+ * K is split across workgroups the partial tiles go to the caller's
+ * workspace (16-byte aligned, at least zt_gemm_q{4,8}t_workspace_bytes(M,
+ * K, N) bytes, which is 0 when K is not split; a smaller or NULL workspace
+ * then gives InvalidValue) and a second kernel sums them in a fixed order,
+ * so C is the same on every run.  The workspace is scratch: calls that
+ * overlap in time need their own. */
 long zt_q4_tiled_bytes(int M, int K);
 long zt_q4_tiled_scale_bytes(int M, int K);
 int zt_q4_tile(const void* A_q4, int M, int K, int data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+long zt_gemm_q4t_workspace_bytes(int M, int K, int N);
 int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                    zt_stream_t stream);
+                    void* workspace, long workspace_bytes, zt_stream_t stream);
 long zt_q8_tiled_bytes(int M, int K);
 long zt_q8_tiled_scale_bytes(int M, int K);
 int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+long zt_gemm_q8t_workspace_bytes(int M, int K, int N);
 int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                    zt_stream_t stream);
+                    void* workspace, long workspace_bytes, zt_stream_t stream);
 
 /* ---- Ternary ----------------------------------------------------------- */
 

@@ -93,10 +93,18 @@ def tile_dev(lib, fmt, raw, rows, K):
     return wt, st
 
 
+def workspace(lib, fmt, rows, K, N):
+    nb = getattr(lib, f"zt_gemm_{fmt}t_workspace_bytes")(rows, K, N)
+    assert nb >= 0
+    return torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda"), nb
+
+
 def run_t(lib, fmt, wt, st, x, rows, K, N):
     xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
     c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
-    lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, stream())
+    ws, nb = workspace(lib, fmt, rows, K, N)
+    lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             ws.data_ptr(), nb, stream())
     return c.cpu().numpy().reshape(rows, N)
 
 
@@ -150,6 +158,8 @@ def test_blockt_llama3_shapes(lib, orc, fmt, rows, K, N):
     name = "zt_gemm_q4_f32" if fmt == "q4" else "zt_gemm_q8sep_f32"
     lib.call(name, a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, off, stream())
     assert rel_err(y, c.cpu().numpy().reshape(rows, N)) <= 1e-5
+    # the split-K reduction runs in a fixed order: a second call is bit-identical
+    assert np.array_equal(run_t(lib, fmt, wt, st, x, rows, K, N), y)
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q8"])
@@ -197,11 +207,20 @@ def test_blockt_invalid_arguments(lib):
     for fmt in ("q4", "q8"):
         g = getattr(lib, f"zt_gemm_{fmt}t_f32")
         for rows, K, N in [(2, 128, 3), (2, 128, 1), (2, 96, 4), (2, 160, 8), (-1, 128, 4)]:
-            assert g(p, p, p, p, rows, K, N, stream()) == 1, (fmt, rows, K, N)
-        assert g(p + 4, p, p, p, 2, 128, 4, stream()) == 1
-        assert g(p, p, p + 4, p, 2, 128, 4, stream()) == 1  # B not 16-byte aligned
-        assert g(p, p, p, p, 0, 128, 4, stream()) == 0  # empty: nothing to do
+            assert g(p, p, p, p, rows, K, N, p, 1 << 16, stream()) == 1, (fmt, rows, K, N)
+        assert g(p + 4, p, p, p, 2, 128, 4, p, 1 << 16, stream()) == 1
+        assert g(p, p, p + 4, p, 2, 128, 4, p, 1 << 16, stream()) == 1  # B not 16-byte aligned
+        assert g(p, p, p, p, 0, 128, 4, 0, 0, stream()) == 0  # empty: nothing to do
         assert getattr(lib, f"zt_{fmt}_tiled_bytes")(2, 96) == -1
+        wsb = getattr(lib, f"zt_gemm_{fmt}t_workspace_bytes")
+        assert wsb(2, 96, 4) == -1 and wsb(2, 128, 3) == -1
+        assert wsb(16, 128, 4) == 0  # one K range: no split, no workspace
+        need = wsb(4096, 4096, 8)
+        assert need > 0
+        # K split but the workspace is missing, short or misaligned
+        assert g(p, p, p, p, 4096, 4096, 8, 0, 0, stream()) == 1
+        assert g(p, p, p, p, 4096, 4096, 8, p, need - 16, stream()) == 1
+        assert g(p, p, p, p, 4096, 4096, 8, p + 4, need, stream()) == 1
     assert lib.zt_q4_tile(p, 2, 96, 16, p, p, stream()) == 1  # K % 128
     assert lib.zt_q8_tile(p, 2, 96, 16, p, p, stream()) == 1
     assert lib.zt_q8_tile(p, 2, 128, 8, p, p, stream()) == 1  # data not 16-byte aligned
@@ -236,22 +255,26 @@ def test_engine_batched_uses_tiled_layout(lib, orc, fmt, side):
 
 @pytest.mark.parametrize("fmt", ["q4", "q8"])
 def test_blockt_split_graph_replays_and_two_streams(lib, orc, fmt):
-    """Split-K calls (zero fill, then atomic adds) captured in a HIP graph and
-    replayed with eager calls in between, then run on two streams at once:
-    every result matches the oracle."""
+    """Split-K calls (partials to a workspace, then the reduction kernel)
+    captured in a HIP graph and replayed with eager calls in between, then
+    run on two streams at once, each with its own workspace: every result
+    matches the oracle."""
     rows, K, N = 4096, 4096, 8
     cases = []
     for seed in (85, 86):
         w = weights(fmt, rows, K, seed)
         x = synth.x_f32(K * N, seed).reshape(K, N)
         wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+        ws, nb = workspace(lib, fmt, rows, K, N)  # one per case: the two streams overlap
+        assert nb > 0
         cases.append((wt, st, torch.from_numpy(np.ascontiguousarray(x).reshape(-1)).cuda(),
                       torch.empty(rows * N, dtype=torch.float32, device="cuda"),
-                      oracle(orc, fmt, w.raw, x, rows, K, N).reshape(-1)))
+                      oracle(orc, fmt, w.raw, x, rows, K, N).reshape(-1), ws, nb))
 
     def call(case, s):
-        wt, st, xd, c, _ = case
-        lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, s)
+        wt, st, xd, c, _, ws, nb = case
+        lib.call(f"zt_gemm_{fmt}t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
+                 ws.data_ptr(), nb, s)
 
     cs = torch.cuda.Stream()
     cs.wait_stream(torch.cuda.current_stream())

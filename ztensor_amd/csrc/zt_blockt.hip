@@ -24,9 +24,11 @@
 //  * Each 16-row x 128-K tile is one contiguous block in MFMA lane order
 //    (1 KB for Q4_0, 2 KB for Q8_0), so a wave's weight load is contiguous;
 //    the workgroup structure (4 waves x 32 rows, UPW 128-K units, XCD-aware
-//    K split with fp32 atomics after a zero fill, X and scales staged behind
-//    an LDS-only barrier while the weights stream) follows the tiled W4A16
-//    and IQ4_NL kernels.
+//    K split, X and scales staged behind an LDS-only barrier while the
+//    weights stream) follows the tiled W4A16 and IQ4_NL kernels.  K splits
+//    store partial tiles to the caller's workspace and a second kernel sums
+//    them in split order (tiled_reduce_kernel): fp32 atomics after a zero
+//    fill measured 4.6 us of the 12.9 us at 14336 x 4096, batch 8.
 //
 // Tiled layouts (ntiles = ceil(M / 16), nunits = K / 128, tile-unit tu =
 // rt * nunits + u; rows past M are zero):
@@ -87,8 +89,8 @@ __device__ __forceinline__ int blkt_lds_row(int r) {
 
 template <BlkFmt F, int UPW, int N>
 __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict__ wt, const void* __restrict__ stl,
-                                                        const float* __restrict__ x, float* __restrict__ y, int rows,
-                                                        int K) {
+                                                        const float* __restrict__ x, float* __restrict__ y,
+                                                        float* __restrict__ ws, int rows, int K) {
     constexpr int W = 4;
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
@@ -280,43 +282,66 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             if constexpr (NPL == 1) v += __shfl_xor(v, 8);  // hi columns n + lo columns 8 + n
             acc[t][i] = ldexpf(v, 24 - sh);
         }
-    if (li < N) {
+    if (gridDim.y > 1) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = row0 / 16 + t;
+            if (rt < ntiles) tiled_store_partial(acc[t], ws, byi, ntiles, rt, lane, N);
+        }
+    } else if (li < N) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = row0 + 16 * t + 4 * lg + i;
-                if (row < rows) {
-                    if (gridDim.y > 1)
-                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
-                    else
-                        y[(long)row * N + li] = acc[t][i];
-                }
+                if (row < rows) y[(long)row * N + li] = acc[t][i];
             }
     }
 }
 
 template <BlkFmt F, int UPW, int N>
-static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y, int M,
-                        int K) {
+static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y, float* ws,
+                        int M, int K) {
     constexpr int NPL = N <= 8 ? 1 : 2;
     constexpr int SB = F == BlkFmt::Q4_0 ? 2 : 4;
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
-    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, x, y, M, K);
+    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, x, y, ws, M, K);
 }
 
 template <BlkFmt F, int N>
 static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y,
-                          int M, int K) {
+                          float* ws, int M, int K) {
     if (upw >= 4)
-        launch_blkt<F, 4, N>(g, st, wt, sc, x, y, M, K);
+        launch_blkt<F, 4, N>(g, st, wt, sc, x, y, ws, M, K);
     else
-        launch_blkt<F, 2, N>(g, st, wt, sc, x, y, M, K);
+        launch_blkt<F, 2, N>(g, st, wt, sc, x, y, ws, M, K);
+}
+
+// Grid of a tiled block GEMM: 128 rows by the largest K range per
+// workgroup, up to 4 units, that still gives >= 256 (Q4_0) or >= 512 (Q8_0)
+// workgroups; measured at the Llama-3-8B shapes, batches 8 and 16: 8 units
+// were 3-14% slower for Q4_0 and 8-40% for Q8_0, and 8 waves a workgroup
+// were slower at every unit count.
+template <BlkFmt F>
+static dim3 blkt_grid(int M, int K, int& upw) {
+    const int nunits = K / 128, gx = ceil_div(M, 128);
+    const long minwg = F == BlkFmt::Q4_0 ? 256 : 512;
+    upw = 4;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < minwg) upw >>= 1;
+    return dim3(gx, ceil_div(nunits, upw));
+}
+
+template <BlkFmt F>
+static long blkt_ws_bytes(int M, int K, int N) {
+    if (M < 0 || K < 0 || K % 128 != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
+    if (M == 0 || K == 0) return 0;
+    int upw;
+    return tiled_ws_bytes(M, (int)blkt_grid<F>(M, K, upw).y);
 }
 
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                     hipStream_t stream) {
+                     void* ws, long ws_bytes, hipStream_t stream) {
     if (M < 0 || K < 0 || K % 128 != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
@@ -325,24 +350,19 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
         return (int)hipErrorInvalidValue;
     constexpr long SB = F == BlkFmt::Q4_0 ? 2 : 4;
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
-    const int nunits = K / 128;
-    const int gx = ceil_div(M, 128);
-    // the largest K range per workgroup, up to 4 units, that still gives
-    // >= 256 (Q4_0) or >= 512 (Q8_0) workgroups; measured at the Llama-3-8B
-    // shapes, batches 8 and 16: 8 units were 3-14% slower for Q4_0 and 8-40%
-    // for Q8_0, and 8 waves a workgroup were slower at every unit count
-    int upw = 4;
-    const long minwg = F == BlkFmt::Q4_0 ? 256 : 512;
-    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < minwg) upw >>= 1;
-    const dim3 g(gx, ceil_div(nunits, upw));
-    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    int upw;
+    const dim3 g = blkt_grid<F>(M, K, upw);
+    const long need = tiled_ws_bytes(M, (int)g.y);
+    if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 15))) return (int)hipErrorInvalidValue;
     const uint4* wt = static_cast<const uint4*>(W_tiled);
+    float* wsf = static_cast<float*>(ws);
     switch (N) {
-        case 4: launch_blkt_n<F, 4>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
-        case 8: launch_blkt_n<F, 8>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
-        case 12: launch_blkt_n<F, 12>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
-        default: launch_blkt_n<F, 16>(upw, g, stream, wt, S_tiled, B, C, M, K); break;
+        case 4: launch_blkt_n<F, 4>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
+        case 8: launch_blkt_n<F, 8>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
+        case 12: launch_blkt_n<F, 12>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
+        default: launch_blkt_n<F, 16>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
     }
+    if (g.y > 1) tiled_reduce(ws, C, M, N, (int)g.y, stream);
     return (int)hipGetLastError();
 }
 
@@ -370,9 +390,11 @@ ZT_EXPORT int zt_q4_tile(const void* A_q4, int M, int K, int data_offset, void* 
     return zt_iq4nl_tile(A_q4, M, K, data_offset, W_tiled, S_tiled, stream);
 }
 
+ZT_EXPORT long zt_gemm_q4t_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q4_0>(M, K, N); }
+
 ZT_EXPORT int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                              hipStream_t stream) {
-    return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, stream);
+                              void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
 }
 
 ZT_EXPORT long zt_q8_tiled_bytes(int M, int K) {
@@ -402,7 +424,9 @@ ZT_EXPORT int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void*
     return (int)hipGetLastError();
 }
 
+ZT_EXPORT long zt_gemm_q8t_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q8_0>(M, K, N); }
+
 ZT_EXPORT int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                              hipStream_t stream) {
-    return gemm_blkt<BlkFmt::Q8_0>(W_tiled, S_tiled, B, C, M, K, N, stream);
+                              void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q8_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
 }

@@ -140,6 +140,54 @@ __host__ __forceinline__ int mfma_splits(int rows, int K) {
     return s;
 }
 
+// ---- split-K through a workspace (tiled kernels)
+//
+// A K-split workgroup of a tiled kernel stores each of its partial 16-row
+// output tiles in MFMA D lane order, one 16-byte store per lane, at
+// ws + ((split * ntiles + rt) * 64 + lane) * 4 floats.  tiled_reduce_kernel
+// then sums the splits of every tile in split order and writes C once: no
+// zero fill, no atomics, and the same result on every run.  The workspace
+// holds splits * ntiles KB.
+
+__device__ __forceinline__ void tiled_store_partial(const float4v& v, float* __restrict__ ws, int split, int ntiles,
+                                                    int rt, int lane, int N) {
+    if ((lane & 15) < N) *reinterpret_cast<float4v*>(ws + (((long)split * ntiles + rt) * 64 + lane) * 4) = v;
+}
+
+static __global__ void tiled_reduce_kernel(const float4v* __restrict__ ws, float* __restrict__ y, int rows, int N,
+                                           int ntiles, int splits) {
+    // thread = (tile, lane of a column < N): lanes 16g + i with i < N
+    const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (long)ntiles * 4 * N) return;
+    const long rt = q / (4 * N);
+    const int r = (int)(q % (4 * N)), lg = r / N, li = r % N, lane = 16 * lg + li;
+    const long p = rt * 64 + lane, stride = (long)ntiles * 64;
+    float4v s0 = ws[p], s1 = (float4v){0.f, 0.f, 0.f, 0.f}, s2 = s1, s3 = s1;
+    int k = 1;
+    for (; k + 3 <= splits; k += 3) {  // three independent loads in flight
+        s1 += ws[k * stride + p];
+        s2 += ws[(k + 1) * stride + p];
+        s3 += ws[(k + 2) * stride + p];
+    }
+    for (; k < splits; k++) s1 += ws[k * stride + p];
+    const float4v s = (s0 + s1) + (s2 + s3);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const long row = rt * 16 + 4 * lg + i;
+        if (row < rows) y[row * N + li] = s[i];
+    }
+}
+
+__host__ __forceinline__ long tiled_ws_bytes(int rows, int splits) {
+    return splits > 1 ? (long)splits * ((rows + 15) / 16) * 1024 : 0;
+}
+
+__host__ __forceinline__ void tiled_reduce(const void* ws, float* y, int rows, int N, int splits, hipStream_t st) {
+    const int ntiles = (rows + 15) / 16;
+    tiled_reduce_kernel<<<(int)(((long)ntiles * 4 * N + 255) / 256), 256, 0, st>>>(
+        static_cast<const float4v*>(ws), y, rows, N, ntiles, splits);
+}
+
 static __global__ void mfma_zero_kernel(float* __restrict__ y, long n) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = 0.0f;

@@ -64,6 +64,18 @@ class ROCmEngine:
     def _s(self) -> int:
         return self.stream.cuda_stream
 
+    def _workspace(self, nbytes: int) -> tuple[int, int]:
+        """Scratch for the split-K partials of the tiled GEMMs: one buffer per
+        engine, grown on demand; calls on the engine's one stream run in
+        order, so they can share it."""
+        if nbytes <= 0:
+            return 0, 0
+        buf = getattr(self, "_wsbuf", None)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self._wsbuf = buf
+        return _p(buf), buf.numel()
+
     # ------------------------------------------------------ KernelRunner level
 
     def gemm_q4_f32(self, a_q4: int, b: int, c: int, m: int, k: int, n: int, data_offset: int) -> None:
@@ -297,7 +309,8 @@ class ROCmEngine:
         if isinstance(s, Q4Storage):
             if x.dtype == torch.float32 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
                 wt, st = self._block_tiled(s, buf, rows, k, "q4")
-                self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
+                ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
+                self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
             elif x.dtype == torch.float32:
                 self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             elif x.dtype == torch.float16:
@@ -319,7 +332,8 @@ class ROCmEngine:
                 raise TypeError("Q8_0 matmul takes fp32 activations")
             if n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
                 wt, st = self._block_tiled(s, buf, rows, k, "q8")
-                self.lib.call("zt_gemm_q8t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
+                ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
+                self.lib.call("zt_gemm_q8t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
                 return c
             self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
         elif isinstance(s, (GPTQStorage, AWQStorage)):
