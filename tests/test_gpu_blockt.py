@@ -305,26 +305,29 @@ def test_blockt_split_graph_replays_and_two_streams(lib, orc, fmt):
 
 
 @pytest.mark.parametrize("n", [2, 3, 5, 20])
-@pytest.mark.parametrize("fmt", ["q4", "q8", "iq4nl", "w4a16"])
+@pytest.mark.parametrize("fmt", ["q4", "q4_f16", "q8", "iq4nl", "w4a16"])
 def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     """Batches outside {4, 8, 12, 16}: ROCmEngine runs them on the tiled
     kernels in column chunks of 16, zero-padded to a multiple of 4, and the
-    result matches the reference CPU product."""
+    result matches the reference CPU product (Q4_0 also with fp16
+    activations, widened exactly to fp32)."""
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import GPTQStorage, IQ4NLStorage, Q4Storage, Q8Storage, Tensor
 
     rows, K = 200, 1024
     eng = ROCmEngine()
-    if fmt in ("q4", "q8"):
-        w = weights(fmt, rows, K, 87)
-        if fmt == "q4":
+    if fmt in ("q4", "q4_f16", "q8"):
+        w = weights(fmt[:2], rows, K, 87)
+        if fmt != "q8":
             s = Q4Storage.from_raw(w.raw, rows * K)
         else:
             q = w.raw.reshape(-1, 36)
             s = Q8Storage.from_blocks(q[:, :4].copy().view("<f4").reshape(-1), q[:, 4:].copy().view(np.int8), rows * K)
         x = synth.x_f32(K * n, 87).reshape(K, n)
-        ref = oracle(orc, fmt, w.raw, x, rows, K, n)
-        xd = torch.from_numpy(x).cuda()
+        if fmt == "q4_f16":  # fp16 activations: the reference widens them to fp32 (tensor/fp16_storage.go:53-63)
+            x = x.astype(np.float16).astype(np.float32)
+        ref = oracle(orc, fmt[:2], w.raw, x, rows, K, n)
+        xd = torch.from_numpy(x.astype(np.float16) if fmt == "q4_f16" else x).cuda()
     elif fmt == "iq4nl":
         w = synth.iq4nl(rows, K, 87)
         s = IQ4NLStorage.from_raw(w.raw, rows * K)

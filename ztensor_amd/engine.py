@@ -275,7 +275,9 @@ class ROCmEngine:
         """Whether this weight and activation dtype have a tiled MFMA path."""
         if k % 128 != 0 or isinstance(s, MmapStorage):
             return False
-        if isinstance(s, (Q4Storage, Q8Storage)):
+        if isinstance(s, Q4Storage):
+            return x.dtype in (torch.float32, torch.float16)
+        if isinstance(s, Q8Storage):
             return x.dtype == torch.float32
         if isinstance(s, IQ4NLStorage):
             return x.dtype == torch.float16
@@ -307,7 +309,9 @@ class ROCmEngine:
         if isinstance(s, MmapStorage):
             return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
-            if x.dtype == torch.float32 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
+            if x.dtype in (torch.float32, torch.float16) and n in _TILED_BATCHES and k % 128 == 0:
+                # fp16 activations widen exactly to fp32 for the tiled kernel
+                x = x.float() if x.dtype == torch.float16 or _p(x) % 16 else x
                 wt, st = self._block_tiled(s, buf, rows, k, "q4")
                 ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
                 self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
