@@ -699,8 +699,9 @@ def main() -> None:
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build "
-              "(see the sharding note in DESIGN.md)", file=sys.stderr)
+        print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build. "
+              "Sharded, each GPU would run the same kernels on its slice: output rows for q/k/v/gate/up, "
+              "K for o/down followed by an all-reduce of the partial outputs", file=sys.stderr)
         raise SystemExit(2)
     if args.suite:
         run_suite(args)
