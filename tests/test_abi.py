@@ -196,3 +196,33 @@ def test_iq4nl_tiled_layout_sizes():
     assert lib.zt_iq4nl_tiled_bytes(17, 256) == 32 * 128
     assert lib.zt_iq4nl_tiled_scale_bytes(17, 256) == 32 * 8 * 2
     assert lib.zt_iq4nl_tiled_bytes(4, 96) == -1 and lib.zt_iq4nl_tiled_scale_bytes(4, 96) == -1
+
+
+def test_q4_q8_tiled_layout_and_workspace_sizes():
+    """The tiled Q4_0 / Q8_0 layouts' byte counts and the split-K workspace
+    sizes (host helpers, no GPU).  The workspace is one KB per 16-row tile
+    per K split and 0 when K is not split; the split counts follow the
+    launch heuristic (128 rows a workgroup, up to 4 units of 128 K, at least
+    256 workgroups for Q4_0 and 512 for Q8_0)."""
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    assert lib.zt_q4_tiled_bytes(4096, 4096) == 4096 * 2048
+    assert lib.zt_q4_tiled_bytes(17, 256) == 32 * 128
+    assert lib.zt_q4_tiled_scale_bytes(17, 256) == 32 * 8 * 2
+    assert lib.zt_q8_tiled_bytes(17, 256) == 32 * 256
+    assert lib.zt_q8_tiled_scale_bytes(17, 256) == 32 * 8 * 4
+    for f in ("q4", "q8"):
+        assert getattr(lib, f"zt_{f}_tiled_bytes")(4, 96) == -1
+        assert getattr(lib, f"zt_{f}_tiled_scale_bytes")(4, 96) == -1
+    q4, q8 = lib.zt_gemm_q4t_workspace_bytes, lib.zt_gemm_q8t_workspace_bytes
+    # 14336 x 4096: 112 row blocks, 4 units -> 8 splits; 896 tiles
+    assert q4(14336, 4096, 8) == 8 * 896 * 1024 and q8(14336, 4096, 8) == 8 * 896 * 1024
+    # 4096 x 4096: Q4_0 keeps 4 units (256 workgroups), Q8_0 drops to 2 (512)
+    assert q4(4096, 4096, 8) == 8 * 256 * 1024 and q8(4096, 4096, 16) == 16 * 256 * 1024
+    # 4096 x 14336: 28 splits
+    assert q4(4096, 14336, 4) == 28 * 256 * 1024
+    # K of one unit: no split, no workspace; unsupported shapes and batches: -1
+    assert q4(100, 128, 8) == 0 and q8(100, 128, 8) == 0
+    assert q4(0, 4096, 8) == 0
+    assert q4(16, 96, 8) == -1 and q8(16, 128, 6) == -1 and q4(16, 128, 1) == -1
