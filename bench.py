@@ -525,6 +525,9 @@ def run_pmc_case(args) -> None:
     if args.pmc_case in ("w4a16_b8", "w4a16t_b8"):
         run_pmc_case_w4a16(torch, lib, tiled=args.pmc_case == "w4a16t_b8")
         return
+    if args.pmc_case == "q4_0t_b8":
+        run_pmc_case_q4t(torch, lib)
+        return
     m = Q4Matrix(torch, lib, 14336, 4096, 0x5EED0024, 20)
     s = torch.cuda.current_stream().cuda_stream
     for i in range(40):
@@ -569,6 +572,40 @@ def run_pmc_case_w4a16(torch, lib, tiled: bool) -> None:
             raise SystemExit(f"bench: W4A16 GEMM returned {rc}")
     torch.cuda.synchronize()
     log(f"bench: pmc case {'w4a16t_b8' if tiled else 'w4a16_b8'} done")
+
+
+def run_pmc_case_q4t(torch, lib) -> None:
+    """40 launches of the batch-8 Q4_0 MFMA GEMM on the tiled layout at the
+    Llama-3-8B gate/up shape (14336 rows, K = 4096), rotating over 20 weight
+    copies (700 MB, beyond the Infinity Cache); K is split 8 ways, so each
+    launch is the GEMM and the split-K reduction."""
+    from ztensor_amd import synth
+
+    rows, K, N = 14336, 4096, 8
+    s = torch.cuda.current_stream().cuda_stream
+    w = synth.q4_0(rows, K, 0x5EED0050)
+    nblk = rows * K // 32
+    host = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+    lib.zt_q4_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+    sep = torch.from_numpy(host).cuda()
+    wt = torch.empty(lib.zt_q4_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+    st = torch.empty(lib.zt_q4_tiled_scale_bytes(rows, K), dtype=torch.uint8, device="cuda")
+    if lib.zt_q4_tile(sep.data_ptr(), rows, K, lib.zt_q4_gpu_data_offset(nblk), wt.data_ptr(), st.data_ptr(), s) != 0:
+        raise SystemExit("bench: zt_q4_tile failed")
+    copies = [(wt, st)] + [(wt.clone(), st.clone()) for _ in range(19)]
+    x = torch.from_numpy(synth.x_f32(K * N, 0x5EED0051)).cuda()
+    y = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    wsb = lib.zt_gemm_q4t_workspace_bytes(rows, K, N)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(40):
+        a, b = copies[i % 20]
+        rc = lib.zt_gemm_q4t_f32(a.data_ptr(), b.data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, ws.data_ptr(), wsb,
+                                 s)
+        if rc != 0:
+            raise SystemExit(f"bench: Q4_0 tiled GEMM returned {rc}")
+    torch.cuda.synchronize()
+    log("bench: pmc case q4_0t_b8 done")
 
 
 def run_suite(args) -> None:
@@ -691,10 +728,11 @@ def main() -> None:
                     help="skip the per-configuration timings reported beside the headline")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
-    ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8", "w4a16t_b8"],
+    ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8", "w4a16t_b8", "q4_0t_b8"],
                     help="short fixed workload for rocprofv3 counter passes: copies + 40 launches of the dominant "
-                         "Q4_0 GEMV (default), or of the W4A16 batch-8 MFMA GEMM at 28672 x 8192 on the row-major "
-                         "(w4a16_b8) or tiled (w4a16t_b8) layout")
+                         "Q4_0 GEMV (default), of the W4A16 batch-8 MFMA GEMM at 28672 x 8192 on the row-major "
+                         "(w4a16_b8) or tiled (w4a16t_b8) layout, or of the batch-8 Q4_0 tiled GEMM at "
+                         "14336 x 4096 (q4_0t_b8)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
