@@ -334,6 +334,7 @@ SUITE = {
     "q8_0_batched": ("q8_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q4_kt": ("q4_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
 }
 
 
@@ -393,6 +394,22 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: gemm(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N,
                                 wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes(fmt[:4], rows, K, N)
+    elif fmt == "q4_kt":
+        # batched Q4_K on the tiled layout (zt_q4k_tile), built once outside the timing
+        w = synth.kquant("q4_k", rows, K, seed)
+        raw = dev(w.raw)
+        wt = torch.empty(lib.zt_q4k_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        ht = torch.empty(lib.zt_q4k_tiled_header_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        lib.call("zt_q4k_tile", raw.data_ptr(), rows, K, wt.data_ptr(), ht.data_ptr(), s)
+        torch.cuda.synchronize()
+        del raw
+        wbufs = [wt, ht]
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        wsb = lib.zt_gemm_q4kt_workspace_bytes(rows, K, N)
+        wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")
+        fn = lambda wb, y: lib.zt_gemm_q4kt_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K,
+                                                N, wsbuf.data_ptr(), wsb, s)
+        nbytes = synth.algorithmic_bytes("q4_k", rows, K, N)
     elif fmt == "w4a16":
         w = synth.w4a16(rows, K, seed)
         wbufs = [dev(w.packed), dev(w.scales), dev(w.zeros)]

@@ -245,6 +245,26 @@ long zt_gemm_q8t_workspace_bytes(int M, int K, int N);
 int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                     void* workspace, long workspace_bytes, zt_stream_t stream);
 
+/* Batched Q4_K on the same MFMA kernel: the raw super-blocks
+ * (Q4KStorage.RawBytes, tensor/quantized_kquant.go:34-79, 144 bytes per 256
+ * values, the layout UploadWeights places on the device,
+ * compute/gpu_engine.go:817-836) are repacked by zt_q4k_tile into the Q4_0
+ * tiled data layout (each 32-value sub-block as a 16-byte Q4_0 block) plus
+ * the 16-byte super-block headers as [tile][super-block][16 rows][16 B]
+ * (zt_q4k_tiled_bytes / zt_q4k_tiled_header_bytes).  zt_gemm_q4kt_f32 takes
+ * both with fp32 B [K, N], N in {4, 8, 12, 16}, K % 256 == 0, and the
+ * split-K workspace of zt_gemm_q4kt_workspace_bytes; each sub-block adds
+ * (d*scale) * sum(q x) - (dmin*min) * sum(x) with the reference's fp32
+ * products d*scale and dmin*min.  16-byte alignment as above, else
+ * InvalidValue.  Replaces the reference's dequantize-then-SGEMM for
+ * batched Q4_K (compute/gpu_engine.go:2240-2255). */
+long zt_q4k_tiled_bytes(int M, int K);
+long zt_q4k_tiled_header_bytes(int M, int K);
+int zt_q4k_tile(const void* W_q4k, int M, int K, void* W_tiled, void* H_tiled, zt_stream_t stream);
+long zt_gemm_q4kt_workspace_bytes(int M, int K, int N);
+int zt_gemm_q4kt_f32(const void* W_tiled, const void* H_tiled, const float* B, float* C, int M, int K, int N,
+                     void* workspace, long workspace_bytes, zt_stream_t stream);
+
 /* ---- Ternary ----------------------------------------------------------- */
 
 /* Replaces ternary_gemv_f32 (internal/cuda/kernels/ternary_gemv.cu:85-99),

@@ -344,3 +344,107 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     assert y.shape == (rows, n)
     assert rel_err(y, ref) <= TOL
     assert getattr(s, "_gpu_tiled", None) is not None
+
+
+# ---- batched Q4_K on the same kernel (zt_q4k_tile, zt_gemm_q4kt_f32)
+
+def q4k_tile_ref(raw: np.ndarray, rows: int, K: int):
+    """Data: every 32-value sub-block rewritten as a 16-byte Q4_0 block (byte
+    j = value j | value j+16 << 4), then the Q4_0 tile order; headers: the
+    first 16 bytes of every super-block as [tile][super-block][16 rows]."""
+    nt, nu, nsb = (rows + 15) // 16, K // 128, K // 256
+    sbk = raw.reshape(rows, nsb, 144)
+    nib = sbk[:, :, 16:].reshape(rows, nsb, 4, 32)
+    q = np.stack([(nib >> 4 * h) & 15 for h in (0, 1)], axis=3).reshape(rows, nsb * 8, 32)  # sub-block 2g+h
+    blocks = (q[:, :, :16] | (q[:, :, 16:] << 4)).astype(np.uint8)
+    d = np.zeros((nt * 16, K // 32, 16), np.uint8)
+    d[:rows] = blocks
+    dt = d.reshape(nt, 16, nu, 4, 4, 4).transpose(0, 2, 4, 1, 3, 5).reshape(-1)
+    hd = np.zeros((nt * 16, nsb, 16), np.uint8)
+    hd[:rows] = sbk[:, :, :16]
+    ht = hd.reshape(nt, 16, nsb, 16).transpose(0, 2, 1, 3).reshape(-1)
+    return dt, ht
+
+
+def q4k_tile_dev(lib, raw, rows, K):
+    a = dev(raw)
+    wt = torch.empty(lib.zt_q4k_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
+    ht = torch.empty(lib.zt_q4k_tiled_header_bytes(rows, K), dtype=torch.uint8, device="cuda")
+    lib.call("zt_q4k_tile", a.data_ptr(), rows, K, wt.data_ptr(), ht.data_ptr(), stream())
+    torch.cuda.synchronize()
+    return wt, ht
+
+
+def run_q4kt(lib, wt, ht, x, rows, K, N):
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    nb = lib.zt_gemm_q4kt_workspace_bytes(rows, K, N)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
+    lib.call("zt_gemm_q4kt_f32", wt.data_ptr(), ht.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, ws.data_ptr(),
+             nb, stream())
+    return c.cpu().numpy().reshape(rows, N)
+
+
+def q4k_oracle(orc, raw, x, rows, K, N):
+    xt = np.ascontiguousarray(np.asarray(x, np.float32).reshape(K, N).T)
+    return orc.gemm_f32_kq_nt("q4_k", xt, raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
+
+
+@pytest.mark.parametrize("rows,K", [(16, 256), (17, 512), (100, 1024), (1, 768)])
+def test_q4k_tile_layout_bytes(lib, rows, K):
+    w = synth.kquant("q4_k", rows, K, 91)
+    wt, ht = q4k_tile_dev(lib, w.raw, rows, K)
+    dref, href = q4k_tile_ref(w.raw, rows, K)
+    assert np.array_equal(wt.cpu().numpy(), dref)
+    assert np.array_equal(ht.cpu().numpy(), href)
+
+
+@pytest.mark.parametrize("rows,K,N", [(16, 256, 4), (17, 512, 8), (33, 2304, 12), (65, 768, 16), (100, 4096, 8),
+                                      (40, 12288, 4), (1, 256, 16), (300, 1024, 16)])
+def test_q4kt_ragged(lib, orc, rows, K, N):
+    print(f"q4kt rows={rows} K={K} N={N}", flush=True)
+    w = synth.kquant("q4_k", rows, K, 92)
+    x = synth.x_f32(K * N, 92).reshape(K, N)
+    wt, ht = q4k_tile_dev(lib, w.raw, rows, K)
+    assert rel_err(run_q4kt(lib, wt, ht, x, rows, K, N), q4k_oracle(orc, w.raw, x, rows, K, N)) <= TOL
+
+
+@pytest.mark.parametrize("N", [4, 8, 16])
+@pytest.mark.parametrize("rows,K", LLAMA)
+def test_q4kt_llama3_shapes(lib, orc, rows, K, N):
+    """The Llama-3-8B shapes at full size against the oracle (the reference
+    CPU engine's GemmF32Q4KNT), and deterministic across calls."""
+    print(f"q4kt rows={rows} K={K} N={N}", flush=True)
+    seed = synth.seed_for(6, LLAMA.index((rows, K)))
+    w = synth.kquant("q4_k", rows, K, seed)
+    x = synth.x_f32(K * N, seed + N).reshape(K, N)
+    wt, ht = q4k_tile_dev(lib, w.raw, rows, K)
+    y = run_q4kt(lib, wt, ht, x, rows, K, N)
+    err = rel_err(y, q4k_oracle(orc, w.raw, x, rows, K, N))
+    assert err <= 1e-5, err
+    assert np.array_equal(run_q4kt(lib, wt, ht, x, rows, K, N), y)
+
+
+def test_q4kt_invalid_arguments(lib):
+    t = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    p = t.data_ptr()
+    g = lib.zt_gemm_q4kt_f32
+    for rows, K, N in [(2, 256, 3), (2, 128, 4), (2, 384, 8), (-1, 256, 4)]:
+        assert g(p, p, p, p, rows, K, N, p, 1 << 16, stream()) == 1, (rows, K, N)
+    assert lib.zt_q4k_tile(p, 2, 128, p, p, stream()) == 1  # K % 256
+    assert lib.zt_q4k_tile(p + 4, 2, 256, p, p, stream()) == 1
+    assert lib.zt_q4k_tiled_bytes(2, 128) == -1 and lib.zt_gemm_q4kt_workspace_bytes(2, 128, 4) == -1
+
+
+@pytest.mark.parametrize("n", [3, 8])
+def test_engine_batched_q4k_uses_tiled_layout(lib, orc, n):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import Q4KStorage, Tensor
+
+    rows, K = 300, 1024
+    w = synth.kquant("q4_k", rows, K, 93)
+    s = Q4KStorage(w.raw, rows * K)
+    x = synth.x_f32(K * n, 93).reshape(K, n)
+    y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
+    assert rel_err(y, q4k_oracle(orc, w.raw, x, rows, K, n)) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None

@@ -45,7 +45,7 @@
 
 namespace zt {
 
-enum class BlkFmt { Q4_0, Q8_0 };
+enum class BlkFmt { Q4_0, Q8_0, Q4_K };
 
 __global__ void q8t_tile_kernel(const uint2* __restrict__ data, const float* __restrict__ scales,
                                 u32x4* __restrict__ wt, float* __restrict__ st, int rows, int nunits, long npieces) {
@@ -66,6 +66,40 @@ __global__ void q8t_tile_kernel(const uint2* __restrict__ data, const float* __r
     if (h == 0) st[tu * 64 + i * 4 + g] = row < rows ? scales[row * nb + 4L * u + g] : 0.0f;
 }
 
+// Q4_K tiled layout: the data in the Q4_0 tile format (each 32-value
+// sub-block rewritten as the 16 bytes of a Q4_0 block: byte j holds values
+// j and j+16), and the 16-byte super-block headers (fp16 d, fp16 dmin, 12
+// bytes of 6-bit scales and mins) as [tile][super-block][16 rows][16 B].
+__global__ void q4kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restrict__ wt, u32x4* __restrict__ ht,
+                                 int rows, int nunits, long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63), i = lane & 15, g = lane >> 4;
+    const long tu = p >> 6;
+    const int u = (int)(tu % nunits);
+    const long rt = tu / nunits;
+    const long row = rt * 16 + i;
+    const int nsb = nunits / 2;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    if (row < rows) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int b = 4 * u + s, sb = b >> 3, j = b & 7, gq = j >> 1;
+            const uint8_t* nib = raw + (row * nsb + sb) * 144 + 16 + 32 * gq;
+            const uint32_t a = *reinterpret_cast<const uint32_t*>(nib + 4 * g);
+            const uint32_t c = *reinterpret_cast<const uint32_t*>(nib + 16 + 4 * g);
+            v[s] = (j & 1) ? (((a >> 4) & 0x0F0F0F0Fu) | (c & 0xF0F0F0F0u))
+                           : ((a & 0x0F0F0F0Fu) | ((c & 0x0F0F0F0Fu) << 4));
+        }
+    }
+    wt[p] = (u32x4){v[0], v[1], v[2], v[3]};
+    if ((u & 1) == 0 && g == 0) {  // header of (row, super-block u/2)
+        u32x4 h = {0u, 0u, 0u, 0u};
+        if (row < rows) h = *reinterpret_cast<const u32x4*>(raw + (row * nsb + u / 2) * 144);
+        ht[(rt * nsb + u / 2) * 16 + i] = h;
+    }
+}
+
 // LDS row of chunk-relative activation row r (K index within the
 // workgroup's range).  Within each 128-K unit, the 8 activations that lane
 // group g of MFMA step s multiplies sit in rows 32 g + 8 s .. +7, in the
@@ -75,7 +109,7 @@ template <BlkFmt F>
 __device__ __forceinline__ int blkt_lds_row(int r) {
     const int u = r >> 7, b = (r >> 5) & 3, e = r & 31;
     int g, j;
-    if constexpr (F == BlkFmt::Q4_0) {
+    if constexpr (F != BlkFmt::Q8_0) {
         // A halves of lane group g: elements 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3, 4g+17, 4g+19
         const int i4 = e & 3;
         g = (e & 15) >> 2;
@@ -98,11 +132,13 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     constexpr int XPB = mfma_chunk_xbytes(KC, 16);      // one plane: 16 fp16 columns, 2 pad rows per 32
     constexpr int PPR = N / 4;                          // 16-byte pieces per fp32 activation row
     constexpr int XP = (KC * PPR + W * 64 - 1) / (W * 64);
-    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : 4;       // scale bytes
+    constexpr bool QK = F == BlkFmt::Q4_K;
+    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : 2;       // scale bytes (Q4_0, Q8_0)
     constexpr int PPT = 4 * SB;                         // 16-byte scale pieces per tile-unit
-    constexpr int SPC = (RW / 16) * UPW * PPT;
+    // 16-byte scale pieces of the workgroup; Q4_K: one super-block header per row and super-block
+    constexpr int SPC = QK ? (RW / 16) * (UPW / 2) * 16 : (RW / 16) * UPW * PPT;
     constexpr int SP = (SPC + W * 64 - 1) / (W * 64);
-    constexpr int WL = F == BlkFmt::Q4_0 ? 1 : 2;       // 16-byte weight loads per lane per tile-unit
+    constexpr int WL = F == BlkFmt::Q8_0 ? 2 : 1;       // 16-byte weight loads per lane per tile-unit
     extern __shared__ __attribute__((aligned(16))) char smem[];
     float* wmax = reinterpret_cast<float*>(smem + NPL * XPB);  // per-wave max |x|
     char* ssm = smem + NPL * XPB + 16;                            // block scales
@@ -129,10 +165,19 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     u32x4 sr[SP];
 #pragma unroll
     for (int i = 0; i < SP; i++) {
-        const int e = tid + i * W * 64, tw = e / (UPW * PPT), u = (e / PPT) % UPW, q = e % PPT;
-        const int rt = rw0 / 16 + tw;
-        const bool ok = e < SPC && rt < ntiles && u0 + u < u1;
-        const uint32_t off = ok ? (uint32_t)(((rt * nunits + u0 + u) * PPT + q) * 16) : 0x80000000u;
+        const int e = tid + i * W * 64;
+        uint32_t off;
+        if constexpr (QK) {
+            const int tw = e / (UPW / 2 * 16), sbl = (e / 16) % (UPW / 2), ri = e % 16;
+            const int rt = rw0 / 16 + tw;
+            const bool ok = e < SPC && rt < ntiles && u0 + 2 * sbl < u1;
+            off = ok ? (uint32_t)(((rt * (nunits / 2) + u0 / 2 + sbl) * 16 + ri) * 16) : 0x80000000u;
+        } else {
+            const int tw = e / (UPW * PPT), u = (e / PPT) % UPW, q = e % PPT;
+            const int rt = rw0 / 16 + tw;
+            const bool ok = e < SPC && rt < ntiles && u0 + u < u1;
+            off = ok ? (uint32_t)(((rt * nunits + u0 + u) * PPT + q) * 16) : 0x80000000u;
+        }
         sr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
     }
     uint4 w[UPW][2][WL];
@@ -171,7 +216,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             const int r = p / PPR, c4 = (p % PPR) * 4;
             // Q4_0: the activations of high-nibble elements (16..31 of a block)
             // are staged at 1/16, as their A halves are q * 2^-20
-            const float cr = (F == BlkFmt::Q4_0 && (r & 16)) ? cs * 0.0625f : cs;
+            const float cr = (F != BlkFmt::Q8_0 && (r & 16)) ? cs * 0.0625f : cs;
             const int base = mfma_xrow(blkt_lds_row<F>(r), 16);
             uint32_t hv[2], lv[2];
 #pragma unroll
@@ -197,7 +242,32 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
 #pragma unroll
     for (int i = 0; i < SP; i++) {
         const int e = tid + i * W * 64;
-        if (e < SPC) *reinterpret_cast<u32x4*>(ssm + e * 16) = sr[i];
+        if constexpr (QK) {
+            // header -> (d * scale, dmin * min) of the super-block's 8 sub-blocks
+            // (tensor/quantized_kquant.go:34-79), fp32 products as the reference
+            // forms them; stored [tile][unit][16 rows][4 blocks] as float2
+            const int tw = e / (UPW / 2 * 16), sbl = (e / 16) % (UPW / 2), ri = e % 16;
+            if (e < SPC && u0 + 2 * sbl < u1) {
+                const u32x4 h = sr[i];
+                const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+                uint8_t b[12];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    b[k] = (uint8_t)(h.y >> (8 * k));
+                    b[4 + k] = (uint8_t)(h.z >> (8 * k));
+                    b[8 + k] = (uint8_t)(h.w >> (8 * k));
+                }
+                float2* dst = reinterpret_cast<float2*>(ssm) + ((tw * UPW + 2 * sbl) * 16 + ri) * 4;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int sc = j < 4 ? (b[j] & 63) : ((b[j + 4] & 0xF) | ((b[j - 4] >> 6) << 4));
+                    const int mn = j < 4 ? (b[4 + j] & 63) : ((b[j + 4] >> 4) | ((b[j] >> 6) << 4));
+                    dst[(j >> 2) * 64 + (j & 3)] = make_float2(d * (float)sc, dmin * (float)mn);
+                }
+            }
+        } else {
+            if (e < SPC) *reinterpret_cast<u32x4*>(ssm + e * 16) = sr[i];
+        }
     }
     // LDS writes visible to the workgroup; the weight loads stay in flight.
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -211,9 +281,11 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     // tiles' weight MFMAs, so each step's D is 2^-24 * sum((q - off) x)
     // (Q4_0: -8 * 2^-20 in the halves of high-nibble elements, whose
     // activations are staged at 1/16)
-    const _Float16 ol = __builtin_bit_cast(_Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : 0x8080u));
-    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)0x8080u);
-    const half8v aoff = F == BlkFmt::Q4_0 ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
+    // Q4_K: +2^-24 (+2^-20 in high-nibble halves), so the MFMA gives
+    // 2^-24 * sum(x) of each sub-block, for its min term.
+    const _Float16 ol = __builtin_bit_cast(_Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : 0x8080u));
+    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)(QK ? 0x0010u : 0x8080u));
+    const half8v aoff = F != BlkFmt::Q8_0 ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
                                           : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
     float4v acc[2];
     acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
@@ -221,13 +293,17 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     for (int u = 0; u < UPW; u++) {
         if (u0 + u < u1) {
             // the 4 block scales of rows 4 lg + i of each tile for this unit
+            // (Q4_K: the (scale, min) pairs of the 4 blocks, two float4 a row)
             using SV = typename std::conditional<F == BlkFmt::Q4_0, uint2, float4>::type;
-            SV sc[2][4];
+            constexpr int SVR = QK ? 2 : 1;
+            SV sc[2][4][SVR];
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    sc[t][i] = reinterpret_cast<const SV*>(ssm)[((2 * wave + t) * UPW + u) * 16 + 4 * lg + i];
+#pragma unroll
+                    for (int h = 0; h < SVR; h++)
+                        sc[t][i][h] = reinterpret_cast<const SV*>(ssm)[(((2 * wave + t) * UPW + u) * 16 + 4 * lg + i) * SVR + h];
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 half8v bv[NPL];
@@ -242,7 +318,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     u32x4 av;
-                    if constexpr (F == BlkFmt::Q4_0) {
+                    if constexpr (F != BlkFmt::Q8_0) {
                         const uint4 q = w[u][t][0];
                         const uint32_t dw = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
                         const uint32_t d8 = dw >> 8;  // halves: q 2^-24 (low nibbles), q 2^-20 (high)
@@ -254,19 +330,26 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                         av = (u32x4){__builtin_amdgcn_perm(da, da, 0x0C010C00u), __builtin_amdgcn_perm(da, da, 0x0C030C02u),
                                      __builtin_amdgcn_perm(db, db, 0x0C010C00u), __builtin_amdgcn_perm(db, db, 0x0C030C02u)};
                     }
-                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[0], dn, 0, 0, 0);
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[0],
+                                                                      QK ? (float4v){0.f, 0.f, 0.f, 0.f} : dn, 0, 0, 0);
                     if constexpr (NPL == 2)
                         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[1], d, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        float sv;
-                        if constexpr (F == BlkFmt::Q4_0) {
-                            const uint32_t h2 = (s < 2) ? sc[t][i].x : sc[t][i].y;
-                            sv = h2f((s & 1) ? (uint16_t)(h2 >> 16) : (uint16_t)(h2 & 0xffffu));
+                        if constexpr (QK) {
+                            const SV& pr = sc[t][i][s >> 1];
+                            const float sv = (s & 1) ? pr.z : pr.x, mv = (s & 1) ? pr.w : pr.y;
+                            acc[t][i] = fmaf(sv, d[i], fmaf(-mv, dn[i], acc[t][i]));
                         } else {
-                            sv = s == 0 ? sc[t][i].x : s == 1 ? sc[t][i].y : s == 2 ? sc[t][i].z : sc[t][i].w;
+                            float sv;
+                            if constexpr (F == BlkFmt::Q4_0) {
+                                const uint32_t h2 = (s < 2) ? sc[t][i][0].x : sc[t][i][0].y;
+                                sv = h2f((s & 1) ? (uint16_t)(h2 >> 16) : (uint16_t)(h2 & 0xffffu));
+                            } else {
+                                sv = s == 0 ? sc[t][i][0].x : s == 1 ? sc[t][i][0].y : s == 2 ? sc[t][i][0].z : sc[t][i][0].w;
+                            }
+                            acc[t][i] = fmaf(sv, d[i], acc[t][i]);
                         }
-                        acc[t][i] = fmaf(sv, d[i], acc[t][i]);
                     }
                 }
             }
@@ -303,7 +386,7 @@ template <BlkFmt F, int UPW, int N>
 static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y, float* ws,
                         int M, int K) {
     constexpr int NPL = N <= 8 ? 1 : 2;
-    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : 4;
+    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : F == BlkFmt::Q8_0 ? 4 : 8;  // LDS bytes per (row, block)
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
     blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, x, y, ws, M, K);
 }
@@ -325,7 +408,7 @@ static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, cons
 template <BlkFmt F>
 static dim3 blkt_grid(int M, int K, int& upw) {
     const int nunits = K / 128, gx = ceil_div(M, 128);
-    const long minwg = F == BlkFmt::Q4_0 ? 256 : 512;
+    const long minwg = F == BlkFmt::Q8_0 ? 512 : 256;
     upw = 4;
     while (upw > 2 && (long)gx * ceil_div(nunits, upw) < minwg) upw >>= 1;
     return dim3(gx, ceil_div(nunits, upw));
@@ -333,7 +416,8 @@ static dim3 blkt_grid(int M, int K, int& upw) {
 
 template <BlkFmt F>
 static long blkt_ws_bytes(int M, int K, int N) {
-    if (M < 0 || K < 0 || K % 128 != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
+    constexpr int KQ = F == BlkFmt::Q4_K ? 256 : 128;
+    if (M < 0 || K < 0 || K % KQ != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
     if (M == 0 || K == 0) return 0;
     int upw;
     return tiled_ws_bytes(M, (int)blkt_grid<F>(M, K, upw).y);
@@ -342,13 +426,14 @@ static long blkt_ws_bytes(int M, int K, int N) {
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                      void* ws, long ws_bytes, hipStream_t stream) {
-    if (M < 0 || K < 0 || K % 128 != 0) return (int)hipErrorInvalidValue;
+    constexpr int KQ = F == BlkFmt::Q4_K ? 256 : 128;  // Q4_K: whole super-blocks, an even unit count
+    if (M < 0 || K < 0 || K % KQ != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
     if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
         return (int)hipErrorInvalidValue;
-    constexpr long SB = F == BlkFmt::Q4_0 ? 2 : 4;
+    constexpr long SB = F == BlkFmt::Q8_0 ? 4 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     int upw;
     const dim3 g = blkt_grid<F>(M, K, upw);
@@ -429,4 +514,35 @@ ZT_EXPORT long zt_gemm_q8t_workspace_bytes(int M, int K, int N) { return blkt_ws
 ZT_EXPORT int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                               void* workspace, long workspace_bytes, hipStream_t stream) {
     return gemm_blkt<BlkFmt::Q8_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
+}
+
+ZT_EXPORT long zt_q4k_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 2);
+}
+
+ZT_EXPORT long zt_q4k_tiled_header_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 256) * 16;
+}
+
+ZT_EXPORT int zt_q4k_tile(const void* W_q4k, int M, int K, void* W_tiled, void* H_tiled, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_q4k == nullptr || W_tiled == nullptr || H_tiled == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_q4k & 15) || ((uintptr_t)W_tiled & 15) || ((uintptr_t)H_tiled & 15))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 64;
+    q4kt_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(W_q4k),
+                                                                static_cast<u32x4*>(W_tiled),
+                                                                static_cast<u32x4*>(H_tiled), M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT long zt_gemm_q4kt_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q4_K>(M, K, N); }
+
+ZT_EXPORT int zt_gemm_q4kt_f32(const void* W_tiled, const void* H_tiled, const float* B, float* C, int M, int K, int N,
+                               void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q4_K>(W_tiled, H_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
 }

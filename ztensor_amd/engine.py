@@ -279,12 +279,30 @@ class ROCmEngine:
             return x.dtype in (torch.float32, torch.float16)
         if isinstance(s, Q8Storage):
             return x.dtype == torch.float32
+        if isinstance(s, Q4KStorage):
+            return x.dtype == torch.float32 and k % 256 == 0
         if isinstance(s, IQ4NLStorage):
             return x.dtype == torch.float16
         if isinstance(s, (GPTQStorage, AWQStorage)):
             return (x.dtype == torch.float16 and s.group_size % 128 == 0 and
                     rows * (k // s.group_size) < 1 << 29)
         return False
+
+    def _q4k_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The tiled copy of uploaded Q4_K super-blocks (data in the Q4_0
+        tile format plus the super-block headers) for batches of 4-16 fp32
+        columns, built on the device on the first batched call."""
+        cached = getattr(s, "_gpu_tiled", None)
+        if cached is not None and cached[0] == (rows, k):
+            return cached[1], cached[2]
+        nbytes, hbytes = self.lib.zt_q4k_tiled_bytes(rows, k), self.lib.zt_q4k_tiled_header_bytes(rows, k)
+        if nbytes < 0 or hbytes < 0:
+            raise ValueError(f"Q4_K tiled layout: unsupported shape [{rows}, {k}]")
+        wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        ht = torch.empty(hbytes, dtype=torch.uint8, device=self.device)
+        self.lib.call("zt_q4k_tile", _p(buf.tensor), rows, k, _p(wt), _p(ht), self._s)
+        s._gpu_tiled = ((rows, k), wt, ht)  # type: ignore[attr-defined]
+        return wt, ht
 
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
@@ -371,6 +389,13 @@ class ROCmEngine:
             if x.dtype != torch.float32:
                 raise TypeError(f"{type(s).__name__} matmul takes fp32 activations")
             q50 = isinstance(s, Q5_0Storage)
+            if isinstance(s, Q4KStorage) and n in _TILED_BATCHES and k % 256 == 0:
+                # batched Q4_K on the tiled MFMA kernel
+                xs = x if _p(x) % 16 == 0 else x.clone()
+                wt, ht = self._q4k_tiled(s, buf, rows, k)
+                ws, wsb = self._workspace(self.lib.zt_gemm_q4kt_workspace_bytes(rows, k, n))
+                self.lib.call("zt_gemm_q4kt_f32", _p(wt), _p(ht), _p(xs), _p(c), rows, k, n, ws, wsb, self._s)
+                return c
             if n == 1 and k % (32 if q50 else 256) == 0:
                 # fused dequant-GEMV (compute/gpu_engine.go:2224-2238, 2505-2510)
                 if q50:
@@ -473,7 +498,7 @@ class ROCmEngine:
         return w
 
 
-_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL / Q4_0 / Q8_0 layouts
+_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL / Q4_0 / Q8_0 / Q4_K layouts
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
