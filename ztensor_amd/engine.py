@@ -428,7 +428,8 @@ class ROCmEngine:
     def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
                     c: torch.Tensor) -> torch.Tensor:
         """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
-        the GGML type picks the kernel.  Q8_0 runs on its own repacked layout
+        the GGML type picks the kernel.  Q4_0 and Q4_K batches of 4-16 run on
+        the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
         (the reference passes the 34-byte blocks to the 36-byte kernel,
         compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
         its CPU engine, runs on the Q5_0 GEMV; types without a quantized
@@ -436,7 +437,17 @@ class ROCmEngine:
         if x.dtype != torch.float32:
             raise TypeError("MmapStorage matmul takes fp32 activations")
         q, p, offs = s.qtype, _p(buf.tensor), s._gpu_offsets
-        if q == GGMLType.Q4_0:
+        tiled = n in _TILED_BATCHES and _p(x) % 16 == 0
+        if q == GGMLType.Q4_0 and tiled and k % 128 == 0:
+            # batches on the tiled MFMA kernel, as for Q4Storage (the device layout is RawBytesGPU)
+            wt, st = self._block_tiled(s, buf, rows, k, "q4")
+            ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
+            self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
+        elif q == GGMLType.Q4_K and tiled and k % 256 == 0:
+            wt, ht = self._q4k_tiled(s, buf, rows, k)
+            ws, wsb = self._workspace(self.lib.zt_gemm_q4kt_workspace_bytes(rows, k, n))
+            self.lib.call("zt_gemm_q4kt_f32", _p(wt), _p(ht), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
+        elif q == GGMLType.Q4_0:
             self.gemm_q4_f32(p, _p(x), _p(c), rows, k, n, offs["data_offset"])
         elif q == GGMLType.Q8_0:
             self.lib.call("zt_gemm_q8gguf_f32", p, _p(x), _p(c), rows, k, n, offs["data_offset"], self._s)
