@@ -241,6 +241,11 @@ int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, fl
 long zt_q8_tiled_bytes(int M, int K);
 long zt_q8_tiled_scale_bytes(int M, int K);
 int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
+/* The same tiled Q8_0 layout built from the GGUF Q8_0 separated layout
+ * (fp16 scales, zt_q8gguf_raw_to_gpu, data_offset = zt_q8gguf_gpu_data_offset):
+ * the scales are widened to fp32 exactly, so zt_gemm_q8t_f32 runs GGUF Q8_0
+ * batches (MmapStorage, tensor/mmap_storage.go:94-96). */
+int zt_q8gguf_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
 long zt_gemm_q8t_workspace_bytes(int M, int K, int N);
 int zt_gemm_q8t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                     void* workspace, long workspace_bytes, zt_stream_t stream);

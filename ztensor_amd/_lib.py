@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q8_tiled_bytes": (L, [I, I]),
     "zt_q8_tiled_scale_bytes": (L, [I, I]),
     "zt_q8_tile": (I, [P, I, I, L, P, P, P]),
+    "zt_q8gguf_tile": (I, [P, I, I, L, P, P, P]),
     "zt_gemm_q8t_workspace_bytes": (L, [I, I, I]),
     "zt_gemm_q8t_f32": (I, [P, P, P, P, I, I, I, P, L, P]),
     "zt_q4k_tiled_bytes": (L, [I, I]),

@@ -47,7 +47,10 @@ namespace zt {
 
 enum class BlkFmt { Q4_0, Q8_0, Q4_K };
 
-__global__ void q8t_tile_kernel(const uint2* __restrict__ data, const float* __restrict__ scales,
+// ST: the separated layout's scale type (float for Q8Storage, fp16 bits for
+// GGUF Q8_0, widened exactly); the tiled scales are fp32 either way.
+template <class ST>
+__global__ void q8t_tile_kernel(const uint2* __restrict__ data, const ST* __restrict__ scales,
                                 u32x4* __restrict__ wt, float* __restrict__ st, int rows, int nunits, long npieces) {
     const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= npieces) return;
@@ -63,7 +66,14 @@ __global__ void q8t_tile_kernel(const uint2* __restrict__ data, const float* __r
         v = (u32x4){a.x, a.y, b.x, b.y};
     }
     wt[p] = v;
-    if (h == 0) st[tu * 64 + i * 4 + g] = row < rows ? scales[row * nb + 4L * u + g] : 0.0f;
+    if (h == 0) {
+        float sv = 0.0f;
+        if (row < rows) {
+            if constexpr (sizeof(ST) == 2) sv = h2f(scales[row * nb + 4L * u + g]);
+            else sv = scales[row * nb + 4L * u + g];
+        }
+        st[tu * 64 + i * 4 + g] = sv;
+    }
 }
 
 // Q4_K tiled layout: the data in the Q4_0 tile format (each 32-value
@@ -492,21 +502,31 @@ ZT_EXPORT long zt_q8_tiled_scale_bytes(int M, int K) {
     return (long)((M + 15) / 16) * 16 * (K / 32) * 4;
 }
 
-ZT_EXPORT int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled,
-                         hipStream_t stream) {
+template <class ST>
+static int q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, hipStream_t stream) {
     if (M < 0 || K < 0 || K % 128 != 0 || data_offset < 0) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
     if (A_q8 == nullptr || W_tiled == nullptr || S_tiled == nullptr) return (int)hipErrorInvalidValue;
     const uint8_t* base = static_cast<const uint8_t*>(A_q8);
-    if (((uintptr_t)base & 3) || ((uintptr_t)(base + data_offset) & 15) || ((uintptr_t)W_tiled & 15) ||
+    if (((uintptr_t)base & (sizeof(ST) - 1)) || ((uintptr_t)(base + data_offset) & 15) || ((uintptr_t)W_tiled & 15) ||
         ((uintptr_t)S_tiled & 15))
         return (int)hipErrorInvalidValue;
     const int nunits = K / 128;
     const long npieces = (long)((M + 15) / 16) * nunits * 128;
-    q8t_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(
-        reinterpret_cast<const uint2*>(base + data_offset), reinterpret_cast<const float*>(base),
+    q8t_tile_kernel<ST><<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        reinterpret_cast<const uint2*>(base + data_offset), reinterpret_cast<const ST*>(base),
         static_cast<u32x4*>(W_tiled), static_cast<float*>(S_tiled), M, nunits, npieces);
     return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled,
+                         hipStream_t stream) {
+    return q8_tile<float>(A_q8, M, K, data_offset, W_tiled, S_tiled, stream);
+}
+
+ZT_EXPORT int zt_q8gguf_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled,
+                             hipStream_t stream) {
+    return q8_tile<uint16_t>(A_q8, M, K, data_offset, W_tiled, S_tiled, stream);
 }
 
 ZT_EXPORT long zt_gemm_q8t_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q8_0>(M, K, N); }

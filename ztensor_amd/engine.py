@@ -260,8 +260,9 @@ class ROCmEngine:
         cached = getattr(s, "_gpu_tiled", None)
         if cached is not None and cached[0] == (rows, k):
             return cached[1], cached[2]
-        nbytes = getattr(self.lib, f"zt_{fmt}_tiled_bytes")(rows, k)
-        sbytes = getattr(self.lib, f"zt_{fmt}_tiled_scale_bytes")(rows, k)
+        size_fmt = "q8" if fmt == "q8gguf" else fmt  # GGUF Q8_0 tiles into the Q8_0 layout
+        nbytes = getattr(self.lib, f"zt_{size_fmt}_tiled_bytes")(rows, k)
+        sbytes = getattr(self.lib, f"zt_{size_fmt}_tiled_scale_bytes")(rows, k)
         if nbytes < 0 or sbytes < 0:
             raise ValueError(f"{fmt} tiled layout: unsupported shape [{rows}, {k}]")
         wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
@@ -428,8 +429,8 @@ class ROCmEngine:
     def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
                     c: torch.Tensor) -> torch.Tensor:
         """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
-        the GGML type picks the kernel.  Q4_0 and Q4_K batches of 4-16 run on
-        the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
+        the GGML type picks the kernel.  Q4_0, Q4_K and Q8_0 batches of 4-16
+        run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
         (the reference passes the 34-byte blocks to the 36-byte kernel,
         compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
         its CPU engine, runs on the Q5_0 GEMV; types without a quantized
@@ -447,6 +448,10 @@ class ROCmEngine:
             wt, ht = self._q4k_tiled(s, buf, rows, k)
             ws, wsb = self._workspace(self.lib.zt_gemm_q4kt_workspace_bytes(rows, k, n))
             self.lib.call("zt_gemm_q4kt_f32", _p(wt), _p(ht), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
+        elif q == GGMLType.Q8_0 and tiled and k % 128 == 0:
+            wt, st = self._block_tiled(s, buf, rows, k, "q8gguf")
+            ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
+            self.lib.call("zt_gemm_q8t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
         elif q == GGMLType.Q4_0:
             self.gemm_q4_f32(p, _p(x), _p(c), rows, k, n, offs["data_offset"])
         elif q == GGMLType.Q8_0:
