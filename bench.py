@@ -335,6 +335,7 @@ SUITE = {
     "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q4_kt": ("q4_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
+    "q5_0t": ("q5_0t", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
 }
 
 
@@ -394,6 +395,25 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: gemm(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N,
                                 wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes(fmt[:4], rows, K, N)
+    elif fmt == "q5_0t":
+        # batched Q5_0 on the tiled layout (zt_q5_0_tile), built once outside the timing
+        w = synth.kquant("q5_0", rows, K, seed)
+        nblk = rows * K // 32
+        host = np.empty(lib.zt_q5_0_gpu_bytes(nblk), np.uint8)
+        lib.zt_q5_0_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
+        sep = dev(host)
+        wbufs = [torch.empty(f(rows, K), dtype=torch.uint8, device="cuda")
+                 for f in (lib.zt_q5_0_tiled_bytes, lib.zt_q5_0_tiled_scale_bytes, lib.zt_q5_0_tiled_qh_bytes)]
+        lib.call("zt_q5_0_tile", sep.data_ptr(), rows, K, lib.zt_q5_0_gpu_qh_offset(nblk),
+                 lib.zt_q5_0_gpu_qs_offset(nblk), *(t.data_ptr() for t in wbufs), s)
+        torch.cuda.synchronize()
+        del sep
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        wsb = lib.zt_gemm_q5_0t_workspace_bytes(rows, K, N)
+        wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")
+        fn = lambda wb, y: lib.zt_gemm_q5_0t_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
+                                                 y.data_ptr(), rows, K, N, wsbuf.data_ptr(), wsb, s)
+        nbytes = synth.algorithmic_bytes("q5_0", rows, K, N)
     elif fmt == "q4_kt":
         # batched Q4_K on the tiled layout (zt_q4k_tile), built once outside the timing
         w = synth.kquant("q4_k", rows, K, seed)

@@ -270,6 +270,24 @@ long zt_gemm_q4kt_workspace_bytes(int M, int K, int N);
 int zt_gemm_q4kt_f32(const void* W_tiled, const void* H_tiled, const float* B, float* C, int M, int K, int N,
                      void* workspace, long workspace_bytes, zt_stream_t stream);
 
+/* Batched Q5_0 on the same MFMA kernel.  zt_q5_0_tile takes Q5_0Storage's
+ * RawBytesGPU (tensor/quantized_q5_0.go:118-165; offsets zt_q5_0_gpu_qh_offset
+ * / zt_q5_0_gpu_qs_offset) and writes the nibbles and fp16 scales in the
+ * Q4_0 tiled layout (zt_q5_0_tiled_bytes, zt_q5_0_tiled_scale_bytes) plus
+ * one dword of fifth bits per lane and tile-unit (zt_q5_0_tiled_qh_bytes;
+ * byte s = block 4u+s, bits = values 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3,
+ * 4g+17, 4g+19 of lane 16g+i's row).  zt_gemm_q5_0t_f32: fp32 B [K, N],
+ * N in {4, 8, 12, 16}, K % 128 == 0, workspace as for Q4_0; each block adds
+ * d * sum((q5 - 16) x).  Replaces the per-column GEMV of batched Q5_0. */
+long zt_q5_0_tiled_bytes(int M, int K);
+long zt_q5_0_tiled_scale_bytes(int M, int K);
+long zt_q5_0_tiled_qh_bytes(int M, int K);
+int zt_q5_0_tile(const void* A_q5, int M, int K, long qh_offset, long qs_offset, void* W_tiled, void* S_tiled,
+                 void* H_tiled, zt_stream_t stream);
+long zt_gemm_q5_0t_workspace_bytes(int M, int K, int N);
+int zt_gemm_q5_0t_f32(const void* W_tiled, const void* S_tiled, const void* H_tiled, const float* B, float* C, int M,
+                      int K, int N, void* workspace, long workspace_bytes, zt_stream_t stream);
+
 /* ---- Ternary ----------------------------------------------------------- */
 
 /* Replaces ternary_gemv_f32 (internal/cuda/kernels/ternary_gemv.cu:85-99),

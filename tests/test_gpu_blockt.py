@@ -448,3 +448,103 @@ def test_engine_batched_q4k_uses_tiled_layout(lib, orc, n):
     y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
     assert rel_err(y, q4k_oracle(orc, w.raw, x, rows, K, n)) <= TOL
     assert getattr(s, "_gpu_tiled", None) is not None
+
+
+# ---- batched Q5_0 on the same kernel (zt_q5_0_tile, zt_gemm_q5_0t_f32)
+
+Q5_BITS = [0, 2, 16, 18, 1, 3, 17, 19]  # fifth-bit order in a lane's byte, offset by 4g
+
+
+def q5_tile_dev(lib, raw, rows, K):
+    nblk = rows * K // 32
+    host = np.empty(lib.zt_q5_0_gpu_bytes(nblk), np.uint8)
+    lib.zt_q5_0_raw_to_gpu(raw.ctypes.data, nblk, host.ctypes.data)
+    a = dev(host)
+    bufs = [torch.empty(f(rows, K), dtype=torch.uint8, device="cuda")
+            for f in (lib.zt_q5_0_tiled_bytes, lib.zt_q5_0_tiled_scale_bytes, lib.zt_q5_0_tiled_qh_bytes)]
+    lib.call("zt_q5_0_tile", a.data_ptr(), rows, K, lib.zt_q5_0_gpu_qh_offset(nblk), lib.zt_q5_0_gpu_qs_offset(nblk),
+             *(b.data_ptr() for b in bufs), stream())
+    torch.cuda.synchronize()
+    return bufs
+
+
+def q5_tile_ref(raw, rows, K):
+    """Nibbles and scales: the Q4_0 tiled layout of the same 16 + 2 bytes;
+    fifth bits: byte s of lane 16g+i's dword = bits 4g + Q5_BITS of block
+    4u+s's qh word."""
+    nt, nu, kb = (rows + 15) // 16, K // 128, K // 32
+    blk = raw.reshape(rows * kb, 22)
+    q4like = np.concatenate([blk[:, :2], blk[:, 6:]], axis=1).reshape(-1)
+    dt, st = tile_ref("q4", q4like, rows, K)
+    qh = np.zeros((nt * 16, kb), np.uint32)
+    qh[:rows] = blk[:, 2:6].copy().view("<u4").reshape(rows, kb)
+    q = qh.reshape(nt, 16, nu, 4)  # [rt, i, u, s]
+    out = np.zeros((nt, nu, 4, 16), np.uint32)  # [rt, u, g, i]
+    for g in range(4):
+        byte = np.zeros((nt, 16, nu, 4), np.uint32)
+        for k, e in enumerate(Q5_BITS):
+            byte |= ((q >> np.uint32(4 * g + e)) & np.uint32(1)) << np.uint32(k)
+        word = byte[..., 0] | (byte[..., 1] << np.uint32(8)) | (byte[..., 2] << np.uint32(16)) | (byte[..., 3] << np.uint32(24))
+        out[:, :, g, :] = word.transpose(0, 2, 1)
+    return dt, st, out.reshape(-1)
+
+
+def run_q5t(lib, bufs, x, rows, K, N):
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    nb = lib.zt_gemm_q5_0t_workspace_bytes(rows, K, N)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
+    lib.call("zt_gemm_q5_0t_f32", *(b.data_ptr() for b in bufs), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             ws.data_ptr(), nb, stream())
+    return c.cpu().numpy().reshape(rows, N)
+
+
+def q5_oracle(orc, raw, x, rows, K, N):
+    xt = np.ascontiguousarray(np.asarray(x, np.float32).reshape(K, N).T)
+    return orc.gemm_f32_q5_0_nt(xt, raw, N, rows, K).reshape(N, rows).T
+
+
+@pytest.mark.parametrize("rows,K", [(16, 128), (17, 256), (100, 1024), (1, 384)])
+def test_q5_tile_layout_bytes(lib, rows, K):
+    w = synth.kquant("q5_0", rows, K, 94)
+    bufs = q5_tile_dev(lib, w.raw, rows, K)
+    dref, sref, href = q5_tile_ref(w.raw, rows, K)
+    assert np.array_equal(bufs[0].cpu().numpy(), dref)
+    assert np.array_equal(bufs[1].cpu().numpy().view("<u2"), sref)
+    assert np.array_equal(bufs[2].cpu().numpy().view("<u4"), href)
+
+
+@pytest.mark.parametrize("rows,K,N", [(16, 128, 4), (17, 256, 8), (33, 2176, 12), (65, 384, 16), (100, 4096, 8),
+                                      (1, 128, 16), (300, 1024, 16)])
+def test_q5t_ragged(lib, orc, rows, K, N):
+    print(f"q5t rows={rows} K={K} N={N}", flush=True)
+    w = synth.kquant("q5_0", rows, K, 95)
+    x = synth.x_f32(K * N, 95).reshape(K, N)
+    bufs = q5_tile_dev(lib, w.raw, rows, K)
+    assert rel_err(run_q5t(lib, bufs, x, rows, K, N), q5_oracle(orc, w.raw, x, rows, K, N)) <= TOL
+
+
+@pytest.mark.parametrize("N", [4, 8, 16])
+@pytest.mark.parametrize("rows,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_q5t_llama3_shapes(lib, orc, rows, K, N):
+    print(f"q5t rows={rows} K={K} N={N}", flush=True)
+    w = synth.kquant("q5_0", rows, K, 96)
+    x = synth.x_f32(K * N, 96 + N).reshape(K, N)
+    bufs = q5_tile_dev(lib, w.raw, rows, K)
+    y = run_q5t(lib, bufs, x, rows, K, N)
+    err = rel_err(y, q5_oracle(orc, w.raw, x, rows, K, N))
+    assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("n", [5, 8])
+def test_engine_batched_q5_0_uses_tiled_layout(lib, orc, n):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import Q5_0Storage, Tensor
+
+    rows, K = 300, 1024
+    w = synth.kquant("q5_0", rows, K, 97)
+    s = Q5_0Storage(w.raw, rows * K)
+    x = synth.x_f32(K * n, 97).reshape(K, n)
+    y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
+    assert rel_err(y, q5_oracle(orc, w.raw, x, rows, K, n)) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None

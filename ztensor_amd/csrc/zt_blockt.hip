@@ -45,7 +45,7 @@
 
 namespace zt {
 
-enum class BlkFmt { Q4_0, Q8_0, Q4_K };
+enum class BlkFmt { Q4_0, Q8_0, Q4_K, Q5_0 };
 
 // ST: the separated layout's scale type (float for Q8Storage, fp16 bits for
 // GGUF Q8_0, widened exactly); the tiled scales are fp32 either way.
@@ -110,6 +110,41 @@ __global__ void q4kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restr
     }
 }
 
+// Q5_0 tiled layout (from Q5_0Storage's RawBytesGPU: fp16 scales, uint32
+// fifth-bit words, nibbles): the nibbles and scales exactly as the Q4_0 tiled
+// layout, plus one dword per lane and tile-unit holding the fifth bits of
+// the lane's 8 values in each of the 4 blocks (byte s = block 4u+s; bits
+// 0..7 = values 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3, 4g+17, 4g+19, the order
+// in which the kernel's masks take them).
+__global__ void q5t_tile_kernel(const uint16_t* __restrict__ scales, const uint32_t* __restrict__ qh,
+                                const uint32_t* __restrict__ qs, u32x4* __restrict__ wt, uint16_t* __restrict__ st,
+                                uint32_t* __restrict__ ht, int rows, int nunits, long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63), i = lane & 15, g = lane >> 4;
+    const long tu = p >> 6;
+    const int u = (int)(tu % nunits);
+    const long row = (tu / nunits) * 16 + i;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    uint32_t h = 0u;
+    uint16_t sc = 0;
+    if (row < rows) {
+        const long b0 = row * (long)nunits * 4 + 4L * u;
+        v = (u32x4){qs[b0 * 4 + g], qs[(b0 + 1) * 4 + g], qs[(b0 + 2) * 4 + g], qs[(b0 + 3) * 4 + g]};
+        const int e[8] = {4 * g, 4 * g + 2, 4 * g + 16, 4 * g + 18, 4 * g + 1, 4 * g + 3, 4 * g + 17, 4 * g + 19};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t w = qh[b0 + s];
+#pragma unroll
+            for (int k = 0; k < 8; k++) h |= ((w >> e[k]) & 1u) << (8 * s + k);
+        }
+        sc = scales[b0 + g];
+    }
+    wt[p] = v;
+    ht[p] = h;
+    st[tu * 64 + i * 4 + g] = sc;
+}
+
 // LDS row of chunk-relative activation row r (K index within the
 // workgroup's range).  Within each 128-K unit, the 8 activations that lane
 // group g of MFMA step s multiplies sit in rows 32 g + 8 s .. +7, in the
@@ -133,8 +168,9 @@ __device__ __forceinline__ int blkt_lds_row(int r) {
 
 template <BlkFmt F, int UPW, int N>
 __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict__ wt, const void* __restrict__ stl,
-                                                        const float* __restrict__ x, float* __restrict__ y,
-                                                        float* __restrict__ ws, int rows, int K) {
+                                                        const uint32_t* __restrict__ aux, const float* __restrict__ x,
+                                                        float* __restrict__ y, float* __restrict__ ws, int rows,
+                                                        int K) {
     constexpr int W = 4;
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
@@ -199,6 +235,18 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             const int rt = min(row0 / 16 + t, ntiles - 1);
 #pragma unroll
             for (int h = 0; h < WL; h++) w[u][t][h] = ld_stream(wt + (((long)rt * nunits + unit) * WL + h) * 64 + lane);
+        }
+    }
+    uint32_t qhw[F == BlkFmt::Q5_0 ? UPW : 1][2];  // Q5_0: fifth bits of the lane's values, 4 blocks a dword
+    if constexpr (F == BlkFmt::Q5_0) {
+#pragma unroll
+        for (int u = 0; u < UPW; u++) {
+            const int unit = min(u0 + u, u1 - 1);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int rt = min(row0 / 16 + t, ntiles - 1);
+                qhw[u][t] = __builtin_nontemporal_load(aux + ((long)rt * nunits + unit) * 64 + lane);
+            }
         }
     }
     // workgroup max |x| -> power-of-two normalisation c = 2^sh
@@ -293,8 +341,10 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     // activations are staged at 1/16)
     // Q4_K: +2^-24 (+2^-20 in high-nibble halves), so the MFMA gives
     // 2^-24 * sum(x) of each sub-block, for its min term.
-    const _Float16 ol = __builtin_bit_cast(_Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : 0x8080u));
-    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)(QK ? 0x0010u : 0x8080u));
+    // (Q5_0: offset 16, -16 * 2^-24 and -16 * 2^-20)
+    const _Float16 ol = __builtin_bit_cast(
+        _Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : F == BlkFmt::Q5_0 ? 0x8010u : 0x8080u));
+    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)(QK ? 0x0010u : F == BlkFmt::Q5_0 ? 0x8100u : 0x8080u));
     const half8v aoff = F != BlkFmt::Q8_0 ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
                                           : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
     float4v acc[2];
@@ -304,7 +354,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
         if (u0 + u < u1) {
             // the 4 block scales of rows 4 lg + i of each tile for this unit
             // (Q4_K: the (scale, min) pairs of the 4 blocks, two float4 a row)
-            using SV = typename std::conditional<F == BlkFmt::Q4_0, uint2, float4>::type;
+            using SV = typename std::conditional<F == BlkFmt::Q4_0 || F == BlkFmt::Q5_0, uint2, float4>::type;
             constexpr int SVR = QK ? 2 : 1;
             SV sc[2][4][SVR];
 #pragma unroll
@@ -333,6 +383,15 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                         const uint32_t dw = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
                         const uint32_t d8 = dw >> 8;  // halves: q 2^-24 (low nibbles), q 2^-20 (high)
                         av = (u32x4){dw & 0x000F000Fu, dw & 0x00F000F0u, d8 & 0x000F000Fu, d8 & 0x00F000F0u};
+                        if constexpr (F == BlkFmt::Q5_0) {
+                            // fifth bits: 16 more in each half, bit 4 (low halves) or bit 8 (high);
+                            // y = byte | byte << 15 puts byte bits k and k+1 16 bits apart
+                            const uint32_t xb = (qhw[u][t] >> (8 * s)) & 0xFFu, yb = xb | (xb << 15);
+                            av[0] |= (yb << 4) & 0x00100010u;
+                            av[1] |= (yb << 6) & 0x01000100u;
+                            av[2] |= yb & 0x00100010u;
+                            av[3] |= (yb << 2) & 0x01000100u;
+                        }
                     } else {
                         const uint4 q = w[u][t][s >> 1];
                         const uint32_t da = ((s & 1) ? q.z : q.x) ^ 0x80808080u;
@@ -352,7 +411,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                             acc[t][i] = fmaf(sv, d[i], fmaf(-mv, dn[i], acc[t][i]));
                         } else {
                             float sv;
-                            if constexpr (F == BlkFmt::Q4_0) {
+                            if constexpr (F == BlkFmt::Q4_0 || F == BlkFmt::Q5_0) {  // fp16 scales
                                 const uint32_t h2 = (s < 2) ? sc[t][i][0].x : sc[t][i][0].y;
                                 sv = h2f((s & 1) ? (uint16_t)(h2 >> 16) : (uint16_t)(h2 & 0xffffu));
                             } else {
@@ -393,21 +452,21 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
 }
 
 template <BlkFmt F, int UPW, int N>
-static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y, float* ws,
-                        int M, int K) {
+static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const uint32_t* aux, const float* x,
+                        float* y, float* ws, int M, int K) {
     constexpr int NPL = N <= 8 ? 1 : 2;
-    constexpr int SB = F == BlkFmt::Q4_0 ? 2 : F == BlkFmt::Q8_0 ? 4 : 8;  // LDS bytes per (row, block)
+    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : F == BlkFmt::Q4_K ? 8 : 2;  // LDS bytes per (row, block)
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
-    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, x, y, ws, M, K);
+    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, aux, x, y, ws, M, K);
 }
 
 template <BlkFmt F, int N>
-static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const void* sc, const float* x, float* y,
-                          float* ws, int M, int K) {
+static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const void* sc, const uint32_t* aux,
+                          const float* x, float* y, float* ws, int M, int K) {
     if (upw >= 4)
-        launch_blkt<F, 4, N>(g, st, wt, sc, x, y, ws, M, K);
+        launch_blkt<F, 4, N>(g, st, wt, sc, aux, x, y, ws, M, K);
     else
-        launch_blkt<F, 2, N>(g, st, wt, sc, x, y, ws, M, K);
+        launch_blkt<F, 2, N>(g, st, wt, sc, aux, x, y, ws, M, K);
 }
 
 // Grid of a tiled block GEMM: 128 rows by the largest K range per
@@ -435,7 +494,7 @@ static long blkt_ws_bytes(int M, int K, int N) {
 
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                     void* ws, long ws_bytes, hipStream_t stream) {
+                     void* ws, long ws_bytes, hipStream_t stream, const void* aux = nullptr) {
     constexpr int KQ = F == BlkFmt::Q4_K ? 256 : 128;  // Q4_K: whole super-blocks, an even unit count
     if (M < 0 || K < 0 || K % KQ != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
@@ -443,6 +502,7 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
     if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
         return (int)hipErrorInvalidValue;
+    if (F == BlkFmt::Q5_0 && (aux == nullptr || ((uintptr_t)aux & 15))) return (int)hipErrorInvalidValue;
     constexpr long SB = F == BlkFmt::Q8_0 ? 4 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     int upw;
@@ -452,10 +512,10 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
     const uint4* wt = static_cast<const uint4*>(W_tiled);
     float* wsf = static_cast<float*>(ws);
     switch (N) {
-        case 4: launch_blkt_n<F, 4>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
-        case 8: launch_blkt_n<F, 8>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
-        case 12: launch_blkt_n<F, 12>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
-        default: launch_blkt_n<F, 16>(upw, g, stream, wt, S_tiled, B, C, wsf, M, K); break;
+        case 4: launch_blkt_n<F, 4>(upw, g, stream, wt, S_tiled, static_cast<const uint32_t*>(aux), B, C, wsf, M, K); break;
+        case 8: launch_blkt_n<F, 8>(upw, g, stream, wt, S_tiled, static_cast<const uint32_t*>(aux), B, C, wsf, M, K); break;
+        case 12: launch_blkt_n<F, 12>(upw, g, stream, wt, S_tiled, static_cast<const uint32_t*>(aux), B, C, wsf, M, K); break;
+        default: launch_blkt_n<F, 16>(upw, g, stream, wt, S_tiled, static_cast<const uint32_t*>(aux), B, C, wsf, M, K); break;
     }
     if (g.y > 1) tiled_reduce(ws, C, M, N, (int)g.y, stream);
     return (int)hipGetLastError();
@@ -565,4 +625,39 @@ ZT_EXPORT long zt_gemm_q4kt_workspace_bytes(int M, int K, int N) { return blkt_w
 ZT_EXPORT int zt_gemm_q4kt_f32(const void* W_tiled, const void* H_tiled, const float* B, float* C, int M, int K, int N,
                                void* workspace, long workspace_bytes, hipStream_t stream) {
     return gemm_blkt<BlkFmt::Q4_K>(W_tiled, H_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
+}
+
+ZT_EXPORT long zt_q5_0_tiled_bytes(int M, int K) { return zt_q4_tiled_bytes(M, K); }
+
+ZT_EXPORT long zt_q5_0_tiled_scale_bytes(int M, int K) { return zt_q4_tiled_scale_bytes(M, K); }
+
+ZT_EXPORT long zt_q5_0_tiled_qh_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 128 != 0) return -1;
+    return (long)((M + 15) / 16) * (K / 128) * 256;
+}
+
+ZT_EXPORT int zt_q5_0_tile(const void* A_q5, int M, int K, long qh_offset, long qs_offset, void* W_tiled,
+                           void* S_tiled, void* H_tiled, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 128 != 0 || qh_offset < 0 || qs_offset < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (A_q5 == nullptr || W_tiled == nullptr || S_tiled == nullptr || H_tiled == nullptr)
+        return (int)hipErrorInvalidValue;
+    const uint8_t* base = static_cast<const uint8_t*>(A_q5);
+    if (((uintptr_t)base & 1) || ((uintptr_t)(base + qh_offset) & 3) || ((uintptr_t)(base + qs_offset) & 15) ||
+        ((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)H_tiled & 15))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 64;
+    q5t_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        reinterpret_cast<const uint16_t*>(base), reinterpret_cast<const uint32_t*>(base + qh_offset),
+        reinterpret_cast<const uint32_t*>(base + qs_offset), static_cast<u32x4*>(W_tiled),
+        static_cast<uint16_t*>(S_tiled), static_cast<uint32_t*>(H_tiled), M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT long zt_gemm_q5_0t_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q5_0>(M, K, N); }
+
+ZT_EXPORT int zt_gemm_q5_0t_f32(const void* W_tiled, const void* S_tiled, const void* H_tiled, const float* B, float* C,
+                                int M, int K, int N, void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q5_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream, H_tiled);
 }

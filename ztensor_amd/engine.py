@@ -282,6 +282,8 @@ class ROCmEngine:
             return x.dtype == torch.float32
         if isinstance(s, Q4KStorage):
             return x.dtype == torch.float32 and k % 256 == 0
+        if isinstance(s, Q5_0Storage):
+            return x.dtype == torch.float32
         if isinstance(s, IQ4NLStorage):
             return x.dtype == torch.float16
         if isinstance(s, (GPTQStorage, AWQStorage)):
@@ -304,6 +306,28 @@ class ROCmEngine:
         self.lib.call("zt_q4k_tile", _p(buf.tensor), rows, k, _p(wt), _p(ht), self._s)
         s._gpu_tiled = ((rows, k), wt, ht)  # type: ignore[attr-defined]
         return wt, ht
+
+    def _q5_0_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, qh: int, qs: int) -> tuple:
+        """The tiled copy of uploaded Q5_0 weights (nibbles and scales in the
+        Q4_0 tiled layout, plus the fifth bits) for batches of 4-16 fp32
+        columns, built on the device on the first batched call."""
+        cached = getattr(s, "_gpu_tiled", None)
+        if cached is not None and cached[0] == (rows, k):
+            return cached[1], cached[2], cached[3]
+        sizes = [self.lib.zt_q5_0_tiled_bytes(rows, k), self.lib.zt_q5_0_tiled_scale_bytes(rows, k),
+                 self.lib.zt_q5_0_tiled_qh_bytes(rows, k)]
+        if min(sizes) < 0:
+            raise ValueError(f"Q5_0 tiled layout: unsupported shape [{rows}, {k}]")
+        wt, st, ht = (torch.empty(n, dtype=torch.uint8, device=self.device) for n in sizes)
+        self.lib.call("zt_q5_0_tile", _p(buf.tensor), rows, k, qh, qs, _p(wt), _p(st), _p(ht), self._s)
+        s._gpu_tiled = ((rows, k), wt, st, ht)  # type: ignore[attr-defined]
+        return wt, st, ht
+
+    def _q5_0_tiled_gemm(self, s: Any, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int, c: torch.Tensor,
+                         qh: int, qs: int) -> None:
+        wt, st, ht = self._q5_0_tiled(s, buf, rows, k, qh, qs)
+        ws, wsb = self._workspace(self.lib.zt_gemm_q5_0t_workspace_bytes(rows, k, n))
+        self.lib.call("zt_gemm_q5_0t_f32", _p(wt), _p(st), _p(ht), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
 
     def _weight_times(self, s: Any, rows: int, k: int, x: torch.Tensor) -> torch.Tensor:
         """dequant(W)[rows, k] @ x[k, n] -> fp32 [rows, n]."""
@@ -390,6 +414,9 @@ class ROCmEngine:
             if x.dtype != torch.float32:
                 raise TypeError(f"{type(s).__name__} matmul takes fp32 activations")
             q50 = isinstance(s, Q5_0Storage)
+            if q50 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
+                self._q5_0_tiled_gemm(s, buf, rows, k, x, n, c, s.gpu_qh_offset(), s.gpu_qs_offset())
+                return c
             if isinstance(s, Q4KStorage) and n in _TILED_BATCHES and k % 256 == 0:
                 # batched Q4_K on the tiled MFMA kernel
                 xs = x if _p(x) % 16 == 0 else x.clone()
@@ -429,8 +456,8 @@ class ROCmEngine:
     def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
                     c: torch.Tensor) -> torch.Tensor:
         """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
-        the GGML type picks the kernel.  Q4_0, Q4_K and Q8_0 batches of 4-16
-        run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
+        the GGML type picks the kernel.  Q4_0, Q4_K, Q5_0 and Q8_0 batches of
+        4-16 run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
         (the reference passes the 34-byte blocks to the 36-byte kernel,
         compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
         its CPU engine, runs on the Q5_0 GEMV; types without a quantized
@@ -452,6 +479,8 @@ class ROCmEngine:
             wt, st = self._block_tiled(s, buf, rows, k, "q8gguf")
             ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
             self.lib.call("zt_gemm_q8t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
+        elif q == GGMLType.Q5_0 and tiled and k % 128 == 0:
+            self._q5_0_tiled_gemm(s, buf, rows, k, x, n, c, offs["qh_offset"], offs["qs_offset"])
         elif q == GGMLType.Q4_0:
             self.gemm_q4_f32(p, _p(x), _p(c), rows, k, n, offs["data_offset"])
         elif q == GGMLType.Q8_0:
@@ -514,7 +543,7 @@ class ROCmEngine:
         return w
 
 
-_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled W4A16 / IQ4_NL / Q4_0 / Q8_0 / Q4_K layouts
+_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled layouts (W4A16, IQ4_NL, Q4_0, Q8_0, Q4_K, Q5_0)
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
