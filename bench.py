@@ -336,6 +336,7 @@ SUITE = {
     "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q4_kt": ("q4_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
     "q5_0t": ("q5_0t", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
+    "q5_kt": ("q5_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
 }
 
 
@@ -414,22 +415,23 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: lib.zt_gemm_q5_0t_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
                                                  y.data_ptr(), rows, K, N, wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes("q5_0", rows, K, N)
-    elif fmt == "q4_kt":
-        # batched Q4_K on the tiled layout (zt_q4k_tile), built once outside the timing
-        w = synth.kquant("q4_k", rows, K, seed)
+    elif fmt in ("q4_kt", "q5_kt"):
+        # batched Q4_K / Q5_K on the tiled layout (zt_q4k_tile / zt_q5k_tile), built once outside the timing
+        f = fmt[:4].replace("_", "")
+        w = synth.kquant(fmt[:4], rows, K, seed)
         raw = dev(w.raw)
-        wt = torch.empty(lib.zt_q4k_tiled_bytes(rows, K), dtype=torch.uint8, device="cuda")
-        ht = torch.empty(lib.zt_q4k_tiled_header_bytes(rows, K), dtype=torch.uint8, device="cuda")
-        lib.call("zt_q4k_tile", raw.data_ptr(), rows, K, wt.data_ptr(), ht.data_ptr(), s)
+        parts = ["tiled_bytes", "tiled_header_bytes"] + (["tiled_qh_bytes"] if f == "q5k" else [])
+        wbufs = [torch.empty(getattr(lib, f"zt_{f}_{p}")(rows, K), dtype=torch.uint8, device="cuda") for p in parts]
+        lib.call(f"zt_{f}_tile", raw.data_ptr(), rows, K, *(t.data_ptr() for t in wbufs), s)
         torch.cuda.synchronize()
         del raw
-        wbufs = [wt, ht]
         x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
-        wsb = lib.zt_gemm_q4kt_workspace_bytes(rows, K, N)
+        wsb = getattr(lib, f"zt_gemm_{f}t_workspace_bytes")(rows, K, N)
         wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")
-        fn = lambda wb, y: lib.zt_gemm_q4kt_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K,
-                                                N, wsbuf.data_ptr(), wsb, s)
-        nbytes = synth.algorithmic_bytes("q4_k", rows, K, N)
+        gemm = getattr(lib, f"zt_gemm_{f}t_f32")
+        fn = lambda wb, y: gemm(*(t.data_ptr() for t in wb), x.data_ptr(), y.data_ptr(), rows, K, N, wsbuf.data_ptr(),
+                                wsb, s)
+        nbytes = synth.algorithmic_bytes(fmt[:4], rows, K, N)
     elif fmt == "w4a16":
         w = synth.w4a16(rows, K, seed)
         wbufs = [dev(w.packed), dev(w.scales), dev(w.zeros)]

@@ -270,6 +270,18 @@ long zt_gemm_q4kt_workspace_bytes(int M, int K, int N);
 int zt_gemm_q4kt_f32(const void* W_tiled, const void* H_tiled, const float* B, float* C, int M, int K, int N,
                      void* workspace, long workspace_bytes, zt_stream_t stream);
 
+/* Batched Q5_K: the Q4_K tiled layout (data, headers) of the 176-byte
+ * super-blocks plus the fifth-bit dwords of the Q5_0 tiled layout
+ * (zt_q5k_tiled_qh_bytes), built by zt_q5k_tile; zt_gemm_q5kt_f32 as
+ * zt_gemm_q4kt_f32 with Q_tiled after H_tiled (11 arguments). */
+long zt_q5k_tiled_bytes(int M, int K);
+long zt_q5k_tiled_header_bytes(int M, int K);
+long zt_q5k_tiled_qh_bytes(int M, int K);
+int zt_q5k_tile(const void* W_q5k, int M, int K, void* W_tiled, void* H_tiled, void* Q_tiled, zt_stream_t stream);
+long zt_gemm_q5kt_workspace_bytes(int M, int K, int N);
+int zt_gemm_q5kt_f32(const void* W_tiled, const void* H_tiled, const void* Q_tiled, const float* B, float* C, int M,
+                     int K, int N, void* workspace, long workspace_bytes, zt_stream_t stream);
+
 /* Batched Q5_0 on the same MFMA kernel.  zt_q5_0_tile takes Q5_0Storage's
  * RawBytesGPU (tensor/quantized_q5_0.go:118-165; offsets zt_q5_0_gpu_qh_offset
  * / zt_q5_0_gpu_qs_offset) and writes the nibbles and fp16 scales in the

@@ -548,3 +548,82 @@ def test_engine_batched_q5_0_uses_tiled_layout(lib, orc, n):
     y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
     assert rel_err(y, q5_oracle(orc, w.raw, x, rows, K, n)) <= TOL
     assert getattr(s, "_gpu_tiled", None) is not None
+
+
+# ---- batched Q5_K (zt_q5k_tile, zt_gemm_q5kt_f32)
+
+def q5k_tile_dev(lib, raw, rows, K):
+    a = dev(raw)
+    bufs = [torch.empty(f(rows, K), dtype=torch.uint8, device="cuda")
+            for f in (lib.zt_q5k_tiled_bytes, lib.zt_q5k_tiled_header_bytes, lib.zt_q5k_tiled_qh_bytes)]
+    lib.call("zt_q5k_tile", a.data_ptr(), rows, K, *(b.data_ptr() for b in bufs), stream())
+    torch.cuda.synchronize()
+    return bufs
+
+
+def run_q5kt(lib, bufs, x, rows, K, N):
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    nb = lib.zt_gemm_q5kt_workspace_bytes(rows, K, N)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
+    lib.call("zt_gemm_q5kt_f32", *(b.data_ptr() for b in bufs), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             ws.data_ptr(), nb, stream())
+    return c.cpu().numpy().reshape(rows, N)
+
+
+@pytest.mark.parametrize("rows,K", [(16, 256), (17, 512), (1, 768)])
+def test_q5k_tile_layout_bytes(lib, rows, K):
+    """Data and headers as the Q4_K layout of the same nibbles (bytes 16..143
+    of each 176-byte super-block, its first 16 bytes); fifth bits: bit j of
+    byte 144 + l is value l of sub-block j, ordered per lane as for Q5_0."""
+    w = synth.kquant("q5_k", rows, K, 98)
+    nsb = K // 256
+    sbk = w.raw.reshape(rows, nsb, 176)
+    as_q4k = np.concatenate([sbk[:, :, :144]], axis=2).reshape(-1)
+    dref, href = q4k_tile_ref(as_q4k, rows, K)
+    bufs = q5k_tile_dev(lib, w.raw, rows, K)
+    assert np.array_equal(bufs[0].cpu().numpy(), dref)
+    assert np.array_equal(bufs[1].cpu().numpy(), href)
+    # fifth bits as a per-block qh word (bit e = value e), then the Q5_0 lane order
+    nt, nu = (rows + 15) // 16, K // 128
+    qhb = sbk[:, :, 144:].astype(np.uint32)  # [rows, nsb, 32]
+    words = np.zeros((nt * 16, nsb * 8), np.uint32)
+    for j in range(8):
+        for e in range(32):
+            words[:rows, np.arange(nsb) * 8 + j] |= ((qhb[:, :, e] >> np.uint32(j)) & np.uint32(1)) << np.uint32(e)
+    q = words.reshape(nt, 16, nu, 4)
+    out = np.zeros((nt, nu, 4, 16), np.uint32)
+    for g in range(4):
+        byte = np.zeros((nt, 16, nu, 4), np.uint32)
+        for k, e in enumerate(Q5_BITS):
+            byte |= ((q >> np.uint32(4 * g + e)) & np.uint32(1)) << np.uint32(k)
+        out[:, :, g, :] = (byte[..., 0] | (byte[..., 1] << np.uint32(8)) | (byte[..., 2] << np.uint32(16))
+                           | (byte[..., 3] << np.uint32(24))).transpose(0, 2, 1)
+    assert np.array_equal(bufs[2].cpu().numpy().view("<u4"), out.reshape(-1))
+
+
+@pytest.mark.parametrize("rows,K,N", [(16, 256, 4), (33, 2304, 12), (100, 4096, 8), (300, 1024, 16),
+                                      (4096, 4096, 8), (14336, 4096, 16), (4096, 14336, 8)])
+def test_q5kt_matches_oracle(lib, orc, rows, K, N):
+    print(f"q5kt rows={rows} K={K} N={N}", flush=True)
+    w = synth.kquant("q5_k", rows, K, 99)
+    x = synth.x_f32(K * N, 99).reshape(K, N)
+    bufs = q5k_tile_dev(lib, w.raw, rows, K)
+    xt = np.ascontiguousarray(x.T)
+    ref = orc.gemm_f32_kq_nt("q5_k", xt, w.raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
+    err = rel_err(run_q5kt(lib, bufs, x, rows, K, N), ref)
+    assert err <= 1e-5, err
+
+
+def test_engine_batched_q5k_uses_tiled_layout(lib, orc):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import Q5KStorage, Tensor
+
+    rows, K, n = 300, 1024, 8
+    w = synth.kquant("q5_k", rows, K, 100)
+    s = Q5KStorage(w.raw, rows * K)
+    x = synth.x_f32(K * n, 100).reshape(K, n)
+    y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = orc.gemm_f32_kq_nt("q5_k", np.ascontiguousarray(x.T), w.raw, n, rows, K).reshape(n, rows).T
+    assert rel_err(y, ref) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None

@@ -81,6 +81,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q5_0_tile": (I, [P, I, I, L, L, P, P, P, P]),
     "zt_gemm_q5_0t_workspace_bytes": (L, [I, I, I]),
     "zt_gemm_q5_0t_f32": (I, [P, P, P, P, P, I, I, I, P, L, P]),
+    "zt_q5k_tiled_bytes": (L, [I, I]),
+    "zt_q5k_tiled_header_bytes": (L, [I, I]),
+    "zt_q5k_tiled_qh_bytes": (L, [I, I]),
+    "zt_q5k_tile": (I, [P, I, I, P, P, P, P]),
+    "zt_gemm_q5kt_workspace_bytes": (L, [I, I, I]),
+    "zt_gemm_q5kt_f32": (I, [P, P, P, P, P, I, I, I, P, L, P]),
     "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),
     "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
     "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),

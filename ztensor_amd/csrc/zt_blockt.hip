@@ -45,7 +45,7 @@
 
 namespace zt {
 
-enum class BlkFmt { Q4_0, Q8_0, Q4_K, Q5_0 };
+enum class BlkFmt { Q4_0, Q8_0, Q4_K, Q5_0, Q5_K };
 
 // ST: the separated layout's scale type (float for Q8Storage, fp16 bits for
 // GGUF Q8_0, widened exactly); the tiled scales are fp32 either way.
@@ -80,8 +80,15 @@ __global__ void q8t_tile_kernel(const uint2* __restrict__ data, const ST* __rest
 // sub-block rewritten as the 16 bytes of a Q4_0 block: byte j holds values
 // j and j+16), and the 16-byte super-block headers (fp16 d, fp16 dmin, 12
 // bytes of 6-bit scales and mins) as [tile][super-block][16 rows][16 B].
+// Q5_K (176-byte super-blocks: header, 128 bytes of nibbles as Q4_K, then
+// 32 bytes of fifth bits, bit j of byte l for value l of sub-block j;
+// tensor/quantized_kquant.go:509-549) tiles the same way, plus the fifth-bit dwords of the
+// Q5_0 tiled layout in hq: bit k of byte s = the fifth bit of value
+// 4g + (0, 2, 16, 18, 1, 3, 17, 19)[k] of block 4u+s.
+template <bool Q5>
 __global__ void q4kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restrict__ wt, u32x4* __restrict__ ht,
-                                 int rows, int nunits, long npieces) {
+                                 uint32_t* __restrict__ hq, int rows, int nunits, long npieces) {
+    constexpr int BB = Q5 ? 176 : 144;  // super-block bytes
     const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= npieces) return;
     const int lane = (int)(p & 63), i = lane & 15, g = lane >> 4;
@@ -90,12 +97,18 @@ __global__ void q4kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restr
     const long rt = tu / nunits;
     const long row = rt * 16 + i;
     const int nsb = nunits / 2;
-    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    uint32_t v[4] = {0u, 0u, 0u, 0u}, fifth = 0u;
     if (row < rows) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const int b = 4 * u + s, sb = b >> 3, j = b & 7, gq = j >> 1;
-            const uint8_t* nib = raw + (row * nsb + sb) * 144 + 16 + 32 * gq;
+            if constexpr (Q5) {
+                const uint8_t* qh = raw + (row * nsb + sb) * BB + 144;
+                const int e[8] = {0, 2, 16, 18, 1, 3, 17, 19};
+#pragma unroll
+                for (int k = 0; k < 8; k++) fifth |= (uint32_t)((qh[4 * g + e[k]] >> j) & 1) << (8 * s + k);
+            }
+            const uint8_t* nib = raw + (row * nsb + sb) * BB + 16 + 32 * gq;
             const uint32_t a = *reinterpret_cast<const uint32_t*>(nib + 4 * g);
             const uint32_t c = *reinterpret_cast<const uint32_t*>(nib + 16 + 4 * g);
             v[s] = (j & 1) ? (((a >> 4) & 0x0F0F0F0Fu) | (c & 0xF0F0F0F0u))
@@ -103,9 +116,10 @@ __global__ void q4kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restr
         }
     }
     wt[p] = (u32x4){v[0], v[1], v[2], v[3]};
+    if constexpr (Q5) hq[p] = fifth;
     if ((u & 1) == 0 && g == 0) {  // header of (row, super-block u/2)
         u32x4 h = {0u, 0u, 0u, 0u};
-        if (row < rows) h = *reinterpret_cast<const u32x4*>(raw + (row * nsb + u / 2) * 144);
+        if (row < rows) h = *reinterpret_cast<const u32x4*>(raw + (row * nsb + u / 2) * BB);
         ht[(rt * nsb + u / 2) * 16 + i] = h;
     }
 }
@@ -178,7 +192,8 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     constexpr int XPB = mfma_chunk_xbytes(KC, 16);      // one plane: 16 fp16 columns, 2 pad rows per 32
     constexpr int PPR = N / 4;                          // 16-byte pieces per fp32 activation row
     constexpr int XP = (KC * PPR + W * 64 - 1) / (W * 64);
-    constexpr bool QK = F == BlkFmt::Q4_K;
+    constexpr bool QK = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K;  // super-block headers: (d*scale, dmin*min)
+    constexpr bool Q5 = F == BlkFmt::Q5_0 || F == BlkFmt::Q5_K;  // fifth-bit dwords in aux
     constexpr int SB = F == BlkFmt::Q8_0 ? 4 : 2;       // scale bytes (Q4_0, Q8_0)
     constexpr int PPT = 4 * SB;                         // 16-byte scale pieces per tile-unit
     // 16-byte scale pieces of the workgroup; Q4_K: one super-block header per row and super-block
@@ -237,8 +252,8 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             for (int h = 0; h < WL; h++) w[u][t][h] = ld_stream(wt + (((long)rt * nunits + unit) * WL + h) * 64 + lane);
         }
     }
-    uint32_t qhw[F == BlkFmt::Q5_0 ? UPW : 1][2];  // Q5_0: fifth bits of the lane's values, 4 blocks a dword
-    if constexpr (F == BlkFmt::Q5_0) {
+    uint32_t qhw[Q5 ? UPW : 1][2];  // Q5_0, Q5_K: fifth bits of the lane's values, 4 blocks a dword
+    if constexpr (Q5) {
 #pragma unroll
         for (int u = 0; u < UPW; u++) {
             const int unit = min(u0 + u, u1 - 1);
@@ -383,7 +398,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                         const uint32_t dw = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
                         const uint32_t d8 = dw >> 8;  // halves: q 2^-24 (low nibbles), q 2^-20 (high)
                         av = (u32x4){dw & 0x000F000Fu, dw & 0x00F000F0u, d8 & 0x000F000Fu, d8 & 0x00F000F0u};
-                        if constexpr (F == BlkFmt::Q5_0) {
+                        if constexpr (Q5) {
                             // fifth bits: 16 more in each half, bit 4 (low halves) or bit 8 (high);
                             // y = byte | byte << 15 puts byte bits k and k+1 16 bits apart
                             const uint32_t xb = (qhw[u][t] >> (8 * s)) & 0xFFu, yb = xb | (xb << 15);
@@ -455,7 +470,7 @@ template <BlkFmt F, int UPW, int N>
 static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const uint32_t* aux, const float* x,
                         float* y, float* ws, int M, int K) {
     constexpr int NPL = N <= 8 ? 1 : 2;
-    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : F == BlkFmt::Q4_K ? 8 : 2;  // LDS bytes per (row, block)
+    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K) ? 8 : 2;  // LDS bytes per (row, block)
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
     blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, aux, x, y, ws, M, K);
 }
@@ -485,7 +500,7 @@ static dim3 blkt_grid(int M, int K, int& upw) {
 
 template <BlkFmt F>
 static long blkt_ws_bytes(int M, int K, int N) {
-    constexpr int KQ = F == BlkFmt::Q4_K ? 256 : 128;
+    constexpr int KQ = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K ? 256 : 128;
     if (M < 0 || K < 0 || K % KQ != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
     if (M == 0 || K == 0) return 0;
     int upw;
@@ -495,14 +510,15 @@ static long blkt_ws_bytes(int M, int K, int N) {
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                      void* ws, long ws_bytes, hipStream_t stream, const void* aux = nullptr) {
-    constexpr int KQ = F == BlkFmt::Q4_K ? 256 : 128;  // Q4_K: whole super-blocks, an even unit count
+    constexpr int KQ = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K ? 256 : 128;  // K-quants: whole super-blocks
     if (M < 0 || K < 0 || K % KQ != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
     if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
         return (int)hipErrorInvalidValue;
-    if (F == BlkFmt::Q5_0 && (aux == nullptr || ((uintptr_t)aux & 15))) return (int)hipErrorInvalidValue;
+    if ((F == BlkFmt::Q5_0 || F == BlkFmt::Q5_K) && (aux == nullptr || ((uintptr_t)aux & 15)))
+        return (int)hipErrorInvalidValue;
     constexpr long SB = F == BlkFmt::Q8_0 ? 4 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     int upw;
@@ -614,9 +630,9 @@ ZT_EXPORT int zt_q4k_tile(const void* W_q4k, int M, int K, void* W_tiled, void* 
         return (int)hipErrorInvalidValue;
     const int nunits = K / 128;
     const long npieces = (long)((M + 15) / 16) * nunits * 64;
-    q4kt_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(W_q4k),
-                                                                static_cast<u32x4*>(W_tiled),
-                                                                static_cast<u32x4*>(H_tiled), M, nunits, npieces);
+    q4kt_tile_kernel<false><<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        static_cast<const uint8_t*>(W_q4k), static_cast<u32x4*>(W_tiled), static_cast<u32x4*>(H_tiled), nullptr, M,
+        nunits, npieces);
     return (int)hipGetLastError();
 }
 
@@ -660,4 +676,36 @@ ZT_EXPORT long zt_gemm_q5_0t_workspace_bytes(int M, int K, int N) { return blkt_
 ZT_EXPORT int zt_gemm_q5_0t_f32(const void* W_tiled, const void* S_tiled, const void* H_tiled, const float* B, float* C,
                                 int M, int K, int N, void* workspace, long workspace_bytes, hipStream_t stream) {
     return gemm_blkt<BlkFmt::Q5_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream, H_tiled);
+}
+
+ZT_EXPORT long zt_q5k_tiled_bytes(int M, int K) { return zt_q4k_tiled_bytes(M, K); }
+
+ZT_EXPORT long zt_q5k_tiled_header_bytes(int M, int K) { return zt_q4k_tiled_header_bytes(M, K); }
+
+ZT_EXPORT long zt_q5k_tiled_qh_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)((M + 15) / 16) * (K / 128) * 256;
+}
+
+ZT_EXPORT int zt_q5k_tile(const void* W_q5k, int M, int K, void* W_tiled, void* H_tiled, void* Q_tiled,
+                          hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_q5k == nullptr || W_tiled == nullptr || H_tiled == nullptr || Q_tiled == nullptr)
+        return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_q5k & 15) || ((uintptr_t)W_tiled & 15) || ((uintptr_t)H_tiled & 15) || ((uintptr_t)Q_tiled & 15))
+        return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 64;
+    q4kt_tile_kernel<true><<<ceil_div(npieces, 256), 256, 0, stream>>>(
+        static_cast<const uint8_t*>(W_q5k), static_cast<u32x4*>(W_tiled), static_cast<u32x4*>(H_tiled),
+        static_cast<uint32_t*>(Q_tiled), M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT long zt_gemm_q5kt_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q5_K>(M, K, N); }
+
+ZT_EXPORT int zt_gemm_q5kt_f32(const void* W_tiled, const void* H_tiled, const void* Q_tiled, const float* B, float* C,
+                               int M, int K, int N, void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q5_K>(W_tiled, H_tiled, B, C, M, K, N, workspace, workspace_bytes, stream, Q_tiled);
 }

@@ -280,7 +280,7 @@ class ROCmEngine:
             return x.dtype in (torch.float32, torch.float16)
         if isinstance(s, Q8Storage):
             return x.dtype == torch.float32
-        if isinstance(s, Q4KStorage):
+        if isinstance(s, (Q4KStorage, Q5KStorage)):
             return x.dtype == torch.float32 and k % 256 == 0
         if isinstance(s, Q5_0Storage):
             return x.dtype == torch.float32
@@ -291,21 +291,31 @@ class ROCmEngine:
                     rows * (k // s.group_size) < 1 << 29)
         return False
 
-    def _q4k_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """The tiled copy of uploaded Q4_K super-blocks (data in the Q4_0
-        tile format plus the super-block headers) for batches of 4-16 fp32
-        columns, built on the device on the first batched call."""
+    def _kq_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, q5: bool) -> tuple:
+        """The tiled copy of uploaded Q4_K / Q5_K super-blocks (data in the
+        Q4_0 tile format, the super-block headers and, for Q5_K, the fifth
+        bits) for batches of 4-16 fp32 columns, built on the device on the
+        first batched call."""
         cached = getattr(s, "_gpu_tiled", None)
         if cached is not None and cached[0] == (rows, k):
-            return cached[1], cached[2]
-        nbytes, hbytes = self.lib.zt_q4k_tiled_bytes(rows, k), self.lib.zt_q4k_tiled_header_bytes(rows, k)
-        if nbytes < 0 or hbytes < 0:
-            raise ValueError(f"Q4_K tiled layout: unsupported shape [{rows}, {k}]")
-        wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-        ht = torch.empty(hbytes, dtype=torch.uint8, device=self.device)
-        self.lib.call("zt_q4k_tile", _p(buf.tensor), rows, k, _p(wt), _p(ht), self._s)
-        s._gpu_tiled = ((rows, k), wt, ht)  # type: ignore[attr-defined]
-        return wt, ht
+            return cached[1:]
+        f = "q5k" if q5 else "q4k"
+        sizes = [getattr(self.lib, f"zt_{f}_tiled_bytes")(rows, k), getattr(self.lib, f"zt_{f}_tiled_header_bytes")(rows, k)]
+        if q5:
+            sizes.append(self.lib.zt_q5k_tiled_qh_bytes(rows, k))
+        if min(sizes) < 0:
+            raise ValueError(f"{f} tiled layout: unsupported shape [{rows}, {k}]")
+        bufs = tuple(torch.empty(n, dtype=torch.uint8, device=self.device) for n in sizes)
+        self.lib.call(f"zt_{f}_tile", _p(buf.tensor), rows, k, *(_p(b) for b in bufs), self._s)
+        s._gpu_tiled = ((rows, k),) + bufs  # type: ignore[attr-defined]
+        return bufs
+
+    def _kq_tiled_gemm(self, s: Any, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int, c: torch.Tensor,
+                       q5: bool) -> None:
+        bufs = self._kq_tiled(s, buf, rows, k, q5)
+        f = "q5k" if q5 else "q4k"
+        ws, wsb = self._workspace(getattr(self.lib, f"zt_gemm_{f}t_workspace_bytes")(rows, k, n))
+        self.lib.call(f"zt_gemm_{f}t_f32", *(_p(b) for b in bufs), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
 
     def _q5_0_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, qh: int, qs: int) -> tuple:
         """The tiled copy of uploaded Q5_0 weights (nibbles and scales in the
@@ -417,12 +427,10 @@ class ROCmEngine:
             if q50 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
                 self._q5_0_tiled_gemm(s, buf, rows, k, x, n, c, s.gpu_qh_offset(), s.gpu_qs_offset())
                 return c
-            if isinstance(s, Q4KStorage) and n in _TILED_BATCHES and k % 256 == 0:
-                # batched Q4_K on the tiled MFMA kernel
+            if isinstance(s, (Q4KStorage, Q5KStorage)) and n in _TILED_BATCHES and k % 256 == 0:
+                # batched Q4_K / Q5_K on the tiled MFMA kernel
                 xs = x if _p(x) % 16 == 0 else x.clone()
-                wt, ht = self._q4k_tiled(s, buf, rows, k)
-                ws, wsb = self._workspace(self.lib.zt_gemm_q4kt_workspace_bytes(rows, k, n))
-                self.lib.call("zt_gemm_q4kt_f32", _p(wt), _p(ht), _p(xs), _p(c), rows, k, n, ws, wsb, self._s)
+                self._kq_tiled_gemm(s, buf, rows, k, xs, n, c, isinstance(s, Q5KStorage))
                 return c
             if n == 1 and k % (32 if q50 else 256) == 0:
                 # fused dequant-GEMV (compute/gpu_engine.go:2224-2238, 2505-2510)
@@ -456,8 +464,8 @@ class ROCmEngine:
     def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
                     c: torch.Tensor) -> torch.Tensor:
         """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
-        the GGML type picks the kernel.  Q4_0, Q4_K, Q5_0 and Q8_0 batches of
-        4-16 run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
+        the GGML type picks the kernel.  Q4_0, Q4_K, Q5_K, Q5_0 and Q8_0
+        batches of 4-16 run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
         (the reference passes the 34-byte blocks to the 36-byte kernel,
         compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
         its CPU engine, runs on the Q5_0 GEMV; types without a quantized
@@ -471,10 +479,8 @@ class ROCmEngine:
             wt, st = self._block_tiled(s, buf, rows, k, "q4")
             ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
             self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
-        elif q == GGMLType.Q4_K and tiled and k % 256 == 0:
-            wt, ht = self._q4k_tiled(s, buf, rows, k)
-            ws, wsb = self._workspace(self.lib.zt_gemm_q4kt_workspace_bytes(rows, k, n))
-            self.lib.call("zt_gemm_q4kt_f32", _p(wt), _p(ht), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
+        elif q in (GGMLType.Q4_K, GGMLType.Q5_K) and tiled and k % 256 == 0:
+            self._kq_tiled_gemm(s, buf, rows, k, x, n, c, q == GGMLType.Q5_K)
         elif q == GGMLType.Q8_0 and tiled and k % 128 == 0:
             wt, st = self._block_tiled(s, buf, rows, k, "q8gguf")
             ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
@@ -543,7 +549,7 @@ class ROCmEngine:
         return w
 
 
-_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes that run on the tiled layouts (W4A16, IQ4_NL, Q4_0, Q8_0, Q4_K, Q5_0)
+_TILED_BATCHES = (4, 8, 12, 16)  # batch sizes on the tiled layouts (W4A16, IQ4_NL, Q4_0, Q8_0, Q4_K, Q5_K, Q5_0)
 
 
 def _detect_w4a16(a: Tensor, b: Tensor):
