@@ -226,3 +226,23 @@ def test_q4_q8_tiled_layout_and_workspace_sizes():
     assert q4(100, 128, 8) == 0 and q8(100, 128, 8) == 0
     assert q4(0, 4096, 8) == 0
     assert q4(16, 96, 8) == -1 and q8(16, 128, 6) == -1 and q4(16, 128, 1) == -1
+
+
+def test_kquant_and_q5_0_tiled_layout_sizes():
+    """Byte counts of the tiled Q4_K / Q5_K / Q5_0 layouts (host helpers, no
+    GPU): the Q4_0 tile data, 16 header bytes per row and super-block, one
+    fifth-bit dword per lane and tile-unit (256 bytes per 16 rows x 128 K)."""
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    for f in ("q4k", "q5k"):
+        assert getattr(lib, f"zt_{f}_tiled_bytes")(4096, 4096) == 4096 * 2048
+        assert getattr(lib, f"zt_{f}_tiled_header_bytes")(17, 512) == 32 * 2 * 16
+        assert getattr(lib, f"zt_{f}_tiled_bytes")(16, 128) == -1  # whole super-blocks only
+        assert getattr(lib, f"zt_gemm_{f}t_workspace_bytes")(16, 256, 8) == 0
+    assert lib.zt_q5k_tiled_qh_bytes(17, 512) == 2 * 4 * 256
+    assert lib.zt_q5_0_tiled_bytes(17, 256) == 32 * 128
+    assert lib.zt_q5_0_tiled_scale_bytes(17, 256) == 32 * 8 * 2
+    assert lib.zt_q5_0_tiled_qh_bytes(17, 256) == 2 * 2 * 256
+    assert lib.zt_q5_0_tiled_qh_bytes(17, 96) == -1
+    assert lib.zt_gemm_q5_0t_workspace_bytes(14336, 4096, 8) == 8 * 896 * 1024
