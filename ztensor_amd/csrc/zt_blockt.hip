@@ -1,5 +1,6 @@
-// Small-batch Q4_0 / Q8_0 GEMM on tiled upload layouts with MFMA, fp32
-// activations (N in {4, 8, 12, 16}, K % 128 == 0), for gfx950.
+// Small-batch GEMM on tiled upload layouts with MFMA, fp32 activations
+// (N in {4, 8, 12, 16}), for gfx950: Q4_0, Q8_0 (and GGUF Q8_0), Q5_0
+// (K % 128 == 0), and the K-quants Q4_K and Q5_K (K % 256 == 0).
 //
 // The reference computes these products with fp32 activations on its CPU
 // engine (xblas.GemmF32Q4NT / GemmF32Q8NT, internal/xblas/gemm_quant.go:81-264)
@@ -36,9 +37,18 @@
 //    layout, which has the same 18-byte block structure: data 1 KB at
 //    tu * 1024, lane l = 16 g + i holds dword g of blocks 4u .. 4u+3 of row
 //    16 rt + i; scales fp16 [16 rows][4 blocks] at tu * 128.
-//  * Q8_0 (zt_q8_tile): data 2 KB at tu * 2048; half h (1 KB) lane
-//    l = 16 g + i holds bytes 8g .. 8g+7 of block 4u + 2h, then of block
-//    4u + 2h + 1, of row 16 rt + i; scales fp32 [16 rows][4 blocks] at tu * 256.
+//  * Q8_0 (zt_q8_tile, zt_q8gguf_tile): data 2 KB at tu * 2048; half h
+//    (1 KB) lane l = 16 g + i holds bytes 8g .. 8g+7 of block 4u + 2h, then
+//    of block 4u + 2h + 1, of row 16 rt + i; scales fp32 [16 rows][4 blocks]
+//    at tu * 256.
+//  * Q5_0 (zt_q5_0_tile): the Q4_0 layout of its nibbles and scales, plus a
+//    dword of fifth bits per lane at tu * 256 + 4 l (aux).
+//  * Q4_K / Q5_K (zt_q4k_tile, zt_q5k_tile): each 32-value sub-block as a
+//    Q4_0 block in the Q4_0 data layout; the 16-byte super-block headers
+//    [tile][super-block][16 rows][16 B] (stl), decoded per workgroup into
+//    (d * scale, dmin * min) pairs; Q5_K adds Q5_0's fifth-bit dwords (aux).
+//    Each sub-block's min term uses an MFMA with all-positive A, which gives
+//    2^-24 sum(x) per step.
 #include <type_traits>
 
 #include "zt_mfma.h"
