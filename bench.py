@@ -337,6 +337,7 @@ SUITE = {
     "q4_kt": ("q4_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
     "q5_0t": ("q5_0t", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
     "q5_kt": ("q5_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
+    "q6_kt": ("q6_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
 }
 
 
@@ -415,12 +416,13 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         fn = lambda wb, y: lib.zt_gemm_q5_0t_f32(wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(), x.data_ptr(),
                                                  y.data_ptr(), rows, K, N, wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes("q5_0", rows, K, N)
-    elif fmt in ("q4_kt", "q5_kt"):
-        # batched Q4_K / Q5_K on the tiled layout (zt_q4k_tile / zt_q5k_tile), built once outside the timing
+    elif fmt in ("q4_kt", "q5_kt", "q6_kt"):
+        # batched K-quants on the tiled layouts (zt_q4k_tile / zt_q5k_tile / zt_q6k_tile), built once outside the timing
         f = fmt[:4].replace("_", "")
         w = synth.kquant(fmt[:4], rows, K, seed)
         raw = dev(w.raw)
-        parts = ["tiled_bytes", "tiled_header_bytes"] + (["tiled_qh_bytes"] if f == "q5k" else [])
+        parts = (["tiled_bytes", "tiled_scale_bytes"] if f == "q6k" else
+                 ["tiled_bytes", "tiled_header_bytes"] + (["tiled_qh_bytes"] if f == "q5k" else []))
         wbufs = [torch.empty(getattr(lib, f"zt_{f}_{p}")(rows, K), dtype=torch.uint8, device="cuda") for p in parts]
         lib.call(f"zt_{f}_tile", raw.data_ptr(), rows, K, *(t.data_ptr() for t in wbufs), s)
         torch.cuda.synchronize()

@@ -282,6 +282,21 @@ long zt_gemm_q5kt_workspace_bytes(int M, int K, int N);
 int zt_gemm_q5kt_f32(const void* W_tiled, const void* H_tiled, const void* Q_tiled, const float* B, float* C, int M,
                      int K, int N, void* workspace, long workspace_bytes, zt_stream_t stream);
 
+/* Batched Q6_K on the same MFMA kernel.  zt_q6k_tile reads Q6KStorage's
+ * 210-byte super-blocks (tensor/quantized_kquant.go:335-382: ql, qh, int8
+ * scales, fp16 d) and writes the 6-bit values as bytes in the Q8_0 tiled
+ * layout (zt_q6k_tiled_bytes) and the fp32 products d * sc of every
+ * 16-value group, [tile-unit][16 rows][8 groups] (zt_q6k_tiled_scale_bytes).
+ * zt_gemm_q6kt_f32: C[M, N] = W * B for N in {4, 8, 12, 16}, K % 256 == 0,
+ * workspace as zt_gemm_q4t_f32.  Replaces the reference's
+ * dequantize-then-SGEMM for batched Q6_K (compute/gpu_engine.go:2240-2255). */
+long zt_q6k_tiled_bytes(int M, int K);
+long zt_q6k_tiled_scale_bytes(int M, int K);
+int zt_q6k_tile(const void* W_q6k, int M, int K, void* W_tiled, void* S_tiled, zt_stream_t stream);
+long zt_gemm_q6kt_workspace_bytes(int M, int K, int N);
+int zt_gemm_q6kt_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                     void* workspace, long workspace_bytes, zt_stream_t stream);
+
 /* Batched Q5_0 on the same MFMA kernel.  zt_q5_0_tile takes Q5_0Storage's
  * RawBytesGPU (tensor/quantized_q5_0.go:118-165; offsets zt_q5_0_gpu_qh_offset
  * / zt_q5_0_gpu_qs_offset) and writes the nibbles and fp16 scales in the

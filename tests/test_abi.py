@@ -241,6 +241,10 @@ def test_kquant_and_q5_0_tiled_layout_sizes():
         assert getattr(lib, f"zt_{f}_tiled_bytes")(16, 128) == -1  # whole super-blocks only
         assert getattr(lib, f"zt_gemm_{f}t_workspace_bytes")(16, 256, 8) == 0
     assert lib.zt_q5k_tiled_qh_bytes(17, 512) == 2 * 4 * 256
+    assert lib.zt_q6k_tiled_bytes(17, 512) == 32 * 512
+    assert lib.zt_q6k_tiled_scale_bytes(17, 512) == 32 * 32 * 4
+    assert lib.zt_q6k_tiled_bytes(16, 128) == -1
+    assert lib.zt_gemm_q6kt_workspace_bytes(16, 256, 8) == 0
     assert lib.zt_q5_0_tiled_bytes(17, 256) == 32 * 128
     assert lib.zt_q5_0_tiled_scale_bytes(17, 256) == 32 * 8 * 2
     assert lib.zt_q5_0_tiled_qh_bytes(17, 256) == 2 * 2 * 256

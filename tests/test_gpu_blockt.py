@@ -627,3 +627,95 @@ def test_engine_batched_q5k_uses_tiled_layout(lib, orc):
     ref = orc.gemm_f32_kq_nt("q5_k", np.ascontiguousarray(x.T), w.raw, n, rows, K).reshape(n, rows).T
     assert rel_err(y, ref) <= TOL
     assert getattr(s, "_gpu_tiled", None) is not None
+
+
+# ---- batched Q6_K (zt_q6k_tile, zt_gemm_q6kt_f32)
+
+def q6k_values(raw, rows, K):
+    """The 6-bit values 0..63 of Q6_K super-blocks as [rows, K] and the int8
+    scales and fp16 d, per DequantizeQ6K (tensor/quantized_kquant.go:355-382):
+    value 128h + 32j + l takes ql[64h + 32(j&1) + l] (low nibble for j < 2,
+    high for j >= 2) and bits 2j..2j+1 of qh[32h + l]."""
+    sbk = raw.reshape(rows, K // 256, 210).astype(np.int32)
+    q = np.zeros((rows, K // 256, 256), np.int32)
+    for h in range(2):
+        for j in range(4):
+            l = np.arange(32)
+            lo = (sbk[:, :, 64 * h + 32 * (j & 1) + l] >> (4 * (j >> 1))) & 15
+            hi = (sbk[:, :, 128 + 32 * h + l] >> (2 * j)) & 3
+            q[:, :, 128 * h + 32 * j + l] = lo | (hi << 4)
+    sc = sbk[:, :, 192:208].astype(np.uint8).view(np.int8).astype(np.float32)
+    d = raw.reshape(rows, K // 256, 210)[:, :, 208:210].copy().view("<f2").astype(np.float32)
+    return q.reshape(rows, K), (d * sc).reshape(rows, K // 16)
+
+
+def q6k_tile_dev(lib, raw, rows, K):
+    a = dev(raw)
+    bufs = [torch.empty(f(rows, K), dtype=torch.uint8, device="cuda")
+            for f in (lib.zt_q6k_tiled_bytes, lib.zt_q6k_tiled_scale_bytes)]
+    lib.call("zt_q6k_tile", a.data_ptr(), rows, K, *(b.data_ptr() for b in bufs), stream())
+    torch.cuda.synchronize()
+    return bufs
+
+
+def run_q6kt(lib, bufs, x, rows, K, N):
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32).reshape(-1)).cuda()
+    c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    nb = lib.zt_gemm_q6kt_workspace_bytes(rows, K, N)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
+    lib.call("zt_gemm_q6kt_f32", *(b.data_ptr() for b in bufs), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             ws.data_ptr(), nb, stream())
+    return c.cpu().numpy().reshape(rows, N)
+
+
+@pytest.mark.parametrize("rows,K", [(16, 256), (17, 512), (1, 768)])
+def test_q6k_tile_layout_bytes(lib, rows, K):
+    """Values in the Q8_0 tile order (lane 16 g + i, half hh: bytes 8g..8g+7
+    of blocks 4u + 2hh and 4u + 2hh + 1 of row 16 rt + i) and d * sc per
+    16-value group as [tile-unit][16 rows][8 groups], zero past the last row."""
+    w = synth.kquant("q6_k", rows, K, 101)
+    q, s = q6k_values(w.raw, rows, K)
+    nt, nu = (rows + 15) // 16, K // 128
+    qp = np.zeros((nt * 16, K), np.uint8)
+    qp[:rows] = q
+    sp = np.zeros((nt * 16, K // 16), np.float32)
+    sp[:rows] = s
+    # [rt, i, u, hh, bb, g, k] -> [rt, u, hh, g, i, bb, k]
+    dref = qp.reshape(nt, 16, nu, 2, 2, 4, 8).transpose(0, 2, 3, 5, 1, 4, 6).reshape(-1)
+    sref = sp.reshape(nt, 16, nu, 8).transpose(0, 2, 1, 3).reshape(-1)
+    bufs = q6k_tile_dev(lib, w.raw, rows, K)
+    assert np.array_equal(bufs[0].cpu().numpy(), dref)
+    assert np.array_equal(bufs[1].cpu().numpy().view(np.float32), sref)
+
+
+@pytest.mark.parametrize("rows,K,N", [(16, 256, 4), (33, 2304, 12), (100, 4096, 8), (300, 1024, 16),
+                                      (4096, 4096, 8), (14336, 4096, 16), (4096, 14336, 8)])
+def test_q6kt_matches_oracle(lib, orc, rows, K, N):
+    print(f"q6kt rows={rows} K={K} N={N}", flush=True)
+    w = synth.kquant("q6_k", rows, K, 102)
+    x = synth.x_f32(K * N, 102).reshape(K, N)
+    bufs = q6k_tile_dev(lib, w.raw, rows, K)
+    xt = np.ascontiguousarray(x.T)
+    ref = orc.gemm_f32_kq_nt("q6_k", xt, w.raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
+    err = rel_err(run_q6kt(lib, bufs, x, rows, K, N), ref)
+    assert err <= 1e-5, err
+
+
+def test_q6kt_invalid_arguments(lib):
+    assert lib.zt_q6k_tiled_bytes(16, 128) == -1
+    assert lib.zt_q6k_tile(0, 16, 384, 0, 0, None) != 0
+    assert lib.zt_gemm_q6kt_f32(0, 0, 0, 0, 16, 256, 5, 0, 0, None) != 0  # N not in {4, 8, 12, 16}
+
+
+def test_engine_batched_q6k_uses_tiled_layout(lib, orc):
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import Q6KStorage, Tensor
+
+    rows, K, n = 300, 1024, 8
+    w = synth.kquant("q6_k", rows, K, 103)
+    s = Q6KStorage(w.raw, rows * K)
+    x = synth.x_f32(K * n, 103).reshape(K, n)
+    y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = orc.gemm_f32_kq_nt("q6_k", np.ascontiguousarray(x.T), w.raw, n, rows, K).reshape(n, rows).T
+    assert rel_err(y, ref) <= TOL
+    assert getattr(s, "_gpu_tiled", None) is not None

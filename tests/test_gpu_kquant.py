@@ -277,7 +277,7 @@ def test_engine_mmap_dispatch_by_ggml_type(orc, qtype):
     raw = {2: lambda: synth.q4_0(rows, K, 93).raw, 6: lambda: synth.kquant("q5_0", rows, K, 93).raw,
            8: lambda: synth.gguf_q8_0(rows, K, 93), 12: lambda: synth.kquant("q4_k", rows, K, 93).raw,
            13: lambda: synth.kquant("q5_k", rows, K, 93).raw, 14: lambda: synth.kquant("q6_k", rows, K, 93).raw}[qtype]()
-    for n in (1, 2, 8):  # 8: Q4_0, Q4_K, Q5_0 and Q8_0 on the tiled MFMA kernels
+    for n in (1, 2, 8):  # 8: every type here on the tiled MFMA kernels
         x = synth.x_f32(K * n, 93 + n)
         ref = orc.gemm_f32_mmap_nt(qtype, x.reshape(K, n).T.copy(), raw, n, rows, K)  # [n, rows]
         # B side (virtually transposed weight): act [n, K] @ W^T

@@ -87,6 +87,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q5k_tile": (I, [P, I, I, P, P, P, P]),
     "zt_gemm_q5kt_workspace_bytes": (L, [I, I, I]),
     "zt_gemm_q5kt_f32": (I, [P, P, P, P, P, I, I, I, P, L, P]),
+    "zt_q6k_tiled_bytes": (L, [I, I]),
+    "zt_q6k_tiled_scale_bytes": (L, [I, I]),
+    "zt_q6k_tile": (I, [P, I, I, P, P, P]),
+    "zt_gemm_q6kt_workspace_bytes": (L, [I, I, I]),
+    "zt_gemm_q6kt_f32": (I, [P, P, P, P, I, I, I, P, L, P]),
     "zt_ternary_gemv_f32": (I, [P, P, P, I, I, P]),
     "zt_ternary_gemv_i8": (I, [P, P, P, P, P, I, I, P]),
     "zt_dequant_ternary_f32": (I, [P, P, I, I, P]),

@@ -49,13 +49,18 @@
 //    (d * scale, dmin * min) pairs; Q5_K adds Q5_0's fifth-bit dwords (aux).
 //    Each sub-block's min term uses an MFMA with all-positive A, which gives
 //    2^-24 sum(x) per step.
+//  * Q6_K (zt_q6k_tile): the values 0..63 as bytes in the Q8_0 data layout;
+//    fp32 d * sc per 16-value group [16 rows][8 groups] at tu * 512.  A step
+//    (one 32-value block) spans two groups, lane groups 0-1 and 2-3, so its
+//    B operand is split into two masked copies and each group gets its own
+//    offset and weight MFMAs and its own scale.
 #include <type_traits>
 
 #include "zt_mfma.h"
 
 namespace zt {
 
-enum class BlkFmt { Q4_0, Q8_0, Q4_K, Q5_0, Q5_K };
+enum class BlkFmt { Q4_0, Q8_0, Q4_K, Q5_0, Q5_K, Q6_K };
 
 // ST: the separated layout's scale type (float for Q8Storage, fp16 bits for
 // GGUF Q8_0, widened exactly); the tiled scales are fp32 either way.
@@ -169,6 +174,53 @@ __global__ void q5t_tile_kernel(const uint16_t* __restrict__ scales, const uint3
     st[tu * 64 + i * 4 + g] = sc;
 }
 
+// Q6_K tiled layout: the 6-bit values q (0..63) as bytes in the Q8_0 tile
+// format (tensor/quantized_kquant.go:355-382: value 128h + 32j + l of a
+// super-block takes its low 4 bits from ql[64h + 32(j&1) + l] (low nibble
+// for j < 2, high for j >= 2) and its top 2 bits from qh[32h + l] >> 2j),
+// and the fp32 products d * scale of every 16-value group as
+// [tile-unit][16 rows][8 groups], the reference's first rounding.
+__global__ void q6kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restrict__ wt, float* __restrict__ st,
+                                 int rows, int nunits, long npieces) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npieces) return;
+    const int lane = (int)(p & 63), hh = (int)((p >> 6) & 1), i = lane & 15, g = lane >> 4;
+    const long tu = p >> 7;
+    const int u = (int)(tu % nunits);
+    const long row = (tu / nunits) * 16 + i;
+    const int nsb = nunits / 2;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    if (row < rows) {
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            const int b = 4 * u + 2 * hh + bb;  // 32-value block of the row
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int val = 32 * b + 8 * g + k, sb = val >> 8, vs = val & 255;
+                const int h = vs >> 7, j = (vs >> 5) & 3, l = vs & 31;
+                const uint8_t* blk = raw + ((long)row * nsb + sb) * 210;
+                const int lo = (blk[64 * h + 32 * (j & 1) + l] >> (4 * (j >> 1))) & 15;
+                const int hi = (blk[128 + 32 * h + l] >> (2 * j)) & 3;
+                v[2 * bb + (k >> 2)] |= (uint32_t)(lo | (hi << 4)) << (8 * (k & 3));
+            }
+        }
+    }
+    wt[p] = (u32x4){v[0], v[1], v[2], v[3]};
+    if (hh == 0 && g == 0) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            float sv = 0.0f;
+            if (row < rows) {
+                const int grp = 8 * u + q, sb = grp >> 4;  // 16 groups per super-block
+                const uint8_t* blk = raw + ((long)row * nsb + sb) * 210;
+                const float d = h2f((uint16_t)(blk[208] | (blk[209] << 8)));
+                sv = d * (float)(int8_t)blk[192 + (grp & 15)];
+            }
+            st[(tu * 16 + i) * 8 + q] = sv;
+        }
+    }
+}
+
 // LDS row of chunk-relative activation row r (K index within the
 // workgroup's range).  Within each 128-K unit, the 8 activations that lane
 // group g of MFMA step s multiplies sit in rows 32 g + 8 s .. +7, in the
@@ -178,7 +230,7 @@ template <BlkFmt F>
 __device__ __forceinline__ int blkt_lds_row(int r) {
     const int u = r >> 7, b = (r >> 5) & 3, e = r & 31;
     int g, j;
-    if constexpr (F != BlkFmt::Q8_0) {
+    if constexpr (F != BlkFmt::Q8_0 && F != BlkFmt::Q6_K) {
         // A halves of lane group g: elements 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3, 4g+17, 4g+19
         const int i4 = e & 3;
         g = (e & 15) >> 2;
@@ -204,12 +256,13 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     constexpr int XP = (KC * PPR + W * 64 - 1) / (W * 64);
     constexpr bool QK = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K;  // super-block headers: (d*scale, dmin*min)
     constexpr bool Q5 = F == BlkFmt::Q5_0 || F == BlkFmt::Q5_K;  // fifth-bit dwords in aux
-    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : 2;       // scale bytes (Q4_0, Q8_0)
+    constexpr bool Q6 = F == BlkFmt::Q6_K;  // byte values, one scale per 16: two half-steps
+    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : F == BlkFmt::Q6_K ? 8 : 2;  // scale bytes per (row, block)
     constexpr int PPT = 4 * SB;                         // 16-byte scale pieces per tile-unit
     // 16-byte scale pieces of the workgroup; Q4_K: one super-block header per row and super-block
     constexpr int SPC = QK ? (RW / 16) * (UPW / 2) * 16 : (RW / 16) * UPW * PPT;
     constexpr int SP = (SPC + W * 64 - 1) / (W * 64);
-    constexpr int WL = F == BlkFmt::Q8_0 ? 2 : 1;       // 16-byte weight loads per lane per tile-unit
+    constexpr int WL = (F == BlkFmt::Q8_0 || F == BlkFmt::Q6_K) ? 2 : 1;  // 16-byte weight loads per lane per tile-unit
     extern __shared__ __attribute__((aligned(16))) char smem[];
     float* wmax = reinterpret_cast<float*>(smem + NPL * XPB);  // per-wave max |x|
     char* ssm = smem + NPL * XPB + 16;                            // block scales
@@ -299,7 +352,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             const int r = p / PPR, c4 = (p % PPR) * 4;
             // Q4_0: the activations of high-nibble elements (16..31 of a block)
             // are staged at 1/16, as their A halves are q * 2^-20
-            const float cr = (F != BlkFmt::Q8_0 && (r & 16)) ? cs * 0.0625f : cs;
+            const float cr = (F != BlkFmt::Q8_0 && F != BlkFmt::Q6_K && (r & 16)) ? cs * 0.0625f : cs;
             const int base = mfma_xrow(blkt_lds_row<F>(r), 16);
             uint32_t hv[2], lv[2];
 #pragma unroll
@@ -367,11 +420,13 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     // Q4_K: +2^-24 (+2^-20 in high-nibble halves), so the MFMA gives
     // 2^-24 * sum(x) of each sub-block, for its min term.
     // (Q5_0: offset 16, -16 * 2^-24 and -16 * 2^-20)
+    // (Q6_K: -32 * 2^-24 in every half)
     const _Float16 ol = __builtin_bit_cast(
-        _Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : F == BlkFmt::Q5_0 ? 0x8010u : 0x8080u));
+        _Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : F == BlkFmt::Q5_0 ? 0x8010u
+                             : Q6 ? 0x8020u : 0x8080u));
     const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)(QK ? 0x0010u : F == BlkFmt::Q5_0 ? 0x8100u : 0x8080u));
-    const half8v aoff = F != BlkFmt::Q8_0 ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
-                                          : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
+    const half8v aoff = (F != BlkFmt::Q8_0 && !Q6) ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
+                                                    : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
     float4v acc[2];
     acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -380,7 +435,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             // the 4 block scales of rows 4 lg + i of each tile for this unit
             // (Q4_K: the (scale, min) pairs of the 4 blocks, two float4 a row)
             using SV = typename std::conditional<F == BlkFmt::Q4_0 || F == BlkFmt::Q5_0, uint2, float4>::type;
-            constexpr int SVR = QK ? 2 : 1;
+            constexpr int SVR = (QK || Q6) ? 2 : 1;
             SV sc[2][4][SVR];
 #pragma unroll
             for (int t = 0; t < 2; t++)
@@ -397,6 +452,47 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                     const int o = pl * XPB + (136 * u + 8 * s) * 32;
                     const short4v ba = tr_read_b64(smem, lbase + o), bb = tr_read_b64(smem, lbase + o + 128);
                     bv[pl] = __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
+                }
+                if constexpr (Q6) {
+                    // the step's two 16-value groups are lane groups 0-1 and 2-3:
+                    // B restricted to each, so every MFMA sums one group
+                    half8v bq[2][NPL];
+                    const half8v hz = (half8v){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                    for (int pl = 0; pl < NPL; pl++) {
+                        bq[0][pl] = lg < 2 ? bv[pl] : hz;
+                        bq[1][pl] = lg < 2 ? hz : bv[pl];
+                    }
+                    float4v dq[2];
+#pragma unroll
+                    for (int hq = 0; hq < 2; hq++) {
+                        dq[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bq[hq][0], (float4v){0.f, 0.f, 0.f, 0.f}, 0,
+                                                                         0, 0);
+                        if constexpr (NPL == 2) dq[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bq[hq][1], dq[hq], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const uint4 q = w[u][t][s >> 1];
+                        const uint32_t da = (s & 1) ? q.z : q.x, db = (s & 1) ? q.w : q.y;
+                        const u32x4 av = {__builtin_amdgcn_perm(da, da, 0x0C010C00u), __builtin_amdgcn_perm(da, da, 0x0C030C02u),
+                                          __builtin_amdgcn_perm(db, db, 0x0C010C00u), __builtin_amdgcn_perm(db, db, 0x0C030C02u)};
+                        float4v d[2];
+#pragma unroll
+                        for (int hq = 0; hq < 2; hq++) {
+                            d[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bq[hq][0], dq[hq],
+                                                                            0, 0, 0);
+                            if constexpr (NPL == 2)
+                                d[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bq[hq][1],
+                                                                                d[hq], 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const SV& pr = sc[t][i][s >> 1];  // groups 2s, 2s+1
+                            const float s0 = (s & 1) ? pr.z : pr.x, s1 = (s & 1) ? pr.w : pr.y;
+                            acc[t][i] = fmaf(s0, d[0][i], fmaf(s1, d[1][i], acc[t][i]));
+                        }
+                    }
+                    continue;
                 }
                 float4v dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bv[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 if constexpr (NPL == 2) dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bv[1], dn, 0, 0, 0);
@@ -480,7 +576,7 @@ template <BlkFmt F, int UPW, int N>
 static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc, const uint32_t* aux, const float* x,
                         float* y, float* ws, int M, int K) {
     constexpr int NPL = N <= 8 ? 1 : 2;
-    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K) ? 8 : 2;  // LDS bytes per (row, block)
+    constexpr int SB = F == BlkFmt::Q8_0 ? 4 : (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K || F == BlkFmt::Q6_K) ? 8 : 2;  // LDS bytes per (row, block)
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
     blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, aux, x, y, ws, M, K);
 }
@@ -502,7 +598,7 @@ static void launch_blkt_n(int upw, dim3 g, hipStream_t st, const uint4* wt, cons
 template <BlkFmt F>
 static dim3 blkt_grid(int M, int K, int& upw) {
     const int nunits = K / 128, gx = ceil_div(M, 128);
-    const long minwg = F == BlkFmt::Q8_0 ? 512 : 256;
+    const long minwg = (F == BlkFmt::Q8_0 || F == BlkFmt::Q6_K) ? 512 : 256;
     upw = 4;
     while (upw > 2 && (long)gx * ceil_div(nunits, upw) < minwg) upw >>= 1;
     return dim3(gx, ceil_div(nunits, upw));
@@ -510,7 +606,7 @@ static dim3 blkt_grid(int M, int K, int& upw) {
 
 template <BlkFmt F>
 static long blkt_ws_bytes(int M, int K, int N) {
-    constexpr int KQ = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K ? 256 : 128;
+    constexpr int KQ = (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K || F == BlkFmt::Q6_K) ? 256 : 128;
     if (M < 0 || K < 0 || K % KQ != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
     if (M == 0 || K == 0) return 0;
     int upw;
@@ -520,7 +616,7 @@ static long blkt_ws_bytes(int M, int K, int N) {
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                      void* ws, long ws_bytes, hipStream_t stream, const void* aux = nullptr) {
-    constexpr int KQ = F == BlkFmt::Q4_K || F == BlkFmt::Q5_K ? 256 : 128;  // K-quants: whole super-blocks
+    constexpr int KQ = (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K || F == BlkFmt::Q6_K) ? 256 : 128;  // K-quants: whole super-blocks
     if (M < 0 || K < 0 || K % KQ != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
@@ -529,7 +625,7 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
         return (int)hipErrorInvalidValue;
     if ((F == BlkFmt::Q5_0 || F == BlkFmt::Q5_K) && (aux == nullptr || ((uintptr_t)aux & 15)))
         return (int)hipErrorInvalidValue;
-    constexpr long SB = F == BlkFmt::Q8_0 ? 4 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
+    constexpr long SB = F == BlkFmt::Q8_0 ? 4 : F == BlkFmt::Q6_K ? 8 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     int upw;
     const dim3 g = blkt_grid<F>(M, K, upw);
@@ -718,4 +814,34 @@ ZT_EXPORT long zt_gemm_q5kt_workspace_bytes(int M, int K, int N) { return blkt_w
 ZT_EXPORT int zt_gemm_q5kt_f32(const void* W_tiled, const void* H_tiled, const void* Q_tiled, const float* B, float* C,
                                int M, int K, int N, void* workspace, long workspace_bytes, hipStream_t stream) {
     return gemm_blkt<BlkFmt::Q5_K>(W_tiled, H_tiled, B, C, M, K, N, workspace, workspace_bytes, stream, Q_tiled);
+}
+
+ZT_EXPORT long zt_q6k_tiled_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * K;
+}
+
+ZT_EXPORT long zt_q6k_tiled_scale_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)((M + 15) / 16) * 16 * (K / 16) * 4;
+}
+
+ZT_EXPORT int zt_q6k_tile(const void* W_q6k, int M, int K, void* W_tiled, void* S_tiled, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_q6k == nullptr || W_tiled == nullptr || S_tiled == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_q6k & 1) || ((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15)) return (int)hipErrorInvalidValue;
+    const int nunits = K / 128;
+    const long npieces = (long)((M + 15) / 16) * nunits * 128;
+    q6kt_tile_kernel<<<ceil_div(npieces, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(W_q6k),
+                                                                static_cast<u32x4*>(W_tiled), static_cast<float*>(S_tiled),
+                                                                M, nunits, npieces);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT long zt_gemm_q6kt_workspace_bytes(int M, int K, int N) { return blkt_ws_bytes<BlkFmt::Q6_K>(M, K, N); }
+
+ZT_EXPORT int zt_gemm_q6kt_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                               void* workspace, long workspace_bytes, hipStream_t stream) {
+    return gemm_blkt<BlkFmt::Q6_K>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
 }

@@ -45,6 +45,7 @@ from .storage import (
 )
 
 _KQ_GEMV = {Q4KStorage: "zt_gemv_q4k_f32", Q5KStorage: "zt_gemv_q5k_f32", Q6KStorage: "zt_gemv_q6k_f32"}
+_KQ_TILED = {Q4KStorage: "q4k", Q5KStorage: "q5k", Q6KStorage: "q6k"}
 _KQ_DEQUANT = {Q4KStorage: "zt_dequant_q4k_f32", Q5KStorage: "zt_dequant_q5k_f32", Q6KStorage: "zt_dequant_q6k_f32"}
 
 
@@ -280,7 +281,7 @@ class ROCmEngine:
             return x.dtype in (torch.float32, torch.float16)
         if isinstance(s, Q8Storage):
             return x.dtype == torch.float32
-        if isinstance(s, (Q4KStorage, Q5KStorage)):
+        if isinstance(s, (Q4KStorage, Q5KStorage, Q6KStorage)):
             return x.dtype == torch.float32 and k % 256 == 0
         if isinstance(s, Q5_0Storage):
             return x.dtype == torch.float32
@@ -291,17 +292,18 @@ class ROCmEngine:
                     rows * (k // s.group_size) < 1 << 29)
         return False
 
-    def _kq_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, q5: bool) -> tuple:
-        """The tiled copy of uploaded Q4_K / Q5_K super-blocks (data in the
-        Q4_0 tile format, the super-block headers and, for Q5_K, the fifth
-        bits) for batches of 4-16 fp32 columns, built on the device on the
-        first batched call."""
+    def _kq_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, f: str) -> tuple:
+        """The tiled copy of uploaded K-quant super-blocks for batches of
+        4-16 fp32 columns, built on the device on the first batched call.
+        f = "q4k" / "q5k": data in the Q4_0 tile format, the super-block
+        headers and, for Q5_K, the fifth bits; f = "q6k": the 6-bit values in
+        the Q8_0 tile format and the per-16 scales d * sc."""
         cached = getattr(s, "_gpu_tiled", None)
         if cached is not None and cached[0] == (rows, k):
             return cached[1:]
-        f = "q5k" if q5 else "q4k"
-        sizes = [getattr(self.lib, f"zt_{f}_tiled_bytes")(rows, k), getattr(self.lib, f"zt_{f}_tiled_header_bytes")(rows, k)]
-        if q5:
+        second = "tiled_scale_bytes" if f == "q6k" else "tiled_header_bytes"
+        sizes = [getattr(self.lib, f"zt_{f}_tiled_bytes")(rows, k), getattr(self.lib, f"zt_{f}_{second}")(rows, k)]
+        if f == "q5k":
             sizes.append(self.lib.zt_q5k_tiled_qh_bytes(rows, k))
         if min(sizes) < 0:
             raise ValueError(f"{f} tiled layout: unsupported shape [{rows}, {k}]")
@@ -311,9 +313,8 @@ class ROCmEngine:
         return bufs
 
     def _kq_tiled_gemm(self, s: Any, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int, c: torch.Tensor,
-                       q5: bool) -> None:
-        bufs = self._kq_tiled(s, buf, rows, k, q5)
-        f = "q5k" if q5 else "q4k"
+                       f: str) -> None:
+        bufs = self._kq_tiled(s, buf, rows, k, f)
         ws, wsb = self._workspace(getattr(self.lib, f"zt_gemm_{f}t_workspace_bytes")(rows, k, n))
         self.lib.call(f"zt_gemm_{f}t_f32", *(_p(b) for b in bufs), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
 
@@ -427,10 +428,10 @@ class ROCmEngine:
             if q50 and n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
                 self._q5_0_tiled_gemm(s, buf, rows, k, x, n, c, s.gpu_qh_offset(), s.gpu_qs_offset())
                 return c
-            if isinstance(s, (Q4KStorage, Q5KStorage)) and n in _TILED_BATCHES and k % 256 == 0:
-                # batched Q4_K / Q5_K on the tiled MFMA kernel
+            if not q50 and n in _TILED_BATCHES and k % 256 == 0:
+                # batched K-quants on the tiled MFMA kernel
                 xs = x if _p(x) % 16 == 0 else x.clone()
-                self._kq_tiled_gemm(s, buf, rows, k, xs, n, c, isinstance(s, Q5KStorage))
+                self._kq_tiled_gemm(s, buf, rows, k, xs, n, c, _KQ_TILED[type(s)])
                 return c
             if n == 1 and k % (32 if q50 else 256) == 0:
                 # fused dequant-GEMV (compute/gpu_engine.go:2224-2238, 2505-2510)
@@ -464,7 +465,7 @@ class ROCmEngine:
     def _mmap_times(self, s: MmapStorage, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int,
                     c: torch.Tensor) -> torch.Tensor:
         """GPUEngine.matMulMmap / matMulMmapB (compute/gpu_engine.go:2813-3070):
-        the GGML type picks the kernel.  Q4_0, Q4_K, Q5_K, Q5_0 and Q8_0
+        the GGML type picks the kernel.  Q4_0, Q4_K, Q5_K, Q6_K, Q5_0 and Q8_0
         batches of 4-16 run on the tiled MFMA kernels, as for the storage types.  Q8_0 runs on its own repacked layout
         (the reference passes the 34-byte blocks to the 36-byte kernel,
         compute/gpu_engine.go:2865-2870); Q5_0, which the reference leaves to
@@ -479,8 +480,8 @@ class ROCmEngine:
             wt, st = self._block_tiled(s, buf, rows, k, "q4")
             ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
             self.lib.call("zt_gemm_q4t_f32", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
-        elif q in (GGMLType.Q4_K, GGMLType.Q5_K) and tiled and k % 256 == 0:
-            self._kq_tiled_gemm(s, buf, rows, k, x, n, c, q == GGMLType.Q5_K)
+        elif q in (GGMLType.Q4_K, GGMLType.Q5_K, GGMLType.Q6_K) and tiled and k % 256 == 0:
+            self._kq_tiled_gemm(s, buf, rows, k, x, n, c, {GGMLType.Q4_K: "q4k", GGMLType.Q5_K: "q5k"}.get(q, "q6k"))
         elif q == GGMLType.Q8_0 and tiled and k % 128 == 0:
             wt, st = self._block_tiled(s, buf, rows, k, "q8gguf")
             ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
