@@ -69,6 +69,33 @@ int zt_gemm_q4_f16(const void* A_q4, const uint16_t* B, float* C, int M, int K, 
  * (tensor/quantized.go:96-114) over the RawBytesGPU layout. */
 int zt_dequant_q4_f32(const void* A_q4, float* out, long nelem, int data_offset, zt_stream_t stream);
 
+/* Grouped Q4_0 GEMV: up to ZT_GROUP_MAX matrices that read the same fp32
+ * activation vector x[K] (a decode layer's q/k/v, or gate/up), batch 1, in
+ * one launch.  Each descriptor names one matrix in its own RawBytesGPU
+ * upload (A, data_offset as for zt_gemm_q4_f32), its row count and its
+ * output y[rows]; the storages are neither merged nor re-laid out.  Matrix
+ * i gets the result of zt_gemm_q4_f32(A_i, x, y_i, rows_i, K, 1, ...) up to
+ * the fp32 summation order (bit for bit when both launches use the same
+ * rows per wave, which the group picks from its total row count).
+ * `descs` is a host array read during the call (the
+ * descriptors travel in the kernel arguments, so nothing is allocated or
+ * copied to the device).  A descriptor with rows == 0 is skipped (its
+ * pointers are not read).  n outside 1..ZT_GROUP_MAX, any bad descriptor,
+ * K % 32 != 0 or a misaligned x -> InvalidValue.
+ * The reference's answer to the same launch cost is merging the storages
+ * (MergeQ4Storage, tensor/quantized.go:224-242), which this entry point
+ * makes unnecessary; its CPU engine runs one GemmF32Q4NT per matrix
+ * (internal/xblas/gemm_quant.go:81-157). */
+#define ZT_GROUP_MAX 8
+typedef struct zt_q4_gemv_desc {
+    const void* A;    /* RawBytesGPU buffer */
+    long data_offset; /* Q4GPUDataOffset(rows*K/32) */
+    float* y;         /* rows fp32 outputs */
+    int rows;
+    int reserved;     /* 0 */
+} zt_q4_gemv_desc;
+int zt_gemm_q4_group_f32(const zt_q4_gemv_desc* descs, int n, const float* x, int K, zt_stream_t stream);
+
 /* Host: RawBytes (18-byte blocks, tensor/quantized.go:146-156) ->
  * RawBytesGPU (tensor/quantized.go:158-187).  out holds
  * zt_q4_gpu_bytes(nblk) bytes. */

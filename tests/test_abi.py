@@ -250,3 +250,29 @@ def test_kquant_and_q5_0_tiled_layout_sizes():
     assert lib.zt_q5_0_tiled_qh_bytes(17, 256) == 2 * 2 * 256
     assert lib.zt_q5_0_tiled_qh_bytes(17, 96) == -1
     assert lib.zt_gemm_q5_0t_workspace_bytes(14336, 4096, 8) == 8 * 896 * 1024
+
+
+def test_q4_group_rejects_bad_arguments_without_launching():
+    """zt_gemm_q4_group_f32 validates every descriptor before any launch:
+    each case returns InvalidValue (1) with no GPU present."""
+    lib = _lib.load()
+    good = (0x10000, 16, 0x20000, 8)
+    x = 0x30000
+    cases = [
+        ([good], 0, x, 64),                      # n < 1
+        ([good] * 9, 9, x, 64),                  # n > ZT_GROUP_MAX
+        ([good], 1, x, 48),                      # K % 32 != 0
+        ([good], 1, x + 4, 64),                  # misaligned activations
+        ([good], 1, 0, 64),                      # null activations
+        ([(0, 16, 0x20000, 8)], 1, x, 64),       # null weights
+        ([(0x10000, 16, 0, 8)], 1, x, 64),       # null output
+        ([(0x10000, 8, 0x20000, 8)], 1, x, 64),  # data not 16-byte aligned
+        ([(0x10000, 16, 0x20000, -1)], 1, x, 64),  # negative rows
+    ]
+    for entries, n, xp, K in cases:
+        descs = _lib.q4_gemv_descs(entries)
+        assert lib.zt_gemm_q4_group_f32(descs, n, xp, K, None) == _lib.HIP_ERROR_INVALID_VALUE, (entries, n, K)
+    assert lib.zt_gemm_q4_group_f32(None, 1, x, 64, None) == _lib.HIP_ERROR_INVALID_VALUE
+    d = _lib.q4_gemv_descs([good])
+    d[0].reserved = 1
+    assert lib.zt_gemm_q4_group_f32(d, 1, x, 64, None) == _lib.HIP_ERROR_INVALID_VALUE

@@ -204,3 +204,30 @@ def test_merged_qkv_storage_equals_separate_gemvs(eng, orc):
     assert rel_err(merged, sep) <= 1e-6  # same kernel, row reduction order may differ with the row-tile size
     ref = np.concatenate([orc.gemm_f32_q4_nt(x.cpu().numpy(), p.raw, 1, p.rows, K) for p in parts])
     assert rel_err(merged, ref) <= TOL
+
+
+def test_gemv_group_equals_separate_gemvs(eng, orc):
+    """ROCmEngine.gemv_group: Q/K/V (and 9 matrices, past one launch's
+    ZT_GROUP_MAX) in grouped launches equal the per-matrix GEMVs, and a
+    non-Q4_0 member falls back to its own GEMV."""
+    K = 4096
+    parts = [synth.q4_0(rows, K, 70 + i) for i, rows in enumerate((4096, 1024, 1024))]
+    ws = [Tensor((p.rows, K), Q4Storage.from_raw(p.raw, p.rows * K)) for p in parts]
+    x = torch.from_numpy(synth.x_f32(K, 70)).cuda()
+    outs = eng.gemv_group(ws, x)
+    for p, y in zip(parts, outs):
+        ref = orc.gemm_f32_q4_nt(x.cpu().numpy(), p.raw, 1, p.rows, K)
+        assert rel_err(y.cpu().numpy(), ref) <= 1e-5
+    many = [synth.q4_0(64 + 8 * i, 256, 80 + i) for i in range(9)]
+    mw = [Tensor((p.rows, 256), Q4Storage.from_raw(p.raw, p.rows * 256)) for p in many]
+    xs = torch.from_numpy(synth.x_f32(256, 80)).cuda()
+    for p, y in zip(many, eng.gemv_group(mw, xs)):
+        assert rel_err(y.cpu().numpy(), orc.gemm_f32_q4_nt(xs.cpu().numpy(), p.raw, 1, p.rows, 256)) <= 1e-5
+    q8 = synth.q8_0(128, 256, 90)
+    qb = q8.raw.reshape(-1, 36)
+    q8s = Q8Storage.from_blocks(qb[:, :4].copy().view("<f4").reshape(-1), qb[:, 4:].copy().view(np.int8), 128 * 256)
+    mixed = [mw[0], Tensor((128, 256), q8s)]
+    y0, y1 = eng.gemv_group(mixed, xs)
+    assert rel_err(y1.cpu().numpy(), orc.gemm_f32_q8_nt(xs.cpu().numpy(), q8.raw, 1, 128, 256)) <= 1e-5
+    with pytest.raises(ValueError):
+        eng.gemv_group(ws, xs)  # K mismatch

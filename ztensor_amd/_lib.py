@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_abi_version": (I, []),
     "zt_gemm_q4_f32": (I, [P, P, P, I, I, I, I, P]),
     "zt_gemm_q4_f16": (I, [P, P, P, I, I, I, I, P]),
+    "zt_gemm_q4_group_f32": (I, [P, I, P, I, P]),
     "zt_dequant_q4_f32": (I, [P, P, L, I, P]),
     "zt_q4_gpu_data_offset": (L, [L]),
     "zt_q4_gpu_bytes": (L, [L]),
@@ -111,6 +112,22 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 }
 
 HIP_ERROR_INVALID_VALUE = 1
+GROUP_MAX = 8  # ZT_GROUP_MAX
+
+
+class Q4GemvDesc(C.Structure):
+    """zt_q4_gemv_desc: one matrix of a grouped Q4_0 GEMV."""
+
+    _fields_ = [("A", C.c_void_p), ("data_offset", C.c_long), ("y", C.c_void_p), ("rows", C.c_int),
+                ("reserved", C.c_int)]
+
+
+def q4_gemv_descs(entries) -> C.Array:
+    """A host array of zt_q4_gemv_desc from (A, data_offset, y, rows) tuples."""
+    arr = (Q4GemvDesc * max(1, len(entries)))()
+    for i, (a, off, y, rows) in enumerate(entries):
+        arr[i].A, arr[i].data_offset, arr[i].y, arr[i].rows, arr[i].reserved = a, off, y, rows, 0
+    return arr
 
 
 class ZTError(RuntimeError):

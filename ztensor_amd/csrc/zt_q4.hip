@@ -211,14 +211,11 @@ __global__ void __launch_bounds__(512) gemv_quad_kernel(const uint16_t* __restri
 //    v_fma_mix chain started at -8*sum(x), and the fp16 block scale enters
 //    v_fma_mix directly.
 template <int S, int R>
-__global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __restrict__ scales,
-                                                             const uint32_t* __restrict__ data,
-                                                             const float* __restrict__ x, float* __restrict__ y,
-                                                             int rows, int kb) {
-    __shared__ float red[16 * R];
+__device__ __forceinline__ void q4_steps_body(const uint16_t* __restrict__ scales, const uint32_t* __restrict__ data,
+                                              const float* __restrict__ x, float* __restrict__ y, int rows, int kb,
+                                              int row0, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 3;
-    const int row0 = blockIdx.x * R;
     const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
@@ -277,6 +274,40 @@ __global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __r
         }
     }
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __restrict__ scales,
+                                                             const uint32_t* __restrict__ data,
+                                                             const float* __restrict__ x, float* __restrict__ y,
+                                                             int rows, int kb) {
+    __shared__ float red[16 * R];
+    q4_steps_body<S, R>(scales, data, x, y, rows, kb, blockIdx.x * R, red);
+}
+
+// Several Q4_0 matrices that read the same activation vector (q/k/v, or
+// gate/up, of a decode layer) in one launch.  Workgroups [wg0[i], wg0[i+1])
+// run matrix i with the fixed-step body above; the matrices keep their own
+// separated uploads, so nothing is merged or re-laid out.  The descriptors
+// travel in the kernel arguments.
+struct Q4GroupArgs {
+    const uint16_t* sc[ZT_GROUP_MAX];
+    const uint32_t* dt[ZT_GROUP_MAX];
+    float* y[ZT_GROUP_MAX];
+    int rows[ZT_GROUP_MAX];
+    int wg0[ZT_GROUP_MAX];
+    int n;
+};
+
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_q4_group_kernel(const Q4GroupArgs g, const float* __restrict__ x,
+                                                             int kb) {
+    __shared__ float red[16 * R];
+    const int b = blockIdx.x;
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < ZT_GROUP_MAX; i++) m += (i < g.n && b >= g.wg0[i]) ? 1 : 0;
+    q4_steps_body<S, R>(g.sc[m], g.dt[m], x, g.y[m], g.rows[m], kb, (b - g.wg0[m]) * R, red);
 }
 
 // IQ4_NL batch-1 GEMV with fp16 activations.  The quad mapping of
@@ -751,6 +782,73 @@ using namespace zt;
 ZT_EXPORT int zt_gemm_q4_f32(const void* A_q4, const float* B, float* C, int M, int K, int N, int data_offset,
                              hipStream_t stream) {
     return gemm_blk18<Fmt::Q4_0, float>(A_q4, B, C, M, K, N, data_offset, stream);
+}
+
+ZT_EXPORT int zt_gemm_q4_group_f32(const zt_q4_gemv_desc* descs, int n, const float* x, int K,
+                                   hipStream_t stream) {
+    if (descs == nullptr || n < 1 || n > ZT_GROUP_MAX || K <= 0 || K % 32 != 0 || x == nullptr ||
+        ((uintptr_t)x & 15))
+        return (int)hipErrorInvalidValue;
+    const int kb = K / 32;
+    long total = 0;
+    for (int i = 0; i < n; i++) {
+        const zt_q4_gemv_desc& d = descs[i];
+        const uint8_t* data = static_cast<const uint8_t*>(d.A) + d.data_offset;
+        if (d.rows < 0 || d.reserved != 0) return (int)hipErrorInvalidValue;
+        if (d.rows > 0 && (d.A == nullptr || d.y == nullptr || d.data_offset < 0 || ((uintptr_t)d.A & 1) ||
+                           ((uintptr_t)data & 15)))
+            return (int)hipErrorInvalidValue;
+        total += d.rows;
+    }
+    if (total == 0) return (int)hipSuccess;
+    bool fixed = kb <= 512;
+    for (int i = 0; i < n; i++) fixed = fixed && (long)descs[i].rows * kb * 16 < 0x7fffffffL;
+    if (!fixed) {
+        // rows past the fixed-step kernel's reach: one launch per matrix
+        for (int i = 0; i < n; i++) {
+            const int rc = descs[i].rows == 0 ? 0
+                         : zt_gemm_q4_f32(descs[i].A, x, descs[i].y, descs[i].rows, K, 1, (int)descs[i].data_offset,
+                                          stream);
+            if (rc != 0) return rc;
+        }
+        return (int)hipSuccess;
+    }
+    // the single-matrix launch configuration, rows per wave from the group's total rows
+    const int S = kb <= 128 ? 1 : 2;
+    int nw = ceil_div(kb, 16 * S);
+    if (nw > 12) nw = 16;
+    const int R = pick_rows_per_wave(total, nw, 1, 2048);
+    Q4GroupArgs g{};
+    int wg = 0;
+    for (int i = 0; i < n; i++) {
+        const uint8_t* base = static_cast<const uint8_t*>(descs[i].A);
+        g.sc[i] = reinterpret_cast<const uint16_t*>(base);
+        g.dt[i] = reinterpret_cast<const uint32_t*>(base + descs[i].data_offset);
+        g.y[i] = descs[i].y;
+        g.rows[i] = descs[i].rows;
+        g.wg0[i] = wg;
+        wg += ceil_div(descs[i].rows, R);
+    }
+    g.n = n;
+    const dim3 grid(wg), block(nw * kWave);
+#define ZT_Q4G(SS, RR) gemv_q4_group_kernel<SS, RR><<<grid, block, 0, stream>>>(g, x, kb)
+    if (S == 1) {
+        switch (R) {
+            case 8: ZT_Q4G(1, 8); break;
+            case 4: ZT_Q4G(1, 4); break;
+            case 2: ZT_Q4G(1, 2); break;
+            default: ZT_Q4G(1, 1); break;
+        }
+    } else {
+        switch (R) {
+            case 8: ZT_Q4G(2, 8); break;
+            case 4: ZT_Q4G(2, 4); break;
+            case 2: ZT_Q4G(2, 2); break;
+            default: ZT_Q4G(2, 1); break;
+        }
+    }
+#undef ZT_Q4G
+    return (int)hipGetLastError();
 }
 
 ZT_EXPORT int zt_gemm_q4_f16(const void* A_q4, const uint16_t* B, float* C, int M, int K, int N,

@@ -524,6 +524,30 @@ class ROCmEngine:
             return self.matmul(w, x.reshape(act.shape))
         return self.matmul(x.reshape(act.shape), w)
 
+    def gemv_group(self, weights: list[Tensor], x: torch.Tensor) -> list[torch.Tensor]:
+        """y_i = W_i @ x for weight Tensors that read the same fp32 activation
+        vector x[K] (a decode layer's q/k/v, or gate/up).  Q4_0 weights run in
+        one zt_gemm_q4_group_f32 launch (up to ZT_GROUP_MAX matrices a
+        launch), each in its own upload: the effect of MergeQ4Storage
+        (tensor/quantized.go:224-242) without re-laying out the storages.
+        Other formats run one GEMV per matrix."""
+        if x.dtype != torch.float32 or x.dim() != 1 or x.device != self.device:
+            raise ValueError("gemv_group takes one fp32 activation vector on the engine's device")
+        k = x.shape[0]
+        for w in weights:
+            if not isinstance(w, Tensor) or w.shape[-1] != k:
+                raise ValueError(f"gemv_group: every weight must be a quantized [rows, {k}] Tensor")
+        if not all(isinstance(w.storage, Q4Storage) for w in weights) or _p(x) % 16 != 0 or k % 32 != 0:
+            return [self._weight_times(w.storage, w.shape[-2], k, x).reshape(-1) for w in weights]
+        self.upload_weights([w.storage for w in weights])
+        outs = [torch.empty(w.shape[-2], dtype=torch.float32, device=self.device) for w in weights]
+        for i0 in range(0, len(weights), _lib.GROUP_MAX):
+            part = list(zip(weights[i0:i0 + _lib.GROUP_MAX], outs[i0:i0 + _lib.GROUP_MAX]))
+            descs = _lib.q4_gemv_descs([(_p(w.storage.gpu_ptr().tensor), w.storage.gpu_ptr().data_offset, _p(y),
+                                         w.shape[-2]) for w, y in part])
+            self.lib.call("zt_gemm_q4_group_f32", descs, len(part), _p(x), k, self._s)
+        return outs
+
     # ---------------------------------------------------------------- ternary
 
     def ternary_gemv(self, weights: TernaryStorage, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
