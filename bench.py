@@ -503,8 +503,10 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         del sep
         wbufs = [wt, st]
         x = dev(synth.x_f16(K * N, seed))
+        wsb = lib.zt_gemm_iq4nlt_workspace_bytes(rows, K, N)
+        wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")  # launches run in order on one stream
         fn = lambda wb, y: lib.zt_gemm_iq4nlt_f16(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows,
-                                                  K, N, s)
+                                                  K, N, wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes("iq4nl", rows, K, N)
     elif fmt == "w4a16sz":
         # batch 1 on the packed (scale, zero) dwords (zt_w4a16_pack_szr), built outside the timing
@@ -530,8 +532,10 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
         del p, sc, zr
         wbufs = [wt, sz]
         x = dev(synth.x_f16(K * N, seed))
+        wsb = lib.zt_gemm_w4a16t_workspace_bytes(rows, K, N)
+        wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")  # launches run in order on one stream
         fn = lambda wb, y: lib.zt_gemm_w4a16t_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows,
-                                                  K, N, 128, s)
+                                                  K, N, 128, wsbuf.data_ptr(), wsb, s)
         nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
     elif fmt == "ternary_i8":
         t = synth.ternary(rows, K, seed)
@@ -646,12 +650,14 @@ def run_pmc_case_w4a16(torch, lib, tiled: bool) -> None:
         copies.append(bufs)
     x = dev(synth.x_f16(K * N, 0x5EED0043))
     y = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    wsb = lib.zt_gemm_w4a16t_workspace_bytes(rows, K, N)
+    wsbuf = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
     for i in range(40):
         b = copies[i % 3]
         if tiled:
             rc = lib.zt_gemm_w4a16t_f32(b[0].data_ptr(), b[1].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, 128,
-                                        s)
+                                        wsbuf.data_ptr(), wsb, s)
         else:
             rc = lib.zt_gemm_w4a16_f32(b[0].data_ptr(), b[1].data_ptr(), b[2].data_ptr(), x.data_ptr(), y.data_ptr(),
                                        rows, K, N, 128, s)

@@ -136,9 +136,14 @@ int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, void* W_tile
 /* C[M, N] = dequant(W) B on the tiled layout, B fp16 [K, N] 16-byte
  * aligned, N in {4, 8, 12, 16}, K % 128 == 0, else InvalidValue.  The
  * codebook enters the MFMAs rounded to fp16 (relative error at most 2^-11
- * per entry); split K ranges add into C with fp32 atomics after a zero fill. */
+ * per entry).  When K is split across workgroups, each split stores its
+ * partial tiles to `workspace` (16-byte aligned, at least
+ * zt_gemm_iq4nlt_workspace_bytes(M, K, N) bytes, 0 when K is not split)
+ * and a second kernel sums them in split order: C is the same on every
+ * run.  A missing or short workspace when one is needed -> InvalidValue. */
+long zt_gemm_iq4nlt_workspace_bytes(int M, int K, int N);
 int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t* B, float* C, int M, int K, int N,
-                       zt_stream_t stream);
+                       void* workspace, long workspace_bytes, zt_stream_t stream);
 
 /* ---- Q8_0 -------------------------------------------------------------- */
 
@@ -228,11 +233,15 @@ int zt_w4a16_tile(const void* W_packed, const uint16_t* scales, const uint16_t* 
 /* C[M, N] = dequant(W) B on the tiled layout, the result of
  * zt_gemm_w4a16_f32 within the fp32 tolerance: N in {4, 8, 12, 16},
  * K % 128 == 0, group_size % 128 == 0, B fp16 [K, N] 16-byte aligned,
- * M * K/group_size < 2^29, else InvalidValue.  Writes C with a zero fill
- * and fp32 atomic adds when K is split across workgroups, so the last bits
- * of C can vary from run to run. */
+ * M * K/group_size < 2^29, else InvalidValue.  When K is split across
+ * workgroups, the splits store partial tiles to `workspace` (16-byte
+ * aligned, at least zt_gemm_w4a16t_workspace_bytes(M, K, N) bytes; 0 when
+ * K is not split) and a second kernel sums them in split order, so C is
+ * the same on every run.  A missing or short workspace when one is needed
+ * -> InvalidValue. */
+long zt_gemm_w4a16t_workspace_bytes(int M, int K, int N);
 int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* B, float* C, int M, int K, int N,
-                       int group_size, zt_stream_t stream);
+                       int group_size, void* workspace, long workspace_bytes, zt_stream_t stream);
 
 /* ---- Batched Q4_0 / Q8_0 on tiled layouts (MFMA) ------------------------- */
 

@@ -3,7 +3,7 @@
 These follow the reference's own engine tests: the quantized MatMul dispatch
 on either operand side (compute/cpu_engine_quant_test.go), the W4A16
 dispatch equalling dequantize + GEMM (compute/w4a16_test.go:255-348, there
-RMSE <= 1e-6 on one CPU engine; here max|y - y_ref| / max|y_ref| <= 1e-3
+RMSE <= 1e-6 on one CPU engine; here max|y - y_ref| / max|y_ref| <= 1e-5
 against the CPU restatement, fp32 accumulation in both), weight residency
 (compute/engine.go:36-38) and TernaryGEMV's known answers
 (compute/ternary_gemv_test.go:25-45).  Everything runs through libzt_hip.so.
@@ -31,7 +31,8 @@ from ztensor_amd.storage import (  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+TOL = 1e-5  # fp32-exact products: only the summation order differs
+TOL_IQ4_F16 = 1e-3  # IQ4_NL with fp16 activations: codebook carried in fp16
 GOLD = Path(__file__).resolve().parent / "golden"
 
 
@@ -99,7 +100,7 @@ def test_iq4nl_matmul_fp16_activations(eng, orc):
     x16 = synth.x_f16(K * N, 15)
     c = eng.matmul(Tensor((rows, K), s), torch.from_numpy(x16.view(np.float16).reshape(K, N)).cuda())
     ref = orc.iq4nl_matmul(w.raw, x16, rows, K, N)
-    assert rel_err(c.cpu().numpy(), np.asarray(ref).reshape(rows, N)) <= TOL
+    assert rel_err(c.cpu().numpy(), np.asarray(ref).reshape(rows, N)) <= TOL_IQ4_F16
 
 
 def _gptq(w):

@@ -74,10 +74,18 @@ def tile_dev(lib, raw, rows, K):
     return wt, st
 
 
+def workspace(lib, rows, K, N):
+    nb = lib.zt_gemm_iq4nlt_workspace_bytes(rows, K, N)
+    assert nb >= 0
+    return torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda"), nb
+
+
 def run_t(lib, wt, st, x16, rows, K, N):
     xd = dev(x16)
     c = torch.empty(rows * N, dtype=torch.float32, device="cuda")
-    lib.call("zt_gemm_iq4nlt_f16", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, stream())
+    ws, nb = workspace(lib, rows, K, N)
+    lib.call("zt_gemm_iq4nlt_f16", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
+             ws.data_ptr(), nb, stream())
     return c.cpu().numpy()
 
 
@@ -126,8 +134,12 @@ def test_iq4nlt_invalid_arguments(lib):
     t = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
     p = t.data_ptr()
     for rows, K, N in [(2, 128, 3), (2, 128, 1), (2, 96, 4), (2, 160, 8)]:
-        assert lib.zt_gemm_iq4nlt_f16(p, p, p, p, rows, K, N, stream()) == 1, (rows, K, N)
-    assert lib.zt_gemm_iq4nlt_f16(p + 4, p, p, p, 2, 128, 4, stream()) == 1
+        assert lib.zt_gemm_iq4nlt_f16(p, p, p, p, rows, K, N, p, 1 << 16, stream()) == 1, (rows, K, N)
+    assert lib.zt_gemm_iq4nlt_f16(p + 4, p, p, p, 2, 128, 4, p, 1 << 16, stream()) == 1
+    need = lib.zt_gemm_iq4nlt_workspace_bytes(3584, 3584, 8)
+    assert need > 0
+    assert lib.zt_gemm_iq4nlt_f16(p, p, p, p, 3584, 3584, 8, 0, 0, stream()) == 1  # workspace missing
+    assert lib.zt_gemm_iq4nlt_f16(p, p, p, p, 3584, 3584, 8, p, need - 1, stream()) == 1  # too short
     assert lib.zt_iq4nl_tile(p, 2, 96, 16, p, p, stream()) == 1  # K % 128
     assert lib.zt_iq4nl_tile(p, 2, 128, 8, p, p, stream()) == 1  # data not 16-byte aligned
 
@@ -154,10 +166,22 @@ def test_engine_batched_iq4nl_uses_tiled_layout(lib, orc, side):
     assert getattr(s, "_gpu_tiled", None) is not None
 
 
+def test_iq4nlt_repeated_calls_bit_identical(lib):
+    """Split-K calls repeat bit for bit (partials summed in split order)."""
+    for rows, K, N in [(3584, 3584, 8), (1024, 8192, 16)]:
+        assert lib.zt_gemm_iq4nlt_workspace_bytes(rows, K, N) > 0
+        w = synth.iq4nl(rows, K, 75)
+        x16 = synth.x_f16(K * N, 75)
+        wt, st = tile_dev(lib, w.raw, rows, K)
+        a = run_t(lib, wt, st, x16, rows, K, N)
+        b = run_t(lib, wt, st, x16, rows, K, N)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (rows, K, N)
+
+
 def test_iq4nlt_split_combine_graph_replays_and_two_streams(lib, orc):
-    """Split-K calls (zero fill, then atomic adds) captured in a HIP graph and replayed with eager calls in
-    between, then run on two streams at once: every result matches the
-    oracle."""
+    """Split-K calls (partials to a workspace, then the ordered sum)
+    captured in a HIP graph and replayed with eager calls in between, then
+    run on two streams at once: every result matches the oracle."""
     rows, K, N = 3584, 3584, 8
     cases = []
     for seed in (73, 74):
@@ -165,11 +189,12 @@ def test_iq4nlt_split_combine_graph_replays_and_two_streams(lib, orc):
         x16 = synth.x_f16(K * N, seed)
         wt, st = tile_dev(lib, w.raw, rows, K)
         cases.append((wt, st, dev(x16), torch.empty(rows * N, dtype=torch.float32, device="cuda"),
-                      orc.iq4nl_matmul(w.raw, x16, rows, K, N)))
+                      orc.iq4nl_matmul(w.raw, x16, rows, K, N), workspace(lib, rows, K, N)))
 
     def call(case, s):
-        wt, st, xd, c, _ = case
-        lib.call("zt_gemm_iq4nlt_f16", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N, s)
+        wt, st, xd, c, _, (ws, nb) = case
+        lib.call("zt_gemm_iq4nlt_f16", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
+                 ws.data_ptr(), nb, s)
 
     cs = torch.cuda.Stream()
     cs.wait_stream(torch.cuda.current_stream())

@@ -18,7 +18,7 @@ from ztensor_amd.storage import Q4KStorage, Q5_0Storage, Q6KStorage, Tensor  # n
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+TOL = 1e-5  # every product exact in fp32: only the summation order differs
 KQ = ["q4_k", "q5_k", "q6_k"]
 LLAMA8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
 RAGGED = [(1, 256), (17, 768), (65, 2560), (5, 6912), (130, 1792)]

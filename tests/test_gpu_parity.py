@@ -3,8 +3,11 @@
 Bars (written into each assertion):
   * dequantizers: bit-exact (uint32 view equality) with the reference's
     dequantizers as restated by the oracle;
-  * GEMV / GEMM: max|y - y_ref| / max|y_ref| <= 1e-3 with fp32 accumulation,
-    y_ref = the reference CPU engine's result (oracle);
+  * GEMV / GEMM: max|y - y_ref| / max|y_ref| <= 1e-5 with fp32 accumulation,
+    y_ref = the reference CPU engine's result (oracle): every product is
+    exact in fp32 on these kernels, so only the summation order differs
+    (measured about 2e-7); 1e-3 for the IQ4_NL kernels
+    that carry the codebook in fp16 (relative error up to 2^-11 an entry);
   * ternary int8: bit-exact (integer accumulation).
 Shapes: the benchmark configurations at full size plus ragged/edge cases.
 """
@@ -21,7 +24,8 @@ from ztensor_amd import _lib, synth  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+TOL = 1e-5
+TOL_IQ4_F16 = 1e-3  # fp16 codebook (gemv_iq4nl_h16_*, iq4nlt)
 GOLD = Path(__file__).resolve().parent / "golden"
 
 LLAMA8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]  # (rows = out features, K)
@@ -91,7 +95,8 @@ def test_q4_dequant_bit_exact(lib, orc, rows, K):
     assert bits_equal(out.cpu().numpy(), orc.q4_dequant(w.raw, rows * K))
 
 
-@pytest.mark.parametrize("rows,K", LLAMA8B + [(1, 32), (3, 64), (65, 96), (130, 2080), (7, 16384)])
+@pytest.mark.parametrize("rows,K", LLAMA8B + [(1, 32), (3, 64), (65, 96), (130, 2080), (7, 16384), (64, 28672),
+                                    (9, 16416)])
 def test_q4_gemv_matches_oracle(lib, orc, rows, K):
     say(f"q4 gemv rows={rows} K={K}")
     seed = synth.seed_for(2, LLAMA8B.index((rows, K)) if (rows, K) in LLAMA8B else 9)
@@ -273,7 +278,7 @@ def test_iq4nl_gemm_matches_oracle(lib, orc, rows, K, N):
     lib.call("zt_gemm_iq4nl_f16", a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, N,
              lib.zt_q4_gpu_data_offset(nblk), stream())
     ref = orc.iq4nl_matmul(w.raw, x16, rows, K, N)
-    assert rel_err(c.cpu().numpy(), ref) <= TOL
+    assert rel_err(c.cpu().numpy(), ref) <= TOL_IQ4_F16
 
 
 @pytest.mark.parametrize("rows,K", [(8193, 4096), (9001, 3616), (8200, 128), (7, 2048), (1, 32), (4099, 3584),
@@ -292,7 +297,7 @@ def test_iq4nl_f16_gemv_ragged(lib, orc, rows, K):
     xd = dev(x16)
     lib.call("zt_gemm_iq4nl_f16", a.data_ptr(), xd.data_ptr(), c.data_ptr(), rows, K, 1,
              lib.zt_q4_gpu_data_offset(nblk), stream())
-    assert rel_err(c.cpu().numpy(), orc.iq4nl_matmul(w.raw, x16, rows, K, 1)) <= TOL
+    assert rel_err(c.cpu().numpy(), orc.iq4nl_matmul(w.raw, x16, rows, K, 1)) <= TOL_IQ4_F16
 
 
 @pytest.mark.parametrize("rows,K,N", [(33, 2176, 4), (1, 128, 16), (100, 3584, 12), (64, 384, 8)])
@@ -332,7 +337,7 @@ def test_iq4nl_fp16_codebook_worst_case(lib, orc):
              lib.zt_q4_gpu_data_offset(nblk), stream())
     ref = orc.iq4nl_matmul(raw, x16, rows, K, 1)
     err = rel_err(c.cpu().numpy(), ref)
-    assert err <= 4e-4 and err <= TOL
+    assert err <= 4e-4 and err <= TOL_IQ4_F16
 
 
 def test_iq4nl_fp32_activations(lib, orc):

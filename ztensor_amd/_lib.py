@@ -37,7 +37,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_iq4nl_tiled_bytes": (L, [I, I]),
     "zt_iq4nl_tiled_scale_bytes": (L, [I, I]),
     "zt_iq4nl_tile": (I, [P, I, I, I, P, P, P]),
-    "zt_gemm_iq4nlt_f16": (I, [P, P, P, P, I, I, I, P]),
+    "zt_gemm_iq4nlt_workspace_bytes": (L, [I, I, I]),
+    "zt_gemm_iq4nlt_f16": (I, [P, P, P, P, I, I, I, P, L, P]),
     "zt_iq4nl_raw_to_gpu": (None, [P, L, P]),
     "zt_gemm_q8_f32": (I, [P, P, P, I, I, I, P]),
     "zt_gemm_q8sep_f32": (I, [P, P, P, I, I, I, L, P]),
@@ -59,7 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_w4a16_tiled_bytes": (L, [I, I]),
     "zt_w4a16_sz_bytes": (L, [I, I, I]),
     "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),
-    "zt_gemm_w4a16t_f32": (I, [P, P, P, P, I, I, I, I, P]),
+    "zt_gemm_w4a16t_workspace_bytes": (L, [I, I, I]),
+    "zt_gemm_w4a16t_f32": (I, [P, P, P, P, I, I, I, I, P, L, P]),
     "zt_q4_tiled_bytes": (L, [I, I]),
     "zt_q4_tiled_scale_bytes": (L, [I, I]),
     "zt_q4_tile": (I, [P, I, I, I, P, P, P]),

@@ -9,7 +9,7 @@
 
 extern "C" {
 
-int zt_abi_version(void) { return 100; }
+int zt_abi_version(void) { return 101; }
 
 long zt_q4_gpu_data_offset(long nblk) { return (nblk * 2 + 15) & ~15L; }
 

@@ -156,8 +156,8 @@ __device__ __forceinline__ void tiled_store_partial(const float4v& v, float* __r
     if ((lane & 15) < N) __builtin_nontemporal_store(v, reinterpret_cast<float4v*>(ws + (((long)split * ntiles + rt) * 64 + lane) * 4));
 }
 
-static __global__ void tiled_reduce_kernel(const float* __restrict__ ws, float* __restrict__ y, int rows, int N,
-                                           int ntiles, int splits) {
+static __global__ void __launch_bounds__(64) tiled_reduce_kernel(const float* __restrict__ ws, float* __restrict__ y,
+                                                                 int rows, int N, int ntiles, int splits) {
     // thread = one output of a lane with column < N: (tile, lane 16g + i, element e),
     // consecutive threads on consecutive floats of the partial tiles
     const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -165,14 +165,14 @@ static __global__ void tiled_reduce_kernel(const float* __restrict__ ws, float* 
     const long rt = q / (16 * N);
     const int r = (int)(q % (16 * N)), lg = r / (4 * N), li = (r / 4) % N, e = r % 4;
     const long p = (rt * 64 + 16 * lg + li) * 4 + e, stride = (long)ntiles * 256;
-    // loads in groups of 8, all issued before the adds; summed in split order
+    // up to 32 splits' loads in flight before the adds, summed in split order
     float s = 0.0f;
-    for (int k0 = 0; k0 < splits; k0 += 8) {
-        float v[8];
+    for (int k0 = 0; k0 < splits; k0 += 32) {
+        float v[32];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = k0 + j < splits ? __builtin_nontemporal_load(ws + (k0 + j) * stride + p) : 0.0f;
+        for (int j = 0; j < 32; j++) v[j] = k0 + j < splits ? __builtin_nontemporal_load(ws + (k0 + j) * stride + p) : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) s += v[j];
+        for (int j = 0; j < 32; j++) s += v[j];
     }
     const long row = rt * 16 + 4 * lg + e;
     if (row < rows) y[row * N + li] = s;
@@ -184,7 +184,7 @@ __host__ __forceinline__ long tiled_ws_bytes(int rows, int splits) {
 
 __host__ __forceinline__ void tiled_reduce(const void* ws, float* y, int rows, int N, int splits, hipStream_t st) {
     const int ntiles = (rows + 15) / 16;
-    tiled_reduce_kernel<<<(int)(((long)ntiles * 16 * N + 255) / 256), 256, 0, st>>>(
+    tiled_reduce_kernel<<<(int)(((long)ntiles * 16 * N + 63) / 64), 64, 0, st>>>(
         static_cast<const float*>(ws), y, rows, N, ntiles, splits);
 }
 

@@ -919,7 +919,7 @@ template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint16_t* __restrict__ stl,
                                                              const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                             int rows, int K) {
+                                                             float* __restrict__ ws, int rows, int K, int nch) {
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
     constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
@@ -939,9 +939,15 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
         byi = j % gridDim.y;
         bxi = (id & 7) + 8 * (j / gridDim.y);
     }
-    const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
     const int ntiles = (rows + 15) / 16;
+    float4v acc[2];
+    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+    // this workgroup's K range: nch chunks of UPW units, one after another
+    for (int ch = 0; ch < nch; ch++) {
+    const int u0 = (byi * nch + ch) * UPW, u1 = min(nunits, u0 + UPW);
+    if (u0 >= nunits) break;
+    if (ch > 0) asm volatile("s_barrier" ::: "memory");  // every wave is done with the previous chunk's LDS
     const int npieces = (u1 - u0) * 128 * 2 * N / 16;
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
@@ -993,8 +999,6 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
     // step s of unit u reads X rows 128u + 32s + 8lg + (li >> 2) (+ 4), whose
     // padded LDS offset is (8lg + (li >> 2)) 2N + (136u + 34s) 2N
     const int lbase = (8 * lg + (li >> 2)) * 2 * N + 8 * (li & 3);
-    float4v acc[2];
-    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < UPW; u++) {
         if (u0 + u < u1) {
@@ -1015,37 +1019,56 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
             }
         }
     }
-    if (li < N) {
+    }
+    if (gridDim.y > 1) {
+        // K split: partial tiles to the workspace, summed in split order by tiled_reduce_kernel
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = row0 / 16 + t;
+            if (rt < ntiles) tiled_store_partial(acc[t], ws, byi, ntiles, rt, lane, N);
+        }
+    } else if (li < N) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = row0 + 16 * t + 4 * lg + i;
-                if (row < rows) {
-                    if (gridDim.y > 1)
-                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
-                    else
-                        y[(long)row * N + li] = acc[t][i];
-                }
+                if (row < rows) y[(long)row * N + li] = acc[t][i];
             }
     }
 }
 
 template <int UPW, int N>
 static void launch_iq4t(dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc, const uint16_t* x, float* y,
-                        int M, int K) {
+                        float* ws, int M, int K, int nch) {
     constexpr int W = 4;
     const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 1024 + (size_t)2 * W * UPW * 64 * 2;
-    iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, y, M, K);
+    iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, y, ws, M, K, nch);
 }
 
 template <int N>
-static void launch_iq4t_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc, const uint16_t* x,
-                          float* y, int M, int K) {
+static void launch_iq4t_n(int upw, int nch, dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc,
+                          const uint16_t* x, float* y, float* ws, int M, int K) {
     if (upw == 4)
-        launch_iq4t<4, N>(g, st, wt, sc, x, y, M, K);
+        launch_iq4t<4, N>(g, st, wt, sc, x, y, ws, M, K, nch);
     else
-        launch_iq4t<2, N>(g, st, wt, sc, x, y, M, K);
+        launch_iq4t<2, N>(g, st, wt, sc, x, y, ws, M, K, nch);
+}
+
+// Grid of the tiled IQ4_NL GEMM: 128 rows a workgroup and the largest K
+// range, up to 4 units, that still gives >= 256 workgroups (8 units measured
+// 8-13% slower at the Qwen2-7B shapes); K ranges split across blockIdx.y.
+// When that leaves more than 8 splits and >= 256 workgroups remain with
+// half as many, each workgroup walks 2 chunks in turn, so fewer partial tiles
+// go through the workspace.
+static dim3 iq4t_grid(int M, int K, int& upw, int& nch) {
+    const int nunits = K / 128;
+    const int gx = ceil_div(M, 128);
+    upw = 4;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    // (2 chunks: 17.2 -> 16.0 us at 18944 x 3584, batch 8; 4 chunks measured 21 us)
+    nch = (ceil_div(nunits, upw) > 8 && (long)gx * ceil_div(nunits, upw * 2) >= 256) ? 2 : 1;
+    return dim3(gx, ceil_div(nunits, upw * nch));
 }
 
 ZT_EXPORT long zt_iq4nl_tiled_bytes(int M, int K) {
@@ -1075,8 +1098,15 @@ ZT_EXPORT int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, vo
     return (int)hipGetLastError();
 }
 
+ZT_EXPORT long zt_gemm_iq4nlt_workspace_bytes(int M, int K, int N) {
+    if (M < 0 || K < 0 || K % 128 != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
+    if (M == 0 || K == 0) return 0;
+    int upw, nch;
+    return tiled_ws_bytes(M, (int)iq4t_grid(M, K, upw, nch).y);
+}
+
 ZT_EXPORT int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t* B, float* C, int M, int K,
-                                 int N, hipStream_t stream) {
+                                 int N, void* workspace, long workspace_bytes, hipStream_t stream) {
     if (M < 0 || K < 0 || K % 128 != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
     if (M == 0 || K == 0) return (int)hipSuccess;
@@ -1084,21 +1114,20 @@ ZT_EXPORT int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const
     if (((uintptr_t)W_tiled & 15) || ((uintptr_t)S_tiled & 15) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
         return (int)hipErrorInvalidValue;
     if ((long)((M + 15) / 16) * (K / 128) * 128 >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
-    const int nunits = K / 128;
-    const int gx = ceil_div(M, 128);
-    // the largest K range per workgroup, up to 4 units, that still gives >= 256
-    // workgroups (8 units measured 8-13% slower at the Qwen2-7B shapes)
-    int upw = 4;
-    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
-    const dim3 g(gx, ceil_div(nunits, upw));
-    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    int upw, nch;
+    const dim3 g = iq4t_grid(M, K, upw, nch);
+    const long need = tiled_ws_bytes(M, (int)g.y);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 15)))
+        return (int)hipErrorInvalidValue;
     const uint4* wt = static_cast<const uint4*>(W_tiled);
     const uint16_t* sc = static_cast<const uint16_t*>(S_tiled);
+    float* ws = static_cast<float*>(workspace);
     switch (N) {
-        case 4: launch_iq4t_n<4>(upw, g, stream, wt, sc, B, C, M, K); break;
-        case 8: launch_iq4t_n<8>(upw, g, stream, wt, sc, B, C, M, K); break;
-        case 12: launch_iq4t_n<12>(upw, g, stream, wt, sc, B, C, M, K); break;
-        default: launch_iq4t_n<16>(upw, g, stream, wt, sc, B, C, M, K); break;
+        case 4: launch_iq4t_n<4>(upw, nch, g, stream, wt, sc, B, C, ws, M, K); break;
+        case 8: launch_iq4t_n<8>(upw, nch, g, stream, wt, sc, B, C, ws, M, K); break;
+        case 12: launch_iq4t_n<12>(upw, nch, g, stream, wt, sc, B, C, ws, M, K); break;
+        default: launch_iq4t_n<16>(upw, nch, g, stream, wt, sc, B, C, ws, M, K); break;
     }
+    if (g.y > 1) tiled_reduce(workspace, C, M, N, (int)g.y, stream);
     return (int)hipGetLastError();
 }

@@ -673,7 +673,7 @@ template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint32_t* __restrict__ szp,
                                                              const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                             int rows, int K, int gs) {
+                                                             float* __restrict__ ws, int rows, int K, int gs, int nch) {
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
     constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
@@ -691,9 +691,16 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
         byi = j % gridDim.y;
         bxi = (id & 7) + 8 * (j / gridDim.y);
     }
-    const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
     const int ntiles = (rows + 15) / 16;
+    const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
+    float4v acc[2];
+    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
+    // this workgroup's K range: nch chunks of UPW units, one after another
+    for (int ch = 0; ch < nch; ch++) {
+    const int u0 = (byi * nch + ch) * UPW, u1 = min(nunits, u0 + UPW);
+    if (u0 >= nunits) break;
+    if (ch > 0) asm volatile("s_barrier" ::: "memory");  // every wave is done with the previous chunk's LDS
     const int npieces = (u1 - u0) * 128 * 2 * N / 16;
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
@@ -744,9 +751,6 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     // step s of unit u reads X rows 128u + 32lg + 8s + offa (+ 2), whose
     // padded LDS offset is (34lg + offa) 2N + (136u + 8s) 2N
     const int lbase = (34 * lg + offa) * 2 * N + 8 * (li & 3);
-    const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
-    float4v acc[2];
-    acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < UPW; u++) {
         if (u0 + u < u1) {
@@ -774,39 +778,58 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
             }
         }
     }
-    if (li < N) {
+    }
+    if (gridDim.y > 1) {
+        // K split: partial tiles to the workspace, summed in split order by tiled_reduce_kernel
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rt = row0 / 16 + t;
+            if (rt < ntiles) tiled_store_partial(acc[t], ws, byi, ntiles, rt, lane, N);
+        }
+    } else if (li < N) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = row0 + 16 * t + 4 * lg + i;
-                if (row < rows) {
-                    if (gridDim.y > 1)
-                        unsafeAtomicAdd(&y[(long)row * N + li], acc[t][i]);
-                    else
-                        y[(long)row * N + li] = acc[t][i];
-                }
+                if (row < rows) y[(long)row * N + li] = acc[t][i];
             }
     }
 }
 
 template <int UPW, int N>
 static void launch_w4t(dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz, const uint16_t* x, float* y,
-                       int M, int K, int gs) {
+                       float* ws, int M, int K, int gs, int nch) {
     constexpr int W = 4;
     const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 8 * UPW * 32 * W;
-    w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, y, M, K, gs);
+    w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, y, ws, M, K, gs, nch);
 }
 
 template <int N>
-static void launch_w4t_n(int upw, dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz, const uint16_t* x,
-                         float* y, int M, int K, int gs) {
+static void launch_w4t_n(int upw, int nch, dim3 g, hipStream_t st, const uint4* wt, const uint32_t* sz,
+                         const uint16_t* x, float* y, float* ws, int M, int K, int gs) {
     if (upw == 8)
-        launch_w4t<8, N>(g, st, wt, sz, x, y, M, K, gs);
+        launch_w4t<8, N>(g, st, wt, sz, x, y, ws, M, K, gs, nch);
     else if (upw == 4)
-        launch_w4t<4, N>(g, st, wt, sz, x, y, M, K, gs);
+        launch_w4t<4, N>(g, st, wt, sz, x, y, ws, M, K, gs, nch);
     else
-        launch_w4t<2, N>(g, st, wt, sz, x, y, M, K, gs);
+        launch_w4t<2, N>(g, st, wt, sz, x, y, ws, M, K, gs, nch);
+}
+
+// Grid of the tiled W4A16 GEMM: 128 rows a workgroup, and the largest K range
+// (up to 8 units) that still gives >= 256 workgroups.  K ranges are split
+// across blockIdx.y; when that leaves more than 8 splits, each workgroup
+// walks nch chunks of upw units in turn, as long as >= 256 workgroups
+// remain, so fewer partial tiles go through the workspace.
+static dim3 w4t_grid(int M, int K, int& upw, int& nch) {
+    const int nunits = K / 128;
+    const int gx = ceil_div(M, 128);
+    upw = 8;
+    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
+    // (28672 x 8192, batch 16: 33.2 us with 28 splits, 31.6 with 2 chunks, 30.2 with 4)
+    nch = 1;
+    while (ceil_div(nunits, upw * nch) > 8 && (long)gx * ceil_div(nunits, upw * nch * 2) >= 256) nch *= 2;
+    return dim3(gx, ceil_div(nunits, upw * nch));
 }
 
 ZT_EXPORT long zt_w4a16_tiled_bytes(int M, int K) {
@@ -836,8 +859,15 @@ ZT_EXPORT int zt_w4a16_tile(const void* W_packed, const uint16_t* scales, const 
     return (int)hipGetLastError();
 }
 
+ZT_EXPORT long zt_gemm_w4a16t_workspace_bytes(int M, int K, int N) {
+    if (M < 0 || K < 0 || K % 128 != 0 || (N != 4 && N != 8 && N != 12 && N != 16)) return -1;
+    if (M == 0 || K == 0) return 0;
+    int upw, nch;
+    return tiled_ws_bytes(M, (int)w4t_grid(M, K, upw, nch).y);
+}
+
 ZT_EXPORT int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const uint16_t* B, float* C, int M, int K,
-                                 int N, int group_size, hipStream_t stream) {
+                                 int N, int group_size, void* workspace, long workspace_bytes, hipStream_t stream) {
     if (M < 0 || K < 0 || K % 128 != 0 || group_size <= 0 || group_size % 128 != 0 || K % group_size != 0)
         return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
@@ -846,19 +876,19 @@ ZT_EXPORT int zt_gemm_w4a16t_f32(const void* W_tiled, const uint32_t* sz, const 
     if (((uintptr_t)W_tiled & 15) || ((uintptr_t)sz & 3) || ((uintptr_t)B & 15) || ((uintptr_t)C & 3))
         return (int)hipErrorInvalidValue;
     if ((long)M * (K / group_size) >= (1L << 29)) return (int)hipErrorInvalidValue;  // 32-bit sz offsets
-    const int nunits = K / 128;
-    const int gx = ceil_div(M, 128);
-    // the largest K range per workgroup that still gives >= 256 workgroups
-    int upw = 8;
-    while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
-    const dim3 g(gx, ceil_div(nunits, upw));
-    if (g.y > 1) mfma_zero(C, (long)M * N, stream);
+    int upw, nch;
+    const dim3 g = w4t_grid(M, K, upw, nch);
+    const long need = tiled_ws_bytes(M, (int)g.y);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 15)))
+        return (int)hipErrorInvalidValue;
     const uint4* wt = static_cast<const uint4*>(W_tiled);
+    float* ws = static_cast<float*>(workspace);
     switch (N) {
-        case 4: launch_w4t_n<4>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
-        case 8: launch_w4t_n<8>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
-        case 12: launch_w4t_n<12>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
-        default: launch_w4t_n<16>(upw, g, stream, wt, sz, B, C, M, K, group_size); break;
+        case 4: launch_w4t_n<4>(upw, nch, g, stream, wt, sz, B, C, ws, M, K, group_size); break;
+        case 8: launch_w4t_n<8>(upw, nch, g, stream, wt, sz, B, C, ws, M, K, group_size); break;
+        case 12: launch_w4t_n<12>(upw, nch, g, stream, wt, sz, B, C, ws, M, K, group_size); break;
+        default: launch_w4t_n<16>(upw, nch, g, stream, wt, sz, B, C, ws, M, K, group_size); break;
     }
+    if (g.y > 1) tiled_reduce(workspace, C, M, N, (int)g.y, stream);
     return (int)hipGetLastError();
 }

@@ -106,7 +106,8 @@ class ROCmEngine:
         self.lib.call("zt_w4a16_tile", w, scales, zeros, m, k, group_size, w_tiled, sz, self._s)
 
     def gemm_w4a16t_f32(self, w_tiled: int, sz: int, b: int, c: int, m: int, k: int, n: int, group_size: int) -> None:
-        self.lib.call("zt_gemm_w4a16t_f32", w_tiled, sz, b, c, m, k, n, group_size, self._s)
+        ws, wsb = self._workspace(self.lib.zt_gemm_w4a16t_workspace_bytes(m, k, n))
+        self.lib.call("zt_gemm_w4a16t_f32", w_tiled, sz, b, c, m, k, n, group_size, ws, wsb, self._s)
 
     def gemv_q4k_f32(self, w: int, x: int, y: int, m: int, k: int) -> None:
         self.lib.call("zt_gemv_q4k_f32", w, x, y, m, k, self._s)
@@ -380,7 +381,8 @@ class ROCmEngine:
                 self.gemm_iq4nl_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             elif x.dtype == torch.float16 and n in _TILED_BATCHES and k % 128 == 0:
                 wt, st = self._iq4nl_tiled(s, buf, rows, k)
-                self.lib.call("zt_gemm_iq4nlt_f16", _p(wt), _p(st), _p(x), _p(c), rows, k, n, self._s)
+                ws, wsb = self._workspace(self.lib.zt_gemm_iq4nlt_workspace_bytes(rows, k, n))
+                self.lib.call("zt_gemm_iq4nlt_f16", _p(wt), _p(st), _p(x), _p(c), rows, k, n, ws, wsb, self._s)
             elif x.dtype == torch.float16:
                 self.gemm_iq4nl_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             else:
