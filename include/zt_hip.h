@@ -274,6 +274,23 @@ int zt_q4_tile(const void* A_q4, int M, int K, int data_offset, void* W_tiled, v
 long zt_gemm_q4t_workspace_bytes(int M, int K, int N);
 int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                     void* workspace, long workspace_bytes, zt_stream_t stream);
+
+/* zt_gemm_q4t_f32 without a workspace argument and without allocating:
+ * no counterpart in the reference.  It is for callers that cannot call
+ * hipMalloc (code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation).  The K-split partials go to a static device array of
+ * ZT_NOALLOC_SCRATCH_BYTES that every GPU holds one copy of from the first
+ * call on it until the process ends; C is bit-identical to
+ * zt_gemm_q4t_f32's.  A call that needs more scratch than that
+ * (zt_gemm_q4t_workspace_bytes(M, K, N) > ZT_NOALLOC_SCRATCH_BYTES, e.g. the
+ * 28672 x 8192 matrices of Llama-3-70B) returns hipErrorOutOfMemory (2)
+ * without launching; other argument errors return InvalidValue as
+ * zt_gemm_q4t_f32 does.  Calls on one GPU share the array: calls that
+ * overlap on one GPU (on different streams) race, calls on one stream do
+ * not.  The current device must be the stream's device. */
+#define ZT_NOALLOC_SCRATCH_BYTES (8L << 20)
+int zt_gemm_q4t_f32_noalloc(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
+                            zt_stream_t stream);
 long zt_q8_tiled_bytes(int M, int K);
 long zt_q8_tiled_scale_bytes(int M, int K);
 int zt_q8_tile(const void* A_q8, int M, int K, long data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q4_tile": (I, [P, I, I, I, P, P, P]),
     "zt_gemm_q4t_workspace_bytes": (L, [I, I, I]),
     "zt_gemm_q4t_f32": (I, [P, P, P, P, I, I, I, P, L, P]),
+    "zt_gemm_q4t_f32_noalloc": (I, [P, P, P, P, I, I, I, P]),
     "zt_q8_tiled_bytes": (L, [I, I]),
     "zt_q8_tiled_scale_bytes": (L, [I, I]),
     "zt_q8_tile": (I, [P, I, I, L, P, P, P]),
@@ -115,6 +116,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 
 HIP_ERROR_INVALID_VALUE = 1
 GROUP_MAX = 8  # ZT_GROUP_MAX
+NOALLOC_SCRATCH_BYTES = 8 << 20  # ZT_NOALLOC_SCRATCH_BYTES
+HIP_ERROR_OUT_OF_MEMORY = 2
 
 
 class Q4GemvDesc(C.Structure):

@@ -54,6 +54,7 @@
 //    (one 32-value block) spans two groups, lane groups 0-1 and 2-3, so its
 //    B operand is split into two masked copies and each group gets its own
 //    offset and weight MFMAs and its own scale.
+#include <mutex>
 #include <type_traits>
 
 #include "zt_mfma.h"
@@ -672,6 +673,54 @@ ZT_EXPORT long zt_gemm_q4t_workspace_bytes(int M, int K, int N) { return blkt_ws
 ZT_EXPORT int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
                               void* workspace, long workspace_bytes, hipStream_t stream) {
     return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, workspace, workspace_bytes, stream);
+}
+
+// ---- allocation-free batched Q4_0: the K-split workspace in static device memory
+//
+// zt_gemm_q4t_f32_noalloc runs the kernels of zt_gemm_q4t_f32 with their
+// workspace in `scratch`, a file-scope device array every GPU holds one copy
+// of (at its own address) from the first call on it until the process ends.
+// Host code never passes the array's name to a kernel: its device address is
+// looked up once per device with hipGetSymbolAddress, with that device
+// current, and kept in scratch_addr.  Calls on one GPU share the array, so
+// calls that overlap on one GPU (different streams) race; on one stream they
+// run in order.  Nothing in it needs clearing: every (split, tile) partial a
+// call reads is written by the same call first.
+static __device__ __align__(256) char scratch[ZT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchDevices = 64;
+static std::mutex scratch_mu;
+static void* scratch_addr[kScratchDevices];
+
+// Device address of `scratch` on the current device, looked up on the first call.
+static int scratch_on_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kScratchDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_addr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (p == nullptr) return (int)hipErrorInvalidSymbol;
+        scratch_addr[dev] = p;
+    }
+    *out = scratch_addr[dev];
+    return (int)hipSuccess;
+}
+
+ZT_EXPORT int zt_gemm_q4t_f32_noalloc(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K,
+                                      int N, hipStream_t stream) {
+    const long need = blkt_ws_bytes<BlkFmt::Q4_0>(M, K, N);
+    if (need < 0) return (int)hipErrorInvalidValue;
+    if (need > ZT_NOALLOC_SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
+    void* ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_on_current_device(&ws);
+        if (rc != 0) return rc;
+    }
+    return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, ws, need, stream);
 }
 
 ZT_EXPORT long zt_q8_tiled_bytes(int M, int K) {
