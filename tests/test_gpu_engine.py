@@ -232,3 +232,47 @@ def test_gemv_group_equals_separate_gemvs(eng, orc):
     assert rel_err(y1.cpu().numpy(), orc.gemm_f32_q8_nt(xs.cpu().numpy(), q8.raw, 1, 128, 256)) <= 1e-5
     with pytest.raises(ValueError):
         eng.gemv_group(ws, xs)  # K mismatch
+
+
+def test_engine_on_a_side_stream_runs_torch_work_on_that_stream(orc):
+    """An engine built on a side stream makes its temporaries (transposes,
+    pads, outputs, tiled copies, the split-K workspace) on that stream: every
+    library call sees it as torch's current stream, and the results are right
+    while the default stream is busy with other work."""
+    side = torch.cuda.Stream()
+    eng = ROCmEngine(0, stream=side)
+    seen = []
+    real_call = eng.lib.call
+
+    def spy(name, *args):
+        seen.append(torch.cuda.current_stream().cuda_stream)
+        return real_call(name, *args)
+
+    eng.lib = type("L", (), {})()
+    for attr in dir(real_call.__self__):
+        if attr.startswith("zt_"):
+            setattr(eng.lib, attr, getattr(real_call.__self__, attr))
+    eng.lib.call = spy
+    rows, K = 512, 1024
+    w = synth.q4_0(rows, K, 71)
+    st = Q4Storage.from_raw(w.raw, rows * K)
+    q8 = synth.q8_0(rows, K, 72)
+    qb = q8.raw.reshape(-1, 36)
+    s8 = Q8Storage.from_blocks(qb[:, :4].copy().view("<f4").reshape(-1), qb[:, 4:].copy().view(np.int8), rows * K)
+    x = synth.x_f32(K * 8, 71).reshape(K, 8)
+    busy = torch.randn(4096, 4096, device="cuda")
+    for _ in range(8):  # keep the default stream busy meanwhile
+        busy = busy @ busy * 1e-3
+    xb = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    c_b = eng.matmul(xb.t().contiguous(), Tensor((K, rows), st))  # B side: transposes on the engine stream
+    c_t = eng.matmul(Tensor((rows, K), s8), xb)  # batched tiled Q8_0: tiled copy + workspace
+    ys = eng.gemv_group([Tensor((rows, K), st)], xb[:, 0].contiguous())
+    side.synchronize()
+    assert seen and all(sid == side.cuda_stream for sid in seen)
+    ref4 = orc.gemm_f32_q4_nt(np.ascontiguousarray(x.T), w.raw, 8, rows, K)
+    ref8 = orc.gemm_f32_q8_nt(np.ascontiguousarray(x.T), q8.raw, 8, rows, K)
+    assert rel_err(c_b.cpu().numpy().reshape(-1), ref4.reshape(-1)) <= TOL
+    assert rel_err(c_t.cpu().numpy().T.reshape(-1), ref8.reshape(-1)) <= TOL
+    assert rel_err(ys[0].cpu().numpy(), ref4.reshape(8, rows)[0]) <= TOL
+    torch.cuda.synchronize()

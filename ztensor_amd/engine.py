@@ -53,6 +53,33 @@ def _p(t: torch.Tensor | None) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def _on_engine_stream(fn):
+    """Runs an engine method with the engine's stream as torch's current
+    stream, so every temporary it makes (clones, transposes, pads, outputs,
+    tiled copies, the workspace) is allocated and written in the same stream
+    order as the kernels that read it, and the caching allocator never hands
+    one of them to other work while a kernel on the engine stream still uses
+    it.  Inputs made on another stream must be ready before the call, and
+    outputs used on another stream must wait for the engine stream, as with
+    any stream-ordered library."""
+
+    def wrapped(self, *args, **kwargs):
+        with torch.cuda.stream(self.stream):
+            return fn(self, *args, **kwargs)
+
+    wrapped.__name__, wrapped.__doc__, wrapped.__wrapped__ = fn.__name__, fn.__doc__, fn  # type: ignore[attr-defined]
+    return wrapped
+
+
+def _tiled_cached(s: Any, key: tuple):
+    """The tiled device copy cached on a storage for `key`
+    (format tag, rows, K, source buffer address), or None."""
+    cached = getattr(s, "_gpu_tiled", None)
+    if cached is not None and cached[0] == key:
+        return cached[1:]
+    return None
+
+
 class ROCmEngine:
     def __init__(self, device: int = 0, stream: torch.cuda.Stream | None = None):
         if not torch.cuda.is_available():
@@ -145,6 +172,7 @@ class ROCmEngine:
         t = torch.from_numpy(np.ascontiguousarray(host).view(np.uint8).reshape(-1))
         return t.to(self.device, non_blocking=False)
 
+    @_on_engine_stream
     def upload_weights(self, storages: list[Any]) -> int:
         """Copies each quantized storage to the device once, in its GPU layout,
         and records the buffer with set_gpu_ptr (compute/gpu_engine.go:778-818).
@@ -196,6 +224,7 @@ class ROCmEngine:
 
     # ---------------------------------------------------------------- matmul
 
+    @_on_engine_stream
     def matmul(self, a: Tensor | torch.Tensor, b: Tensor | torch.Tensor) -> torch.Tensor:
         """C = A @ B where one operand is a quantized weight Tensor and the
         other an fp32 (or fp16, for the W4A16 formats) device tensor.
@@ -225,9 +254,10 @@ class ROCmEngine:
         """The tiled copy of uploaded W4A16 weights for batches of 4-16
         columns, built on the device on the first batched call and kept
         beside the row-major upload (which batch 1 reads)."""
-        cached = getattr(s, "_gpu_tiled", None)
-        if cached is not None and cached[0] == (rows, k):
-            return cached[1], cached[2]
+        key = ("w4a16t", rows, k, _p(s.gpu_ptr().tensor))
+        cached = _tiled_cached(s, key)
+        if cached is not None:
+            return cached
         nbytes = self.lib.zt_w4a16_tiled_bytes(rows, k)
         szbytes = self.lib.zt_w4a16_sz_bytes(rows, k, s.group_size)
         if nbytes < 0 or szbytes < 0:
@@ -236,22 +266,23 @@ class ROCmEngine:
         sz = torch.empty(szbytes // 4, dtype=torch.int32, device=self.device)
         zeros = _p(s._gpu_zeros) if s._gpu_zeros is not None else 0
         self.w4a16_tile(_p(s.gpu_ptr().tensor), _p(s._gpu_scales), zeros, rows, k, s.group_size, _p(wt), _p(sz))
-        s._gpu_tiled = ((rows, k), wt, sz)  # type: ignore[attr-defined]
+        s._gpu_tiled = (key, wt, sz)  # type: ignore[attr-defined]
         return wt, sz
 
     def _iq4nl_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int) -> tuple[torch.Tensor, torch.Tensor]:
         """The tiled copy of uploaded IQ4_NL weights for batches of 4-16
         fp16 columns, built on the device on first use."""
-        cached = getattr(s, "_gpu_tiled", None)
-        if cached is not None and cached[0] == (rows, k):
-            return cached[1], cached[2]
+        key = ("iq4nlt", rows, k, _p(buf.tensor))
+        cached = _tiled_cached(s, key)
+        if cached is not None:
+            return cached
         nbytes, sbytes = self.lib.zt_iq4nl_tiled_bytes(rows, k), self.lib.zt_iq4nl_tiled_scale_bytes(rows, k)
         if nbytes < 0 or sbytes < 0:
             raise ValueError(f"IQ4_NL tiled layout: unsupported shape [{rows}, {k}]")
         wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         st = torch.empty(sbytes, dtype=torch.uint8, device=self.device)
         self.lib.call("zt_iq4nl_tile", _p(buf.tensor), rows, k, buf.data_offset, _p(wt), _p(st), self._s)
-        s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
+        s._gpu_tiled = (key, wt, st)  # type: ignore[attr-defined]
         return wt, st
 
     def _block_tiled(self, s: Any, buf: GPUBuffer, rows: int, k: int, fmt: str) -> tuple[torch.Tensor, torch.Tensor]:
@@ -259,9 +290,10 @@ class ROCmEngine:
         batches of 4-16 fp32 columns, built on the device from the separated
         upload on the first batched call and kept beside it (batch 1 reads
         the separated layout)."""
-        cached = getattr(s, "_gpu_tiled", None)
-        if cached is not None and cached[0] == (rows, k):
-            return cached[1], cached[2]
+        key = (fmt + "t", rows, k, _p(buf.tensor))
+        cached = _tiled_cached(s, key)
+        if cached is not None:
+            return cached
         size_fmt = "q8" if fmt == "q8gguf" else fmt  # GGUF Q8_0 tiles into the Q8_0 layout
         nbytes = getattr(self.lib, f"zt_{size_fmt}_tiled_bytes")(rows, k)
         sbytes = getattr(self.lib, f"zt_{size_fmt}_tiled_scale_bytes")(rows, k)
@@ -270,7 +302,7 @@ class ROCmEngine:
         wt = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         st = torch.empty(sbytes, dtype=torch.uint8, device=self.device)
         self.lib.call(f"zt_{fmt}_tile", _p(buf.tensor), rows, k, buf.data_offset, _p(wt), _p(st), self._s)
-        s._gpu_tiled = ((rows, k), wt, st)  # type: ignore[attr-defined]
+        s._gpu_tiled = (key, wt, st)  # type: ignore[attr-defined]
         return wt, st
 
     @staticmethod
@@ -299,9 +331,10 @@ class ROCmEngine:
         f = "q4k" / "q5k": data in the Q4_0 tile format, the super-block
         headers and, for Q5_K, the fifth bits; f = "q6k": the 6-bit values in
         the Q8_0 tile format and the per-16 scales d * sc."""
-        cached = getattr(s, "_gpu_tiled", None)
-        if cached is not None and cached[0] == (rows, k):
-            return cached[1:]
+        key = (f + "t", rows, k, _p(buf.tensor))
+        cached = _tiled_cached(s, key)
+        if cached is not None:
+            return cached
         second = "tiled_scale_bytes" if f == "q6k" else "tiled_header_bytes"
         sizes = [getattr(self.lib, f"zt_{f}_tiled_bytes")(rows, k), getattr(self.lib, f"zt_{f}_{second}")(rows, k)]
         if f == "q5k":
@@ -310,7 +343,7 @@ class ROCmEngine:
             raise ValueError(f"{f} tiled layout: unsupported shape [{rows}, {k}]")
         bufs = tuple(torch.empty(n, dtype=torch.uint8, device=self.device) for n in sizes)
         self.lib.call(f"zt_{f}_tile", _p(buf.tensor), rows, k, *(_p(b) for b in bufs), self._s)
-        s._gpu_tiled = ((rows, k),) + bufs  # type: ignore[attr-defined]
+        s._gpu_tiled = (key,) + bufs  # type: ignore[attr-defined]
         return bufs
 
     def _kq_tiled_gemm(self, s: Any, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int, c: torch.Tensor,
@@ -323,16 +356,17 @@ class ROCmEngine:
         """The tiled copy of uploaded Q5_0 weights (nibbles and scales in the
         Q4_0 tiled layout, plus the fifth bits) for batches of 4-16 fp32
         columns, built on the device on the first batched call."""
-        cached = getattr(s, "_gpu_tiled", None)
-        if cached is not None and cached[0] == (rows, k):
-            return cached[1], cached[2], cached[3]
+        key = ("q5_0t", rows, k, _p(buf.tensor))
+        cached = _tiled_cached(s, key)
+        if cached is not None:
+            return cached
         sizes = [self.lib.zt_q5_0_tiled_bytes(rows, k), self.lib.zt_q5_0_tiled_scale_bytes(rows, k),
                  self.lib.zt_q5_0_tiled_qh_bytes(rows, k)]
         if min(sizes) < 0:
             raise ValueError(f"Q5_0 tiled layout: unsupported shape [{rows}, {k}]")
         wt, st, ht = (torch.empty(n, dtype=torch.uint8, device=self.device) for n in sizes)
         self.lib.call("zt_q5_0_tile", _p(buf.tensor), rows, k, qh, qs, _p(wt), _p(st), _p(ht), self._s)
-        s._gpu_tiled = ((rows, k), wt, st, ht)  # type: ignore[attr-defined]
+        s._gpu_tiled = (key, wt, st, ht)  # type: ignore[attr-defined]
         return wt, st, ht
 
     def _q5_0_tiled_gemm(self, s: Any, buf: GPUBuffer, rows: int, k: int, x: torch.Tensor, n: int, c: torch.Tensor,
@@ -514,6 +548,7 @@ class ROCmEngine:
             raise TypeError(f"GGML type {q.name} has no quantized GEMV on this path")
         return c
 
+    @_on_engine_stream
     def matmul_w4a16(self, a: Tensor, b: Tensor) -> torch.Tensor:
         """W4A16MatMuler.MatMulW4A16 (compute/w4a16.go:137-143): one operand
         holds 4-bit weights (Q4_0, GPTQ bits=4 or AWQ), the other a
@@ -526,6 +561,7 @@ class ROCmEngine:
             return self.matmul(w, x.reshape(act.shape))
         return self.matmul(x.reshape(act.shape), w)
 
+    @_on_engine_stream
     def gemv_group(self, weights: list[Tensor], x: torch.Tensor) -> list[torch.Tensor]:
         """y_i = W_i @ x for weight Tensors that read the same fp32 activation
         vector x[K] (a decode layer's q/k/v, or gate/up).  Q4_0 weights run in
@@ -552,6 +588,7 @@ class ROCmEngine:
 
     # ---------------------------------------------------------------- ternary
 
+    @_on_engine_stream
     def ternary_gemv(self, weights: TernaryStorage, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
         """TernaryGEMVGPU (compute/ternary_gemv_gpu.go:18-91): host x in, host
         y out.  The reference repacks and uploads the weights on every call
