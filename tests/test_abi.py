@@ -288,3 +288,21 @@ def test_q4t_noalloc_rejects_oversized_and_bad_calls_without_launching():
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 28672, 8192, 8, None) == _lib.HIP_ERROR_OUT_OF_MEMORY
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 64, 96, 8, None) == _lib.HIP_ERROR_INVALID_VALUE  # K % 128
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 64, 128, 5, None) == _lib.HIP_ERROR_INVALID_VALUE  # N
+
+
+def test_ccall_style_calls_through_all_uintptr_signature(tmp_path):
+    """tests/ccall_abi.c, compiled here with gcc, dlopens libzt_hip.so and
+    calls entry points through a 20-argument all-uintptr_t function pointer,
+    as the reference's Ccall does; only validation paths, no kernel."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    exe = tmp_path / "ccall_abi"
+    subprocess.run([cc, "-O1", "-std=c11", "-Wall", "-o", str(exe), str(ROOT / "tests" / "ccall_abi.c"), "-ldl"],
+                   check=True)
+    r = subprocess.run([str(exe), str(_lib.LIB_PATH)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all checks passed" in r.stdout
