@@ -145,6 +145,41 @@ long zt_gemm_iq4nlt_workspace_bytes(int M, int K, int N);
 int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t* B, float* C, int M, int K, int N,
                        void* workspace, long workspace_bytes, zt_stream_t stream);
 
+/* ---- Dequantizer registry formats ---------------------------------------- */
+
+/* Device twins of the reference's registered Dequantizers
+ * (tensor/quant_registry.go:10-73, 231-240; GetQuantType(name).Dequantize(
+ * src, dst)): src holds the same bytes the registered Dequantize takes, in
+ * device memory; out receives nelem fp32 values, bit-exact with the
+ * reference's.  Names and entry points:
+ *   "Q4_0"     zt_dequant_q4raw_f32  (Q4Storage.RawBytes, 18-byte blocks;
+ *                                     tensor/quantized.go:96-114)
+ *   "Q8_0"     zt_dequant_q8_f32     (36-byte blocks, above)
+ *   "Q4_K" / "Q5_K" / "Q6_K" / "Q5_0"
+ *              zt_dequant_q4k/q5k/q6k/q5_0_f32 (raw blocks, below)
+ *   "AWQ_4"    zt_awq4_wire_header on the host copy, then zt_dequant_awq4_f32
+ *              (tensor/quantized_awq.go:242-308)
+ *   "FP8_E4M3" / "FP8_E5M2"
+ *              zt_dequant_fp8_f32 (4-byte LE fp32 scale, then one byte per
+ *              element; tensor/quant_registry.go:190-229, decoders
+ *              tensor/fp8_storage.go:229-250, 304-331)
+ * A source shorter than the format needs, a misaligned source (2 bytes for
+ * Q4_0, 4 for AWQ_4 and FP8) or a null pointer -> InvalidValue, as the
+ * reference's errShortData (tensor/quant_registry.go:242-245).  nelem == 0
+ * is a no-op success. */
+int zt_dequant_q4raw_f32(const void* src, long src_bytes, float* out, long nelem, zt_stream_t stream);
+/* Host: checks the AWQ_4 wire header against nelem as the reference's
+ * Dequantize and NewAWQStorageFromRaw do (numElements == nelem, groupSize > 0,
+ * nGroups == ceil(nelem / groupSize), enough bytes for the (scale, zero)
+ * pairs and every group's packed words) and returns groupSize and nGroups;
+ * InvalidValue otherwise. */
+int zt_awq4_wire_header(const void* wire, long wire_bytes, long nelem, int* group_size, int* ngroups);
+int zt_dequant_awq4_f32(const void* wire, long wire_bytes, float* out, long nelem, int group_size, int ngroups,
+                        zt_stream_t stream);
+/* e5m2: 0 = FP8_E4M3 (no NaN or infinity: exponent 15 is an ordinary
+ * binade, as the reference decodes it), 1 = FP8_E5M2. */
+int zt_dequant_fp8_f32(const void* wire, long wire_bytes, float* out, long nelem, int e5m2, zt_stream_t stream);
+
 /* ---- Q8_0 -------------------------------------------------------------- */
 
 /* Replaces gemm_q8_f32 (internal/cuda/kernels/gemm_q8.cu:156-182) behind

@@ -52,6 +52,8 @@ _SIG = {
     "orc_gemm_f32_q5_0_nt": (None, [L, L, L, P, P, P, P, P]),
     "orc_gguf_q8_0_dequant": (None, [P, L, P]),
     "orc_gemm_f32_mmap_nt": (I, [I, L, L, L, P, P, P, I, P]),
+    "orc_awq4_wire_dequant": (I, [P, L, P, L]),
+    "orc_fp8_dequant": (I, [P, L, P, L, I]),
 }
 
 _lib = None
@@ -153,6 +155,23 @@ def awq_dequant(words, scales, zeros, nelem: int, group: int) -> np.ndarray:
     out = np.empty(nelem, np.float32)
     lib().orc_awq_dequant(_p(words), _p(scales), _p(zeros), nelem, group, _p(out))
     return out
+
+
+def awq4_wire_dequant(src, n: int):
+    """(status, values): the registry's AWQ_4 Dequantize on wire bytes;
+    status 0 ok, 1 short data, 2 numElements mismatch, 3 bad group fields."""
+    src = np.ascontiguousarray(src, np.uint8)
+    out = np.zeros(max(n, 1), np.float32)
+    rc = lib().orc_awq4_wire_dequant(_p(src), src.size, _p(out), n)
+    return rc, out[:n]
+
+
+def fp8_dequant(src, n: int, e5m2: bool):
+    """(status, values): the registry's FP8_E4M3 / FP8_E5M2 Dequantize."""
+    src = np.ascontiguousarray(src, np.uint8)
+    out = np.zeros(max(n, 1), np.float32)
+    rc = lib().orc_fp8_dequant(_p(src), src.size, _p(out), n, int(bool(e5m2)))
+    return rc, out[:n]
 
 
 def sgemm_simd(a: np.ndarray, b: np.ndarray, m: int, n: int, k: int) -> np.ndarray:

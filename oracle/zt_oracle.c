@@ -369,6 +369,89 @@ EXPORT void orc_awq_dequant(const uint32_t* words, const uint16_t* scales, const
     }
 }
 
+/* tensor/quantized_awq.go:245-305 awqDequantizer.Dequantize (the registry's
+ * "AWQ_4" wire format) with NewAWQStorageFromRaw's checks (:187-214):
+ * header numElements, groupSize, nGroups (uint32 LE), nGroups (fp16 scale,
+ * fp16 zero) pairs, then every group's packed words, each group starting on
+ * a fresh word.  Returns 0, or 1 for short data, 2 for a numElements
+ * mismatch, 3 for a bad groupSize / nGroups or a group count other than
+ * ceil(n / groupSize).  n == 0 returns 0 without reading src. */
+EXPORT int orc_awq4_wire_dequant(const uint8_t* src, int64_t src_len, float* dst, int64_t n) {
+    if (n == 0) return 0;
+    if (src_len < 12) return 1;
+    uint32_t hdr[3];
+    memcpy(hdr, src, 12);
+    const int64_t num = (int64_t)hdr[0], group = (int64_t)(int32_t)hdr[1], ngroups = (int64_t)(int32_t)hdr[2];
+    if (num != n) return 2;
+    if (group <= 0 || ngroups <= 0) return 3;
+    const int64_t meta = 12 + ngroups * 4;
+    if (src_len < meta) return 1;
+    int64_t total = 0;
+    for (int64_t gi = 0; gi < ngroups; gi++) {
+        int64_t count = group, remaining = num - gi * group;
+        if (remaining < group) count = remaining;
+        total += (count + 7) / 8;
+    }
+    if (src_len - meta < total * 4) return 1;
+    if (ngroups != (num + group - 1) / group) return 3;
+    uint16_t* scales = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)ngroups);
+    uint16_t* zeros = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)ngroups);
+    uint32_t* words = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(total > 0 ? total : 1));
+    for (int64_t gi = 0; gi < ngroups; gi++) {
+        memcpy(&scales[gi], src + 12 + gi * 4, 2);
+        memcpy(&zeros[gi], src + 12 + gi * 4 + 2, 2);
+    }
+    memcpy(words, src + meta, (size_t)total * 4);
+    orc_awq_dequant(words, scales, zeros, num, group, dst);
+    free(scales);
+    free(zeros);
+    free(words);
+    return 0;
+}
+
+/* tensor/fp8_storage.go:229-250 decodeE4M3 (no NaN or infinity: exponent 15
+ * is an ordinary binade) and :304-331 decodeE5M2, then the registry's
+ * "FP8_E4M3" / "FP8_E5M2" Dequantize (tensor/quant_registry.go:190-229):
+ * src = 4-byte LE fp32 scale, then one byte per element;
+ * dst[i] = decode(src[4+i]) * scale.  Returns 1 for short data. */
+static float orc_decode_e4m3(uint8_t b) {
+    uint32_t sign = (b >> 7) & 1u, exp = (b >> 3) & 0xfu, mant = b & 7u;
+    if (exp == 0 && mant == 0) return sign ? -0.0f : 0.0f;
+    if (exp == 0) {
+        float v = (float)mant / 8.0f * (float)pow(2.0, 1 - 7);
+        return sign ? -v : v;
+    }
+    uint32_t bits = (sign << 31) | ((exp - 7 + 127) << 23) | (mant << 20);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static float orc_decode_e5m2(uint8_t b) {
+    uint32_t sign = (b >> 7) & 1u, exp = (b >> 2) & 0x1fu, mant = b & 3u;
+    if (exp == 0 && mant == 0) return sign ? -0.0f : 0.0f;
+    if (exp == 31) {
+        if (mant == 0) return sign ? -INFINITY : INFINITY;
+        return NAN;
+    }
+    if (exp == 0) {
+        float v = (float)mant / 4.0f * (float)pow(2.0, 1 - 15);
+        return sign ? -v : v;
+    }
+    uint32_t bits = (sign << 31) | ((exp - 15 + 127) << 23) | (mant << 21);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+EXPORT int orc_fp8_dequant(const uint8_t* src, int64_t src_len, float* dst, int64_t n, int e5m2) {
+    if (src_len < 4 + n) return 1;
+    float scale;
+    memcpy(&scale, src, 4);
+    for (int64_t i = 0; i < n; i++) dst[i] = (e5m2 ? orc_decode_e5m2(src[4 + i]) : orc_decode_e4m3(src[4 + i])) * scale;
+    return 0;
+}
+
 /* ----------------------------------------- dequant + SgemmSimd matmuls */
 
 /* tensor/fp16_storage.go:53-63 Float16Storage.Slice. */

@@ -27,7 +27,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     for name in declared:
         assert hasattr(lib.cdll, name)
-    assert lib.zt_abi_version() == 101
+    assert lib.zt_abi_version() == 102
 
 
 def test_header_arity_matches_binding():

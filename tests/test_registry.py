@@ -1,0 +1,132 @@
+"""The Dequantizer registry (tensor/quant_registry.go:10-73) and the oracle's
+restatement of its wire formats, on the CPU.
+
+Pins:
+  * names, BlockSize and BitsPerWeight of every built-in format, as the
+    reference's own tests assert them (tensor/quant_registry_test.go:169-229,
+    tensor/quantized_awq_test.go:293-304), and RegisterQuantType's errors;
+  * orc_fp8_dequant: all 256 codes of both formats against the exact value
+    of the bit fields, (-1)^s 2^(e-bias) (1 + m/2^M) or the subnormal
+    (-1)^s 2^(1-bias) m/2^M, computed with Python fractions; E4M3's exponent
+    15 is an ordinary binade (0x7F = 480), E5M2's exponent 31 is inf / NaN;
+  * orc_awq4_wire_dequant: equal to orc_awq_dequant (pinned by the AWQ known
+    vectors in test_oracle.py) on wire bytes from the independent packer in
+    ztensor_amd/synth.py, for group sizes that do and do not divide the
+    element count or 8, and the reference's error cases (short header, short
+    pairs, short data, numElements mismatch, bad groupSize / nGroups, a group
+    count other than ceil(n / groupSize)).
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from ztensor_amd import registry, synth
+
+
+def test_builtin_names_and_sizes_match_the_reference():
+    assert registry.list_quant_types() == sorted(
+        ["Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q5_0", "FP8_E4M3", "FP8_E5M2", "AWQ_4"])
+    want = {"Q4_0": (32, 4), "Q8_0": (32, 8), "Q4_K": (256, 4), "Q5_K": (256, 5), "Q6_K": (256, 6),
+            "Q5_0": (32, 5), "FP8_E4M3": (1, 8), "FP8_E5M2": (1, 8), "AWQ_4": (128, 4)}
+    for name, (bs, bits) in want.items():
+        d, ok = registry.get_quant_type(name)
+        assert ok and (d.block_size, d.bits_per_weight) == (bs, bits), name
+    assert registry.get_quant_type("NOPE") == (None, False)
+
+
+def test_register_quant_type_rejects_like_the_reference():
+    d, _ = registry.get_quant_type("Q4_0")
+    with pytest.raises(ValueError, match="empty name"):
+        registry.register_quant_type("", d)
+    with pytest.raises(ValueError, match="nil Dequantizer"):
+        registry.register_quant_type("X_TEST", None)
+    with pytest.raises(ValueError, match="twice for Q4_0"):
+        registry.register_quant_type("Q4_0", d)
+
+
+def exact_fp8(code: int, e5m2: bool) -> float:
+    s, rest = code >> 7, code & 0x7F
+    eb, mb, bias = (5, 2, 15) if e5m2 else (4, 3, 7)
+    e, m = rest >> mb, rest & ((1 << mb) - 1)
+    sign = -1 if s else 1
+    if e5m2 and e == 31:
+        return float("nan") if m else sign * float("inf")
+    if e == 0:
+        v = Fraction(m, 1 << mb) * Fraction(2) ** (1 - bias)
+    else:
+        v = (1 + Fraction(m, 1 << mb)) * Fraction(2) ** (e - bias)
+    return float(sign * v) if v else (-0.0 if s else 0.0)
+
+
+@pytest.mark.parametrize("e5m2", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 0.0123, -3.5])
+def test_oracle_fp8_all_codes(orc, e5m2, scale):
+    codes = np.arange(256, dtype=np.uint8)
+    rc, got = orc.fp8_dequant(synth.fp8_wire(codes, scale), 256, e5m2)
+    assert rc == 0
+    want = np.array([exact_fp8(int(c), e5m2) for c in codes], np.float64)
+    want32 = (want.astype(np.float32) * np.float32(scale)).astype(np.float32)
+    nan = np.isnan(want32)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want32[~nan].view(np.uint32))
+    if not e5m2 and scale == 1.0:
+        assert got[0x7F] == 480.0 and got[0xFF] == -480.0 and got[0x01] == 2.0 ** -9
+
+
+def test_oracle_fp8_short_data(orc):
+    assert orc.fp8_dequant(np.zeros(4 + 7, np.uint8), 8, False)[0] == 1
+
+
+@pytest.mark.parametrize("n,group", [(1000, 128), (999, 128), (300, 36), (37, 5), (4096, 64), (1, 128)])
+def test_oracle_awq4_wire_equals_flat_groups(orc, n, group):
+    wire, q, s, z = synth.awq4_wire(n, group, 40 + n % 7)
+    rc, got = orc.awq4_wire_dequant(wire, n)
+    assert rc == 0
+    # the same codes as flat groups of packed words (orc_awq_dequant's input)
+    words = []
+    for gi in range(-(-n // group)):
+        c = q[gi * group:(gi + 1) * group]
+        w = np.zeros(-(-c.size // 8), np.uint64)
+        for j in range(8):
+            w[:c[j::8].size] |= c[j::8].astype(np.uint64) << np.uint64(4 * j)
+        words.append(w.astype(np.uint32))
+    ref = orc.awq_dequant(np.concatenate(words), s, z, n, group)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_oracle_awq4_wire_errors(orc):
+    n, group = 300, 128
+    wire, _, _, _ = synth.awq4_wire(n, group, 41)
+    assert orc.awq4_wire_dequant(wire[:11], n)[0] == 1          # header short
+    assert orc.awq4_wire_dequant(wire[:12 + 4 * 2], n)[0] == 1  # pairs short
+    assert orc.awq4_wire_dequant(wire[:-1], n)[0] == 1          # data short
+    assert orc.awq4_wire_dequant(wire, n + 1)[0] == 2           # numElements mismatch
+    bad = wire.copy()
+    bad[4:8] = np.array([0], "<u4").view(np.uint8)
+    assert orc.awq4_wire_dequant(bad, n)[0] == 3                # groupSize 0
+    bad = wire.copy()
+    bad[8:12] = np.array([2], "<u4").view(np.uint8)
+    assert orc.awq4_wire_dequant(bad, n)[0] == 3                # nGroups != ceil(n / group)
+    assert orc.awq4_wire_dequant(np.zeros(0, np.uint8), 0)[0] == 0  # n == 0 reads nothing
+
+
+def test_awq4_wire_header_host_check_agrees_with_the_oracle(orc):
+    import ctypes as C
+
+    from ztensor_amd import _lib
+
+    lib = _lib.load()
+    n, group = 300, 128
+    wire, _, _, _ = synth.awq4_wire(n, group, 42)
+    cases = [(wire, n), (wire[:11], n), (wire[:-1], n), (wire, n + 1)]
+    bad = wire.copy()
+    bad[8:12] = np.array([2], "<u4").view(np.uint8)
+    cases.append((bad, n))
+    for w, nn in cases:
+        g, ng = C.c_int(-1), C.c_int(-1)
+        w = np.ascontiguousarray(w)
+        rc = lib.zt_awq4_wire_header(w.ctypes.data, w.size, nn, C.byref(g), C.byref(ng))
+        assert (rc == 0) == (orc.awq4_wire_dequant(w, nn)[0] == 0)
+        if rc == 0:
+            assert (g.value, ng.value) == (group, 3)

@@ -112,6 +112,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q5_0_gpu_qs_offset": (L, [L]),
     "zt_q5_0_gpu_bytes": (L, [L]),
     "zt_q5_0_raw_to_gpu": (None, [P, L, P]),
+    "zt_dequant_q4raw_f32": (I, [P, L, P, L, P]),
+    "zt_awq4_wire_header": (I, [P, L, L, P, P]),
+    "zt_dequant_awq4_f32": (I, [P, L, P, L, I, I, P]),
+    "zt_dequant_fp8_f32": (I, [P, L, P, L, I, P]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1

@@ -9,7 +9,33 @@
 
 extern "C" {
 
-int zt_abi_version(void) { return 101; }
+int zt_abi_version(void) { return 102; }
+
+// The header checks of the registry's AWQ_4 Dequantize
+// (tensor/quantized_awq.go:245-297) and NewAWQStorageFromRaw's group count
+// (:187-199), on the host copy of the wire bytes.
+int zt_awq4_wire_header(const void* wire, long wire_bytes, long nelem, int* group_size, int* ngroups) {
+    if (nelem < 0 || wire_bytes < 0 || group_size == nullptr || ngroups == nullptr) return 1;
+    *group_size = 0;
+    *ngroups = 0;
+    if (nelem == 0) return 0;  // nothing to decode, the header is not read
+    if (wire == nullptr || wire_bytes < 12) return 1;
+    const unsigned char* b = static_cast<const unsigned char*>(wire);
+    auto u32 = [b](int o) {
+        return (unsigned long)b[o] | ((unsigned long)b[o + 1] << 8) | ((unsigned long)b[o + 2] << 16) |
+               ((unsigned long)b[o + 3] << 24);
+    };
+    const long n = (long)u32(0), g = (long)(int)u32(4), ng = (long)(int)u32(8);
+    if (n != nelem || g <= 0 || ng <= 0) return 1;
+    if (ng != (n + g - 1) / g) return 1;
+    if (wire_bytes < 12 + 4 * ng) return 1;
+    const long last = n - (ng - 1) * g;
+    const long words = (ng - 1) * ((g + 7) / 8) + (last + 7) / 8;
+    if (wire_bytes - 12 - 4 * ng < 4 * words) return 1;
+    *group_size = (int)g;
+    *ngroups = (int)ng;
+    return 0;
+}
 
 long zt_q4_gpu_data_offset(long nblk) { return (nblk * 2 + 15) & ~15L; }
 

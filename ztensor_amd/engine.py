@@ -586,6 +586,27 @@ class ROCmEngine:
             self.lib.call("zt_gemm_q4_group_f32", descs, len(part), _p(x), k, self._s)
         return outs
 
+    @_on_engine_stream
+    def dequantize(self, name: str, src: np.ndarray, n: int) -> torch.Tensor:
+        """GetQuantType(name).Dequantize(src, dst) with dst on the device
+        (tensor/quant_registry.go:10-73): src holds the registered format's
+        bytes on the host; they are copied to the device once and decoded
+        there into n fp32 values, bit for bit with the reference."""
+        from . import registry
+
+        d, ok = registry.get_quant_type(name)
+        if not ok:
+            raise ValueError(f"tensor: quantization type {name!r} is not registered")
+        src = np.ascontiguousarray(src, np.uint8).reshape(-1)
+        dst = torch.empty(n, dtype=torch.float32, device=self.device)
+        if n == 0:
+            return dst
+        sd = self._to_dev(np.concatenate([src, np.zeros(-src.size % 16, np.uint8)]) if src.size % 16 else src)
+        rc = d.run(self.lib, src, sd, dst, self._s)
+        if rc != 0:
+            raise _lib.ZTError(f"dequantize {name}", rc)
+        return dst
+
     # ---------------------------------------------------------------- ternary
 
     @_on_engine_stream

@@ -361,3 +361,45 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
     if fmt == "ternary_i8":
         return rows * ((K + 3) // 4) + K * N + 4 * rows * N + 8
     raise ValueError(fmt)
+
+
+# ---- the Dequantizer registry's byte formats (tensor/quant_registry.go)
+
+
+def pack_awq4_wire(q: np.ndarray, scales: np.ndarray, zeros: np.ndarray, group: int) -> np.ndarray:
+    """The registry's AWQ_4 bytes (tensor/quantized_awq.go:242-305) for the
+    flat codes q (uint4 values, any length) with fp16 scale / zero bits per
+    group: header (numElements, groupSize, nGroups as uint32 LE), the
+    (scale, zero) pairs, then each group's codes as little-endian uint32
+    words of 8 nibbles, every group starting on a fresh word."""
+    q = np.asarray(q, np.uint8).reshape(-1)
+    n = q.size
+    ng = -(-n // group)
+    parts = [np.array([n, group, ng], "<u4").view(np.uint8),
+             np.stack([np.asarray(scales, "<u2"), np.asarray(zeros, "<u2")], axis=1).reshape(-1).view(np.uint8)]
+    for gi in range(ng):
+        c = q[gi * group:(gi + 1) * group]
+        words = np.zeros(-(-c.size // 8), np.uint64)
+        for j in range(8):
+            sel = c[j::8].astype(np.uint64)
+            words[:sel.size] |= sel << np.uint64(4 * j)
+        parts.append(words.astype("<u4").view(np.uint8))
+    return np.concatenate(parts)
+
+
+def awq4_wire(n: int, group: int, seed: int) -> tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
+    """(wire bytes, codes, scale bits, zero bits) of n seeded AWQ weights:
+    codes U[0,15], fp16 scales |N(0,1)|*0.02, fp16 zeros U[0,15) (not only
+    integers, as QuantizeAWQ's zero = -min/scale is not)."""
+    g = rng(seed)
+    ng = -(-n // group)
+    q = g.integers(0, 16, size=n, dtype=np.uint8)
+    s = f16_bits(np.abs(g.standard_normal(ng, dtype=np.float32)) * np.float32(0.02))
+    z = f16_bits(g.random(ng, dtype=np.float32) * np.float32(15.0))
+    return pack_awq4_wire(q, s, z, group), q, s, z
+
+
+def fp8_wire(codes: np.ndarray, scale: float) -> np.ndarray:
+    """The registry's FP8_E4M3 / FP8_E5M2 bytes: 4-byte LE fp32 scale, then
+    one code byte per element (tensor/quant_registry.go:190-229)."""
+    return np.concatenate([np.array([scale], "<f4").view(np.uint8), np.asarray(codes, np.uint8)])
