@@ -246,6 +246,16 @@ int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_
  * and AWQStorage.Dequantize (tensor/quantized_awq.go:118-136). */
 int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,
                       int group_size, zt_stream_t stream);
+/* DequantW4ToFP16 (compute/w4a16.go:170-175: Slice, then
+ * NewFloat16StorageFromF32) on the device, "fp16 weights for HGEMM": the
+ * fp32 values of zt_dequant_w4_f32 / zt_dequant_q4_f32, each rounded to
+ * fp16 to nearest, ties to even (fp16 bits out).  Values beyond the fp16
+ * range become +-inf.  The reference's fp32 -> fp16 rounding lives in
+ * github.com/zerfoo/float16 v0.2.0, which no reference test pins; IEEE
+ * round-to-nearest-even is assumed. */
+int zt_dequant_w4_f16(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, uint16_t* out, long nelem,
+                      int group_size, zt_stream_t stream);
+int zt_dequant_q4_f16(const void* A_q4, uint16_t* out, long nelem, int data_offset, zt_stream_t stream);
 
 /* Tiled upload layout for the small-batch path of the same MatMulW4A16
  * (compute/w4a16.go:137-143).  The reference uploads W4A16 weights as

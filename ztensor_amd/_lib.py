@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_q8gguf_raw_to_gpu": (None, [P, L, P]),
     "zt_gemm_w4a16_f32": (I, [P, P, P, P, P, I, I, I, I, P]),
     "zt_dequant_w4_f32": (I, [P, P, P, P, L, I, P]),
+    "zt_dequant_w4_f16": (I, [P, P, P, P, L, I, P]),
+    "zt_dequant_q4_f16": (I, [P, P, L, I, P]),
     "zt_w4a16_pack_szr": (I, [P, P, I, I, I, P, P]),
     "zt_gemv_w4a16sz_f32": (I, [P, P, P, P, I, I, I, P]),
     "zt_w4a16_tiled_bytes": (L, [I, I]),

@@ -30,6 +30,15 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// A dequantized value as stored: fp32 as is, or fp16 bits rounded to
+// nearest, ties to even (v_cvt_f16_f32 in the default rounding mode).
+template <class OutT>
+__device__ __forceinline__ OutT out_cvt(float v);
+template <>
+__device__ __forceinline__ float out_cvt<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ uint16_t out_cvt<uint16_t>(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
 // 128-bit streaming load of weight data that is read exactly once: the
 // nontemporal hint keeps it from evicting the reused activations.
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {

@@ -732,9 +732,9 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
 
 // ------------------------------------------------------------ dequantize
 
-template <Fmt F>
+template <Fmt F, class OutT>
 __global__ void dequant_blk18_kernel(const uint16_t* __restrict__ scales, const uint4* __restrict__ data,
-                                     float* __restrict__ out, long nelem) {
+                                     OutT* __restrict__ out, long nelem) {
     const long blk = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long nblk = (nelem + 31) / 32;
     if (blk >= nblk) return;
@@ -753,24 +753,24 @@ __global__ void dequant_blk18_kernel(const uint16_t* __restrict__ scales, const 
             v[2 * i + 1] = d * kIQ4NLTable[byte >> 4];
         }
     }
-    float* o = out + blk * 32;
+    OutT* o = out + blk * 32;
     const long rem = nelem - blk * 32;
     if (rem >= 32) {
 #pragma unroll
-        for (int i = 0; i < 32; i++) o[i] = v[i];
+        for (int i = 0; i < 32; i++) o[i] = out_cvt<OutT>(v[i]);
     } else {
-        for (int i = 0; i < rem; i++) o[i] = v[i];
+        for (int i = 0; i < rem; i++) o[i] = out_cvt<OutT>(v[i]);
     }
 }
 
-template <Fmt F>
-static int dequant_blk18(const void* A, float* out, long nelem, int data_offset, hipStream_t st) {
+template <Fmt F, class OutT = float>
+static int dequant_blk18(const void* A, OutT* out, long nelem, int data_offset, hipStream_t st) {
     if (nelem < 0 || data_offset < 0) return (int)hipErrorInvalidValue;
     if (nelem == 0) return (int)hipSuccess;
     const uint8_t* base = static_cast<const uint8_t*>(A);
     if (((uintptr_t)base & 1) || ((uintptr_t)(base + data_offset) & 15)) return (int)hipErrorInvalidValue;
     const long nblk = (nelem + 31) / 32;
-    dequant_blk18_kernel<F><<<ceil_div(nblk, 256), 256, 0, st>>>(
+    dequant_blk18_kernel<F, OutT><<<ceil_div(nblk, 256), 256, 0, st>>>(
         reinterpret_cast<const uint16_t*>(base), reinterpret_cast<const uint4*>(base + data_offset), out, nelem);
     return (int)hipGetLastError();
 }
@@ -868,6 +868,10 @@ ZT_EXPORT int zt_gemm_iq4nl_f16(const void* A_iq4, const uint16_t* B, float* C, 
 
 ZT_EXPORT int zt_dequant_q4_f32(const void* A_q4, float* out, long nelem, int data_offset, hipStream_t stream) {
     return dequant_blk18<Fmt::Q4_0>(A_q4, out, nelem, data_offset, stream);
+}
+
+ZT_EXPORT int zt_dequant_q4_f16(const void* A_q4, uint16_t* out, long nelem, int data_offset, hipStream_t stream) {
+    return dequant_blk18<Fmt::Q4_0, uint16_t>(A_q4, out, nelem, data_offset, stream);
 }
 
 ZT_EXPORT int zt_dequant_iq4nl_f32(const void* A_iq4, float* out, long nelem, int data_offset,

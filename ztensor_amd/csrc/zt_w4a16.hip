@@ -476,8 +476,12 @@ static size_t w4_mfma_lds_bytes(int N) {
 // ------------------------------------------------------------ dequantize
 
 // One thread per 32-weight chunk; bit-exact with GPTQStorage.Dequantize.
+// OutT = uint16_t writes the fp32 value rounded to fp16 (round to nearest,
+// ties to even: v_cvt_f16_f32 in the default mode), DequantW4ToFP16's
+// Slice-then-FromFloat32 (compute/w4a16.go:170-175).
+template <class OutT>
 __global__ void w4_dequant_kernel(const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
-                                  const uint16_t* __restrict__ zeros, float* __restrict__ out, long nchunk,
+                                  const uint16_t* __restrict__ zeros, OutT* __restrict__ out, long nchunk,
                                   int chunks_per_group) {
     const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= nchunk) return;
@@ -486,11 +490,11 @@ __global__ void w4_dequant_kernel(const uint4* __restrict__ packed, const uint16
     const float z = zeros ? h2f(zeros[g]) : 8.0f;
     const uint4 w = packed[c];
     const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-    float* o = out + c * 32;
+    OutT* o = out + c * 32;
 #pragma unroll
     for (int i = 0; i < 32; i++) {
         const int q = (int)((d[i / 8] >> (4 * (i % 8))) & 0xfu);
-        o[i] = ((float)q - z) * s;
+        o[i] = out_cvt<OutT>(((float)q - z) * s);
     }
 }
 
@@ -599,16 +603,28 @@ ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, con
     return (int)hipGetLastError();
 }
 
-ZT_EXPORT int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out,
-                                long nelem, int group_size, hipStream_t stream) {
+template <class OutT>
+static int dequant_w4(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, OutT* out, long nelem,
+                      int group_size, hipStream_t stream) {
     if (nelem < 0 || group_size <= 0 || group_size % 32 != 0 || nelem % group_size != 0)
         return (int)hipErrorInvalidValue;
     if (nelem == 0) return (int)hipSuccess;
-    if ((uintptr_t)W_packed & 15) return (int)hipErrorInvalidValue;
+    if (W_packed == nullptr || scales == nullptr || out == nullptr || ((uintptr_t)W_packed & 15))
+        return (int)hipErrorInvalidValue;
     const long nchunk = nelem / 32;
-    w4_dequant_kernel<<<ceil_div(nchunk, 256), 256, 0, stream>>>(static_cast<const uint4*>(W_packed), scales, zeros,
-                                                                  out, nchunk, group_size / 32);
+    w4_dequant_kernel<OutT><<<ceil_div(nchunk, 256), 256, 0, stream>>>(static_cast<const uint4*>(W_packed), scales,
+                                                                        zeros, out, nchunk, group_size / 32);
     return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out,
+                                long nelem, int group_size, hipStream_t stream) {
+    return dequant_w4<float>(W_packed, scales, zeros, out, nelem, group_size, stream);
+}
+
+ZT_EXPORT int zt_dequant_w4_f16(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, uint16_t* out,
+                                long nelem, int group_size, hipStream_t stream) {
+    return dequant_w4<uint16_t>(W_packed, scales, zeros, out, nelem, group_size, stream);
 }
 
 // ------------------------------------------------------------ tiled layout

@@ -587,6 +587,29 @@ class ROCmEngine:
         return outs
 
     @_on_engine_stream
+    def dequant_w4_to_fp16(self, w: Tensor) -> torch.Tensor:
+        """DequantW4ToFP16 (compute/w4a16.go:170-175) on the device: the
+        4-bit weights (Q4_0, GPTQ bits=4, AWQ) dequantized in fp32 exactly as
+        their Dequantize does, then rounded to fp16 (nearest, ties to even),
+        as an fp16 device tensor of the weight's shape - the operand of an
+        fp16 GEMM."""
+        s = w.storage
+        n = int(np.prod(w.shape))
+        self.upload_weights([s])
+        out = torch.empty(n, dtype=torch.float16, device=self.device)
+        buf = s.gpu_ptr()
+        if isinstance(s, Q4Storage):
+            self.lib.call("zt_dequant_q4_f16", _p(buf.tensor), _p(out), n, buf.data_offset, self._s)
+        elif isinstance(s, (GPTQStorage, AWQStorage)):
+            if isinstance(s, GPTQStorage) and s.bits != 4:
+                raise ValueError("DequantW4ToFP16 takes 4-bit weights")
+            self.lib.call("zt_dequant_w4_f16", _p(buf.tensor), _p(s._gpu_scales), _p(s._gpu_zeros), _p(out), n,
+                          s.group_size, self._s)
+        else:
+            raise TypeError(f"DequantW4ToFP16: {type(s).__name__} is not a 4-bit weight storage")
+        return out.reshape(w.shape)
+
+    @_on_engine_stream
     def dequantize(self, name: str, src: np.ndarray, n: int) -> torch.Tensor:
         """GetQuantType(name).Dequantize(src, dst) with dst on the device
         (tensor/quant_registry.go:10-73): src holds the registered format's
