@@ -290,24 +290,60 @@ __global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __r
 // run matrix i with the fixed-step body above; the matrices keep their own
 // separated uploads, so nothing is merged or re-laid out.  The descriptors
 // travel in the kernel arguments.
+// Up to three matrices in the standard RawBytesGPU layout (data offset
+// Q4GPUDataOffset(rows * K/32)): everything a workgroup needs before its
+// first weight load - the activations, K, the matrix bases and row counts
+// - is in the first 13 argument dwords, which arrive preloaded in SGPRs; the
+// matrix index and data offset are computed from them.  The output
+// pointers come later, by ordinary argument loads that the weight loads
+// hide.  (The general kernel below reads a 32-byte descriptor first: about
+// 0.5 us more a launch.)
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_q4_group3_kernel(const float* __restrict__ x, int kb, int n,
+                                                              const uint8_t* a0, const uint8_t* a1,
+                                                              const uint8_t* a2, int rows0, int rows1, int rows2,
+                                                              float* y0, float* y1, float* y2) {
+    __shared__ float red[16 * R];
+    const int b = blockIdx.x;
+    const int w1 = (rows0 + R - 1) / R, w2 = w1 + (rows1 + R - 1) / R;
+    const int m = (b >= w1 ? 1 : 0) + (n > 2 && b >= w2 ? 1 : 0);
+    const uint8_t* a = m == 0 ? a0 : m == 1 ? a1 : a2;
+    const int rows = m == 0 ? rows0 : m == 1 ? rows1 : rows2;
+    float* y = m == 0 ? y0 : m == 1 ? y1 : y2;
+    const long nblk = (long)rows * kb;
+    const uint32_t* dt = reinterpret_cast<const uint32_t*>(a + ((nblk * 2 + 15) & ~15L));
+    q4_steps_body<S, R>(reinterpret_cast<const uint16_t*>(a), dt, x, y, rows, kb,
+                        (b - (m == 0 ? 0 : m == 1 ? w1 : w2)) * R, red);
+}
+
+// The kernel's x and kb arguments, then the workgroup starts and the count,
+// arrive in preloaded SGPRs, so finding the matrix costs no memory access;
+// its 32-byte descriptor is then one scalar load.
+struct Q4GroupMat {
+    const uint16_t* sc;
+    const uint32_t* dt;
+    float* y;
+    int rows;
+    int wg0;
+};
+
 struct Q4GroupArgs {
-    const uint16_t* sc[ZT_GROUP_MAX];
-    const uint32_t* dt[ZT_GROUP_MAX];
-    float* y[ZT_GROUP_MAX];
-    int rows[ZT_GROUP_MAX];
-    int wg0[ZT_GROUP_MAX];
+    int wg0[ZT_GROUP_MAX];  // first workgroup of matrix i (wg0[0] = 0); unused entries past n
     int n;
+    int pad[3];
+    Q4GroupMat mat[ZT_GROUP_MAX];
 };
 
 template <int S, int R>
-__global__ void __launch_bounds__(1024) gemv_q4_group_kernel(const Q4GroupArgs g, const float* __restrict__ x,
-                                                             int kb) {
+__global__ void __launch_bounds__(1024) gemv_q4_group_kernel(const float* __restrict__ x, int kb,
+                                                             const Q4GroupArgs g) {
     __shared__ float red[16 * R];
     const int b = blockIdx.x;
     int m = 0;
 #pragma unroll
     for (int i = 1; i < ZT_GROUP_MAX; i++) m += (i < g.n && b >= g.wg0[i]) ? 1 : 0;
-    q4_steps_body<S, R>(g.sc[m], g.dt[m], x, g.y[m], g.rows[m], kb, (b - g.wg0[m]) * R, red);
+    const Q4GroupMat d = g.mat[m];
+    q4_steps_body<S, R>(d.sc, d.dt, x, d.y, d.rows, kb, (b - d.wg0) * R, red);
 }
 
 // IQ4_NL batch-1 GEMV with fp16 activations.  The quad mapping of
@@ -818,20 +854,58 @@ ZT_EXPORT int zt_gemm_q4_group_f32(const zt_q4_gemv_desc* descs, int n, const fl
     int nw = ceil_div(kb, 16 * S);
     if (nw > 12) nw = 16;
     const int R = pick_rows_per_wave(total, nw, 1, 2048);
+    bool std_layout = n <= 3;
+    for (int i = 0; i < n; i++)
+        std_layout = std_layout && descs[i].rows > 0 &&
+                     descs[i].data_offset == ((2L * descs[i].rows * kb + 15) & ~15L);
+    if (std_layout) {
+        const uint8_t* a[3] = {nullptr, nullptr, nullptr};
+        float* yv[3] = {nullptr, nullptr, nullptr};
+        int rw[3] = {0, 0, 0};
+        int wg3 = 0;
+        for (int i = 0; i < n; i++) {
+            a[i] = static_cast<const uint8_t*>(descs[i].A);
+            yv[i] = descs[i].y;
+            rw[i] = descs[i].rows;
+            wg3 += ceil_div(descs[i].rows, R);
+        }
+        const dim3 grid3(wg3), block3(nw * kWave);
+#define ZT_Q4G3(SS, RR) gemv_q4_group3_kernel<SS, RR><<<grid3, block3, 0, stream>>>(x, kb, n, a[0], a[1], a[2], \
+                                                                                     rw[0], rw[1], rw[2], yv[0], \
+                                                                                     yv[1], yv[2])
+        if (S == 1) {
+            switch (R) {
+                case 8: ZT_Q4G3(1, 8); break;
+                case 4: ZT_Q4G3(1, 4); break;
+                case 2: ZT_Q4G3(1, 2); break;
+                default: ZT_Q4G3(1, 1); break;
+            }
+        } else {
+            switch (R) {
+                case 8: ZT_Q4G3(2, 8); break;
+                case 4: ZT_Q4G3(2, 4); break;
+                case 2: ZT_Q4G3(2, 2); break;
+                default: ZT_Q4G3(2, 1); break;
+            }
+        }
+#undef ZT_Q4G3
+        return (int)hipGetLastError();
+    }
     Q4GroupArgs g{};
     int wg = 0;
     for (int i = 0; i < n; i++) {
         const uint8_t* base = static_cast<const uint8_t*>(descs[i].A);
-        g.sc[i] = reinterpret_cast<const uint16_t*>(base);
-        g.dt[i] = reinterpret_cast<const uint32_t*>(base + descs[i].data_offset);
-        g.y[i] = descs[i].y;
-        g.rows[i] = descs[i].rows;
+        g.mat[i].sc = reinterpret_cast<const uint16_t*>(base);
+        g.mat[i].dt = reinterpret_cast<const uint32_t*>(base + descs[i].data_offset);
+        g.mat[i].y = descs[i].y;
+        g.mat[i].rows = descs[i].rows;
+        g.mat[i].wg0 = wg;
         g.wg0[i] = wg;
         wg += ceil_div(descs[i].rows, R);
     }
     g.n = n;
     const dim3 grid(wg), block(nw * kWave);
-#define ZT_Q4G(SS, RR) gemv_q4_group_kernel<SS, RR><<<grid, block, 0, stream>>>(g, x, kb)
+#define ZT_Q4G(SS, RR) gemv_q4_group_kernel<SS, RR><<<grid, block, 0, stream>>>(x, kb, g)
     if (S == 1) {
         switch (R) {
             case 8: ZT_Q4G(1, 8); break;
