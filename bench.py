@@ -367,6 +367,7 @@ SUITE = {
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "w4a16sz_70b": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [1]),
+    "w4a16sz_70b_k28672": ("w4a16sz", [(8192, 28672)], [1]),
     "w4a16_70b_k28672": ("w4a16", [(8192, 28672)], [1]),
     "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
@@ -725,7 +726,7 @@ def run_suite(args) -> None:
 # packed (scale, zero) dwords, batched W4A16
 # and IQ4_NL on their tiled layouts), reported beside the headline.
 CONFIGS = {
-    "1_w4a16_gemv": ["w4a16_c1"],
+    "1_w4a16_gemv": ["w4a16sz_c1"],
     "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
     "3_ternary_bitnet": ["ternary"],
     "4_w4a16_llama3_70b": ["w4a16sz_70b", "w4a16_70b_k28672", "w4a16t_70b"],

@@ -325,13 +325,12 @@ static void launch_w4a16_steps(int R, dim3 g, dim3 b, hipStream_t st, const uint
     }
 }
 
-// Rows per wave of the batch-1 steps kernel: about 8192 waves (4 at
-// 4096 x 4096 measured 10% faster than 8), but not below 4 where 2048 waves
-// allow it.
+// Rows per wave of the batch-1 steps kernel.
 static int w4a16_steps_rows(int M, int nw) {
-    int R = pick_rows_per_wave(M, nw, 1, 8192);
-    if (R < 4) R = min(4, pick_rows_per_wave(M, nw, 1, 2048));
-    return R;
+    // about 4096 waves, but at least 4 rows a wave where 2048 waves allow it: 8 rows from 4096 rows at
+    // K = 4096 (3.98 against 4.16 us with 4 rows at 4096 x 4096 on packed scales; 24.4 against 27.0 us at
+    // 28672 x 8192 rows x K), 4 rows at 1024 x 8192 (3.18 us, against 3.37 with 2 and 3.85 with 8)
+    return max(pick_rows_per_wave(M, nw, 1, 4096), min(4, pick_rows_per_wave(M, nw, 1, 2048)));
 }
 
 // Packs (scale, zero) into one dword per (row, group), row-major.
