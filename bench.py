@@ -388,7 +388,10 @@ SUITE = {
 }
 
 
-def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> dict:
+def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eager: int = 0) -> dict:
+    """One suite measurement.  With eager > 0 the case instead runs that many
+    plain launches (no graph, no timing) over its rotating copies, the
+    workload of a rocprofv3 counter pass."""
     from ztensor_amd import synth
 
     s = torch.cuda.current_stream().cuda_stream
@@ -585,6 +588,14 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
     # at least 256 launches a graph, two untimed replays, then 10 timed: 60-128-launch
     # graphs measured 5-10% slower per launch and varied more between runs
     n = copies * max(1, -(-256 // copies))
+    if eager:
+        torch.cuda.synchronize()
+        for i in range(eager):
+            rc = fn(sets[i % copies], ys[i % copies])
+            if rc != 0:
+                raise RuntimeError(f"{fmt} launch returned {rc}")
+        torch.cuda.synchronize()
+        return {"format": fmt, "K": K, "N": rows, "batch": N, "launches": eager, "rotating_copies": copies}
 
     def loop():
         nonlocal s
@@ -603,6 +614,19 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int) -> d
             "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
 
 
+SUITE_FORMATS = ("q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
+                 "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "q4_k", "q5_k", "q6_k", "q8_0_gguf", "q5_0")
+
+
+def _pmc_case_arg(v: str) -> str:
+    if v in ("q4_0", "w4a16_b8", "w4a16t_b8", "q4_0t_b8"):
+        return v
+    parts = v.split(":")
+    if len(parts) == 4 and parts[0] in SUITE_FORMATS and all(p.isdigit() for p in parts[1:]):
+        return v
+    raise argparse.ArgumentTypeError(f"not a pmc case: {v}")
+
+
 def run_pmc_case(args) -> None:
     """A short, fixed workload for rocprofv3 counter passes: the 64 MiB
     calibration copies, then 40 launches of the dominant Q4_0 GEMV (14336 x
@@ -614,6 +638,13 @@ def run_pmc_case(args) -> None:
 
     lib = _lib.load()
     calibration_copy(torch)
+    if ":" in args.pmc_case:
+        fmt, rows, K, N = args.pmc_case.split(":")
+        if fmt not in SUITE_FORMATS:
+            raise SystemExit(f"bench: unknown pmc format {fmt}")
+        r = _suite_case(torch, lib, fmt, int(rows), int(K), int(N), 0x5EED0060, eager=40)
+        log(f"bench: pmc case {r}")
+        return
     if args.pmc_case in ("w4a16_b8", "w4a16t_b8"):
         run_pmc_case_w4a16(torch, lib, tiled=args.pmc_case == "w4a16t_b8")
         return
@@ -822,11 +853,12 @@ def main() -> None:
                     help="skip the per-configuration timings reported beside the headline")
     ap.add_argument("--suite", action="store_true", help="per-configuration table instead of the headline")
     ap.add_argument("--only", default="", help="comma-separated suite entries (with --suite)")
-    ap.add_argument("--pmc-case", nargs="?", const="q4_0", choices=["q4_0", "w4a16_b8", "w4a16t_b8", "q4_0t_b8"],
+    ap.add_argument("--pmc-case", nargs="?", const="q4_0", type=_pmc_case_arg,
                     help="short fixed workload for rocprofv3 counter passes: copies + 40 launches of the dominant "
                          "Q4_0 GEMV (default), of the W4A16 batch-8 MFMA GEMM at 28672 x 8192 on the row-major "
                          "(w4a16_b8) or tiled (w4a16t_b8) layout, or of the batch-8 Q4_0 tiled GEMM at "
-                         "14336 x 4096 (q4_0t_b8)")
+                         "14336 x 4096 (q4_0t_b8); FORMAT:ROWS:K:BATCH runs 40 launches of any suite "
+                         "format at that shape (e.g. iq4nlt:3584:3584:8)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()

@@ -32,7 +32,6 @@ from ztensor_amd.storage import (  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5  # fp32-exact products: only the summation order differs
-TOL_IQ4_F16 = 1e-3  # IQ4_NL with fp16 activations: codebook carried in fp16
 GOLD = Path(__file__).resolve().parent / "golden"
 
 
@@ -100,7 +99,7 @@ def test_iq4nl_matmul_fp16_activations(eng, orc):
     x16 = synth.x_f16(K * N, 15)
     c = eng.matmul(Tensor((rows, K), s), torch.from_numpy(x16.view(np.float16).reshape(K, N)).cuda())
     ref = orc.iq4nl_matmul(w.raw, x16, rows, K, N)
-    assert rel_err(c.cpu().numpy(), np.asarray(ref).reshape(rows, N)) <= TOL_IQ4_F16
+    assert rel_err(c.cpu().numpy(), np.asarray(ref).reshape(rows, N)) <= TOL
 
 
 def _gptq(w):

@@ -2,7 +2,7 @@
 the CPU oracle, through the C ABI and the engine.
 
 Bars: dequantizers bit-exact (uint32 view equality); GEMVs
-max|y - y_ref| / max|y_ref| <= 1e-3 with fp32 accumulation, y_ref = the
+max|y - y_ref| / max|y_ref| <= 1e-5 with fp32 accumulation, y_ref = the
 reference CPU engine's GemmF32Q4KNT / Q5KNT / Q6KNT and its Q5_0 B-side
 matmul as restated by the oracle.  Shapes: the Llama-3-8B decode layers,
 plus ragged cases (one super-block, partial wave steps, odd super-block

@@ -5,7 +5,7 @@ This is the batch-1 form of W4A16MatMuler.MatMulW4A16 (compute/w4a16.go:
 137-143) that the engine runs.  Bars:
   * the packing: byte-identical with scale | zero << 16 per (row, group),
     row-major, zero 8.0 (0x4800) when zeros is NULL;
-  * the GEMV: max|y - y_ref| / max|y_ref| <= 1e-3 against the oracle's
+  * the GEMV: max|y - y_ref| / max|y_ref| <= 1e-5 against the oracle's
     restatement of the reference CPU engine (dequantize, then SgemmSimd),
     and within 1e-5 of zt_gemm_w4a16_f32 with N = 1 on the same operands.
 """

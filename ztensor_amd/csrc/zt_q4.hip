@@ -41,6 +41,32 @@ __constant__ float kIQ4NLTable[16] = {
     -1.0f, -0.6961928f, -0.5250730f, -0.3947555f, -0.2831612f, -0.1790887f, -0.0805542f, 0.0f,
     0.0805542f, 0.1790887f, 0.2831612f, 0.3947555f, 0.5250730f, 0.6961928f, 1.0f, 1.3312578f};
 
+// Codebook entry of data byte i (element pair: low nibble first) as two fp16
+// pairs: .x = (T_hi[low], T_hi[high]), .y = (T_lo'[low], T_lo'[high]) with
+// T_hi = fp16(T) and T_lo' = fp16(2^11 (T - T_hi)), so T = T_hi + 2^-11 T_lo'
+// to within 2^-22 |T|.
+__device__ __forceinline__ uint2 iq4_pair_entry(int i) {
+    const float a = kIQ4NLTable[i & 15], b = kIQ4NLTable[i >> 4];
+    const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+    const _Float16 al = (_Float16)((a - (float)ah) * 2048.0f), bl = (_Float16)((b - (float)bh) * 2048.0f);
+    return make_uint2((uint32_t)__builtin_bit_cast(uint16_t, ah) | ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16),
+                      (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16));
+}
+
+// Dot product of one data dword (8 codes, elements in order) with the fp16
+// activation dwords xx[0..3]: hi and lo parts summed separately by
+// v_dot2_f32_f16 and joined as hi + 2^-11 lo.
+__device__ __forceinline__ float iq4_dot16(const uint2* tbl, uint32_t w, const uint32_t (&xx)[4]) {
+    float v = 0.0f, vl = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint2 e = tbl[(w >> (8 * j)) & 0xffu];
+        v = __builtin_amdgcn_fdot2(as_half2(e.x), as_half2(xx[j]), v, false);
+        vl = __builtin_amdgcn_fdot2(as_half2(e.y), as_half2(xx[j]), vl, false);
+    }
+    return __builtin_fmaf(vl, 0x1p-11f, v);
+}
+
 template <class XT>
 __device__ __forceinline__ float to_f32(XT v);
 template <>
@@ -349,14 +375,14 @@ __global__ void __launch_bounds__(1024) gemv_q4_group_kernel(const float* __rest
 // IQ4_NL batch-1 GEMV with fp16 activations.  The quad mapping of
 // gemv_quad_kernel (lane q of a quad holds dword q of a block: elements
 // 8q .. 8q+7, byte j = elements 8q+2j (low nibble) and 8q+2j+1 (high)),
-// with a 1 KB LDS table from a data byte to the fp16 pair (T[low], T[high]).
-// The pair lines up with the activation dword (x[8q+2j], x[8q+2j+1]), so each
-// byte is one ds_read_b32 and one v_dot2_f32_f16 (products exact in fp32,
-// fp32 sums).  The fp32 codebook (tensor/iq4_storage.go:28-33) is rounded to
-// fp16 here: relative error at most 2^-11 per entry (3.25e-4 for -0.5250730,
-// the worst), so the output's error relative to max|y| is bounded by that
-// even when no per-weight errors cancel.  A float-pair table with v_fma_mix
-// (exact fp32 codebook) measured 10-20% slower at the Qwen2-7B shapes.
+// with a 2 KB LDS table from a data byte to two fp16 pairs (iq4_pair_entry):
+// the codebook (tensor/iq4_storage.go:28-33) split as T = T_hi + 2^-11 T_lo',
+// exact to 2^-22 |T|.  Each pair lines up with the activation dword
+// (x[8q+2j], x[8q+2j+1]), so each byte is one ds_read_b64 and two
+// v_dot2_f32_f16 into separate hi and lo sums (products exact in fp32, fp32
+// sums), joined once per block before the scale.  The fp16-rounded table
+// alone (one ds_read_b32 and one dot a byte, error up to 2^-11 per entry)
+// measured no faster: 11.3 us against 10.1 us for the split at 18944 x 3584.
 // Buffer loads take the wave-uniform row offsets as scalar offsets; lanes
 // past the last block read zeros through out-of-range offsets.
 template <int R>
@@ -365,17 +391,14 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_kernel(const uint16_t* __
                                                               const uint16_t* __restrict__ x, float* __restrict__ y,
                                                               int rows, int kb) {
     __shared__ float red[16 * R];
-    __shared__ uint32_t tbl[256];
+    __shared__ uint2 tbl[256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int q = lane & 3;
     const int row0 = blockIdx.x * R;
     const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 64, 0x00020000);
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
-        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-    }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = iq4_pair_entry(i);
     __syncthreads();
     uint32_t rofs[R];
 #pragma unroll
@@ -396,13 +419,7 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_kernel(const uint16_t* __
         const u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (uint32_t)(b * 64 + q * 16) : 0x80000000u, 0, 0);
         const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float v = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                v = __builtin_amdgcn_fdot2(as_half2(tbl[(w[r] >> (8 * j)) & 0xffu]), as_half2(xx[j]), v, false);
-            acc[r] = __builtin_fmaf(h2f(s[r]), v, acc[r]);
-        }
+        for (int r = 0; r < R; r++) acc[r] = __builtin_fmaf(h2f(s[r]), iq4_dot16(tbl, w[r], xx), acc[r]);
     }
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
@@ -419,7 +436,7 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_steps_kernel(const uint16
                                                                     const uint16_t* __restrict__ x,
                                                                     float* __restrict__ y, int rows, int kb) {
     __shared__ float red[16 * R];
-    __shared__ uint32_t tbl[256];
+    __shared__ uint2 tbl[256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 3;
     const int row0 = blockIdx.x * R;
@@ -449,10 +466,7 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_steps_kernel(const uint16
         }
         xv[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, b < kb ? (uint32_t)(b * 64 + q * 16) : 0x80000000u, 0, 0);
     }
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
-        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-    }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = iq4_pair_entry(i);
     // the table is visible to the workgroup; the loads stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     float acc[R];
@@ -462,13 +476,7 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_steps_kernel(const uint16
     for (int t = 0; t < S; t++) {
         const uint32_t xx[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float v = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                v = __builtin_amdgcn_fdot2(as_half2(tbl[(w[t][r] >> (8 * j)) & 0xffu]), as_half2(xx[j]), v, false);
-            acc[r] = __builtin_fmaf(h2f(s[t][r]), v, acc[r]);
-        }
+        for (int r = 0; r < R; r++) acc[r] = __builtin_fmaf(h2f(s[t][r]), iq4_dot16(tbl, w[t][r], xx), acc[r]);
     }
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
@@ -988,11 +996,14 @@ __global__ void iq4t_tile_kernel(const uint32_t* __restrict__ data, const uint16
 // Batched IQ4_NL on the tiled layout: the W4A16 tiled kernel's structure
 // (4 waves x 32 rows a workgroup, UPW 128-K units, XCD-aware mapping, X and
 // scales staged in LDS behind an LDS-only barrier while the 1 KB weight
-// loads stream).  A operand: one ds_read_b32 per data byte from a 1 KB LDS
-// table byte -> fp16 pair (T[low], T[high]), the codebook rounded to fp16
-// (relative error at most 2^-11 per entry, as in the fp16 GEMV); the pairs
-// are in element order, so the B rows of a lane group are read in natural
-// order.  Each step's result is scaled by its block's fp16 scale in fp32.
+// loads stream).  A operand: one ds_read_b64 per data byte from a 2 KB LDS
+// table byte -> (hi pair, lo pair) (iq4_pair_entry, the codebook as T_hi +
+// 2^-11 T_lo', exact to 2^-22 |T|); two MFMAs a step, the lo part's result
+// scaled by 2^-11 and accumulated into the hi part's.  The pairs are in
+// element order, so the B rows of a lane group are read in natural order.
+// Each step's result is scaled by its block's fp16 scale in fp32.  The
+// fp16-rounded table with one MFMA a step measured no faster (18.4 against
+// 17.4 us at 18944 x 3584, batch 8).
 template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint16_t* __restrict__ stl,
@@ -1006,7 +1017,7 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
     constexpr int XB = mfma_chunk_xbytes(KC, N);
     extern __shared__ __attribute__((aligned(16))) char smem[];
     char* zero_area = smem + XB;
-    uint32_t* tbl = reinterpret_cast<uint32_t*>(zero_area + 16);   // 256 fp16 pairs
+    uint2* tbl = reinterpret_cast<uint2*>(zero_area + 16);         // 256 x (hi pair, lo pair)
     uint16_t* ssm = reinterpret_cast<uint16_t*>(tbl + 256);        // [tile in WG][unit][16 rows][4 blocks]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -1055,10 +1066,7 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
         }
     }
     if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
-    for (int i = tid; i < 256; i += W * 64) {
-        const _Float16 lo = (_Float16)kIQ4NLTable[i & 15], hi = (_Float16)kIQ4NLTable[i >> 4];
-        tbl[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-    }
+    for (int i = tid; i < 256; i += W * 64) tbl[i] = iq4_pair_entry(i);
 #pragma unroll
     for (int i = 0; i < XP; i++) {
         const int p = tid + i * W * 64;
@@ -1086,9 +1094,14 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
-                    const u32x4 av = {tbl[dw & 0xffu], tbl[(dw >> 8) & 0xffu], tbl[(dw >> 16) & 0xffu], tbl[dw >> 24]};
-                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv,
-                                                                            (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const uint2 e0 = tbl[dw & 0xffu], e1 = tbl[(dw >> 8) & 0xffu], e2 = tbl[(dw >> 16) & 0xffu],
+                                e3 = tbl[dw >> 24];
+                    const u32x4 ah = {e0.x, e1.x, e2.x, e3.x}, al = {e0.y, e1.y, e2.y, e3.y};
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, al), bv,
+                                                                       (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) d[i] *= 0x1p-11f;
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, ah), bv, d, 0, 0, 0);
                     // scales of rows 4 lg + i of this tile, block 4u + s
                     const uint16_t* sp = ssm + ((2 * wave + t) * UPW + u) * 64 + 16 * lg + s;
 #pragma unroll
@@ -1120,7 +1133,7 @@ template <int UPW, int N>
 static void launch_iq4t(dim3 g, hipStream_t st, const uint4* wt, const uint16_t* sc, const uint16_t* x, float* y,
                         float* ws, int M, int K, int nch) {
     constexpr int W = 4;
-    const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 1024 + (size_t)2 * W * UPW * 64 * 2;
+    const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 2048 + (size_t)2 * W * UPW * 64 * 2;
     iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, y, ws, M, K, nch);
 }
 
