@@ -45,6 +45,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "quant GEMV effective HBM GB/s (% of peak) at Llama-3-8B decode shapes, batch 1"
 PEAK_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 LLAMA3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
              ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]  # (name, rows=N_out, K)
 MALL_BYTES = 256 << 20
@@ -378,6 +379,14 @@ SUITE = {
     "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_gguf": ("q8_0_gguf", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q4_0_batched": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    # gemm_int4.cu / gemm_int8.cu: decode shapes, and the reference benchmark's square GEMMs
+    # (gemm_bench_test.go:159-165, batch = rows)
+    "int4": ("int4", [(4096, 4096), (14336, 4096)], [1, 4]),
+    "int4_rmul": ("int4_rmul", [(4096, 4096)], [1, 4]),
+    "int8": ("int8", [(4096, 4096), (4096, 14336)], [1, 4]),
+    "int4_gemm": ("int4", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
+    "int4_rmul_gemm": ("int4_rmul", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
+    "int8_gemm": ("int8", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "q8_0_batched": ("q8_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
@@ -569,6 +578,24 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
         fn = lambda wb, y: lib.zt_gemm_q8gguf_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
         nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
+    elif fmt in ("int4", "int4_rmul"):
+        # the reference benchmark's group size (gemm_bench_test.go:47); int4: A [rows, K]; rmul: W [K, rows]
+        gs = 32
+        w = synth.int4(rows, K, gs, seed) if fmt == "int4" else synth.int4(K, rows, gs, seed)
+        wbufs = [dev(w.packed), dev(w.scales), dev(w.zeros)]
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        if fmt == "int4":
+            fn = lambda wb, y: lib.zt_gemm_int4_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), wb[1].data_ptr(),
+                                                    wb[2].data_ptr(), rows, K, N, gs, s)
+        else:
+            fn = lambda wb, y: lib.zt_gemm_int4_f32_rmul(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                         wb[1].data_ptr(), wb[2].data_ptr(), N, K, rows, gs, s)
+        nbytes = synth.algorithmic_bytes("int4", rows, K, N, group=gs)
+    elif fmt == "int8":
+        wbufs = [dev(synth.int8(rows, K, seed))]
+        x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
+        fn = lambda wb, y: lib.zt_gemm_int8_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, s)
+        nbytes = synth.algorithmic_bytes("int8", rows, K, N)
     elif fmt == "q5_0":
         w = synth.kquant(fmt, rows, K, seed)
         nblk = rows * K // 32
@@ -610,11 +637,17 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     g.replay()
     us = time_graph(torch, g, 10) * 1e3 / n
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
-            "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
+    r = {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
+         "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
+    if fmt in ("int4", "int4_rmul", "int8"):
+        # 2 M K N flops against the dense fp32 MFMA peak these kernels compute at
+        tf = 2.0 * rows * K * N / (us * 1e-6) / 1e12
+        r["TFLOP/s"] = round(tf, 2)
+        r["pct_peak_fp32_mfma"] = round(100 * tf / PEAK_FP32_TFLOPS, 1)
+    return r
 
 
-SUITE_FORMATS = ("q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
+SUITE_FORMATS = ("int4", "int4_rmul", "int8", "q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
                  "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "q4_k", "q5_k", "q6_k", "q8_0_gguf", "q5_0")
 
 
@@ -745,6 +778,7 @@ def run_suite(args) -> None:
             continue
         for si, (rows, K) in enumerate(shapes):
             for N in batches:
+                N = rows if N == "square" else N
                 r = _suite_case(torch, lib, fmt, rows, K, N, 0x5EED0000 + 16 * ci + si)
                 r["config"] = name
                 print(json.dumps(r), flush=True)

@@ -480,6 +480,33 @@ long zt_q5_0_gpu_qs_offset(long nblk);
 long zt_q5_0_gpu_bytes(long nblk);
 void zt_q5_0_raw_to_gpu(const void* raw, long nblk, void* out);
 
+/* ---- int4 / int8 GEMMs with fp32 activations -------------------------- */
+
+/* The reference's group-quantized int4 and plain int8 GEMMs
+ * (internal/cuda/kernels/gemm_int4.h, gemm_int8.h; gemm_int4.cu:29-144,
+ * gemm_int8.cu:16-73; Go GemmInt4F32 / GemmInt4F32RMul / GemmInt8F32,
+ * gemm_quantized.go:24-89), same argument order.  int4 values are signed
+ * [-8, 7], two a byte, the even element in the low nibble; a weight is
+ * float32(v - zero) * scale with fp32 scales and uint8 zeros per group.
+ *   zt_gemm_int4_f32: C[M, N] = dequant(A) B, A [M, K/2] packed, B [K, N]
+ *     fp32, scales / zeros [M, ceil(K / group_size)] (groups along K).
+ *   zt_gemm_int4_f32_rmul: C[batch, out] = B dequant(W), W [in, out/2]
+ *     packed along out, B [batch, in] fp32, scales / zeros
+ *     [in, ceil(out / group_size)] (groups along out).
+ *   zt_gemm_int8_f32: C[M, N] = float(A) B, A [M, K] int8.
+ * Errors as the reference's launchers: an odd K (rmul: odd out_features) or
+ * group_size <= 0 -> InvalidValue (1); also negative sizes or NULL buffers.
+ * An empty M, N (batch, out) is a no-op; K = 0 writes zeros.  Any shape and
+ * alignment is accepted; batches of 1-4 on K % 16 == 0 (int4 also
+ * group_size % 16 == 0, A 8-byte and B 16-byte aligned; int8 A and B
+ * 16-byte aligned) take the streaming GEMV kernels, everything else an fp32
+ * MFMA GEMM.  Results equal the reference's within fp32 summation order. */
+int zt_gemm_int4_f32(const void* A, const float* B, float* C, const float* scales, const void* zeros, int M, int K,
+                     int N, int group_size, zt_stream_t stream);
+int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, const float* scales, const void* zeros, int batch,
+                          int in_features, int out_features, int group_size, zt_stream_t stream);
+int zt_gemm_int8_f32(const void* A, const float* B, float* C, int M, int K, int N, zt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,9 @@ _SIG = {
     "orc_gemm_f32_mmap_nt": (I, [I, L, L, L, P, P, P, I, P]),
     "orc_awq4_wire_dequant": (I, [P, L, P, L]),
     "orc_fp8_dequant": (I, [P, L, P, L, I]),
+    "orc_gemm_int4_f32": (I, [P, P, P, P, P, L, L, L, L, I]),
+    "orc_gemm_int4_f32_rmul": (I, [P, P, P, P, P, L, L, L, L, I]),
+    "orc_gemm_int8_f32": (None, [P, P, P, L, L, L, I]),
 }
 
 _lib = None
@@ -298,4 +301,40 @@ def gemm_f32_mmap_nt(qtype: int, a: np.ndarray, raw: np.ndarray, m: int, n: int,
     rc = lib().orc_gemm_f32_mmap_nt(qtype, m, n, k, _p(a), _p(raw), _p(c), threads, _p(wt))
     if rc != 0:
         raise ValueError(f"GGML type {qtype} has no quantized GEMV here")
+    return c
+
+
+# ---- int4 / int8 GEMMs (gemm_int4.cu, gemm_int8.cu) ---------------------------
+
+def gemm_int4_f32(a: np.ndarray, b: np.ndarray, scales: np.ndarray, zeros: np.ndarray, m: int, k: int, n: int,
+                  gs: int, threads: int = 8) -> np.ndarray:
+    """C[m, n] of gemm_int4_f32; raises ValueError where the launcher returns
+    InvalidValue (odd K, group_size <= 0)."""
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.float32)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zeros = np.ascontiguousarray(zeros, np.uint8)
+    c = np.empty(m * n, np.float32)
+    if lib().orc_gemm_int4_f32(_p(a), _p(b), _p(c), _p(scales), _p(zeros), m, k, n, gs, threads) != 0:
+        raise ValueError("gemm_int4_f32: invalid value")
+    return c
+
+
+def gemm_int4_f32_rmul(w: np.ndarray, x: np.ndarray, scales: np.ndarray, zeros: np.ndarray, batch: int, inf: int,
+                       outf: int, gs: int, threads: int = 8) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zeros = np.ascontiguousarray(zeros, np.uint8)
+    c = np.empty(batch * outf, np.float32)
+    if lib().orc_gemm_int4_f32_rmul(_p(w), _p(x), _p(c), _p(scales), _p(zeros), batch, inf, outf, gs, threads) != 0:
+        raise ValueError("gemm_int4_f32_rmul: invalid value")
+    return c
+
+
+def gemm_int8_f32(a: np.ndarray, b: np.ndarray, m: int, k: int, n: int, threads: int = 8) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.int8)
+    b = np.ascontiguousarray(b, np.float32)
+    c = np.empty(m * n, np.float32)
+    lib().orc_gemm_int8_f32(_p(a), _p(b), _p(c), m, k, n, threads)
     return c

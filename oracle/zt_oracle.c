@@ -834,3 +834,104 @@ EXPORT int orc_gemm_f32_mmap_nt(int qtype, int64_t m, int64_t n, int64_t k, cons
         }
     return 0;
 }
+
+/* ------------------------------------------------ int4 / int8 GEMMs (a18) */
+
+/* internal/cuda/kernels/gemm_int4.cu:20-27 extract_int4: element idx of a
+ * packed row, even idx in the low nibble, sign-extended from 4 bits. */
+static int orc_int4_at(const uint8_t* packed, int64_t idx) {
+    uint8_t byte = packed[idx >> 1];
+    int val = (idx & 1) ? (byte >> 4) : (byte & 0x0F);
+    if (val >= 8) val -= 16;
+    return val;
+}
+
+typedef struct {
+    const uint8_t* a; const float* b; float* c; const float* scales; const uint8_t* zeros;
+    int64_t m, k, n, gs;
+} int4_ctx;
+
+/* gemm_int4.cu:29-56 gemm_int4_kernel, one output (row, col) at a time:
+ * dequant = (float)(v - zero) * scale, acc += dequant * B[k, col] in k order.
+ * nvcc contracts the accumulation into an FMA (its default -fmad=true), so
+ * the restatement calls fmaf. */
+static void int4_rows(void* p, int64_t r0, int64_t r1) {
+    const int4_ctx* x = (const int4_ctx*)p;
+    int64_t ng = (x->k + x->gs - 1) / x->gs;
+    for (int64_t row = r0; row < r1; row++)
+        for (int64_t col = 0; col < x->n; col++) {
+            float acc = 0.0f;
+            for (int64_t kk = 0; kk < x->k; kk++) {
+                int64_t g = kk / x->gs;
+                float scale = x->scales[row * ng + g];
+                int zero = (int)x->zeros[row * ng + g];
+                int v = orc_int4_at(x->a + row * (x->k / 2), kk);
+                float dequant = (float)(v - zero) * scale;
+                acc = fmaf(dequant, x->b[kk * x->n + col], acc);
+            }
+            x->c[row * x->n + col] = acc;
+        }
+}
+
+/* gemm_int4.cu:58-81 gemm_int4_f32: returns 1 (InvalidValue) for an odd K
+ * or group_size <= 0, as the launcher does, else 0. */
+EXPORT int orc_gemm_int4_f32(const uint8_t* a, const float* b, float* c, const float* scales, const uint8_t* zeros,
+                             int64_t m, int64_t k, int64_t n, int64_t gs, int nthreads) {
+    if (k % 2 != 0 || gs <= 0) return 1;
+    int4_ctx ctx = {a, b, c, scales, zeros, m, k, n, gs};
+    orc_parallel_rows(m, nthreads, int4_rows, &ctx);
+    return 0;
+}
+
+/* gemm_int4.cu:89-115 gemm_int4_rmul_kernel: C[b, j] = sum_k B[b, k] *
+ * dequant(W[k, j]), W [in, out/2] packed along out, scales / zeros
+ * [in, ceil(out/gs)] with groups along out; acc += B * dequant (FMA). */
+static void int4_rmul_rows(void* p, int64_t r0, int64_t r1) {
+    const int4_ctx* x = (const int4_ctx*)p; /* m = batch, k = in, n = out */
+    int64_t ng = (x->n + x->gs - 1) / x->gs;
+    for (int64_t row = r0; row < r1; row++)
+        for (int64_t col = 0; col < x->n; col++) {
+            float acc = 0.0f;
+            int64_t g = col / x->gs;
+            for (int64_t kk = 0; kk < x->k; kk++) {
+                float scale = x->scales[kk * ng + g];
+                int zero = (int)x->zeros[kk * ng + g];
+                int v = orc_int4_at(x->a + kk * (x->n / 2), col);
+                float dequant = (float)(v - zero) * scale;
+                acc = fmaf(x->b[row * x->k + kk], dequant, acc);
+            }
+            x->c[row * x->n + col] = acc;
+        }
+}
+
+/* gemm_int4.cu:117-144 gemm_int4_f32_rmul: 1 for an odd out_features or
+ * group_size <= 0, else 0. */
+EXPORT int orc_gemm_int4_f32_rmul(const uint8_t* w, const float* x, float* c, const float* scales,
+                                  const uint8_t* zeros, int64_t batch, int64_t in, int64_t out, int64_t gs,
+                                  int nthreads) {
+    if (out % 2 != 0 || gs <= 0) return 1;
+    int4_ctx ctx = {w, x, c, scales, zeros, batch, in, out, gs};
+    orc_parallel_rows(batch, nthreads, int4_rmul_rows, &ctx);
+    return 0;
+}
+
+typedef struct { const int8_t* a; const float* b; float* c; int64_t m, k, n; } int8_ctx;
+
+/* gemm_int8.cu:16-56 gemm_int8_kernel: acc += float(A[row, k]) * B[k, col]
+ * over 32-wide K tiles in k order (zero-padded past K), one FMA each. */
+static void int8_rows(void* p, int64_t r0, int64_t r1) {
+    const int8_ctx* x = (const int8_ctx*)p;
+    for (int64_t row = r0; row < r1; row++)
+        for (int64_t col = 0; col < x->n; col++) {
+            float acc = 0.0f;
+            for (int64_t kk = 0; kk < x->k; kk++) acc = fmaf((float)x->a[row * x->k + kk], x->b[kk * x->n + col], acc);
+            x->c[row * x->n + col] = acc;
+        }
+}
+
+/* gemm_int8.cu:58-73 gemm_int8_f32. */
+EXPORT void orc_gemm_int8_f32(const int8_t* a, const float* b, float* c, int64_t m, int64_t k, int64_t n,
+                              int nthreads) {
+    int8_ctx ctx = {a, b, c, m, k, n};
+    orc_parallel_rows(m, nthreads, int8_rows, &ctx);
+}

@@ -290,6 +290,26 @@ def test_q4t_noalloc_rejects_oversized_and_bad_calls_without_launching():
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 64, 128, 5, None) == _lib.HIP_ERROR_INVALID_VALUE  # N
 
 
+def test_int4_int8_gemms_reject_like_the_reference_without_launching():
+    """zt_gemm_int4_f32 / _rmul return InvalidValue for an odd K (odd
+    out_features) or group_size <= 0, as gemm_int4.cu:64-69, 122-127 do, and
+    for negative sizes or NULL buffers; empty outputs return 0.  No GPU."""
+    lib = _lib.load()
+    p, bad = 0x10000, _lib.HIP_ERROR_INVALID_VALUE
+    assert lib.zt_gemm_int4_f32(p, p, p, p, p, 4, 33, 4, 32, None) == bad  # odd K
+    assert lib.zt_gemm_int4_f32(p, p, p, p, p, 4, 32, 4, 0, None) == bad  # group_size
+    assert lib.zt_gemm_int4_f32(p, p, p, p, p, -1, 32, 4, 32, None) == bad
+    assert lib.zt_gemm_int4_f32(p, None, p, p, p, 4, 32, 4, 32, None) == bad
+    assert lib.zt_gemm_int4_f32(p, p, p, p, p, 0, 32, 4, 32, None) == 0
+    assert lib.zt_gemm_int4_f32_rmul(p, p, p, p, p, 4, 32, 33, 32, None) == bad  # odd out
+    assert lib.zt_gemm_int4_f32_rmul(p, p, p, p, p, 4, 32, 32, -2, None) == bad
+    assert lib.zt_gemm_int4_f32_rmul(p, p, p, p, None, 4, 32, 32, 32, None) == bad
+    assert lib.zt_gemm_int4_f32_rmul(p, p, p, p, p, 4, 32, 0, 32, None) == 0
+    assert lib.zt_gemm_int8_f32(p, p, p, 4, -1, 4, None) == bad
+    assert lib.zt_gemm_int8_f32(None, p, p, 4, 16, 4, None) == bad
+    assert lib.zt_gemm_int8_f32(p, p, p, 4, 16, 0, None) == 0
+
+
 def test_ccall_style_calls_through_all_uintptr_signature(tmp_path):
     """tests/ccall_abi.c, compiled here with gcc, dlopens libzt_hip.so and
     calls entry points through a 20-argument all-uintptr_t function pointer,

@@ -1,0 +1,211 @@
+"""GPU parity of the int4 / int8 GEMMs (zt_gemm_int4_f32, zt_gemm_int4_f32_rmul,
+zt_gemm_int8_f32) against the oracle's restatement of the reference's
+kernels (internal/cuda/kernels/gemm_int4.cu:29-144, gemm_int8.cu:16-73),
+through the C ABI.
+
+Bars: max|y - y_ref| / max|y_ref| <= 1e-5 with y_ref the oracle: every
+weight is dequantized as the reference does (one fp32 multiply) and every
+product is an fp32 product, so only the summation order differs.  Shapes:
+the streaming batch-1..4 kernels (K % 16 == 0, group_size % 16 == 0) and
+the MFMA GEMM (every other shape: odd group sizes, K not a multiple of 16 or
+32, partial 64-row and 64-column tiles, batches past 4), the reference
+benchmark's square GEMMs at 1024 in full and at 4096 on sampled rows, and
+its inputs (bytes 0x53, scale 0.1, activations 0.01) at 4096 cubed on every
+output against the fp32 FMA chain of its k loop.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from ztensor_amd import _lib, synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return _lib.load()
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rel_err(y, ref) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def run_int4(lib, w, b, M, K, N, gs):
+    c = torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda")
+    a, bd, s, z = dev(w.packed), dev(b), dev(w.scales), dev(w.zeros)
+    lib.call("zt_gemm_int4_f32", a.data_ptr(), bd.data_ptr(), c.data_ptr(), s.data_ptr(), z.data_ptr(), M, K, N, gs,
+             stream())
+    return c.cpu().numpy()
+
+
+def run_rmul(lib, w, x, batch, inf, outf, gs):
+    c = torch.full((batch * outf,), float("nan"), dtype=torch.float32, device="cuda")
+    wd, xd, s, z = dev(w.packed), dev(x), dev(w.scales), dev(w.zeros)
+    lib.call("zt_gemm_int4_f32_rmul", wd.data_ptr(), xd.data_ptr(), c.data_ptr(), s.data_ptr(), z.data_ptr(), batch,
+             inf, outf, gs, stream())
+    return c.cpu().numpy()
+
+
+def run_int8(lib, a, b, M, K, N):
+    c = torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda")
+    ad, bd = dev(a), dev(b)
+    lib.call("zt_gemm_int8_f32", ad.data_ptr(), bd.data_ptr(), c.data_ptr(), M, K, N, stream())
+    return c.cpu().numpy()
+
+
+INT4_CASES = [  # M, K, N, group_size
+    (4096, 4096, 1, 32), (4096, 4096, 1, 128), (14336, 4096, 1, 128), (4096, 4096, 4, 32), (333, 1024, 3, 64),
+    (1, 16, 1, 16), (4096, 4096, 2, 32),
+    # MFMA GEMM: group sizes not a multiple of 16, odd shapes, wider batches
+    (1000, 1000, 2, 20), (77, 130, 5, 7), (65, 34, 9, 2), (512, 4096, 16, 128), (100, 2048, 64, 32), (3, 2, 1, 1),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs", INT4_CASES)
+def test_int4_nt(lib, orc, M, K, N, gs):
+    say(f"int4 M={M} K={K} N={N} gs={gs}")
+    w = synth.int4(M, K, gs, 300 + M + K, zero_max=15)
+    b = synth.x_f32(K * N, 301 + N).reshape(K, N)
+    y = run_int4(lib, w, b, M, K, N, gs)
+    assert rel_err(y, orc.gemm_int4_f32(w.packed, b, w.scales, w.zeros, M, K, N, gs)) <= TOL
+
+
+RMUL_CASES = [  # batch, in, out, group_size
+    (1, 4096, 4096, 32), (4, 4096, 4096, 128), (3, 1000, 1002, 7), (2, 64, 30, 16), (1, 1, 2, 1),
+    (5, 512, 256, 32), (64, 1024, 1000, 32), (17, 33, 66, 5),
+]
+
+
+@pytest.mark.parametrize("batch,inf,outf,gs", RMUL_CASES)
+def test_int4_rmul(lib, orc, batch, inf, outf, gs):
+    say(f"int4 rmul batch={batch} in={inf} out={outf} gs={gs}")
+    w = synth.int4(inf, outf, gs, 400 + inf + outf, zero_max=15)
+    x = synth.x_f32(batch * inf, 401 + batch).reshape(batch, inf)
+    y = run_rmul(lib, w, x, batch, inf, outf, gs)
+    assert rel_err(y, orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, batch, inf, outf, gs)) <= TOL
+
+
+INT8_CASES = [  # M, K, N
+    (4096, 4096, 1), (4096, 14336, 1), (4096, 4096, 4), (1, 16, 1), (333, 1024, 3),
+    (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65),
+]
+
+
+@pytest.mark.parametrize("M,K,N", INT8_CASES)
+def test_int8(lib, orc, M, K, N):
+    say(f"int8 M={M} K={K} N={N}")
+    a = synth.int8(M, K, 500 + M + K)
+    b = synth.x_f32(K * N, 501 + N).reshape(K, N)
+    y = run_int8(lib, a, b, M, K, N)
+    assert rel_err(y, orc.gemm_int8_f32(a, b, M, K, N)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "rmul"])
+def test_reference_benchmark_square_1024(lib, orc, fmt):
+    """The reference benchmark's 1024-cubed GEMM on random operands, every
+    output against the oracle."""
+    n = 1024
+    say(f"{fmt} square {n}")
+    x = synth.x_f32(n * n, 600).reshape(n, n)
+    if fmt == "int4":
+        w = synth.int4(n, n, 32, 601)
+        assert rel_err(run_int4(lib, w, x, n, n, n, 32), orc.gemm_int4_f32(w.packed, x, w.scales, w.zeros, n, n, n,
+                                                                           32, threads=16)) <= TOL
+    elif fmt == "rmul":
+        w = synth.int4(n, n, 32, 602)
+        assert rel_err(run_rmul(lib, w, x, n, n, n, 32), orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, n, n,
+                                                                                n, 32, threads=16)) <= TOL
+    else:
+        a = synth.int8(n, n, 603)
+        assert rel_err(run_int8(lib, a, x, n, n, n), orc.gemm_int8_f32(a, x, n, n, n, threads=16)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_reference_benchmark_square_4096_sampled_rows(lib, orc, fmt):
+    """4096 cubed on random operands; the oracle runs the first and last 8
+    rows of A (all K, all N) against the same rows of the GPU result."""
+    n = 4096
+    say(f"{fmt} square {n}")
+    x = synth.x_f32(n * n, 610).reshape(n, n)
+    rows = np.r_[0:8, n - 8:n]
+    if fmt == "int4":
+        w = synth.int4(n, n, 32, 611)
+        y = run_int4(lib, w, x, n, n, n, 32).reshape(n, n)
+        ref = orc.gemm_int4_f32(w.packed[rows], x, w.scales[rows], w.zeros[rows], len(rows), n, n, 32, threads=16)
+    else:
+        a = synth.int8(n, n, 612)
+        y = run_int8(lib, a, x, n, n, n).reshape(n, n)
+        ref = orc.gemm_int8_f32(a[rows], x, len(rows), n, n, threads=16)
+    assert rel_err(y[rows].reshape(-1), ref) <= TOL
+    assert np.isfinite(y).all()
+
+
+def test_reference_benchmark_inputs_4096_every_output(lib):
+    """gemm_bench_test.go's inputs at 4096 cubed (int4: bytes 0x53, scale 0.1,
+    zero 0, group 32; int8: bytes 42; activations 0.01): every output equals
+    the fp32 FMA chain of the reference kernel's k loop within the bar."""
+    n = 4096
+    say("benchmark inputs 4096")
+    x = np.full((n, n), 0.01, np.float32)
+    w = synth.Int4Weights(np.zeros((1, 1), np.int8), np.full((n, n // 2), 0x53, np.uint8),
+                          np.full((n, n // 32), 0.1, np.float32), np.zeros((n, n // 32), np.uint8))
+    y = run_int4(lib, w, x, n, n, n, 32)
+    dq = [np.float32(np.float32(3) * np.float32(0.1)), np.float32(np.float32(5) * np.float32(0.1))]
+    acc = np.float32(0.0)
+    for k in range(n):
+        acc = np.float32(np.longdouble(acc) + np.longdouble(dq[k & 1]) * np.longdouble(np.float32(0.01)))
+    assert rel_err(y, np.full(n * n, acc)) <= TOL
+    y8 = run_int8(lib, np.full((n, n), 42, np.int8), x, n, n, n)
+    acc8 = np.float32(0.0)
+    for _ in range(n):
+        acc8 = np.float32(np.longdouble(acc8) + np.longdouble(42) * np.longdouble(np.float32(0.01)))
+    assert rel_err(y8, np.full(n * n, acc8)) <= TOL
+
+
+def test_zero_k_writes_zeros_and_empty_calls(lib):
+    c = torch.full((12,), float("nan"), dtype=torch.float32, device="cuda")
+    t = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    p = t.data_ptr()
+    assert lib.zt_gemm_int8_f32(p, p, c.data_ptr(), 3, 0, 4, stream()) == 0
+    torch.cuda.synchronize()
+    assert not c.cpu().numpy().any()
+    c.fill_(float("nan"))
+    assert lib.zt_gemm_int4_f32(p, p, c.data_ptr(), p, p, 4, 0, 3, 32, stream()) == 0
+    torch.cuda.synchronize()
+    assert not c.cpu().numpy().any()
+    c.fill_(float("nan"))
+    assert lib.zt_gemm_int4_f32_rmul(p, p, c.data_ptr(), p, p, 2, 0, 6, 32, stream()) == 0
+    torch.cuda.synchronize()
+    assert not c.cpu().numpy().any()
+    # empty outputs: nothing to do, nothing written
+    assert lib.zt_gemm_int8_f32(p, p, p, 0, 16, 4, stream()) == 0
+    assert lib.zt_gemm_int4_f32(p, p, p, p, p, 4, 32, 0, 32, stream()) == 0
+    assert lib.zt_gemm_int4_f32_rmul(p, p, p, p, p, 0, 32, 64, 32, stream()) == 0
+
+
+def test_repeated_calls_bit_identical(lib):
+    M, K, N, gs = 1000, 1000, 40, 20
+    w = synth.int4(M, K, gs, 700)
+    b = synth.x_f32(K * N, 701).reshape(K, N)
+    y1 = run_int4(lib, w, b, M, K, N, gs)
+    y2 = run_int4(lib, w, b, M, K, N, gs)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))

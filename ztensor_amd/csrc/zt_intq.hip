@@ -1,0 +1,446 @@
+// Group-quantized int4 and plain int8 GEMMs with fp32 activations: the
+// reference's gemm_int4_f32, gemm_int4_f32_rmul and gemm_int8_f32
+// (internal/cuda/kernels/gemm_int4.cu:29-144, gemm_int8.cu:16-73; Go
+// GemmInt4F32 / GemmInt4F32RMul / GemmInt8F32, gemm_quantized.go:24-89).
+//
+// Formats, as the reference defines them:
+//  * int4: two signed values per byte, element 2b in the low nibble of byte
+//    b, sign-extended to [-8, 7]; per-group fp32 scale and uint8 zero,
+//    w = float32(v - zero) * scale.  gemm_int4_f32: A [M, K/2], groups of
+//    group_size along K (scales, zeros [M, ceil(K / group_size)]).
+//    gemm_int4_f32_rmul: W [in, out/2], groups along out (scales, zeros
+//    [in, ceil(out / group_size)]), C[b, j] = sum_k X[b, k] w[k, j].
+//  * int8: A [M, K] int8, C = float(A) B.
+//
+// Kernels:
+//  * batches of 1-4 on aligned shapes: VALU kernels that stream the weights
+//    once (intq_gemv_kernel for A B, int4_rmul_valu_kernel for X W);
+//  * every other call: intq_mfma_kernel, an LDS-tiled fp32 MFMA GEMM
+//    (v_mfma_f32_16x16x4f32) that dequantizes each weight on its way into
+//    LDS exactly as the reference does (one fp32 multiply), so every product
+//    is the reference's fp32 product and only the summation order differs.
+#include "zt_common.h"
+#include "zt_mfma.h"
+
+namespace zt {
+
+// The low 4 bits of v, sign-extended (gemm_int4.cu:20-27).
+__device__ __forceinline__ int sext4(uint32_t v) { return ((int)(v << 28)) >> 28; }
+// Byte i of v, sign-extended.
+__device__ __forceinline__ int sext8(uint32_t v, int i) { return ((int)(v << (24 - 8 * i))) >> 24; }
+
+// ------------------------------------------------------------ A B, batch 1-4
+//
+// C[M, N] = dequant(A) B for N = NB in 1..4.  A wave owns R rows; lane l of
+// wave w takes 16-element chunks c = l + 64 (w + nwaves i) of K (int8: one
+// 16-byte load a row; int4: one 8-byte load, within one group since
+// group_size % 16 == 0) and the 16 N-wide activation rows of the chunk (4 NB
+// contiguous 16-byte loads, shared by the R rows).  int4 sums (v - z) x over
+// the chunk and applies the scale once: s * sum((v - z) x).  The waves of a
+// workgroup then combine through LDS (block_reduce_store).
+template <bool INT4, int R, int NB>
+__global__ void __launch_bounds__(1024) intq_gemv_kernel(const uint8_t* __restrict__ A, const float* __restrict__ x,
+                                                         float* __restrict__ y, const float* __restrict__ scales,
+                                                         const uint8_t* __restrict__ zeros, int rows, int K, int gs,
+                                                         int ng) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int row0 = blockIdx.x * R;
+    const int nchunks = K / 16;
+    const long rowbytes = INT4 ? K / 2 : K;
+    float acc[NB][R];
+#pragma unroll
+    for (int n = 0; n < NB; n++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[n][r] = 0.0f;
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rr[r] = min(row0 + r, rows - 1);
+    for (int c = wave * 64 + lane; c < nchunks; c += nwaves * 64) {
+        float xv[16 * NB];
+        const float4* xp = reinterpret_cast<const float4*>(x + (long)c * 16 * NB);
+#pragma unroll
+        for (int q = 0; q < 4 * NB; q++) {
+            const float4 t = xp[q];
+            xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+        }
+        if constexpr (INT4) {
+            uint2 w[R];
+            float s[R];
+            int z[R];
+            const int g = c * 16 / gs;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                w[r] = *reinterpret_cast<const uint2*>(A + rr[r] * rowbytes + (long)c * 8);
+                s[r] = scales[(long)rr[r] * ng + g];
+                z[r] = zeros[(long)rr[r] * ng + g];
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float ag[NB];
+#pragma unroll
+                for (int n = 0; n < NB; n++) ag[n] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t d = e < 8 ? w[r].x : w[r].y;
+                    const float v = (float)(sext4(d >> (4 * (e & 7))) - z[r]);
+#pragma unroll
+                    for (int n = 0; n < NB; n++) ag[n] = __builtin_fmaf(v, xv[e * NB + n], ag[n]);
+                }
+#pragma unroll
+                for (int n = 0; n < NB; n++) acc[n][r] = __builtin_fmaf(s[r], ag[n], acc[n][r]);
+            }
+        } else {
+            uint4 w[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) w[r] = *reinterpret_cast<const uint4*>(A + rr[r] * rowbytes + (long)c * 16);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t d4[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float v = (float)sext8(d4[e >> 2], e & 3);
+#pragma unroll
+                    for (int n = 0; n < NB; n++) acc[n][r] = __builtin_fmaf(v, xv[e * NB + n], acc[n][r]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NB; n++) {
+        if (n > 0) __syncthreads();  // red is reused by the next column
+        block_reduce_store<R>(acc[n], red, y + n, NB, row0, rows);
+    }
+}
+
+template <bool INT4, int NB>
+static void launch_intq_gemv_r(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* A, const float* x, float* y,
+                               const float* s, const uint8_t* z, int M, int K, int gs, int ng) {
+    switch (R) {
+        case 8: intq_gemv_kernel<INT4, 8, NB><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng); break;
+        case 4: intq_gemv_kernel<INT4, 4, NB><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng); break;
+        case 2: intq_gemv_kernel<INT4, 2, NB><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng); break;
+        default: intq_gemv_kernel<INT4, 1, NB><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng); break;
+    }
+}
+
+template <bool INT4>
+static void launch_intq_gemv(hipStream_t st, const uint8_t* A, const float* x, float* y, const float* s,
+                             const uint8_t* z, int M, int K, int N, int gs, int ng) {
+    const int nchunks = K / 16;
+    const int nw = max(1, min(16, ceil_div(nchunks, 64)));
+    // fewer rows a wave for wider batches: acc holds N x R values
+    int R = pick_rows_per_wave(M, nw, 1, 2048);
+    if (N > 2 && R > 4) R = 4;
+    const dim3 g(ceil_div(M, R)), b(nw * kWave);
+    switch (N) {
+        case 1: launch_intq_gemv_r<INT4, 1>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
+        case 2: launch_intq_gemv_r<INT4, 2>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
+        case 3: launch_intq_gemv_r<INT4, 3>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
+        default: launch_intq_gemv_r<INT4, 4>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
+    }
+}
+
+// ------------------------------------------------------------ X W, batch 1-4
+//
+// C[b, j] = sum_k X[b, k] w[k, j], batch NB in 1..4.  Lane l of workgroup
+// g owns the byte column p = 64 g + l of W, outputs 2p and 2p+1, whose
+// groups are fixed for the whole call; the 16 waves of the workgroup take
+// contiguous K ranges in turn, each row a 64-byte coalesced load, and sum
+// their ranges through LDS in wave order.  Each weight is dequantized as the
+// reference does, float32(v - zero) * scale, then multiplied into the
+// accumulators.
+template <int NB>
+__global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __restrict__ W,
+                                                              const float* __restrict__ X, float* __restrict__ C,
+                                                              const float* __restrict__ scales,
+                                                              const uint8_t* __restrict__ zeros, int K, int Nout,
+                                                              int gs, int ng) {
+    __shared__ float red[16][2 * NB][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int npairs = Nout / 2;
+    const int p = blockIdx.x * 64 + lane;
+    const int pc = min(p, npairs - 1);
+    const int g0 = 2 * pc / gs, g1 = (2 * pc + 1) / gs;
+    const int kc = (K + nwaves - 1) / nwaves;
+    const int k0 = wave * kc, k1 = min(K, k0 + kc);
+    float acc[NB][2];
+#pragma unroll
+    for (int n = 0; n < NB; n++) acc[n][0] = acc[n][1] = 0.0f;
+#pragma unroll 8
+    for (int k = k0; k < k1; k++) {
+        const uint32_t b = W[(long)k * npairs + pc];
+        const long sb = (long)k * ng;
+        const float w0 = (float)(sext4(b) - (int)zeros[sb + g0]) * scales[sb + g0];
+        const float w1 = (float)(sext4(b >> 4) - (int)zeros[sb + g1]) * scales[sb + g1];
+#pragma unroll
+        for (int n = 0; n < NB; n++) {
+            const float xv = X[(long)n * K + k];
+            acc[n][0] = __builtin_fmaf(xv, w0, acc[n][0]);
+            acc[n][1] = __builtin_fmaf(xv, w1, acc[n][1]);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NB; n++) {
+        red[wave][2 * n][lane] = acc[n][0];
+        red[wave][2 * n + 1][lane] = acc[n][1];
+    }
+    __syncthreads();
+    if (wave == 0 && p < npairs) {
+#pragma unroll
+        for (int j = 0; j < 2 * NB; j++) {
+            float s = 0.0f;
+            for (int w = 0; w < nwaves; w++) s += red[w][j][lane];
+            C[(long)(j >> 1) * Nout + 2 * p + (j & 1)] = s;
+        }
+    }
+}
+
+// ------------------------------------------------------------ fp32 MFMA GEMM
+//
+// C[M, N] = sum_k Aop(m, k) Bop(k, n) with
+//   V = 0 (int8 A B):  Aop = float(A[m, k]),  Bop = B[k, n];
+//   V = 1 (int4 A B):  Aop = float(v - z) * s of A[m, k] (groups along K),
+//                      Bop = B[k, n];
+//   V = 2 (X W):       Aop = X[m, k] (M = batch), Bop = float(v - z) * s of
+//                      W[k, n] (groups along N).
+// A workgroup of 4 waves owns a 64 x 64 tile of C; each wave a 32 x 32
+// quarter, 2 x 2 tiles of v_mfma_f32_16x16x4f32 (lane l supplies A[l % 16]
+// [l / 16] and B[l / 16][l % 16]; D lane l holds rows 4 (l / 16) .. +3 of
+// column l % 16).  K advances 32 at a time through two LDS buffers, [k][m]
+// and [k][n] with rows padded to 80 floats, so each lane group's reads hit
+// distinct banks; the next K step's global loads are issued before the
+// current step's MFMAs.  Every global load is a scalar element load
+// coalesced across lanes, so no shape or alignment is required.
+constexpr int kIqTM = 64, kIqTN = 64, kIqTK = 32, kIqLP = 80;
+
+template <int V>
+__global__ void __launch_bounds__(256) intq_mfma_kernel(const void* __restrict__ Ap, const void* __restrict__ Bp,
+                                                        float* __restrict__ C, const float* __restrict__ scales,
+                                                        const uint8_t* __restrict__ zeros, int M, int N, int K, int gs,
+                                                        int ng) {
+    __shared__ float As[2][kIqTK][kIqLP];
+    __shared__ float Bs[2][kIqTK][kIqLP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.y * kIqTM, n0 = blockIdx.x * kIqTN;
+    float ra[8], rb[8];
+
+    // the A operand of K step k0 into ra
+    auto load_a = [&](int k0) {
+        if constexpr (V == 0 || V == 1) {
+            // thread: row m0 + tid / 4, K positions k0 + 8 (tid % 4) .. +7
+            const int m = m0 + (tid >> 2), kb = k0 + 8 * (tid & 3);
+            if constexpr (V == 0) {
+                const int8_t* a = static_cast<const int8_t*>(Ap) + (long)min(m, M - 1) * K;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ra[e] = (m < M && kb + e < K) ? (float)a[kb + e] : 0.0f;
+            } else {
+                const uint8_t* a = static_cast<const uint8_t*>(Ap) + (long)min(m, M - 1) * (K / 2);
+                const long gbase = (long)min(m, M - 1) * ng;
+                int g = min(kb, K - 1) / gs, rem = min(kb, K - 1) - g * gs;
+                float s = scales[gbase + g];
+                int z = zeros[gbase + g];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int k = kb + e;
+                    if (rem == gs) {
+                        g++;
+                        rem = 0;
+                        if (k < K) {
+                            s = scales[gbase + g];
+                            z = zeros[gbase + g];
+                        }
+                    }
+                    rem++;
+                    float v = 0.0f;
+                    if (m < M && k < K) {
+                        const uint32_t byte = a[k >> 1];
+                        v = (float)(sext4((k & 1) ? byte >> 4 : byte) - z) * s;
+                    }
+                    ra[e] = v;
+                }
+            }
+        } else {
+            // X rows: thread K position k0 + tid % 32, rows m0 + tid / 32 + 8 i
+            const float* xr = static_cast<const float*>(Ap);
+            const int k = k0 + (tid & 31);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int m = m0 + (tid >> 5) + 8 * i;
+                ra[i] = (m < M && k < K) ? xr[(long)m * K + k] : 0.0f;
+            }
+        }
+    };
+    // the B operand of K step k0 into rb
+    auto load_b = [&](int k0) {
+        if constexpr (V == 0 || V == 1) {
+            // thread: column n0 + tid % 64, K rows k0 + tid / 64 + 4 i
+            const float* b = static_cast<const float*>(Bp);
+            const int n = n0 + (tid & 63);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int k = k0 + (tid >> 6) + 4 * i;
+                rb[i] = (n < N && k < K) ? b[(long)k * N + n] : 0.0f;
+            }
+        } else {
+            // W row k0 + tid / 8, columns n0 + 8 (tid % 8) .. +7
+            const int k = k0 + (tid >> 3), nb = n0 + 8 * (tid & 7);
+            const uint8_t* w = static_cast<const uint8_t*>(Bp) + (long)min(k, K - 1) * (N / 2);
+            const long gbase = (long)min(k, K - 1) * ng;
+            int g = min(nb, N - 1) / gs, rem = min(nb, N - 1) - g * gs;
+            float s = scales[gbase + g];
+            int z = zeros[gbase + g];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int n = nb + e;
+                if (rem == gs) {
+                    g++;
+                    rem = 0;
+                    if (n < N) {
+                        s = scales[gbase + g];
+                        z = zeros[gbase + g];
+                    }
+                }
+                rem++;
+                float v = 0.0f;
+                if (k < K && n < N) {
+                    const uint32_t byte = w[n >> 1];
+                    v = (float)(sext4((n & 1) ? byte >> 4 : byte) - z) * s;
+                }
+                rb[e] = v;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+        if constexpr (V == 0 || V == 1) {
+            const int m = tid >> 2, kb = 8 * (tid & 3);
+#pragma unroll
+            for (int e = 0; e < 8; e++) As[buf][kb + e][m] = ra[e];
+            const int n = tid & 63, kr = tid >> 6;
+#pragma unroll
+            for (int i = 0; i < 8; i++) Bs[buf][kr + 4 * i][n] = rb[i];
+        } else {
+            const int k = tid & 31, mr = tid >> 5;
+#pragma unroll
+            for (int i = 0; i < 8; i++) As[buf][k][mr + 8 * i] = ra[i];
+            const int kr = tid >> 3, nb = 8 * (tid & 7);
+#pragma unroll
+            for (int e = 0; e < 8; e++) Bs[buf][kr][nb + e] = rb[e];
+        }
+    };
+
+    const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+    const int li = lane & 15, lk = lane >> 4;
+    float4v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+    const int nsteps = (K + kIqTK - 1) / kIqTK;
+    if (nsteps > 0) {
+        load_a(0);
+        load_b(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < nsteps; t++) {
+        const int buf = t & 1;
+        if (t + 1 < nsteps) {
+            load_a((t + 1) * kIqTK);
+            load_b((t + 1) * kIqTK);
+        }
+#pragma unroll
+        for (int kk = 0; kk < kIqTK / 4; kk++) {
+            const int kr = 4 * kk + lk;
+            const float a0 = As[buf][kr][wm + li], a1 = As[buf][kr][wm + 16 + li];
+            const float b0 = Bs[buf][kr][wn + li], b1 = Bs[buf][kr][wn + 16 + li];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        // the other buffer was last read in step t - 1, before the barrier that ended it
+        if (t + 1 < nsteps) store(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn + 16 * j + li;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + 16 * i + 4 * lk + r;
+                if (m < M && n < N) C[(long)m * N + n] = acc[i][j][r];
+            }
+        }
+}
+
+template <int V>
+static void launch_intq_mfma(hipStream_t st, const void* A, const void* B, float* C, const float* s, const uint8_t* z,
+                             int M, int N, int K, int gs, int ng) {
+    const dim3 g(ceil_div(N, kIqTN), ceil_div(M, kIqTM));
+    intq_mfma_kernel<V><<<g, 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+}
+
+}  // namespace zt
+
+using namespace zt;
+
+// Grid limits of the MFMA GEMM: blockIdx.y holds M / 64.
+static bool intq_grid_ok(long M, long N) { return (M + kIqTM - 1) / kIqTM <= 65535 && (N + kIqTN - 1) / kIqTN < 0x7fffffffL; }
+
+ZT_EXPORT int zt_gemm_int8_f32(const void* A, const float* B, float* C, int M, int K, int N, hipStream_t stream) {
+    if (M < 0 || K < 0 || N < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    if (A == nullptr || C == nullptr || (K > 0 && B == nullptr) || !intq_grid_ok(M, N)) return (int)hipErrorInvalidValue;
+    const uint8_t* a = static_cast<const uint8_t*>(A);
+    if (N <= 4 && K > 0 && K % 16 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)B & 15) == 0)
+        launch_intq_gemv<false>(stream, a, B, C, nullptr, nullptr, M, K, N, 1, 1);
+    else
+        launch_intq_mfma<0>(stream, A, B, C, nullptr, nullptr, M, N, K, 1, 1);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_int4_f32(const void* A, const float* B, float* C, const float* scales, const void* zeros, int M,
+                               int K, int N, int group_size, hipStream_t stream) {
+    if (K % 2 != 0 || group_size <= 0) return (int)hipErrorInvalidValue;  // gemm_int4.cu:64-69
+    if (M < 0 || K < 0 || N < 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    if (A == nullptr || C == nullptr || !intq_grid_ok(M, N)) return (int)hipErrorInvalidValue;
+    if (K > 0 && (B == nullptr || scales == nullptr || zeros == nullptr)) return (int)hipErrorInvalidValue;
+    const int ng = K > 0 ? ceil_div(K, group_size) : 1;
+    const uint8_t* a = static_cast<const uint8_t*>(A);
+    const uint8_t* z = static_cast<const uint8_t*>(zeros);
+    if (N <= 4 && K > 0 && K % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 15) == 0)
+        launch_intq_gemv<true>(stream, a, B, C, scales, z, M, K, N, group_size, ng);
+    else
+        launch_intq_mfma<1>(stream, A, B, C, scales, z, M, N, K, group_size, ng);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, const float* scales, const void* zeros,
+                                    int batch, int in_features, int out_features, int group_size, hipStream_t stream) {
+    if (out_features % 2 != 0 || group_size <= 0) return (int)hipErrorInvalidValue;  // gemm_int4.cu:122-127
+    if (batch < 0 || in_features < 0 || out_features < 0) return (int)hipErrorInvalidValue;
+    if (batch == 0 || out_features == 0) return (int)hipSuccess;
+    if (C == nullptr || !intq_grid_ok(batch, out_features)) return (int)hipErrorInvalidValue;
+    if (in_features > 0 && (W == nullptr || B == nullptr || scales == nullptr || zeros == nullptr))
+        return (int)hipErrorInvalidValue;
+    const int ng = ceil_div(out_features, group_size);
+    const uint8_t* z = static_cast<const uint8_t*>(zeros);
+    if (batch <= 4 && in_features > 0) {
+        const int nw = max(1, min(16, in_features / 64));
+        const dim3 g(ceil_div(out_features / 2, 64)), b(nw * kWave);
+        const uint8_t* w = static_cast<const uint8_t*>(W);
+        switch (batch) {
+            case 1: int4_rmul_valu_kernel<1><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 2: int4_rmul_valu_kernel<2><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 3: int4_rmul_valu_kernel<3><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            default: int4_rmul_valu_kernel<4><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+        }
+    } else {
+        launch_intq_mfma<2>(stream, B, W, C, scales, z, batch, out_features, in_features, group_size, ng);
+    }
+    return (int)hipGetLastError();
+}

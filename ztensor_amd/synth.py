@@ -360,6 +360,11 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
         return rows * K // vals * nbytes + 4 * K * N + 4 * rows * N
     if fmt == "ternary_i8":
         return rows * ((K + 3) // 4) + K * N + 4 * rows * N + 8
+    if fmt == "int4":
+        ng = rows * (-(-K // group))
+        return rows * K // 2 + 5 * ng + 4 * K * N + 4 * rows * N
+    if fmt == "int8":
+        return rows * K + 4 * K * N + 4 * rows * N
     raise ValueError(fmt)
 
 
@@ -403,3 +408,44 @@ def fp8_wire(codes: np.ndarray, scale: float) -> np.ndarray:
     """The registry's FP8_E4M3 / FP8_E5M2 bytes: 4-byte LE fp32 scale, then
     one code byte per element (tensor/quant_registry.go:190-229)."""
     return np.concatenate([np.array([scale], "<f4").view(np.uint8), np.asarray(codes, np.uint8)])
+
+
+# ---- int4 / int8 GEMM operands (gemm_int4.h, gemm_int8.h)
+
+
+def pack_int4(v: np.ndarray) -> np.ndarray:
+    """Signed int4 values [-8, 7], row-major with an even row length, two a
+    byte: element 2b in the low nibble of byte b (gemm_int4.cu:20-27)."""
+    q = (np.asarray(v, np.int16) & 0xF).astype(np.uint8).reshape(v.shape[0], -1)
+    return (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+
+
+@dataclass
+class Int4Weights:
+    v: np.ndarray  # int8 [rows, cols], values -8..7
+    packed: np.ndarray  # uint8 [rows, cols/2]
+    scales: np.ndarray  # float32 [rows, ngroups]
+    zeros: np.ndarray  # uint8 [rows, ngroups]
+
+
+def int4(rows: int, cols: int, group: int, seed: int, zero_max: int = 15) -> Int4Weights:
+    """Random int4 weights, groups of `group` along each row of `cols`
+    values (the K of gemm_int4_f32, the out of gemm_int4_f32_rmul)."""
+    g = rng(seed)
+    v = g.integers(-8, 8, size=(rows, cols), dtype=np.int8)
+    ng = -(-cols // group)
+    scales = (np.abs(g.standard_normal((rows, ng), dtype=np.float32)) * np.float32(0.02) + np.float32(1e-3)).astype(
+        np.float32)
+    zeros = g.integers(0, zero_max + 1, size=(rows, ng), dtype=np.uint8)
+    return Int4Weights(v, pack_int4(v), scales, zeros)
+
+
+def int4_dense(w: Int4Weights, group: int) -> np.ndarray:
+    """float64 weights (v - zero) * scale, groups along each row."""
+    cols = w.v.shape[1]
+    gi = np.arange(cols) // group
+    return (w.v.astype(np.float64) - w.zeros[:, gi].astype(np.float64)) * w.scales[:, gi].astype(np.float64)
+
+
+def int8(rows: int, cols: int, seed: int) -> np.ndarray:
+    return rng(seed).integers(-128, 128, size=(rows, cols), dtype=np.int8)
