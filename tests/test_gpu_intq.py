@@ -6,7 +6,9 @@ through the C ABI.
 Bars: max|y - y_ref| / max|y_ref| <= 1e-5 with y_ref the oracle: every
 weight is dequantized as the reference does (one fp32 multiply) and every
 product is an fp32 product, so only the summation order differs.  Shapes:
-the streaming batch-1..4 kernels (K % 16 == 0, group_size % 16 == 0) and
+the streaming batch-1..4 kernels (K % 16 == 0, group_size % 16 == 0; K
+past one 4096-element activation chunk, rows not a multiple of a
+workgroup's; for X W out % 16 == 0, partial 256-column blocks) and
 the MFMA GEMM (every other shape: odd group sizes, K not a multiple of 16 or
 32, partial 64-row and 64-column tiles, batches past 4), the reference
 benchmark's square GEMMs at 1024 in full and at 4096 on sampled rows, and
@@ -74,7 +76,7 @@ def run_int8(lib, a, b, M, K, N):
 
 INT4_CASES = [  # M, K, N, group_size
     (4096, 4096, 1, 32), (4096, 4096, 1, 128), (14336, 4096, 1, 128), (4096, 4096, 4, 32), (333, 1024, 3, 64),
-    (1, 16, 1, 16), (4096, 4096, 2, 32),
+    (1, 16, 1, 16), (4096, 4096, 2, 32), (100, 4112, 4, 16), (33, 8208, 2, 48),
     # MFMA GEMM: group sizes not a multiple of 16, odd shapes, wider batches
     (1000, 1000, 2, 20), (77, 130, 5, 7), (65, 34, 9, 2), (512, 4096, 16, 128), (100, 2048, 64, 32), (3, 2, 1, 1),
 ]
@@ -92,6 +94,7 @@ def test_int4_nt(lib, orc, M, K, N, gs):
 RMUL_CASES = [  # batch, in, out, group_size
     (1, 4096, 4096, 32), (4, 4096, 4096, 128), (3, 1000, 1002, 7), (2, 64, 30, 16), (1, 1, 2, 1),
     (5, 512, 256, 32), (64, 1024, 1000, 32), (17, 33, 66, 5),
+    (3, 100, 272, 16), (2, 1000, 4112, 48), (4, 130, 32, 32), (1, 63, 16, 16),
 ]
 
 
@@ -106,7 +109,7 @@ def test_int4_rmul(lib, orc, batch, inf, outf, gs):
 
 INT8_CASES = [  # M, K, N
     (4096, 4096, 1), (4096, 14336, 1), (4096, 4096, 4), (1, 16, 1), (333, 1024, 3),
-    (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65),
+    (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65), (64, 4112, 2), (31, 8208, 4),
 ]
 
 

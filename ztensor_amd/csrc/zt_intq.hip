@@ -14,11 +14,14 @@
 //
 // Kernels:
 //  * batches of 1-4 on aligned shapes: VALU kernels that stream the weights
-//    once (intq_gemv_kernel for A B, int4_rmul_valu_kernel for X W);
+//    once (intq_gemv_kernel for A B, int4_rmul_valu_kernel for X W, the
+//    latter for out % 16 == 0 and group_size % 16 == 0);
 //  * every other call: intq_mfma_kernel, an LDS-tiled fp32 MFMA GEMM
 //    (v_mfma_f32_16x16x4f32) that dequantizes each weight on its way into
 //    LDS exactly as the reference does (one fp32 multiply), so every product
 //    is the reference's fp32 product and only the summation order differs.
+#include <type_traits>
+
 #include "zt_common.h"
 #include "zt_mfma.h"
 
@@ -31,7 +34,7 @@ __device__ __forceinline__ int sext8(uint32_t v, int i) { return ((int)(v << (24
 
 // ------------------------------------------------------------ A B, batch 1-4
 //
-// C[M, N] = dequant(A) B for N = NB in 1..4.  A wave owns R rows; lane l of
+// C[M, N] = dequant(A) B for N = NB = 1.  A wave owns R rows; lane l of
 // wave w takes 16-element chunks c = l + 64 (w + nwaves i) of K (int8: one
 // 16-byte load a row; int4: one 8-byte load, within one group since
 // group_size % 16 == 0) and the 16 N-wide activation rows of the chunk (4 NB
@@ -113,6 +116,112 @@ __global__ void __launch_bounds__(1024) intq_gemv_kernel(const uint8_t* __restri
     }
 }
 
+// Batches of 2-4: the kernel above reads the activation chunk of every
+// 16 elements once per R rows of a wave, 8 N / R times the weight bytes.
+// Here a wave owns R = 2 or 4 rows over all of K and the 8 waves of a workgroup
+// share the activations through LDS: chunks of 4096 elements (16 N KB) are
+// staged once per workgroup, in the order the lanes read them (a lane's
+// 16 N floats of step s as 4 N slots of 64 consecutive float4, so every
+// ds_read_b128 is conflict-free), while the chunk's weight loads (4 steps of
+// 1024 elements a row, all issued first) are in flight.  No cross-wave sum:
+// each wave reduces its own rows across its lanes.
+constexpr int kIqxKC = 4096;
+
+template <bool INT4, int NB, int R>
+__global__ void __launch_bounds__(512) intq_gemv_xlds_kernel(const uint8_t* __restrict__ A, const float* __restrict__ x,
+                                                             float* __restrict__ y, const float* __restrict__ scales,
+                                                             const uint8_t* __restrict__ zeros, int rows, int K, int gs,
+                                                             int ng) {
+    constexpr int S = kIqxKC / 1024, Q = 4 * NB;  // steps a chunk, float4 slots a step
+    __shared__ float4 xs[S * Q * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 8 + wave) * R;
+    const long rowbytes = INT4 ? K / 2 : K;
+    int rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rr[r] = min(row0 + r, rows - 1);
+    float acc[NB][R];
+#pragma unroll
+    for (int n = 0; n < NB; n++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[n][r] = 0.0f;
+    for (int kc0 = 0; kc0 < K; kc0 += kIqxKC) {
+        const int kn = min(kIqxKC, K - kc0);
+        typedef typename std::conditional<INT4, uint2, uint4>::type WT;
+        WT w[S][R];
+        float sc[S][R];
+        int zr[S][R];
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            const int e = 1024 * st + 16 * lane;  // first element of the lane's 16 in the chunk
+            const bool ok = e < kn;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const long off = rr[r] * rowbytes + (long)(ok ? kc0 + e : 0) / (INT4 ? 2 : 1);
+                if constexpr (INT4) {
+                    w[st][r] = ok ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
+                    const long gi = (long)rr[r] * ng + (ok ? kc0 + e : 0) / gs;
+                    sc[st][r] = scales[gi];
+                    zr[st][r] = zeros[gi];
+                } else {
+                    w[st][r] = ok ? *reinterpret_cast<const uint4*>(A + off) : make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+        }
+        if (kc0 > 0) __syncthreads();  // every wave is done with the previous chunk
+        const float4* xg = reinterpret_cast<const float4*>(x + (long)kc0 * NB);
+        for (int t = threadIdx.x; t < kn * NB / 4; t += 512) {
+            const int st = t / (256 * NB), f = 4 * (t % (256 * NB));  // step, float index within the step
+            const int ln = f / (16 * NB), q = (f % (16 * NB)) / 4;
+            xs[(st * Q + q) * 64 + ln] = xg[t];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            if (1024 * st + 16 * lane >= kn) continue;
+            float xv[16 * NB];
+#pragma unroll
+            for (int q = 0; q < Q; q++) {
+                const float4 v = xs[(st * Q + q) * 64 + lane];
+                xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                if constexpr (INT4) {
+                    float ag[NB];
+#pragma unroll
+                    for (int n = 0; n < NB; n++) ag[n] = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t d = e < 8 ? w[st][r].x : w[st][r].y;
+                        const float v = (float)(sext4(d >> (4 * (e & 7))) - zr[st][r]);
+#pragma unroll
+                        for (int n = 0; n < NB; n++) ag[n] = __builtin_fmaf(v, xv[e * NB + n], ag[n]);
+                    }
+#pragma unroll
+                    for (int n = 0; n < NB; n++) acc[n][r] = __builtin_fmaf(sc[st][r], ag[n], acc[n][r]);
+                } else {
+                    const uint32_t d4[4] = {w[st][r].x, w[st][r].y, w[st][r].z, w[st][r].w};
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float v = (float)sext8(d4[e >> 2], e & 3);
+#pragma unroll
+                        for (int n = 0; n < NB; n++) acc[n][r] = __builtin_fmaf(v, xv[e * NB + n], acc[n][r]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NB; n++) {
+        wave_reduce_rows<R>(acc[n]);
+        if (is_row_writer<R>(lane)) {
+            const int row = row0 + row_of_lane<R>(lane);
+            if (row < rows) y[(long)row * NB + n] = acc[n][0];
+        }
+    }
+}
+
 template <bool INT4, int NB>
 static void launch_intq_gemv_r(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* A, const float* x, float* y,
                                const float* s, const uint8_t* z, int M, int K, int gs, int ng) {
@@ -127,73 +236,133 @@ static void launch_intq_gemv_r(int R, dim3 g, dim3 b, hipStream_t st, const uint
 template <bool INT4>
 static void launch_intq_gemv(hipStream_t st, const uint8_t* A, const float* x, float* y, const float* s,
                              const uint8_t* z, int M, int K, int N, int gs, int ng) {
+    if (N >= 2) {
+        // 4 rows a wave from 8192 rows (>= 256 workgroups), else 2
+        const bool r4 = M >= 8192;
+        const dim3 g(ceil_div(M, r4 ? 32 : 16)), b(512);
+        switch (N) {
+            case 2:
+                if (r4) intq_gemv_xlds_kernel<INT4, 2, 4><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                else intq_gemv_xlds_kernel<INT4, 2, 2><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                break;
+            case 3:
+                if (r4) intq_gemv_xlds_kernel<INT4, 3, 4><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                else intq_gemv_xlds_kernel<INT4, 3, 2><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                break;
+            default:
+                if (r4) intq_gemv_xlds_kernel<INT4, 4, 4><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                else intq_gemv_xlds_kernel<INT4, 4, 2><<<g, b, 0, st>>>(A, x, y, s, z, M, K, gs, ng);
+                break;
+        }
+        return;
+    }
     const int nchunks = K / 16;
     const int nw = max(1, min(16, ceil_div(nchunks, 64)));
-    // fewer rows a wave for wider batches: acc holds N x R values
-    int R = pick_rows_per_wave(M, nw, 1, 2048);
-    if (N > 2 && R > 4) R = 4;
-    const dim3 g(ceil_div(M, R)), b(nw * kWave);
-    switch (N) {
-        case 1: launch_intq_gemv_r<INT4, 1>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
-        case 2: launch_intq_gemv_r<INT4, 2>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
-        case 3: launch_intq_gemv_r<INT4, 3>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
-        default: launch_intq_gemv_r<INT4, 4>(R, g, b, st, A, x, y, s, z, M, K, gs, ng); break;
-    }
+    const int R = pick_rows_per_wave(M, nw, 1, 2048);
+    launch_intq_gemv_r<INT4, 1>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, A, x, y, s, z, M, K, gs, ng);
 }
 
 // ------------------------------------------------------------ X W, batch 1-4
 //
-// C[b, j] = sum_k X[b, k] w[k, j], batch NB in 1..4.  Lane l of workgroup
-// g owns the byte column p = 64 g + l of W, outputs 2p and 2p+1, whose
-// groups are fixed for the whole call; the 16 waves of the workgroup take
-// contiguous K ranges in turn, each row a 64-byte coalesced load, and sum
-// their ranges through LDS in wave order.  Each weight is dequantized as the
-// reference does, float32(v - zero) * scale, then multiplied into the
-// accumulators.
-template <int NB>
+// C[b, j] = sum_k X[b, k] w[k, j], batch NB in 1..4, out % 16 == 0 and
+// group_size % 16 == 0.  A workgroup of 16 waves owns 64 output columns:
+// lane l owns columns 16 (l % 4) .. +15 (one 8-byte load a row, all in one
+// group) and row phase l / 4, so a load instruction reads 16 rows x 32
+// bytes; wave w takes the w-th sixteenth of K, and U rows a lane are loaded
+// before any is used (at K = 4096 that is all of the lane's rows).  Per row
+// the lane forms t = X[b, k] * scale and adds t * float(v - zero) for its 16
+// columns (the reference rounds float(v - zero) * scale first, then
+// multiplies by X: the two differ by one fp32 rounding per product).  The 16
+// row phases are added by lane shuffles, the 16 waves through LDS in wave
+// order.
+template <int NB, int U>
 __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __restrict__ W,
                                                               const float* __restrict__ X, float* __restrict__ C,
                                                               const float* __restrict__ scales,
                                                               const uint8_t* __restrict__ zeros, int K, int Nout,
                                                               int gs, int ng) {
-    __shared__ float red[16][2 * NB][64];
+    __shared__ float red[16][4][16 * NB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int npairs = Nout / 2;
-    const int p = blockIdx.x * 64 + lane;
-    const int pc = min(p, npairs - 1);
-    const int g0 = 2 * pc / gs, g1 = (2 * pc + 1) / gs;
-    const int kc = (K + nwaves - 1) / nwaves;
-    const int k0 = wave * kc, k1 = min(K, k0 + kc);
-    float acc[NB][2];
+    const int cl = lane & 3, ph = lane >> 2;
+    const int col = blockIdx.x * 64 + 16 * cl;  // first of the lane's 16 columns
+    const bool colok = col < Nout;
+    const int cc = colok ? col : 0;
+    const int g = cc / gs;
+    const long rowbytes = Nout / 2;
+    const int kw = (K + nwaves - 1) / nwaves;
+    const int kbeg = wave * kw, kend = min(K, kbeg + kw);
+    float acc[NB][16];
 #pragma unroll
-    for (int n = 0; n < NB; n++) acc[n][0] = acc[n][1] = 0.0f;
-#pragma unroll 8
-    for (int k = k0; k < k1; k++) {
-        const uint32_t b = W[(long)k * npairs + pc];
-        const long sb = (long)k * ng;
-        const float w0 = (float)(sext4(b) - (int)zeros[sb + g0]) * scales[sb + g0];
-        const float w1 = (float)(sext4(b >> 4) - (int)zeros[sb + g1]) * scales[sb + g1];
+    for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int n = 0; n < NB; n++) {
-            const float xv = X[(long)n * K + k];
-            acc[n][0] = __builtin_fmaf(xv, w0, acc[n][0]);
-            acc[n][1] = __builtin_fmaf(xv, w1, acc[n][1]);
+        for (int j = 0; j < 16; j++) acc[b][j] = 0.0f;
+    for (int k0 = kbeg + ph; k0 < kend; k0 += 16 * U) {
+        uint2 w[U];
+        float s[U], xv[U][NB];
+        int z[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + 16 * u;
+            const bool ok = colok && k < kend;
+            const int kk = ok ? k : kbeg;
+            w[u] = ok ? *reinterpret_cast<const uint2*>(W + (long)kk * rowbytes + cc / 2) : make_uint2(0u, 0u);
+            s[u] = scales[(long)kk * ng + g];
+            z[u] = zeros[(long)kk * ng + g];
+#pragma unroll
+            for (int b = 0; b < NB; b++) xv[u][b] = ok ? X[(long)b * K + kk] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float t[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) t[b] = xv[u][b] * s[u];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t d = j < 8 ? w[u].x : w[u].y;
+                const float v = (float)(sext4(d >> (4 * (j & 7))) - z[u]);
+#pragma unroll
+                for (int b = 0; b < NB; b++) acc[b][j] = __builtin_fmaf(t[b], v, acc[b][j]);
+            }
         }
     }
+    // row phases (lane bits 2-5) into lanes 0..3
 #pragma unroll
-    for (int n = 0; n < NB; n++) {
-        red[wave][2 * n][lane] = acc[n][0];
-        red[wave][2 * n + 1][lane] = acc[n][1];
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            float v = acc[b][j];
+            v += __shfl_xor(v, 4);
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[b][j] = v;
+        }
+    if (ph == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) red[wave][cl][16 * b + j] = acc[b][j];
     }
     __syncthreads();
-    if (wave == 0 && p < npairs) {
-#pragma unroll
-        for (int j = 0; j < 2 * NB; j++) {
-            float s = 0.0f;
-            for (int w = 0; w < nwaves; w++) s += red[w][j][lane];
-            C[(long)(j >> 1) * Nout + 2 * p + (j & 1)] = s;
+    // outputs (b, column) over the workgroup's threads, the waves summed in order
+    for (int t = threadIdx.x; t < 64 * NB; t += blockDim.x) {
+        const int b = t >> 6, c = t & 63;
+        const int n = blockIdx.x * 64 + c;
+        if (n < Nout) {
+            float sum = 0.0f;
+            for (int w = 0; w < nwaves; w++) sum += red[w][c >> 4][16 * b + (c & 15)];
+            C[(long)b * Nout + n] = sum;
         }
     }
+}
+
+template <int NB>
+static void launch_int4_rmul_valu(hipStream_t st, const uint8_t* W, const float* X, float* C, const float* s,
+                                  const uint8_t* z, int K, int Nout, int gs, int ng) {
+    const int nw = max(1, min(16, K / 256));
+    const dim3 g(ceil_div(Nout, 64)), b(nw * kWave);
+    constexpr int U = NB == 1 ? 16 : NB == 2 ? 8 : NB == 3 ? 4 : 2;  // within 128 VGPRs (1024-thread workgroups)
+    int4_rmul_valu_kernel<NB, U><<<g, b, 0, st>>>(W, X, C, s, z, K, Nout, gs, ng);
 }
 
 // ------------------------------------------------------------ fp32 MFMA GEMM
@@ -429,15 +598,13 @@ ZT_EXPORT int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, con
         return (int)hipErrorInvalidValue;
     const int ng = ceil_div(out_features, group_size);
     const uint8_t* z = static_cast<const uint8_t*>(zeros);
-    if (batch <= 4 && in_features > 0) {
-        const int nw = max(1, min(16, in_features / 64));
-        const dim3 g(ceil_div(out_features / 2, 64)), b(nw * kWave);
-        const uint8_t* w = static_cast<const uint8_t*>(W);
+    const uint8_t* w = static_cast<const uint8_t*>(W);
+    if (batch <= 4 && in_features > 0 && out_features % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)w & 7) == 0) {
         switch (batch) {
-            case 1: int4_rmul_valu_kernel<1><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 2: int4_rmul_valu_kernel<2><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 3: int4_rmul_valu_kernel<3><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            default: int4_rmul_valu_kernel<4><<<g, b, 0, stream>>>(w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 1: launch_int4_rmul_valu<1>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 2: launch_int4_rmul_valu<2>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 3: launch_int4_rmul_valu<3>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            default: launch_int4_rmul_valu<4>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
         }
     } else {
         launch_intq_mfma<2>(stream, B, W, C, scales, z, batch, out_features, in_features, group_size, ng);
