@@ -46,6 +46,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "quant GEMV effective HBM GB/s (% of peak) at Llama-3-8B decode shapes, batch 1"
 PEAK_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 LLAMA3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
              ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]  # (name, rows=N_out, K)
 MALL_BYTES = 256 << 20
@@ -639,11 +640,23 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     gbs = nbytes / (us * 1e-6) / 1e9
     r = {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
          "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
-    if fmt in ("int4", "int4_rmul", "int8"):
-        # 2 M K N flops against the dense fp32 MFMA peak these kernels compute at
+    if fmt in ("int4", "int4_rmul", "int8") and N > 4:
+        # useful flops 2 M K N; the MFMA unit the call runs on (zt_intq.hip's dispatch) and its
+        # actual MFMA work: bf16 runs 3 MFMAs per product (int4: plus 3 all-ones MFMAs per column
+        # tile and step, over TI row tiles), fp32 one
         tf = 2.0 * rows * K * N / (us * 1e-6) / 1e12
         r["TFLOP/s"] = round(tf, 2)
-        r["pct_peak_fp32_mfma"] = round(100 * tf / PEAK_FP32_TFLOPS, 1)
+        bf16 = fmt != "int4_rmul" and K % 32 == 0 and N % 2 == 0
+        if bf16:
+            ti = 4 if -(-rows // 128) * -(-N // 128) >= 256 else 2
+            work = 3.0 if fmt == "int8" else 3.0 + 3.0 / ti
+            r["mfma"] = "bf16"
+            r["mfma_TFLOP/s"] = round(tf * work, 1)
+            r["pct_peak_mfma"] = round(100 * tf * work / PEAK_BF16_TFLOPS, 1)
+        else:
+            r["mfma"] = "fp32"
+            r["mfma_TFLOP/s"] = round(tf, 1)
+            r["pct_peak_mfma"] = round(100 * tf / PEAK_FP32_TFLOPS, 1)
     return r
 
 

@@ -8,12 +8,15 @@ weight is dequantized as the reference does (one fp32 multiply) and every
 product is an fp32 product, so only the summation order differs.  Shapes:
 the streaming batch-1..4 kernels (K % 16 == 0, group_size % 16 == 0; K
 past one 4096-element activation chunk, rows not a multiple of a
-workgroup's; for X W out % 16 == 0, partial 256-column blocks) and
-the MFMA GEMM (every other shape: odd group sizes, K not a multiple of 16 or
-32, partial 64-row and 64-column tiles, batches past 4), the reference
+workgroup's; for X W out % 16 == 0, partial column blocks), the bf16 MFMA
+GEMM (A B with K % 32 == 0, group_size % 32 == 0, even N; partial 128 x 128
+tiles, int4 zero points up to 255) and the fp32 MFMA GEMM (every other
+shape: odd group sizes, K not a multiple of 16 or 32, odd N, partial 64-row
+and 64-column tiles, X W past batch 4), the reference
 benchmark's square GEMMs at 1024 in full and at 4096 on sampled rows, and
 its inputs (bytes 0x53, scale 0.1, activations 0.01) at 4096 cubed on every
-output against the fp32 FMA chain of its k loop.
+output against the fp32 FMA chain of its k loop and the exact sum, within
+the summation bound K * 2^-24 that equal positive terms call for.
 """
 import numpy as np
 import pytest
@@ -79,6 +82,8 @@ INT4_CASES = [  # M, K, N, group_size
     (1, 16, 1, 16), (4096, 4096, 2, 32), (100, 4112, 4, 16), (33, 8208, 2, 48),
     # MFMA GEMM: group sizes not a multiple of 16, odd shapes, wider batches
     (1000, 1000, 2, 20), (77, 130, 5, 7), (65, 34, 9, 2), (512, 4096, 16, 128), (100, 2048, 64, 32), (3, 2, 1, 1),
+    # bf16 MFMA GEMM (K % 32, group % 32, N even): partial 128 x 128 tiles
+    (130, 96, 6, 32), (300, 4128, 130, 96), (64, 64, 8, 64),
 ]
 
 
@@ -110,6 +115,7 @@ def test_int4_rmul(lib, orc, batch, inf, outf, gs):
 INT8_CASES = [  # M, K, N
     (4096, 4096, 1), (4096, 14336, 1), (4096, 4096, 4), (1, 16, 1), (333, 1024, 3),
     (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65), (64, 4112, 2), (31, 8208, 4),
+    (200, 4128, 130), (129, 32, 6),
 ]
 
 
@@ -120,6 +126,19 @@ def test_int8(lib, orc, M, K, N):
     b = synth.x_f32(K * N, 501 + N).reshape(K, N)
     y = run_int8(lib, a, b, M, K, N)
     assert rel_err(y, orc.gemm_int8_f32(a, b, M, K, N)) <= TOL
+
+
+@pytest.mark.parametrize("zmax", [255, 0])
+def test_int4_nt_zero_points_full_range(lib, orc, zmax):
+    """uint8 zero points up to 255 (v - z down to -263) and all zero, on the
+    bf16 MFMA GEMM, whose int4 operand is 128 + (v ^ 8) with the offset
+    136 + z applied through an all-ones product."""
+    M, K, N, gs = 256, 1024, 32, 64
+    say(f"int4 zeros<={zmax}")
+    w = synth.int4(M, K, gs, 320 + zmax, zero_max=zmax)
+    b = synth.x_f32(K * N, 321).reshape(K, N)
+    y = run_int4(lib, w, b, M, K, N, gs)
+    assert rel_err(y, orc.gemm_int4_f32(w.packed, b, w.scales, w.zeros, M, K, N, gs)) <= TOL
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "rmul"])
@@ -164,9 +183,15 @@ def test_reference_benchmark_square_4096_sampled_rows(lib, orc, fmt):
 
 def test_reference_benchmark_inputs_4096_every_output(lib):
     """gemm_bench_test.go's inputs at 4096 cubed (int4: bytes 0x53, scale 0.1,
-    zero 0, group 32; int8: bytes 42; activations 0.01): every output equals
-    the fp32 FMA chain of the reference kernel's k loop within the bar."""
+    zero 0, group 32; int8: bytes 42; activations 0.01).  Every term of a sum
+    is equal and positive, so the rounding errors of any fp32 summation order
+    add up instead of cancelling: the reference kernel's sequential FMA chain
+    (replayed exactly in long double) ends 2.0e-5 above the exact sum, and a
+    different order may land on the other side.  The bar for these inputs is
+    therefore the summation bound K * 2^-24 (2.4e-4), against both the chain
+    and the exact value; the random-operand tests above keep 1e-5."""
     n = 4096
+    bound = n * 2.0 ** -24
     say("benchmark inputs 4096")
     x = np.full((n, n), 0.01, np.float32)
     w = synth.Int4Weights(np.zeros((1, 1), np.int8), np.full((n, n // 2), 0x53, np.uint8),
@@ -176,12 +201,18 @@ def test_reference_benchmark_inputs_4096_every_output(lib):
     acc = np.float32(0.0)
     for k in range(n):
         acc = np.float32(np.longdouble(acc) + np.longdouble(dq[k & 1]) * np.longdouble(np.float32(0.01)))
-    assert rel_err(y, np.full(n * n, acc)) <= TOL
+    exact = n // 2 * (np.float64(dq[0]) + np.float64(dq[1])) * np.float64(np.float32(0.01))
+    assert rel_err(y, np.full(n * n, acc)) <= bound
+    assert rel_err(y, np.full(n * n, exact)) <= bound
+    assert np.all(y == y[0])  # every output is the same sum
     y8 = run_int8(lib, np.full((n, n), 42, np.int8), x, n, n, n)
     acc8 = np.float32(0.0)
     for _ in range(n):
         acc8 = np.float32(np.longdouble(acc8) + np.longdouble(42) * np.longdouble(np.float32(0.01)))
-    assert rel_err(y8, np.full(n * n, acc8)) <= TOL
+    exact8 = n * 42 * np.float64(np.float32(0.01))
+    assert rel_err(y8, np.full(n * n, acc8)) <= bound
+    assert rel_err(y8, np.full(n * n, exact8)) <= bound
+    assert np.all(y8 == y8[0])
 
 
 def test_zero_k_writes_zeros_and_empty_calls(lib):

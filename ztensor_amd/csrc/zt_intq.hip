@@ -16,6 +16,8 @@
 //  * batches of 1-4 on aligned shapes: VALU kernels that stream the weights
 //    once (intq_gemv_kernel for A B, int4_rmul_valu_kernel for X W, the
 //    latter for out % 16 == 0 and group_size % 16 == 0);
+//  * wider batches of A B with K % 32 == 0 (int4: group_size % 32 == 0) and
+//    an even N: intq_bf16_kernel, bf16 MFMA on exact three-part activations;
 //  * every other call: intq_mfma_kernel, an LDS-tiled fp32 MFMA GEMM
 //    (v_mfma_f32_16x16x4f32) that dequantizes each weight on its way into
 //    LDS exactly as the reference does (one fp32 multiply), so every product
@@ -545,6 +547,226 @@ __global__ void __launch_bounds__(256) intq_mfma_kernel(const void* __restrict__
         }
 }
 
+// ------------------------------------------------------------ bf16 MFMA GEMM
+//
+// C[M, N] = dequant(A) B on bf16 MFMA (v_mfma_f32_16x16x32_bf16), exact
+// to fp32 accumulation: every fp32 activation is split into three bf16
+// parts, x = b1 + b2 + b3 (b1 = x with its low 16 bits cleared, b2 the same
+// of x - b1, b3 = x - b1 - b2, which has at most 8 significant bits), so
+// each bf16 x bf16 product is exact and only the fp32 sums round.  The
+// weights enter exactly too:
+//   int8: float(q) has at most 8 significant bits, so it is a bf16 exactly;
+//   int4: 128 + (v ^ 8) as the bf16 0x4300 | u' (u' = nibble ^ 8 in 0..15),
+//     with v - z = u' - (8 + z); an all-ones A operand gives sum_k x per
+//     column and step, and each output takes s * (D - (136 + z) Dx), s and
+//     z of its row and the step's group (group_size % 32 == 0).
+// A workgroup of 4 waves owns a 32 TI x 32 TI tile of C, each wave
+// 16 TI x 16 TI (TI x TI MFMA tiles; TI = 4, or 2 when 128 x 128 tiles would
+// leave fewer than 256 workgroups); K advances 32 a step.  Weight A operands come straight from
+// global memory (lane 16 g + i: 8 consecutive K values of row i, one 8-byte
+// int8 or 4-byte int4 load); the activation tile is split into its parts
+// and staged in LDS as [part][column][32 K values in operand order], read
+// with one ds_read_b128 a part, tile and step; the next step's loads are in
+// flight during the current step's MFMAs.  int4 slot order within 8 K values
+// is 0 4 1 5 2 6 3 7, the order the nibble masks 0x000F000F yield.
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+constexpr int kBfLP = 40;  // LDS row: 32 bf16 + 8 pad
+
+__device__ __forceinline__ uint32_t hi16_pack(float a, float b) {
+    // (bf16 bits of a) | (bf16 bits of b) << 16, both exact truncations
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+template <bool INT4, int TI>
+__global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restrict__ A, const float* __restrict__ B,
+                                                        float* __restrict__ C, const float* __restrict__ scales,
+                                                        const uint8_t* __restrict__ zeros, int M, int N, int K, int gs,
+                                                        int ng) {
+    constexpr int TM = 32 * TI, TN = 32 * TI, CP = 16 * TI;  // tile, column pairs
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][3][TN][kBfLP];
+    __shared__ float scs[2][TM], zzs[2][TM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    int byi = blockIdx.y, bxi = blockIdx.x;
+    const int m0 = byi * TM, n0 = bxi * TN;
+    const int wm = (wave & 1) * 16 * TI, wn = (wave >> 1) * 16 * TI;
+    const long rowbytes = INT4 ? K / 2 : K;
+    // this lane's A rows (one per row tile), clamped; rows past M load zeros
+    int arow[TI];
+    bool aok[TI];
+#pragma unroll
+    for (int i = 0; i < TI; i++) {
+        const int m = m0 + wm + 16 * i + li;
+        aok[i] = m < M;
+        arow[i] = aok[i] ? m : 0;
+    }
+    // activation staging role: column pair cp, K octet ko (threads past 4 octets idle)
+    const int cp = tid % CP, ko = tid / CP;
+    const bool stager = TI == 4 || ko < 4;  // every thread stages with 128-column tiles
+    const int bn = n0 + 2 * cp;
+    const bool bok = stager && bn < N;
+
+    uint2 araw8[TI];
+    uint32_t araw4[TI];
+    float2 braw[8];
+    float sreg = 0.0f, zreg = 0.0f;
+    auto load_step = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+            const long off = (long)arow[i] * rowbytes + (INT4 ? (k0 + 8 * lg) / 2 : k0 + 8 * lg);
+            if constexpr (INT4)
+                araw4[i] = aok[i] ? *reinterpret_cast<const uint32_t*>(A + off) : 0x88888888u;  // u' = 0
+            else
+                araw8[i] = aok[i] ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+            braw[r] = bok ? *reinterpret_cast<const float2*>(B + (long)(k0 + 8 * ko + r) * N + bn) : make_float2(0.f, 0.f);
+        if constexpr (INT4) {
+            if (tid < TM && k0 % gs == 0) {
+                const int m = m0 + tid;
+                const long gi = (long)(m < M ? m : 0) * ng + k0 / gs;
+                sreg = m < M ? scales[gi] : 0.0f;
+                zreg = 136.0f + (float)zeros[gi];
+            }
+        }
+    };
+    auto stage = [&](int buf, int k0) {
+        // B parts: for each of the 2 columns, 8 K values in slot order
+#pragma unroll
+        for (int c = 0; c < 2 && stager; c++) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int r = INT4 ? ((j & 1) ? 4 + (j >> 1) : (j >> 1)) : j;  // slot j holds K offset r
+                v[j] = c == 0 ? braw[r].x : braw[r].y;
+            }
+            uint32_t p1[4], p2[4], p3[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float a = v[2 * q], b = v[2 * q + 1];
+                const float a1 = __uint_as_float(__float_as_uint(a) & 0xFFFF0000u);
+                const float b1 = __uint_as_float(__float_as_uint(b) & 0xFFFF0000u);
+                const float ar = a - a1, br = b - b1;
+                const float a2 = __uint_as_float(__float_as_uint(ar) & 0xFFFF0000u);
+                const float b2 = __uint_as_float(__float_as_uint(br) & 0xFFFF0000u);
+                p1[q] = hi16_pack(a1, b1);
+                p2[q] = hi16_pack(a2, b2);
+                p3[q] = hi16_pack(ar - a2, br - b2);
+            }
+            const int n = 2 * cp + c;
+            *reinterpret_cast<u32x4*>(&Bs[buf][0][n][8 * ko]) = (u32x4){p1[0], p1[1], p1[2], p1[3]};
+            *reinterpret_cast<u32x4*>(&Bs[buf][1][n][8 * ko]) = (u32x4){p2[0], p2[1], p2[2], p2[3]};
+            *reinterpret_cast<u32x4*>(&Bs[buf][2][n][8 * ko]) = (u32x4){p3[0], p3[1], p3[2], p3[3]};
+        }
+        if constexpr (INT4) {
+            if (tid < TM) {
+                // the group changes only at a multiple of gs; otherwise carry the last one
+                scs[buf][tid] = sreg;
+                zzs[buf][tid] = zreg;
+            }
+        }
+        (void)k0;
+    };
+
+    float4v acc[TI][TI];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TI; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+    const int nsteps = K / 32;
+    load_step(0);
+    stage(0, 0);
+    __syncthreads();
+    for (int t = 0; t < nsteps; t++) {
+        const int buf = t & 1;
+        // decode this step's A operands before the next step's loads overwrite the registers
+        u32x4 av[TI];
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+            if constexpr (INT4) {
+                const uint32_t d = araw4[i] ^ 0x88888888u;
+                av[i] = (u32x4){(d & 0x000F000Fu) | 0x43004300u, ((d >> 4) & 0x000F000Fu) | 0x43004300u,
+                                ((d >> 8) & 0x000F000Fu) | 0x43004300u, ((d >> 12) & 0x000F000Fu) | 0x43004300u};
+            } else {
+                const uint32_t w2[2] = {araw8[i].x, araw8[i].y};
+                uint32_t q[4];
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const uint32_t wd = w2[h >> 1];
+                    const int b0 = 2 * (h & 1);
+                    q[h] = hi16_pack((float)sext8(wd, b0), (float)sext8(wd, b0 + 1));
+                }
+                av[i] = (u32x4){q[0], q[1], q[2], q[3]};
+            }
+        }
+        if (t + 1 < nsteps) load_step(32 * (t + 1));
+        float4v sc4[TI], zz4[TI];
+        if constexpr (INT4) {
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+                sc4[i] = *reinterpret_cast<const float4v*>(&scs[buf][wm + 16 * i + 4 * lg]);
+                zz4[i] = *reinterpret_cast<const float4v*>(&zzs[buf][wm + 16 * i + 4 * lg]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TI; j++) {
+            const int n = wn + 16 * j + li;
+            bf16x8v bp[3];
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                bp[p] = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const u32x4*>(&Bs[buf][p][n][8 * lg]));
+            if constexpr (INT4) {
+                const bf16x8v ones = __builtin_bit_cast(bf16x8v, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+                float4v dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[1], dx, 0, 0, 0);
+                dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[2], dx, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const bf16x8v a = __builtin_bit_cast(bf16x8v, av[i]);
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[2], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[i][j][r] = __builtin_fmaf(sc4[i][r], __builtin_fmaf(-zz4[i][r], dx[r], d[r]), acc[i][j][r]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const bf16x8v a = __builtin_bit_cast(bf16x8v, av[i]);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[0], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[1], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[2], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        // the other buffer was last read in step t - 1, before the barrier that ended it
+        if (t + 1 < nsteps) stage(buf ^ 1, 32 * (t + 1));
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TI; j++) {
+            const int n = n0 + wn + 16 * j + li;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + 16 * i + 4 * lg + r;
+                if (m < M && n < N) C[(long)m * N + n] = acc[i][j][r];
+            }
+        }
+}
+
+template <bool INT4>
+static void launch_intq_bf16(hipStream_t st, const uint8_t* A, const float* B, float* C, const float* s,
+                             const uint8_t* z, int M, int N, int K, int gs, int ng) {
+    if ((long)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
+        intq_bf16_kernel<INT4, 4><<<dim3(ceil_div(N, 128), ceil_div(M, 128)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+    else
+        intq_bf16_kernel<INT4, 2><<<dim3(ceil_div(N, 64), ceil_div(M, 64)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+}
+
 template <int V>
 static void launch_intq_mfma(hipStream_t st, const void* A, const void* B, float* C, const float* s, const uint8_t* z,
                              int M, int N, int K, int gs, int ng) {
@@ -566,6 +788,8 @@ ZT_EXPORT int zt_gemm_int8_f32(const void* A, const float* B, float* C, int M, i
     const uint8_t* a = static_cast<const uint8_t*>(A);
     if (N <= 4 && K > 0 && K % 16 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)B & 15) == 0)
         launch_intq_gemv<false>(stream, a, B, C, nullptr, nullptr, M, K, N, 1, 1);
+    else if (K > 0 && K % 32 == 0 && N % 2 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 7) == 0)
+        launch_intq_bf16<false>(stream, a, B, C, nullptr, nullptr, M, N, K, 1, 1);
     else
         launch_intq_mfma<0>(stream, A, B, C, nullptr, nullptr, M, N, K, 1, 1);
     return (int)hipGetLastError();
@@ -583,6 +807,9 @@ ZT_EXPORT int zt_gemm_int4_f32(const void* A, const float* B, float* C, const fl
     const uint8_t* z = static_cast<const uint8_t*>(zeros);
     if (N <= 4 && K > 0 && K % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 15) == 0)
         launch_intq_gemv<true>(stream, a, B, C, scales, z, M, K, N, group_size, ng);
+    else if (K > 0 && K % 32 == 0 && group_size % 32 == 0 && N % 2 == 0 && ((uintptr_t)a & 3) == 0 &&
+             ((uintptr_t)B & 7) == 0)
+        launch_intq_bf16<true>(stream, a, B, C, scales, z, M, N, K, group_size, ng);
     else
         launch_intq_mfma<1>(stream, A, B, C, scales, z, M, N, K, group_size, ng);
     return (int)hipGetLastError();
