@@ -807,7 +807,7 @@ CONFIGS = {
     "1_w4a16_gemv": ["w4a16sz_c1"],
     "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
     "3_ternary_bitnet": ["ternary"],
-    "4_w4a16_llama3_70b": ["w4a16sz_70b", "w4a16_70b_k28672", "w4a16t_70b"],
+    "4_w4a16_llama3_70b": ["w4a16sz_70b", "w4a16sz_70b_k28672", "w4a16t_70b"],
     "5_iq4nl_qwen2_7b": [("iq4nl", [1]), "iq4nlt"],
 }
 

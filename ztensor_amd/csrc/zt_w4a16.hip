@@ -230,21 +230,24 @@ static void launch_w4a16_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint3
 //  * SZ = true: szr holds one dword per (row, group), scale | zero << 16,
 //    row-major (zt_w4a16_pack_szr): one load per row and step.  At
 //    28672 x 8192 this measured 23.4 us against 27.6 us for the two loads.
+//  The arguments fit the 14 kernel-argument dwords gfx950 preloads into
+//  SGPRs (meta = szr for SZ, else the scales), and the group of chunk c is
+//  int((c + 0.5) * (1 / chunks_per_group)) in fp32, exact for every c <= 1024
+//  and up to 4096 chunks a group (checked exhaustively: the 0.5 margin dwarfs
+//  the product's rounding), so no wave waits on an argument load or an
+//  integer division before its scale loads.
 template <int S, int R, bool SZ>
 __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __restrict__ packed,
-                                                           const uint16_t* __restrict__ scales,
+                                                           const void* __restrict__ meta,
                                                            const uint16_t* __restrict__ zeros,
-                                                           const uint32_t* __restrict__ szr,
                                                            const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                           int rows, int nchunk, int chunks_per_group) {
+                                                           int rows, int nchunk, int ngroups, float inv_cpg) {
     __shared__ float red[16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 3;
-    const int ngroups = nchunk / chunks_per_group;
     const int row0 = blockIdx.x * R;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)packed, (short)0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(SZ ? (void*)szr : (void*)scales, (short)0,
-                                                                        0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)meta, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, zeros ? 0x7fffffff : 0,
                                                                         0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nchunk * 64, 0x00020000);
@@ -265,7 +268,7 @@ __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __res
 #pragma unroll
     for (int t = 0; t < S; t++) {
         const int c = (wave * S + t) * 16 + (lane >> 2);
-        const uint32_t g = (uint32_t)(c / chunks_per_group);
+        const uint32_t g = (uint32_t)(((float)c + 0.5f) * inv_cpg);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t rowg = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)ngroups;
@@ -317,11 +320,14 @@ template <int S, bool SZ>
 static void launch_w4a16_steps(int R, dim3 g, dim3 b, hipStream_t st, const uint32_t* w, const uint16_t* s,
                                const uint16_t* z, const uint32_t* szr, const uint16_t* x, float* y, int rows,
                                int nchunk, int cpg) {
+    const void* meta = SZ ? static_cast<const void*>(szr) : static_cast<const void*>(s);
+    const int ngroups = nchunk / cpg;
+    const float inv = 1.0f / (float)cpg;
     switch (R) {
-        case 8: w4a16_steps_kernel<S, 8, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
-        case 4: w4a16_steps_kernel<S, 4, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
-        case 2: w4a16_steps_kernel<S, 2, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
-        default: w4a16_steps_kernel<S, 1, SZ><<<g, b, 0, st>>>(w, s, z, szr, x, y, rows, nchunk, cpg); break;
+        case 8: w4a16_steps_kernel<S, 8, SZ><<<g, b, 0, st>>>(w, meta, z, x, y, rows, nchunk, ngroups, inv); break;
+        case 4: w4a16_steps_kernel<S, 4, SZ><<<g, b, 0, st>>>(w, meta, z, x, y, rows, nchunk, ngroups, inv); break;
+        case 2: w4a16_steps_kernel<S, 2, SZ><<<g, b, 0, st>>>(w, meta, z, x, y, rows, nchunk, ngroups, inv); break;
+        default: w4a16_steps_kernel<S, 1, SZ><<<g, b, 0, st>>>(w, meta, z, x, y, rows, nchunk, ngroups, inv); break;
     }
 }
 

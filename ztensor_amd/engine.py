@@ -437,10 +437,10 @@ class ROCmEngine:
             if n in _TILED_BATCHES and tiled_ok:
                 wt, sz = self._w4a16_tiled(s, rows, k)
                 self.gemm_w4a16t_f32(_p(wt), _p(sz), _p(x), _p(c), rows, k, n, s.group_size)
-            elif (n == 1 and s._gpu_szr is not None and k <= 16384 and rows * k // 2 < 1 << 31
+            elif (n == 1 and s._gpu_szr is not None and k <= 32768 and rows * k // 2 < 1 << 31
                   and _p(x) % 16 == 0):
-                # packed (scale, zero) dwords, one load a row and step instead of two: 2-20%
-                # faster for K <= 16384 (3.98 against 4.08 us at 4096 x 4096); at K = 28672 they tie
+                # packed (scale, zero) dwords, one load a row and step instead of two: faster at every
+                # Llama-3 shape (3.73 against 3.88 us at 4096 x 4096, 26.3 against 27.8 us at K = 28672)
                 self.lib.call("zt_gemv_w4a16sz_f32", _p(buf.tensor), _p(s._gpu_szr), _p(x), _p(c), rows, k,
                               s.group_size, self._s)
             else:
