@@ -135,8 +135,9 @@ long zt_iq4nl_tiled_scale_bytes(int M, int K);
 int zt_iq4nl_tile(const void* A_iq4, int M, int K, int data_offset, void* W_tiled, void* S_tiled, zt_stream_t stream);
 /* C[M, N] = dequant(W) B on the tiled layout, B fp16 [K, N] 16-byte
  * aligned, N in {4, 8, 12, 16}, K % 128 == 0, else InvalidValue.  The
- * codebook enters the MFMAs rounded to fp16 (relative error at most 2^-11
- * per entry).  When K is split across workgroups, each split stores its
+ * codebook enters the MFMAs as two fp16 parts whose sum is within
+ * 2^-22.3 of each entry (relative), so the products match the reference's
+ * fp32 table to that bound and only fp32 summation order differs.  When K is split across workgroups, each split stores its
  * partial tiles to `workspace` (16-byte aligned, at least
  * zt_gemm_iq4nlt_workspace_bytes(M, K, N) bytes, 0 when K is not split)
  * and a second kernel sums them in split order: C is the same on every

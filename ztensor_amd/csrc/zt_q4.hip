@@ -53,6 +53,19 @@ __device__ __forceinline__ uint2 iq4_pair_entry(int i) {
                       (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16));
 }
 
+// Table entry for a data byte i of the tiled MFMA kernel: (T_hi of the low
+// nibble, T_hi of the high nibble, T_lo of the low, T_lo of the high) as
+// fp16, with T_lo = fp16(T - T_hi) unscaled (subnormal for the smallest
+// entries).  T_hi + T_lo is within 2^-22.3 |T| of every codebook value
+// (exact for 0, +-1, +-0.6961928 and 1.3312578).
+__device__ __forceinline__ uint2 iq4_quad_entry(int i) {
+    const float a = kIQ4NLTable[i & 15], b = kIQ4NLTable[i >> 4];
+    const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+    const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
+    return make_uint2((uint32_t)__builtin_bit_cast(uint16_t, ah) | ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16),
+                      (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16));
+}
+
 // Dot product of one data dword (8 codes, elements in order) with the fp16
 // activation dwords xx[0..3]: hi and lo parts summed separately by
 // v_dot2_f32_f16 and joined as hi + 2^-11 lo.
@@ -535,9 +548,10 @@ static void launch_quad(int R, dim3 grid, dim3 block, hipStream_t st, const uint
 //    (lane group g supplies its elements 8g .. 8g+7), and the block's fp16
 //    scale multiplies the step's result.
 //  * The fp32 codebook value T[q] enters the MFMA as two exact fp16 parts,
-//    T_hi = fp16(T) and T_lo = fp16(T - T_hi) (|T - T_hi - T_lo| <= 2^-23 |T|),
-//    looked up together as one dword from a 16-entry LDS table; two MFMAs
-//    per step accumulate both parts.
+//    T_hi = fp16(T) and T_lo = fp16(T - T_hi) (|T - T_hi - T_lo| <=
+//    2^-22.3 |T|, T_lo subnormal for +-0.0805542), looked up together as
+//    one dword from a 16-entry LDS table; two MFMAs per step accumulate
+//    both parts.
 __device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
@@ -997,13 +1011,16 @@ __global__ void iq4t_tile_kernel(const uint32_t* __restrict__ data, const uint16
 // (4 waves x 32 rows a workgroup, UPW 128-K units, XCD-aware mapping, X and
 // scales staged in LDS behind an LDS-only barrier while the 1 KB weight
 // loads stream).  A operand: one ds_read_b64 per data byte from a 2 KB LDS
-// table byte -> (hi pair, lo pair) (iq4_pair_entry, the codebook as T_hi +
-// 2^-11 T_lo', exact to 2^-22 |T|); two MFMAs a step, the lo part's result
-// scaled by 2^-11 and accumulated into the hi part's.  The pairs are in
-// element order, so the B rows of a lane group are read in natural order.
-// Each step's result is scaled by its block's fp16 scale in fp32.  The
-// fp16-rounded table with one MFMA a step measured no faster (18.4 against
-// 17.4 us at 18944 x 3584, batch 8).
+// table byte -> (hi pair, lo pair) (iq4_quad_entry, the codebook as T_hi +
+// T_lo, within 2^-22.3 |T|).  The entries of two bytes are one A operand
+// whose k slots hold Th Th Tl Tl Th Th Tl Tl of 4 elements, against a B
+// operand with each activation pair twice, so the step's 8 elements of a
+// lane take two chained MFMAs with no rescaling in between (an earlier form
+// with a hi-part and a 2^-11-scaled lo-part MFMA needed a multiply per
+// output and register moves to gather the parts: 17.0 -> 15.9 us at
+// 18944 x 3584, batch 8).  Each step's result is scaled by its block's fp16
+// scale in fp32.  The fp16-rounded table with one MFMA a step measured no
+// faster than the split.
 template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint16_t* __restrict__ stl,
@@ -1066,7 +1083,7 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
         }
     }
     if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
-    for (int i = tid; i < 256; i += W * 64) tbl[i] = iq4_pair_entry(i);
+    for (int i = tid; i < 256; i += W * 64) tbl[i] = iq4_quad_entry(i);
 #pragma unroll
     for (int i = 0; i < XP; i++) {
         const int p = tid + i * W * 64;
@@ -1090,18 +1107,20 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
         if (u0 + u < u1) {
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                const half8v bv = mfma_b_pair(smem, lbase + (136 * u + 34 * s) * 2 * N, 8 * N);
+                const u32x4 bw = __builtin_bit_cast(u32x4, mfma_b_pair(smem, lbase + (136 * u + 34 * s) * 2 * N, 8 * N));
+                // activation pairs (x0 x1), (x2 x3) each twice: k slots of the
+                // A operand {entry(byte 0), entry(byte 1)} = Th0 Th1 Tl0 Tl1 Th2 Th3 Tl2 Tl3
+                const half8v b1 = __builtin_bit_cast(half8v, (u32x4){bw[0], bw[0], bw[1], bw[1]});
+                const half8v b2 = __builtin_bit_cast(half8v, (u32x4){bw[2], bw[2], bw[3], bw[3]});
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
                     const uint2 e0 = tbl[dw & 0xffu], e1 = tbl[(dw >> 8) & 0xffu], e2 = tbl[(dw >> 16) & 0xffu],
                                 e3 = tbl[dw >> 24];
-                    const u32x4 ah = {e0.x, e1.x, e2.x, e3.x}, al = {e0.y, e1.y, e2.y, e3.y};
-                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, al), bv,
+                    const u32x4 a1 = {e0.x, e0.y, e1.x, e1.y}, a2 = {e2.x, e2.y, e3.x, e3.y};
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a1), b1,
                                                                        (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) d[i] *= 0x1p-11f;
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, ah), bv, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a2), b2, d, 0, 0, 0);
                     // scales of rows 4 lg + i of this tile, block 4u + s
                     const uint16_t* sp = ssm + ((2 * wave + t) * UPW + u) * 64 + 16 * lg + s;
 #pragma unroll
