@@ -383,8 +383,10 @@ int zt_gemm_q5kt_f32(const void* W_tiled, const void* H_tiled, const void* Q_til
 
 /* Batched Q6_K on the same MFMA kernel.  zt_q6k_tile reads Q6KStorage's
  * 210-byte super-blocks (tensor/quantized_kquant.go:335-382: ql, qh, int8
- * scales, fp16 d) and writes the 6-bit values as bytes in the Q8_0 tiled
- * layout (zt_q6k_tiled_bytes) and the fp32 products d * sc of every
+ * scales, fp16 d) and writes the 6-bit values as bytes in the Q8_0 tile
+ * positions (zt_q6k_tiled_bytes; piece 16 g + i of a tile-unit half holds,
+ * for each of its two blocks, values 4g .. 4g+3 and 16 + 4g .. 16 + 4g+3
+ * of row i) and the fp32 products d * sc of every
  * 16-value group, [tile-unit][16 rows][8 groups] (zt_q6k_tiled_scale_bytes).
  * zt_gemm_q6kt_f32: C[M, N] = W * B for N in {4, 8, 12, 16}, K % 256 == 0,
  * workspace as zt_gemm_q4t_f32.  Replaces the reference's

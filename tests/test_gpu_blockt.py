@@ -672,9 +672,10 @@ def run_q6kt(lib, bufs, x, rows, K, N):
 
 @pytest.mark.parametrize("rows,K", [(16, 256), (17, 512), (1, 768)])
 def test_q6k_tile_layout_bytes(lib, rows, K):
-    """Values in the Q8_0 tile order (lane 16 g + i, half hh: bytes 8g..8g+7
-    of blocks 4u + 2hh and 4u + 2hh + 1 of row 16 rt + i) and d * sc per
-    16-value group as [tile-unit][16 rows][8 groups], zero past the last row."""
+    """Values as bytes (lane 16 g + i, half hh: for blocks 4u + 2hh and
+    4u + 2hh + 1 of row 16 rt + i, values 4g .. 4g+3 and then 16 + 4g ..
+    16 + 4g+3 of the block) and d * sc per 16-value group as [tile-unit]
+    [16 rows][8 groups], zero past the last row."""
     w = synth.kquant("q6_k", rows, K, 101)
     q, s = q6k_values(w.raw, rows, K)
     nt, nu = (rows + 15) // 16, K // 128
@@ -682,8 +683,8 @@ def test_q6k_tile_layout_bytes(lib, rows, K):
     qp[:rows] = q
     sp = np.zeros((nt * 16, K // 16), np.float32)
     sp[:rows] = s
-    # [rt, i, u, hh, bb, g, k] -> [rt, u, hh, g, i, bb, k]
-    dref = qp.reshape(nt, 16, nu, 2, 2, 4, 8).transpose(0, 2, 3, 5, 1, 4, 6).reshape(-1)
+    # [rt, i, u, hh, bb, h2, g, k4] -> [rt, u, hh, g, i, bb, h2, k4]
+    dref = qp.reshape(nt, 16, nu, 2, 2, 2, 4, 4).transpose(0, 2, 3, 6, 1, 4, 5, 7).reshape(-1)
     sref = sp.reshape(nt, 16, nu, 8).transpose(0, 2, 1, 3).reshape(-1)
     bufs = q6k_tile_dev(lib, w.raw, rows, K)
     assert np.array_equal(bufs[0].cpu().numpy(), dref)

@@ -49,11 +49,13 @@
 //    (d * scale, dmin * min) pairs; Q5_K adds Q5_0's fifth-bit dwords (aux).
 //    Each sub-block's min term uses an MFMA with all-positive A, which gives
 //    2^-24 sum(x) per step.
-//  * Q6_K (zt_q6k_tile): the values 0..63 as bytes in the Q8_0 data layout;
-//    fp32 d * sc per 16-value group [16 rows][8 groups] at tu * 512.  A step
-//    (one 32-value block) spans two groups, lane groups 0-1 and 2-3, so its
-//    B operand is split into two masked copies and each group gets its own
-//    offset and weight MFMAs and its own scale.
+//  * Q6_K (zt_q6k_tile): the values 0..63 as bytes in the Q8_0 tile
+//    positions, ordered so that lane group g holds values 4g .. 4g+3 of each
+//    of a block's two 16-value groups; fp32 d * sc per group [16 rows]
+//    [8 groups] at tu * 512.  Each group of a step is one 16x16x16 MFMA over
+//    half of the A and B operands, with its own offset MFMA and scale (an
+//    earlier form zeroed the other group's lane groups in two copies of B
+//    for 16x16x32 MFMAs: 3.5-8% slower).
 #include <mutex>
 #include <type_traits>
 
@@ -176,7 +178,8 @@ __global__ void q5t_tile_kernel(const uint16_t* __restrict__ scales, const uint3
 }
 
 // Q6_K tiled layout: the 6-bit values q (0..63) as bytes in the Q8_0 tile
-// format (tensor/quantized_kquant.go:355-382: value 128h + 32j + l of a
+// positions, lane group g taking values 4g .. 4g+3 and 16 + 4g .. 16 + 4g+3
+// of each 32-value block (tensor/quantized_kquant.go:355-382: value 128h + 32j + l of a
 // super-block takes its low 4 bits from ql[64h + 32(j&1) + l] (low nibble
 // for j < 2, high for j >= 2) and its top 2 bits from qh[32h + l] >> 2j),
 // and the fp32 products d * scale of every 16-value group as
@@ -197,7 +200,9 @@ __global__ void q6kt_tile_kernel(const uint8_t* __restrict__ raw, u32x4* __restr
             const int b = 4 * u + 2 * hh + bb;  // 32-value block of the row
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                const int val = 32 * b + 8 * g + k, sb = val >> 8, vs = val & 255;
+                // lane group g: values 4g .. 4g+3 of the block's first 16-value
+                // group, then 4g .. 4g+3 of its second
+                const int val = 32 * b + 16 * (k >> 2) + 4 * g + (k & 3), sb = val >> 8, vs = val & 255;
                 const int h = vs >> 7, j = (vs >> 5) & 3, l = vs & 31;
                 const uint8_t* blk = raw + ((long)row * nsb + sb) * 210;
                 const int lo = (blk[64 * h + 32 * (j & 1) + l] >> (4 * (j >> 1))) & 15;
@@ -231,7 +236,11 @@ template <BlkFmt F>
 __device__ __forceinline__ int blkt_lds_row(int r) {
     const int u = r >> 7, b = (r >> 5) & 3, e = r & 31;
     int g, j;
-    if constexpr (F != BlkFmt::Q8_0 && F != BlkFmt::Q6_K) {
+    if constexpr (F == BlkFmt::Q6_K) {
+        // lane group g: elements 4g .. 4g+3, then 16 + 4g .. 16 + 4g+3
+        g = (e & 15) >> 2;
+        j = ((e >> 4) << 2) + (e & 3);
+    } else if constexpr (F != BlkFmt::Q8_0) {
         // A halves of lane group g: elements 4g, 4g+2, 4g+16, 4g+18, 4g+1, 4g+3, 4g+17, 4g+19
         const int i4 = e & 3;
         g = (e & 15) >> 2;
@@ -455,36 +464,38 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                     bv[pl] = __builtin_bit_cast(half8v, (short8v){ba[0], ba[1], ba[2], ba[3], bb[0], bb[1], bb[2], bb[3]});
                 }
                 if constexpr (Q6) {
-                    // the step's two 16-value groups are lane groups 0-1 and 2-3:
-                    // B restricted to each, so every MFMA sums one group
-                    half8v bq[2][NPL];
-                    const half8v hz = (half8v){0, 0, 0, 0, 0, 0, 0, 0};
+                    // lane group g holds values 4g .. 4g+3 of each of the step's
+                    // two 16-value groups (slots 0-3, then 4-7), so a 16x16x16
+                    // MFMA over one half of A and B is exactly one group's sum
+                    half4v bq[2][NPL];
 #pragma unroll
                     for (int pl = 0; pl < NPL; pl++) {
-                        bq[0][pl] = lg < 2 ? bv[pl] : hz;
-                        bq[1][pl] = lg < 2 ? hz : bv[pl];
+                        const short8v b8 = __builtin_bit_cast(short8v, bv[pl]);
+                        bq[0][pl] = __builtin_bit_cast(half4v, (short4v){b8[0], b8[1], b8[2], b8[3]});
+                        bq[1][pl] = __builtin_bit_cast(half4v, (short4v){b8[4], b8[5], b8[6], b8[7]});
                     }
+                    const half4v ao = (half4v){ol, ol, ol, ol};
                     float4v dq[2];
 #pragma unroll
                     for (int hq = 0; hq < 2; hq++) {
-                        dq[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bq[hq][0], (float4v){0.f, 0.f, 0.f, 0.f}, 0,
-                                                                         0, 0);
-                        if constexpr (NPL == 2) dq[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aoff, bq[hq][1], dq[hq], 0, 0, 0);
+                        dq[hq] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, bq[hq][0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        if constexpr (NPL == 2) dq[hq] = __builtin_amdgcn_mfma_f32_16x16x16f16(ao, bq[hq][1], dq[hq], 0, 0, 0);
                     }
 #pragma unroll
                     for (int t = 0; t < 2; t++) {
                         const uint4 q = w[u][t][s >> 1];
                         const uint32_t da = (s & 1) ? q.z : q.x, db = (s & 1) ? q.w : q.y;
-                        const u32x4 av = {__builtin_amdgcn_perm(da, da, 0x0C010C00u), __builtin_amdgcn_perm(da, da, 0x0C030C02u),
-                                          __builtin_amdgcn_perm(db, db, 0x0C010C00u), __builtin_amdgcn_perm(db, db, 0x0C030C02u)};
+                        const half4v aq[2] = {
+                            __builtin_bit_cast(half4v, (uint2){__builtin_amdgcn_perm(da, da, 0x0C010C00u),
+                                                               __builtin_amdgcn_perm(da, da, 0x0C030C02u)}),
+                            __builtin_bit_cast(half4v, (uint2){__builtin_amdgcn_perm(db, db, 0x0C010C00u),
+                                                               __builtin_amdgcn_perm(db, db, 0x0C030C02u)})};
                         float4v d[2];
 #pragma unroll
                         for (int hq = 0; hq < 2; hq++) {
-                            d[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bq[hq][0], dq[hq],
-                                                                            0, 0, 0);
+                            d[hq] = __builtin_amdgcn_mfma_f32_16x16x16f16(aq[hq], bq[hq][0], dq[hq], 0, 0, 0);
                             if constexpr (NPL == 2)
-                                d[hq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bq[hq][1],
-                                                                                d[hq], 0, 0, 0);
+                                d[hq] = __builtin_amdgcn_mfma_f32_16x16x16f16(aq[hq], bq[hq][1], d[hq], 0, 0, 0);
                         }
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
