@@ -377,6 +377,7 @@ SUITE = {
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "q6_ks": ("q6_ks", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_gguf": ("q8_0_gguf", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q4_0_batched": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
@@ -569,6 +570,16 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         name = f"zt_gemv_{fmt.replace('_', '')}_f32"
         fn = lambda wb, y: getattr(lib, name)(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, s)
         nbytes = synth.algorithmic_bytes(fmt, rows, K, N)
+    elif fmt == "q6_ks":
+        # Q6_K batch 1 on the split layout (zt_q6k_split), the same bytes regrouped
+        w = synth.kquant("q6_k", rows, K, seed)
+        raw = dev(w.raw)
+        sp = torch.empty(lib.zt_q6k_split_bytes(rows, K), dtype=torch.uint8, device="cuda")
+        lib.call("zt_q6k_split", raw.data_ptr(), rows, K, sp.data_ptr(), s)
+        wbufs = [sp]
+        x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
+        fn = lambda wb, y: lib.zt_gemv_q6ks_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, s)
+        nbytes = synth.algorithmic_bytes("q6_k", rows, K, N)
     elif fmt == "q8_0_gguf":
         raw = synth.gguf_q8_0(rows, K, seed)
         nblk = rows * K // 32
@@ -661,7 +672,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
 
 
 SUITE_FORMATS = ("int4", "int4_rmul", "int8", "q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
-                 "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "q4_k", "q5_k", "q6_k", "q8_0_gguf", "q5_0")
+                 "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "q4_k", "q5_k", "q6_k", "q6_ks", "q8_0_gguf", "q5_0")
 
 
 def _pmc_case_arg(v: str) -> str:

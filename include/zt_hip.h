@@ -453,6 +453,19 @@ int zt_gemv_q4k_f32(const void* W, const float* x, float* y, int M, int K, zt_st
 int zt_gemv_q5k_f32(const void* W, const float* x, float* y, int M, int K, zt_stream_t stream);
 int zt_gemv_q6k_f32(const void* W, const float* x, float* y, int M, int K, zt_stream_t stream);
 
+/* Q6_K split layout for the batch-1 GEMV (the same GemvQ6KF32 product over
+ * a load-time regrouping; the reference reads the raw 210-byte
+ * super-blocks, which are only 2-byte aligned).  zt_q6k_split writes the
+ * raw super-blocks' bytes (W_q6k 2-byte aligned) as four naturally aligned
+ * arrays over the T = M * K/256 super-blocks t = row * K/256 + sb: ql at
+ * 128 t, qh at 128 T + 64 t, int8 scales at 192 T + 16 t, fp16 d at
+ * 208 T + 2 t (zt_q6k_split_bytes = 210 T bytes; W_split 16-byte aligned).
+ * zt_gemv_q6ks_f32 is zt_gemv_q6k_f32 on that layout (x 16-byte aligned,
+ * K % 256 == 0, 210 T < 2^31, else InvalidValue). */
+long zt_q6k_split_bytes(int M, int K);
+int zt_q6k_split(const void* W_q6k, int M, int K, void* W_split, zt_stream_t stream);
+int zt_gemv_q6ks_f32(const void* W_split, const float* x, float* y, int M, int K, zt_stream_t stream);
+
 /* Replaces gemv_q5_0_f32 (internal/cuda/kernels/gemv_q5_0.cu:108-125) behind
  * KernelRunner.GemvQ5_0F32 (internal/gpuapi/kernels.go:65-69; ROCm stub
  * internal/gpuapi/rocm_kernels.go:125-127).  W is the RawBytesGPU layout,

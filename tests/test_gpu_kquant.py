@@ -105,6 +105,59 @@ def test_q6k_gemv_on_a_2_byte_aligned_base(lib, orc):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.kq_dequant("q6_k", w.raw, rows * K).view(np.uint32))
 
 
+def q6k_split_dev(lib, raw, rows, K, off=0):
+    """The split copy of raw Q6_K super-blocks (uploaded at byte offset off)."""
+    d = dev(raw, pad=off)
+    out = torch.empty(lib.zt_q6k_split_bytes(rows, K), dtype=torch.uint8, device="cuda")
+    assert lib.call("zt_q6k_split", d.data_ptr() + off, rows, K, out.data_ptr(), stream()) is None
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("rows,K,off", [(1, 256, 0), (17, 768, 2), (33, 2560, 0)])
+def test_q6k_split_layout_bytes(lib, rows, K, off):
+    """ql, qh, scales and d of every super-block regrouped into four arrays,
+    checked against a numpy regrouping of the raw 210-byte blocks."""
+    say(f"q6k split layout {rows}x{K} off {off}")
+    w = synth.kquant("q6_k", rows, K, 91)
+    raw = np.frombuffer(w.raw, np.uint8).reshape(-1, 210)
+    want = np.concatenate([raw[:, :128].reshape(-1), raw[:, 128:192].reshape(-1), raw[:, 192:208].reshape(-1),
+                           raw[:, 208:210].reshape(-1)])
+    assert lib.zt_q6k_split_bytes(rows, K) == raw.size
+    got = q6k_split_dev(lib, w.raw, rows, K, off).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED + [(9, 16640), (300, 28672)])
+def test_q6k_split_gemv_matches_oracle(lib, orc, rows, K):
+    """zt_gemv_q6ks_f32 on the split layout against GemmF32Q6KNT, at the
+    Llama-3-8B shapes, ragged ones and K past one step of 16 waves."""
+    say(f"q6ks gemv {rows}x{K}")
+    w = synth.kquant("q6_k", rows, K, synth.seed_for(6, K % 16))
+    x = synth.x_f32(K, synth.seed_for(6, K % 16))
+    ws = q6k_split_dev(lib, w.raw, rows, K)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = devf(x)
+    lib.call("zt_gemv_q6ks_f32", ws.data_ptr(), xd.data_ptr(), y.data_ptr(), rows, K, stream())
+    torch.cuda.synchronize()
+    err = rel_err(y.cpu().numpy(), orc.gemm_f32_kq_nt("q6_k", x, w.raw, 1, rows, K, threads=orc.nthreads()))
+    say(f"  rel err {err:.2e}")
+    assert err <= TOL
+
+
+def test_q6k_split_invalid_arguments(lib):
+    t = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    p = t.data_ptr()
+    assert lib.zt_q6k_split_bytes(4, 100) == -1
+    assert lib.zt_q6k_split(p, 4, 100, p, stream()) == 1     # K % 256
+    assert lib.zt_q6k_split(p + 1, 1, 256, p, stream()) == 1  # raw alignment
+    assert lib.zt_q6k_split(p, 1, 256, p + 8, stream()) == 1  # split alignment
+    assert lib.zt_gemv_q6ks_f32(p, p, p, 4, 100, stream()) == 1
+    assert lib.zt_gemv_q6ks_f32(p + 8, p, p, 1, 256, stream()) == 1  # W alignment
+    assert lib.zt_gemv_q6ks_f32(p, p + 4, p, 1, 256, stream()) == 1  # x alignment
+    assert lib.zt_gemv_q6ks_f32(p, p, p, 1 << 20, 4096, stream()) == 1  # 210 T >= 2^31
+
+
 @pytest.mark.parametrize("fmt,K,off", [("q4_k", 768, 0), ("q5_k", 4352, 0), ("q6_k", 768, 0), ("q6_k", 768, 2),
                                         ("q6_k", 4352, 2), ("q6_k", 4096, 2)])
 def test_kquant_fixed_step_kernel_odd_superblocks_and_offset_base(lib, orc, fmt, K, off):
@@ -227,6 +280,31 @@ def test_engine_q6k_and_q5_0(orc):
     got = eng.matmul(Tensor((rows, K), Q5_0Storage.from_raw(w5.raw, rows * K)), devf(x2)).cpu().numpy()
     W5 = orc.q5_0_dequant(w5.raw, rows * K).reshape(rows, K).astype(np.float64)
     assert rel_err(got, W5 @ x2.astype(np.float64)) <= TOL
+
+
+def test_engine_q6k_batch1_split_copy(orc):
+    """Q6_K batch 1 through the engine runs on the split copy: built once on
+    the first call, reused on the next, dropped when the storage is uploaded
+    again (then rebuilt from the new buffer)."""
+    from ztensor_amd.engine import ROCmEngine
+
+    eng = ROCmEngine()
+    rows, K = 96, 2048
+    w = synth.kquant("q6_k", rows, K, 93)
+    st = Q6KStorage.from_raw(w.raw, rows * K)
+    x = synth.x_f32(K, 93)
+    ref = orc.gemm_f32_kq_nt("q6_k", x, w.raw, 1, rows, K)
+    t = Tensor((rows, K), st)
+    assert rel_err(eng.matmul(t, devf(x)).cpu().numpy().reshape(-1), ref) <= TOL
+    first = st._gpu_split[1]
+    assert first.numel() == rows * (K // 256) * 210
+    assert rel_err(eng.matmul(t, devf(x)).cpu().numpy().reshape(-1), ref) <= TOL
+    assert st._gpu_split[1] is first
+    st.set_gpu_ptr(None)
+    assert st._gpu_split is None
+    eng.upload_weights([st])
+    assert rel_err(eng.matmul(t, devf(x)).cpu().numpy().reshape(-1), ref) <= TOL
+    assert st._gpu_split is not None and st._gpu_split[1] is not first
 
 
 # ------------------------------------------------------------------ GGUF mmap

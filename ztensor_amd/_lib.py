@@ -105,6 +105,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_gemv_q4k_f32": (I, [P, P, P, I, I, P]),
     "zt_gemv_q5k_f32": (I, [P, P, P, I, I, P]),
     "zt_gemv_q6k_f32": (I, [P, P, P, I, I, P]),
+    "zt_q6k_split_bytes": (L, [I, I]),
+    "zt_q6k_split": (I, [P, I, I, P, P]),
+    "zt_gemv_q6ks_f32": (I, [P, P, P, I, I, P]),
     "zt_gemv_q5_0_f32": (I, [P, P, P, I, I, I, I, P]),
     "zt_dequant_q4k_f32": (I, [P, P, I, I, P]),
     "zt_dequant_q5k_f32": (I, [P, P, I, I, P]),

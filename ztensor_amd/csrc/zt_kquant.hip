@@ -393,6 +393,122 @@ static int gemv_kq(const void* W, const float* x, float* y, int M, int K, hipStr
     return (int)hipGetLastError();
 }
 
+// ------------------------------------------------------------ Q6_K split layout
+//
+// The raw 210-byte super-blocks are only 2-byte aligned, so the raw-layout
+// GEMV reads every field as aligned dwords joined with v_alignbit.  The
+// split layout (zt_q6k_split) regroups the same 210 bytes a super-block
+// into four naturally aligned arrays over all M * nsb super-blocks t = row
+// * nsb + sb: QL at 128 t, QH at 128 T + 64 t, SC at 192 T + 16 t and D at
+// 208 T + 2 t (T = M * nsb).  Each lane's fields are then single 8-byte
+// (ql, qh, scales) and 2-byte (d) buffer loads.
+
+__global__ void q6k_split_kernel(const uint16_t* __restrict__ raw, uint16_t* __restrict__ out, long total) {
+    const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;  // super-block
+    if (t >= total) return;
+    const uint16_t* b = raw + t * 105;  // 210 bytes
+#pragma unroll 8
+    for (int i = 0; i < 64; i++) out[t * 64 + i] = b[i];                     // ql
+#pragma unroll 8
+    for (int i = 0; i < 32; i++) out[total * 64 + t * 32 + i] = b[64 + i];   // qh
+#pragma unroll
+    for (int i = 0; i < 8; i++) out[total * 96 + t * 8 + i] = b[96 + i];     // scales
+    out[total * 104 + t] = b[104];                                           // d
+}
+
+// Q6_K batch-1 GEMV on the split layout: 16 lanes a super-block (8 ql bytes
+// each, the lane roles of kq_gemv_kernel with NW = 2), 4 super-blocks a
+// wave and step, the waves of a workgroup splitting K.  Every load of a
+// step is issued before any arithmetic, as buffer loads whose wave-uniform
+// row offsets are scalar offsets; lanes past the last super-block read
+// zeros through out-of-range offsets.
+template <int R>
+__global__ void __launch_bounds__(1024) q6ks_gemv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                         float* __restrict__ y, int rows, int nsb) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int slot = lane >> 4, t = lane & 15;
+    const int byte0 = t * 8, h6 = byte0 >> 6, w6 = byte0 & 63;
+    // ql bytes 64 h + w .. +7: low nibbles are values vlo .. vlo+7, high
+    // nibbles vlo+64 ..; qh bytes 32 h + w % 32 .. +7 hold their top two bits
+    const int vlo = 128 * h6 + 32 * (w6 >= 32) + (w6 & 31), vhi = vlo + 64;
+    const uint32_t qsh = (w6 >= 32) ? 2u : 0u;
+    const int si = 2 * (w6 >= 32) + ((w6 & 31) >> 4);  // scale of vlo within 8 h .. 8 h + 7; vhi's is si + 4
+    const int row0 = blockIdx.x * R;
+    const uint32_t T = (uint32_t)rows * (uint32_t)nsb;
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)(T * 210u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nsb * 1024, 0x00020000);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int sb0 = wave * 4; sb0 < nsb; sb0 += nwaves * 4) {
+        const int sb = sb0 + slot;
+        const bool ok = sb < nsb;
+        const uint32_t vql = ok ? (uint32_t)(sb * 128 + byte0) : 0x80000000u;
+        const uint32_t vqh = ok ? (uint32_t)(T * 128u + sb * 64 + 32 * h6 + (w6 & 31)) : 0x80000000u;
+        const uint32_t vsc = ok ? (uint32_t)(T * 192u + sb * 16 + 8 * h6) : 0x80000000u;
+        const uint32_t vd = ok ? (uint32_t)(T * 208u + sb * 2) : 0x80000000u;
+        uint2 ql[R], qh[R], sc[R];
+        uint32_t dd[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t rs = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)nsb;
+            ql[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vql, rs * 128u, 2));
+            qh[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vqh, rs * 64u, 2));
+            sc[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vsc, rs * 16u, 0));
+            dd[r] = __builtin_amdgcn_raw_buffer_load_b16(rw, vd, rs * 2u, 0);
+        }
+        const uint32_t xo = ok ? (uint32_t)((sb * 256 + vlo) * 4) : 0x80000000u;
+        const u32x4 xl0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        const u32x4 xl1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+        const u32x4 xh0 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 256, 0, 0);
+        const u32x4 xh1 = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 272, 0, 0);
+        const uint32_t lw[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+        const uint32_t hw[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+        float xlo[8], xhi[8], slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float a = __uint_as_float(lw[i]), b = __uint_as_float(hw[i]);
+            slo += a;
+            shi += b;
+            xlo[i] = a * 16777216.0f;  // low-nibble chain: q * 2^-24
+            xhi[i] = b * 1048576.0f;   // high-nibble chain: q * 2^-20
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t qd[2] = {ql[r].x, ql[r].y}, hd[2] = {qh[r].x, qh[r].y};
+            uint32_t ml[2][2], mh[2][2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t d = qd[j], d8 = d >> 8;
+                const uint32_t L = hd[j] >> qsh, H = hd[j] >> (qsh + 4);
+                ml[j][0] = (d & 0x000F000Fu) | ((L << 4) & 0x00300030u);
+                ml[j][1] = (d8 & 0x000F000Fu) | ((L >> 4) & 0x00300030u);
+                mh[j][0] = (d & 0x00F000F0u) | ((H << 8) & 0x03000300u);
+                mh[j][1] = (d8 & 0x00F000F0u) | (H & 0x03000300u);
+            }
+            const float S0 = chainw<2>(ml, xlo, -32.0f * slo);
+            const float S1 = chainw<2>(mh, xhi, -32.0f * shi);
+            const int sc0 = __builtin_amdgcn_sbfe((int)sc[r].x, 8 * si, 8);
+            const int sc1 = __builtin_amdgcn_sbfe((int)sc[r].y, 8 * si, 8);
+            const float tq = __builtin_fmaf((float)sc1, S1, (float)sc0 * S0);
+            acc[r] = __builtin_fmaf(h2f((uint16_t)dd[r]), tq, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+static void launch_q6ks(int R, dim3 grid, dim3 block, hipStream_t st, const uint8_t* W, const float* x, float* y,
+                        int rows, int nsb) {
+    switch (R) {
+        case 8: q6ks_gemv_kernel<8><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 4: q6ks_gemv_kernel<4><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        case 2: q6ks_gemv_kernel<2><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+        default: q6ks_gemv_kernel<1><<<grid, block, 0, st>>>(W, x, y, rows, nsb); break;
+    }
+}
+
 // ------------------------------------------------------------ Q5_0 GEMV
 
 // Spreads bits 0..3 of v into bit 0 of bytes 0..3 (distinct partial
@@ -678,6 +794,44 @@ ZT_EXPORT int zt_gemv_q5k_f32(const void* W, const float* x, float* y, int M, in
 ZT_EXPORT int zt_gemv_q6k_f32(const void* W, const float* x, float* y, int M, int K, hipStream_t stream) {
     return gemv_kq<6>(W, x, y, M, K, stream);
 }
+ZT_EXPORT long zt_q6k_split_bytes(int M, int K) {
+    if (M < 0 || K < 0 || K % 256 != 0) return -1;
+    return (long)M * (K / 256) * 210;
+}
+
+ZT_EXPORT int zt_q6k_split(const void* W_q6k, int M, int K, void* W_split, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) return (int)hipSuccess;
+    if (W_q6k == nullptr || W_split == nullptr || ((uintptr_t)W_q6k & 1) || ((uintptr_t)W_split & 15))
+        return (int)hipErrorInvalidValue;
+    const long total = (long)M * (K / 256);
+    q6k_split_kernel<<<ceil_div(total, 256), 256, 0, stream>>>(static_cast<const uint16_t*>(W_q6k),
+                                                              static_cast<uint16_t*>(W_split), total);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemv_q6ks_f32(const void* W_split, const float* x, float* y, int M, int K, hipStream_t stream) {
+    if (M < 0 || K < 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M == 0 || K == 0) {
+        if (M > 0 && K == 0 && y) {  // empty sum
+            mfma_zero(y, M, stream);
+            return (int)hipGetLastError();
+        }
+        return (int)hipSuccess;
+    }
+    if (W_split == nullptr || x == nullptr || y == nullptr || ((uintptr_t)W_split & 15) || ((uintptr_t)x & 15))
+        return (int)hipErrorInvalidValue;
+    const int nsb = K / 256;
+    if ((long)M * nsb * 210 >= 0x7fffffffL || nsb > (1 << 20)) return (int)hipErrorInvalidValue;  // 32-bit buffer offsets
+    // 4 super-blocks a wave and step, up to 16 waves splitting K (one step
+    // each for K <= 16384), up to 8 rows a wave (16 spill registers at
+    // 1024-thread workgroups)
+    const int nw = min(16, ceil_div(nsb, 4));
+    const int R = pick_rows_per_wave(M, nw, 1, 2048);
+    launch_q6ks(R, dim3(ceil_div(M, R)), dim3(nw * kWave), stream, static_cast<const uint8_t*>(W_split), x, y, M, nsb);
+    return (int)hipGetLastError();
+}
+
 ZT_EXPORT int zt_gemv_q5_0_f32(const void* W, const float* x, float* y, int M, int K, int qh_offset, int qs_offset,
                                hipStream_t stream) {
     return gemv_q5_0(W, x, y, M, K, qh_offset, qs_offset, stream);

@@ -56,6 +56,7 @@ class _GPUPtrMixin:
     def set_gpu_ptr(self, buf: GPUBuffer | None) -> None:
         self._gpu = buf
         self._gpu_tiled = None  # a tiled copy built from the previous upload is stale
+        self._gpu_split = None  # so is a split copy (Q6_K batch 1)
 
     def gpu_ptr(self) -> GPUBuffer | None:
         return self._gpu
