@@ -267,26 +267,28 @@ static void launch_intq_gemv(hipStream_t st, const uint8_t* A, const float* x, f
 // ------------------------------------------------------------ X W, batch 1-4
 //
 // C[b, j] = sum_k X[b, k] w[k, j], batch NB in 1..4, out % 16 == 0 and
-// group_size % 16 == 0.  A workgroup of 16 waves owns 64 output columns:
-// lane l owns columns 16 (l % 4) .. +15 (one 8-byte load a row, all in one
-// group) and row phase l / 4, so a load instruction reads 16 rows x 32
-// bytes; wave w takes the w-th sixteenth of K, and U rows a lane are loaded
-// before any is used (at K = 4096 that is all of the lane's rows).  Per row
+// group_size % 16 == 0.  A workgroup of 16 waves owns 16 LPR output
+// columns: lane l owns columns 16 (l % LPR) .. +15 (one 8-byte load a row,
+// all in one group) and row phase l / LPR, so a load instruction reads
+// 64 / LPR rows x 8 LPR bytes; wave w takes the w-th sixteenth of K, and U
+// rows a lane are loaded before any is used (at K = 4096 that is all of the
+// lane's rows).  Per row
 // the lane forms t = X[b, k] * scale and adds t * float(v - zero) for its 16
 // columns (the reference rounds float(v - zero) * scale first, then
-// multiplies by X: the two differ by one fp32 rounding per product).  The 16
+// multiplies by X: the two differ by one fp32 rounding per product).  The
 // row phases are added by lane shuffles, the 16 waves through LDS in wave
 // order.
-template <int NB, int U>
+template <int NB, int U, int LPR>
 __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __restrict__ W,
                                                               const float* __restrict__ X, float* __restrict__ C,
                                                               const float* __restrict__ scales,
                                                               const uint8_t* __restrict__ zeros, int K, int Nout,
                                                               int gs, int ng) {
-    __shared__ float red[16][4][16 * NB];
+    constexpr int NPH = 64 / LPR;  // row phases
+    __shared__ float red[16][LPR][16 * NB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-    const int cl = lane & 3, ph = lane >> 2;
-    const int col = blockIdx.x * 64 + 16 * cl;  // first of the lane's 16 columns
+    const int cl = lane % LPR, ph = lane / LPR;
+    const int col = blockIdx.x * 16 * LPR + 16 * cl;  // first of the lane's 16 columns
     const bool colok = col < Nout;
     const int cc = colok ? col : 0;
     const int g = cc / gs;
@@ -298,13 +300,13 @@ __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __r
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int j = 0; j < 16; j++) acc[b][j] = 0.0f;
-    for (int k0 = kbeg + ph; k0 < kend; k0 += 16 * U) {
+    for (int k0 = kbeg + ph; k0 < kend; k0 += NPH * U) {
         uint2 w[U];
         float s[U], xv[U][NB];
         int z[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int k = k0 + 16 * u;
+            const int k = k0 + NPH * u;
             const bool ok = colok && k < kend;
             const int kk = ok ? k : kbeg;
             w[u] = ok ? *reinterpret_cast<const uint2*>(W + (long)kk * rowbytes + cc / 2) : make_uint2(0u, 0u);
@@ -327,16 +329,14 @@ __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __r
             }
         }
     }
-    // row phases (lane bits 2-5) into lanes 0..3
+    // row phases (the lane bits above those of cl) into lanes 0 .. LPR-1
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             float v = acc[b][j];
-            v += __shfl_xor(v, 4);
-            v += __shfl_xor(v, 8);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
+#pragma unroll
+            for (int m = LPR; m < 64; m <<= 1) v += __shfl_xor(v, m);
             acc[b][j] = v;
         }
     if (ph == 0) {
@@ -347,9 +347,9 @@ __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __r
     }
     __syncthreads();
     // outputs (b, column) over the workgroup's threads, the waves summed in order
-    for (int t = threadIdx.x; t < 64 * NB; t += blockDim.x) {
-        const int b = t >> 6, c = t & 63;
-        const int n = blockIdx.x * 64 + c;
+    for (int t = threadIdx.x; t < 16 * LPR * NB; t += blockDim.x) {
+        const int b = t / (16 * LPR), c = t % (16 * LPR);
+        const int n = blockIdx.x * 16 * LPR + c;
         if (n < Nout) {
             float sum = 0.0f;
             for (int w = 0; w < nwaves; w++) sum += red[w][c >> 4][16 * b + (c & 15)];
@@ -362,9 +362,13 @@ template <int NB>
 static void launch_int4_rmul_valu(hipStream_t st, const uint8_t* W, const float* X, float* C, const float* s,
                                   const uint8_t* z, int K, int Nout, int gs, int ng) {
     const int nw = max(1, min(16, K / 256));
-    const dim3 g(ceil_div(Nout, 64)), b(nw * kWave);
-    constexpr int U = NB == 1 ? 16 : NB == 2 ? 8 : NB == 3 ? 4 : 2;  // within 128 VGPRs (1024-thread workgroups)
-    int4_rmul_valu_kernel<NB, U><<<g, b, 0, st>>>(W, X, C, s, z, K, Nout, gs, ng);
+    // 16 columns a workgroup (one lane a row, 64 row phases): 4096 x 4096
+    // batch 1 21.1 us, against 25.6 with 32 columns and 28.0 with 64 (more
+    // workgroups keep more rows in flight; neighbouring workgroups share
+    // each row's 64-byte lines in L2); batch 4 28.8 against 31.3 us
+    // (4 rows a lane per pass, 2 at batch 4 to stay within 128 VGPRs)
+    int4_rmul_valu_kernel<NB, NB == 4 ? 2 : 4, 1><<<dim3(ceil_div(Nout, 16)), dim3(nw * kWave), 0, st>>>(
+        W, X, C, s, z, K, Nout, gs, ng);
 }
 
 // ------------------------------------------------------------ fp32 MFMA GEMM
