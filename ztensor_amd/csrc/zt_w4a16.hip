@@ -726,10 +726,23 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc((void*)(x + (long)u0 * 128 * N), (short)0, npieces * 16, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsz = __builtin_amdgcn_make_buffer_rsrc((void*)szp, (short)0, 0x7fffffff, 0x00020000);
-    u32x4 xr[XP];
+    // N = 16: a wave's 64 pieces of 16 bytes are one padded 32-row segment
+    // (64 N bytes), so they go to LDS directly (buffer_load ... lds, the
+    // lanes' bytes at consecutive 16-byte slots from the segment's base):
+    // no registers held and no LDS writes for the activations
+    constexpr bool XDMA = N == 16;
+    u32x4 xr[XDMA ? 1 : XP];
 #pragma unroll
-    for (int i = 0; i < XP; i++)
-        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+    for (int i = 0; i < XP; i++) {
+        if constexpr (XDMA) {
+            const int c = wave + i * W;  // segment of this wave's pieces
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (__attribute__((address_space(3))) void*)(smem + c * 68 * N), 16,
+                (uint32_t)(tid + i * W * 64) * 16u, 0, 0, 0);
+        } else {
+            xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + i * W * 64) * 16u, 0, 0);
+        }
+    }
     uint32_t sr[SP];
 #pragma unroll
     for (int i = 0; i < SP; i++) {
@@ -752,7 +765,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
 #pragma unroll
     for (int i = 0; i < XP; i++) {
         const int p = tid + i * W * 64;
-        if (p < npieces) {
+        if (!XDMA && p < npieces) {
             const int off = p * 16;
             *reinterpret_cast<u32x4*>(smem + off + (off / (64 * N)) * (4 * N)) = xr[i];
         }
