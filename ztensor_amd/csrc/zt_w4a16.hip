@@ -751,6 +751,10 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
         const uint32_t off = ok ? (uint32_t)(((u0 + u) * 128 / gs) * rows + min(rw0 + r, rows - 1)) * 4u : 0x80000000u;
         sr[i] = __builtin_amdgcn_raw_buffer_load_b32(rsz, off, 0, 0);
     }
+    // the weight loads stay behind the activation loads in issue order, so
+    // the barrier below can wait for the activations alone (vmcnt counts in
+    // issue order)
+    if constexpr (XDMA) __builtin_amdgcn_sched_barrier(0);
     uint4 w[UPW][2];
 #pragma unroll
     for (int u = 0; u < UPW; u++) {
@@ -761,6 +765,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
             w[u][t] = ld_stream(wt + ((long)rt * nunits + unit) * 64 + lane);
         }
     }
+    if constexpr (XDMA) __builtin_amdgcn_sched_barrier(0);
     if (tid < 4) reinterpret_cast<uint32_t*>(zero_area)[tid] = 0u;
 #pragma unroll
     for (int i = 0; i < XP; i++) {
@@ -779,7 +784,12 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
         }
     }
     // LDS writes visible to the workgroup; the weight loads stay in flight.
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // With direct activation loads, each wave first waits for its own: at
+    // most the 2 UPW weight loads issued after them may be outstanding.
+    if constexpr (XDMA)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * UPW) : "memory");
+    else
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const int jq = li >> 2;
     const int offa = (jq == 0) ? 0 : (jq == 1) ? 4 : (jq == 2) ? 1 : 5;  // rows {0,4,1,5}, then + 2: {2,6,3,7}
     // step s of unit u reads X rows 128u + 32lg + 8s + offa (+ 2), whose
