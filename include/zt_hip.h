@@ -164,6 +164,13 @@ int zt_gemm_iq4nlt_f16(const void* W_tiled, const void* S_tiled, const uint16_t*
  *              zt_dequant_fp8_f32 (4-byte LE fp32 scale, then one byte per
  *              element; tensor/quant_registry.go:190-229, decoders
  *              tensor/fp8_storage.go:229-250, 304-331)
+ *   "IQ3_S"    zt_dequant_iq3s_f32 (110-byte super-blocks of 256 values;
+ *              tensor/iq3_storage.go:12-95, 98-128, 169-186; the grid of
+ *              tensor/iq3_grid.go:15-27).  The reference's Dequantize
+ *              rejects nelem == 0 (NewIQ3SStorageFromRaw); the host binding
+ *              raises there, the entry point treats it as a no-op.
+ *   "W8A8"     zt_dequant_q8_f32 (the Q8_0 36-byte groups;
+ *              tensor/quantized_w8a8.go:285-322)
  * A source shorter than the format needs, a misaligned source (2 bytes for
  * Q4_0, 4 for AWQ_4 and FP8) or a null pointer -> InvalidValue, as the
  * reference's errShortData (tensor/quant_registry.go:242-245).  nelem == 0
@@ -180,6 +187,7 @@ int zt_dequant_awq4_f32(const void* wire, long wire_bytes, float* out, long nele
 /* e5m2: 0 = FP8_E4M3 (no NaN or infinity: exponent 15 is an ordinary
  * binade, as the reference decodes it), 1 = FP8_E5M2. */
 int zt_dequant_fp8_f32(const void* wire, long wire_bytes, float* out, long nelem, int e5m2, zt_stream_t stream);
+int zt_dequant_iq3s_f32(const void* src, long src_bytes, float* out, long nelem, zt_stream_t stream);
 
 /* ---- Q8_0 -------------------------------------------------------------- */
 

@@ -54,6 +54,7 @@ _SIG = {
     "orc_gemm_f32_mmap_nt": (I, [I, L, L, L, P, P, P, I, P]),
     "orc_awq4_wire_dequant": (I, [P, L, P, L]),
     "orc_fp8_dequant": (I, [P, L, P, L, I]),
+    "orc_iq3s_dequant": (I, [P, L, P, L]),
     "orc_gemm_int4_f32": (I, [P, P, P, P, P, L, L, L, L, I]),
     "orc_gemm_int4_f32_rmul": (I, [P, P, P, P, P, L, L, L, L, I]),
     "orc_gemm_int8_f32": (None, [P, P, P, L, L, L, I]),
@@ -175,6 +176,15 @@ def fp8_dequant(src, n: int, e5m2: bool):
     out = np.zeros(max(n, 1), np.float32)
     rc = lib().orc_fp8_dequant(_p(src), src.size, _p(out), n, int(bool(e5m2)))
     return rc, out[:n]
+
+
+def iq3s_dequant(src, n: int):
+    """(status, values): the registry's IQ3_S Dequantize (status 1 where the
+    reference returns an error)."""
+    src = np.ascontiguousarray(src, np.uint8)
+    out = np.zeros(max(n, 1), np.float32)
+    rc = lib().orc_iq3s_dequant(_p(src), src.size, _p(out), n)
+    return rc, out[:max(n, 0)]
 
 
 def sgemm_simd(a: np.ndarray, b: np.ndarray, m: int, n: int, k: int) -> np.ndarray:

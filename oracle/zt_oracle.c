@@ -452,6 +452,70 @@ EXPORT int orc_fp8_dequant(const uint8_t* src, int64_t src_len, float* dst, int6
     return 0;
 }
 
+/* tensor/iq3_storage.go:31-95 DequantizeIQ3S, one 110-byte super-block to
+ * 256 values, in the reference's loop order: sub-block i (scale nibble of
+ * byte 106 + i/2, multiplier d * (1 + 2 sc)), group j (qs bytes consumed in
+ * pairs, one sign byte), grid entries from tensor/iq3_grid.go:17-27 (2-bit
+ * field k of the 8 low index bits -> 1 + 2 field; the 9th bit, from qh,
+ * selects an identical half of the table). */
+static const uint8_t* orc_iq3s_grid(void) {
+    static uint8_t grid[512][4];
+    static int init = 0;
+    if (!init) {
+        for (int i = 0; i < 256; i++)
+            for (int k = 0; k < 4; k++) grid[i][k] = grid[256 + i][k] = (uint8_t)(1 + 2 * ((i >> (2 * k)) & 3));
+        init = 1;
+    }
+    return &grid[0][0];
+}
+
+static void orc_iq3s_block(const uint8_t* raw, float* dst) {
+    const uint8_t* grid = orc_iq3s_grid();
+    const float d = orc_f16_to_f32(rd16(raw));
+    const uint8_t *qs = raw + 2, *qh = raw + 66, *signs = raw + 74, *scales = raw + 106;
+    int qsi = 0, sgi = 0;
+    for (int i = 0; i < 8; i++) {
+        const uint8_t sc = (i % 2 == 0) ? (scales[i / 2] & 0x0F) : (scales[i / 2] >> 4);
+        const float sub = d * (float)(1 + 2 * (int)sc);
+        const uint8_t qhb = qh[i];
+        for (int j = 0; j < 4; j++) {
+            const int g1 = qs[qsi] | (((qhb >> (2 * j)) & 1) << 8);
+            qsi++;
+            const uint8_t sb = signs[sgi];
+            sgi++;
+            for (int k = 0; k < 4; k++) {
+                float v = sub * (float)grid[4 * g1 + k];
+                if (sb & (1 << k)) v = -v;
+                dst[i * 32 + j * 8 + k] = v;
+            }
+            const int g2 = qs[qsi] | (((qhb >> (2 * j + 1)) & 1) << 8);
+            qsi++;
+            for (int k = 0; k < 4; k++) {
+                float v = sub * (float)grid[4 * g2 + k];
+                if (sb & (1 << (k + 4))) v = -v;
+                dst[i * 32 + j * 8 + 4 + k] = v;
+            }
+        }
+    }
+}
+
+/* IQ3SStorage.Dequantize (tensor/iq3_storage.go:113-128) behind the
+ * registry's Dequantize (:169-179): status 1 when NewIQ3SStorageFromRaw
+ * rejects the input (n <= 0, fewer than ceil(n/256) * 110 bytes); a partial
+ * last block is decoded whole and its first values kept. */
+EXPORT int orc_iq3s_dequant(const uint8_t* src, int64_t src_len, float* dst, int64_t n) {
+    if (n <= 0) return 1;
+    const int64_t nb = (n + 255) / 256;
+    if (src_len < nb * 110) return 1;
+    float tmp[256];
+    for (int64_t b = 0; b < nb; b++) {
+        orc_iq3s_block(src + b * 110, tmp);
+        const int64_t rem = n - b * 256 < 256 ? n - b * 256 : 256;
+        memcpy(dst + b * 256, tmp, (size_t)rem * sizeof(float));
+    }
+    return 0;
+}
+
 /* ----------------------------------------- dequant + SgemmSimd matmuls */
 
 /* tensor/fp16_storage.go:53-63 Float16Storage.Slice. */

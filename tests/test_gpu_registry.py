@@ -67,6 +67,28 @@ def test_fp8_all_codes(eng, orc, name, e5m2):
         eng.dequantize(name, wire[:-1], codes.size)
 
 
+@pytest.mark.parametrize("n", [256, 4096, 300, 1])
+def test_iq3s(eng, orc, n):
+    raw = synth.iq3s(-(-n // 256), 54 + n)
+    rc, ref = orc.iq3s_dequant(raw, n)
+    assert rc == 0
+    assert bits_equal(eng.dequantize("IQ3_S", raw, n).cpu().numpy(), ref)
+    with pytest.raises(ValueError):
+        eng.dequantize("IQ3_S", raw[:-1], n)
+    with pytest.raises(ValueError):
+        eng.dequantize("IQ3_S", raw, 0)  # NewIQ3SStorageFromRaw rejects zero elements
+
+
+@pytest.mark.parametrize("n", [32, 1000, 7])
+def test_w8a8(eng, orc, n):
+    # W8A8's 36-byte groups are Q8_0's (tensor/quantized_w8a8.go:285-316)
+    w = synth.q8_0(1, -(-n // 32) * 32, 55)
+    assert bits_equal(eng.dequantize("W8A8", w.raw, n).cpu().numpy(), orc.q8_dequant(w.raw, n))
+    with pytest.raises(ValueError):
+        eng.dequantize("W8A8", w.raw[:-1], n)
+    assert eng.dequantize("W8A8", w.raw, 0).numel() == 0
+
+
 def test_unknown_name_and_empty(eng):
     with pytest.raises(ValueError):
         eng.dequantize("NOPE", np.zeros(4, np.uint8), 1)

@@ -3,8 +3,15 @@ restatement of its wire formats, on the CPU.
 
 Pins:
   * names, BlockSize and BitsPerWeight of every built-in format, as the
-    reference's own tests assert them (tensor/quant_registry_test.go:169-229,
-    tensor/quantized_awq_test.go:293-304), and RegisterQuantType's errors;
+    reference's own tests assert them (tensor/quant_registry_test.go:9-27,
+    169-229, 320-340, tensor/quantized_awq_test.go:293-304,
+    tensor/iq3_storage_test.go:400-411), and RegisterQuantType's errors;
+  * orc_iq3s_dequant: the known blocks of tensor/iq3_storage_test.go:199-289
+    (zeros, d = 0.5 with grid entries 0 and 255, the sign bits), the element
+    definition evaluated field by field in numpy on seeded blocks (bit for
+    bit: every product is exact), outputs independent of the qh bits (the
+    reference's grid repeats for the 9th index bit), partial last blocks,
+    and NewIQ3SStorageFromRaw's errors (short data, n <= 0);
   * orc_fp8_dequant: all 256 codes of both formats against the exact value
     of the bit fields, (-1)^s 2^(e-bias) (1 + m/2^M) or the subnormal
     (-1)^s 2^(1-bias) m/2^M, computed with Python fractions; E4M3's exponent
@@ -25,10 +32,12 @@ from ztensor_amd import registry, synth
 
 
 def test_builtin_names_and_sizes_match_the_reference():
-    assert registry.list_quant_types() == sorted(
-        ["Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q5_0", "FP8_E4M3", "FP8_E5M2", "AWQ_4"])
+    # TestQuantRegistryInitRegistrations (tensor/quant_registry_test.go:9-27), in its sorted order
+    assert registry.list_quant_types() == ["AWQ_4", "FP8_E4M3", "FP8_E5M2", "IQ3_S", "Q4_0", "Q4_K", "Q5_0",
+                                           "Q5_K", "Q6_K", "Q8_0", "W8A8"]
     want = {"Q4_0": (32, 4), "Q8_0": (32, 8), "Q4_K": (256, 4), "Q5_K": (256, 5), "Q6_K": (256, 6),
-            "Q5_0": (32, 5), "FP8_E4M3": (1, 8), "FP8_E5M2": (1, 8), "AWQ_4": (128, 4)}
+            "Q5_0": (32, 5), "FP8_E4M3": (1, 8), "FP8_E5M2": (1, 8), "AWQ_4": (128, 4), "W8A8": (32, 8),
+            "IQ3_S": (256, 3)}
     for name, (bs, bits) in want.items():
         d, ok = registry.get_quant_type(name)
         assert ok and (d.block_size, d.bits_per_weight) == (bs, bits), name
@@ -130,3 +139,51 @@ def test_awq4_wire_header_host_check_agrees_with_the_oracle(orc):
         assert (rc == 0) == (orc.awq4_wire_dequant(w, nn)[0] == 0)
         if rc == 0:
             assert (g.value, ng.value) == (group, 3)
+
+
+# ---- IQ3_S (tensor/iq3_storage.go) ------------------------------------------
+
+
+def iq3s_block(d: float) -> np.ndarray:
+    raw = np.zeros(110, np.uint8)
+    raw[0:2] = np.array([d], np.float16).view(np.uint8)
+    return raw
+
+
+def test_iq3s_known_blocks(orc):
+    # TestDequantizeIQ3S_Zeros / _KnownBlock / _Signs (tensor/iq3_storage_test.go:199-289)
+    rc, v = orc.iq3s_dequant(np.zeros(110, np.uint8), 256)
+    assert rc == 0 and not v.any()
+    raw = iq3s_block(0.5)
+    raw[3] = 0xFF  # second qs byte: grid entry 255 -> {7, 7, 7, 7}
+    rc, v = orc.iq3s_dequant(raw, 256)
+    assert rc == 0
+    assert np.array_equal(v[:4], np.full(4, 0.5, np.float32)) and np.array_equal(v[4:8], np.full(4, 3.5, np.float32))
+    raw = iq3s_block(1.0)
+    raw[74] = (1 << 0) | (1 << 6)
+    rc, v = orc.iq3s_dequant(raw, 256)
+    assert (v[0], v[1], v[6], v[7]) == (-1.0, 1.0, -1.0, 1.0)
+
+
+@pytest.mark.parametrize("n", [256, 768, 300, 1])
+def test_iq3s_element_definition_and_qh_independence(orc, n):
+    raw = synth.iq3s(-(-n // 256), 71 + n)
+    rc, v = orc.iq3s_dequant(raw, n)
+    assert rc == 0
+    want = synth.iq3s_values(raw, n).astype(np.float32)
+    assert np.array_equal(v.view(np.uint32), want.view(np.uint32))
+    flipped = raw.reshape(-1, 110).copy()
+    flipped[:, 66:74] ^= 0xFF  # the 9th grid-index bits
+    rc2, v2 = orc.iq3s_dequant(flipped.reshape(-1), n)
+    assert rc2 == 0 and np.array_equal(v2.view(np.uint32), v.view(np.uint32))
+
+
+def test_iq3s_errors(orc):
+    # TestNewIQ3SStorageFromRaw_InvalidSize / _InvalidElements (tensor/iq3_storage_test.go:313-330)
+    assert orc.iq3s_dequant(np.zeros(10, np.uint8), 256)[0] == 1
+    assert orc.iq3s_dequant(np.zeros(219, np.uint8), 257)[0] == 1
+    assert orc.iq3s_dequant(np.zeros(110, np.uint8), 0)[0] == 1
+    assert orc.iq3s_dequant(np.zeros(110, np.uint8), -1)[0] == 1
+    d, ok = registry.get_quant_type("IQ3_S")
+    assert ok and not d.empty_ok
+

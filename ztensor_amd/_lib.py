@@ -121,6 +121,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_awq4_wire_header": (I, [P, L, L, P, P]),
     "zt_dequant_awq4_f32": (I, [P, L, P, L, I, I, P]),
     "zt_dequant_fp8_f32": (I, [P, L, P, L, I, P]),
+    "zt_dequant_iq3s_f32": (I, [P, L, P, L, P]),
     "zt_gemm_int8_f32": (I, [P, P, P, I, I, I, P]),
     "zt_gemm_int4_f32": (I, [P, P, P, P, P, I, I, I, I, P]),
     "zt_gemm_int4_f32_rmul": (I, [P, P, P, P, P, I, I, I, I, P]),

@@ -17,6 +17,19 @@
 //    The decoders follow tensor/fp8_storage.go:229-250, 304-331: E4M3 has no
 //    NaN or infinity (exponent 15 is an ordinary binade), E5M2 maps
 //    exponent 31 to +-inf and NaN.
+//  * "IQ3_S": 110-byte super-blocks of 256 values [fp16 d][64 qs][8 qh]
+//    [32 sign bytes][4 scale bytes] (tensor/iq3_storage.go:12-95): value
+//    32 i + 8 j + 4 h + k of the block (sub-block i, group j, half h) takes
+//    qs byte 8 i + 2 j + h, whose 2-bit field k gives the magnitude
+//    1 + 2 field (the reference's grid, tensor/iq3_grid.go:15-27, is that
+//    formula for both values of the qh bit, so qh does not enter), the
+//    sub-block scale d * (1 + 2 sc) with sc the low / high nibble of scale
+//    byte i / 2, and sign bit k + 4 h of sign byte 4 i + j.
+//    w = (d * (1 + 2 sc)) * magnitude, negated when the sign bit is set;
+//    both products are exact in fp32.
+//  * "W8A8": the 36-byte [fp32 scale][32 int8] groups of Q8_0, with the same
+//    w = float32(q) * scale (tensor/quantized_w8a8.go:92-103, 285-316), so it
+//    runs zt_dequant_q8_f32.
 // "Q8_0", "Q4_K", "Q5_K", "Q6_K" and "Q5_0" are the raw blocks that
 // zt_dequant_q8_f32, zt_dequant_q4k/q5k/q6k_f32 and zt_dequant_q5_0_f32
 // already take.
@@ -98,6 +111,22 @@ __global__ void dequant_fp8_kernel(const uint8_t* __restrict__ wire, float* __re
     out[i] = (E5M2 ? decode_e5m2(b) : decode_e4m3(b)) * scale;
 }
 
+// One thread per output element of the IQ3_S super-blocks.
+__global__ void dequant_iq3s_kernel(const uint8_t* __restrict__ src, float* __restrict__ out, long nelem) {
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nelem) return;
+    const uint8_t* blk = src + (e >> 8) * 110;
+    const int v = (int)(e & 255), i = v >> 5, j = (v >> 3) & 3, h = (v >> 2) & 1, k = v & 3;
+    const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    const uint32_t sb = blk[106 + (i >> 1)];
+    const uint32_t sc = (i & 1) ? (sb >> 4) : (sb & 15u);
+    const float sub = d * (float)(1 + 2 * (int)sc);
+    const uint32_t q = blk[2 + 8 * i + 2 * j + h];
+    const float mag = (float)(1 + 2 * (int)((q >> (2 * k)) & 3u));
+    const float w = sub * mag;
+    out[e] = ((blk[74 + 4 * i + j] >> (k + 4 * h)) & 1u) ? -w : w;
+}
+
 }  // namespace zt
 
 using namespace zt;
@@ -138,5 +167,14 @@ ZT_EXPORT int zt_dequant_fp8_f32(const void* wire, long wire_bytes, float* out, 
         dequant_fp8_kernel<true><<<ceil_div(nelem, 256), 256, 0, stream>>>(w, out, nelem);
     else
         dequant_fp8_kernel<false><<<ceil_div(nelem, 256), 256, 0, stream>>>(w, out, nelem);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_dequant_iq3s_f32(const void* src, long src_bytes, float* out, long nelem, hipStream_t stream) {
+    if (nelem < 0 || src_bytes < 0) return (int)hipErrorInvalidValue;
+    if (nelem == 0) return (int)hipSuccess;
+    const long nblk = (nelem + 255) / 256;
+    if (src == nullptr || out == nullptr || src_bytes < nblk * 110) return (int)hipErrorInvalidValue;
+    dequant_iq3s_kernel<<<ceil_div(nelem, 256), 256, 0, stream>>>(static_cast<const uint8_t*>(src), out, nelem);
     return (int)hipGetLastError();
 }

@@ -646,6 +646,8 @@ class ROCmEngine:
         src = np.ascontiguousarray(src, np.uint8).reshape(-1)
         dst = torch.empty(n, dtype=torch.float32, device=self.device)
         if n == 0:
+            if not d.empty_ok:  # IQ3_S: NewIQ3SStorageFromRaw (tensor/iq3_storage.go:99-101)
+                raise ValueError(f"numElements must be positive, got {n}")
             return dst
         sd = self._to_dev(np.concatenate([src, np.zeros(-src.size % 16, np.uint8)]) if src.size % 16 else src)
         rc = d.run(self.lib, src, sd, dst, self._s)

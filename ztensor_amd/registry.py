@@ -5,8 +5,9 @@ Dequantize(src []byte, dst []float32), BlockSize(), BitsPerWeight(), with
 RegisterQuantType (panics on an empty name, a nil dequantizer or a second
 registration), GetQuantType and ListQuantTypes (sorted).  The built-in
 names are "Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q5_0", "FP8_E4M3",
-"FP8_E5M2" (tensor/quant_registry.go:231-240) and "AWQ_4"
-(tensor/quantized_awq.go:306-308).
+"FP8_E5M2" (tensor/quant_registry.go:231-240), "AWQ_4"
+(tensor/quantized_awq.go:306-308), "W8A8" (tensor/quantized_w8a8.go:320-322)
+and "IQ3_S" (tensor/iq3_storage.go:184-186).
 
 Here every built-in name maps to a libzt_hip.so entry point that decodes the
 same bytes on the GPU, bit for bit with the reference; ROCmEngine.dequantize
@@ -38,6 +39,7 @@ class DeviceDequantizer:
     block_size: int
     bits_per_weight: int
     run: DeviceFn
+    empty_ok: bool = True  # IQ3_S: the reference rejects zero elements (NewIQ3SStorageFromRaw)
 
 
 def _short(name: str, need: int, got: int) -> ValueError:
@@ -83,6 +85,29 @@ def _blocks(fn: str, name: str, vals: int, block_bytes: int) -> DeviceFn:
         return rc
 
     return run
+
+
+def _w8a8(lib, src, sd, dst, s):
+    # the Q8_0 36-byte groups (tensor/quantized_w8a8.go:285-316)
+    n = dst.numel()
+    need = -(-n // 32) * 36
+    if src.size < need:
+        raise _short("W8A8", need, src.size)
+    if n == 0:
+        return 0
+    return lib.zt_dequant_q8_f32(sd.data_ptr(), dst.data_ptr(), n, s)
+
+
+def _iq3s(lib, src, sd, dst, s):
+    # NewIQ3SStorageFromRaw (tensor/iq3_storage.go:98-111): a positive count
+    # and ceil(n / 256) super-blocks of 110 bytes
+    n = dst.numel()
+    if n <= 0:
+        raise ValueError(f"numElements must be positive, got {n}")
+    nb = -(-n // 256)
+    if src.size < nb * 110:
+        raise ValueError(f"IQ3_S raw data too short: need {nb * 110} bytes for {nb} blocks, got {src.size}")
+    return lib.zt_dequant_iq3s_f32(sd.data_ptr(), src.size, dst.data_ptr(), n, s)
 
 
 def _awq4(lib, src, sd, dst, s):
@@ -144,5 +169,7 @@ for _name, _bs, _bits, _fn in [
     ("FP8_E4M3", 1, 8, _fp8(0, "FP8_E4M3")),
     ("FP8_E5M2", 1, 8, _fp8(1, "FP8_E5M2")),
     ("AWQ_4", 128, 4, _awq4),
+    ("W8A8", 32, 8, _w8a8),
+    ("IQ3_S", 256, 3, _iq3s),
 ]:
-    register_quant_type(_name, DeviceDequantizer(_name, _bs, _bits, _fn))
+    register_quant_type(_name, DeviceDequantizer(_name, _bs, _bits, _fn, _name != "IQ3_S"))

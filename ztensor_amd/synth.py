@@ -410,6 +410,34 @@ def fp8_wire(codes: np.ndarray, scale: float) -> np.ndarray:
     return np.concatenate([np.array([scale], "<f4").view(np.uint8), np.asarray(codes, np.uint8)])
 
 
+def iq3s(nblocks: int, seed: int) -> np.ndarray:
+    """Seeded IQ3_S super-blocks (tensor/iq3_storage.go:12-29 layout, 110
+    bytes each): fp16 d = |N(0,1)| * 0.01, every qs, qh, sign and scale byte
+    uniform."""
+    g = rng(seed)
+    raw = g.integers(0, 256, size=(nblocks, 110), dtype=np.uint8)
+    d = f16_bits(np.abs(g.standard_normal(nblocks, dtype=np.float32)) * np.float32(0.01))
+    raw[:, 0:2] = d.reshape(-1, 1).view(np.uint8).reshape(nblocks, 2)
+    return raw.reshape(-1)
+
+
+def iq3s_values(raw: np.ndarray, n: int) -> np.ndarray:
+    """The IQ3_S element definition evaluated field by field in numpy (fp64):
+    value 32 i + 8 j + 4 h + k of a block = +-d (1 + 2 sc_i) (1 + 2 f), with
+    f the 2-bit field k of qs byte 8 i + 2 j + h, sc_i the low (even i) or
+    high (odd i) nibble of scale byte 106 + i / 2, and the sign from bit
+    k + 4 h of sign byte 74 + 4 i + j."""
+    b = np.asarray(raw, np.uint8).reshape(-1, 110)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1, 1)
+    v = np.arange(256)
+    i, j, h, k = v >> 5, (v >> 3) & 3, (v >> 2) & 1, v & 3
+    sc = np.where(i % 2 == 0, b[:, 106 + i // 2] & 15, b[:, 106 + i // 2] >> 4).astype(np.float64)
+    f = (b[:, 2 + 8 * i + 2 * j + h] >> (2 * k)) & 3
+    neg = (b[:, 74 + 4 * i + j] >> (k + 4 * h)) & 1
+    out = d * (1 + 2 * sc) * (1 + 2 * f.astype(np.float64))
+    return np.where(neg == 1, -out, out).reshape(-1)[:n]
+
+
 # ---- int4 / int8 GEMM operands (gemm_int4.h, gemm_int8.h)
 
 
