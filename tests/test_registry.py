@@ -54,6 +54,33 @@ def test_register_quant_type_rejects_like_the_reference():
         registry.register_quant_type("Q4_0", d)
 
 
+def test_registry_concurrent_registration_and_lookup(monkeypatch):
+    # TestQuantRegistryConcurrency (tensor/quant_registry_test.go:120-166) on an empty registry
+    import threading
+
+    monkeypatch.setattr(registry, "_registry", {})
+    fn = registry.get_quant_type  # noqa: F841 (the module functions read the patched dict)
+
+    def reg(i):
+        name = "CONCURRENT_" + chr(ord("A") + i)
+        registry.register_quant_type(name, registry.DeviceDequantizer(name, i + 1, 4, lambda *a: 0))
+
+    ts = [threading.Thread(target=reg, args=(i,)) for i in range(50)]
+    [t.start() for t in ts]
+    [t.join() for t in ts]
+    errs = []
+
+    def look(i):
+        d, ok = registry.get_quant_type("CONCURRENT_" + chr(ord("A") + i))
+        if not ok or d.block_size != i + 1:
+            errs.append(i)
+
+    ts = [threading.Thread(target=look, args=(i,)) for i in range(50)]
+    [t.start() for t in ts]
+    [t.join() for t in ts]
+    assert not errs and len(registry.list_quant_types()) == 50
+
+
 def exact_fp8(code: int, e5m2: bool) -> float:
     s, rest = code >> 7, code & 0x7F
     eb, mb, bias = (5, 2, 15) if e5m2 else (4, 3, 7)
