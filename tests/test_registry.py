@@ -59,7 +59,6 @@ def test_registry_concurrent_registration_and_lookup(monkeypatch):
     import threading
 
     monkeypatch.setattr(registry, "_registry", {})
-    fn = registry.get_quant_type  # noqa: F841 (the module functions read the patched dict)
 
     def reg(i):
         name = "CONCURRENT_" + chr(ord("A") + i)
