@@ -22,6 +22,10 @@ TOL = 1e-5  # every product exact in fp32: only the summation order differs
 KQ = ["q4_k", "q5_k", "q6_k"]
 LLAMA8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
 RAGGED = [(1, 256), (17, 768), (65, 2560), (5, 6912), (130, 1792)]
+# the reference's own GEMV test shapes (internal/cuda/kernels/gemv_q4k_test.go:363-368,
+# gemv_q5k_test.go:374-379, gemv_q6k_test.go:329-334; Q5_0: gemv_q5_0_test.go:260-265)
+REF_KQ = [(32, 256), (64, 512), (256, 256), (128, 1024), (1024, 256), (512, 2048)]
+REF_Q5_0 = [(32, 32), (64, 128), (128, 128), (128, 1024), (1024, 32), (512, 2048)]
 
 
 @pytest.fixture(scope="module")
@@ -77,7 +81,7 @@ def test_kquant_dequant_bit_exact(lib, orc, fmt, rows, K):
 
 
 @pytest.mark.parametrize("fmt", KQ)
-@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED)
+@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED + REF_KQ)
 def test_kquant_gemv_matches_oracle(lib, orc, fmt, rows, K):
     say(f"gemv {fmt} {rows}x{K}")
     w = synth.kquant(fmt, rows, K, synth.seed_for(6, K % 16))
@@ -128,7 +132,7 @@ def test_q6k_split_layout_bytes(lib, rows, K, off):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED + [(9, 16640), (300, 28672)])
+@pytest.mark.parametrize("rows,K", LLAMA8B + RAGGED + REF_KQ + [(9, 16640), (300, 28672)])
 def test_q6k_split_gemv_matches_oracle(lib, orc, rows, K):
     """zt_gemv_q6ks_f32 on the split layout against GemmF32Q6KNT, at the
     Llama-3-8B shapes, ragged ones and K past one step of 16 waves."""
@@ -218,7 +222,7 @@ def test_q5_0_dequant_bit_exact(lib, orc, rows, K):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.q5_0_dequant(w.raw, rows * K).view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,K", LLAMA8B + [(1, 32), (3, 96), (17, 4128), (65, 2080)])
+@pytest.mark.parametrize("rows,K", LLAMA8B + [(1, 32), (3, 96), (17, 4128), (65, 2080)] + REF_Q5_0)
 def test_q5_0_gemv_matches_oracle(lib, orc, rows, K):
     say(f"gemv q5_0 {rows}x{K}")
     w = synth.kquant("q5_0", rows, K, synth.seed_for(7, K % 16))

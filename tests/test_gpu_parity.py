@@ -109,9 +109,10 @@ def test_q4_gemv_matches_oracle(lib, orc, rows, K):
     assert rel_err(y.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("N", [2, 3, 8])
-def test_q4_batched_matches_oracle(lib, orc, N):
-    rows, K = 100, 512
+# (2, 32, 4) and (64, 128, 64): the reference's gemm_q4_f32 tests
+# (internal/cuda/kernels/gemm_q4_test.go:152, 235)
+@pytest.mark.parametrize("rows,K,N", [(100, 512, 2), (100, 512, 3), (100, 512, 8), (2, 32, 4), (64, 128, 64)])
+def test_q4_batched_matches_oracle(lib, orc, rows, K, N):
     w = synth.q4_0(rows, K, 21)
     x = synth.x_f32(K * N, 21).reshape(K, N)  # B is [K, N]
     a, off = q4_dev(w)
