@@ -811,9 +811,11 @@ def run_suite(args) -> None:
                 torch.cuda.empty_cache()
 
 
-# The BASELINE configurations as run by the engine's dispatch (batch-1 W4A16 on
-# packed (scale, zero) dwords, batched W4A16
-# and IQ4_NL on their tiled layouts), reported beside the headline.
+# The five benchmark configurations of this path (W4A16 GEMV, Q4_0 / Q8_0 at
+# the Llama-3-8B shapes, BitNet ternary, W4A16 at the Llama-3-70B shapes,
+# IQ4_NL at the Qwen2-7B shapes) as run by the engine's dispatch (batch-1
+# W4A16 on packed (scale, zero) dwords, batched W4A16 and IQ4_NL on their
+# tiled layouts), reported beside the headline.
 CONFIGS = {
     "1_w4a16_gemv": ["w4a16sz_c1"],
     "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
