@@ -458,7 +458,9 @@ def test_w4a16_invalid_group(lib):
 # --------------------------------------------------------------- Ternary
 
 
-@pytest.mark.parametrize("rows,K", BITNET + [(3, 4), (5, 33), (7, 64), (9, 260), (65, 2560)])
+@pytest.mark.parametrize("rows,K", BITNET + [(3, 4), (5, 33), (7, 64), (9, 260), (65, 2560), (33, 4160),
+                                              (6, 65536), (4, 65600), (2049, 128),
+                                              (1501, 256), (16397, 128), (3, 4096)])
 def test_ternary_i8_bit_exact(lib, orc, rows, K):
     say(f"ternary i8 rows={rows} K={K}")
     seed = synth.seed_for(3, BITNET.index((rows, K)) if (rows, K) in BITNET else 6)
