@@ -255,8 +255,8 @@ __device__ __forceinline__ int blkt_lds_row(int r) {
 template <BlkFmt F, int UPW, int N>
 __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict__ wt, const void* __restrict__ stl,
                                                         const uint32_t* __restrict__ aux, const float* __restrict__ x,
-                                                        float* __restrict__ y, float* __restrict__ ws, int rows,
-                                                        int K) {
+                                                        int rows, int K, int gx, int gy, float* __restrict__ y,
+                                                        float* __restrict__ ws) {
     constexpr int W = 4;
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
@@ -280,10 +280,12 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     const int li = lane & 15, lg = lane >> 4;
     const int nunits = K / 128;
     int byi = blockIdx.y, bxi = blockIdx.x;
-    if ((gridDim.x & 7) == 0) {
-        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
-        byi = j % gridDim.y;
-        bxi = (id & 7) + 8 * (j / gridDim.y);
+    // gx, gy: the grid's size, passed as arguments so they arrive in preloaded
+    // SGPRs (gridDim is a kernel-argument load that every address waits for)
+    if ((gx & 7) == 0) {
+        const int id = blockIdx.x + gx * blockIdx.y, j = id >> 3;
+        byi = j % gy;
+        bxi = (id & 7) + 8 * (j / gy);
     }
     const int u0 = byi * UPW, u1 = min(nunits, u0 + UPW);
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
@@ -567,7 +569,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             if constexpr (NPL == 1) v += __shfl_xor(v, 8);  // hi columns n + lo columns 8 + n
             acc[t][i] = ldexpf(v, 24 - sh);
         }
-    if (gridDim.y > 1) {
+    if (gy > 1) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const int rt = row0 / 16 + t;
@@ -590,7 +592,7 @@ static void launch_blkt(dim3 g, hipStream_t st, const uint4* wt, const void* sc,
     constexpr int NPL = N <= 8 ? 1 : 2;
     constexpr int SB = F == BlkFmt::Q8_0 ? 4 : (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K || F == BlkFmt::Q6_K) ? 8 : 2;  // LDS bytes per (row, block)
     const size_t lds = (size_t)NPL * mfma_chunk_xbytes(128 * UPW, 16) + 16 + (size_t)8 * UPW * 64 * SB;
-    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, aux, x, y, ws, M, K);
+    blkt_mfma_kernel<F, UPW, N><<<g, 256, lds, st>>>(wt, sc, aux, x, M, K, (int)g.x, (int)g.y, y, ws);
 }
 
 template <BlkFmt F, int N>

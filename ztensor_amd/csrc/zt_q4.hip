@@ -1024,8 +1024,9 @@ __global__ void iq4t_tile_kernel(const uint32_t* __restrict__ data, const uint16
 template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint16_t* __restrict__ stl,
-                                                             const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                             float* __restrict__ ws, int rows, int K, int nch) {
+                                                             const uint16_t* __restrict__ x, int rows, int K, int nch,
+                                                             int gx, int gy, float* __restrict__ y,
+                                                             float* __restrict__ ws) {
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
     constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
@@ -1040,10 +1041,12 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
     const int li = lane & 15, lg = lane >> 4;
     const int nunits = K / 128;
     int byi = blockIdx.y, bxi = blockIdx.x;
-    if ((gridDim.x & 7) == 0) {
-        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
-        byi = j % gridDim.y;
-        bxi = (id & 7) + 8 * (j / gridDim.y);
+    // gx, gy: the grid's size, passed as arguments so they arrive in preloaded
+    // SGPRs (gridDim is a kernel-argument load that every address waits for)
+    if ((gx & 7) == 0) {
+        const int id = blockIdx.x + gx * blockIdx.y, j = id >> 3;
+        byi = j % gy;
+        bxi = (id & 7) + 8 * (j / gy);
     }
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
     const int ntiles = (rows + 15) / 16;
@@ -1130,7 +1133,7 @@ __global__ void __launch_bounds__(W * 64) iq4nlt_mfma_kernel(const uint4* __rest
         }
     }
     }
-    if (gridDim.y > 1) {
+    if (gy > 1) {
         // K split: partial tiles to the workspace, summed in split order by tiled_reduce_kernel
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -1153,7 +1156,7 @@ static void launch_iq4t(dim3 g, hipStream_t st, const uint4* wt, const uint16_t*
                         float* ws, int M, int K, int nch) {
     constexpr int W = 4;
     const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 2048 + (size_t)2 * W * UPW * 64 * 2;
-    iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, y, ws, M, K, nch);
+    iq4nlt_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sc, x, M, K, nch, (int)g.x, (int)g.y, y, ws);
 }
 
 template <int N>

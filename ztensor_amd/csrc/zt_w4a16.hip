@@ -693,8 +693,9 @@ __global__ void w4t_sz_kernel(const uint16_t* __restrict__ scales, const uint16_
 template <int UPW, int W, int N>
 __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __restrict__ wt,
                                                              const uint32_t* __restrict__ szp,
-                                                             const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                             float* __restrict__ ws, int rows, int K, int gs, int nch) {
+                                                             const uint16_t* __restrict__ x, int rows, int K, int gs,
+                                                             int nch, int gx, int gy, float* __restrict__ y,
+                                                             float* __restrict__ ws) {
     constexpr int KC = 128 * UPW;
     constexpr int RW = 32 * W;
     constexpr int XP = (KC * 2 * N / 16 + W * 64 - 1) / (W * 64);
@@ -707,10 +708,12 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     const int li = lane & 15, lg = lane >> 4;
     const int nunits = K / 128;
     int byi = blockIdx.y, bxi = blockIdx.x;
-    if ((gridDim.x & 7) == 0) {
-        const int id = blockIdx.x + gridDim.x * blockIdx.y, j = id >> 3;
-        byi = j % gridDim.y;
-        bxi = (id & 7) + 8 * (j / gridDim.y);
+    // gx, gy: the grid's size, passed as arguments so they arrive in preloaded
+    // SGPRs (gridDim is a kernel-argument load that every address waits for)
+    if ((gx & 7) == 0) {
+        const int id = blockIdx.x + gx * blockIdx.y, j = id >> 3;
+        byi = j % gy;
+        bxi = (id & 7) + 8 * (j / gy);
     }
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
     const int ntiles = (rows + 15) / 16;
@@ -823,7 +826,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
         }
     }
     }
-    if (gridDim.y > 1) {
+    if (gy > 1) {
         // K split: partial tiles to the workspace, summed in split order by tiled_reduce_kernel
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -846,7 +849,7 @@ static void launch_w4t(dim3 g, hipStream_t st, const uint4* wt, const uint32_t* 
                        float* ws, int M, int K, int gs, int nch) {
     constexpr int W = 4;
     const size_t lds = (size_t)mfma_chunk_xbytes(128 * UPW, N) + 16 + 8 * UPW * 32 * W;
-    w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, y, ws, M, K, gs, nch);
+    w4a16t_mfma_kernel<UPW, W, N><<<g, W * 64, lds, st>>>(wt, sz, x, M, K, gs, nch, (int)g.x, (int)g.y, y, ws);
 }
 
 template <int N>
