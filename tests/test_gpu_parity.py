@@ -206,7 +206,8 @@ def test_q8_dequant_bit_exact_both_layouts(lib, orc, rows, K):
     assert np.array_equal(r[: 4 * nblk], s[: 4 * nblk]) and np.array_equal(r[off:], s[off:])
 
 
-@pytest.mark.parametrize("rows,K", LLAMA8B + [(3, 32), (65, 2080)])
+@pytest.mark.parametrize("rows,K", LLAMA8B + [(3, 32), (65, 2080), (17, 8160), (2, 6144), (2048, 16384),
+                                              (2047, 8224)])
 def test_q8_gemv_matches_oracle_both_layouts(lib, orc, rows, K):
     say(f"q8 gemv rows={rows} K={K}")
     seed = synth.seed_for(2, 8 + (LLAMA8B.index((rows, K)) if (rows, K) in LLAMA8B else 5))

@@ -183,15 +183,16 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
-// The same quad mapping in the fixed-step form of the Q4_0 kernel, for the
-// separated layouts: each wave does S steps of 16 blocks, every load issued
-// before any arithmetic as buffer loads with the wave-uniform row offsets as
-// scalar offsets; lanes past the last block read zeros.
+// The same quad mapping in the fixed-step form of the Q4_0 kernel: each wave
+// does S steps of 16 blocks, every load issued before any arithmetic as
+// buffer loads with the wave-uniform row offsets as scalar offsets; lanes
+// past the last block read zeros.  On the raw 36-byte blocks a lane's 8 data
+// bytes sit at block offset 4 + 8q, dword- but not 8-byte-aligned, which a
+// buffer load takes as one 8-byte load.
 template <int L, int S, int R>
 __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __restrict__ base, long data_offset,
                                                              const float* __restrict__ x, float* __restrict__ y,
                                                              int rows, int kb) {
-    static_assert(L != kRaw36, "separated layouts only");
     __shared__ float red[16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 3;
@@ -212,8 +213,12 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
-            d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rd, ok ? (uint32_t)(b * 32 + q * 8) : 0x80000000u,
-                                                           row * (uint32_t)kb * 32u, 2);  // nontemporal
+            if constexpr (L == kRaw36)
+                d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rs, ok ? (uint32_t)(b * 36 + 4 + q * 8) : 0x80000000u,
+                                                               row * (uint32_t)kb * 36u, 2);  // nontemporal
+            else
+                d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rd, ok ? (uint32_t)(b * 32 + q * 8) : 0x80000000u,
+                                                               row * (uint32_t)kb * 32u, 2);  // nontemporal
         }
     }
 #pragma unroll
@@ -224,7 +229,10 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
         for (int r = 0; r < R; r++) {
             const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
             const uint32_t so = ok ? (uint32_t)b * SB : 0x80000000u;
-            if constexpr (L == kSep16)
+            if constexpr (L == kRaw36)
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)b * 36u : 0x80000000u,
+                                                                row * (uint32_t)kb * 36u, 0);
+            else if constexpr (L == kSep16)
                 sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, row * (uint32_t)kb * SB, 0);
             else
                 sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, row * (uint32_t)kb * SB, 0);
@@ -293,20 +301,23 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
     if (N == 1) {
-        if constexpr (L != kRaw36) {
-            // fixed steps: S = 1 for K <= 4096, 2 for K <= 8192; longer rows
-            // (K = 14336 measured) stay on the loop kernel
-            if ((long)M * kb * 32 < 0x7fffffffL && data_offset < 0x7fffffffL && kb <= 256) {
-                const int S = kb <= 128 ? 1 : 2;
-                const int nws = ceil_div(kb, 16 * S);
-                const int Rs = pick_rows_per_wave(M, nws, 1, 2048);
-                const dim3 g(ceil_div(M, Rs)), blk(nws * kWave);
-                if (S == 1)
-                    launch_q8_steps<L, 1>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
-                else
-                    launch_q8_steps<L, 2>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
-                return (int)hipGetLastError();
-            }
+        // fixed steps: S = 1 for K <= 4096, 2 (up to 16 waves) beyond.  The
+        // separated layouts keep the loop kernel past K = 8192 (at K = 14336
+        // it measured 1-7% faster); on the raw blocks the fixed steps are
+        // faster up to K = 16384 once M >= 2048 (K = 14336: 17.6 against
+        // 22.6 us at 4096 rows, but 8.4 against 5.9 us at 1024 rows)
+        const bool steps_ok = kb <= 256 || (L == kRaw36 && kb <= 512 && M >= 2048);
+        if ((long)M * kb * (L == kRaw36 ? 36 : 32) < 0x7fffffffL && data_offset < 0x7fffffffL && steps_ok) {
+            const int S = kb <= 128 ? 1 : 2;
+            int nws = ceil_div(kb, 16 * S);
+            if (nws > 12) nws = 16;
+            const int Rs = pick_rows_per_wave(M, nws, 1, 2048);
+            const dim3 g(ceil_div(M, Rs)), blk(nws * kWave);
+            if (S == 1)
+                launch_q8_steps<L, 1>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
+            else
+                launch_q8_steps<L, 2>(Rs, g, blk, st, base, data_offset, B, C, M, kb);
+            return (int)hipGetLastError();
         }
         const int nw = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
