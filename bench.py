@@ -367,6 +367,7 @@ SUITE = {
     "q8_0": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_raw": ("q8_0_raw", [(4096, 4096), (14336, 4096)], [1]),
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
+    "ternary_f32": ("ternary_f32", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "w4a16sz_70b": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [1]),
     "w4a16sz_70b_k28672": ("w4a16sz", [(8192, 28672)], [1]),
@@ -563,6 +564,14 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         fn = lambda wb, y: lib.zt_ternary_gemv_i8(wb[0].data_ptr(), x.data_ptr(), sc.data_ptr(), sc.data_ptr() + 4,
                                                   y.data_ptr(), rows, K, s)
         nbytes = synth.algorithmic_bytes("ternary_i8", rows, K, N)
+    elif fmt == "ternary_f32":
+        t = synth.ternary(rows, K, seed)
+        from ztensor_amd.storage import TernaryStorage
+
+        wbufs = [dev(TernaryStorage(t.raw, rows * K).row_aligned(rows, K))]
+        x = torch.from_numpy(synth.x_f32(K, seed)).cuda()
+        fn = lambda wb, y: lib.zt_ternary_gemv_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, s)
+        nbytes = synth.algorithmic_bytes("ternary_f32", rows, K, N)
     elif fmt in ("q4_k", "q5_k", "q6_k"):
         w = synth.kquant(fmt, rows, K, seed)
         wbufs = [dev(w.raw)]
@@ -672,7 +681,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
 
 
 SUITE_FORMATS = ("int4", "int4_rmul", "int8", "q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
-                 "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "q4_k", "q5_k", "q6_k", "q6_ks", "q8_0_gguf", "q5_0")
+                 "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "ternary_f32", "q4_k", "q5_k", "q6_k", "q6_ks", "q8_0_gguf", "q5_0")
 
 
 def _pmc_case_arg(v: str) -> str:

@@ -488,7 +488,8 @@ def test_ternary_f32_reference_known_answers(lib, orc):
         assert np.array_equal(y.cpu().numpy(), np.array(case["want"], np.float32)), case["name"]
 
 
-@pytest.mark.parametrize("rows,K", BITNET + [(7, 33), (128, 256)])
+@pytest.mark.parametrize("rows,K", BITNET + [(7, 33), (128, 256), (65, 2560), (6, 65536), (4, 65600), (1501, 256),
+                                              (16397, 128), (3, 4096), (2049, 64)])
 def test_ternary_f32_matches_oracle(lib, orc, rows, K):
     t = synth.ternary(rows, K, 77)
     x = synth.x_f32(K, 77)

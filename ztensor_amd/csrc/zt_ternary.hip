@@ -235,6 +235,80 @@ __global__ void __launch_bounds__(1024) ternary_i8_steps_kernel(const uint8_t* _
 
 // ----------------------------------------------------------- fp32 x
 
+// fp32 x with K % 64 == 0 and K <= 65536: the fixed-step form of the int8
+// kernel above (each lane one 16-byte chunk of R rows, every load issued
+// before any arithmetic), with the 64 fp32 activations of the chunk as 16
+// buffer loads shared by the R rows, and sum (c - 1) x = sum c x - sum x.
+template <int R>
+__global__ void __launch_bounds__(1024) ternary_f32_steps_kernel(const uint8_t* __restrict__ W,
+                                                                 const float* __restrict__ x, float* __restrict__ y,
+                                                                 int rows, int bpr, int nw) {
+    __shared__ float red[16 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * R;
+    const int c = wave * 64 + lane;  // 16-byte chunk of the row: codes of elements 64c .. 64c+63
+    const bool ok = c * 16 < bpr;
+    const uint32_t voff = ok ? (uint32_t)c * 16u : 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, bpr * 16, 0x00020000);
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+        w[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff, row * (uint32_t)bpr, 2);  // nontemporal
+    }
+    u32x4 xv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (uint32_t)c * 256u + 16u * i : 0x80000000u, 0, 0);
+    float xs[64];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        xs[4 * i] = __uint_as_float(xv[i].x);
+        xs[4 * i + 1] = __uint_as_float(xv[i].y);
+        xs[4 * i + 2] = __uint_as_float(xv[i].z);
+        xs[4 * i + 3] = __uint_as_float(xv[i].w);
+    }
+    float xsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 64; e += 4) xsum += (xs[e] + xs[e + 1]) + (xs[e + 2] + xs[e + 3]);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                // codes of elements 16i + 4j + s, j = 0..3, one per byte
+                const uint32_t cds = (wd[i] >> (2 * s)) & 0x03030303u;
+                s0 = fmaf((float)(cds & 0xffu), xs[16 * i + s], s0);
+                s1 = fmaf((float)((cds >> 8) & 0xffu), xs[16 * i + 4 + s], s1);
+                s0 = fmaf((float)((cds >> 16) & 0xffu), xs[16 * i + 8 + s], s0);
+                s1 = fmaf((float)(cds >> 24), xs[16 * i + 12 + s], s1);
+            }
+        acc[r] = (s0 + s1) - xsum;
+    }
+    wave_reduce_rows<R>(acc);
+    if (nw == 1) {
+        if (is_row_writer<R>(lane)) {
+            const int r = row0 + row_of_lane<R>(lane);
+            if (r < rows) y[r] = acc[0];
+        }
+        return;
+    }
+    if (is_row_writer<R>(lane)) red[wave * R + row_of_lane<R>(lane)] = acc[0];
+    __syncthreads();
+    if ((int)threadIdx.x < R) {
+        float sm = 0.0f;
+        for (int w2 = 0; w2 < nw; w2++) sm += red[w2 * R + threadIdx.x];
+        const int r = row0 + threadIdx.x;
+        if (r < rows) y[r] = sm;
+    }
+}
+
+
 template <int CB, int R>
 __global__ void __launch_bounds__(512) ternary_f32_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                           float* __restrict__ y, int rows, int K, int bpr) {
@@ -331,6 +405,23 @@ static int ternary_gemv(bool i8, const void* Wv, const void* x, const float* xs,
     if (i8 && (xs == nullptr || ws == nullptr)) return (int)hipErrorInvalidValue;
     const uint8_t* W = static_cast<const uint8_t*>(Wv);
     const int bpr = (K + 3) / 4;
+    if (!i8 && K % 64 == 0 && K <= 65536 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
+        (long)M * bpr < 0x7fffffffL) {
+        // 4 rows a wave, as for int8 (at the BitNet shapes R = 1 / 2 / 4 / 8
+        // measured 5.33 / 3.87 / 3.77 / 3.77, 10.7 / 6.75 / 5.52 / 6.30 and
+        // 11.4 / 7.71 / 6.18 / 7.74 us)
+        const int nw = (K + 4095) / 4096;
+        int R = 4;
+        while (R > 1 && (long)ceil_div(M, R) * nw < 512) R >>= 1;
+        const dim3 g(ceil_div(M, R)), b(nw * kWave);
+        const float* xf = static_cast<const float*>(x);
+        switch (R) {
+            case 4: ternary_f32_steps_kernel<4><<<g, b, 0, st>>>(W, xf, y, M, bpr, nw); break;
+            case 2: ternary_f32_steps_kernel<2><<<g, b, 0, st>>>(W, xf, y, M, bpr, nw); break;
+            default: ternary_f32_steps_kernel<1><<<g, b, 0, st>>>(W, xf, y, M, bpr, nw); break;
+        }
+        return (int)hipGetLastError();
+    }
     if (i8 && K % 64 == 0 && K <= 65536 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
         (long)M * bpr < 0x7fffffffL) {
         const int nw = (K + 4095) / 4096;  // 16-byte chunks of 64 codes, 64 chunks a wave

@@ -360,6 +360,8 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
         return rows * K // vals * nbytes + 4 * K * N + 4 * rows * N
     if fmt == "ternary_i8":
         return rows * ((K + 3) // 4) + K * N + 4 * rows * N + 8
+    if fmt == "ternary_f32":
+        return rows * ((K + 3) // 4) + 4 * K * N + 4 * rows * N
     if fmt == "int4":
         ng = rows * (-(-K // group))
         return rows * K // 2 + 5 * ng + 4 * K * N + 4 * rows * N
