@@ -20,9 +20,10 @@
 // Work split: a lane owns CB consecutive bytes of a row (4*CB weights);
 // CB = 16 when bpr % 16 == 0 (one 128-bit load), 4 when bpr % 4 == 0, else
 // 1.  Its activations stay in registers while the wave walks R rows; waves of
-// a workgroup split K and combine through LDS.  int8 activations with
-// K % 64 == 0 (every BitNet shape) take a fixed-step form of the same split
-// (ternary_i8_steps_kernel) with every load issued first.
+// a workgroup split K and combine through LDS.  With K % 64 == 0 (every
+// BitNet shape) both activation types take a fixed-step form of the same
+// split (ternary_i8_steps_kernel, ternary_f32_steps_kernel) with every load
+// issued first.
 #include "zt_common.h"
 
 namespace zt {
