@@ -675,7 +675,8 @@ __global__ void w4t_sz_kernel(const uint16_t* __restrict__ scales, const uint16_
 // Small-batch W4A16 GEMM on the tiled layout (N in {4, 8, 12, 16}, K % 128 == 0,
 // group size % 128 == 0).  A workgroup of W waves owns 32 W rows (two 16-row
 // tiles a wave) and a K range of UPW 128-K units; K ranges are split across
-// workgroups (blockIdx.y) and add into C with fp32 atomics after a zero fill.
+// workgroups (blockIdx.y), each split stores its partial tiles to the
+// caller's workspace and tiled_reduce_kernel sums them in split order.
 //  * The X chunk and the workgroup's (scale, zero) dwords are loaded first
 //    (coalesced buffer loads), the weights next (each tile one contiguous
 //    1 KB load), and X / scales are written to LDS while the weights stream;
