@@ -371,6 +371,10 @@ SUITE = {
     "w4a16_70b": ("w4a16", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "w4a16sz_70b": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [1]),
     "w4a16sz_70b_k28672": ("w4a16sz", [(8192, 28672)], [1]),
+    "w4a16sz_70b_batched": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8]),
+    "w4a16sz_8b_batched": ("w4a16sz", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8]),
+    "w4a16_8b_batched": ("w4a16", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [12, 16]),
+    "w4a16t_8b": ("w4a16t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16]),
     "w4a16_70b_k28672": ("w4a16", [(8192, 28672)], [1]),
     "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
@@ -532,9 +536,10 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         if lib.zt_w4a16_pack_szr(sc.data_ptr(), zr.data_ptr(), rows, K, 128, szr.data_ptr(), s) != 0:
             raise RuntimeError("zt_w4a16_pack_szr failed")
         wbufs = [dev(w.packed), szr]
-        x = dev(synth.x_f16(K, seed))
-        fn = lambda wb, y: lib.zt_gemv_w4a16sz_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(),
-                                                   rows, K, 128, s)
+        x = dev(synth.x_f16(K * N, seed))
+        # batch 1: zt_gemv_w4a16sz_f32; batches of 4 and 8: the single-launch row-block MFMA GEMM
+        fn = lambda wb, y: lib.zt_gemm_w4a16sz_f32(wb[0].data_ptr(), wb[1].data_ptr(), x.data_ptr(), y.data_ptr(),
+                                                   rows, K, N, 128, s)
         nbytes = synth.algorithmic_bytes("w4a16", rows, K, N)
     elif fmt == "w4a16t":
         # the tiled upload layout (zt_w4a16_tile), built once outside the timing

@@ -251,6 +251,14 @@ int zt_w4a16_pack_szr(const uint16_t* scales, const uint16_t* zeros, int M, int 
                       zt_stream_t stream);
 int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* x, float* y, int M, int K,
                         int group_size, zt_stream_t stream);
+/* Batches of the same MatMulW4A16 (compute/w4a16.go:137-143) on the packed
+ * (scale, zero) dwords and the row-major weights as uploaded: B fp16 [K, N],
+ * C fp32 [M, N].  N == 1 is zt_gemv_w4a16sz_f32; N = 4, 8, 12 or 16 runs
+ * one launch with no workspace and the same result on every call.  Same
+ * conditions as zt_gemv_w4a16sz_f32 plus B 16-byte aligned, K <= 32768
+ * (N = 12, 16: K <= 8192); other N -> InvalidValue. */
+int zt_gemm_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* B, float* C, int M, int K, int N,
+                        int group_size, zt_stream_t stream);
 /* Bit-exact with GPTQStorage.Dequantize (tensor/quantized_gptq.go:134-163)
  * and AWQStorage.Dequantize (tensor/quantized_awq.go:118-136). */
 int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,

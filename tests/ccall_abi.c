@@ -77,6 +77,11 @@ int main(int argc, char** argv) {
     ccall20 grp = sym("zt_gemm_q4_group_f32");
     ccall20 off = sym("zt_q4_gpu_data_offset");
     ccall20 wsb = sym("zt_gemm_q4t_workspace_bytes");
+    ccall20 w4sz = sym("zt_gemm_w4a16sz_f32");
+    ccall20 w4t = sym("zt_gemm_w4a16t_f32");
+    ccall20 w4tws = sym("zt_gemm_w4a16t_workspace_bytes");
+    ccall20 iqt = sym("zt_gemm_iq4nlt_f16");
+    ccall20 iqtws = sym("zt_gemm_iq4nlt_workspace_bytes");
     if (failures) return 1;
 
     /* int return, no arguments */
@@ -93,6 +98,19 @@ int main(int argc, char** argv) {
     expect_int("zt_gemm_w4a16_f32(group = 48)", call(w4, p, p, p, p, p, 4, 96, 1, 48, 0, 0), 1);
     /* 11 arguments, the largest arity: N = 5 is not a tiled batch */
     expect_int("zt_gemm_q5_0t_f32(N = 5)", call(q50t, p, p, p, p, p, 16, 128, 5, p, 4096, 0), 1);
+    /* the batched W4A16 GEMM on packed scales: 9 arguments, N = 5 is not a batch it takes, M = 0 is a no-op */
+    expect_int("zt_gemm_w4a16sz_f32(N = 5)", call(w4sz, p, p, p, p, 4, 128, 5, 128, 0, 0, 0), 1);
+    expect_int("zt_gemm_w4a16sz_f32(M = 0)", call(w4sz, p, p, p, p, 0, 128, 4, 128, 0, 0, 0), 0);
+    /* the tiled GEMMs take (workspace, workspace_bytes) before the stream: a split-K shape with no
+       workspace is InvalidValue, and with the workspace it needs in the right argument slots the
+       validation passes on to the size checks (a K that is not a multiple of 128 stays invalid) */
+    expect_int("zt_gemm_w4a16t_workspace_bytes(1024, 8192, 8) > 0",
+               (long)call(w4tws, 1024, 8192, 8, 0, 0, 0, 0, 0, 0, 0, 0) > 0, 1);
+    expect_int("zt_gemm_w4a16t_f32(no workspace)", call(w4t, p, p, p, p, 1024, 8192, 8, 128, 0, 0, 0), 1);
+    expect_int("zt_gemm_w4a16t_f32(M = 0, workspace slots)", call(w4t, p, p, p, p, 0, 8192, 8, 128, p, 1 << 20, 0), 0);
+    expect_int("zt_gemm_iq4nlt_workspace_bytes(1024, 8192, 8) > 0",
+               (long)call(iqtws, 1024, 8192, 8, 0, 0, 0, 0, 0, 0, 0, 0) > 0, 1);
+    expect_int("zt_gemm_iq4nlt_f16(no workspace)", call(iqt, p, p, p, p, 1024, 8192, 8, 0, 0, 0, 0), 1);
     /* a host pointer argument: zero descriptors */
     expect_int("zt_gemm_q4_group_f32(n = 0)", call(grp, p, 0, p, 64, 0, 0, 0, 0, 0, 0, 0), 1);
     /* long returns come back whole */

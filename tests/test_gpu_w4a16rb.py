@@ -1,0 +1,188 @@
+"""GPU parity of the single-launch batched W4A16 GEMM on the row-major
+upload layout (zt_gemm_w4a16sz_f32 with N = 4, 8, 12 or 16, and
+zt_gemm_w4a16_f32, which routes the same batches to the same kernel on its
+two-array scales; past K = 8192 its N = 12 and 16 run the 16x16x32 MFMA
+kernel without a K split).
+
+This is the small-batch path of W4A16MatMuler.MatMulW4A16
+(compute/w4a16.go:137-143).  Bars:
+  * max|y - y_ref| / max|y_ref| <= 1e-5 against the oracle's restatement of
+    the reference CPU engine (dequantize, then SgemmSimd): each nibble enters
+    the MFMA as the fp16 2^14 + 2^10 q and every product is exact in fp32, so
+    only the summation order (and the cancellation of the 2^14 sum(x) term,
+    about one bit) differ;
+  * bit-identical from call to call and between the two entry points (one
+    launch, every output written once, a fixed order of adds: no atomics);
+  * the row-major entry point never adds K splits with atomics: repeated
+    calls give the same bits at every batch size.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from ztensor_amd import _lib, synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+LLAMA70B = [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return _lib.load()
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rel_err(y, ref) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def szr_dev(lib, w, zeros=True):
+    s = dev(w.scales)
+    z = dev(w.zeros) if zeros else None
+    szr = torch.empty(w.scales.size, dtype=torch.int32, device="cuda")
+    lib.call("zt_w4a16_pack_szr", s.data_ptr(), z.data_ptr() if zeros else 0, w.rows, w.K, w.group, szr.data_ptr(),
+             stream())
+    return szr
+
+
+def run_sz(lib, w, x16, N, zeros=True):
+    p, xd = dev(w.packed), dev(x16)
+    szr = szr_dev(lib, w, zeros)
+    c = torch.empty(w.rows * N, dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_w4a16sz_f32", p.data_ptr(), szr.data_ptr(), xd.data_ptr(), c.data_ptr(), w.rows, w.K, N, w.group,
+             stream())
+    return c.cpu().numpy()
+
+
+def run_rm(lib, w, x16, N, zeros=True):
+    p, s, xd = dev(w.packed), dev(w.scales), dev(x16)
+    z = dev(w.zeros) if zeros else None
+    c = torch.empty(w.rows * N, dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_w4a16_f32", p.data_ptr(), s.data_ptr(), z.data_ptr() if zeros else 0, xd.data_ptr(),
+             c.data_ptr(), w.rows, w.K, N, w.group, stream())
+    return c.cpu().numpy()
+
+
+@pytest.mark.parametrize("N", [4, 8, 12, 16])
+@pytest.mark.parametrize("rows,K,g", [(1, 32, 32), (3, 96, 32), (5, 128, 128), (17, 544, 32), (100, 4128, 32),
+                                      (300, 8192, 256), (64, 12288, 128), (33, 16896, 64), (9, 32768, 128),
+                                      (2049, 1024, 128)])
+def test_rb_ragged(lib, orc, rows, K, g, N):
+    """Partial row sets and workgroups, K not a multiple of a step (512) or of
+    16 waves' steps, group sizes 32-256, one to four steps a wave (K up to
+    32768), on both entry points."""
+    if N >= 12 and K > 8192:
+        pytest.skip("N >= 12 takes K <= 8192 on zt_gemm_w4a16sz_f32")
+    print(f"w4a16 rb rows={rows} K={K} g={g} N={N}", flush=True)
+    w = synth.w4a16(rows, K, 71, group=g)
+    x16 = synth.x_f16(K * N, 71 + N)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, g)
+    a = run_sz(lib, w, x16, N)
+    assert rel_err(a, ref) <= TOL
+    b = run_rm(lib, w, x16, N)
+    if N <= 8 or rows <= 2048:  # the row-major entry runs the same kernel
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    else:  # past 2048 rows it runs batches of 12 and 16 on the 16x16x32 MFMA kernel
+        assert rel_err(b, ref) <= TOL
+
+
+@pytest.mark.parametrize("N", [4, 8])
+@pytest.mark.parametrize("rows,K", LLAMA70B)
+def test_rb_70b_shapes(lib, orc, rows, K, N):
+    """The Llama-3-70B layer at full size against the oracle."""
+    print(f"w4a16 rb rows={rows} K={K} N={N}", flush=True)
+    seed = synth.seed_for(4, LLAMA70B.index((rows, K)))
+    w = synth.w4a16(rows, K, seed)
+    x16 = synth.x_f16(K * N, seed + N)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    assert rel_err(run_sz(lib, w, x16, N), ref) <= TOL
+
+
+def test_rb_non_integer_zero_and_default_zero(lib, orc):
+    """Any fp16 zero point (y subtracts z * sum(x) exactly); zeros == NULL is
+    the symmetric zero-point 8, on both entry points."""
+    rows, K, N = 64, 1024, 8
+    w = synth.w4a16(rows, K, 73)
+    rng = np.random.default_rng(73)
+    zeros = synth.f16_bits((rng.random(w.zeros.shape, dtype=np.float32) * 15).astype(np.float32))
+    w2 = synth.W4Weights(rows, K, w.group, w.packed, w.scales, zeros)
+    x16 = synth.x_f16(K * N, 73)
+    ref = orc.w4a16_matmul(w2.packed, w2.scales, w2.zeros, x16, rows, K, N, 128)
+    assert rel_err(run_sz(lib, w2, x16, N), ref) <= TOL
+    assert rel_err(run_rm(lib, w2, x16, N), ref) <= TOL
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)  # synth zeros are all 8
+    assert rel_err(run_sz(lib, w, x16, N, zeros=False), ref) <= TOL
+    assert rel_err(run_rm(lib, w, x16, N, zeros=False), ref) <= TOL
+
+
+def test_rb_small_and_single_activations(lib, orc):
+    """Activations of order 1e-4 (many fp16 subnormals: the A operands are
+    staged unscaled and the products stay exact), and a single nonzero
+    activation per column (each output is then one rounded product sum of
+    one chunk)."""
+    rows, K, N = 256, 2048, 4
+    w = synth.w4a16(rows, K, 74)
+    rng = np.random.default_rng(74)
+    x16 = synth.f16_bits(rng.standard_normal(K * N).astype(np.float32) * np.float32(1e-4))
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    assert rel_err(run_sz(lib, w, x16, N), ref) <= TOL
+    x = np.zeros((K, N), np.float32)
+    for n in range(N):
+        x[37 * (n + 1), n] = 1.5 + n
+    x16 = synth.f16_bits(x.reshape(-1))
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    assert rel_err(run_sz(lib, w, x16, N), ref) <= 1e-6
+
+
+def test_rb_repeated_calls_bit_identical(lib):
+    for rows, K, N in [(4096, 4096, 8), (1024, 8192, 4), (300, 28672, 8), (1024, 8192, 16)]:
+        w = synth.w4a16(rows, K, 75)
+        x16 = synth.x_f16(K * N, 75)
+        a = run_sz(lib, w, x16, N)
+        b = run_sz(lib, w, x16, N)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (rows, K, N)
+
+
+@pytest.mark.parametrize("N", [12, 16])
+def test_rm_large_k_wide_batch(lib, orc, N):
+    """zt_gemm_w4a16_f32 past K = 8192 at N = 12 and 16 (the 16x16x32 MFMA
+    kernel, one workgroup per 32 rows over all of K): the oracle's result,
+    bit for bit the same on a second call."""
+    rows, K = 256, 20480
+    w = synth.w4a16(rows, K, 76)
+    x16 = synth.x_f16(K * N, 76)
+    ref = orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, N, 128)
+    a = run_rm(lib, w, x16, N)
+    assert rel_err(a, ref) <= TOL
+    b = run_rm(lib, w, x16, N)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_rb_invalid_arguments(lib):
+    t = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    p = t.data_ptr()
+    f = lib.zt_gemm_w4a16sz_f32
+    assert f(p, p, p, p, 2, 128, 3, 128, stream()) == 1    # N not in {1, 4, 8, 12, 16}
+    assert f(p, p, p, p, 2, 128, 20, 128, stream()) == 1
+    assert f(p, p, p, p, 2, 8320, 12, 128, stream()) == 1   # N >= 12: K <= 8192
+    assert f(p, p, p, p, 2, 96, 4, 64, stream()) == 1      # K % group
+    assert f(p, p, p, p, 2, 128, 4, 48, stream()) == 1     # group % 32
+    assert f(p, p, p, p, 2, 32800, 4, 32, stream()) == 1   # K > 32768
+    assert f(p + 4, p, p, p, 2, 128, 4, 128, stream()) == 1  # W alignment
+    assert f(p, p, p + 8, p, 2, 128, 4, 128, stream()) == 1  # B alignment
+    assert f(p, p + 2, p, p, 2, 128, 4, 128, stream()) == 1  # szr alignment
+    assert f(p, p, p, 0, 2, 128, 4, 128, stream()) == 1    # C missing
+    assert f(p, p, p, p, 0, 128, 4, 128, stream()) == 0    # empty

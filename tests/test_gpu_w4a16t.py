@@ -200,14 +200,17 @@ def test_w4t_invalid_arguments(lib):
     assert lib.zt_w4a16_tile(p + 8, p, 0, 2, 128, 32, p, p, stream()) == 1  # W_packed alignment
 
 
+@pytest.mark.parametrize("N", [8, 16])
 @pytest.mark.parametrize("side", ["A", "B"])
-def test_engine_batched_w4a16_uses_tiled_layout(lib, orc, side):
-    """ROCmEngine.matmul_w4a16 with 8 activation columns (A side) or rows
-    (B side) builds the tiled copy once and matches the oracle."""
+def test_engine_batched_w4a16_dispatch(lib, orc, side, N):
+    """ROCmEngine.matmul_w4a16 with 8 or 16 activation columns (A side) or
+    rows (B side) matches the oracle.  16 columns build the tiled copy once;
+    8 columns of this short matrix run the row-block GEMM on the row-major
+    upload and build none."""
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import Float16Storage, GPTQStorage, Tensor
 
-    rows, K, N = 512, 1024, 8
+    rows, K = 512, 1024
     w = synth.w4a16(rows, K, 66)
     st = GPTQStorage.from_raw(w.packed.reshape(-1), w.scales.reshape(-1), w.zeros.reshape(-1), rows * K, 128, 4)
     eng = ROCmEngine()
@@ -224,7 +227,7 @@ def test_engine_batched_w4a16_uses_tiled_layout(lib, orc, side):
         y = eng.matmul_w4a16(act, Tensor((K, rows), st)).cpu().numpy()
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
-    assert getattr(st, "_gpu_tiled", None) is not None
+    assert (getattr(st, "_gpu_tiled", None) is not None) == (N == 16)
 
 
 def _w4t_call(lib, wt, sz, xd, c, rows, K, N, s, ws):

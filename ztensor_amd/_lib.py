@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_dequant_q4_f16": (I, [P, P, L, I, P]),
     "zt_w4a16_pack_szr": (I, [P, P, I, I, I, P, P]),
     "zt_gemv_w4a16sz_f32": (I, [P, P, P, P, I, I, I, P]),
+    "zt_gemm_w4a16sz_f32": (I, [P, P, P, P, I, I, I, I, P]),
     "zt_w4a16_tiled_bytes": (L, [I, I]),
     "zt_w4a16_sz_bytes": (L, [I, I, I]),
     "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),

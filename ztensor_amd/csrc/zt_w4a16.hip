@@ -27,7 +27,7 @@
 //
 // Small-batch GEMM (N = 4, 8, 12, 16): v_mfma_f32_16x16x32_f16, see the
 // MFMA section below.
-#include "zt_mfma.h"
+#include "zt_rbmfma.h"
 
 namespace zt {
 
@@ -348,6 +348,247 @@ __global__ void w4_szr_kernel(const uint16_t* __restrict__ scales, const uint16_
     szr[e] = (uint32_t)scales[e] | ((uint32_t)z << 16);
 }
 
+// ------------------------------------------------------------ row-block GEMM
+//
+// Batches of N = 4 or 8 on the row-major layout in one launch
+// (v_mfma_f32_4x4x4_16b_f16; lane roles, activation staging and the
+// reductions: zt_rbmfma.h).  A workgroup of nw waves owns 4R rows (R sets
+// of 4) over all of K; wave w takes steps w S .. w S + S - 1 (16 chunks of
+// 32 K each).  Every weight and (scale, zero) load of the wave's S steps is
+// issued up front, right after the first step's activation loads.
+//  * B operand of step s (0-7) of a lane's 16-byte chunk: the nibble pairs
+//    (e_m, e_m+4) of dword s/2, m = 2(s%2) and 2(s%2) + 1, K order
+//    8(s/2) + 2(s%2) + {0, 4, 1, 5}, each moved to mantissa bits 6-9 of
+//    the fp16 0x7400 = 2^14: b = 2^14 + 2^10 q exactly (a shift and an
+//    and-or a dword).  The MFMA products x b are exact in fp32.  (fp16
+//    subnormal weights, q 2^-24, would be one op cheaper, but products of
+//    that size come out of the gfx950 MFMAs about 100 ulp low on average,
+//    measured against fp64 sums; normal-range operands come out within
+//    0.2 ulp.)
+//  * a chunk lies in one group (group % 32 == 0), so its 8 MFMAs start from
+//    zero.  With X = sum(x b) and X1 = sum(x 2^14) (8 MFMAs with B = 2^14,
+//    per chunk and column), sum((q - z) x) s = (s 2^-10) X - (s (16 + z)
+//    2^-14) X1: two FMAs per output and chunk, exact for any fp16 zero.
+//  * the activation block of a step is read back as 8 A operands per n-set
+//    (ds_read_b64_tr_b16), which every row set of the step shares.
+// B operand of one MFMA step from a weight dword q: nibbles m and m + 1
+// (m = 2 odd) of each half moved to mantissa bits 6-9 under the exponent of
+// 2^14, two VALU ops a dword: a shift and v_and_or_b32, which the caller
+// enables by holding the mask in a VGPR and the exponent in an SGPR (two
+// literal constants do not fit one VOP3 instruction).
+__device__ __forceinline__ half4v rb_w4_operand(uint32_t q, int odd, uint32_t mask, uint32_t expo) {
+    const uint32_t lo = odd ? q >> 2 : q << 6, hi = odd ? q >> 6 : q << 2;
+    return __builtin_bit_cast(half4v, (uint2){(lo & mask) | expo, (hi & mask) | expo});
+}
+
+// SZ: meta is the packed (scale | zero << 16) dwords of zt_w4a16_pack_szr;
+// else meta is the fp16 scales and zeros the fp16 zeros (NULL: 8).
+template <int NB, int R, int S, bool SZ>
+__global__ void __launch_bounds__(1024) w4a16_rb_kernel(const uint32_t* __restrict__ packed,
+                                                        const void* __restrict__ meta,
+                                                        const uint16_t* __restrict__ zeros,
+                                                        const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                        int rows, int nchunk, int ngroups, float inv_cpg) {
+    using Lay = RbLayout<NB>;
+    constexpr int N = Lay::N, V = 4 * R * NB;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int blk = lane >> 2, j = lane & 3;
+    char* xs = smem + wave * Lay::STEP;
+    const int row0 = blockIdx.x * 4 * R;
+    // rows past M read zeros: the buffers end at row M
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)packed, (short)0, rows * nchunk * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)meta, (short)0, rows * ngroups * (SZ ? 4 : 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rz =
+        __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, zeros ? rows * ngroups * 2 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, nchunk * 64 * N, 0x00020000);
+    const int step0 = wave * S;
+    rb_stage_x<NB>(rx, xs, (uint32_t)step0 * Lay::STEP, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 w[S][R];
+    uint32_t sc[S][R], zr[S][R];
+    const uint32_t wrow = (uint32_t)(row0 + j) * (uint32_t)nchunk * 16u, wstep = 4u * (uint32_t)nchunk * 16u;
+    const uint32_t srow = (uint32_t)(row0 + j) * (uint32_t)ngroups * (SZ ? 4u : 2u),
+                   sstep = 4u * (uint32_t)ngroups * (SZ ? 4u : 2u);
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (step0 + t) * 16 + blk;
+        const bool ok = c < nchunk;
+        const uint32_t g = (uint32_t)(((float)c + 0.5f) * inv_cpg);
+        const uint32_t wo = ok ? wrow + (uint32_t)c * 16u : 0x80000000u;
+        const uint32_t so = ok ? srow + g * (SZ ? 4u : 2u) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + r * wstep, 0, 2);  // nontemporal
+            if (SZ) {
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, so + r * sstep, 0, 0);
+            } else {
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, so + r * sstep, 0, 0);
+                zr[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rz, so + r * sstep, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+    const half4v ones = (half4v){16384, 16384, 16384, 16384};  // 2^14
+    uint32_t bmask = 0x03C003C0u, bexp = 0x74007400u;
+    asm volatile("" : "+v"(bmask), "+s"(bexp));  // the mask in a VGPR, the exponent in an SGPR
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        if (t > 0) {
+            // every read of the previous step's activations has returned before the
+            // direct loads overwrite them (the compiler would otherwise sink some reads
+            // past the loads, which it does not see as writes to the same LDS)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            rb_stage_x<NB>(rx, xs, (uint32_t)(step0 + t) * Lay::STEP, lane);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            // wait for the activations only: the S R weight and S R (2 S R) scale loads issued after them may
+            // still be outstanding
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(SZ ? 2 * S * R : 3 * S * R) : "memory");
+        }
+        half4v xa[NB][8];
+        float4v dx[NB];
+#pragma unroll
+        for (int js = 0; js < NB; js++) {
+            dx[js] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; s++) xa[js][s] = rb_tr_read(xs, rb_tr_offset<NB>(lane, s, js));
+#pragma unroll
+            for (int s = 0; s < 8; s++) dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[js][s], ones, dx[js], 0, 0, 0);
+        }
+        // MFMA step outer, row set inner, in batches of RC row sets: the RC x NB
+        // accumulation chains of a batch interleave
+        constexpr int RC = R < 4 / NB ? R : 4 / NB;
+#pragma unroll
+        for (int r0 = 0; r0 < R; r0 += RC) {
+            float4v d[RC][NB];
+#pragma unroll
+            for (int r = 0; r < RC; r++)
+#pragma unroll
+                for (int js = 0; js < NB; js++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+#pragma unroll
+                for (int r = 0; r < RC; r++) {
+                    const u32x4& wv = w[t][r0 + r];
+                    const uint32_t q = (s >> 1) == 0 ? wv.x : (s >> 1) == 1 ? wv.y : (s >> 1) == 2 ? wv.z : wv.w;
+                    const half4v bv = rb_w4_operand(q, s & 1, bmask, bexp);
+#pragma unroll
+                    for (int js = 0; js < NB; js++)
+                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[js][s], bv, d[r][js], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RC; r++) {
+                const half2v szh = as_h2(sc[t][r0 + r]);
+                const float sv = (float)szh.x;
+                const float zv = SZ ? (float)szh.y : zeros ? (float)as_h2(zr[t][r0 + r]).x : 8.0f;
+                const float sa = sv * 0x1p-10f, sz = sv * (16.0f + zv) * 0x1p-14f;
+#pragma unroll
+                for (int js = 0; js < NB; js++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        float& a = acc[((r0 + r) * NB + js) * 4 + v];
+                        a = __builtin_fmaf(sa, d[r][js][v], __builtin_fmaf(-sz, dx[js][v], a));
+                    }
+            }
+        }
+    }
+    rb_block_reduce<V>(acc);
+    // waves split K: each wave leaves its sums in its own LDS region, then the
+    // workgroup adds them in wave order
+    float* red = reinterpret_cast<float*>(xs);
+    if ((lane & 12) == 0) {
+#pragma unroll
+        for (int i = 0; i < V / 4; i++) red[rb_value_index<V>(lane, i) * 4 + j] = acc[i];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < 4 * V; o += blockDim.x) {
+        // o walks C[row0 .., :] contiguously: o = (row - row0) * N + n
+        const int rl = o / N, n = o % N;
+        const int r = rl >> 2, jj = rl & 3, js = n >> 2, v = n & 3;
+        const int idx = ((r * NB + js) * 4 + v) * 4 + jj;
+        float sum = 0.0f;
+        for (int wv = 0; wv < nw; wv++) sum += reinterpret_cast<const float*>(smem + wv * Lay::STEP)[idx];
+        if (row0 + rl < rows) y[(long)row0 * N + o] = sum;
+    }
+}
+
+template <int NB, int R, int S, bool SZ>
+static void launch_w4a16_rb_t(dim3 g, int nw, hipStream_t st, const uint32_t* w, const void* meta,
+                              const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+    const size_t lds = (size_t)nw * RbLayout<NB>::STEP;
+    if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
+        static const bool raised = [] {
+            return hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_rb_kernel<NB, R, S, SZ>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        }();
+        (void)raised;
+    }
+    w4a16_rb_kernel<NB, R, S, SZ><<<g, nw * kWave, lds, st>>>(w, meta, z, x, y, rows, nchunk, nchunk / cpg,
+                                                               1.0f / (float)cpg);
+}
+
+template <int NB, bool SZ>
+static void launch_w4a16_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint32_t* w, const void* meta,
+                              const uint16_t* z, const uint16_t* x, float* y, int rows, int nchunk, int cpg) {
+#define ZT_RB(RR, SS) \
+    if (R == RR && S == SS) return launch_w4a16_rb_t<NB, RR, SS, SZ>(g, nw, st, w, meta, z, x, y, rows, nchunk, cpg);
+    if constexpr (NB <= 2) {
+        ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
+        ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(4, 2)
+        ZT_RB(1, 4) ZT_RB(2, 4)
+    } else {
+        ZT_RB(1, 1) ZT_RB(1, 2)
+    }
+    if constexpr (NB == 1) { ZT_RB(8, 1) }
+#undef ZT_RB
+}
+
+// Launch shape of the row-block GEMM: S steps a wave and up to 16 waves
+// splitting K (8 for N >= 12, whose activation blocks take 12-16 KB of LDS a
+// wave), and R row sets a workgroup chosen so that the grid holds about 512
+// workgroups, within 128 VGPRs (N >= 12: one row set).
+static void w4a16_rb_shape(int M, int N, int nchunk, int& R, int& S, int& nw) {
+    const int steps = ceil_div(nchunk, 16), wmax = N >= 12 ? 8 : 16;
+    S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
+    nw = ceil_div(steps, S);
+    const int rmax = N >= 12 ? 1 : min(8 / S, 32 / N);
+    R = 1;
+    while (R < rmax && ceil_div(M, 8 * R) >= 512) R *= 2;
+}
+
+// Shapes the row-block GEMM takes: N % 4 == 0 up to 16, K <= 32768 (N >= 12:
+// K <= 8192, two steps of 8 waves), 32-bit buffer offsets.
+static bool w4a16_rb_ok(int N, int nchunk, long M) {
+    if (N < 4 || N > 16 || N % 4 != 0 || M * nchunk * 16 >= 0x7fffffffL) return false;
+    return nchunk <= (N >= 12 ? 8 * 16 * 2 : 16 * 16 * 4);
+}
+
+template <bool SZ>
+static int launch_w4a16_rb(const uint32_t* w, const void* meta, const uint16_t* z, const uint16_t* x, float* y,
+                           int M, int K, int N, int group_size, hipStream_t st) {
+    const int nchunk = K / 32;
+    int R, S, nw;
+    w4a16_rb_shape(M, N, nchunk, R, S, nw);
+    const dim3 g(ceil_div(M, 4 * R));
+    switch (N) {
+        case 4: launch_w4a16_rb_n<1, SZ>(R, S, g, nw, st, w, meta, z, x, y, M, nchunk, group_size / 32); break;
+        case 8: launch_w4a16_rb_n<2, SZ>(R, S, g, nw, st, w, meta, z, x, y, M, nchunk, group_size / 32); break;
+        case 12: launch_w4a16_rb_n<3, SZ>(R, S, g, nw, st, w, meta, z, x, y, M, nchunk, group_size / 32); break;
+        default: launch_w4a16_rb_n<4, SZ>(R, S, g, nw, st, w, meta, z, x, y, M, nchunk, group_size / 32); break;
+    }
+    return (int)hipGetLastError();
+}
+
 // ------------------------------------------------------------ MFMA GEMM
 //
 // C[rows, N] = W[rows, K] x X[K, N] for 4 <= N <= 16, N % 4 == 0, K and the
@@ -522,10 +763,16 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     if (((uintptr_t)W_packed & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1))
         return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
+    // N = 4, 8 (and 12, 16 on up to 2048 rows, where the 32-row workgroups below would leave most
+    // CUs idle: 4.3 against 9.7 us at 1024 x 4096, batch 16; from 4096 rows the 16x16x32 kernel is
+    // faster, 10.2 against 13.3 us at 4096 x 4096)
+    if (w4a16_rb_ok(N, K / 32, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 2048))
+        return launch_w4a16_rb<false>(static_cast<const uint32_t*>(W_packed), scales, zeros, B, C, M, K, N,
+                                      group_size, stream);
     if (mfma_shape_ok(N, K, B) && group_size % 128 == 0) {
-        const int splits = mfma_splits(M, K);
-        if (splits > 1) mfma_zero(C, (long)M * N, stream);
-        w4a16_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), splits), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
+        // N = 12 or 16: one workgroup per 32 rows over all of K, so every output is written once
+        // (no K split, no atomics)
+        w4a16_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), 1), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
             static_cast<const uint8_t*>(W_packed), scales, zeros, B, C, M, K, N, group_size);
         return (int)hipGetLastError();
     }
@@ -606,6 +853,25 @@ ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, con
     else
         launch_w4a16_steps<4, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
     return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemm_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* B, float* C, int M,
+                                  int K, int N, int group_size, hipStream_t stream) {
+    if (N == 1) return zt_gemv_w4a16sz_f32(W_packed, szr, B, C, M, K, group_size, stream);
+    if (M < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0 || N < 4 || N > 16 ||
+        N % 4 != 0)
+        return (int)hipErrorInvalidValue;
+    if (M == 0) return (int)hipSuccess;
+    if (C == nullptr) return (int)hipErrorInvalidValue;
+    if (K == 0) {  // empty sums
+        mfma_zero(C, (long)M * N, stream);
+        return (int)hipGetLastError();
+    }
+    if (W_packed == nullptr || szr == nullptr || B == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)W_packed & 15) || ((uintptr_t)szr & 3) || ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
+    if (!w4a16_rb_ok(N, K / 32, M)) return (int)hipErrorInvalidValue;
+    return launch_w4a16_rb<true>(static_cast<const uint32_t*>(W_packed), szr, nullptr, B, C, M, K, N, group_size,
+                                 stream);
 }
 
 template <class OutT>

@@ -453,7 +453,13 @@ class ROCmEngine:
             if x.dtype != torch.float16:
                 raise TypeError("W4A16 matmul takes fp16 activations")
             tiled_ok = k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29
-            if n in _TILED_BATCHES and tiled_ok:
+            if (n in (4, 8) and s._gpu_szr is not None and rows * k // 2 < 1 << 31 and _p(x) % 16 == 0
+                    and _w4a16_rowblock(rows, k, n)):
+                # one launch on the row-major upload and the packed (scale, zero) dwords: no tiled copy,
+                # no workspace, no second kernel
+                self.lib.call("zt_gemm_w4a16sz_f32", _p(buf.tensor), _p(s._gpu_szr), _p(x), _p(c), rows, k, n,
+                              s.group_size, self._s)
+            elif n in _TILED_BATCHES and tiled_ok:
                 wt, sz = self._w4a16_tiled(s, rows, k)
                 self.gemm_w4a16t_f32(_p(wt), _p(sz), _p(x), _p(c), rows, k, n, s.group_size)
             elif (n == 1 and s._gpu_szr is not None and k <= 32768 and rows * k // 2 < 1 << 31
@@ -680,6 +686,22 @@ class ROCmEngine:
         w = self._to_dev(s.row_aligned(rows, cols))
         s._gpu_rows = ((rows, cols), w)  # type: ignore[attr-defined]
         return w
+
+
+def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
+    """Whether a batch of 4 or 8 W4A16 columns runs faster on the single-launch
+    row-block GEMM over the row-major upload (zt_gemm_w4a16sz_f32) than on the
+    tiled layout with its split-K reduction.  Measured (us, row-block against
+    tiled): batch 4 at 8192 x 8192 10.2 / 12.0, 4096 x 14336 (rows x K)
+    10.4 / 11.1, 8192 x 28672 37.2 / 28.8; batch 8 at 14336 x 4096
+    11.8 / 12.6, 1024 x 8192 4.1 / 6.2, 8192 x 8192 13.3 / 12.2, 4096 x 14336
+    15.1 / 11.3.  A batch-8 workgroup re-reads more activation bytes than
+    weight bytes once the rows are many and K is long."""
+    if k > 32768:
+        return False
+    if n == 4:
+        return k <= 16384
+    return k <= 4096 or rows <= 2048
 
 
 _TILED_BATCHES = (4, 8, 12, 16)  # batch sizes on the tiled layouts (W4A16, IQ4_NL, Q4_0, Q8_0, Q4_K, Q5_K, Q5_0)
