@@ -948,11 +948,13 @@ __global__ void w4t_sz_kernel(const uint16_t* __restrict__ scales, const uint16_
 //    1 KB load), and X / scales are written to LDS while the weights stream;
 //    the barrier waits for LDS only, so each unit computes as soon as its own
 //    weights arrive.
-//  * A operand: the nibble pairs (e_m, e_m+4) of a dword, (d >> 4m) &
-//    0x000F000F, are the fp16 subnormals e * 2^-24 exactly (7 VALU per 8
-//    weights), so a unit's MFMA sum is 2^-24 * sum(q x) with the products
-//    exact in fp32.  A sum-of-x MFMA with an all-ones A gives sum(x), and
-//    y += (s 2^24) * D - (s z) * sum(x), with s 2^24 and s z formed once per
+//  * A operand: the nibble pairs (e_m, e_m+4) of a dword moved to mantissa
+//    bits 6-9 under the exponent of 2^14 (a shift and an and-or a dword):
+//    a = 2^14 + 2^10 q exactly, and the MFMA products a x are exact in fp32.
+//    (fp16 subnormal weights q 2^-24 with unscaled activations give products
+//    that the gfx950 MFMAs sum about 100 ulp low.)  With D = sum(a x) and X1
+//    = sum(2^14 x) from an MFMA whose A is all 2^14,
+//    y += (s 2^-10) D - (s (16 + z) 2^-14) X1, both factors formed once per
 //    (row, unit) in fp32.
 //  * Workgroups are mapped XCD-aware: workgroup id mod 8 selects the XCD,
 //    and every K range of a row block runs on one XCD, whose L2 then holds
@@ -984,7 +986,9 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
     }
     const int rw0 = bxi * RW, row0 = rw0 + 32 * wave;
     const int ntiles = (rows + 15) / 16;
-    const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
+    const half8v ones = (half8v){16384, 16384, 16384, 16384, 16384, 16384, 16384, 16384};  // 2^14
+    uint32_t bmask = 0x03C003C0u, bexp = 0x74007400u;
+    asm volatile("" : "+v"(bmask), "+s"(bexp));  // v_and_or_b32: mask in a VGPR, exponent in an SGPR
     float4v acc[2];
     acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
     // this workgroup's K range: nch chunks of UPW units, one after another
@@ -1050,7 +1054,7 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
         const int e = tid + i * W * 64;
         if (e < UPW * RW && u0 + e / RW < u1) {
             const float sc = h2f(sr[i] & 0xffff), zz = h2f(sr[i] >> 16);
-            szs[e] = make_float2(sc * 16777216.0f, sc * zz);
+            szs[e] = make_float2(sc * 0x1p-10f, sc * (16.0f + zz) * 0x1p-14f);
         }
     }
     // LDS writes visible to the workgroup; the weight loads stay in flight.
@@ -1076,8 +1080,8 @@ __global__ void __launch_bounds__(W * 64) w4a16t_mfma_kernel(const uint4* __rest
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const uint32_t dw = s == 0 ? w[u][t].x : s == 1 ? w[u][t].y : s == 2 ? w[u][t].z : w[u][t].w;
-                    const u32x4 av = {dw & 0x000F000Fu, (dw >> 4) & 0x000F000Fu, (dw >> 8) & 0x000F000Fu,
-                                      (dw >> 12) & 0x000F000Fu};
+                    const u32x4 av = {((dw << 6) & bmask) | bexp, ((dw << 2) & bmask) | bexp,
+                                      ((dw >> 2) & bmask) | bexp, ((dw >> 6) & bmask) | bexp};
                     d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv, d[t], 0, 0, 0);
                 }
                 dn = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, bv, dn, 0, 0, 0);
