@@ -379,6 +379,8 @@ SUITE = {
     "w4a16t_70b": ("w4a16t", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8, 16]),
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
     "iq4nlt": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [8]),
+    "iq4nlt_b4": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [4]),
+    "iq4nl_batched": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [4, 8]),
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q6_k": ("q6_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),

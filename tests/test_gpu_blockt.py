@@ -345,8 +345,8 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     y = eng.matmul(Tensor((rows, K), s), xd).cpu().numpy()
     assert y.shape == (rows, n)
     assert rel_err(y, ref) <= TOL
-    if fmt == "w4a16" and n < 12:
-        # W4A16 chunks of 4 or 8 columns run the row-block GEMM on the row-major upload
+    if fmt in ("w4a16", "iq4nl") and n < 12:
+        # chunks of 4 or 8 columns run the row-block GEMM on the batch-1 upload
         assert getattr(s, "_gpu_tiled", None) is None
     else:
         assert getattr(s, "_gpu_tiled", None) is not None

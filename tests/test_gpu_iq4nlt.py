@@ -144,12 +144,15 @@ def test_iq4nlt_invalid_arguments(lib):
     assert lib.zt_iq4nl_tile(p, 2, 128, 8, p, p, stream()) == 1  # data not 16-byte aligned
 
 
+@pytest.mark.parametrize("N", [8, 16])
 @pytest.mark.parametrize("side", ["A", "B"])
-def test_engine_batched_iq4nl_uses_tiled_layout(lib, orc, side):
+def test_engine_batched_iq4nl_dispatch(lib, orc, side, N):
+    """16 columns build the tiled copy; 8 columns at K <= 8192 run the
+    row-block GEMM on the separated upload and build none."""
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import IQ4NLStorage, Tensor
 
-    rows, K, N = 512, 1024, 8
+    rows, K = 512, 1024
     w = synth.iq4nl(rows, K, 73)
     s = IQ4NLStorage.from_raw(w.raw, rows * K)
     eng = ROCmEngine()
@@ -163,7 +166,7 @@ def test_engine_batched_iq4nl_uses_tiled_layout(lib, orc, side):
         y = eng.matmul(xk.t().contiguous(), Tensor((K, rows), s)).cpu().numpy()
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
-    assert getattr(s, "_gpu_tiled", None) is not None
+    assert (getattr(s, "_gpu_tiled", None) is not None) == (N == 16)
 
 
 def test_iq4nlt_repeated_calls_bit_identical(lib):

@@ -30,7 +30,7 @@
 // Batched IQ4_NL calls with fp16 activations and 4 <= N <= 16 use the MFMA
 // GEMM further down; other batched calls (N > 1, column-strided
 // activations) use the block-per-lane kernel with one grid row per column.
-#include "zt_mfma.h"
+#include "zt_rbmfma.h"
 
 namespace zt {
 
@@ -650,6 +650,171 @@ __global__ void __launch_bounds__(512) iq4nl_mfma_kernel(const uint16_t* __restr
     mfma_reduce_store(acc, smem, y, row0, rows, N, gridDim.y > 1);
 }
 
+// ------------------------------------------------------------ IQ4_NL row-block GEMM
+//
+// Batches of N = 4, 8 (12, 16) with fp16 activations on the separated upload
+// layout, in one launch: the row-block structure of zt_rbmfma.h
+// (v_mfma_f32_4x4x4_16b_f16, lane = 32-element block of row j of a 4-row
+// set, waves splitting K, activations staged per wave and read back
+// transposed).  A block is one chunk, so it needs no regrouping.
+//  * MFMA step u (0-15) covers data byte u of the lane's block, elements
+//    2u and 2u+1: B = the byte's entry of a 2 KB LDS table,
+//    (T_hi[lo], T_hi[hi], T_lo[lo], T_lo[hi]) (iq4_quad_entry), against
+//    A = (x[2u], x[2u+1], x[2u], x[2u+1]), so the step's sum is
+//    x0 (T_hi + T_lo)[lo] + x1 (T_hi + T_lo)[hi], the fp32 codebook to
+//    within 2^-22 per entry, with every product exact;
+//  * the block's sum then takes the block's fp16 scale: y += d D.
+template <int NB, int R, int S>
+__global__ void __launch_bounds__(1024) iq4nl_rb_kernel(const uint16_t* __restrict__ scales,
+                                                        const uint32_t* __restrict__ data,
+                                                        const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                        int rows, int kb) {
+    using Lay = RbLayout<NB>;
+    constexpr int V = 4 * R * NB;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    uint2* tbl = reinterpret_cast<uint2*>(smem);  // 256 entries, one per data byte
+    char* regions = smem + 2048;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int blk = lane >> 2, j = lane & 3;
+    char* xs = regions + wave * Lay::STEP;
+    const int row0 = blockIdx.x * 4 * R;
+    // rows past M read zeros: the buffers end at row M
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, rows * kb * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, rows * kb * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 64 * Lay::N, 0x00020000);
+    const int step0 = wave * S;
+    rb_stage_x<NB>(rx, xs, (uint32_t)step0 * Lay::STEP, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 w[S][R];
+    uint32_t sc[S][R];
+    const uint32_t brow = (uint32_t)(row0 + j) * (uint32_t)kb, bstep = 4u * (uint32_t)kb;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (step0 + t) * 16 + blk;
+        const bool ok = c < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t b = brow + r * bstep + (uint32_t)c;
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? b * 16u : 0x80000000u, 0, 2);  // nontemporal
+            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? b * 2u : 0x80000000u, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = iq4_quad_entry(i);
+    // the table is visible to the workgroup; the loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        if (t > 0) {
+            // every read of the previous step's activations has returned before the
+            // direct loads overwrite them
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            rb_stage_x<NB>(rx, xs, (uint32_t)(step0 + t) * Lay::STEP, lane);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            // the activations only: the 2 S R weight and scale loads after them may be outstanding
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S * R) : "memory");
+        }
+        constexpr int RC = R < 4 / NB ? R : 4 / NB;
+#pragma unroll
+        for (int r0 = 0; r0 < R; r0 += RC) {
+            float4v d[RC][NB];
+#pragma unroll
+            for (int r = 0; r < RC; r++)
+#pragma unroll
+                for (int js = 0; js < NB; js++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                half4v xa[NB];
+#pragma unroll
+                for (int js = 0; js < NB; js++) xa[js] = rb_tr_read(xs, rb_tr_offset_pair<NB>(lane, u, js));
+#pragma unroll
+                for (int r = 0; r < RC; r++) {
+                    const u32x4& wv = w[t][r0 + r];
+                    const uint32_t q = (u >> 2) == 0 ? wv.x : (u >> 2) == 1 ? wv.y : (u >> 2) == 2 ? wv.z : wv.w;
+                    const int sh = 8 * (u & 3);
+                    const uint32_t off = (sh == 0 ? q << 3 : q >> (sh - 3)) & 0x7F8u;  // byte * 8
+                    const half4v bv = __builtin_bit_cast(half4v, *reinterpret_cast<const uint2*>(smem + off));
+#pragma unroll
+                    for (int js = 0; js < NB; js++)
+                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[js], bv, d[r][js], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RC; r++) {
+                const float dv = h2f((uint16_t)sc[t][r0 + r]);
+#pragma unroll
+                for (int js = 0; js < NB; js++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        float& a = acc[((r0 + r) * NB + js) * 4 + v];
+                        a = __builtin_fmaf(dv, d[r][js][v], a);
+                    }
+            }
+        }
+    }
+    rb_finish<NB, R>(acc, regions, Lay::STEP, xs, y, row0, rows);
+}
+
+template <int NB, int R, int S>
+static void launch_iq4nl_rb_t(dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data,
+                              const uint16_t* x, float* y, int rows, int kb) {
+    const size_t lds = 2048 + (size_t)nw * RbLayout<NB>::STEP;
+    if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
+        static const bool raised = [] {
+            return hipFuncSetAttribute(reinterpret_cast<const void*>(&iq4nl_rb_kernel<NB, R, S>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        }();
+        (void)raised;
+    }
+    iq4nl_rb_kernel<NB, R, S><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb);
+}
+
+template <int NB>
+static void launch_iq4nl_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data,
+                              const uint16_t* x, float* y, int rows, int kb) {
+#define ZT_RB(RR, SS) \
+    if (R == RR && S == SS) return launch_iq4nl_rb_t<NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb);
+    ZT_RB(1, 1) ZT_RB(1, 2)
+    if constexpr (NB <= 2) { ZT_RB(2, 1) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4) ZT_RB(4, 1) }
+#undef ZT_RB
+}
+
+// Launch shape and eligibility: as the W4A16 row-block GEMM (steps of 16
+// blocks, up to 16 waves splitting K, 8 for N >= 12), K <= 32768 (N >= 12:
+// K <= 8192).
+static bool iq4nl_rb_ok(int N, int kb, long M) {
+    if (N < 4 || N > 16 || N % 4 != 0 || M * kb * 16 >= 0x7fffffffL) return false;
+    return kb <= (N >= 12 ? 8 * 16 * 2 : 16 * 16 * 4);
+}
+
+static int launch_iq4nl_rb(const uint16_t* sc, const uint32_t* data, const uint16_t* x, float* y, int M, int kb, int N,
+                           hipStream_t st) {
+    const int steps = ceil_div(kb, 16), wmax = N >= 12 ? 8 : 16;
+    const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
+    const int nw = ceil_div(steps, S);
+    // R row sets a workgroup: up to 4 (2 past one step a wave) while about 200 or more workgroups
+    // remain.  Measured at 3584 x 3584 (rows x K): batch 4 R = 1 / 2 / 4: 5.42 / 4.99 / 5.11 us, batch 8
+    // 8.13 / 6.10 / 6.00; at 18944 x 3584, batch 8: 32.4 / 21.4 / 17.4 us (fewer activation bytes
+    // staged per weight byte)
+    const int rmax = N >= 12 ? 1 : S == 1 ? 4 : 2;
+    int R = 1;
+    while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
+    const dim3 g(ceil_div(M, 4 * R));
+    switch (N) {
+        case 4: launch_iq4nl_rb_n<1>(R, S, g, nw, st, sc, data, x, y, M, kb); break;
+        case 8: launch_iq4nl_rb_n<2>(R, S, g, nw, st, sc, data, x, y, M, kb); break;
+        case 12: launch_iq4nl_rb_n<3>(R, S, g, nw, st, sc, data, x, y, M, kb); break;
+        default: launch_iq4nl_rb_n<4>(R, S, g, nw, st, sc, data, x, y, M, kb); break;
+    }
+    return (int)hipGetLastError();
+}
+
 static size_t iq4_mfma_lds_bytes(int N) {
     const size_t stage = (size_t)mfma_xbytes(N) + 16 + 16 * 4 + kMfmaUC * 4 * kMfmaRows * sizeof(uint16_t);
     return stage > mfma_reduce_bytes() ? stage : mfma_reduce_bytes();
@@ -773,10 +938,13 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         return (int)hipGetLastError();
     }
     if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
+        // N = 4, 8 (12, 16 on up to 2048 rows): the row-block GEMM, one launch
+        if (iq4nl_rb_ok(N, kb, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 2048))
+            return launch_iq4nl_rb(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const uint16_t*>(B),
+                                   C, M, kb, N, st);
         if (mfma_shape_ok(N, K, B)) {
-            const int splits = mfma_splits(M, K);
-            if (splits > 1) mfma_zero(C, (long)M * N, st);
-            iq4nl_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), splits), kMfmaWaves * kWave, iq4_mfma_lds_bytes(N), st>>>(
+            // one workgroup per 32 rows over all of K: every output written once (no K split, no atomics)
+            iq4nl_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), 1), kMfmaWaves * kWave, iq4_mfma_lds_bytes(N), st>>>(
                 sc, reinterpret_cast<const uint4*>(data), reinterpret_cast<const uint16_t*>(B), C, M, K, N);
             return (int)hipGetLastError();
         }

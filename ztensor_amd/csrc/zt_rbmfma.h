@@ -77,6 +77,18 @@ __device__ __forceinline__ int rb_tr_offset(int lane, int s, int js) {
     return (c * Lay::PPC + p) * 16 + (b & 8);
 }
 
+// The same for the element pairs of IQ4_NL's interleaved nibbles: MFMA
+// step u reads K positions 2u + {0, 1, 0, 1} (each pair twice).
+template <int NB>
+__device__ __forceinline__ int rb_tr_offset_pair(int lane, int u, int js) {
+    using Lay = RbLayout<NB>;
+    const int e = (lane >> 2) & 3, q = lane & 3, c = 4 * (lane >> 4) + q;
+    const int k = 2 * u + (e & 1);
+    const int b = 2 * Lay::N * k + 8 * js;
+    const int p = (b / 16 + Lay::sig(c)) % Lay::PPC;
+    return (c * Lay::PPC + p) * 16 + (b & 8);
+}
+
 __device__ __forceinline__ half4v rb_tr_read(char* xs, int off) {
     return __builtin_bit_cast(half4v, tr_read_b64(xs, off));
 }
@@ -115,6 +127,34 @@ __device__ __forceinline__ void rb_block_reduce(float (&v)[V]) {
 template <int V>
 __device__ __forceinline__ int rb_value_index(int lane, int i) {
     return i + ((lane & 32) ? V / 2 : 0) + ((lane & 16) ? V / 4 : 0);
+}
+
+// End of a row-block GEMM: sums the wave's 16 blocks (lane exchanges), leaves
+// the wave's sums in its own LDS region `own`, and, after a barrier, adds the
+// waves' sums in wave order (wave w's region at regions + w * region_bytes)
+// and stores C rows row0 .. row0 + 4R - 1.  acc[(r NB + js) 4 + v] holds row
+// row0 + 4r + (lane & 3), column 4js + v.
+template <int NB, int R>
+__device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* regions, int region_bytes, char* own,
+                                          float* __restrict__ y, int row0, int rows) {
+    constexpr int N = 4 * NB, V = 4 * R * NB;
+    const int lane = threadIdx.x & 63, j = lane & 3, nw = blockDim.x >> 6;
+    rb_block_reduce<V>(acc);
+    float* red = reinterpret_cast<float*>(own);
+    if ((lane & 12) == 0) {
+#pragma unroll
+        for (int i = 0; i < V / 4; i++) red[rb_value_index<V>(lane, i) * 4 + j] = acc[i];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < 4 * V; o += blockDim.x) {
+        // o walks C[row0 .., :] contiguously: o = (row - row0) * N + n
+        const int rl = o / N, n = o % N;
+        const int r = rl >> 2, jj = rl & 3, js = n >> 2, v = n & 3;
+        const int idx = ((r * NB + js) * 4 + v) * 4 + jj;
+        float sum = 0.0f;
+        for (int wv = 0; wv < nw; wv++) sum += reinterpret_cast<const float*>(regions + wv * region_bytes)[idx];
+        if (row0 + rl < rows) y[(long)row0 * N + o] = sum;
+    }
 }
 
 }  // namespace zt

@@ -502,24 +502,9 @@ __global__ void __launch_bounds__(1024) w4a16_rb_kernel(const uint32_t* __restri
             }
         }
     }
-    rb_block_reduce<V>(acc);
     // waves split K: each wave leaves its sums in its own LDS region, then the
     // workgroup adds them in wave order
-    float* red = reinterpret_cast<float*>(xs);
-    if ((lane & 12) == 0) {
-#pragma unroll
-        for (int i = 0; i < V / 4; i++) red[rb_value_index<V>(lane, i) * 4 + j] = acc[i];
-    }
-    __syncthreads();
-    for (int o = threadIdx.x; o < 4 * V; o += blockDim.x) {
-        // o walks C[row0 .., :] contiguously: o = (row - row0) * N + n
-        const int rl = o / N, n = o % N;
-        const int r = rl >> 2, jj = rl & 3, js = n >> 2, v = n & 3;
-        const int idx = ((r * NB + js) * 4 + v) * 4 + jj;
-        float sum = 0.0f;
-        for (int wv = 0; wv < nw; wv++) sum += reinterpret_cast<const float*>(smem + wv * Lay::STEP)[idx];
-        if (row0 + rl < rows) y[(long)row0 * N + o] = sum;
-    }
+    rb_finish<NB, R>(acc, smem, Lay::STEP, xs, y, row0, rows);
 }
 
 template <int NB, int R, int S, bool SZ>

@@ -432,6 +432,11 @@ class ROCmEngine:
         elif isinstance(s, IQ4NLStorage):
             if x.dtype == torch.float32:
                 self.gemm_iq4nl_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype == torch.float16 and n in (4, 8) and k <= 8192 and _p(x) % 16 == 0:
+                # one launch on the separated upload (the row-block GEMM): no tiled copy, no workspace;
+                # faster than the tiled layout at K <= 8192 (3584 x 3584: 5.0 / 6.0 against 7.3 / 7.5 us at
+                # batch 4 / 8), slower past it (K = 18944, batch 8: 23.8 against 15.7 us)
+                self.gemm_iq4nl_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             elif x.dtype == torch.float16 and n in _TILED_BATCHES and k % 128 == 0:
                 wt, st = self._iq4nl_tiled(s, buf, rows, k)
                 ws, wsb = self._workspace(self.lib.zt_gemm_iq4nlt_workspace_bytes(rows, k, n))
