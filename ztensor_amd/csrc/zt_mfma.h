@@ -11,12 +11,9 @@
 //    with two ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b
 //    addresses X row r(a) and columns 4b .. 4b+3, and the read hands lane n
 //    the four values X[r(0..3)][n]; columns >= N address a zero word;
-//  * the waves' partial output tiles are summed through LDS at the end;
-//  * when the matrix has too few rows to fill the GPU, blockIdx.y splits K
-//    into contiguous unit ranges; the caller zeroes C first (mfma_zero, a
-//    plain kernel so that it can sit in a captured graph) and each split
-//    adds its partial tile with a hardware fp32 atomic.  The summation order
-//    of the splits, and so the last bits of C, then vary from run to run.
+//  * the waves' partial output tiles are summed through LDS at the end and
+//    every output is stored once: a workgroup covers all of K, so the
+//    result is the same on every run.
 #pragma once
 
 #include "zt_common.h"
@@ -100,7 +97,7 @@ __device__ __forceinline__ half8v mfma_b_pair(char* smem, int a, int db) {
 // D layout).  Uses smem as scratch; the caller has passed a barrier after
 // its last read of the staged chunk.
 __device__ __forceinline__ void mfma_reduce_store(float4v (&acc)[kMfmaTiles], char* smem, float* __restrict__ y,
-                                                  int row0, int rows, int N, bool split) {
+                                                  int row0, int rows, int N) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
@@ -115,30 +112,8 @@ __device__ __forceinline__ void mfma_reduce_store(float4v (&acc)[kMfmaTiles], ch
 #pragma unroll
         for (int wv = 0; wv < kMfmaWaves; wv++) sum += red[((wv * kMfmaTiles + t) * 4 + i) * 64 + ln];
         const int row = row0 + 16 * t + r;
-        if (n < N && row < rows) {
-            if (split)
-                unsafeAtomicAdd(&y[(long)row * N + n], sum);
-            else
-                y[(long)row * N + n] = sum;
-        }
+        if (n < N && row < rows) y[(long)row * N + n] = sum;
     }
-}
-
-// The unit range [ub, ue) of K-split blockIdx.y out of gridDim.y.
-__device__ __forceinline__ void mfma_split_range(int nunits, int& ub, int& ue) {
-    const int per = (nunits + gridDim.y - 1) / gridDim.y;
-    ub = min(nunits, (int)blockIdx.y * per);
-    ue = min(nunits, ub + per);
-}
-
-// Number of K splits: enough workgroups for ~2 per CU, each split keeping
-// at least one 128-K unit per wave.
-__host__ __forceinline__ int mfma_splits(int rows, int K) {
-    const int wgs = (rows + kMfmaRows - 1) / kMfmaRows;
-    const int nunits = K / 128;
-    int s = 1;
-    while (s < 16 && wgs * s < 512 && nunits / (2 * s) >= kMfmaWaves) s *= 2;
-    return s;
 }
 
 // ---- split-K through a workspace (tiled kernels)

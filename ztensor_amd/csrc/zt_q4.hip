@@ -27,9 +27,10 @@
 //  * IQ4_NL: a 256-entry LDS table maps a data byte to the fp32 codebook
 //    values of its two nibbles, one ds_read_b64 per two weights;
 //  * the block scale multiplies the block's partial sum once.
-// Batched IQ4_NL calls with fp16 activations and 4 <= N <= 16 use the MFMA
-// GEMM further down; other batched calls (N > 1, column-strided
-// activations) use the block-per-lane kernel with one grid row per column.
+// Batched IQ4_NL calls with fp16 activations and N = 4, 8, 12 or 16 use the
+// row-block MFMA GEMM further down (12 and 16 past 2048 rows the 16x16x32
+// MFMA GEMM); other batched calls (N > 1, column-strided activations) use
+// the block-per-lane kernel with one grid row per column.
 #include "zt_rbmfma.h"
 
 namespace zt {
@@ -587,8 +588,7 @@ __global__ void __launch_bounds__(512) iq4nl_mfma_kernel(const uint16_t* __restr
     for (int t = 0; t < NT; t++) abase[t] = (long)min(row0 + 16 * t + li, rows - 1) * kb;
     const MfmaBRole ro(li, N);
 
-    int ub, ue;
-    mfma_split_range(nunits, ub, ue);
+    const int ub = 0, ue = nunits;
     for (int c0 = ub; c0 < ue; c0 += kMfmaUC) {
         uint4 w[kMfmaUPW][NT];
 #pragma unroll
@@ -647,7 +647,7 @@ __global__ void __launch_bounds__(512) iq4nl_mfma_kernel(const uint16_t* __restr
         }
         __syncthreads();
     }
-    mfma_reduce_store(acc, smem, y, row0, rows, N, gridDim.y > 1);
+    mfma_reduce_store(acc, smem, y, row0, rows, N);
 }
 
 // ------------------------------------------------------------ IQ4_NL row-block GEMM
@@ -944,7 +944,7 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
                                    C, M, kb, N, st);
         if (mfma_shape_ok(N, K, B)) {
             // one workgroup per 32 rows over all of K: every output written once (no K split, no atomics)
-            iq4nl_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), 1), kMfmaWaves * kWave, iq4_mfma_lds_bytes(N), st>>>(
+            iq4nl_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows)), kMfmaWaves * kWave, iq4_mfma_lds_bytes(N), st>>>(
                 sc, reinterpret_cast<const uint4*>(data), reinterpret_cast<const uint16_t*>(B), C, M, K, N);
             return (int)hipGetLastError();
         }

@@ -25,8 +25,9 @@
 // 0x000F000F, which pairs element e with e+4 inside each dword; the
 // activations are pre-permuted into the same pairs once per lane.
 //
-// Small-batch GEMM (N = 4, 8, 12, 16): v_mfma_f32_16x16x32_f16, see the
-// MFMA section below.
+// Small-batch GEMM (N = 4, 8, 12, 16): the row-block GEMM on
+// v_mfma_f32_4x4x4_16b_f16, and for N = 12 and 16 past 2048 rows
+// v_mfma_f32_16x16x32_f16 (see the sections below).
 #include "zt_rbmfma.h"
 
 namespace zt {
@@ -630,8 +631,7 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
     const int offb = offa + 2;                                                      // rows {2,6,3,7}
     const half8v ones = (half8v){1, 1, 1, 1, 1, 1, 1, 1};
 
-    int ub, ue;
-    mfma_split_range(nunits, ub, ue);
+    const int ub = 0, ue = nunits;
     // Weights of the next chunk are loaded while the current chunk computes.
     uint4 wn[kMfmaUPW][NT];
     auto load_w = [&](int c0) {
@@ -696,7 +696,7 @@ __global__ void __launch_bounds__(512) w4a16_mfma_kernel(const uint8_t* __restri
         }
         __syncthreads();
     }
-    mfma_reduce_store(acc, smem, y, row0, rows, N, gridDim.y > 1);
+    mfma_reduce_store(acc, smem, y, row0, rows, N);
 }
 
 static size_t w4_mfma_lds_bytes(int N) {
@@ -757,7 +757,7 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     if (mfma_shape_ok(N, K, B) && group_size % 128 == 0) {
         // N = 12 or 16: one workgroup per 32 rows over all of K, so every output is written once
         // (no K split, no atomics)
-        w4a16_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows), 1), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
+        w4a16_mfma_kernel<<<dim3(ceil_div(M, kMfmaRows)), kMfmaWaves * kWave, w4_mfma_lds_bytes(N), stream>>>(
             static_cast<const uint8_t*>(W_packed), scales, zeros, B, C, M, K, N, group_size);
         return (int)hipGetLastError();
     }
