@@ -13,12 +13,16 @@ Also reported on the same JSON line:
   roofline      the dominant kernel (Q4_0 GEMV at 14336 x 4096, the gate/up
                 shape) timed with HIP events around graph replays of
                 back-to-back launches over rotating weight copies;
+  ceiling       a plain streaming read of the same weight bytes in the same
+                timing at each shape (per_shape.*.frac_of_ceiling = read
+                time / GEMV time): what one launch per GEMV can reach;
   cpu_baseline  the C restatement of the reference CPU engine's Q4_0 GEMV
                 (GemmF32Q4NT, internal/xblas/gemm_quant.go:81-157) on the
                 host cores, over one layer's seven matrices;
   configs       every benchmark configuration's shapes and batches as the
-                engine runs them (batched W4A16 / IQ4_NL on their tiled
-                layouts): [format, "KxN", batch, us per matmul, % of peak]
+                engine runs them (batched W4A16 / IQ4_NL on the row-block
+                GEMM or the tiled layouts, whichever the engine picks):
+                [format, "KxN", batch, us per matmul, % of peak]
                 (skipped with --no-configs);
   configs_cpu   the CPU restatement of each configuration's reference CPU
                 path on one representative shape, about 2 s each (skipped
@@ -208,8 +212,13 @@ def run_headline(args) -> dict:
     log(f"bench: {ms * 1e3:.1f} us/step, {value:.1f} GB/s ({100 * value / PEAK_GBS:.1f}% of peak), wall {wall:.2f}s")
 
     # Per-shape and dominant-kernel timings: graphs of back-to-back launches
-    # rotating over the layer copies.
+    # rotating over the layer copies, each beside the ceiling: a plain
+    # 16-byte-a-lane streaming read of the same weight buffers in the same
+    # graph timing (zt_bench_stream_read).
     per_shape = {}
+    ceiling = {"kernel": "zt_bench_stream_read: nontemporal 16-byte loads a lane, no arithmetic, over the same "
+                         "rotating weight buffers and graph timing as the GEMV", "per_shape": {}}
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     dom = None
     for (name, rows, K), m in zip(LLAMA3_8B, mats):
         if name in ("k", "up"):
@@ -225,20 +234,38 @@ def run_headline(args) -> dict:
         gl.replay()
         us = time_graph(torch, gl, max(3, args.steps // 20)) * 1e3 / n
         gbs = m.bytes / (us * 1e-6) / 1e9
+
+        def read_loop(m=m, n=n):
+            s = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                buf = m.copies[i % layers]
+                if lib.zt_bench_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), s) != 0:
+                    raise RuntimeError("zt_bench_stream_read failed")
+
+        gr = graph_of(torch, read_loop)
+        gr.replay()
+        cus = time_graph(torch, gr, max(3, args.steps // 20)) * 1e3 / n
+        wbytes = m.copies[0].numel()
+        ceiling["per_shape"][f"{name} {K}x{rows}"] = {
+            "us": round(cus, 3), "bytes_read": wbytes, "GB/s": round(wbytes / (cus * 1e-6) / 1e9, 1),
+            "pct_peak": round(100 * wbytes / (cus * 1e-6) / 1e9 / PEAK_GBS, 1)}
         per_shape[f"{name} {K}x{rows}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
-                                           "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": m.bytes}
+                                           "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": m.bytes,
+                                           "ceiling_us": round(cus, 3), "frac_of_ceiling": round(cus / us, 3)}
         if name == "gate":
             dom = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                   "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                   "frac": round(gbs / PEAK_GBS, 4), "frac_of_ceiling": round(cus / us, 4), "traffic": None,
                    "kernel": "gemv_q4_steps_kernel<S=1, R=8> (zt_gemm_q4_f32), K=4096 x N=14336, batch 1",
                    "bytes_per_launch": m.bytes, "us_per_launch": round(us, 3)}
-        log(f"bench: {name:5s} K={K:5d} N={rows:5d}: {us:7.2f} us  {gbs:7.1f} GB/s")
+        log(f"bench: {name:5s} K={K:5d} N={rows:5d}: {us:7.2f} us  {gbs:7.1f} GB/s  (streaming read of the same "
+            f"bytes: {cus:.2f} us)")
 
     if dom is not None:
         dom["traffic"] = measured_traffic(dom["kernel"])
 
     grouped = run_grouped_step(torch, lib, args, mats, step_bytes)
     merged = run_merged_step(torch, lib, args) if args.merged else None
+    bitnet = run_bitnet_step(torch, lib, args) if args.merged else None
 
     # Parity spot check of the last replayed outputs against the oracle.
     from oracle import oracle
@@ -275,8 +302,10 @@ def run_headline(args) -> dict:
             "parity_rel_err": err,
         },
         "per_shape": per_shape,
+        "ceiling": ceiling,
         "grouped_projections": grouped,
         "merged_projections": merged,
+        "bitnet_layer_step": bitnet,
         "roofline": dom,
         "cpu_baseline": cpu,
     }
@@ -324,6 +353,84 @@ def run_grouped_step(torch, lib, args, mats, step_bytes: int) -> dict:
             "pct_of_peak": round(100 * value / PEAK_GBS, 1), "launches_per_layer": 4,
             "workload": "the headline step, q/k/v and gate/up each one zt_gemm_q4_group_f32 launch over the "
                         "separate uploads"}
+
+
+def run_bitnet_step(torch, lib, args, layers: int = 32) -> dict:
+    """A BitNet-2B decode step over the configuration-3 shapes with int8
+    activations: per layer q, k, v, o (2560 x 2560), gate, up (6912 x 2560)
+    and down (2560 x 6912) as rows x K, 32 distinct layer copies resident
+    (about 630 MB, beyond the Infinity Cache).  Timed as 7 zt_ternary_gemv_i8
+    launches a layer, and as 4 with q/k/v and gate/up each one
+    zt_ternary_gemv_i8_group launch over the same uploads."""
+    from ztensor_amd import _lib as zl
+    from ztensor_amd import synth
+    from ztensor_amd.storage import TernaryStorage
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+    shapes = [("q", 2560, 2560), ("k", 2560, 2560), ("v", 2560, 2560), ("o", 2560, 2560), ("gate", 6912, 2560),
+              ("up", 6912, 2560), ("down", 2560, 6912)]
+    mats = {}
+    for i, (name, rows, K) in enumerate(shapes):
+        t = synth.ternary(rows, K, 0x5EED0070 + i)
+        w = dev(TernaryStorage(t.raw, rows * K).row_aligned(rows, K))
+        mats[name] = {"rows": rows, "K": K, "w": [w] + [w.clone() for _ in range(layers - 1)],
+                      "ws": torch.tensor([t.w_scale], dtype=torch.float32, device="cuda"),
+                      "y": [torch.empty(rows, dtype=torch.float32, device="cuda") for _ in range(layers)]}
+    xq = {}
+    for K in (2560, 6912):
+        q, xs = synth.x_i8(K, 0x5EED0078 + K)
+        xq[K] = (dev(q), torch.tensor([xs], dtype=torch.float32, device="cuda"))
+    step_bytes = layers * sum(synth.algorithmic_bytes("ternary_i8", rows, K, 1) for _, rows, K in shapes)
+
+    def single(name, layer, s):
+        m = mats[name]
+        x, xs = xq[m["K"]]
+        rc = lib.zt_ternary_gemv_i8(m["w"][layer].data_ptr(), x.data_ptr(), xs.data_ptr(), m["ws"].data_ptr(),
+                                    m["y"][layer].data_ptr(), m["rows"], m["K"], s)
+        if rc != 0:
+            raise RuntimeError(f"zt_ternary_gemv_i8 returned {rc}")
+
+    plan = []
+    for layer in range(layers):
+        for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            if len(names) == 1:
+                plan.append(("one", names[0], layer))
+                continue
+            descs = zl.ternary_gemv_descs([(mats[n]["w"][layer].data_ptr(), mats[n]["ws"].data_ptr(),
+                                           mats[n]["y"][layer].data_ptr(), mats[n]["rows"]) for n in names])
+            plan.append(("group", descs, len(names), 2560))
+
+    def step_single():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            for name, _, _ in shapes:
+                single(name, layer, s)
+
+    def step_grouped():
+        s = torch.cuda.current_stream().cuda_stream
+        for item in plan:
+            if item[0] == "one":
+                single(item[1], item[2], s)
+            else:
+                _, descs, n, K = item
+                x, xs = xq[K]
+                rc = lib.zt_ternary_gemv_i8_group(descs, n, x.data_ptr(), xs.data_ptr(), K, s)
+                if rc != 0:
+                    raise RuntimeError(f"zt_ternary_gemv_i8_group returned {rc}")
+
+    out = {"workload": f"BitNet-2B decode step, {layers} layers x {{q,k,v,o 2560x2560; gate,up 6912x2560; "
+                       "down 2560x6912}} (rows x K) ternary GEMVs, int8 activations", "bytes_per_step": step_bytes}
+    for key, fn, launches in (("per_gemv", step_single, 7), ("grouped", step_grouped, 4)):
+        g = graph_of(torch, fn)
+        for _ in range(args.warmup):
+            g.replay()
+        ms = time_graph(torch, g, args.steps)
+        out[key] = {"us_per_layer": round(ms * 1e3 / layers, 3), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                    "launches_per_layer": launches}
+        log(f"bench: BitNet step, {key}: {ms * 1e3 / layers:.2f} us per layer")
+    del mats
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_merged_step(torch, lib, args) -> dict:
@@ -380,6 +487,9 @@ SUITE = {
     "iq4nl": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 8]),
     "iq4nlt": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [8]),
     "iq4nlt_b4": ("iq4nlt", [(3584, 3584), (18944, 3584), (3584, 18944)], [4]),
+    # the engine's dispatch (row-block or tiled) at the configuration shapes
+    "w4a16_70b_engine": ("w4a16_engine", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
+    "iq4nl_engine": ("iq4nl_engine", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 4, 8]),
     "iq4nl_batched": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [4, 8]),
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
@@ -414,6 +524,12 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
 
     s = torch.cuda.current_stream().cuda_stream
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+    if fmt == "w4a16_engine":  # the kernel ROCmEngine picks for this batch
+        from ztensor_amd.engine import _w4a16_rowblock
+
+        fmt = "w4a16sz" if N == 1 or (N in (4, 8) and _w4a16_rowblock(rows, K, N)) else "w4a16t"
+    elif fmt == "iq4nl_engine":
+        fmt = "iq4nl" if N == 1 or (N in (4, 8) and K <= 8192) else "iq4nlt"
     if fmt == "q4_0" or fmt == "iq4nl":
         w = synth.q4_0(rows, K, seed) if fmt == "q4_0" else synth.iq4nl(rows, K, seed)
         nblk = rows * K // 32
@@ -687,7 +803,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     return r
 
 
-SUITE_FORMATS = ("int4", "int4_rmul", "int8", "q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
+SUITE_FORMATS = ("w4a16_engine", "iq4nl_engine", "int4", "int4_rmul", "int8", "q4_0", "iq4nl", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
                  "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "ternary_f32", "q4_k", "q5_k", "q6_k", "q6_ks", "q8_0_gguf", "q5_0")
 
 
@@ -836,8 +952,8 @@ CONFIGS = {
     "1_w4a16_gemv": ["w4a16sz_c1"],
     "2_q4_0_q8_0_llama3_8b": ["q4_0", "q8_0"],
     "3_ternary_bitnet": ["ternary"],
-    "4_w4a16_llama3_70b": ["w4a16sz_70b", "w4a16sz_70b_k28672", "w4a16t_70b"],
-    "5_iq4nl_qwen2_7b": [("iq4nl", [1]), "iq4nlt"],
+    "4_w4a16_llama3_70b": ["w4a16_70b_engine"],
+    "5_iq4nl_qwen2_7b": ["iq4nl_engine"],
 }
 
 
@@ -857,7 +973,7 @@ def run_configs(torch, lib) -> dict:
                     if only_batches is not None and N not in only_batches:
                         continue
                     r = _suite_case(torch, lib, fmt, rows, K, N, 0x5EED0000 + 16 * ci + si)
-                    rows_out.append([fmt, f"{K}x{rows}", N, r["us"], r["pct_peak"]])
+                    rows_out.append([r["format"], f"{K}x{rows}", N, r["us"], r["pct_peak"]])
                     torch.cuda.empty_cache()
         out[cfg] = rows_out
         log(f"bench: config {cfg}: " + ", ".join(f"{f} {s} b{n} {us:.2f}us {p:.1f}%" for f, s, n, us, p in rows_out))

@@ -447,6 +447,25 @@ int zt_ternary_gemv_f32(const void* W_ternary, const float* x, float* y, int M, 
  * result equals TernaryGEMV(W, float(q)) * (w_scale * x_scale) bit for bit. */
 int zt_ternary_gemv_i8(const void* W_ternary, const int8_t* x_q, const float* x_scale, const float* w_scale,
                        float* y, int M, int K, zt_stream_t stream);
+/* Grouped BitNet GEMV: up to ZT_GROUP_MAX ternary matrices that read the
+ * same int8 activations x_q[K] and x_scale (a layer's q/k/v, or gate/up)
+ * in one launch (up to 3 matrices with K % 64 == 0 and K <= 65536 and
+ * 16-byte aligned rows, else one launch per matrix).  No reference
+ * counterpart (TernaryGEMV, compute/ternary_gemv.go:12, takes one matrix):
+ * matrix i gets zt_ternary_gemv_i8(W_i, x_q, x_scale, w_scale_i, y_i,
+ * rows_i, K) bit for bit (exact integer sums times the same scale product).
+ * `descs` is a host array read during the call; rows == 0 skips a matrix.
+ * n outside 1..ZT_GROUP_MAX, a bad descriptor or a misaligned x_q ->
+ * InvalidValue. */
+typedef struct zt_ternary_gemv_desc {
+    const void* W;         /* row-aligned 2-bit codes, rows x ceil(K/4) bytes */
+    const float* w_scale;  /* device pointer, one fp32 */
+    float* y;              /* rows fp32 outputs */
+    int rows;
+    int reserved;          /* 0 */
+} zt_ternary_gemv_desc;
+int zt_ternary_gemv_i8_group(const zt_ternary_gemv_desc* descs, int n, const int8_t* x_q, const float* x_scale, int K,
+                             zt_stream_t stream);
 /* Codes -> fp32 {-1,0,+1} (TernaryStorage.Get, tensor/ternary_storage.go:39-47). */
 int zt_dequant_ternary_f32(const void* W_ternary, float* out, int M, int K, zt_stream_t stream);
 /* Host: flat TernaryStorage.RawBytes (tensor/ternary_storage.go:91-92) ->
@@ -538,6 +557,16 @@ int zt_gemm_int4_f32(const void* A, const float* B, float* C, const float* scale
 int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, const float* scales, const void* zeros, int batch,
                           int in_features, int out_features, int group_size, zt_stream_t stream);
 int zt_gemm_int8_f32(const void* A, const float* B, float* C, int M, int K, int N, zt_stream_t stream);
+
+/* ---- measurement ------------------------------------------------------- */
+
+/* No counterpart in the reference: a plain streaming read of nbytes at p
+ * (16-byte aligned; a trailing partial 16 bytes is not read), 16 bytes a lane
+ * with nontemporal loads, no arithmetic.  Its time is the ceiling a GEMV
+ * over the same bytes is compared with (the benchmark's `ceiling`).  sink
+ * (4 bytes of device memory) is written only if the data xor-reduces to a
+ * fixed key, which keeps the loads live. */
+int zt_bench_stream_read(const void* p, long nbytes, void* sink, zt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_w4a16_pack_szr": (I, [P, P, I, I, I, P, P]),
     "zt_gemv_w4a16sz_f32": (I, [P, P, P, P, I, I, I, P]),
     "zt_gemm_w4a16sz_f32": (I, [P, P, P, P, I, I, I, I, P]),
+    "zt_bench_stream_read": (I, [P, L, P, P]),
+    "zt_ternary_gemv_i8_group": (I, [P, I, P, P, I, P]),
     "zt_w4a16_tiled_bytes": (L, [I, I]),
     "zt_w4a16_sz_bytes": (L, [I, I, I]),
     "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),
@@ -146,6 +148,21 @@ def q4_gemv_descs(entries) -> C.Array:
     arr = (Q4GemvDesc * max(1, len(entries)))()
     for i, (a, off, y, rows) in enumerate(entries):
         arr[i].A, arr[i].data_offset, arr[i].y, arr[i].rows, arr[i].reserved = a, off, y, rows, 0
+    return arr
+
+
+class TernaryGemvDesc(C.Structure):
+    """zt_ternary_gemv_desc: one matrix of a grouped BitNet GEMV."""
+
+    _fields_ = [("W", C.c_void_p), ("w_scale", C.c_void_p), ("y", C.c_void_p), ("rows", C.c_int),
+                ("reserved", C.c_int)]
+
+
+def ternary_gemv_descs(entries) -> C.Array:
+    """A host array of zt_ternary_gemv_desc from (W, w_scale, y, rows) tuples."""
+    arr = (TernaryGemvDesc * max(1, len(entries)))()
+    for i, (w, ws, y, rows) in enumerate(entries):
+        arr[i].W, arr[i].w_scale, arr[i].y, arr[i].rows, arr[i].reserved = w, ws, y, rows, 0
     return arr
 
 

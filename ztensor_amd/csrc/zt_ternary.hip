@@ -156,14 +156,11 @@ __global__ void __launch_bounds__(512) ternary_i8_kernel(const uint8_t* __restri
 // loop kernel above waited for its scale loads (and the workgroup size)
 // before its first weight load: a full memory round trip per wave.
 template <int R>
-__global__ void __launch_bounds__(1024) ternary_i8_steps_kernel(const uint8_t* __restrict__ W,
-                                                                const int8_t* __restrict__ xq,
-                                                                const float* __restrict__ x_scale,
-                                                                const float* __restrict__ w_scale,
-                                                                float* __restrict__ y, int rows, int bpr, int nw) {
-    __shared__ float red[16 * R];
+__device__ __forceinline__ void ternary_i8_steps_body(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ x_scale,
+                                                      const float* __restrict__ w_scale, float* __restrict__ y,
+                                                      int rows, int bpr, int nw, int row0, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = blockIdx.x * R;
     const int c = wave * 64 + lane;  // 16-byte chunk of the row
     const uint32_t voff = c * 16 < bpr ? (uint32_t)c * 16u : 0x80000000u;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, 0x00020000);
@@ -232,6 +229,40 @@ __global__ void __launch_bounds__(1024) ternary_i8_steps_kernel(const uint8_t* _
         const int r = row0 + threadIdx.x;
         if (r < rows) y[r] = sm * scale;
     }
+}
+
+template <int R>
+__global__ void __launch_bounds__(1024) ternary_i8_steps_kernel(const uint8_t* __restrict__ W,
+                                                                const int8_t* __restrict__ xq,
+                                                                const float* __restrict__ x_scale,
+                                                                const float* __restrict__ w_scale,
+                                                                float* __restrict__ y, int rows, int bpr, int nw) {
+    __shared__ float red[16 * R];
+    ternary_i8_steps_body<R>(W, xq, x_scale, w_scale, y, rows, bpr, nw, blockIdx.x * R, red);
+}
+
+// Up to three ternary matrices that read the same int8 activation vector
+// (a BitNet layer's q/k/v, or gate/up) in one launch: workgroups are
+// numbered through the matrices in turn, and each finds its matrix from the
+// row counts.  The activations, the three weight bases, the row counts and
+// the row length come first in the arguments, inside the dwords gfx950
+// preloads into SGPRs, so no wave waits on an argument load before its
+// first weight load; scales and outputs follow.
+template <int R>
+__global__ void __launch_bounds__(1024) ternary_i8_group3_kernel(const int8_t* __restrict__ xq, const uint8_t* w0,
+                                                                 const uint8_t* w1, const uint8_t* w2, int rows0,
+                                                                 int rows1, int rows2, int bpr, int nw, int n,
+                                                                 const float* __restrict__ x_scale,
+                                                                 const float* ws0, const float* ws1,
+                                                                 const float* ws2, float* y0, float* y1, float* y2) {
+    __shared__ float red[16 * R];
+    const int b = blockIdx.x;
+    const int g1 = (rows0 + R - 1) / R, g2 = g1 + (rows1 + R - 1) / R;
+    const int m = (b >= g1 ? 1 : 0) + (n > 2 && b >= g2 ? 1 : 0);
+    const uint8_t* W = m == 0 ? w0 : m == 1 ? w1 : w2;
+    const int rows = m == 0 ? rows0 : m == 1 ? rows1 : rows2;
+    ternary_i8_steps_body<R>(W, xq, x_scale, m == 0 ? ws0 : m == 1 ? ws1 : ws2, m == 0 ? y0 : m == 1 ? y1 : y2, rows,
+                             bpr, nw, (b - (m == 0 ? 0 : m == 1 ? g1 : g2)) * R, red);
 }
 
 // ----------------------------------------------------------- fp32 x
@@ -475,6 +506,60 @@ ZT_EXPORT int zt_ternary_gemv_f32(const void* W_ternary, const float* x, float* 
 ZT_EXPORT int zt_ternary_gemv_i8(const void* W_ternary, const int8_t* x_q, const float* x_scale,
                                  const float* w_scale, float* y, int M, int K, hipStream_t stream) {
     return ternary_gemv(true, W_ternary, x_q, x_scale, w_scale, y, M, K, stream);
+}
+
+ZT_EXPORT int zt_ternary_gemv_i8_group(const zt_ternary_gemv_desc* descs, int n, const int8_t* x_q,
+                                       const float* x_scale, int K, hipStream_t stream) {
+    if (descs == nullptr || n < 1 || n > ZT_GROUP_MAX || K < 0 || x_scale == nullptr ||
+        (K > 0 && (x_q == nullptr || ((uintptr_t)x_q & 15))))
+        return (int)hipErrorInvalidValue;
+    const int bpr = (K + 3) / 4;
+    long total = 0;
+    for (int i = 0; i < n; i++) {
+        const zt_ternary_gemv_desc& d = descs[i];
+        if (d.rows < 0 || d.reserved != 0) return (int)hipErrorInvalidValue;
+        if (d.rows > 0 && (d.W == nullptr || d.w_scale == nullptr || d.y == nullptr)) return (int)hipErrorInvalidValue;
+        total += d.rows;
+    }
+    if (total == 0) return (int)hipSuccess;
+    bool fused = n <= 3 && K > 0 && K % 64 == 0 && K <= 65536;
+    for (int i = 0; i < n; i++)
+        fused = fused && descs[i].rows > 0 && ((uintptr_t)descs[i].W & 15) == 0 && (long)descs[i].rows * bpr < 0x7fffffffL;
+    if (!fused) {
+        // shapes or counts outside the grouped kernel: one launch per matrix
+        for (int i = 0; i < n; i++) {
+            const zt_ternary_gemv_desc& d = descs[i];
+            const int rc = d.rows == 0 ? 0 : ternary_gemv(true, d.W, x_q, x_scale, d.w_scale, d.y, d.rows, K, stream);
+            if (rc != 0) return rc;
+        }
+        return (int)hipSuccess;
+    }
+    // the single-matrix configuration, rows per wave from the group's total rows
+    const int nw = (K + 4095) / 4096;
+    int R = 4;
+    while (R > 1 && (long)ceil_div(total, R) * nw < 512) R >>= 1;
+    const uint8_t* w[3] = {nullptr, nullptr, nullptr};
+    const float* ws[3] = {nullptr, nullptr, nullptr};
+    float* y[3] = {nullptr, nullptr, nullptr};
+    int rw[3] = {0, 0, 0}, wgs = 0;
+    for (int i = 0; i < n; i++) {
+        w[i] = static_cast<const uint8_t*>(descs[i].W);
+        ws[i] = descs[i].w_scale;
+        y[i] = descs[i].y;
+        rw[i] = descs[i].rows;
+        wgs += ceil_div(rw[i], R);
+    }
+#define ZT_TG3(RR)                                                                                                  \
+    ternary_i8_group3_kernel<RR><<<wgs, nw * kWave, 0, stream>>>(x_q, w[0], w[1], w[2], rw[0], rw[1], rw[2], bpr,  \
+                                                                 nw, n, x_scale, ws[0], ws[1], ws[2], y[0], y[1],   \
+                                                                 y[2])
+    switch (R) {
+        case 4: ZT_TG3(4); break;
+        case 2: ZT_TG3(2); break;
+        default: ZT_TG3(1); break;
+    }
+#undef ZT_TG3
+    return (int)hipGetLastError();
 }
 
 ZT_EXPORT int zt_dequant_ternary_f32(const void* W_ternary, float* out, int M, int K, hipStream_t stream) {

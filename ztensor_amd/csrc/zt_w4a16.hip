@@ -535,19 +535,20 @@ static void launch_w4a16_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, cons
     } else {
         ZT_RB(1, 1) ZT_RB(1, 2)
     }
-    if constexpr (NB == 1) { ZT_RB(8, 1) }
 #undef ZT_RB
 }
 
 // Launch shape of the row-block GEMM: S steps a wave and up to 16 waves
 // splitting K (8 for N >= 12, whose activation blocks take 12-16 KB of LDS a
-// wave), and R row sets a workgroup chosen so that the grid holds about 512
-// workgroups, within 128 VGPRs (N >= 12: one row set).
+// wave), and R row sets a workgroup (up to 4) chosen so that the grid holds
+// about 512 workgroups, within 128 VGPRs (N >= 12: one row set).
 static void w4a16_rb_shape(int M, int N, int nchunk, int& R, int& S, int& nw) {
     const int steps = ceil_div(nchunk, 16), wmax = N >= 12 ? 8 : 16;
     S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
     nw = ceil_div(steps, S);
-    const int rmax = N >= 12 ? 1 : min(8 / S, 32 / N);
+    // (8 row sets measured slower than 4 wherever the grid allows both: 10.35 / 10.1 us at 8192 x 8192,
+    // 32.1 / 28.3 us at 28672 x 8192, batch 4)
+    const int rmax = N >= 12 ? 1 : min(min(8 / S, 32 / N), 4);
     R = 1;
     while (R < rmax && ceil_div(M, 8 * R) >= 512) R *= 2;
 }

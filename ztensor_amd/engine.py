@@ -166,6 +166,16 @@ class ROCmEngine:
     def ternary_gemv_i8(self, w: int, xq: int, x_scale: int, w_scale: int, y: int, m: int, k: int) -> None:
         self.lib.call("zt_ternary_gemv_i8", w, xq, x_scale, w_scale, y, m, k, self._s)
 
+    def ternary_gemv_i8_group(self, mats: list[tuple[int, int, int, int]], xq: int, x_scale: int, k: int) -> None:
+        """Ternary GEMVs over one int8 activation vector (a BitNet layer's
+        q/k/v, or gate/up), given as (W, w_scale, y, rows) device pointers:
+        one zt_ternary_gemv_i8_group launch per ZT_GROUP_MAX matrices, each
+        result the one zt_ternary_gemv_i8 gives (bit for bit)."""
+        for i0 in range(0, len(mats), _lib.GROUP_MAX):
+            part = mats[i0:i0 + _lib.GROUP_MAX]
+            self.lib.call("zt_ternary_gemv_i8_group", _lib.ternary_gemv_descs(part), len(part), xq, x_scale, k,
+                          self._s)
+
     # ------------------------------------------------------------ residency
 
     def _to_dev(self, host: np.ndarray) -> torch.Tensor:
