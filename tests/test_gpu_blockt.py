@@ -165,11 +165,14 @@ def test_blockt_llama3_shapes(lib, orc, fmt, rows, K, N):
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q8"])
-@pytest.mark.parametrize("case", ["huge", "tiny", "mixed_columns", "zero", "one_hot"])
+@pytest.mark.parametrize("case", ["huge", "tiny", "mixed_columns", "span_2e20", "zero", "one_hot"])
 def test_blockt_activation_ranges(lib, orc, fmt, case):
     """Activations outside fp16's range (|x| up to 1e7), far below its normal
-    range (1e-7), columns 1e4 apart in scale, all zero, and a single
-    nonzero activation (the result is one weight column times x)."""
+    range (1e-7), columns 1e4 apart in scale, magnitudes spread over 2^-20 ..
+    2^20 inside every workgroup's K range (the power-of-two scaling follows
+    the largest; each hi + lo pair holds an activation to 2^-22 relative down
+    to 2^-17 of that largest, and to 2^-25 / c absolute below), all zero, and
+    a single nonzero activation (the result is one weight column times x)."""
     rows, K, N = 96, 1024, 8
     w = weights(fmt, rows, K, 83)
     x = synth.x_f32(K * N, 83).reshape(K, N)
@@ -179,6 +182,9 @@ def test_blockt_activation_ranges(lib, orc, fmt, case):
         x = x * np.float32(1e-7)
     elif case == "mixed_columns":
         x = x * np.float32(1e4) ** (np.arange(N) % 2).astype(np.float32)
+    elif case == "span_2e20":
+        e = np.random.default_rng(84).uniform(-20.0, 20.0, x.shape)
+        x = (x * np.exp2(e)).astype(np.float32)
     elif case == "zero":
         x = np.zeros_like(x)
     else:
@@ -196,7 +202,7 @@ def test_blockt_activation_ranges(lib, orc, fmt, case):
     elif case == "one_hot":
         # the reference rounds q * scale, then x * that (gemm_quant.go:199-201): one ulp apart at most
         assert rel_err(y, ref) <= 2.0 ** -22
-    elif case == "mixed_columns":
+    elif case in ("mixed_columns", "span_2e20"):
         for n in range(N):  # each column on its own scale
             assert rel_err(y[:, n], ref[:, n]) <= TOL, n
     else:
@@ -762,3 +768,38 @@ def test_tiled_gemms_repeat_bit_for_bit(lib, fmt):
         run = lambda: run_q5t(lib, bufs, x, rows, K, N)
     a, b = run(), run()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8", "q5_0", "q4_k", "q5_k", "q6_k"])
+def test_tiled_close_to_fp64_with_spread_activations(lib, orc, fmt):
+    """Activations whose magnitudes spread over 2^-20 .. 2^20 inside every
+    workgroup's K range: each column within 2e-6 of the exact (fp64) product
+    of the dequantized weights (measured 2-7e-7).  The weights enter the
+    MFMAs as normal-range fp16 (2^14 + 2^10 q and the like); as fp16
+    subnormals (q 2^-24) the 4- and 5-bit formats came out up to 1.5e-5 off
+    here."""
+    rows, K, N = 96, 1024, 8
+    x = synth.x_f32(K * N, 85).reshape(K, N)
+    x = np.ascontiguousarray((x * np.exp2(np.random.default_rng(85).uniform(-20.0, 20.0, x.shape))).astype(np.float32))
+    if fmt in ("q4", "q8"):
+        w = weights(fmt, rows, K, 85)
+        wt, st = tile_dev(lib, fmt, w.raw, rows, K)
+        y = run_t(lib, fmt, wt, st, x, rows, K, N)
+        deq = orc.q4_dequant(w.raw, rows * K) if fmt == "q4" else orc.q8_dequant(w.raw, rows * K)
+    elif fmt == "q5_0":
+        w = synth.kquant("q5_0", rows, K, 85)
+        y = run_q5t(lib, q5_tile_dev(lib, w.raw, rows, K), x, rows, K, N)
+        deq = orc.q5_0_dequant(w.raw, rows * K)
+    else:
+        w = synth.kquant(fmt, rows, K, 85)
+        if fmt == "q4_k":
+            wt, ht = q4k_tile_dev(lib, w.raw, rows, K)
+            y = run_q4kt(lib, wt, ht, x, rows, K, N)
+        elif fmt == "q5_k":
+            y = run_q5kt(lib, q5k_tile_dev(lib, w.raw, rows, K), x, rows, K, N)
+        else:
+            y = run_q6kt(lib, q6k_tile_dev(lib, w.raw, rows, K), x, rows, K, N)
+        deq = orc.kq_dequant(fmt, w.raw, rows * K)
+    exact = deq.astype(np.float64).reshape(rows, K) @ x.astype(np.float64)
+    for n in range(N):
+        assert rel_err(y[:, n], exact[:, n]) <= 2e-6, n

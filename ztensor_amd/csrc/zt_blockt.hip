@@ -7,13 +7,19 @@
 // and with the per-row CUDA kernels gemm_q4_f32 / gemm_q8_f32
 // (internal/cuda/kernels/gemm_q4.cu:117-201, gemm_q8.cu:121-182).  Here the
 // batched product runs on v_mfma_f32_16x16x32_f16 instead:
-//  * Weights are exact small integers in fp16: a Q4_0 nibble q or a Q8_0
-//    byte q + 128 becomes the fp16 subnormal q * 2^-24 with masks (Q4_0) or
-//    byte permutes (Q8_0), and the products are exact in fp32.  The offset
-//    (8 for Q4_0, 128 for Q8_0) is one more MFMA a step, with every A element
-//    -off * 2^-24 (an fp16 subnormal), whose result is the C input of the
-//    weight MFMAs of both tiles: each step's D is 2^-24 sum((q - off) x), and
-//    one v_fma_mix per output takes the block's fp16 scale straight from LDS.
+//  * Weights are exact fp16 values of the normal range: a 4-bit value q
+//    (Q4_0, Q4_K) becomes 2^14 + 2^10 q (the nibble moved to mantissa bits
+//    6-9 under the exponent of 2^14: a shift and an and-or), a 5-bit value
+//    (Q5_0, Q5_K) 2^15 + 2^10 q, a Q6_K value 2^15 + 2^9 q and a Q8_0 byte
+//    2^15 + 2^7 (q + 128) (byte permutes and a shift-or).  Products with the
+//    normalised activations are exact in fp32.  (These once entered as fp16
+//    subnormals, q 2^-24; with activations spread in magnitude the gfx950
+//    MFMAs sum such small products up to 1.5e-5 off, measured against fp64
+//    products.)  The offset and the base are one more MFMA a step, every A
+//    element -(base + off 2^10) (Q6_K 2^9, Q8_0 2^7), whose result is the C
+//    input of the weight MFMAs of both tiles: each step's D is
+//    2^10 sum((q - off) x), and one v_fma_mix per output takes the block's
+//    fp16 scale straight from LDS.
 //  * fp32 activations are split into two fp16 parts, x = hi + lo, after a
 //    power-of-two normalisation per workgroup (max |x| of the workgroup's K
 //    range maps into [2^14, 2^15)), so each activation is carried to about
@@ -47,8 +53,8 @@
 //    Q4_0 block in the Q4_0 data layout; the 16-byte super-block headers
 //    [tile][super-block][16 rows][16 B] (stl), decoded per workgroup into
 //    (d * scale, dmin * min) pairs; Q5_K adds Q5_0's fifth-bit dwords (aux).
-//    Each sub-block's min term uses an MFMA with all-positive A, which gives
-//    2^-24 sum(x) per step.
+//    Each sub-block's min term uses the base MFMA (A all -2^14, Q5_K -2^15),
+//    -2^14 sum(x) per step, which is also the C input of its weight MFMAs.
 //  * Q6_K (zt_q6k_tile): the values 0..63 as bytes in the Q8_0 tile
 //    positions, ordered so that lane group g holds values 4g .. 4g+3 of each
 //    of a block's two 16-value groups; fp32 d * sc per group [16 rows]
@@ -362,9 +368,7 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
         const int p = tid + i * W * 64;
         if (p < npieces) {
             const int r = p / PPR, c4 = (p % PPR) * 4;
-            // Q4_0: the activations of high-nibble elements (16..31 of a block)
-            // are staged at 1/16, as their A halves are q * 2^-20
-            const float cr = (F != BlkFmt::Q8_0 && F != BlkFmt::Q6_K && (r & 16)) ? cs * 0.0625f : cs;
+            const float cr = cs;
             const int base = mfma_xrow(blkt_lds_row<F>(r), 16);
             uint32_t hv[2], lv[2];
 #pragma unroll
@@ -424,21 +428,20 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
     // 4 qq + 3; mfma_xrow of that row is this lane base plus (136u + 8s) * 32.
     const int jq = li >> 2, qq = li & 3;
     const int lbase = (34 * lg + jq) * 32 + 8 * qq;
-    // -off * 2^-24 in every A element (fp16 subnormal bits 0x8008 / 0x8080):
-    // one MFMA a step gives -off * 2^-24 * sum(x), the C input of both
-    // tiles' weight MFMAs, so each step's D is 2^-24 * sum((q - off) x)
-    // (Q4_0: -8 * 2^-20 in the halves of high-nibble elements, whose
-    // activations are staged at 1/16)
-    // Q4_K: +2^-24 (+2^-20 in high-nibble halves), so the MFMA gives
-    // 2^-24 * sum(x) of each sub-block, for its min term.
-    // (Q5_0: offset 16, -16 * 2^-24 and -16 * 2^-20)
-    // (Q6_K: -32 * 2^-24 in every half)
+    // -(base + off 2^10) in every A element: one MFMA a step gives that times
+    // sum(x), the C input of both tiles' weight MFMAs, so each step's D is
+    // 2^10 sum((q - off) x) (Q6_K: 2^9, Q8_0: 2^7).
+    // Q4_0: -(2^14 + 8 2^10) = -24576; Q5_0: -(2^15 + 16 2^10) = -49152;
+    // Q4_K: -2^14 and Q5_K: -2^15 (no offset; the MFMA's result is also the
+    // sub-block's min term); Q6_K: -(2^15 + 32 2^9); Q8_0: -(2^15 + 128 2^7).
     const _Float16 ol = __builtin_bit_cast(
-        _Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0x8008u : QK ? 0x0001u : F == BlkFmt::Q5_0 ? 0x8010u
-                             : Q6 ? 0x8020u : 0x8080u));
-    const _Float16 oh = __builtin_bit_cast(_Float16, (uint16_t)(QK ? 0x0010u : F == BlkFmt::Q5_0 ? 0x8100u : 0x8080u));
-    const half8v aoff = (F != BlkFmt::Q8_0 && !Q6) ? (half8v){ol, ol, oh, oh, ol, ol, oh, oh}
-                                                    : (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
+        _Float16, (uint16_t)(F == BlkFmt::Q4_0 ? 0xF600u : F == BlkFmt::Q4_K ? 0xF400u : F == BlkFmt::Q5_K ? 0xF800u
+                             : 0xFA00u));
+    const half8v aoff = (half8v){ol, ol, ol, ol, ol, ol, ol, ol};
+    // nibble (or 5-bit value) to mantissa: mask in a VGPR, exponent in an SGPR (v_and_or_b32)
+    uint32_t nmask = Q5 ? 0x01E001E0u : 0x03C003C0u,
+             nexp = (Q5 || Q6 || F == BlkFmt::Q8_0) ? 0x78007800u : 0x74007400u;
+    asm volatile("" : "+v"(nmask), "+s"(nexp));
     float4v acc[2];
     acc[0] = acc[1] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -487,11 +490,13 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                     for (int t = 0; t < 2; t++) {
                         const uint4 q = w[u][t][s >> 1];
                         const uint32_t da = (s & 1) ? q.z : q.x, db = (s & 1) ? q.w : q.y;
+                        // values 0..63 to 2^15 + 2^9 q: byte permute, then v_lshl_or_b32
+                        auto q6h = [&](uint32_t v) { return (v << 4) | nexp; };
                         const half4v aq[2] = {
-                            __builtin_bit_cast(half4v, (uint2){__builtin_amdgcn_perm(da, da, 0x0C010C00u),
-                                                               __builtin_amdgcn_perm(da, da, 0x0C030C02u)}),
-                            __builtin_bit_cast(half4v, (uint2){__builtin_amdgcn_perm(db, db, 0x0C010C00u),
-                                                               __builtin_amdgcn_perm(db, db, 0x0C030C02u)})};
+                            __builtin_bit_cast(half4v, (uint2){q6h(__builtin_amdgcn_perm(da, da, 0x0C010C00u)),
+                                                               q6h(__builtin_amdgcn_perm(da, da, 0x0C030C02u))}),
+                            __builtin_bit_cast(half4v, (uint2){q6h(__builtin_amdgcn_perm(db, db, 0x0C010C00u)),
+                                                               q6h(__builtin_amdgcn_perm(db, db, 0x0C030C02u))})};
                         float4v d[2];
 #pragma unroll
                         for (int hq = 0; hq < 2; hq++) {
@@ -516,34 +521,47 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
                     if constexpr (F != BlkFmt::Q8_0) {
                         const uint4 q = w[u][t][0];
                         const uint32_t dw = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-                        const uint32_t d8 = dw >> 8;  // halves: q 2^-24 (low nibbles), q 2^-20 (high)
-                        av = (u32x4){dw & 0x000F000Fu, dw & 0x00F000F0u, d8 & 0x000F000Fu, d8 & 0x00F000F0u};
+                        // nibbles at bits 0-3, 4-7, 8-11, 12-15 of each half to mantissa bits 6-9
+                        // (Q5: 5-8, the fifth bit then at 9)
+                        if constexpr (Q5)
+                            av = (u32x4){((dw << 5) & nmask) | nexp, ((dw << 1) & nmask) | nexp,
+                                         ((dw >> 3) & nmask) | nexp, ((dw >> 7) & nmask) | nexp};
+                        else
+                            av = (u32x4){((dw << 6) & nmask) | nexp, ((dw << 2) & nmask) | nexp,
+                                         ((dw >> 2) & nmask) | nexp, ((dw >> 6) & nmask) | nexp};
                         if constexpr (Q5) {
-                            // fifth bits: 16 more in each half, bit 4 (low halves) or bit 8 (high);
-                            // y = byte | byte << 15 puts byte bits k and k+1 16 bits apart
+                            // fifth bits to bit 9 of each half (2^10 16 more); y = byte | byte << 15
+                            // puts byte bits k and k+1 16 bits apart
                             const uint32_t xb = (qhw[u][t] >> (8 * s)) & 0xFFu, yb = xb | (xb << 15);
-                            av[0] |= (yb << 4) & 0x00100010u;
-                            av[1] |= (yb << 6) & 0x01000100u;
-                            av[2] |= yb & 0x00100010u;
-                            av[3] |= (yb << 2) & 0x01000100u;
+                            av[0] |= (yb << 9) & 0x02000200u;
+                            av[1] |= (yb << 7) & 0x02000200u;
+                            av[2] |= (yb << 5) & 0x02000200u;
+                            av[3] |= (yb << 3) & 0x02000200u;
                         }
                     } else {
                         const uint4 q = w[u][t][s >> 1];
                         const uint32_t da = ((s & 1) ? q.z : q.x) ^ 0x80808080u;
                         const uint32_t db = ((s & 1) ? q.w : q.y) ^ 0x80808080u;
-                        av = (u32x4){__builtin_amdgcn_perm(da, da, 0x0C010C00u), __builtin_amdgcn_perm(da, da, 0x0C030C02u),
-                                     __builtin_amdgcn_perm(db, db, 0x0C010C00u), __builtin_amdgcn_perm(db, db, 0x0C030C02u)};
+                        // bytes q + 128 to 2^15 + 2^7 (q + 128): byte permute, then v_lshl_or_b32
+                        auto q8h = [&](uint32_t v) { return (v << 2) | nexp; };
+                        av = (u32x4){q8h(__builtin_amdgcn_perm(da, da, 0x0C010C00u)),
+                                     q8h(__builtin_amdgcn_perm(da, da, 0x0C030C02u)),
+                                     q8h(__builtin_amdgcn_perm(db, db, 0x0C010C00u)),
+                                     q8h(__builtin_amdgcn_perm(db, db, 0x0C030C02u))};
                     }
-                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[0],
-                                                                      QK ? (float4v){0.f, 0.f, 0.f, 0.f} : dn, 0, 0, 0);
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[0], dn,
+                                                                      0, 0, 0);
                     if constexpr (NPL == 2)
                         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, av), bv[1], d, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         if constexpr (QK) {
+                            // D = 2^10 sum(q x) and dn = -2^14 sum(x) (Q5_K: -2^15):
+                            // 2^10 (d sc sum(q x) - dmin mn sum(x)) = sv D + (mv 2^-4) dn
                             const SV& pr = sc[t][i][s >> 1];
                             const float sv = (s & 1) ? pr.z : pr.x, mv = (s & 1) ? pr.w : pr.y;
-                            acc[t][i] = fmaf(sv, d[i], fmaf(-mv, dn[i], acc[t][i]));
+                            acc[t][i] = fmaf(sv, d[i], fmaf(mv * (F == BlkFmt::Q5_K ? 0.03125f : 0.0625f), dn[i],
+                                                            acc[t][i]));
                         } else {
                             float sv;
                             if constexpr (F == BlkFmt::Q4_0 || F == BlkFmt::Q5_0) {  // fp16 scales
@@ -559,15 +577,16 @@ __global__ void __launch_bounds__(256) blkt_mfma_kernel(const uint4* __restrict_
             }
         }
     }
-    // y = 2^24 * acc / c: the 2^-24 of the weight encoding and the
-    // activation normalisation undone in one exact power-of-two scaling
+    // y = acc / (2^10 c) (Q6_K: 2^9 c; Q8_0: 2^7 c): the weight encoding's
+    // factor and the activation normalisation undone in one exact
+    // power-of-two scaling
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float v = acc[t][i];
             if constexpr (NPL == 1) v += __shfl_xor(v, 8);  // hi columns n + lo columns 8 + n
-            acc[t][i] = ldexpf(v, 24 - sh);
+            acc[t][i] = ldexpf(v, (F == BlkFmt::Q8_0 ? -7 : Q6 ? -9 : -10) - sh);
         }
     if (gy > 1) {
 #pragma unroll
