@@ -325,6 +325,124 @@ __global__ void __launch_bounds__(1024) gemv_q4_steps_kernel(const uint16_t* __r
     q4_steps_body<S, R>(scales, data, x, y, rows, kb, blockIdx.x * R, red);
 }
 
+// NC fp32 activation columns of a batch at once (C[M, N] = A B, B[K, N]
+// row-major), on the fixed-step form above: every weight dword and scale is
+// loaded once for all NC columns, and each lane keeps R x NC sums.  The lane
+// reads, for each of its 8 K positions (4q .. 4q+3 and 16+4q .. 16+4q+3 of
+// its block), the NC consecutive floats of columns n0 .. n0+NC-1 of that B
+// row (row stride ldx floats): one 16-byte load per 4 columns, or one 8-byte
+// load for NC = 2.  Products are formed exactly as at batch 1 (fp16
+// subnormal nibbles against activations pre-scaled by 2^24 / 2^20, a chain
+// started at -8 sum(x) per column), so each column's sums are those of the
+// batch-1 kernel.  The R x NC values are summed across the wave by the
+// halving exchanges, across the waves through LDS in wave order, and stored
+// once: no atomics, the same bits every call.
+template <int NC>
+__device__ __forceinline__ void q4n_load_row(__amdgpu_buffer_rsrc_t rx, uint32_t off, float (&v)[NC]) {
+    if constexpr (NC == 2) {
+        const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rx, off, 0, 0));
+        v[0] = __uint_as_float(d.x);
+        v[1] = __uint_as_float(d.y);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NC / 4; c++) {
+            const u32x4 d = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16u * c, 0, 0);
+            v[4 * c] = __uint_as_float(d.x);
+            v[4 * c + 1] = __uint_as_float(d.y);
+            v[4 * c + 2] = __uint_as_float(d.z);
+            v[4 * c + 3] = __uint_as_float(d.w);
+        }
+    }
+}
+
+template <int S, int R, int NC>
+__global__ void __launch_bounds__(1024) gemv_q4n_steps_kernel(const uint16_t* __restrict__ scales,
+                                                              const uint32_t* __restrict__ data,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int rows, int kb, int ldx, int n0) {
+    constexpr int V = R * NC;
+    __shared__ float red[16 * V];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128 * ldx, 0x00020000);
+    uint32_t w[S][R], s[S][R];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+        const uint32_t voff = ok ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+        const uint32_t soff = ok ? (uint32_t)(b * 2) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, row * (uint32_t)kb * 16u, 2);  // nontemporal
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            s[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, row * (uint32_t)kb * 2u, 0);
+        }
+    }
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const bool ok = b < kb;
+        // K rows 32b + 4q + i (low nibbles) and 32b + 16 + 4q + i (high nibbles)
+        float xl[4][NC], xh[4][NC];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t kl = (uint32_t)(32 * b + 4 * q + i);
+            q4n_load_row<NC>(rx, ok ? (kl * (uint32_t)ldx + (uint32_t)n0) * 4u : 0x80000000u, xl[i]);
+            q4n_load_row<NC>(rx, ok ? ((kl + 16u) * (uint32_t)ldx + (uint32_t)n0) * 4u : 0x80000000u, xh[i]);
+        }
+        float c0[NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            c0[n] = -8.0f * (((xl[0][n] + xl[1][n]) + (xl[2][n] + xl[3][n])) +
+                             ((xh[0][n] + xh[1][n]) + (xh[2][n] + xh[3][n])));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xl[i][n] *= 16777216.0f;
+                xh[i][n] *= 1048576.0f;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t d = w[t][r], d8 = d >> 8;
+            const half2v m0 = as_half2(d & 0x000F000Fu), m1 = as_half2(d & 0x00F000F0u);
+            const half2v m2 = as_half2(d8 & 0x000F000Fu), m3 = as_half2(d8 & 0x00F000F0u);
+            const float sc = (float)as_half2(s[t][r]).x;
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                float v = __builtin_fmaf((float)m0.x, xl[0][n], c0[n]);
+                v = __builtin_fmaf((float)m1.x, xh[0][n], v);
+                v = __builtin_fmaf((float)m2.x, xl[1][n], v);
+                v = __builtin_fmaf((float)m3.x, xh[1][n], v);
+                v = __builtin_fmaf((float)m0.y, xl[2][n], v);
+                v = __builtin_fmaf((float)m1.y, xh[2][n], v);
+                v = __builtin_fmaf((float)m2.y, xl[3][n], v);
+                v = __builtin_fmaf((float)m3.y, xh[3][n], v);
+                acc[r * NC + n] = __builtin_fmaf(sc, v, acc[r * NC + n]);
+            }
+        }
+    }
+    wave_reduce_rows<V>(acc);
+    if (is_row_writer<V>(lane)) red[wave * V + row_of_lane<V>(lane)] = acc[0];
+    __syncthreads();
+    if ((int)threadIdx.x < V) {
+        float sum = 0.0f;
+        for (int wv = 0; wv < nwaves; wv++) sum += red[wv * V + threadIdx.x];
+        const int r = row0 + (int)threadIdx.x / NC;
+        if (r < rows) y[(long)r * ldx + n0 + (int)threadIdx.x % NC] = sum;
+    }
+}
+
 // Several Q4_0 matrices that read the same activation vector (q/k/v, or
 // gate/up, of a decode layer) in one launch.  Workgroups [wg0[i], wg0[i+1])
 // run matrix i with the fixed-step body above; the matrices keep their own
@@ -815,6 +933,242 @@ static int launch_iq4nl_rb(const uint16_t* sc, const uint32_t* data, const uint1
     return (int)hipGetLastError();
 }
 
+// ------------------------------------------------------------ Q4_0 row-block GEMM (fp32 activations)
+//
+// Groups of 4 or 8 fp32 activation columns (columns n0 .. n0 + 4NB - 1 of
+// B[K, ldx]) on the separated upload layout, one launch per group: the
+// row-block structure of zt_rbmfma.h (v_mfma_f32_4x4x4_16b_f16, lane =
+// block of row j of a 4-row set, waves splitting K, activations staged per
+// wave and read back transposed).  fp32 activations cannot be MFMA operands
+// as they are, so each wave step
+//  * loads its 512 x 4NB activations into VGPRs (16-byte loads), takes the
+//    step's max |x| over the wave and a power of two c with c max|x| in
+//    [2^14, 2^15), and splits every c x into fp16 hi = fp16(c x) and
+//    lo = fp16(c x - hi): hi + lo equals c x to about 2^-22 relative, for
+//    any fp32 x, and c is undone exactly when the step's sums are taken;
+//  * writes hi and lo as 8NB fp16 columns (hi n-sets 0 .. NB-1, lo n-sets
+//    NB .. 2NB-1) in the Q4_0-order layout (RbQ4Layout).
+// B operand of MFMA step s (0-7) of a lane's block: the low (s even) or
+// high (s odd) nibbles of the four bytes of dword s/2, K order 4(s/2) +
+// 16(s%2) + {0, 2, 1, 3}, each as the fp16 2^14 + 2^10 q (normal range:
+// MFMA products of that size are exact and sum without the low bias of
+// subnormal operands).  Per block, n-set and step: D = sum (hi + lo) b
+// (hi and lo MFMAs into one chain) and X = sum (hi + lo) 2^14 (the same
+// with B = 2^14, shared by the row sets), so sum((q - 8) x) = 2^-10 (D -
+// 1.5 X) / c, and the block's fp16 scale d takes it: y += d 2^-10 (D/c -
+// 1.5 X/c).  Sums in wave and wave order (rb_finish): no atomics.
+template <int NB>
+__device__ __forceinline__ void q4rb_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr)[8 * NB], int step, int ldx, int n0,
+                                            int lane) {
+#pragma unroll
+    for (int i = 0; i < 8 * NB; i++) {
+        const int k = step * 512 + (NB == 1 ? 64 * i + lane : 32 * i + (lane >> 1));
+        const int col = n0 + (NB == 1 ? 0 : 4 * (lane & 1));
+        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(k * ldx + col) * 4u, 0, 0);
+    }
+}
+
+// B operand of MFMA step s from weight dword q: the low (hi_half = 0) or
+// high nibbles of bytes (0, 2) and (1, 3) moved to mantissa bits 6-9 under
+// the exponent of 2^14 (mask in a VGPR, exponent in an SGPR, as
+// rb_w4_operand).
+__device__ __forceinline__ half4v rb_q4_operand(uint32_t q, int hi_half, uint32_t mask, uint32_t expo) {
+    const uint32_t a = hi_half ? q << 2 : q << 6, b = hi_half ? q >> 6 : q >> 2;
+    return __builtin_bit_cast(half4v, (uint2){(a & mask) | expo, (b & mask) | expo});
+}
+
+template <int NB, int R, int S>
+__global__ void __launch_bounds__(1024) q4_rb_kernel(const uint16_t* __restrict__ scales,
+                                                     const uint32_t* __restrict__ data, const float* __restrict__ x,
+                                                     float* __restrict__ y, int rows, int kb, int ldx, int n0) {
+    using Lay = RbQ4Layout<2 * NB>;
+    constexpr int V = 4 * R * NB;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int blk = lane >> 2, j = lane & 3;
+    char* xs = smem + wave * Lay::STEP;
+    const int row0 = blockIdx.x * 4 * R;
+    // rows past M and K read zeros: the buffers end at row M and at K
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, rows * kb * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, rows * kb * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128 * ldx, 0x00020000);
+    const int step0 = wave * S;
+    u32x4 xr[8 * NB];
+    q4rb_load_x<NB>(rx, xr, step0, ldx, n0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 w[S][R];
+    uint32_t sc[S][R];
+    const uint32_t brow = (uint32_t)(row0 + j) * (uint32_t)kb, bstep = 4u * (uint32_t)kb;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (step0 + t) * 16 + blk;
+        const bool ok = c < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t b = brow + r * bstep + (uint32_t)c;
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? b * 16u : 0x80000000u, 0, 2);  // nontemporal
+            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? b * 2u : 0x80000000u, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+    const half4v ones = (half4v){16384, 16384, 16384, 16384};  // 2^14
+    uint32_t bmask = 0x03C003C0u, bexp = 0x74007400u;
+    asm volatile("" : "+v"(bmask), "+s"(bexp));  // the mask in a VGPR, the exponent in an SGPR
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        if (t > 0) {
+            q4rb_load_x<NB>(rx, xr, step0 + t, ldx, n0, lane);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            // the activations only: the 2 S R weight and scale loads after them may be outstanding
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S * R) : "memory");
+        }
+        // the step's normalisation c = 2^sh
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8 * NB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(__uint_as_float(xr[i][e])));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        int sh = 0;
+        if (m > 0.0f && m <= 3.402823466e38f) {
+            int e2;
+            (void)frexpf(m, &e2);  // m = f 2^e2, f in [0.5, 1)
+            sh = min(127, 15 - e2);
+        }
+        const float cs = ldexpf(1.0f, sh), ic = ldexpf(1.0f, -sh);
+        // the previous step's transposing reads precede these writes in the wave's
+        // LDS order; the scheduler must not move either across
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8 * NB; i++) {
+            uint32_t hv[2], lv[2];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float v0 = __uint_as_float(xr[i][e]) * cs, v1 = __uint_as_float(xr[i][e + 1]) * cs;
+                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+                const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+                hv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            if constexpr (NB == 1) {
+                // K row k: one 16-byte piece (hi columns, then lo columns)
+                const int k = 64 * i + lane, c = k >> 5, p = ((k & 31) + Lay::sig(c)) & 31;
+                *reinterpret_cast<uint4*>(xs + (c * 32 + p) * 16) = make_uint4(hv[0], hv[1], lv[0], lv[1]);
+            } else {
+                // K row k: pieces 2k (hi) and 2k + 1 (lo), this lane's 4 columns at byte 8 (lane & 1)
+                const int k = 32 * i + (lane >> 1), c = k >> 5, hf = 8 * (lane & 1);
+                const int ph = (2 * (k & 31) + Lay::sig(c)) & 63, pl = (2 * (k & 31) + 1 + Lay::sig(c)) & 63;
+                *reinterpret_cast<uint2*>(xs + (c * 64 + ph) * 16 + hf) = make_uint2(hv[0], hv[1]);
+                *reinterpret_cast<uint2*>(xs + (c * 64 + pl) * 16 + hf) = make_uint2(lv[0], lv[1]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float4v d[R][NB], dx[NB];
+#pragma unroll
+        for (int js = 0; js < NB; js++) {
+            dx[js] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < R; r++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            half4v xa[2 * NB];
+#pragma unroll
+            for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_q4_tr_offset<2 * NB>(lane, s, js));
+            half4v bv[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const u32x4& wv = w[t][r];
+                const uint32_t q = (s >> 1) == 0 ? wv.x : (s >> 1) == 1 ? wv.y : (s >> 1) == 2 ? wv.z : wv.w;
+                bv[r] = rb_q4_operand(q, s & 1, bmask, bexp);
+            }
+            // hi parts, then lo parts: consecutive MFMAs of one chain are R NB + NB apart
+#pragma unroll
+            for (int hl = 0; hl < 2; hl++) {
+#pragma unroll
+                for (int js = 0; js < NB; js++)
+                    dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], ones, dx[js], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int js = 0; js < NB; js++)
+                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], bv[r], d[r][js], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int js = 0; js < NB; js++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float xo = 1.5f * dx[js][v] * ic;  // 1.5 X / c (exact scalings)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    float& a = acc[(r * NB + js) * 4 + v];
+                    a = __builtin_fmaf(h2f((uint16_t)sc[t][r]) * 0x1p-10f, __builtin_fmaf(d[r][js][v], ic, -xo), a);
+                }
+            }
+    }
+    // waves split K: each wave leaves its sums in its own LDS region, then the
+    // workgroup adds them in wave order
+    rb_finish<NB, R>(acc, smem, Lay::STEP, xs, y, row0, rows, ldx, n0);
+}
+
+template <int NB, int R, int S>
+static void launch_q4_rb_t(dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data, const float* x,
+                           float* y, int rows, int kb, int ldx, int n0) {
+    const size_t lds = (size_t)nw * RbQ4Layout<2 * NB>::STEP;
+    if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
+        static const bool raised = [] {
+            return hipFuncSetAttribute(reinterpret_cast<const void*>(&q4_rb_kernel<NB, R, S>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        }();
+        (void)raised;
+    }
+    q4_rb_kernel<NB, R, S><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
+}
+
+template <int NB>
+static void launch_q4_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data,
+                           const float* x, float* y, int rows, int kb, int ldx, int n0) {
+#define ZT_RB(RR, SS) \
+    if (R == RR && S == SS) return launch_q4_rb_t<NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
+    ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
+    if constexpr (NB == 1) { ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(4, 2) ZT_RB(1, 4) ZT_RB(2, 4) }
+#undef ZT_RB
+}
+
+// Q4_0 row-block launches for the column groups of an fp32 batch: K split
+// into steps of 16 blocks over up to 16 waves, 1, 2 or 4 steps a wave, up
+// to 4 row sets a workgroup while about 200 workgroups remain.  8-column
+// groups (16 KB of hi/lo activations a wave) run one step a wave on up to
+// 8 waves (K <= 4096: with two steps a wave the kernel spills registers);
+// other columns go in groups of 4.
+static bool q4_rb_ok(int N, int kb, long M, const float* B) {
+    return N >= 4 && N % 4 == 0 && ((uintptr_t)B & 15) == 0 && kb <= 16 * 16 * 4 && M * kb * 16 < 0x7fffffffL &&
+           (long)(kb + 16) * 128 * N < 0x7fffffffL;
+}
+
+static void launch_q4_rb(const uint16_t* sc, const uint32_t* data, const float* B, float* C, int M, int kb, int N,
+                         hipStream_t st) {
+    for (int n0 = 0; n0 < N;) {
+        const int nc = (N - n0 >= 8 && kb <= 8 * 16) ? 8 : 4;
+        const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
+        const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
+        const int nw = ceil_div(steps, S);
+        const int rmax = S == 4 ? 2 : 4;
+        int R = 1;
+        while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
+        const dim3 g(ceil_div(M, 4 * R));
+        if (nc == 8) launch_q4_rb_n<2>(R, S, g, nw, st, sc, data, B, C, M, kb, N, n0);
+        else launch_q4_rb_n<1>(R, S, g, nw, st, sc, data, B, C, M, kb, N, n0);
+        n0 += nc;
+    }
+}
+
 static size_t iq4_mfma_lds_bytes(int N) {
     const size_t stage = (size_t)mfma_xbytes(N) + 16 + 16 * 4 + kMfmaUC * 4 * kMfmaRows * sizeof(uint16_t);
     return stage > mfma_reduce_bytes() ? stage : mfma_reduce_bytes();
@@ -873,6 +1227,51 @@ static void launch_gemv_r(int R, dim3 grid, dim3 block, hipStream_t st, const ui
         case 2: gemv_blk18_kernel<F, 2, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
         default: gemv_blk18_kernel<F, 1, XT, CONTIG><<<grid, block, 0, st>>>(sc, dt, x, y, stride, rows, kb); break;
     }
+}
+
+template <int S, int NC>
+static void launch_q4n_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc, const uint32_t* dt,
+                             const float* x, float* y, int rows, int kb, int ldx, int n0) {
+    switch (R) {
+        case 8:
+            if constexpr (NC <= 4) gemv_q4n_steps_kernel<S, 8, NC><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb, ldx, n0);
+            break;
+        case 4: gemv_q4n_steps_kernel<S, 4, NC><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb, ldx, n0); break;
+        case 2: gemv_q4n_steps_kernel<S, 2, NC><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb, ldx, n0); break;
+        default: gemv_q4n_steps_kernel<S, 1, NC><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb, ldx, n0); break;
+    }
+}
+
+// Q4_0 with N > 1 fp32 columns on gemv_q4n_steps_kernel: column groups of 8
+// (then 4) when B rows are 16-byte aligned, else groups of 2 when they are
+// 8-byte aligned; each group is one launch that reads the weights once.
+// Returns false (nothing launched) where the layout does not fit.
+static bool launch_q4n(const uint16_t* sc, const uint32_t* dt, const float* B, float* C, int M, int kb, int N,
+                       hipStream_t st) {
+    if (N < 2 || kb > 512 || (long)M * kb * 16 >= 0x7fffffffL || (long)kb * 128 * N >= 0x7fffffffL) return false;
+    const bool a16 = N % 4 == 0 && ((uintptr_t)B & 15) == 0;
+    const bool a8 = N % 2 == 0 && ((uintptr_t)B & 7) == 0;
+    if (!a16 && !a8) return false;
+    const int S = kb <= 128 ? 1 : 2;
+    int nw = ceil_div(kb, 16 * S);
+    if (nw > 12) nw = 16;
+    const dim3 block(nw * kWave);
+    for (int n0 = 0; n0 < N;) {
+        const int nc = a16 ? (N - n0 >= 8 ? 8 : 4) : 2;
+        const int R = min(pick_rows_per_wave(M, nw, 1, 2048), 32 / nc);
+        const dim3 grid(ceil_div(M, R));
+        if (S == 1) {
+            if (nc == 8) launch_q4n_steps<1, 8>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+            else if (nc == 4) launch_q4n_steps<1, 4>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+            else launch_q4n_steps<1, 2>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+        } else {
+            if (nc == 8) launch_q4n_steps<2, 8>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+            else if (nc == 4) launch_q4n_steps<2, 4>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+            else launch_q4n_steps<2, 2>(R, grid, block, st, sc, dt, B, C, M, kb, N, n0);
+        }
+        n0 += nc;
+    }
+    return true;
 }
 
 template <Fmt F, class XT>
@@ -936,6 +1335,15 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         launch_quad<F, XT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, sc,
                            reinterpret_cast<const uint32_t*>(data), B, C, M, kb);
         return (int)hipGetLastError();
+    }
+    if constexpr (F == Fmt::Q4_0 && sizeof(XT) == 4) {
+        if (q4_rb_ok(N, kb, M, reinterpret_cast<const float*>(B))) {
+            launch_q4_rb(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const float*>(B), C, M, kb, N,
+                         st);
+            return (int)hipGetLastError();
+        }
+        if (launch_q4n(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const float*>(B), C, M, kb, N, st))
+            return (int)hipGetLastError();
     }
     if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
         // N = 4, 8 (12, 16 on up to 2048 rows): the row-block GEMM, one launch

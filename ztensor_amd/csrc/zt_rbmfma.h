@@ -47,6 +47,34 @@ struct RbLayout {
     }
 };
 
+// The same step layout for K-orders whose MFMA steps read K offsets
+// {0, 2, 1, 3} + const (Q4_0's nibble order: a step takes the low nibbles
+// of bytes 0 and 2, then of bytes 1 and 3, of one dword).  The rotations
+// {0, 4, 8, 12} (N = 8) and {0, 1, 8, 9} (N = 16) put the 16 rows of a
+// transposing read on 16 distinct 8-byte bank slots: slot 2((k + sig) mod 16)
+// + (js & 1) for N = 8 and 2((2k + js/2 + sig) mod 16) + (js & 1) for N = 16.
+template <int NB>
+struct RbQ4Layout {
+    static_assert(NB == 2 || NB == 4, "Q4_0-order layout: N = 8 or 16");
+    static constexpr int N = 4 * NB;
+    static constexpr int PPC = 4 * N;
+    static constexpr int STEP = 1024 * N;
+    __device__ static __forceinline__ int sig(int c) { return NB == 2 ? 4 * (c & 3) : ((c & 1) | ((c & 2) << 2)); }
+};
+
+// LDS byte offset of the transposing read of MFMA step s (K positions
+// 4(s/2) + 16(s%2) + {0, 2, 1, 3}) and n-set js in the Q4_0-order layout.
+template <int NB>
+__device__ __forceinline__ int rb_q4_tr_offset(int lane, int s, int js) {
+    using Lay = RbQ4Layout<NB>;
+    const int e = (lane >> 2) & 3, q = lane & 3, c = 4 * (lane >> 4) + q;
+    const int ko = ((e & 1) << 1) | (e >> 1);  // {0, 2, 1, 3}
+    const int k = 4 * (s >> 1) + 16 * (s & 1) + ko;
+    const int b = 2 * Lay::N * k + 8 * js;
+    const int p = (b / 16 + Lay::sig(c)) % Lay::PPC;
+    return (c * Lay::PPC + p) * 16 + (b & 8);
+}
+
 // Issues the direct loads of one step's activations (global bytes
 // [gstep, gstep + STEP) of x) into the wave's LDS region `xs`.  Lanes past
 // the end of x read zeros (out-of-range buffer offsets).
@@ -133,10 +161,11 @@ __device__ __forceinline__ int rb_value_index(int lane, int i) {
 // the wave's sums in its own LDS region `own`, and, after a barrier, adds the
 // waves' sums in wave order (wave w's region at regions + w * region_bytes)
 // and stores C rows row0 .. row0 + 4R - 1.  acc[(r NB + js) 4 + v] holds row
-// row0 + 4r + (lane & 3), column 4js + v.
+// row0 + 4r + (lane & 3), column 4js + v; C row m, column n is at
+// y[m ldy + n0 + n] (ldy = N, n0 = 0 when the launch covers all of C's columns).
 template <int NB, int R>
 __device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* regions, int region_bytes, char* own,
-                                          float* __restrict__ y, int row0, int rows) {
+                                          float* __restrict__ y, int row0, int rows, int ldy = 4 * NB, int n0 = 0) {
     constexpr int N = 4 * NB, V = 4 * R * NB;
     const int lane = threadIdx.x & 63, j = lane & 3, nw = blockDim.x >> 6;
     rb_block_reduce<V>(acc);
@@ -153,7 +182,7 @@ __device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* 
         const int idx = ((r * NB + js) * 4 + v) * 4 + jj;
         float sum = 0.0f;
         for (int wv = 0; wv < nw; wv++) sum += reinterpret_cast<const float*>(regions + wv * region_bytes)[idx];
-        if (row0 + rl < rows) y[(long)row0 * N + o] = sum;
+        if (row0 + rl < rows) y[(long)(row0 + rl) * ldy + n0 + n] = sum;
     }
 }
 
