@@ -497,7 +497,7 @@ SUITE = {
     "q6_ks": ("q6_ks", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_0": ("q5_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q8_0_gguf": ("q8_0_gguf", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
-    "q4_0_batched": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q4_0_batched": ("q4_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     # gemm_int4.cu / gemm_int8.cu: decode shapes, and the reference benchmark's square GEMMs
     # (gemm_bench_test.go:159-165, batch = rows)
     "int4": ("int4", [(4096, 4096), (14336, 4096)], [1, 4]),
@@ -506,7 +506,8 @@ SUITE = {
     "int4_gemm": ("int4", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int4_rmul_gemm": ("int4_rmul", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int8_gemm": ("int8", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
-    "q8_0_batched": ("q8_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q8_0_batched": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
+    "q8_0_raw_batched": ("q8_0_raw", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8]),
     "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q8_0t": ("q8_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q4_kt": ("q4_kt", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),

@@ -240,7 +240,7 @@ def test_engine_batched_uses_tiled_layout(lib, orc, fmt, side):
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import Q4Storage, Q8Storage, Tensor
 
-    rows, K, N = 512, 1024, 8
+    rows, K, N = 8192, 4096, 8  # past the row-block GEMM's shapes (engine._block_rowblock)
     w = weights(fmt, rows, K, 84)
     if fmt == "q4":
         s = Q4Storage.from_raw(w.raw, rows * K)
@@ -259,6 +259,27 @@ def test_engine_batched_uses_tiled_layout(lib, orc, fmt, side):
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
     assert getattr(s, "_gpu_tiled", None) is not None
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+@pytest.mark.parametrize("rows,K,N", [(512, 1024, 4), (1024, 4096, 8), (4096, 4096, 4), (4100, 4096, 4)])
+def test_engine_batched_rowblock_dispatch(lib, orc, fmt, rows, K, N):
+    """Batches the row-block GEMM wins run on the batch-1 upload (no tiled
+    copy is built); the others keep the tiled layout; both give the
+    oracle's result."""
+    from ztensor_amd.engine import ROCmEngine, _block_rowblock
+    from ztensor_amd.storage import Q4Storage, Q8Storage, Tensor
+
+    w = weights(fmt, rows, K, 88)
+    if fmt == "q4":
+        s = Q4Storage.from_raw(w.raw, rows * K)
+    else:
+        q = w.raw.reshape(-1, 36)
+        s = Q8Storage.from_blocks(q[:, :4].copy().view("<f4").reshape(-1), q[:, 4:].copy().view(np.int8), rows * K)
+    x = synth.x_f32(K * N, 88).reshape(K, N)
+    y = ROCmEngine().matmul(Tensor((rows, K), s), torch.from_numpy(x).cuda()).cpu().numpy()
+    assert rel_err(y.reshape(-1), oracle(orc, fmt, w.raw, x, rows, K, N).reshape(-1)) <= TOL
+    assert (getattr(s, "_gpu_tiled", None) is None) == _block_rowblock(fmt, rows, K, N)
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q8"])
@@ -318,8 +339,9 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     """Batches outside {4, 8, 12, 16}: ROCmEngine runs them on the tiled
     kernels in column chunks of 16, zero-padded to a multiple of 4, and the
     result matches the reference CPU product (Q4_0 also with fp16
-    activations, widened exactly to fp32)."""
-    from ztensor_amd.engine import ROCmEngine
+    activations, widened exactly to fp32); chunks that the row-block GEMM
+    takes run on the batch-1 upload instead."""
+    from ztensor_amd.engine import ROCmEngine, _block_rowblock
     from ztensor_amd.storage import GPTQStorage, IQ4NLStorage, Q4Storage, Q8Storage, Tensor
 
     rows, K = 200, 1024
@@ -351,7 +373,8 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     y = eng.matmul(Tensor((rows, K), s), xd).cpu().numpy()
     assert y.shape == (rows, n)
     assert rel_err(y, ref) <= TOL
-    if fmt in ("w4a16", "iq4nl") and n < 12:
+    if (fmt in ("w4a16", "iq4nl") and n < 12) or (fmt in ("q4", "q4_f16", "q8") and
+                                                   _block_rowblock(fmt[:2], rows, K, -(-n // 4) * 4 if n < 16 else 16)):
         # chunks of 4 or 8 columns run the row-block GEMM on the batch-1 upload
         assert getattr(s, "_gpu_tiled", None) is None
     else:

@@ -41,7 +41,8 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 # VALU right away; the VGPR form of the MFMAs avoids copying each result out
 # of the accumulation registers first.
 _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-EXTRA = {"zt_blockt.hip": _VGPR_MFMA, "zt_q4.hip": _VGPR_MFMA, "zt_w4a16.hip": _VGPR_MFMA, "zt_intq.hip": _VGPR_MFMA}
+EXTRA = {"zt_blockt.hip": _VGPR_MFMA, "zt_q4.hip": _VGPR_MFMA, "zt_q8.hip": _VGPR_MFMA, "zt_w4a16.hip": _VGPR_MFMA,
+         "zt_intq.hip": _VGPR_MFMA}
 
 
 def sources() -> list[Path]:

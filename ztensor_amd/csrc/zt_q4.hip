@@ -933,242 +933,6 @@ static int launch_iq4nl_rb(const uint16_t* sc, const uint32_t* data, const uint1
     return (int)hipGetLastError();
 }
 
-// ------------------------------------------------------------ Q4_0 row-block GEMM (fp32 activations)
-//
-// Groups of 4 or 8 fp32 activation columns (columns n0 .. n0 + 4NB - 1 of
-// B[K, ldx]) on the separated upload layout, one launch per group: the
-// row-block structure of zt_rbmfma.h (v_mfma_f32_4x4x4_16b_f16, lane =
-// block of row j of a 4-row set, waves splitting K, activations staged per
-// wave and read back transposed).  fp32 activations cannot be MFMA operands
-// as they are, so each wave step
-//  * loads its 512 x 4NB activations into VGPRs (16-byte loads), takes the
-//    step's max |x| over the wave and a power of two c with c max|x| in
-//    [2^14, 2^15), and splits every c x into fp16 hi = fp16(c x) and
-//    lo = fp16(c x - hi): hi + lo equals c x to about 2^-22 relative, for
-//    any fp32 x, and c is undone exactly when the step's sums are taken;
-//  * writes hi and lo as 8NB fp16 columns (hi n-sets 0 .. NB-1, lo n-sets
-//    NB .. 2NB-1) in the Q4_0-order layout (RbQ4Layout).
-// B operand of MFMA step s (0-7) of a lane's block: the low (s even) or
-// high (s odd) nibbles of the four bytes of dword s/2, K order 4(s/2) +
-// 16(s%2) + {0, 2, 1, 3}, each as the fp16 2^14 + 2^10 q (normal range:
-// MFMA products of that size are exact and sum without the low bias of
-// subnormal operands).  Per block, n-set and step: D = sum (hi + lo) b
-// (hi and lo MFMAs into one chain) and X = sum (hi + lo) 2^14 (the same
-// with B = 2^14, shared by the row sets), so sum((q - 8) x) = 2^-10 (D -
-// 1.5 X) / c, and the block's fp16 scale d takes it: y += d 2^-10 (D/c -
-// 1.5 X/c).  Sums in wave and wave order (rb_finish): no atomics.
-template <int NB>
-__device__ __forceinline__ void q4rb_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr)[8 * NB], int step, int ldx, int n0,
-                                            int lane) {
-#pragma unroll
-    for (int i = 0; i < 8 * NB; i++) {
-        const int k = step * 512 + (NB == 1 ? 64 * i + lane : 32 * i + (lane >> 1));
-        const int col = n0 + (NB == 1 ? 0 : 4 * (lane & 1));
-        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(k * ldx + col) * 4u, 0, 0);
-    }
-}
-
-// B operand of MFMA step s from weight dword q: the low (hi_half = 0) or
-// high nibbles of bytes (0, 2) and (1, 3) moved to mantissa bits 6-9 under
-// the exponent of 2^14 (mask in a VGPR, exponent in an SGPR, as
-// rb_w4_operand).
-__device__ __forceinline__ half4v rb_q4_operand(uint32_t q, int hi_half, uint32_t mask, uint32_t expo) {
-    const uint32_t a = hi_half ? q << 2 : q << 6, b = hi_half ? q >> 6 : q >> 2;
-    return __builtin_bit_cast(half4v, (uint2){(a & mask) | expo, (b & mask) | expo});
-}
-
-template <int NB, int R, int S>
-__global__ void __launch_bounds__(1024) q4_rb_kernel(const uint16_t* __restrict__ scales,
-                                                     const uint32_t* __restrict__ data, const float* __restrict__ x,
-                                                     float* __restrict__ y, int rows, int kb, int ldx, int n0) {
-    using Lay = RbQ4Layout<2 * NB>;
-    constexpr int V = 4 * R * NB;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int blk = lane >> 2, j = lane & 3;
-    char* xs = smem + wave * Lay::STEP;
-    const int row0 = blockIdx.x * 4 * R;
-    // rows past M and K read zeros: the buffers end at row M and at K
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, rows * kb * 16, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, rows * kb * 2, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128 * ldx, 0x00020000);
-    const int step0 = wave * S;
-    u32x4 xr[8 * NB];
-    q4rb_load_x<NB>(rx, xr, step0, ldx, n0, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 w[S][R];
-    uint32_t sc[S][R];
-    const uint32_t brow = (uint32_t)(row0 + j) * (uint32_t)kb, bstep = 4u * (uint32_t)kb;
-#pragma unroll
-    for (int t = 0; t < S; t++) {
-        const int c = (step0 + t) * 16 + blk;
-        const bool ok = c < kb;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint32_t b = brow + r * bstep + (uint32_t)c;
-            w[t][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? b * 16u : 0x80000000u, 0, 2);  // nontemporal
-            sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? b * 2u : 0x80000000u, 0, 0);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; i++) acc[i] = 0.0f;
-    const half4v ones = (half4v){16384, 16384, 16384, 16384};  // 2^14
-    uint32_t bmask = 0x03C003C0u, bexp = 0x74007400u;
-    asm volatile("" : "+v"(bmask), "+s"(bexp));  // the mask in a VGPR, the exponent in an SGPR
-#pragma unroll
-    for (int t = 0; t < S; t++) {
-        if (t > 0) {
-            q4rb_load_x<NB>(rx, xr, step0 + t, ldx, n0, lane);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        } else {
-            // the activations only: the 2 S R weight and scale loads after them may be outstanding
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * S * R) : "memory");
-        }
-        // the step's normalisation c = 2^sh
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8 * NB; i++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(__uint_as_float(xr[i][e])));
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        int sh = 0;
-        if (m > 0.0f && m <= 3.402823466e38f) {
-            int e2;
-            (void)frexpf(m, &e2);  // m = f 2^e2, f in [0.5, 1)
-            sh = min(127, 15 - e2);
-        }
-        const float cs = ldexpf(1.0f, sh), ic = ldexpf(1.0f, -sh);
-        // the previous step's transposing reads precede these writes in the wave's
-        // LDS order; the scheduler must not move either across
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 8 * NB; i++) {
-            uint32_t hv[2], lv[2];
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-                const float v0 = __uint_as_float(xr[i][e]) * cs, v1 = __uint_as_float(xr[i][e + 1]) * cs;
-                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-                const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
-                hv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                lv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-            }
-            if constexpr (NB == 1) {
-                // K row k: one 16-byte piece (hi columns, then lo columns)
-                const int k = 64 * i + lane, c = k >> 5, p = ((k & 31) + Lay::sig(c)) & 31;
-                *reinterpret_cast<uint4*>(xs + (c * 32 + p) * 16) = make_uint4(hv[0], hv[1], lv[0], lv[1]);
-            } else {
-                // K row k: pieces 2k (hi) and 2k + 1 (lo), this lane's 4 columns at byte 8 (lane & 1)
-                const int k = 32 * i + (lane >> 1), c = k >> 5, hf = 8 * (lane & 1);
-                const int ph = (2 * (k & 31) + Lay::sig(c)) & 63, pl = (2 * (k & 31) + 1 + Lay::sig(c)) & 63;
-                *reinterpret_cast<uint2*>(xs + (c * 64 + ph) * 16 + hf) = make_uint2(hv[0], hv[1]);
-                *reinterpret_cast<uint2*>(xs + (c * 64 + pl) * 16 + hf) = make_uint2(lv[0], lv[1]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        float4v d[R][NB], dx[NB];
-#pragma unroll
-        for (int js = 0; js < NB; js++) {
-            dx[js] = (float4v){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int r = 0; r < R; r++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            half4v xa[2 * NB];
-#pragma unroll
-            for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_q4_tr_offset<2 * NB>(lane, s, js));
-            half4v bv[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const u32x4& wv = w[t][r];
-                const uint32_t q = (s >> 1) == 0 ? wv.x : (s >> 1) == 1 ? wv.y : (s >> 1) == 2 ? wv.z : wv.w;
-                bv[r] = rb_q4_operand(q, s & 1, bmask, bexp);
-            }
-            // hi parts, then lo parts: consecutive MFMAs of one chain are R NB + NB apart
-#pragma unroll
-            for (int hl = 0; hl < 2; hl++) {
-#pragma unroll
-                for (int js = 0; js < NB; js++)
-                    dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], ones, dx[js], 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < R; r++)
-#pragma unroll
-                    for (int js = 0; js < NB; js++)
-                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], bv[r], d[r][js], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int js = 0; js < NB; js++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float xo = 1.5f * dx[js][v] * ic;  // 1.5 X / c (exact scalings)
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    float& a = acc[(r * NB + js) * 4 + v];
-                    a = __builtin_fmaf(h2f((uint16_t)sc[t][r]) * 0x1p-10f, __builtin_fmaf(d[r][js][v], ic, -xo), a);
-                }
-            }
-    }
-    // waves split K: each wave leaves its sums in its own LDS region, then the
-    // workgroup adds them in wave order
-    rb_finish<NB, R>(acc, smem, Lay::STEP, xs, y, row0, rows, ldx, n0);
-}
-
-template <int NB, int R, int S>
-static void launch_q4_rb_t(dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data, const float* x,
-                           float* y, int rows, int kb, int ldx, int n0) {
-    const size_t lds = (size_t)nw * RbQ4Layout<2 * NB>::STEP;
-    if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
-        static const bool raised = [] {
-            return hipFuncSetAttribute(reinterpret_cast<const void*>(&q4_rb_kernel<NB, R, S>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-        }();
-        (void)raised;
-    }
-    q4_rb_kernel<NB, R, S><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
-}
-
-template <int NB>
-static void launch_q4_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint16_t* sc, const uint32_t* data,
-                           const float* x, float* y, int rows, int kb, int ldx, int n0) {
-#define ZT_RB(RR, SS) \
-    if (R == RR && S == SS) return launch_q4_rb_t<NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
-    ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
-    if constexpr (NB == 1) { ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(4, 2) ZT_RB(1, 4) ZT_RB(2, 4) }
-#undef ZT_RB
-}
-
-// Q4_0 row-block launches for the column groups of an fp32 batch: K split
-// into steps of 16 blocks over up to 16 waves, 1, 2 or 4 steps a wave, up
-// to 4 row sets a workgroup while about 200 workgroups remain.  8-column
-// groups (16 KB of hi/lo activations a wave) run one step a wave on up to
-// 8 waves (K <= 4096: with two steps a wave the kernel spills registers);
-// other columns go in groups of 4.
-static bool q4_rb_ok(int N, int kb, long M, const float* B) {
-    return N >= 4 && N % 4 == 0 && ((uintptr_t)B & 15) == 0 && kb <= 16 * 16 * 4 && M * kb * 16 < 0x7fffffffL &&
-           (long)(kb + 16) * 128 * N < 0x7fffffffL;
-}
-
-static void launch_q4_rb(const uint16_t* sc, const uint32_t* data, const float* B, float* C, int M, int kb, int N,
-                         hipStream_t st) {
-    for (int n0 = 0; n0 < N;) {
-        const int nc = (N - n0 >= 8 && kb <= 8 * 16) ? 8 : 4;
-        const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
-        const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
-        const int nw = ceil_div(steps, S);
-        const int rmax = S == 4 ? 2 : 4;
-        int R = 1;
-        while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
-        const dim3 g(ceil_div(M, 4 * R));
-        if (nc == 8) launch_q4_rb_n<2>(R, S, g, nw, st, sc, data, B, C, M, kb, N, n0);
-        else launch_q4_rb_n<1>(R, S, g, nw, st, sc, data, B, C, M, kb, N, n0);
-        n0 += nc;
-    }
-}
-
 static size_t iq4_mfma_lds_bytes(int N) {
     const size_t stage = (size_t)mfma_xbytes(N) + 16 + 16 * 4 + kMfmaUC * 4 * kMfmaRows * sizeof(uint16_t);
     return stage > mfma_reduce_bytes() ? stage : mfma_reduce_bytes();
@@ -1337,9 +1101,8 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         return (int)hipGetLastError();
     }
     if constexpr (F == Fmt::Q4_0 && sizeof(XT) == 4) {
-        if (q4_rb_ok(N, kb, M, reinterpret_cast<const float*>(B))) {
-            launch_q4_rb(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const float*>(B), C, M, kb, N,
-                         st);
+        if (rbf_ok<RbFmt::Q4_0>(N, kb, M, B)) {
+            launch_rbf<RbFmt::Q4_0>(sc, data, B, C, M, kb, N, st);
             return (int)hipGetLastError();
         }
         if (launch_q4n(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const float*>(B), C, M, kb, N, st))

@@ -14,12 +14,14 @@
 //                loads, so a wave reads 2 KiB of a row contiguously.
 //
 // Batch 1 uses the quad mapping of zt_q4.hip (four lanes per block, see
-// gemv_q8_quad_kernel); batched calls use lane <-> block column, R rows per
-// wave with the 32 activations held in registers, split-K across the waves
-// of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
+// gemv_q8_quad_kernel); batches of 4, 8, 12, ... columns run the row-block
+// MFMA GEMM of zt_rbmfma.h (rbf_kernel); other batches use lane <-> block
+// column, R rows per wave with the 32 activations held in registers, one
+// column per grid row, split-K across the waves of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
 // which v_cvt_f32_ubyte converts directly; sum (q+128) x - 128 sum x
 // recovers the signed dot product.
 #include "zt_common.h"
+#include "zt_rbmfma.h"
 
 namespace zt {
 
@@ -322,6 +324,13 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
         const int nw = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
         launch_q8_quad<L>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
+        return (int)hipGetLastError();
+    }
+    // N = 4, 8, 12, ...: the row-block MFMA GEMM, every weight read once per
+    // group of 4 or 8 columns
+    constexpr RbFmt RF = L == kRaw36 ? RbFmt::Q8_RAW : L == kSep32 ? RbFmt::Q8_SEP : RbFmt::Q8_SEP16;
+    if (rbf_ok<RF>(N, kb, M, B) && data_offset < 0x7fffffffL) {
+        launch_rbf<RF>(base, L == kRaw36 ? base : base + data_offset, B, C, M, kb, N, st);
         return (int)hipGetLastError();
     }
     const int nwaves = kb <= 64 ? 1 : (kb >= 8 * 64 ? 8 : ceil_div(kb, 64));

@@ -47,29 +47,28 @@ struct RbLayout {
     }
 };
 
-// The same step layout for K-orders whose MFMA steps read K offsets
-// {0, 2, 1, 3} + const (Q4_0's nibble order: a step takes the low nibbles
-// of bytes 0 and 2, then of bytes 1 and 3, of one dword).  The rotations
+// The same step layout for K orders whose MFMA steps read the K offsets
+// {0, 2, 1, 3} + const (a step takes bytes (0, 2) and then (1, 3) of a
+// dword: Q8_0's bytes, or the low or high nibbles of Q4_0's).  The rotations
 // {0, 4, 8, 12} (N = 8) and {0, 1, 8, 9} (N = 16) put the 16 rows of a
 // transposing read on 16 distinct 8-byte bank slots: slot 2((k + sig) mod 16)
 // + (js & 1) for N = 8 and 2((2k + js/2 + sig) mod 16) + (js & 1) for N = 16.
 template <int NB>
-struct RbQ4Layout {
-    static_assert(NB == 2 || NB == 4, "Q4_0-order layout: N = 8 or 16");
+struct RbO4Layout {
+    static_assert(NB == 2 || NB == 4, "offset-{0,2,1,3} layout: N = 8 or 16");
     static constexpr int N = 4 * NB;
     static constexpr int PPC = 4 * N;
     static constexpr int STEP = 1024 * N;
     __device__ static __forceinline__ int sig(int c) { return NB == 2 ? 4 * (c & 3) : ((c & 1) | ((c & 2) << 2)); }
 };
 
-// LDS byte offset of the transposing read of MFMA step s (K positions
-// 4(s/2) + 16(s%2) + {0, 2, 1, 3}) and n-set js in the Q4_0-order layout.
+// LDS byte offset of the transposing read of the MFMA step whose K
+// positions are kbase + {0, 2, 1, 3}, n-set js, in that layout.
 template <int NB>
-__device__ __forceinline__ int rb_q4_tr_offset(int lane, int s, int js) {
-    using Lay = RbQ4Layout<NB>;
+__device__ __forceinline__ int rb_o4_tr_offset(int lane, int kbase, int js) {
+    using Lay = RbO4Layout<NB>;
     const int e = (lane >> 2) & 3, q = lane & 3, c = 4 * (lane >> 4) + q;
-    const int ko = ((e & 1) << 1) | (e >> 1);  // {0, 2, 1, 3}
-    const int k = 4 * (s >> 1) + 16 * (s & 1) + ko;
+    const int k = kbase + (((e & 1) << 1) | (e >> 1));  // {0, 2, 1, 3}
     const int b = 2 * Lay::N * k + 8 * js;
     const int p = (b / 16 + Lay::sig(c)) % Lay::PPC;
     return (c * Lay::PPC + p) * 16 + (b & 8);
@@ -183,6 +182,290 @@ __device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* 
         float sum = 0.0f;
         for (int wv = 0; wv < nw; wv++) sum += reinterpret_cast<const float*>(regions + wv * region_bytes)[idx];
         if (row0 + rl < rows) y[(long)(row0 + rl) * ldy + n0 + n] = sum;
+    }
+}
+
+// ------------------------------------------------------------ fp32-activation row-block GEMMs
+//
+// Q4_0 and Q8_0 blocks (32 weights, one scale) with groups of 4 or 8 fp32
+// activation columns (columns n0 .. n0 + 4NB - 1 of B[K, ldx]), one launch a
+// group: the row-block structure above (v_mfma_f32_4x4x4_16b_f16, lane =
+// block of row j of a 4-row set, waves splitting K, activations staged per
+// wave and read back transposed, no K split across workgroups).  fp32
+// activations cannot be MFMA operands as they are, so each wave step
+//  * loads its 512 x 4NB activations into VGPRs (16-byte loads), takes the
+//    step's max |x| over the wave and a power of two c with c max|x| in
+//    [2^14, 2^15), and splits every c x into fp16 hi = fp16(c x) and
+//    lo = fp16(c x - hi): hi + lo equals c x to 2^-22 |c x| wherever lo is a
+//    normal fp16 (|x| >= 2^-17 max|x|), and to 2^-25 absolute below that;
+//    c is undone exactly (a power of two) when the step's sums are taken;
+//  * writes hi and lo as 8NB fp16 columns (hi n-sets 0 .. NB-1, lo n-sets
+//    NB .. 2NB-1) in the offset-{0,2,1,3} layout.
+// B operand of MFMA step s (0-7): four weights of the lane's block as
+// normal-range fp16, whose products with hi and lo are exact in fp32 and
+// sum without the low bias that subnormal operands get:
+//  * Q4_0: the low (s even) or high nibbles of bytes (0, 2) and (1, 3) of
+//    dword s/2 (K positions 4(s/2) + 16(s%2) + {0, 2, 1, 3}) as
+//    2^14 + 2^10 q;
+//  * Q8_0: bytes (0, 2) and (1, 3) of dword s (K positions 4s + {0, 2, 1,
+//    3}) as 2^15 + 2^7 u, u = q + 128 (q XOR 0x80).
+// Per block, n-set and step: D = sum (hi + lo) b (hi and lo MFMAs into one
+// chain) and X = sum (hi + lo) 2^14 (B = 2^14, shared by the row sets), so
+// sum(q x) c = 2^-10 (D - 1.5 X) for Q4_0 (q - 8) and 2^-7 (D - 3 X) for
+// Q8_0, and the block's scale d takes it: y += d 2^-e (D/c - o X/c).  Every
+// output is summed in wave and then wave order and stored once (rb_finish).
+enum class RbFmt { Q4_0, Q8_RAW, Q8_SEP, Q8_SEP16 };
+
+template <RbFmt F>
+struct RbFmtInfo {
+    static constexpr bool Q4 = F == RbFmt::Q4_0, RAW = F == RbFmt::Q8_RAW;
+    static constexpr int WD = Q4 ? 4 : 8;                                        // weight dwords a block
+    static constexpr int WL = Q4 ? 1 : RAW ? 4 : 2;                             // weight loads a block
+    static constexpr int BB = Q4 ? 16 : RAW ? 36 : 32;                           // data bytes a block
+    static constexpr int SBY = RAW ? 36 : (Q4 || F == RbFmt::Q8_SEP16) ? 2 : 4;  // scale stride
+};
+
+template <int NB>
+__device__ __forceinline__ void rbf_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr)[8 * NB], int step, int ldx, int n0,
+                                           int lane) {
+#pragma unroll
+    for (int i = 0; i < 8 * NB; i++) {
+        const int k = step * 512 + (NB == 1 ? 64 * i + lane : 32 * i + (lane >> 1));
+        const int col = n0 + (NB == 1 ? 0 : 4 * (lane & 1));
+        xr[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(k * ldx + col) * 4u, 0, 0);
+    }
+}
+
+// scales: fp16 or fp32 scales (Q8_RAW: the 36-byte blocks); data: 16- or
+// 32-byte blocks (Q8_RAW: the 36-byte blocks again).
+template <RbFmt F, int NB, int R, int S>
+__global__ void __launch_bounds__(1024) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
+                                                   const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                   int kb, int ldx, int n0) {
+    using Info = RbFmtInfo<F>;
+    using Lay = RbO4Layout<2 * NB>;
+    constexpr int V = 4 * R * NB;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int blk = lane >> 2, j = lane & 3;
+    char* xs = smem + wave * Lay::STEP;
+    const int row0 = blockIdx.x * 4 * R;
+    // rows past M and K read zeros: the buffers end at row M and at K
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, rows * kb * Info::BB, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, rows * kb * Info::SBY, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128 * ldx, 0x00020000);
+    const int step0 = wave * S;
+    u32x4 xr[8 * NB];
+    rbf_load_x<NB>(rx, xr, step0, ldx, n0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t w[S][R][Info::WD], sc[S][R];
+    const uint32_t brow = (uint32_t)(row0 + j) * (uint32_t)kb, bstep = 4u * (uint32_t)kb;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int c = (step0 + t) * 16 + blk;
+        const bool ok = c < kb;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t b = brow + r * bstep + (uint32_t)c;
+            const uint32_t wo = ok ? b * (uint32_t)Info::BB : 0x80000000u;
+            if constexpr (Info::RAW) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {  // 8 bytes at block offsets 4 + 8i (dword aligned)
+                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, wo + 4 + 8 * i, 0, 2));
+                    w[t][r][2 * i] = v.x;
+                    w[t][r][2 * i + 1] = v.y;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < Info::WL; i++) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 16 * i, 0, 2);  // nontemporal
+                    w[t][r][4 * i] = v.x;
+                    w[t][r][4 * i + 1] = v.y;
+                    w[t][r][4 * i + 2] = v.z;
+                    w[t][r][4 * i + 3] = v.w;
+                }
+            }
+            const uint32_t so = ok ? b * (uint32_t)Info::SBY : 0x80000000u;
+            sc[t][r] = Info::SBY == 2 ? __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0)
+                                      : __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+    const half4v ones = (half4v){16384, 16384, 16384, 16384};  // 2^14
+    uint32_t bmask = Info::Q4 ? 0x03C003C0u : 0x03FC03FCu, bexp = Info::Q4 ? 0x74007400u : 0x78007800u;
+    asm volatile("" : "+v"(bmask), "+s"(bexp));  // the mask in a VGPR, the exponent in an SGPR (v_and_or_b32)
+    constexpr float kSm = Info::Q4 ? 0x1p-10f : 0x1p-7f, kOff = Info::Q4 ? 1.5f : 3.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        if (t > 0) {
+            rbf_load_x<NB>(rx, xr, step0 + t, ldx, n0, lane);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            // the activations only: the weight and scale loads after them may be outstanding
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S * R * (Info::WL + 1)) : "memory");
+        }
+        // the step's normalisation c = 2^sh
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8 * NB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(__uint_as_float(xr[i][e])));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        int sh = 0;
+        if (m > 0.0f && m <= 3.402823466e38f) {
+            int e2;
+            (void)frexpf(m, &e2);  // m = f 2^e2, f in [0.5, 1)
+            sh = min(127, 15 - e2);
+        }
+        const float cs = ldexpf(1.0f, sh), ic = ldexpf(1.0f, -sh);
+        // the previous step's transposing reads precede these writes in the
+        // wave's LDS order; the scheduler must not move either across
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8 * NB; i++) {
+            uint32_t hv[2], lv[2];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const float v0 = __uint_as_float(xr[i][e]) * cs, v1 = __uint_as_float(xr[i][e + 1]) * cs;
+                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+                const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+                hv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lv[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            if constexpr (NB == 1) {
+                // K row k: one 16-byte piece (hi columns, then lo columns)
+                const int k = 64 * i + lane, c = k >> 5, p = ((k & 31) + Lay::sig(c)) & 31;
+                *reinterpret_cast<uint4*>(xs + (c * 32 + p) * 16) = make_uint4(hv[0], hv[1], lv[0], lv[1]);
+            } else {
+                // K row k: pieces 2k (hi) and 2k + 1 (lo), this lane's 4 columns at byte 8 (lane & 1)
+                const int k = 32 * i + (lane >> 1), c = k >> 5, hf = 8 * (lane & 1);
+                const int ph = (2 * (k & 31) + Lay::sig(c)) & 63, pl = (2 * (k & 31) + 1 + Lay::sig(c)) & 63;
+                *reinterpret_cast<uint2*>(xs + (c * 64 + ph) * 16 + hf) = make_uint2(hv[0], hv[1]);
+                *reinterpret_cast<uint2*>(xs + (c * 64 + pl) * 16 + hf) = make_uint2(lv[0], lv[1]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float4v d[R][NB], dx[NB];
+#pragma unroll
+        for (int js = 0; js < NB; js++) {
+            dx[js] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < R; r++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int kbase = Info::Q4 ? 4 * (s >> 1) + 16 * (s & 1) : 4 * s;
+            half4v xa[2 * NB];
+#pragma unroll
+            for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_o4_tr_offset<2 * NB>(lane, kbase, js));
+            half4v bv[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                uint32_t a, b;
+                if constexpr (Info::Q4) {
+                    const uint32_t q = w[t][r][s >> 1];
+                    a = (s & 1) ? q << 2 : q << 6;  // bytes 0, 2: low or high nibbles
+                    b = (s & 1) ? q >> 6 : q >> 2;  // bytes 1, 3
+                } else {
+                    const uint32_t u = w[t][r][s] ^ 0x80808080u;  // q + 128
+                    a = u << 2;                                  // bytes 0, 2
+                    b = u >> 6;                                  // bytes 1, 3
+                }
+                bv[r] = __builtin_bit_cast(half4v, (uint2){(a & bmask) | bexp, (b & bmask) | bexp});
+            }
+            // hi parts, then lo parts: consecutive MFMAs of one chain are R NB + NB apart
+#pragma unroll
+            for (int hl = 0; hl < 2; hl++) {
+#pragma unroll
+                for (int js = 0; js < NB; js++)
+                    dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], ones, dx[js], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < R; r++)
+#pragma unroll
+                    for (int js = 0; js < NB; js++)
+                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], bv[r], d[r][js], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float dv = (Info::SBY == 2 ? h2f((uint16_t)sc[t][r]) : __uint_as_float(sc[t][r])) * kSm;
+#pragma unroll
+            for (int js = 0; js < NB; js++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    float& a = acc[(r * NB + js) * 4 + v];
+                    a = __builtin_fmaf(dv, __builtin_fmaf(d[r][js][v], ic, -kOff * dx[js][v] * ic), a);
+                }
+        }
+    }
+    // waves split K: each wave leaves its sums in its own LDS region, then the
+    // workgroup adds them in wave order
+    rb_finish<NB, R>(acc, smem, Lay::STEP, xs, y, row0, rows, ldx, n0);
+}
+
+template <RbFmt F, int NB, int R, int S>
+static void launch_rbf_t(dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data, const float* x,
+                         float* y, int rows, int kb, int ldx, int n0) {
+    const size_t lds = (size_t)nw * RbO4Layout<2 * NB>::STEP;
+    if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
+        static const bool raised = [] {
+            return hipFuncSetAttribute(reinterpret_cast<const void*>(&rbf_kernel<F, NB, R, S>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        }();
+        (void)raised;
+    }
+    rbf_kernel<F, NB, R, S><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
+}
+
+template <RbFmt F, int NB>
+static void launch_rbf_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data,
+                         const float* x, float* y, int rows, int kb, int ldx, int n0) {
+#define ZT_RB(RR, SS) \
+    if (R == RR && S == SS) return launch_rbf_t<F, NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
+    ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
+    if constexpr (NB == 1) { ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4) }
+    if constexpr (NB == 1 && RbFmtInfo<F>::Q4) { ZT_RB(4, 2) }
+#undef ZT_RB
+}
+
+// Shapes the fp32-activation row-block GEMM takes: N % 4 == 0, 16-byte
+// aligned activation rows, K <= 32768, 32-bit buffer offsets.
+template <RbFmt F>
+static bool rbf_ok(int N, int kb, long M, const void* B) {
+    return N >= 4 && N % 4 == 0 && ((uintptr_t)B & 15) == 0 && kb <= 16 * 16 * 4 &&
+           M * kb * RbFmtInfo<F>::BB < 0x7fffffffL && (long)(kb + 16) * 128 * N < 0x7fffffffL;
+}
+
+// One launch per column group: K in steps of 16 blocks over up to 16 waves,
+// 1, 2 or 4 steps a wave, up to 4 row sets a workgroup (2 at 4 steps, and
+// for Q8_0's 32-byte blocks at 2 steps: more spill registers) while about
+// 200 workgroups remain.  8-column groups (16 KB of hi/lo activations a
+// wave) run one step a wave on up to 8 waves (K <= 4096: at two steps a wave
+// the kernel spills registers); other columns go in groups of 4.
+template <RbFmt F>
+static void launch_rbf(const void* scales, const void* data, const void* B, float* C, int M, int kb, int N,
+                       hipStream_t st) {
+    const uint8_t* sc = static_cast<const uint8_t*>(scales);
+    const uint8_t* dt = static_cast<const uint8_t*>(data);
+    const float* x = static_cast<const float*>(B);
+    for (int n0 = 0; n0 < N;) {
+        const int nc = (N - n0 >= 8 && kb <= 8 * 16) ? 8 : 4;
+        const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
+        const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
+        const int nw = ceil_div(steps, S);
+        const int rmax = S == 4 || (S == 2 && !RbFmtInfo<F>::Q4) ? 2 : 4;
+        int R = 1;
+        while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
+        const dim3 g(ceil_div(M, 4 * R));
+        if (nc == 8) launch_rbf_n<F, 2>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
+        else launch_rbf_n<F, 1>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
+        n0 += nc;
     }
 }
 

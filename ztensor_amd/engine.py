@@ -427,7 +427,12 @@ class ROCmEngine:
         if isinstance(s, MmapStorage):
             return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
-            if x.dtype in (torch.float32, torch.float16) and n in _TILED_BATCHES and k % 128 == 0:
+            if x.dtype in (torch.float32, torch.float16) and _block_rowblock("q4", rows, k, n):
+                # one launch on the separated upload (the row-block GEMM): no tiled copy, no workspace
+                x = x.float() if x.dtype == torch.float16 else x
+                x = x if _p(x) % 16 == 0 else x.clone()
+                self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype in (torch.float32, torch.float16) and n in _TILED_BATCHES and k % 128 == 0:
                 # fp16 activations widen exactly to fp32 for the tiled kernel
                 x = x.float() if x.dtype == torch.float16 or _p(x) % 16 else x
                 wt, st = self._block_tiled(s, buf, rows, k, "q4")
@@ -458,6 +463,10 @@ class ROCmEngine:
         elif isinstance(s, Q8Storage):
             if x.dtype != torch.float32:
                 raise TypeError("Q8_0 matmul takes fp32 activations")
+            if _block_rowblock("q8", rows, k, n) and _p(x) % 16 == 0:
+                # one launch on the separated upload (the row-block GEMM)
+                self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+                return c
             if n in _TILED_BATCHES and k % 128 == 0 and _p(x) % 16 == 0:
                 wt, st = self._block_tiled(s, buf, rows, k, "q8")
                 ws, wsb = self._workspace(self.lib.zt_gemm_q8t_workspace_bytes(rows, k, n))
@@ -553,7 +562,11 @@ class ROCmEngine:
             raise TypeError("MmapStorage matmul takes fp32 activations")
         q, p, offs = s.qtype, _p(buf.tensor), s._gpu_offsets
         tiled = n in _TILED_BATCHES and _p(x) % 16 == 0
-        if q == GGMLType.Q4_0 and tiled and k % 128 == 0:
+        if q == GGMLType.Q4_0 and tiled and _block_rowblock("q4", rows, k, n):
+            self.gemm_q4_f32(p, _p(x), _p(c), rows, k, n, offs["data_offset"])
+        elif q == GGMLType.Q8_0 and tiled and _block_rowblock("q8", rows, k, n):
+            self.lib.call("zt_gemm_q8gguf_f32", p, _p(x), _p(c), rows, k, n, offs["data_offset"], self._s)
+        elif q == GGMLType.Q4_0 and tiled and k % 128 == 0:
             # batches on the tiled MFMA kernel, as for Q4Storage (the device layout is RawBytesGPU)
             wt, st = self._block_tiled(s, buf, rows, k, "q4")
             ws, wsb = self._workspace(self.lib.zt_gemm_q4t_workspace_bytes(rows, k, n))
@@ -701,6 +714,22 @@ class ROCmEngine:
         w = self._to_dev(s.row_aligned(rows, cols))
         s._gpu_rows = ((rows, cols), w)  # type: ignore[attr-defined]
         return w
+
+
+def _block_rowblock(fmt: str, rows: int, k: int, n: int) -> bool:
+    """Whether a batch of fp32 columns on Q4_0 ("q4") or Q8_0 ("q8") weights
+    runs faster as one launch of the row-block GEMM on the batch-1 upload
+    (zt_gemm_q4_f32 / zt_gemm_q8sep_f32 with N > 1) than on the tiled layout
+    with its split-K reduction.  Measured (us, row-block against tiled) at
+    batch 4 / 8: Q4_0 4096 x 4096 5.2 / 7.0 against 6.6 / 7.4, 1024 x 4096
+    4.4 / 5.6 against 5.6 / 5.6, 14336 x 4096 12.6 / 24.1 against 11.7 /
+    13.0; Q8_0 4096 x 4096 7.2 / 8.8 against 7.7 / 7.9, 1024 x 4096 4.4 / 5.8
+    against 5.7 / 5.8.  The row-block kernel stages each wave step's
+    activations as fp16 hi + lo parts (16 KB a wave at batch 8), which caps
+    its occupancy on large matrices."""
+    if n not in (4, 8) or rows * k > 4096 * 4096 or k > 32768:
+        return False
+    return fmt == "q4" or n == 4
 
 
 def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
