@@ -9,8 +9,15 @@
  * Only argument-validation paths are called: every call returns before any
  * HIP runtime call, so no GPU is needed and no kernel is launched.
  *
+ * The zero-CGo linux/amd64 binding resolves dlopen and dlsym as dynamic
+ * imports of the executable and calls them through the same all-uintptr_t
+ * trampoline as the entry points.  The first checks below do exactly that:
+ * dlopen and dlsym are taken as plain addresses and called through the
+ * 20-argument signature, and what they return must equal the direct calls.
+ *
  * Usage: ccall_abi /path/to/libzt_hip.so   (exit status 0 = all checks pass)
  */
+#define _GNU_SOURCE /* RTLD_DEFAULT */
 #include <dlfcn.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -65,6 +72,19 @@ int main(int argc, char** argv) {
         printf("FAIL dlopen: %s\n", dlerror());
         return 1;
     }
+    /* dlopen and dlsym as addresses, called through the trampoline's signature */
+    ccall20 dlopen_u = (ccall20)dlsym(RTLD_DEFAULT, "dlopen");
+    ccall20 dlsym_u = (ccall20)dlsym(RTLD_DEFAULT, "dlsym");
+    if (dlopen_u == NULL || dlsym_u == NULL) {
+        printf("FAIL dlsym(RTLD_DEFAULT, dlopen/dlsym): %s\n", dlerror());
+        return 1;
+    }
+    const u h = call(dlopen_u, (u)argv[1], RTLD_NOW | RTLD_GLOBAL, 0, 0, 0, 0, 0, 0, 0, 0, 0);
+    expect_int("dlopen through the trampoline signature returns the library's handle", h == (u)lib, 1);
+    const u fa = call(dlsym_u, h, (u) "zt_abi_version", 0, 0, 0, 0, 0, 0, 0, 0, 0);
+    expect_int("dlsym through the trampoline signature finds zt_abi_version", fa == (u)dlsym(lib, "zt_abi_version"), 1);
+    expect_int("dlsym through the trampoline signature of a missing name is 0",
+               call(dlsym_u, h, (u) "zt_no_such_symbol", 0, 0, 0, 0, 0, 0, 0, 0, 0) == 0, 1);
     const u p = 0x100000; /* a 16-byte-aligned pointer value that is never dereferenced */
     const u neg1 = (u)(intptr_t)-1;
 
@@ -82,6 +102,8 @@ int main(int argc, char** argv) {
     ccall20 w4tws = sym("zt_gemm_w4a16t_workspace_bytes");
     ccall20 iqt = sym("zt_gemm_iq4nlt_f16");
     ccall20 iqtws = sym("zt_gemm_iq4nlt_workspace_bytes");
+    ccall20 tgrp = sym("zt_ternary_gemv_i8_group");
+    ccall20 rd = sym("zt_bench_stream_read");
     if (failures) return 1;
 
     /* int return, no arguments */
@@ -113,6 +135,19 @@ int main(int argc, char** argv) {
     expect_int("zt_gemm_iq4nlt_f16(no workspace)", call(iqt, p, p, p, p, 1024, 8192, 8, 0, 0, 0, 0), 1);
     /* a host pointer argument: zero descriptors */
     expect_int("zt_gemm_q4_group_f32(n = 0)", call(grp, p, 0, p, 64, 0, 0, 0, 0, 0, 0, 0), 1);
+    /* the grouped ternary GEMV reads its host descriptors before any launch: a matrix without
+       weights is InvalidValue, every matrix empty is a no-op success */
+    struct {
+        u W, w_scale, y;
+        int rows, reserved;
+    } td[2] = {{0, p, p, 4, 0}, {0, 0, 0, 0, 0}};
+    expect_int("zt_ternary_gemv_i8_group(no weights)", call(tgrp, (u)&td[0], 1, p, p, 64, 0, 0, 0, 0, 0, 0), 1);
+    expect_int("zt_ternary_gemv_i8_group(all empty)", call(tgrp, (u)&td[1], 1, p, p, 64, 0, 0, 0, 0, 0, 0), 0);
+    expect_int("zt_ternary_gemv_i8_group(n = 0)", call(tgrp, (u)&td[1], 0, p, p, 64, 0, 0, 0, 0, 0, 0), 1);
+    /* the streaming-read measurement kernel: a long size argument, a misaligned buffer, an empty read */
+    expect_int("zt_bench_stream_read(p + 8)", call(rd, p + 8, 4096, p, 0, 0, 0, 0, 0, 0, 0, 0), 1);
+    expect_int("zt_bench_stream_read(nbytes = -1)", call(rd, p, neg1, p, 0, 0, 0, 0, 0, 0, 0, 0), 1);
+    expect_int("zt_bench_stream_read(nbytes = 0)", call(rd, p, 0, p, 0, 0, 0, 0, 0, 0, 0, 0), 0);
     /* long returns come back whole */
     expect_long("zt_q4_gpu_data_offset(5)", call(off, 5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0), 16);
     expect_long("zt_q4_gpu_data_offset(1<<31)", call(off, (u)1 << 31, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0), 1L << 32);
