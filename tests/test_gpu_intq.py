@@ -80,6 +80,8 @@ def run_int8(lib, a, b, M, K, N):
 INT4_CASES = [  # M, K, N, group_size
     (4096, 4096, 1, 32), (4096, 4096, 1, 128), (14336, 4096, 1, 128), (4096, 4096, 4, 32), (333, 1024, 3, 64),
     (1, 16, 1, 16), (4096, 4096, 2, 32), (100, 4112, 4, 16), (33, 8208, 2, 48),
+    # batches 2-4 on 8192 rows: 4 rows a wave of the LDS-staged kernel, a partial last 4096-K chunk
+    (8192, 4112, 2, 16), (8192, 4112, 3, 16), (8192, 4112, 4, 16),
     # MFMA GEMM: group sizes not a multiple of 16, odd shapes, wider batches
     (1000, 1000, 2, 20), (77, 130, 5, 7), (65, 34, 9, 2), (512, 4096, 16, 128), (100, 2048, 64, 32), (3, 2, 1, 1),
     # bf16 MFMA GEMM (K % 32, group % 32, N even): partial 128 x 128 tiles
@@ -116,6 +118,8 @@ INT8_CASES = [  # M, K, N
     (4096, 4096, 1), (4096, 14336, 1), (4096, 4096, 4), (1, 16, 1), (333, 1024, 3),
     (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65), (64, 4112, 2), (31, 8208, 4),
     (200, 4128, 130), (129, 32, 6),
+    # batches 2-4 on 8192 rows: 4 rows a wave of the LDS-staged kernel, a partial last 4096-K chunk
+    (8192, 4112, 2), (8192, 4112, 3), (8192, 4112, 4),
 ]
 
 
@@ -139,6 +143,29 @@ def test_int4_nt_zero_points_full_range(lib, orc, zmax):
     b = synth.x_f32(K * N, 321).reshape(K, N)
     y = run_int4(lib, w, b, M, K, N, gs)
     assert rel_err(y, orc.gemm_int4_f32(w.packed, b, w.scales, w.zeros, M, K, N, gs)) <= TOL
+
+
+@pytest.mark.parametrize("zmax", [0, 15, 255])
+def test_int4_bf16_per_element_error(lib, orc, zmax):
+    """Each output of the bf16 MFMA GEMM against the exact product,
+    relative to that output's own sum of |w x| (not to max |y|, which hides
+    small outputs), beside the same measure of the reference's fp32 loop
+    (the oracle).  The int4 operand is 136 + v and the offset (136 + z) sum(x)
+    comes off once per 32-K step, so each step's fp32 sums are about
+    (272 + z) / |v - z| times larger than the step's result."""
+    M, K, N, gs = 512, 4096, 32, 128
+    w = synth.int4(M, K, gs, 330 + zmax, zero_max=zmax)
+    b = synth.x_f32(K * N, 331).reshape(K, N)
+    y = run_int4(lib, w, b, M, K, N, gs).reshape(M, N).astype(np.float64)
+    W = synth.int4_dense(w, gs).astype(np.float64).reshape(M, K)
+    exact = W @ b.astype(np.float64)
+    mag = np.abs(W) @ np.abs(b.astype(np.float64))
+    ref = np.asarray(orc.gemm_int4_f32(w.packed, b, w.scales, w.zeros, M, K, N, gs), np.float64).reshape(M, N)
+    ours = float(np.max(np.abs(y - exact) / mag))
+    theirs = float(np.max(np.abs(ref - exact) / mag))
+    say(f"int4 bf16 zmax={zmax}: per-element |y - exact| / sum|w x|: {ours:.3e} (reference loop {theirs:.3e})")
+    # measured 3.8e-7 / 1.6e-7 / 3.9e-8 against the loop's 2.2e-7 / 2.9e-7 / 2.0e-7 (z <= 0 / 15 / 255)
+    assert ours <= 1e-6 and ours <= 4 * theirs
 
 
 @pytest.mark.parametrize("fmt", ["int4", "int8", "rmul"])

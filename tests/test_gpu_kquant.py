@@ -311,6 +311,29 @@ def test_engine_q6k_batch1_split_copy(orc):
     assert st._gpu_split is not None and st._gpu_split[1] is not first
 
 
+@pytest.mark.parametrize("opts", [dict(q6k_split=False), dict(split_reserve_bytes=1 << 62)])
+def test_engine_q6k_split_opt_out(orc, opts):
+    """With q6k_split=False, or when the copy would leave less than the
+    reserve free, Q6_K batch 1 reads the raw super-blocks: no split copy is
+    built and the result is the raw-layout GEMV's, bit for bit."""
+    from ztensor_amd import _lib
+    from ztensor_amd.engine import ROCmEngine
+
+    eng = ROCmEngine(**opts)
+    rows, K = 96, 2048
+    w = synth.kquant("q6_k", rows, K, 94)
+    st = Q6KStorage.from_raw(w.raw, rows * K)
+    x = synth.x_f32(K, 94)
+    got = eng.matmul(Tensor((rows, K), st), devf(x)).cpu().numpy().reshape(-1)
+    assert getattr(st, "_gpu_split", None) is None
+    assert rel_err(got, orc.gemm_f32_kq_nt("q6_k", x, w.raw, 1, rows, K)) <= TOL
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xd = devf(x)
+    _lib.load().call("zt_gemv_q6k_f32", st.gpu_ptr().tensor.data_ptr(), xd.data_ptr(), y.data_ptr(), rows, K,
+                     torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(got.view(np.uint32), y.cpu().numpy().view(np.uint32))
+
+
 # ------------------------------------------------------------------ GGUF mmap
 
 

@@ -81,12 +81,20 @@ def _tiled_cached(s: Any, key: tuple):
 
 
 class ROCmEngine:
-    def __init__(self, device: int = 0, stream: torch.cuda.Stream | None = None):
+    def __init__(self, device: int = 0, stream: torch.cuda.Stream | None = None, q6k_split: bool = True,
+                 split_reserve_bytes: int = 1 << 30):
+        """q6k_split: Q6_K batch 1 on a split copy of the super-blocks (35-55%
+        faster; it doubles the resident Q6_K bytes).  The copy is built only
+        while at least split_reserve_bytes of device memory stay free after
+        it; otherwise, or with q6k_split=False, batch 1 reads the raw
+        super-blocks."""
         if not torch.cuda.is_available():
             raise RuntimeError("ROCmEngine needs a ROCm GPU (torch.cuda.is_available() is False)")
         self.device = torch.device("cuda", device)
         self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
         self.lib = _lib.load()
+        self.q6k_split = q6k_split
+        self.split_reserve_bytes = split_reserve_bytes
 
     @property
     def _s(self) -> int:
@@ -368,14 +376,20 @@ class ROCmEngine:
         uploaded raw super-blocks on the first batch-1 call and kept beside
         them: 35-55% faster than the raw-layout GEMV at the Llama-3-8B
         shapes.  Falls back to the raw-layout GEMV where the split kernel's
-        32-bit offsets or x's alignment do not allow it."""
-        if rows * (k // 256) * 210 >= 1 << 31 or _p(x) % 16 != 0:
-            self.lib.call("zt_gemv_q6k_f32", raw_ptr, _p(x), _p(c), rows, k, self._s)
-            return
+        32-bit offsets or x's alignment do not allow it, when the engine was
+        made with q6k_split=False, and when building the copy would leave less
+        than split_reserve_bytes of device memory free."""
         key = ("q6ks", rows, k, raw_ptr)
         cached = getattr(s, "_gpu_split", None)
-        if cached is None or cached[0] != key:
-            sp = torch.empty(self.lib.zt_q6k_split_bytes(rows, k), dtype=torch.uint8, device=self.device)
+        if cached is not None and cached[0] != key:
+            s._gpu_split = cached = None  # type: ignore[attr-defined]  # a stale copy goes before a new one
+        nbytes = self.lib.zt_q6k_split_bytes(rows, k)
+        if (rows * (k // 256) * 210 >= 1 << 31 or _p(x) % 16 != 0 or not self.q6k_split
+                or (cached is None and torch.cuda.mem_get_info(self.device)[0] < nbytes + self.split_reserve_bytes)):
+            self.lib.call("zt_gemv_q6k_f32", raw_ptr, _p(x), _p(c), rows, k, self._s)
+            return
+        if cached is None:
+            sp = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
             self.lib.call("zt_q6k_split", raw_ptr, rows, k, _p(sp), self._s)
             cached = (key, sp)
             s._gpu_split = cached  # type: ignore[attr-defined]
