@@ -238,8 +238,11 @@ __device__ __forceinline__ void rbf_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr
 
 // scales: fp16 or fp32 scales (Q8_RAW: the 36-byte blocks); data: 16- or
 // 32-byte blocks (Q8_RAW: the 36-byte blocks again).
+// 8-column groups run at most 8 waves a workgroup, and their 16 KB of LDS a
+// wave allow no more than 8 waves a CU anyway, so their launch bound of 512
+// threads costs no occupancy and leaves up to 256 VGPRs a lane.
 template <RbFmt F, int NB, int R, int S>
-__global__ void __launch_bounds__(1024) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
+__global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
                                                    const float* __restrict__ x, float* __restrict__ y, int rows,
                                                    int kb, int ldx, int n0) {
     using Info = RbFmtInfo<F>;
@@ -428,9 +431,8 @@ static void launch_rbf_n(int R, int S, dim3 g, int nw, hipStream_t st, const uin
                          const float* x, float* y, int rows, int kb, int ldx, int n0) {
 #define ZT_RB(RR, SS) \
     if (R == RR && S == SS) return launch_rbf_t<F, NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
-    ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
-    if constexpr (NB == 1) { ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4) }
-    if constexpr (NB == 1 && RbFmtInfo<F>::Q4) { ZT_RB(4, 2) }
+    ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1) ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4)
+    if constexpr (RbFmtInfo<F>::Q4) { ZT_RB(8, 1) ZT_RB(4, 2) }
 #undef ZT_RB
 }
 
@@ -442,24 +444,29 @@ static bool rbf_ok(int N, int kb, long M, const void* B) {
            M * kb * RbFmtInfo<F>::BB < 0x7fffffffL && (long)(kb + 16) * 128 * N < 0x7fffffffL;
 }
 
-// One launch per column group: K in steps of 16 blocks over up to 16 waves,
-// 1, 2 or 4 steps a wave, up to 4 row sets a workgroup (2 at 4 steps, and
-// for Q8_0's 32-byte blocks at 2 steps: more spill registers) while about
-// 200 workgroups remain.  8-column groups (16 KB of hi/lo activations a
-// wave) run one step a wave on up to 8 waves (K <= 4096: at two steps a wave
-// the kernel spills registers); other columns go in groups of 4.
+// One launch per column group: K in steps of 16 blocks over up to 16 waves
+// (8 for 8-column groups, whose hi/lo activations take 16 KB of LDS a wave),
+// 1, 2 or 4 steps a wave, and row sets doubled while about 200 workgroups
+// remain: up to 8 for Q4_0 at one step a wave, 4 at two, 2 at four steps
+// and for Q8_0's 32-byte blocks past one step (beyond that the kernel
+// spills registers).  Columns go in groups of 8 up to K = 8192 (Q4_0) or
+// 32768 (Q8_0), else of 4.  Measured (us, batch 4 / 8): Q4_0 14336 x 4096
+// 10.8 / 17.8 with 8 row sets against 12.6 / 24.1 with 4; at 4096 x 14336
+// two 4-column launches beat one 8-column launch at four steps a wave
+// (29.8 against 31.6), for Q8_0 the 8-column launch wins (38.5 against 55.0).
 template <RbFmt F>
 static void launch_rbf(const void* scales, const void* data, const void* B, float* C, int M, int kb, int N,
                        hipStream_t st) {
     const uint8_t* sc = static_cast<const uint8_t*>(scales);
     const uint8_t* dt = static_cast<const uint8_t*>(data);
     const float* x = static_cast<const float*>(B);
+    constexpr bool Q4 = RbFmtInfo<F>::Q4;
     for (int n0 = 0; n0 < N;) {
-        const int nc = (N - n0 >= 8 && kb <= 8 * 16) ? 8 : 4;
+        const int nc = (N - n0 >= 8 && kb <= (Q4 ? 8 * 16 * 2 : 8 * 16 * 4)) ? 8 : 4;
         const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
         const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
         const int nw = ceil_div(steps, S);
-        const int rmax = S == 4 || (S == 2 && !RbFmtInfo<F>::Q4) ? 2 : 4;
+        const int rmax = S == 4 || (S == 2 && !Q4) ? 2 : (S == 1 && Q4) ? 8 : 4;
         int R = 1;
         while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
         const dim3 g(ceil_div(M, 4 * R));

@@ -735,15 +735,18 @@ def _block_rowblock(fmt: str, rows: int, k: int, n: int) -> bool:
     runs faster as one launch of the row-block GEMM on the batch-1 upload
     (zt_gemm_q4_f32 / zt_gemm_q8sep_f32 with N > 1) than on the tiled layout
     with its split-K reduction.  Measured (us, row-block against tiled) at
-    batch 4 / 8: Q4_0 4096 x 4096 5.2 / 7.0 against 6.6 / 7.4, 1024 x 4096
-    4.4 / 5.6 against 5.6 / 5.6, 14336 x 4096 12.6 / 24.1 against 11.7 /
-    13.0; Q8_0 4096 x 4096 7.2 / 8.8 against 7.7 / 7.9, 1024 x 4096 4.4 / 5.8
-    against 5.7 / 5.8.  The row-block kernel stages each wave step's
-    activations as fp16 hi + lo parts (16 KB a wave at batch 8), which caps
-    its occupancy on large matrices."""
-    if n not in (4, 8) or rows * k > 4096 * 4096 or k > 32768:
+    batch 4 / 8: Q4_0 4096 x 4096 5.2 / 7.1 against 6.6 / 7.4, 1024 x 4096
+    4.4 / 5.6 against 5.6 / 5.6, 14336 x 4096 10.8 / 17.8 against 11.7 /
+    13.0, 4096 x 14336 14.1 / 29.8 against 11.5 / 12.7; Q8_0 4096 x 4096
+    7.2 / 8.6 against 7.7 / 7.9, 1024 x 4096 4.4 / 5.9 against 5.7 / 5.8.
+    The row-block kernel stages each wave step's activations as fp16 hi + lo
+    parts (16 KB a wave at batch 8), which caps its occupancy on large
+    matrices."""
+    if n not in (4, 8) or k > 32768:
         return False
-    return fmt == "q4" or n == 4
+    if fmt == "q4" and n == 4:
+        return rows * k <= 4096 * 4096 or k <= 4096
+    return rows * k <= 4096 * 4096 and (fmt == "q4" or n == 4)
 
 
 def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
