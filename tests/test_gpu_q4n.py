@@ -179,3 +179,49 @@ def test_q4n_scaled_and_zero_columns(lib, orc):
     for n in (0, 1, 3):
         assert rel_err(c[:, n], ref[:, n]) <= TOL
     assert np.all(c[:, 2] == 0.0)
+
+
+def test_rowblock_gemms_in_hip_graph_replays(lib, orc):
+    """The one-launch batched GEMMs (fp32 row-block on Q4_0, fp16 row-block on
+    W4A16 packed scales and on IQ4_NL) captured in a HIP graph: every replay,
+    with eager work and synchronisations between replays, gives the eager
+    result bit for bit (they need no memset, workspace or second kernel)."""
+    rows, K, N = 1024, 4096, 8
+    w = synth.q4_0(rows, K, 107)
+    a, off = upload(lib, w)
+    x = torch.from_numpy(synth.x_f32(K * N, 107)).cuda()
+    w4 = synth.w4a16(rows, K, 108)
+    p4, s4, z4 = (torch.from_numpy(np.ascontiguousarray(v).view(np.uint8).reshape(-1).copy()).cuda()
+                  for v in (w4.packed, w4.scales, w4.zeros))
+    szr = torch.empty(w4.scales.size, dtype=torch.int32, device="cuda")
+    lib.call("zt_w4a16_pack_szr", s4.data_ptr(), z4.data_ptr(), rows, K, 128, szr.data_ptr(), stream())
+    wi = synth.iq4nl(rows, K, 109)
+    nblk = rows * K // 32
+    sep = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
+    lib.zt_iq4nl_raw_to_gpu(wi.raw.ctypes.data, nblk, sep.ctypes.data)
+    ai = torch.from_numpy(sep).cuda()
+    x16 = torch.from_numpy(synth.x_f16(K * N, 109).view(np.uint8).copy()).cuda()
+    outs = [torch.empty(rows * N, dtype=torch.float32, device="cuda") for _ in range(3)]
+
+    def launch(s):
+        lib.call("zt_gemm_q4_f32", a.data_ptr(), x.data_ptr(), outs[0].data_ptr(), rows, K, N, off, s)
+        lib.call("zt_gemm_w4a16sz_f32", p4.data_ptr(), szr.data_ptr(), x16.data_ptr(), outs[1].data_ptr(), rows, K,
+                 N, 128, s)
+        lib.call("zt_gemm_iq4nl_f16", ai.data_ptr(), x16.data_ptr(), outs[2].data_ptr(), rows, K, N,
+                 lib.zt_q4_gpu_data_offset(nblk), s)
+
+    launch(stream())
+    torch.cuda.synchronize()
+    eager = [o.cpu().numpy().copy() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch(torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), e.view(np.uint32)), rep
+        launch(stream())  # eager work between replays
+        torch.cuda.synchronize()
