@@ -56,7 +56,12 @@ int zt_abi_version(void);
  * implementation is a "not implemented" stub
  * (internal/gpuapi/rocm_kernels.go:109-111).  A_q4 is the RawBytesGPU
  * layout, data_offset = Q4GPUDataOffset(M*K/32) (tensor/quantized.go:195-198).
- * K % 32 != 0 -> InvalidValue (gemm_q4.cu:169-171).  fp32 activations. */
+ * K % 32 != 0 -> InvalidValue (gemm_q4.cu:169-171).  fp32 activations.
+ * B is [K, N] row-major.  N == 1 needs B 16-byte aligned.  Batches (N > 1)
+ * run one launch per group of 8 or 4 columns when N % 4 == 0 and B is
+ * 16-byte aligned (an MFMA GEMM that reads every weight once a group, no
+ * workspace, the same bits every call), groups of 2 for other even N with B
+ * 8-byte aligned, else one launch per column. */
 int zt_gemm_q4_f32(const void* A_q4, const float* B, float* C, int M, int K, int N, int data_offset,
                    zt_stream_t stream);
 
@@ -113,6 +118,10 @@ void zt_q4_raw_to_gpu(const void* raw, long nblk, void* out);
  * (tensor/iq4_storage.go:36-46): interleaved nibbles, float IQ4NLTable. */
 int zt_gemm_iq4nl_f32(const void* A_iq4, const float* B, float* C, int M, int K, int N, int data_offset,
                       zt_stream_t stream);
+/* fp16 activations: batches of 4 and 8 (12 and 16 up to 2048 rows) with B
+ * 16-byte aligned run one launch with no workspace (the row-block MFMA GEMM),
+ * 12 and 16 past 2048 rows a 16x16x32 MFMA GEMM, one workgroup per 32 rows
+ * over all of K; both store every output once. */
 int zt_gemm_iq4nl_f16(const void* A_iq4, const uint16_t* B, float* C, int M, int K, int N, int data_offset,
                       zt_stream_t stream);
 /* Bit-exact with IQ4NLStorage.Dequantize (tensor/iq4_storage.go:75-89). */
@@ -194,7 +203,11 @@ int zt_dequant_iq3s_f32(const void* src, long src_bytes, float* out, long nelem,
 /* Replaces gemm_q8_f32 (internal/cuda/kernels/gemm_q8.cu:156-182) behind
  * KernelRunner.GemmQ8F32 (internal/gpuapi/kernels.go:79-81; ROCm stub
  * internal/gpuapi/rocm_kernels.go:133-135).  A_q8 is Q8Storage.RawBytes()
- * (36-byte blocks, fp32 scale), 4-byte aligned. */
+ * (36-byte blocks, fp32 scale), 4-byte aligned.  B is [K, N] row-major.
+ * Batches with N % 4 == 0 and B 16-byte aligned run one MFMA launch per
+ * group of 8 or 4 columns (every weight read once a group, no workspace);
+ * other N one launch per column.  The same holds for zt_gemm_q8sep_f32 and
+ * zt_gemm_q8gguf_f32. */
 int zt_gemm_q8_f32(const void* A_q8, const float* B, float* C, int M, int K, int N, zt_stream_t stream);
 
 /* Same product over the separated Q8_0 layout (aligned 32-byte payloads;
