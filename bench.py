@@ -266,6 +266,7 @@ def run_headline(args) -> dict:
     grouped = run_grouped_step(torch, lib, args, mats, step_bytes)
     merged = run_merged_step(torch, lib, args) if args.merged else None
     bitnet = run_bitnet_step(torch, lib, args) if args.merged else None
+    w4step = run_w4a16_step(torch, lib, args) if args.merged else None
 
     # Parity spot check of the last replayed outputs against the oracle.
     from oracle import oracle
@@ -306,6 +307,7 @@ def run_headline(args) -> dict:
         "grouped_projections": grouped,
         "merged_projections": merged,
         "bitnet_layer_step": bitnet,
+        "w4a16_70b_layer_step": w4step,
         "roofline": dom,
         "cpu_baseline": cpu,
     }
@@ -353,6 +355,85 @@ def run_grouped_step(torch, lib, args, mats, step_bytes: int) -> dict:
             "pct_of_peak": round(100 * value / PEAK_GBS, 1), "launches_per_layer": 4,
             "workload": "the headline step, q/k/v and gate/up each one zt_gemm_q4_group_f32 launch over the "
                         "separate uploads"}
+
+
+def run_w4a16_step(torch, lib, args, layers: int = 4) -> dict:
+    """A Llama-3-70B W4A16 decode step at batch 1 (configuration 4's shapes,
+    group 128, fp16 activations, packed (scale, zero) dwords): per layer q,
+    o (8192 x 8192), k, v (1024 x 8192), gate, up (28672 x 8192) and down
+    (8192 x 28672) as rows x K, `layers` distinct layer copies resident (1.7
+    GB at 4, beyond the Infinity Cache).  Timed as 7 zt_gemv_w4a16sz_f32
+    launches a layer, and as 4 with q/k/v and gate/up each one
+    zt_gemv_w4a16sz_group_f32 launch over the same uploads."""
+    from ztensor_amd import _lib as zl
+    from ztensor_amd import synth
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).cuda()
+    s0 = torch.cuda.current_stream().cuda_stream
+    shapes = [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192), ("gate", 28672, 8192),
+              ("up", 28672, 8192), ("down", 8192, 28672)]
+    mats = {}
+    for i, (name, rows, K) in enumerate(shapes):
+        w = synth.w4a16(rows, K, 0x5EED0090 + i)
+        p, sc, z = dev(w.packed), dev(w.scales), dev(w.zeros)
+        szr = torch.empty(w.scales.size, dtype=torch.int32, device="cuda")
+        if lib.zt_w4a16_pack_szr(sc.data_ptr(), z.data_ptr(), rows, K, 128, szr.data_ptr(), s0) != 0:
+            raise RuntimeError("zt_w4a16_pack_szr failed")
+        mats[name] = {"rows": rows, "K": K, "w": [p] + [p.clone() for _ in range(layers - 1)],
+                      "szr": [szr] + [szr.clone() for _ in range(layers - 1)],
+                      "y": [torch.empty(rows, dtype=torch.float32, device="cuda") for _ in range(layers)]}
+        del sc, z
+    xs = {K: dev(synth.x_f16(K, 0x5EED0098 + K)) for K in (8192, 28672)}
+    step_bytes = layers * sum(synth.algorithmic_bytes("w4a16", rows, K, 1) for _, rows, K in shapes)
+
+    def single(name, layer, s):
+        m = mats[name]
+        rc = lib.zt_gemv_w4a16sz_f32(m["w"][layer].data_ptr(), m["szr"][layer].data_ptr(), xs[m["K"]].data_ptr(),
+                                     m["y"][layer].data_ptr(), m["rows"], m["K"], 128, s)
+        if rc != 0:
+            raise RuntimeError(f"zt_gemv_w4a16sz_f32 returned {rc}")
+
+    plan = []
+    for layer in range(layers):
+        for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            if len(names) == 1:
+                plan.append(("one", names[0], layer))
+                continue
+            descs = zl.w4a16_gemv_descs([(mats[n]["w"][layer].data_ptr(), mats[n]["szr"][layer].data_ptr(),
+                                          mats[n]["y"][layer].data_ptr(), mats[n]["rows"]) for n in names])
+            plan.append(("group", descs, len(names), 8192))
+
+    def step_single():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            for name, _, _ in shapes:
+                single(name, layer, s)
+
+    def step_grouped():
+        s = torch.cuda.current_stream().cuda_stream
+        for item in plan:
+            if item[0] == "one":
+                single(item[1], item[2], s)
+            else:
+                _, descs, n, K = item
+                rc = lib.zt_gemv_w4a16sz_group_f32(descs, n, xs[K].data_ptr(), K, 128, s)
+                if rc != 0:
+                    raise RuntimeError(f"zt_gemv_w4a16sz_group_f32 returned {rc}")
+
+    out = {"workload": f"Llama-3-70B decode step, {layers} layers x {{q,o 8192x8192; k,v 1024x8192; gate,up "
+                       "28672x8192; down 8192x28672}} (rows x K) W4A16 GEMVs (group 128, packed scale/zero), batch 1",
+           "bytes_per_step": step_bytes}
+    for key, fn, launches in (("per_gemv", step_single, 7), ("grouped", step_grouped, 4)):
+        g = graph_of(torch, fn)
+        for _ in range(args.warmup):
+            g.replay()
+        ms = time_graph(torch, g, args.steps)
+        out[key] = {"us_per_layer": round(ms * 1e3 / layers, 3), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                    "pct_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 1), "launches_per_layer": launches}
+        log(f"bench: W4A16 70B step, {key}: {ms * 1e3 / layers:.2f} us per layer")
+    del mats
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_bitnet_step(torch, lib, args, layers: int = 32) -> dict:

@@ -272,6 +272,25 @@ int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_
  * (N = 12, 16: K <= 8192); other N -> InvalidValue. */
 int zt_gemm_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* B, float* C, int M, int K, int N,
                         int group_size, zt_stream_t stream);
+/* Grouped batch-1 W4A16: up to ZT_GROUP_MAX matrices on packed (scale,
+ * zero) dwords that read the same fp16 activation vector x[K] (a decode
+ * layer's q/k/v, or gate/up: MatMulW4A16 per projection, compute/
+ * w4a16.go:137-143), one launch.  No reference counterpart: the reference
+ * has no grouped or merged W4A16 matmul (MergeQ4Storage,
+ * tensor/quantized.go:224-242, covers Q4_0 only).  Each y_i is
+ * zt_gemv_w4a16sz_f32 on matrix i, bit for bit.  All matrices share K and
+ * group_size; rows == 0 entries are skipped (their pointers are not read).
+ * n outside 1..ZT_GROUP_MAX, a bad descriptor, a misaligned x or a bad
+ * group size -> InvalidValue.  Allocates nothing. */
+typedef struct zt_w4a16_gemv_desc {
+    const void* W;        /* packed nibbles [rows, K/2], 16-byte aligned */
+    const uint32_t* szr;  /* zt_w4a16_pack_szr dwords [rows][K/group_size] */
+    float* y;             /* rows fp32 outputs */
+    int rows;
+    int reserved;         /* 0 */
+} zt_w4a16_gemv_desc;
+int zt_gemv_w4a16sz_group_f32(const zt_w4a16_gemv_desc* descs, int n, const uint16_t* x, int K, int group_size,
+                              zt_stream_t stream);
 /* Bit-exact with GPTQStorage.Dequantize (tensor/quantized_gptq.go:134-163)
  * and AWQStorage.Dequantize (tensor/quantized_awq.go:118-136). */
 int zt_dequant_w4_f32(const void* W_packed, const uint16_t* scales, const uint16_t* zeros, float* out, long nelem,

@@ -104,6 +104,7 @@ int main(int argc, char** argv) {
     ccall20 iqtws = sym("zt_gemm_iq4nlt_workspace_bytes");
     ccall20 tgrp = sym("zt_ternary_gemv_i8_group");
     ccall20 rd = sym("zt_bench_stream_read");
+    ccall20 w4grp = sym("zt_gemv_w4a16sz_group_f32");
     if (failures) return 1;
 
     /* int return, no arguments */
@@ -144,6 +145,13 @@ int main(int argc, char** argv) {
     expect_int("zt_ternary_gemv_i8_group(no weights)", call(tgrp, (u)&td[0], 1, p, p, 64, 0, 0, 0, 0, 0, 0), 1);
     expect_int("zt_ternary_gemv_i8_group(all empty)", call(tgrp, (u)&td[1], 1, p, p, 64, 0, 0, 0, 0, 0, 0), 0);
     expect_int("zt_ternary_gemv_i8_group(n = 0)", call(tgrp, (u)&td[1], 0, p, p, 64, 0, 0, 0, 0, 0, 0), 1);
+    /* the grouped W4A16 GEMV: host descriptors, a group size that is not a multiple of 32, all empty */
+    struct {
+        u W, szr, y;
+        int rows, reserved;
+    } wd[2] = {{p, p, p, 4, 0}, {0, 0, 0, 0, 0}};
+    expect_int("zt_gemv_w4a16sz_group_f32(group = 48)", call(w4grp, (u)&wd[0], 1, p, 96, 48, 0, 0, 0, 0, 0, 0), 1);
+    expect_int("zt_gemv_w4a16sz_group_f32(all empty)", call(w4grp, (u)&wd[1], 1, p, 128, 128, 0, 0, 0, 0, 0, 0), 0);
     /* the streaming-read measurement kernel: a long size argument, a misaligned buffer, an empty read */
     expect_int("zt_bench_stream_read(p + 8)", call(rd, p + 8, 4096, p, 0, 0, 0, 0, 0, 0, 0, 0), 1);
     expect_int("zt_bench_stream_read(nbytes = -1)", call(rd, p, neg1, p, 0, 0, 0, 0, 0, 0, 0, 0), 1);

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "zt_gemm_w4a16sz_f32": (I, [P, P, P, P, I, I, I, I, P]),
     "zt_bench_stream_read": (I, [P, L, P, P]),
     "zt_ternary_gemv_i8_group": (I, [P, I, P, P, I, P]),
+    "zt_gemv_w4a16sz_group_f32": (I, [P, I, P, I, I, P]),
     "zt_w4a16_tiled_bytes": (L, [I, I]),
     "zt_w4a16_sz_bytes": (L, [I, I, I]),
     "zt_w4a16_tile": (I, [P, P, P, I, I, I, P, P, P]),
@@ -163,6 +164,20 @@ def ternary_gemv_descs(entries) -> C.Array:
     arr = (TernaryGemvDesc * max(1, len(entries)))()
     for i, (w, ws, y, rows) in enumerate(entries):
         arr[i].W, arr[i].w_scale, arr[i].y, arr[i].rows, arr[i].reserved = w, ws, y, rows, 0
+    return arr
+
+
+class W4A16GemvDesc(C.Structure):
+    """zt_w4a16_gemv_desc: one matrix of a grouped batch-1 W4A16 GEMV."""
+
+    _fields_ = [("W", C.c_void_p), ("szr", C.c_void_p), ("y", C.c_void_p), ("rows", C.c_int), ("reserved", C.c_int)]
+
+
+def w4a16_gemv_descs(entries) -> C.Array:
+    """A host array of zt_w4a16_gemv_desc from (W, szr, y, rows) tuples."""
+    arr = (W4A16GemvDesc * max(1, len(entries)))()
+    for i, (w, szr, y, rows) in enumerate(entries):
+        arr[i].W, arr[i].szr, arr[i].y, arr[i].rows, arr[i].reserved = w, szr, y, rows, 0
     return arr
 
 

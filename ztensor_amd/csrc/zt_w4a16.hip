@@ -238,15 +238,12 @@ static void launch_w4a16_quad(int R, dim3 g, dim3 b, hipStream_t st, const uint3
 //  the product's rounding), so no wave waits on an argument load or an
 //  integer division before its scale loads.
 template <int S, int R, bool SZ>
-__global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __restrict__ packed,
-                                                           const void* __restrict__ meta,
-                                                           const uint16_t* __restrict__ zeros,
-                                                           const uint16_t* __restrict__ x, float* __restrict__ y,
-                                                           int rows, int nchunk, int ngroups, float inv_cpg) {
-    __shared__ float red[16 * R];
+__device__ __forceinline__ void w4a16_steps_body(const uint32_t* __restrict__ packed, const void* __restrict__ meta,
+                                                 const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ x,
+                                                 float* __restrict__ y, int rows, int nchunk, int ngroups,
+                                                 float inv_cpg, int row0, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane & 3;
-    const int row0 = blockIdx.x * R;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)packed, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)meta, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, zeros ? 0x7fffffff : 0,
@@ -315,6 +312,64 @@ __global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __res
         }
     }
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S, int R, bool SZ>
+__global__ void __launch_bounds__(1024) w4a16_steps_kernel(const uint32_t* __restrict__ packed,
+                                                           const void* __restrict__ meta,
+                                                           const uint16_t* __restrict__ zeros,
+                                                           const uint16_t* __restrict__ x, float* __restrict__ y,
+                                                           int rows, int nchunk, int ngroups, float inv_cpg) {
+    __shared__ float red[16 * R];
+    w4a16_steps_body<S, R, SZ>(packed, meta, zeros, x, y, rows, nchunk, ngroups, inv_cpg, blockIdx.x * R, red);
+}
+
+// Several W4A16 matrices on packed (scale, zero) dwords that read the same
+// activation vector (q/k/v, or gate/up, of a decode layer) in one launch:
+// workgroups [wg0[i], wg0[i+1]) run matrix i with the body above, so each
+// output is the single-matrix kernel's to the bit (the same steps and waves
+// for one K, and a reduction tree that does not depend on the row count).
+// The activation pointer, the step counts and the table of first workgroups
+// arrive in preloaded argument SGPRs; a workgroup's matrix descriptor is one
+// scalar load.
+struct W4GroupMat {
+    const uint32_t* w;
+    const uint32_t* szr;
+    float* y;
+    int rows;
+    int wg0;
+};
+
+struct W4GroupArgs {
+    int wg0[ZT_GROUP_MAX];  // first workgroup of matrix i (wg0[0] = 0); entries past n hold the grid size
+    int n;
+    int pad[3];
+    W4GroupMat mat[ZT_GROUP_MAX];
+};
+
+template <int S, int R>
+__global__ void __launch_bounds__(1024) w4a16sz_group_kernel(const uint16_t* __restrict__ x, int nchunk, int ngroups,
+                                                             float inv_cpg, const W4GroupArgs g) {
+    __shared__ float red[16 * R];
+    const int b = blockIdx.x;
+    // entries past the last matrix hold the grid size, which no workgroup id reaches,
+    // so the lookup needs only the table (argument dwords 6-13, preloaded)
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < ZT_GROUP_MAX; i++) m += b >= g.wg0[i] ? 1 : 0;
+    const W4GroupMat d = g.mat[m];
+    w4a16_steps_body<S, R, true>(d.w, d.szr, nullptr, x, d.y, d.rows, nchunk, ngroups, inv_cpg, (b - d.wg0) * R, red);
+}
+
+template <int S>
+static void launch_w4a16sz_group(int R, dim3 g, dim3 b, hipStream_t st, const uint16_t* x, int nchunk, int ngroups,
+                                 float inv, const W4GroupArgs& a) {
+    switch (R) {
+        case 8: w4a16sz_group_kernel<S, 8><<<g, b, 0, st>>>(x, nchunk, ngroups, inv, a); break;
+        case 4: w4a16sz_group_kernel<S, 4><<<g, b, 0, st>>>(x, nchunk, ngroups, inv, a); break;
+        case 2: w4a16sz_group_kernel<S, 2><<<g, b, 0, st>>>(x, nchunk, ngroups, inv, a); break;
+        default: w4a16sz_group_kernel<S, 1><<<g, b, 0, st>>>(x, nchunk, ngroups, inv, a); break;
+    }
 }
 
 template <int S, bool SZ>
@@ -813,6 +868,17 @@ ZT_EXPORT int zt_w4a16_pack_szr(const uint16_t* scales, const uint16_t* zeros, i
     return (int)hipGetLastError();
 }
 
+// Steps a wave and waves of the batch-1 kernel on packed scales, for K / 32 chunks.
+static void w4a16sz_steps_shape(int nchunk, int& S, int& nw) {
+    S = nchunk <= 128 ? 1 : nchunk <= 256 ? 2 : 4;
+    nw = ceil_div(nchunk, 16 * S);
+    // whole SIMD sets: 14 waves measured 3% (K = 14336) to 30% (K = 28672) slower than 16
+    if (nw > 12)
+        nw = 16;
+    else if (S == 4)
+        nw = (nw + 3) & ~3;
+}
+
 ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, const uint16_t* x, float* y, int M,
                                   int K, int group_size, hipStream_t stream) {
     if (M < 0 || K < 0 || group_size <= 0 || group_size % 32 != 0 || K % group_size != 0)
@@ -828,13 +894,8 @@ ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, con
     const int nchunk = K / 32;
     // 32-bit buffer offsets; at most 16 waves of 4 steps
     if ((long)M * nchunk * 16 >= 0x7fffffffL || nchunk > 1024) return (int)hipErrorInvalidValue;
-    const int S = nchunk <= 128 ? 1 : nchunk <= 256 ? 2 : 4;
-    int nw = ceil_div(nchunk, 16 * S);
-    // whole SIMD sets: 14 waves measured 3% (K = 14336) to 30% (K = 28672) slower than 16
-    if (nw > 12)
-        nw = 16;
-    else if (S == 4)
-        nw = (nw + 3) & ~3;
+    int S, nw;
+    w4a16sz_steps_shape(nchunk, S, nw);
     const int R = w4a16_steps_rows(M, nw);
     const dim3 g(ceil_div(M, R)), b(nw * kWave);
     const uint32_t* w = static_cast<const uint32_t*>(W_packed);
@@ -845,6 +906,64 @@ ZT_EXPORT int zt_gemv_w4a16sz_f32(const void* W_packed, const uint32_t* szr, con
         launch_w4a16_steps<2, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
     else
         launch_w4a16_steps<4, true>(R, g, b, stream, w, nullptr, nullptr, szr, x, y, M, nchunk, cpg);
+    return (int)hipGetLastError();
+}
+
+ZT_EXPORT int zt_gemv_w4a16sz_group_f32(const zt_w4a16_gemv_desc* descs, int n, const uint16_t* x, int K,
+                                        int group_size, hipStream_t stream) {
+    if (descs == nullptr || n < 1 || n > ZT_GROUP_MAX || K < 0 || group_size <= 0 || group_size % 32 != 0 ||
+        K % group_size != 0)
+        return (int)hipErrorInvalidValue;
+    long total = 0;
+    bool fits = true;
+    const int nchunk = K / 32;
+    for (int i = 0; i < n; i++) {
+        const zt_w4a16_gemv_desc& d = descs[i];
+        if (d.rows < 0 || d.reserved != 0) return (int)hipErrorInvalidValue;
+        if (d.rows == 0) continue;
+        if (d.y == nullptr) return (int)hipErrorInvalidValue;
+        if (K > 0 && (d.W == nullptr || d.szr == nullptr || ((uintptr_t)d.W & 15) || ((uintptr_t)d.szr & 3)))
+            return (int)hipErrorInvalidValue;
+        total += d.rows;
+        fits = fits && (long)d.rows * nchunk * 16 < 0x7fffffffL;
+    }
+    if (total == 0) return (int)hipSuccess;
+    if (K > 0 && (x == nullptr || ((uintptr_t)x & 15))) return (int)hipErrorInvalidValue;
+    if (K == 0 || !fits || nchunk > 1024) {
+        // empty sums, or shapes past the kernel's 32-bit offsets: one call per matrix
+        for (int i = 0; i < n; i++) {
+            const zt_w4a16_gemv_desc& d = descs[i];
+            if (d.rows == 0) continue;
+            const int rc = zt_gemv_w4a16sz_f32(d.W, d.szr, x, d.y, d.rows, K, group_size, stream);
+            if (rc != 0) return rc;
+        }
+        return (int)hipSuccess;
+    }
+    int S, nw;
+    w4a16sz_steps_shape(nchunk, S, nw);
+    // rows a wave from the group's total rows, as for one matrix of that many rows
+    const int R = w4a16_steps_rows((int)min(total, 0x7fffffffL), nw);
+    W4GroupArgs a{};
+    int wg = 0, m = 0;
+    for (int i = 0; i < n; i++) {
+        const zt_w4a16_gemv_desc& d = descs[i];
+        if (d.rows == 0) continue;
+        a.wg0[m] = wg;
+        a.mat[m] = W4GroupMat{static_cast<const uint32_t*>(d.W), d.szr, d.y, d.rows, wg};
+        wg += ceil_div(d.rows, R);
+        m++;
+    }
+    a.n = m;
+    for (int i = m; i < ZT_GROUP_MAX; i++) a.wg0[i] = wg;
+    const int cpg = group_size / 32;
+    const dim3 g(wg), b(nw * kWave);
+    const float inv = 1.0f / (float)cpg;
+    if (S == 1)
+        launch_w4a16sz_group<1>(R, g, b, stream, x, nchunk, nchunk / cpg, inv, a);
+    else if (S == 2)
+        launch_w4a16sz_group<2>(R, g, b, stream, x, nchunk, nchunk / cpg, inv, a);
+    else
+        launch_w4a16sz_group<4>(R, g, b, stream, x, nchunk, nchunk / cpg, inv, a);
     return (int)hipGetLastError();
 }
 
