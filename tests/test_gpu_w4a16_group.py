@@ -102,3 +102,27 @@ def test_w4a16_group_invalid_arguments(lib):
     bad[0].reserved = 1
     assert f(bad, 1, p, 128, 128, stream()) == 1
     assert f(_lib.w4a16_gemv_descs([(0, 0, 0, 0)]), 1, p, 128, 128, stream()) == 0    # all empty
+
+
+def test_engine_gemv_group_w4a16(lib, orc):
+    """ROCmEngine.gemv_group on GPTQ weights with an fp16 activation vector:
+    one grouped launch, each result equal to the engine's own batch-1 matmul
+    of that weight, bit for bit, and within 1e-5 of the oracle."""
+    from ztensor_amd.engine import ROCmEngine
+    from ztensor_amd.storage import GPTQStorage, Tensor
+
+    K = 4096
+    x16 = synth.x_f16(K, 125)
+    xd = torch.from_numpy(x16.view(np.float16).copy()).cuda()
+    eng = ROCmEngine()
+    ts, refs = [], []
+    for i, rows in enumerate([1024, 256, 256]):
+        w = synth.w4a16(rows, K, 126 + i)
+        st = GPTQStorage.from_raw(w.packed.reshape(-1), w.scales.reshape(-1), w.zeros.reshape(-1), rows * K, 128, 4)
+        ts.append(Tensor((rows, K), st))
+        refs.append(orc.w4a16_matmul(w.packed, w.scales, w.zeros, x16, rows, K, 1, 128))
+    outs = eng.gemv_group(ts, xd)
+    for t, y, r in zip(ts, outs, refs):
+        single = eng.matmul(t, xd.reshape(K, 1)).reshape(-1)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), single.cpu().numpy().view(np.uint32))
+        assert rel_err(y.cpu().numpy(), r) <= TOL

@@ -634,19 +634,37 @@ class ROCmEngine:
 
     @_on_engine_stream
     def gemv_group(self, weights: list[Tensor], x: torch.Tensor) -> list[torch.Tensor]:
-        """y_i = W_i @ x for weight Tensors that read the same fp32 activation
-        vector x[K] (a decode layer's q/k/v, or gate/up).  Q4_0 weights run in
-        one zt_gemm_q4_group_f32 launch (up to ZT_GROUP_MAX matrices a
-        launch), each in its own upload: the effect of MergeQ4Storage
-        (tensor/quantized.go:224-242) without re-laying out the storages.
-        Other formats run one GEMV per matrix."""
-        if x.dtype != torch.float32 or x.dim() != 1 or x.device != self.device:
-            raise ValueError("gemv_group takes one fp32 activation vector on the engine's device")
+        """y_i = W_i @ x for weight Tensors that read the same activation
+        vector x[K] (a decode layer's q/k/v, or gate/up).  Q4_0 weights with
+        fp32 x run in one zt_gemm_q4_group_f32 launch (up to ZT_GROUP_MAX
+        matrices a launch), each in its own upload: the effect of
+        MergeQ4Storage (tensor/quantized.go:224-242) without re-laying out
+        the storages.  W4A16 weights (GPTQ/AWQ) of one group size with fp16 x
+        run in one zt_gemv_w4a16sz_group_f32 launch on their packed (scale,
+        zero) dwords, each result the single-matrix GEMV's to the bit.  Other
+        formats run one GEMV per matrix."""
+        if x.dtype not in (torch.float32, torch.float16) or x.dim() != 1 or x.device != self.device:
+            raise ValueError("gemv_group takes one fp32 (fp16 for W4A16) activation vector on the engine's device")
         k = x.shape[0]
         for w in weights:
             if not isinstance(w, Tensor) or w.shape[-1] != k:
                 raise ValueError(f"gemv_group: every weight must be a quantized [rows, {k}] Tensor")
-        if not all(isinstance(w.storage, Q4Storage) for w in weights) or _p(x) % 16 != 0 or k % 32 != 0:
+        if x.dtype == torch.float16 and all(isinstance(w.storage, (GPTQStorage, AWQStorage)) for w in weights):
+            self.upload_weights([w.storage for w in weights])
+            groups = {w.storage.group_size for w in weights}
+            gs = groups.pop() if len(groups) == 1 else 0
+            if (gs and gs % 32 == 0 and k % gs == 0 and k <= 32768 and _p(x) % 16 == 0
+                    and all(getattr(w.storage, "_gpu_szr", None) is not None for w in weights)):
+                outs = [torch.empty(w.shape[-2], dtype=torch.float32, device=self.device) for w in weights]
+                for i0 in range(0, len(weights), _lib.GROUP_MAX):
+                    part = list(zip(weights[i0:i0 + _lib.GROUP_MAX], outs[i0:i0 + _lib.GROUP_MAX]))
+                    descs = _lib.w4a16_gemv_descs([(_p(w.storage.gpu_ptr().tensor), _p(w.storage._gpu_szr), _p(y),
+                                                    w.shape[-2]) for w, y in part])
+                    self.lib.call("zt_gemv_w4a16sz_group_f32", descs, len(part), _p(x), k, gs, self._s)
+                return outs
+            return [self._weight_times(w.storage, w.shape[-2], k, x).reshape(-1) for w in weights]
+        if (x.dtype != torch.float32 or not all(isinstance(w.storage, Q4Storage) for w in weights) or _p(x) % 16 != 0
+                or k % 32 != 0):
             return [self._weight_times(w.storage, w.shape[-2], k, x).reshape(-1) for w in weights]
         self.upload_weights([w.storage for w in weights])
         outs = [torch.empty(w.shape[-2], dtype=torch.float32, device=self.device) for w in weights]
