@@ -115,7 +115,12 @@ void zt_q4_raw_to_gpu(const void* raw, long nblk, void* out);
  * CPUEngine.MatMul falls back to Data() + SGEMM); the device layout is the
  * Q4_0 RawBytesGPU layout applied to IQ4_NL's 18-byte blocks
  * (tensor/iq4_storage.go:12-23).  Decode follows DequantizeIQ4NL
- * (tensor/iq4_storage.go:36-46): interleaved nibbles, float IQ4NLTable. */
+ * (tensor/iq4_storage.go:36-46): interleaved nibbles, float IQ4NLTable.
+ * fp32 activations, B [K, N] row-major.  Batches (N > 1) run one launch per
+ * group of 8 or 4 columns when N % 4 == 0 and B is 16-byte aligned (an MFMA
+ * GEMM that reads every weight once a group, no workspace, the same bits
+ * every call; activations and codebook both enter it as fp16 hi + lo parts,
+ * within about 2^-22 of their fp32 values), else one launch per column. */
 int zt_gemm_iq4nl_f32(const void* A_iq4, const float* B, float* C, int M, int K, int N, int data_offset,
                       zt_stream_t stream);
 /* fp16 activations: batches of 4 and 8 (12 and 16 up to 2048 rows) with B

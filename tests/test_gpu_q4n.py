@@ -90,10 +90,11 @@ def exact64(orc, w, x):
 
 @pytest.mark.parametrize("N", [2, 4, 8])
 @pytest.mark.parametrize("rows,K", [(1, 32), (3, 96), (17, 544), (100, 4096), (65, 4128), (33, 8192), (9, 16384),
-                                    (2049, 1024), (5, 20480), (7, 32768)])
+                                    (2049, 1024), (5, 20480), (7, 32768), (3301, 17024)])
 def test_q4n_ragged(lib, orc, rows, K, N):
     """Partial row sets and workgroups, K not a multiple of a step (512),
-    one, two and four steps a wave: the oracle's result; 2 columns: each
+    one, two and four steps a wave (3301 x 17024: four row sets at four
+    steps, 9 waves, a partial last workgroup): the oracle's result; 2 columns: each
     column the batch-1 kernel's bits; 4 and 8: the same bits on a second
     call."""
     print(f"q4n rows={rows} K={K} N={N}", flush=True)

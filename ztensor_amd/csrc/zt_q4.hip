@@ -67,6 +67,11 @@ __device__ __forceinline__ uint2 iq4_quad_entry(int i) {
                       (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16));
 }
 
+// The IQ4_NL codebook table of the fp32-activation row-block GEMM (rbf_kernel).
+struct Iq4QuadTbl {
+    __device__ static uint2 entry(int i) { return iq4_quad_entry(i); }
+};
+
 // Dot product of one data dword (8 codes, elements in order) with the fp16
 // activation dwords xx[0..3]: hi and lo parts summed separately by
 // v_dot2_f32_f16 and joined as hi + 2^-11 lo.
@@ -1099,6 +1104,13 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         launch_quad<F, XT>(R, dim3(ceil_div(M, R)), dim3(nwaves * kWave), st, sc,
                            reinterpret_cast<const uint32_t*>(data), B, C, M, kb);
         return (int)hipGetLastError();
+    }
+    if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 4) {
+        // fp32 activations, N % 4 == 0: the row-block GEMM, one launch a group of 4 or 8 columns
+        if (rbf_ok<RbFmt::IQ4NL>(N, kb, M, B)) {
+            launch_rbf<RbFmt::IQ4NL, Iq4QuadTbl>(sc, data, B, C, M, kb, N, st);
+            return (int)hipGetLastError();
+        }
     }
     if constexpr (F == Fmt::Q4_0 && sizeof(XT) == 4) {
         if (rbf_ok<RbFmt::Q4_0>(N, kb, M, B)) {

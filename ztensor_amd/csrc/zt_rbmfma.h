@@ -65,13 +65,26 @@ struct RbO4Layout {
 // LDS byte offset of the transposing read of the MFMA step whose K
 // positions are kbase + {0, 2, 1, 3}, n-set js, in that layout.
 template <int NB>
-__device__ __forceinline__ int rb_o4_tr_offset(int lane, int kbase, int js) {
+__device__ __forceinline__ int rb_o4_tr_offset_at(int lane, int k, int js) {
     using Lay = RbO4Layout<NB>;
-    const int e = (lane >> 2) & 3, q = lane & 3, c = 4 * (lane >> 4) + q;
-    const int k = kbase + (((e & 1) << 1) | (e >> 1));  // {0, 2, 1, 3}
+    const int c = 4 * (lane >> 4) + (lane & 3);
     const int b = 2 * Lay::N * k + 8 * js;
     const int p = (b / 16 + Lay::sig(c)) % Lay::PPC;
     return (c * Lay::PPC + p) * 16 + (b & 8);
+}
+
+template <int NB>
+__device__ __forceinline__ int rb_o4_tr_offset(int lane, int kbase, int js) {
+    const int e = (lane >> 2) & 3;
+    return rb_o4_tr_offset_at<NB>(lane, kbase + (((e & 1) << 1) | (e >> 1)), js);  // {0, 2, 1, 3}
+}
+
+// The natural-order reads of IQ4_NL's MFMA step v: K positions 4v + {0, 1,
+// 2, 3}, the same 16 rows as the offset-{0,2,1,3} reads of that step, so
+// again on 16 distinct bank slots.
+template <int NB>
+__device__ __forceinline__ int rb_o4_tr_offset_nat(int lane, int kbase, int js) {
+    return rb_o4_tr_offset_at<NB>(lane, kbase + ((lane >> 2) & 3), js);
 }
 
 // Issues the direct loads of one step's activations (global bytes
@@ -208,21 +221,36 @@ __device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* 
 //    dword s/2 (K positions 4(s/2) + 16(s%2) + {0, 2, 1, 3}) as
 //    2^14 + 2^10 q;
 //  * Q8_0: bytes (0, 2) and (1, 3) of dword s (K positions 4s + {0, 2, 1,
-//    3}) as 2^15 + 2^7 u, u = q + 128 (q XOR 0x80).
+//    3}) as 2^15 + 2^7 u, u = q + 128 (q XOR 0x80);
+//  * IQ4_NL: 8 steps a block, step v on elements 4v .. 4v+3 (data bytes
+//    2v and 2v+1, low nibble first) in natural K order; a 2 KB LDS table
+//    gives each byte (T_hi[low], T_hi[high], T_lo[low], T_lo[high]), the
+//    fp32 codebook as fp16 hi + lo (within 2^-22 per entry), so the two
+//    entries' first dwords are the step's T_hi operand and their second
+//    dwords its T_lo operand.  Three MFMAs a step, x_hi T_hi + x_lo T_hi +
+//    x_hi T_lo, leave out x_lo T_lo, at most 2^-22 |x T| a product; no
+//    offset, so no X chain, and y += d D / c.
 // Per block, n-set and step: D = sum (hi + lo) b (hi and lo MFMAs into one
 // chain) and X = sum (hi + lo) 2^14 (B = 2^14, shared by the row sets), so
 // sum(q x) c = 2^-10 (D - 1.5 X) for Q4_0 (q - 8) and 2^-7 (D - 3 X) for
 // Q8_0, and the block's scale d takes it: y += d 2^-e (D/c - o X/c).  Every
 // output is summed in wave and then wave order and stored once (rb_finish).
-enum class RbFmt { Q4_0, Q8_RAW, Q8_SEP, Q8_SEP16 };
+enum class RbFmt { Q4_0, Q8_RAW, Q8_SEP, Q8_SEP16, IQ4NL };
 
 template <RbFmt F>
 struct RbFmtInfo {
-    static constexpr bool Q4 = F == RbFmt::Q4_0, RAW = F == RbFmt::Q8_RAW;
+    static constexpr bool IQ = F == RbFmt::IQ4NL;                                // codebook table, no offset
+    static constexpr bool Q4 = F == RbFmt::Q4_0 || IQ, RAW = F == RbFmt::Q8_RAW;  // 16-byte blocks
     static constexpr int WD = Q4 ? 4 : 8;                                        // weight dwords a block
     static constexpr int WL = Q4 ? 1 : RAW ? 4 : 2;                             // weight loads a block
     static constexpr int BB = Q4 ? 16 : RAW ? 36 : 32;                           // data bytes a block
     static constexpr int SBY = RAW ? 36 : (Q4 || F == RbFmt::Q8_SEP16) ? 2 : 4;  // scale stride
+    static constexpr int TBL = IQ ? 2048 : 0;                                    // LDS table bytes
+};
+
+// No codebook: the block formats whose values the B operand encodes directly.
+struct RbNoTable {
+    __device__ static uint2 entry(int) { return make_uint2(0u, 0u); }
 };
 
 template <int NB>
@@ -238,11 +266,15 @@ __device__ __forceinline__ void rbf_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr
 
 // scales: fp16 or fp32 scales (Q8_RAW: the 36-byte blocks); data: 16- or
 // 32-byte blocks (Q8_RAW: the 36-byte blocks again).
-// 8-column groups run at most 8 waves a workgroup, and their 16 KB of LDS a
-// wave allow no more than 8 waves a CU anyway, so their launch bound of 512
-// threads costs no occupancy and leaves up to 256 VGPRs a lane.
-template <RbFmt F, int NB, int R, int S>
-__global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
+// Threads a workgroup may have.  8-column groups run at most 8 waves (their
+// 16 KB of LDS a wave allow no more than 8 waves a CU anyway), so 512
+// threads cost no occupancy and leave up to 256 VGPRs a lane; 4 row sets at
+// four steps a wave (16-byte blocks, K <= 20480) run at most 10 waves and
+// need about 170 VGPRs.
+constexpr int rbf_bound(int NB, int R, int S) { return NB == 2 ? 512 : R == 4 && S == 4 ? 640 : 1024; }
+
+template <RbFmt F, int NB, int R, int S, class Tbl = RbNoTable>
+__global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
                                                    const float* __restrict__ x, float* __restrict__ y, int rows,
                                                    int kb, int ldx, int n0) {
     using Info = RbFmtInfo<F>;
@@ -251,7 +283,8 @@ __global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int blk = lane >> 2, j = lane & 3;
-    char* xs = smem + wave * Lay::STEP;
+    char* regions = smem + Info::TBL;  // IQ4_NL: the codebook table first
+    char* xs = regions + wave * Lay::STEP;
     const int row0 = blockIdx.x * 4 * R;
     // rows past M and K read zeros: the buffers end at row M and at K
     const __amdgpu_buffer_rsrc_t rw =
@@ -296,18 +329,23 @@ __global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Info::IQ) {
+        uint2* tbl = reinterpret_cast<uint2*>(smem);
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = Tbl::entry(i);
+        // the table is visible to the workgroup; the loads stay in flight
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; i++) acc[i] = 0.0f;
     const half4v ones = (half4v){16384, 16384, 16384, 16384};  // 2^14
     uint32_t bmask = Info::Q4 ? 0x03C003C0u : 0x03FC03FCu, bexp = Info::Q4 ? 0x74007400u : 0x78007800u;
     asm volatile("" : "+v"(bmask), "+s"(bexp));  // the mask in a VGPR, the exponent in an SGPR (v_and_or_b32)
-    constexpr float kSm = Info::Q4 ? 0x1p-10f : 0x1p-7f, kOff = Info::Q4 ? 1.5f : 3.0f;
+    constexpr float kSm = Info::IQ ? 1.0f : Info::Q4 ? 0x1p-10f : 0x1p-7f, kOff = Info::Q4 ? 1.5f : 3.0f;
 #pragma unroll
     for (int t = 0; t < S; t++) {
         if (t > 0) {
-            rbf_load_x<NB>(rx, xr, step0 + t, ldx, n0, lane);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's activations, issued a step ahead
         } else {
             // the activations only: the weight and scale loads after them may be outstanding
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S * R * (Info::WL + 1)) : "memory");
@@ -354,6 +392,9 @@ __global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        // the registers are free again: the next step's activations load
+        // while this step's MFMAs run
+        if (t + 1 < S) rbf_load_x<NB>(rx, xr, step0 + t + 1, ldx, n0, lane);
         float4v d[R][NB], dx[NB];
 #pragma unroll
         for (int js = 0; js < NB; js++) {
@@ -361,40 +402,67 @@ __global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t
 #pragma unroll
             for (int r = 0; r < R; r++) d[r][js] = (float4v){0.f, 0.f, 0.f, 0.f};
         }
+        if constexpr (Info::IQ) {
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const int kbase = Info::Q4 ? 4 * (s >> 1) + 16 * (s & 1) : 4 * s;
-            half4v xa[2 * NB];
+            for (int v = 0; v < 8; v++) {
+                half4v xa[2 * NB];
 #pragma unroll
-            for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_o4_tr_offset<2 * NB>(lane, kbase, js));
-            half4v bv[R];
+                for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_o4_tr_offset_nat<2 * NB>(lane, 4 * v, js));
+                half4v bh[R], bl[R];
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                uint32_t a, b;
-                if constexpr (Info::Q4) {
-                    const uint32_t q = w[t][r][s >> 1];
-                    a = (s & 1) ? q << 2 : q << 6;  // bytes 0, 2: low or high nibbles
-                    b = (s & 1) ? q >> 6 : q >> 2;  // bytes 1, 3
-                } else {
-                    const uint32_t u = w[t][r][s] ^ 0x80808080u;  // q + 128
-                    a = u << 2;                                  // bytes 0, 2
-                    b = u >> 6;                                  // bytes 1, 3
+                for (int r = 0; r < R; r++) {
+                    const uint32_t q = w[t][r][v >> 1] >> (16 * (v & 1));  // bytes 2v, 2v + 1 in bits 0-15
+                    const uint2 e0 = *reinterpret_cast<const uint2*>(smem + ((q << 3) & 0x7F8u));
+                    const uint2 e1 = *reinterpret_cast<const uint2*>(smem + ((q >> 5) & 0x7F8u));
+                    bh[r] = __builtin_bit_cast(half4v, make_uint2(e0.x, e1.x));  // T_hi of elements 4v .. 4v+3
+                    bl[r] = __builtin_bit_cast(half4v, make_uint2(e0.y, e1.y));  // T_lo
                 }
-                bv[r] = __builtin_bit_cast(half4v, (uint2){(a & bmask) | bexp, (b & bmask) | bexp});
+                // x_hi T_hi, x_lo T_hi, x_hi T_lo: consecutive MFMAs of one chain are R NB apart
+#pragma unroll
+                for (int tm = 0; tm < 3; tm++)
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+#pragma unroll
+                        for (int js = 0; js < NB; js++)
+                            d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[(tm == 1 ? NB : 0) + js],
+                                                                         tm == 2 ? bl[r] : bh[r], d[r][js], 0, 0, 0);
             }
-            // hi parts, then lo parts: consecutive MFMAs of one chain are R NB + NB apart
+        } else {
 #pragma unroll
-            for (int hl = 0; hl < 2; hl++) {
+            for (int s = 0; s < 8; s++) {
+                const int kbase = Info::Q4 ? 4 * (s >> 1) + 16 * (s & 1) : 4 * s;
+                half4v xa[2 * NB];
 #pragma unroll
-                for (int js = 0; js < NB; js++)
-                    dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], ones, dx[js], 0, 0, 0);
+                for (int js = 0; js < 2 * NB; js++) xa[js] = rb_tr_read(xs, rb_o4_tr_offset<2 * NB>(lane, kbase, js));
+                half4v bv[R];
 #pragma unroll
-                for (int r = 0; r < R; r++)
+                for (int r = 0; r < R; r++) {
+                    uint32_t a, b;
+                    if constexpr (Info::Q4) {
+                        const uint32_t q = w[t][r][s >> 1];
+                        a = (s & 1) ? q << 2 : q << 6;  // bytes 0, 2: low or high nibbles
+                        b = (s & 1) ? q >> 6 : q >> 2;  // bytes 1, 3
+                    } else {
+                        const uint32_t u = w[t][r][s] ^ 0x80808080u;  // q + 128
+                        a = u << 2;                                  // bytes 0, 2
+                        b = u >> 6;                                  // bytes 1, 3
+                    }
+                    bv[r] = __builtin_bit_cast(half4v, (uint2){(a & bmask) | bexp, (b & bmask) | bexp});
+                }
+                // hi parts, then lo parts: consecutive MFMAs of one chain are R NB + NB apart
+#pragma unroll
+                for (int hl = 0; hl < 2; hl++) {
 #pragma unroll
                     for (int js = 0; js < NB; js++)
-                        d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], bv[r], d[r][js], 0, 0, 0);
+                        dx[js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], ones, dx[js], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+#pragma unroll
+                        for (int js = 0; js < NB; js++)
+                            d[r][js] = __builtin_amdgcn_mfma_f32_4x4x4f16(xa[hl * NB + js], bv[r], d[r][js], 0, 0, 0);
+                }
             }
-        }
+        }  // Q4_0 / Q8_0 steps
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float dv = (Info::SBY == 2 ? h2f((uint16_t)sc[t][r]) : __uint_as_float(sc[t][r])) * kSm;
@@ -403,36 +471,40 @@ __global__ void __launch_bounds__(NB == 2 ? 512 : 1024) rbf_kernel(const uint8_t
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     float& a = acc[(r * NB + js) * 4 + v];
-                    a = __builtin_fmaf(dv, __builtin_fmaf(d[r][js][v], ic, -kOff * dx[js][v] * ic), a);
+                    if constexpr (Info::IQ)
+                        a = __builtin_fmaf(dv, d[r][js][v] * ic, a);
+                    else
+                        a = __builtin_fmaf(dv, __builtin_fmaf(d[r][js][v], ic, -kOff * dx[js][v] * ic), a);
                 }
         }
     }
     // waves split K: each wave leaves its sums in its own LDS region, then the
     // workgroup adds them in wave order
-    rb_finish<NB, R>(acc, smem, Lay::STEP, xs, y, row0, rows, ldx, n0);
+    rb_finish<NB, R>(acc, regions, Lay::STEP, xs, y, row0, rows, ldx, n0);
 }
 
-template <RbFmt F, int NB, int R, int S>
+template <RbFmt F, int NB, int R, int S, class Tbl>
 static void launch_rbf_t(dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data, const float* x,
                          float* y, int rows, int kb, int ldx, int n0) {
-    const size_t lds = (size_t)nw * RbO4Layout<2 * NB>::STEP;
+    const size_t lds = RbFmtInfo<F>::TBL + (size_t)nw * RbO4Layout<2 * NB>::STEP;
     if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
         static const bool raised = [] {
-            return hipFuncSetAttribute(reinterpret_cast<const void*>(&rbf_kernel<F, NB, R, S>),
+            return hipFuncSetAttribute(reinterpret_cast<const void*>(&rbf_kernel<F, NB, R, S, Tbl>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
         }();
         (void)raised;
     }
-    rbf_kernel<F, NB, R, S><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
+    rbf_kernel<F, NB, R, S, Tbl><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
 }
 
-template <RbFmt F, int NB>
+template <RbFmt F, int NB, class Tbl>
 static void launch_rbf_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data,
                          const float* x, float* y, int rows, int kb, int ldx, int n0) {
 #define ZT_RB(RR, SS) \
-    if (R == RR && S == SS) return launch_rbf_t<F, NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
+    if (R == RR && S == SS) return launch_rbf_t<F, NB, RR, SS, Tbl>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
     ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1) ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4)
     if constexpr (RbFmtInfo<F>::Q4) { ZT_RB(8, 1) ZT_RB(4, 2) }
+    if constexpr (RbFmtInfo<F>::Q4 && NB == 1) { ZT_RB(4, 4) }
 #undef ZT_RB
 }
 
@@ -447,31 +519,35 @@ static bool rbf_ok(int N, int kb, long M, const void* B) {
 // One launch per column group: K in steps of 16 blocks over up to 16 waves
 // (8 for 8-column groups, whose hi/lo activations take 16 KB of LDS a wave),
 // 1, 2 or 4 steps a wave, and row sets doubled while about 200 workgroups
-// remain: up to 8 for Q4_0 at one step a wave, 4 at two, 2 at four steps
-// and for Q8_0's 32-byte blocks past one step (beyond that the kernel
-// spills registers).  Columns go in groups of 8 up to K = 8192 (Q4_0) or
-// 32768 (Q8_0), else of 4.  Measured (us, batch 4 / 8): Q4_0 14336 x 4096
-// 10.8 / 17.8 with 8 row sets against 12.6 / 24.1 with 4; at 4096 x 14336
-// two 4-column launches beat one 8-column launch at four steps a wave
+// remain: up to 8 for the 16-byte blocks (Q4_0, IQ4_NL) at one step a wave,
+// 4 at two, and at four when that takes no more than 10 waves (K <= 20480),
+// else 2; 2 for Q8_0's 32-byte blocks past one step (beyond that the kernel
+// spills registers).  Columns go in groups of 8 up to K = 8192 (16-byte
+// blocks) or 16384 (Q8_0), else of 4.  Measured (us, batch 4 / 8): Q4_0
+// 14336 x 4096 10.8 / 17.8 with 8 row sets against 12.6 / 24.1 with 4;
+// IQ4_NL 3584 x 18944 24.1 / 48.9 with 4 row sets at four steps against
+// 32.2 / 65.7 with 2 (that launch's 10 waves and 82 KB of LDS hold one
+// workgroup a CU, so halving the workgroups halves the rounds); at 4096 x
+// 14336 two 4-column launches beat one 8-column launch at four steps a wave
 // (29.8 against 31.6), for Q8_0 the 8-column launch wins (38.5 against 55.0).
-template <RbFmt F>
+template <RbFmt F, class Tbl = RbNoTable>
 static void launch_rbf(const void* scales, const void* data, const void* B, float* C, int M, int kb, int N,
                        hipStream_t st) {
     const uint8_t* sc = static_cast<const uint8_t*>(scales);
     const uint8_t* dt = static_cast<const uint8_t*>(data);
     const float* x = static_cast<const float*>(B);
-    constexpr bool Q4 = RbFmtInfo<F>::Q4;
+    constexpr bool Q4 = RbFmtInfo<F>::Q4;  // 16-byte blocks: Q4_0 and IQ4_NL
     for (int n0 = 0; n0 < N;) {
         const int nc = (N - n0 >= 8 && kb <= (Q4 ? 8 * 16 * 2 : 8 * 16 * 4)) ? 8 : 4;
         const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
         const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
         const int nw = ceil_div(steps, S);
-        const int rmax = S == 4 || (S == 2 && !Q4) ? 2 : (S == 1 && Q4) ? 8 : 4;
+        const int rmax = S == 4 ? (Q4 && nc == 4 && nw <= 10 ? 4 : 2) : (S == 2 && !Q4) ? 2 : (S == 1 && Q4) ? 8 : 4;
         int R = 1;
         while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
         const dim3 g(ceil_div(M, 4 * R));
-        if (nc == 8) launch_rbf_n<F, 2>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
-        else launch_rbf_n<F, 1>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
+        if (nc == 8) launch_rbf_n<F, 2, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
+        else launch_rbf_n<F, 1, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
         n0 += nc;
     }
 }
