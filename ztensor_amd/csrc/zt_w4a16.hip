@@ -439,8 +439,14 @@ __device__ __forceinline__ half4v rb_w4_operand(uint32_t q, int odd, uint32_t ma
 
 // SZ: meta is the packed (scale | zero << 16) dwords of zt_w4a16_pack_szr;
 // else meta is the fp16 scales and zeros the fp16 zeros (NULL: 8).
+// Threads a workgroup may have: 4 row sets of 8 columns at two or four steps
+// a wave run at most 8 waves (the launch shape keeps them there), so 512
+// threads leave them up to 256 VGPRs (the 1024-thread bound spills the
+// two-step form); everything else may take 16 waves.
+constexpr int w4rb_bound(int NB, int R, int S) { return NB == 2 && R == 4 && S >= 2 ? 512 : 1024; }
+
 template <int NB, int R, int S, bool SZ>
-__global__ void __launch_bounds__(1024) w4a16_rb_kernel(const uint32_t* __restrict__ packed,
+__global__ void __launch_bounds__(w4rb_bound(NB, R, S)) w4a16_rb_kernel(const uint32_t* __restrict__ packed,
                                                         const void* __restrict__ meta,
                                                         const uint16_t* __restrict__ zeros,
                                                         const uint16_t* __restrict__ x, float* __restrict__ y,
@@ -587,25 +593,34 @@ static void launch_w4a16_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, cons
         ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1)
         ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(4, 2)
         ZT_RB(1, 4) ZT_RB(2, 4)
-    } else {
+    }
+    if constexpr (NB == 2) {
+        ZT_RB(4, 4)
+    } else if constexpr (NB > 2) {
         ZT_RB(1, 1) ZT_RB(1, 2)
     }
 #undef ZT_RB
 }
 
 // Launch shape of the row-block GEMM: S steps a wave and up to 16 waves
-// splitting K (8 for N >= 12, whose activation blocks take 12-16 KB of LDS a
-// wave), and R row sets a workgroup (up to 4) chosen so that the grid holds
-// about 512 workgroups, within 128 VGPRs (N >= 12: one row set).
+// splitting K (8 for N >= 8: 8-column activation blocks take 8 KB of LDS a
+// wave, so 8 waves let two or more workgroups share a CU; N >= 12 also caps
+// VGPRs), and R row sets a workgroup (up to 4) doubled while about 256
+// workgroups remain; N >= 12: one row set.  Measured on the packed-scale
+// kernel (us, default against the former >= 512 workgroups and 16 waves at
+// N = 8): batch 8 4096 x 14336 (rows x K) 12.18 against 15.20, 28672 x
+// 8192 37.97 against 42.83, 8192 x 8192 13.16 against 13.68, 4096 x 4096
+// 4.92 against 5.45; batch 4 4096 x 14336 9.97 against 10.38, 4096 x 4096
+// 4.38 against 4.31.  8 row sets were slower wherever the grid allows them.
 static void w4a16_rb_shape(int M, int N, int nchunk, int& R, int& S, int& nw) {
-    const int steps = ceil_div(nchunk, 16), wmax = N >= 12 ? 8 : 16;
+    const int steps = ceil_div(nchunk, 16), wmax = N >= 8 ? 8 : 16;
     S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
     nw = ceil_div(steps, S);
-    // (8 row sets measured slower than 4 wherever the grid allows both: 10.35 / 10.1 us at 8192 x 8192,
-    // 32.1 / 28.3 us at 28672 x 8192, batch 4)
-    const int rmax = N >= 12 ? 1 : min(min(8 / S, 32 / N), 4);
+    // four steps a wave on more than 8 waves (N = 8: K > 16384) keeps 2 row
+    // sets: 4 need the 512-thread bound
+    const int rmax = N >= 12 ? 1 : (S == 4 && (nw > 8 || N == 4)) ? 2 : 4;
     R = 1;
-    while (R < rmax && ceil_div(M, 8 * R) >= 512) R *= 2;
+    while (R < rmax && ceil_div(M, 8 * R) >= 256) R *= 2;
     // few rows (one row set a workgroup) and K of 16 steps or more: two steps a
     // wave on half the waves (1024 x 8192, batch 4 / 8: 3.56 / 4.06 us against
     // 3.73 / 4.74 at one step on 16 waves)
