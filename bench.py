@@ -585,6 +585,7 @@ SUITE = {
     # (gemm_bench_test.go:159-165, batch = rows)
     "int4": ("int4", [(4096, 4096), (14336, 4096)], [1, 4]),
     "int4_rmul": ("int4_rmul", [(4096, 4096)], [1, 4]),
+    "int4_rmul_shapes": ("int4_rmul", [(4096, 4096), (14336, 4096), (4096, 14336)], [1, 2, 3, 4]),
     "int8": ("int8", [(4096, 4096), (4096, 14336)], [1, 4]),
     "int4_gemm": ("int4", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int4_rmul_gemm": ("int4_rmul", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),

@@ -102,6 +102,10 @@ RMUL_CASES = [  # batch, in, out, group_size
     (1, 4096, 4096, 32), (4, 4096, 4096, 128), (3, 1000, 1002, 7), (2, 64, 30, 16), (1, 1, 2, 1),
     (5, 512, 256, 32), (64, 1024, 1000, 32), (17, 33, 66, 5),
     (3, 100, 272, 16), (2, 1000, 4112, 48), (4, 130, 32, 32), (1, 63, 16, 16),
+    # the 16-byte-load kernel (out % 32 == 0, group_size % 32 == 0): partial column blocks, K not a
+    # multiple of the 8 waves' rows, batches 1-4
+    (2, 1000, 4160, 64), (3, 2048, 96, 32), (1, 8191, 1024, 256), (4, 64, 4096, 32), (1, 14336, 4096, 32),
+    (2, 4096, 14336, 128),
 ]
 
 
@@ -112,6 +116,16 @@ def test_int4_rmul(lib, orc, batch, inf, outf, gs):
     x = synth.x_f32(batch * inf, 401 + batch).reshape(batch, inf)
     y = run_rmul(lib, w, x, batch, inf, outf, gs)
     assert rel_err(y, orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, batch, inf, outf, gs)) <= TOL
+
+
+def test_int4_rmul_repeat_bit_identical(lib):
+    """The X W kernels sum in a fixed order: two calls give the same bits."""
+    for batch, inf, outf, gs in [(1, 4096, 4096, 32), (4, 2048, 1024, 128), (3, 1000, 1002, 7)]:
+        w = synth.int4(inf, outf, gs, 402 + batch, zero_max=15)
+        x = synth.x_f32(batch * inf, 403 + batch).reshape(batch, inf)
+        a = run_rmul(lib, w, x, batch, inf, outf, gs)
+        b = run_rmul(lib, w, x, batch, inf, outf, gs)
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), (batch, inf, outf)
 
 
 INT8_CASES = [  # M, K, N

@@ -23,6 +23,15 @@ namespace zt {
 
 constexpr int kWave = 64;
 
+// Workgroups of a 1-D grid of G go to the 8 XCDs in turn (workgroup b to XCD
+// b mod 8).  This maps b to a logical index so that each XCD takes one
+// contiguous range of logical indices (the first G mod 8 XCDs one more):
+// neighbouring logical workgroups then share one XCD's L2.
+__device__ __forceinline__ int xcd_contiguous(int b, int G) {
+    const int x = b & 7, i = b >> 3, per = G >> 3, rem = G & 7;
+    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 // fp16 bits -> fp32, exact widening (v_cvt_f32_f16; fp16 denormals are kept).
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));

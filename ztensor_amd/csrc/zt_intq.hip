@@ -14,8 +14,9 @@
 //
 // Kernels:
 //  * batches of 1-4 on aligned shapes: VALU kernels that stream the weights
-//    once (intq_gemv_kernel for A B, int4_rmul_valu_kernel for X W, the
-//    latter for out % 16 == 0 and group_size % 16 == 0);
+//    once (intq_gemv_kernel for A B; for X W int4_rmul_v16_kernel, 16-byte
+//    loads, for out % 32 == 0, group_size % 32 == 0 and in <= 8192, else
+//    int4_rmul_valu_kernel for out % 16 == 0 and group_size % 16 == 0);
 //  * wider batches of A B with K % 32 == 0 (int4: group_size % 32 == 0) and
 //    an even N: intq_bf16_kernel, bf16 MFMA on exact three-part activations;
 //  * every other call: intq_mfma_kernel, an LDS-tiled fp32 MFMA GEMM
@@ -288,7 +289,10 @@ __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __r
     __shared__ float red[16][LPR][16 * NB];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int cl = lane % LPR, ph = lane / LPR;
-    const int col = blockIdx.x * 16 * LPR + 16 * cl;  // first of the lane's 16 columns
+    // neighbouring column blocks read the same weight, scale and zero lines:
+    // keep them on one XCD (one L2)
+    const int bx = xcd_contiguous(blockIdx.x, (Nout + 16 * LPR - 1) / (16 * LPR));
+    const int col = bx * 16 * LPR + 16 * cl;  // first of the lane's 16 columns
     const bool colok = col < Nout;
     const int cc = colok ? col : 0;
     const int g = cc / gs;
@@ -349,7 +353,7 @@ __global__ void __launch_bounds__(1024) int4_rmul_valu_kernel(const uint8_t* __r
     // outputs (b, column) over the workgroup's threads, the waves summed in order
     for (int t = threadIdx.x; t < 16 * LPR * NB; t += blockDim.x) {
         const int b = t / (16 * LPR), c = t % (16 * LPR);
-        const int n = blockIdx.x * 16 * LPR + c;
+        const int n = bx * 16 * LPR + c;
         if (n < Nout) {
             float sum = 0.0f;
             for (int w = 0; w < nwaves; w++) sum += red[w][c >> 4][16 * b + (c & 15)];
@@ -369,6 +373,122 @@ static void launch_int4_rmul_valu(hipStream_t st, const uint8_t* W, const float*
     // (4 rows a lane per pass, 2 at batch 4 to stay within 128 VGPRs)
     int4_rmul_valu_kernel<NB, NB == 4 ? 2 : 4, 1><<<dim3(ceil_div(Nout, 16)), dim3(nw * kWave), 0, st>>>(
         W, X, C, s, z, K, Nout, gs, ng);
+}
+
+// X W, batch 1-4, out % 32 == 0 and group_size % 32 == 0: the same sum with
+// 16-byte weight loads.  A lane owns 32 output columns (one 16-byte piece of
+// a row, all in one group), the 64 lanes of a wave take K rows in turn, and
+// a workgroup of NW waves owns 32 columns and all of K.  Per row the lane
+// forms t = X[b, k] * scale and adds t * u for u = v + 8 in [0, 15]: the
+// nibble enters v_fma_mix as an fp16 subnormal u 2^-24 against t 2^24, so
+// the product is t u exactly and each weight costs one FMA and half a mask;
+// sum t (8 + zero) goes to one more accumulator and comes off at the end:
+// C = sum t u - sum t (8 + zero) = sum t (v - zero).  Against the reference
+// (float(v - zero) * scale first, then times X, one sum) each product
+// differs by one fp32 rounding, and the two sums carry sum t u's magnitude,
+// about twice sum |t (v - zero)| for nibbles spread over [0, 15].  Each
+// wave sums its 64 lanes by halving exchanges (wave_reduce_rows), and the
+// workgroup adds the waves in wave order: the same bits every call.
+template <int NB, int U, int NW>
+__global__ void __launch_bounds__(NW * 64) int4_rmul_v16_kernel(const uint8_t* __restrict__ W,
+                                                                const float* __restrict__ X, float* __restrict__ C,
+                                                                const float* __restrict__ scales,
+                                                                const uint8_t* __restrict__ zeros, int K, int Nout,
+                                                                int gs, int ng) {
+    __shared__ float red[NW][NB][33];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bx = xcd_contiguous(blockIdx.x, Nout / 32);
+    const int col = bx * 32, g = col / gs;
+    const uint32_t rowbytes = (uint32_t)Nout / 2u;
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)((uint32_t)K * rowbytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, K * ng * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, K * ng, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, NB * K * 4, 0x00020000);
+    const int kw = (K + NW - 1) / NW;
+    const int kbeg = wave * kw, kend = min(K, kbeg + kw);
+    float acc[NB][32], ctr[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        ctr[b] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) acc[b][j] = 0.0f;
+    }
+    for (int k0 = kbeg + lane; k0 < kend; k0 += 64 * U) {
+        u32x4 w[U];
+        float sv[U], xv[U][NB];
+        uint32_t zv[U];
+        // rows past the wave's range read zeros (out-of-range buffer offsets), so t = 0
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + 64 * u;
+            const bool ok = k < kend;
+            w[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (uint32_t)k * rowbytes + (uint32_t)col / 2u : 0x80000000u,
+                                                         0, 2);  // nontemporal
+            sv[u] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)(k * ng + g) * 4u : 0x80000000u, 0, 0));
+            zv[u] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? (uint32_t)(k * ng + g) : 0x80000000u, 0, 0);
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+                xv[u][b] = __uint_as_float(
+                    __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? (uint32_t)(b * K + k) * 4u : 0x80000000u, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float tp[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const float t = xv[u][b] * sv[u];
+                ctr[b] = __builtin_fmaf(t, (float)(8u + (zv[u] & 0xffu)), ctr[b]);
+                tp[b] = t * 16777216.0f;  // 2^24
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t d = w[u][i] ^ 0x88888888u;  // u = v + 8 in every nibble
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // nibbles e and e + 4 of the dword: elements 8i + e and 8i + e + 4
+                    const half2v m = as_half2((d >> (4 * e)) & 0x000F000Fu);
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        acc[b][8 * i + e] = __builtin_fmaf((float)m.x, tp[b], acc[b][8 * i + e]);
+                        acc[b][8 * i + e + 4] = __builtin_fmaf((float)m.y, tp[b], acc[b][8 * i + e + 4]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        wave_reduce_rows<32>(acc[b]);
+        float c = ctr[b];
+        c = single_step<32>(c);
+        c = single_step<16>(c);
+        c = single_step<8>(c);
+        c = single_step<4>(c);
+        c = single_step<2>(c);
+        c = single_step<1>(c);
+        if (is_row_writer<32>(lane)) red[wave][b][row_of_lane<32>(lane)] = acc[b][0];
+        if (lane == 0) red[wave][b][32] = c;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 32 * NB; t += NW * 64) {
+        const int b = t >> 5, j = t & 31;
+        float sa = 0.0f, sc = 0.0f;
+        for (int wv = 0; wv < NW; wv++) {
+            sa += red[wv][b][j];
+            sc += red[wv][b][32];
+        }
+        C[(long)b * Nout + col + j] = sa - sc;
+    }
+}
+
+template <int NB>
+static void launch_int4_rmul_v16(hipStream_t st, const uint8_t* W, const float* X, float* C, const float* s,
+                                 const uint8_t* z, int K, int Nout, int gs, int ng) {
+    constexpr int U = NB <= 2 ? 8 : 4;  // rows a lane loads before using any (within 256 VGPRs)
+    int4_rmul_v16_kernel<NB, U, 8><<<dim3(Nout / 32), dim3(8 * kWave), 0, st>>>(W, X, C, s, z, K, Nout, gs, ng);
 }
 
 // ------------------------------------------------------------ fp32 MFMA GEMM
@@ -835,7 +955,20 @@ ZT_EXPORT int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, con
     const int ng = ceil_div(out_features, group_size);
     const uint8_t* z = static_cast<const uint8_t*>(zeros);
     const uint8_t* w = static_cast<const uint8_t*>(W);
-    if (batch <= 4 && in_features > 0 && out_features % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)w & 7) == 0) {
+    // the 16-byte-load kernel up to K = 8192; beyond, its half as many
+    // workgroups each walk too long a K (us, batch 1 / 4: in x out 4096 x 4096
+    // 19.2 / 22.1 against 19.1 / 27.3, 4096 x 14336 41.1 / 45.5 against
+    // 64.1 / 102.6, 14336 x 4096 68.8 / 68.5 against 53.2 / 57.4)
+    if (batch <= 4 && in_features > 0 && in_features <= 8192 && out_features % 32 == 0 && group_size % 32 == 0 &&
+        ((uintptr_t)w & 15) == 0 && (long)in_features * (out_features / 2) < 0x7fffffffL &&
+        (long)in_features * ng * 4 < 0x7fffffffL) {
+        switch (batch) {
+            case 1: launch_int4_rmul_v16<1>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 2: launch_int4_rmul_v16<2>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            case 3: launch_int4_rmul_v16<3>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+            default: launch_int4_rmul_v16<4>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+        }
+    } else if (batch <= 4 && in_features > 0 && out_features % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)w & 7) == 0) {
         switch (batch) {
             case 1: launch_int4_rmul_valu<1>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
             case 2: launch_int4_rmul_valu<2>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
