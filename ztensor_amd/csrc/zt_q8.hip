@@ -126,7 +126,9 @@ static void launch_q8(int R, dim3 g, dim3 b, hipStream_t st, const uint8_t* base
 
 // Batch-1 GEMV: four lanes share one block.  Lane q of a quad takes bytes
 // 8q .. 8q+7 of the block's 32 int8 weights (one 8-byte load in the
-// separated layout, two dwords in the raw 36-byte blocks) and the matching 8
+// separated layout; in the raw 36-byte blocks one 12-byte load of dwords
+// 2q .. 2q+2, whose second and third are the lane's data and whose first is,
+// in lane 0, the block's scale, broadcast over the quad) and the matching 8
 // activations as two 16-byte loads, so a quad reads its block's 128 bytes of
 // activations contiguously.  R rows per wave, split-K over the waves.
 template <int L, int R>
@@ -144,6 +146,14 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    // raw blocks: one buffer resource a row (wave-uniform), so offsets within
+    // a row fit 32 bits at any matrix size
+    __amdgpu_buffer_rsrc_t rrow[L == kRaw36 ? R : 1];
+    if constexpr (L == kRaw36) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            rrow[r] = __builtin_amdgcn_make_buffer_rsrc((void*)(base + rbase[r] * 36), (short)0, kb * 36, 0x00020000);
+    }
 
     for (int b = wave * 16 + (lane >> 2); b < kb; b += nwaves * 16) {
         uint32_t d[R][2];
@@ -158,10 +168,13 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
                 d[r][1] = v.y;
                 s[r] = sep_scale<L>(base, blk);
             } else {
-                const uint32_t* p = reinterpret_cast<const uint32_t*>(base + blk * 36);
-                s[r] = __uint_as_float(p[0]);
-                d[r][0] = __builtin_nontemporal_load(p + 1 + 2 * q);
-                d[r][1] = __builtin_nontemporal_load(p + 2 + 2 * q);
+                typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+                const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rrow[r], (uint32_t)(b * 36 + 8 * q), 0, 2);
+                d[r][0] = v.y;
+                d[r][1] = v.z;
+                // quad_perm [0, 0, 0, 0]: lane 0's first dword is the block's scale
+                s[r] = __int_as_float(__builtin_amdgcn_update_dpp(0, (int)v.x, 0x00, 0xF, 0xF, false));
+                (void)blk;
             }
         }
         const float4 xa = *reinterpret_cast<const float4*>(x + (long)b * 32 + 8 * q);
@@ -188,9 +201,12 @@ __global__ void __launch_bounds__(512) gemv_q8_quad_kernel(const uint8_t* __rest
 // The same quad mapping in the fixed-step form of the Q4_0 kernel: each wave
 // does S steps of 16 blocks, every load issued before any arithmetic as
 // buffer loads with the wave-uniform row offsets as scalar offsets; lanes
-// past the last block read zeros.  On the raw 36-byte blocks a lane's 8 data
-// bytes sit at block offset 4 + 8q, dword- but not 8-byte-aligned, which a
-// buffer load takes as one 8-byte load.
+// past the last block read zeros.  On the raw 36-byte blocks (9 dwords: the
+// fp32 scale, then 8 data dwords) lane q of a quad loads the 12 bytes at
+// block offset 8q, dwords 2q .. 2q + 2: its data dwords 2q + 1, 2q + 2 are
+// always the second and third, and lane 0's first is the block's scale,
+// which a DPP quad broadcast hands to the other three.  One load instruction
+// a block and row, where a separate scale load touched the same lines again.
 template <int L, int S, int R>
 __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __restrict__ base, long data_offset,
                                                              const float* __restrict__ x, float* __restrict__ y,
@@ -205,6 +221,7 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
     u32x2 d[S][R];
     uint32_t sc[S][R];
     u32x4 xa[S], xb[S];
@@ -215,10 +232,12 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
-            if constexpr (L == kRaw36)
-                d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rs, ok ? (uint32_t)(b * 36 + 4 + q * 8) : 0x80000000u,
-                                                               row * (uint32_t)kb * 36u, 2);  // nontemporal
-            else
+            if constexpr (L == kRaw36) {
+                const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rs, ok ? (uint32_t)(b * 36 + q * 8) : 0x80000000u,
+                                                                     row * (uint32_t)kb * 36u, 2);  // nontemporal
+                d[t][r] = (u32x2){v.y, v.z};
+                sc[t][r] = v.x;  // the scale in lane 0 of the quad
+            } else
                 d[t][r] = __builtin_amdgcn_raw_buffer_load_b64(rd, ok ? (uint32_t)(b * 32 + q * 8) : 0x80000000u,
                                                                row * (uint32_t)kb * 32u, 2);  // nontemporal
         }
@@ -232,8 +251,7 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
             const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
             const uint32_t so = ok ? (uint32_t)b * SB : 0x80000000u;
             if constexpr (L == kRaw36)
-                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)b * 36u : 0x80000000u,
-                                                                row * (uint32_t)kb * 36u, 0);
+                continue;
             else if constexpr (L == kSep16)
                 sc[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, row * (uint32_t)kb * SB, 0);
             else
@@ -263,7 +281,9 @@ __global__ void __launch_bounds__(1024) gemv_q8_steps_kernel(const uint8_t* __re
                 s0 = fmaf((float)((u >> 16) & 0xffu), xv[4 * i + 2], s0);
                 s1 = fmaf((float)(u >> 24), xv[4 * i + 3], s1);
             }
-            const float scale = L == kSep16 ? h2f(sc[t][r] & 0xffffu) : __uint_as_float(sc[t][r]);
+            const uint32_t sb = L == kRaw36 ? (uint32_t)__builtin_amdgcn_update_dpp(0, (int)sc[t][r], 0x00, 0xF, 0xF, false)
+                                            : sc[t][r];  // raw: quad_perm [0, 0, 0, 0]
+            const float scale = L == kSep16 ? h2f(sb & 0xffffu) : __uint_as_float(sb);
             acc[r] = fmaf(scale, s0 + s1, acc[r]);
         }
     }
@@ -303,12 +323,10 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
     const int kb = K / 32;
     if (N == 1) {
-        // fixed steps: S = 1 for K <= 4096, 2 (up to 16 waves) beyond.  The
-        // separated layouts keep the loop kernel past K = 8192 (at K = 14336
-        // it measured 1-7% faster); on the raw blocks the fixed steps are
-        // faster up to K = 16384 once M >= 2048 (K = 14336: 17.6 against
-        // 22.6 us at 4096 rows, but 8.4 against 5.9 us at 1024 rows)
-        const bool steps_ok = kb <= 256 || (L == kRaw36 && kb <= 512 && M >= 2048);
+        // fixed steps: S = 1 for K <= 4096, 2 (up to 16 waves) up to K = 8192;
+        // the loop kernel beyond (at K = 14336 it measured 1-7% faster on
+        // the separated layout)
+        const bool steps_ok = kb <= 256;
         if ((long)M * kb * (L == kRaw36 ? 36 : 32) < 0x7fffffffL && data_offset < 0x7fffffffL && steps_ok) {
             const int S = kb <= 128 ? 1 : 2;
             int nws = ceil_div(kb, 16 * S);
