@@ -118,6 +118,21 @@ def test_int4_rmul(lib, orc, batch, inf, outf, gs):
     assert rel_err(y, orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, batch, inf, outf, gs)) <= TOL
 
 
+@pytest.mark.parametrize("batch", [1, 3])
+def test_int4_rmul_large_zero_points(lib, orc, batch):
+    """uint8 zero points up to 255 (the 16-byte-load kernel takes sum t (8 + zero) off at the end) and
+    activations of mixed sign, against the oracle and the fp64 product."""
+    inf, outf, gs = 2048, 1024, 64
+    w = synth.int4(inf, outf, gs, 404 + batch, zero_max=255)
+    x = synth.x_f32(batch * inf, 405 + batch).reshape(batch, inf)
+    y = np.asarray(run_rmul(lib, w, x, batch, inf, outf, gs), np.float64).reshape(batch, outf)
+    ref = np.asarray(orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, batch, inf, outf, gs)).reshape(batch, outf)
+    assert rel_err(y, ref) <= TOL
+    exact = np.asarray(x, np.float64) @ synth.int4_dense(w, gs)
+    for b in range(batch):
+        assert rel_err(y[b], exact[b]) <= 1e-6, b
+
+
 def test_int4_rmul_repeat_bit_identical(lib):
     """The X W kernels sum in a fixed order: two calls give the same bits."""
     for batch, inf, outf, gs in [(1, 4096, 4096, 32), (4, 2048, 1024, 128), (3, 1000, 1002, 7)]:
