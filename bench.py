@@ -560,6 +560,7 @@ SUITE = {
     "w4a16sz_70b": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [1]),
     "w4a16sz_70b_k28672": ("w4a16sz", [(8192, 28672)], [1]),
     "w4a16sz_70b_batched": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8]),
+    "w4a16sz_70b_wide": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [12, 16]),
     "w4a16sz_8b_batched": ("w4a16sz", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8]),
     "w4a16_8b_batched": ("w4a16", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [12, 16]),
     "w4a16t_8b": ("w4a16t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16]),
@@ -612,7 +613,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     if fmt == "w4a16_engine":  # the kernel ROCmEngine picks for this batch
         from ztensor_amd.engine import _w4a16_rowblock
 
-        fmt = "w4a16sz" if N == 1 or (N in (4, 8) and _w4a16_rowblock(rows, K, N)) else "w4a16t"
+        fmt = "w4a16sz" if N == 1 or (N in (4, 8, 12, 16) and _w4a16_rowblock(rows, K, N)) else "w4a16t"
     elif fmt == "iq4nl_engine":
         fmt = "iq4nl" if N == 1 or (N in (4, 8) and K <= 8192) else "iq4nlt"
     if fmt in ("q4_0", "iq4nl", "iq4nl32"):

@@ -200,17 +200,18 @@ def test_w4t_invalid_arguments(lib):
     assert lib.zt_w4a16_tile(p + 8, p, 0, 2, 128, 32, p, p, stream()) == 1  # W_packed alignment
 
 
+@pytest.mark.parametrize("rows", [512, 4096])
 @pytest.mark.parametrize("N", [8, 16])
 @pytest.mark.parametrize("side", ["A", "B"])
-def test_engine_batched_w4a16_dispatch(lib, orc, side, N):
+def test_engine_batched_w4a16_dispatch(lib, orc, side, N, rows):
     """ROCmEngine.matmul_w4a16 with 8 or 16 activation columns (A side) or
-    rows (B side) matches the oracle.  16 columns build the tiled copy once;
-    8 columns of this short matrix run the row-block GEMM on the row-major
-    upload and build none."""
+    rows (B side) matches the oracle.  16 columns of the 4096-row matrix
+    build the tiled copy once; 8 columns, and 16 of the 512-row matrix, run
+    the row-block GEMM on the row-major upload and build none."""
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import Float16Storage, GPTQStorage, Tensor
 
-    rows, K = 512, 1024
+    K = 1024
     w = synth.w4a16(rows, K, 66)
     st = GPTQStorage.from_raw(w.packed.reshape(-1), w.scales.reshape(-1), w.zeros.reshape(-1), rows * K, 128, 4)
     eng = ROCmEngine()
@@ -227,7 +228,7 @@ def test_engine_batched_w4a16_dispatch(lib, orc, side, N):
         y = eng.matmul_w4a16(act, Tensor((K, rows), st)).cpu().numpy()
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
-    assert (getattr(st, "_gpu_tiled", None) is not None) == (N == 16)
+    assert (getattr(st, "_gpu_tiled", None) is not None) == (N == 16 and rows > 2048)
 
 
 def _w4t_call(lib, wt, sz, xd, c, rows, K, N, s, ws):

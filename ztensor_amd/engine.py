@@ -491,7 +491,7 @@ class ROCmEngine:
             if x.dtype != torch.float16:
                 raise TypeError("W4A16 matmul takes fp16 activations")
             tiled_ok = k % 128 == 0 and s.group_size % 128 == 0 and rows * (k // s.group_size) < 1 << 29
-            if (n in (4, 8) and s._gpu_szr is not None and rows * k // 2 < 1 << 31 and _p(x) % 16 == 0
+            if (n in (4, 8, 12, 16) and s._gpu_szr is not None and rows * k // 2 < 1 << 31 and _p(x) % 16 == 0
                     and _w4a16_rowblock(rows, k, n)):
                 # one launch on the row-major upload and the packed (scale, zero) dwords: no tiled copy,
                 # no workspace, no second kernel
@@ -768,18 +768,23 @@ def _block_rowblock(fmt: str, rows: int, k: int, n: int) -> bool:
 
 
 def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
-    """Whether a batch of 4 or 8 W4A16 columns runs faster on the single-launch
+    """Whether a batch of 4-16 W4A16 columns runs faster on the single-launch
     row-block GEMM over the row-major upload (zt_gemm_w4a16sz_f32) than on the
     tiled layout with its split-K reduction.  Measured (us, row-block against
-    tiled): batch 4 at 8192 x 8192 10.2 / 12.0, 4096 x 14336 (rows x K)
-    10.4 / 11.1, 8192 x 28672 37.2 / 28.8; batch 8 at 14336 x 4096
-    11.8 / 12.6, 1024 x 8192 4.1 / 6.2, 8192 x 8192 13.3 / 12.2, 4096 x 14336
-    15.1 / 11.3.  A batch-8 workgroup re-reads more activation bytes than
-    weight bytes once the rows are many and K is long."""
+    tiled): batch 4 at 8192 x 8192 10.1 / 12.2, 4096 x 14336 (rows x K)
+    10.0 / 11.3, 8192 x 28672 37.1 / 29.7; batch 8 at 14336 x 4096
+    11.8 / 12.8, 4096 x 4096 4.9 / 6.8, 1024 x 8192 4.1 / 6.0, 8192 x 8192
+    13.2 / 12.5, 4096 x 14336 12.3 / 11.6, 28672 x 8192 37.7 / 29.0; batch
+    16 at 1024 x 8192 5.98 / 6.22, 8192 x 8192 37.3 / 13.5.  A batch-8
+    workgroup re-reads more activation bytes than weight bytes once the rows
+    are many and K is long; batches of 12 and 16 take one row set a
+    workgroup, which only few-row matrices afford."""
     if k > 32768:
         return False
     if n == 4:
         return k <= 16384
+    if n in (12, 16):
+        return k <= 8192 and rows <= 2048
     return k <= 4096 or rows <= 2048
 
 
