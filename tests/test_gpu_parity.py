@@ -489,7 +489,11 @@ def test_ternary_f32_reference_known_answers(lib, orc):
 
 
 @pytest.mark.parametrize("rows,K", BITNET + [(7, 33), (128, 256), (65, 2560), (6, 65536), (4, 65600), (1501, 256),
-                                              (16397, 128), (3, 4096), (2049, 64)])
+                                              (16397, 128), (3, 4096), (2049, 64),
+                                              # activations staged in LDS: 8 row groups of 4 rows at one wave
+                                              # a row group, 4 at two; partial last workgroups, K not a
+                                              # multiple of a wave's 4096
+                                              (6405, 2560), (8191, 64), (2053, 6912), (4099, 8192)])
 def test_ternary_f32_matches_oracle(lib, orc, rows, K):
     t = synth.ternary(rows, K, 77)
     x = synth.x_f32(K, 77)
