@@ -1,7 +1,8 @@
-"""GPU parity of IQ4_NL with several fp32 activation columns
-(zt_gemm_iq4nl_f32 with N > 1): with N % 4 == 0 and 16-byte aligned B, the
-fp32-activation row-block MFMA GEMM (rbf_kernel, groups of 8 columns up to
-K = 16384, else 4), one launch per group; other N one GEMV per column.
+"""GPU parity of IQ4_NL with fp32 activations (zt_gemm_iq4nl_f32): batch 1
+on the fixed-step GEMV for K <= 4096 (one or two steps a wave; 8197 rows
+take two) and the loop GEMV beyond; with N % 4 == 0 and 16-byte aligned B,
+the fp32-activation row-block MFMA GEMM (rbf_kernel, groups of 8 columns up
+to K = 8192, else 4), one launch per group; other N one GEMV per column.
 
 The reference's IQ4_NL matmul is its fp32 CPU engine: IQ4NLStorage's
 Dequantize (tensor/iq4_storage.go:36-46) and then an fp32 GEMM
@@ -68,7 +69,7 @@ def reference(orc, w, x):
     return (W @ np.asarray(x, np.float32)).astype(np.float32)
 
 
-@pytest.mark.parametrize("N", [4, 8])
+@pytest.mark.parametrize("N", [1, 4, 8])
 @pytest.mark.parametrize("rows,K", [(1, 32), (3, 96), (17, 544), (100, 3584), (65, 4128), (33, 8192), (9, 16384),
                                     (2049, 1024), (5, 20480), (3301, 17024)])
 def test_iq4n32_ragged(lib, orc, rows, K, N):
@@ -85,8 +86,8 @@ def test_iq4n32_ragged(lib, orc, rows, K, N):
     assert np.array_equal(c.view(np.uint32), gemm(lib, a, off, x, rows, K, N).view(np.uint32))
 
 
-@pytest.mark.parametrize("N", [4, 8])
-@pytest.mark.parametrize("rows,K", [(3584, 3584), (18944, 3584), (3584, 18944)])
+@pytest.mark.parametrize("N", [1, 4, 8])
+@pytest.mark.parametrize("rows,K", [(3584, 3584), (18944, 3584), (3584, 18944), (8197, 4096)])
 def test_iq4n32_qwen2_shapes(lib, orc, rows, K, N):
     print(f"iq4n32 rows={rows} K={K} N={N}", flush=True)
     w = synth.iq4nl(rows, K, synth.seed_for(5, rows % 7))

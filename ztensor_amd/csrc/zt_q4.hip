@@ -618,6 +618,140 @@ __global__ void __launch_bounds__(1024) gemv_iq4nl_h16_steps_kernel(const uint16
     block_reduce_store<R>(acc, red, y, 1, row0, rows);
 }
 
+// fp32 activations in the same fixed-step form: the lane's 8 activations
+// (elements 8q .. 8q+7 of its block) are two 16-byte loads a step, and the
+// 2 KB table maps a data byte to the fp32 pair (T[low], T[high]) of the
+// reference's codebook, so each product is the reference's fp32 product:
+// two FMAs a byte.
+template <int S, int R>
+__global__ void __launch_bounds__(1024) gemv_iq4nl_f32_steps_kernel(const uint16_t* __restrict__ scales,
+                                                                    const uint32_t* __restrict__ data,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int rows, int kb) {
+    __shared__ float red[16 * R];
+    __shared__ float2 tbl[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
+    uint32_t w[S][R], s[S][R];
+    u32x4 xa[S], xb[S];
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t voff = b < kb ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            w[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, row * (uint32_t)kb * 16u, 2);  // nontemporal
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const int b = (wave * S + t) * 16 + (lane >> 2);
+        const uint32_t soff = b < kb ? (uint32_t)(b * 2) : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+            s[t][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, row * (uint32_t)kb * 2u, 0);
+        }
+        const uint32_t xo = b < kb ? (uint32_t)(b * 128 + q * 32) : 0x80000000u;
+        xa[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        xb[t] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    }
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = make_float2(kIQ4NLTable[i & 15], kIQ4NLTable[i >> 4]);
+    // the table is visible to the workgroup; the loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < S; t++) {
+        const float xv[8] = {__uint_as_float(xa[t].x), __uint_as_float(xa[t].y), __uint_as_float(xa[t].z),
+                             __uint_as_float(xa[t].w), __uint_as_float(xb[t].x), __uint_as_float(xb[t].y),
+                             __uint_as_float(xb[t].z), __uint_as_float(xb[t].w)};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {  // byte j: elements 8q+2j (low nibble), 8q+2j+1 (high nibble)
+                const float2 e = tbl[(w[t][r] >> (8 * j)) & 0xffu];
+                s0 = __builtin_fmaf(e.x, xv[2 * j], s0);
+                s1 = __builtin_fmaf(e.y, xv[2 * j + 1], s1);
+            }
+            acc[r] = __builtin_fmaf(h2f((uint16_t)s[t][r]), s0 + s1, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+// fp32 activations past K = 4096: the loop form of gemv_iq4nl_h16_kernel
+// (buffer loads with wave-uniform row offsets as scalar offsets, a grid of
+// about 8192 waves) with the fp32 pair table.
+template <int R>
+__global__ void __launch_bounds__(1024) gemv_iq4nl_f32_kernel(const uint16_t* __restrict__ scales,
+                                                              const uint32_t* __restrict__ data,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int rows, int kb) {
+    __shared__ float red[16 * R];
+    __shared__ float2 tbl[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int q = lane & 3;
+    const int row0 = blockIdx.x * R;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128, 0x00020000);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = make_float2(kIQ4NLTable[i & 15], kIQ4NLTable[i >> 4]);
+    __syncthreads();
+    uint32_t rofs[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rofs[r] = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)kb;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int b0 = wave * 16; b0 < kb; b0 += nwaves * 16) {
+        const int b = b0 + (lane >> 2);
+        const bool ok = b < kb;
+        const uint32_t voff = ok ? (uint32_t)(b * 16 + q * 4) : 0x80000000u;
+        const uint32_t soff = ok ? (uint32_t)(b * 2) : 0x80000000u;
+        uint32_t w[R], sv[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) w[r] = __builtin_amdgcn_raw_buffer_load_b32(rd, voff, rofs[r] * 16u, 2);  // nontemporal
+#pragma unroll
+        for (int r = 0; r < R; r++) sv[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, rofs[r] * 2u, 0);
+        const uint32_t xo = ok ? (uint32_t)(b * 128 + q * 32) : 0x80000000u;
+        const u32x4 xa = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        const u32x4 xb = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+        const float xv[8] = {__uint_as_float(xa.x), __uint_as_float(xa.y), __uint_as_float(xa.z), __uint_as_float(xa.w),
+                             __uint_as_float(xb.x), __uint_as_float(xb.y), __uint_as_float(xb.z), __uint_as_float(xb.w)};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float2 e = tbl[(w[r] >> (8 * j)) & 0xffu];
+                s0 = __builtin_fmaf(e.x, xv[2 * j], s0);
+                s1 = __builtin_fmaf(e.y, xv[2 * j + 1], s1);
+            }
+            acc[r] = __builtin_fmaf(h2f((uint16_t)sv[r]), s0 + s1, acc[r]);
+        }
+    }
+    block_reduce_store<R>(acc, red, y, 1, row0, rows);
+}
+
+template <int S>
+static void launch_iq4nl_f32_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc,
+                                   const uint32_t* dt, const float* x, float* y, int rows, int kb) {
+    switch (R) {
+        case 8: gemv_iq4nl_f32_steps_kernel<S, 8><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 4: gemv_iq4nl_f32_steps_kernel<S, 4><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        case 2: gemv_iq4nl_f32_steps_kernel<S, 2><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+        default: gemv_iq4nl_f32_steps_kernel<S, 1><<<grid, block, 0, st>>>(sc, dt, x, y, rows, kb); break;
+    }
+}
+
 template <int S>
 static void launch_iq4nl_h16_steps(int R, dim3 grid, dim3 block, hipStream_t st, const uint16_t* sc,
                                    const uint32_t* dt, const uint16_t* x, float* y, int rows, int kb) {
@@ -1073,6 +1207,38 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
                     launch_q4_steps<1>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
                 else
                     launch_q4_steps<2>(Rs, dim3(ceil_div(M, Rs)), dim3(nw * kWave), st, sc, dt, B, C, M, kb);
+                return (int)hipGetLastError();
+            }
+        }
+        if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 4) {
+            // K <= 4096: the fixed-step form with the launch shape of the fp16 kernel below
+            if ((long)M * kb * 16 < 0x7fffffffL && kb <= 128) {
+                const int S = M >= 8192 ? 2 : 1;
+                int nw = ceil_div(kb, 16 * S);
+                if (nw > 4) nw = (nw + 3) & ~3;
+                const int Rs = (long)ceil_div(M, 4) * nw >= 2048 ? 4 : pick_rows_per_wave(M, nw, 1, 2048);
+                const dim3 g(ceil_div(M, Rs)), b(nw * kWave);
+                const uint32_t* dt = reinterpret_cast<const uint32_t*>(data);
+                const float* xf = reinterpret_cast<const float*>(B);
+                if (S == 2)
+                    launch_iq4nl_f32_steps<2>(Rs, g, b, st, sc, dt, xf, C, M, kb);
+                else
+                    launch_iq4nl_f32_steps<1>(Rs, g, b, st, sc, dt, xf, C, M, kb);
+                return (int)hipGetLastError();
+            }
+            if ((long)M * kb * 16 < 0x7fffffffL) {
+                const int Ri = pick_rows_per_wave(M, 16, 1, 2048);
+                const int groups = ceil_div(M, Ri);
+                const int nw = min(min(16, max(4, ceil_div(8192, groups))), ceil_div(kb, 16));
+                const dim3 g(groups), b(nw * kWave);
+                const uint32_t* dt = reinterpret_cast<const uint32_t*>(data);
+                const float* xf = reinterpret_cast<const float*>(B);
+                switch (Ri) {
+                    case 8: gemv_iq4nl_f32_kernel<8><<<g, b, 0, st>>>(sc, dt, xf, C, M, kb); break;
+                    case 4: gemv_iq4nl_f32_kernel<4><<<g, b, 0, st>>>(sc, dt, xf, C, M, kb); break;
+                    case 2: gemv_iq4nl_f32_kernel<2><<<g, b, 0, st>>>(sc, dt, xf, C, M, kb); break;
+                    default: gemv_iq4nl_f32_kernel<1><<<g, b, 0, st>>>(sc, dt, xf, C, M, kb); break;
+                }
                 return (int)hipGetLastError();
             }
         }
