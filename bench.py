@@ -574,6 +574,8 @@ SUITE = {
     "iq4nl_engine": ("iq4nl_engine", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 4, 8]),
     "iq4nl_batched": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [4, 8]),
     # zt_gemm_iq4nl_f32: fp32 activations (the reference's IQ4_NL matmul input type)
+    # zt_gemm_q4_f16: Q4_0 with fp16 activations (Float16Storage activations on the Q4_0 path)
+    "q4_0h": ("q4_0h", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "iq4nl32_batched": ("iq4nl32", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 4, 8]),
     "q4_k": ("q4_k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q5_k": ("q5_k", [(4096, 4096), (14336, 4096), (4096, 14336)], [1]),
@@ -616,8 +618,8 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         fmt = "w4a16sz" if N == 1 or (N in (4, 8, 12, 16) and _w4a16_rowblock(rows, K, N)) else "w4a16t"
     elif fmt == "iq4nl_engine":
         fmt = "iq4nl" if N == 1 or (N in (4, 8) and K <= 8192) else "iq4nlt"
-    if fmt in ("q4_0", "iq4nl", "iq4nl32"):
-        w = synth.q4_0(rows, K, seed) if fmt == "q4_0" else synth.iq4nl(rows, K, seed)
+    if fmt in ("q4_0", "q4_0h", "iq4nl", "iq4nl32"):
+        w = synth.q4_0(rows, K, seed) if fmt in ("q4_0", "q4_0h") else synth.iq4nl(rows, K, seed)
         nblk = rows * K // 32
         host = np.empty(lib.zt_q4_gpu_bytes(nblk), np.uint8)
         lib.zt_q4_raw_to_gpu(w.raw.ctypes.data, nblk, host.ctypes.data)
@@ -626,6 +628,9 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         if fmt == "q4_0":
             x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
             fn = lambda wb, y: lib.zt_gemm_q4_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
+        elif fmt == "q4_0h":
+            x = dev(synth.x_f16(K * N, seed))
+            fn = lambda wb, y: lib.zt_gemm_q4_f16(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off, s)
         elif fmt == "iq4nl32":
             x = torch.from_numpy(synth.x_f32(K * N, seed)).cuda()
             fn = lambda wb, y: lib.zt_gemm_iq4nl_f32(wb[0].data_ptr(), x.data_ptr(), y.data_ptr(), rows, K, N, off,
@@ -893,7 +898,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     return r
 
 
-SUITE_FORMATS = ("w4a16_engine", "iq4nl_engine", "int4", "int4_rmul", "int8", "q4_0", "iq4nl", "iq4nl32", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
+SUITE_FORMATS = ("w4a16_engine", "iq4nl_engine", "int4", "int4_rmul", "int8", "q4_0", "q4_0h", "iq4nl", "iq4nl32", "q8_0", "q8_0_raw", "q4_0t", "q8_0t", "q5_0t", "q4_kt", "q5_kt", "q6_kt", "w4a16",
                  "iq4nlt", "w4a16sz", "w4a16t", "ternary_i8", "ternary_f32", "q4_k", "q5_k", "q6_k", "q6_ks", "q8_0_gguf", "q5_0")
 
 

@@ -122,15 +122,25 @@ def test_q4_batched_matches_oracle(lib, orc, rows, K, N):
     assert rel_err(c.cpu().numpy().reshape(rows, N), ref) <= TOL
 
 
-def test_q4_fp16_activations(lib, orc):
-    rows, K = 256, 4096
+@pytest.mark.parametrize("rows,K", [(256, 4096), (1, 32), (17, 544), (100, 4128), (33, 8192), (9, 16384),
+                                    (5, 20480), (4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_q4_fp16_activations(lib, orc, rows, K):
+    """zt_gemm_q4_f16 at batch 1 against the oracle, and bit-identical to
+    zt_gemm_q4_f32 on the same activations widened to fp32: both run the
+    same kernel (fixed steps up to K = 16384, the loop beyond) with the same
+    products in the same order."""
     w = synth.q4_0(rows, K, 5)
     x16 = synth.x_f16(K, 5)
+    x32 = np.asarray(orc.f16_to_f32(x16), np.float32)
     a, off = q4_dev(w)
     xd, y = dev(x16), torch.empty(rows, dtype=torch.float32, device="cuda")
     lib.call("zt_gemm_q4_f16", a.data_ptr(), xd.data_ptr(), y.data_ptr(), rows, K, 1, off, stream())
-    ref = orc.gemm_f32_q4_nt(orc.f16_to_f32(x16), w.raw, 1, rows, K)
-    assert rel_err(y.cpu().numpy(), ref) <= TOL
+    ref = orc.gemm_f32_q4_nt(x32, w.raw, 1, rows, K)
+    got = y.cpu().numpy()
+    assert rel_err(got, ref) <= TOL
+    y32 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_q4_f32", a.data_ptr(), devf(x32).data_ptr(), y32.data_ptr(), rows, K, 1, off, stream())
+    assert np.array_equal(got.view(np.uint32), y32.cpu().numpy().view(np.uint32))
 
 
 def test_q4_reference_known_answers(lib):

@@ -350,6 +350,8 @@ def algorithmic_bytes(fmt: str, rows: int, K: int, N: int = 1, group: int = 128,
         return nblk * 36 + 4 * K * N + 4 * rows * N
     if fmt == "iq4nl":
         return nblk * 18 + 2 * K * N + 4 * rows * N
+    if fmt == "q4_0h":  # Q4_0 weights, fp16 activations
+        return nblk * 18 + 2 * K * N + 4 * rows * N
     if fmt == "iq4nl32":  # IQ4_NL weights, fp32 activations
         return nblk * 18 + 4 * K * N + 4 * rows * N
     if fmt == "w4a16":
