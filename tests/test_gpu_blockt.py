@@ -267,7 +267,7 @@ def test_engine_batched_rowblock_dispatch(lib, orc, fmt, rows, K, N):
     """Batches the row-block GEMM wins run on the batch-1 upload (no tiled
     copy is built); the others keep the tiled layout; both give the
     oracle's result."""
-    from ztensor_amd.engine import ROCmEngine, _block_rowblock
+    from ztensor_amd.engine import ROCmEngine, _block_rowblock, _w4a16_rowblock
     from ztensor_amd.storage import Q4Storage, Q8Storage, Tensor
 
     w = weights(fmt, rows, K, 88)
@@ -341,7 +341,7 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     result matches the reference CPU product (Q4_0 also with fp16
     activations, widened exactly to fp32); chunks that the row-block GEMM
     takes run on the batch-1 upload instead."""
-    from ztensor_amd.engine import ROCmEngine, _block_rowblock
+    from ztensor_amd.engine import ROCmEngine, _block_rowblock, _w4a16_rowblock
     from ztensor_amd.storage import GPTQStorage, IQ4NLStorage, Q4Storage, Q8Storage, Tensor
 
     rows, K = 200, 1024
@@ -373,8 +373,9 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     y = eng.matmul(Tensor((rows, K), s), xd).cpu().numpy()
     assert y.shape == (rows, n)
     assert rel_err(y, ref) <= TOL
-    if (fmt in ("w4a16", "iq4nl") and n < 12) or (fmt in ("q4", "q4_f16", "q8") and
-                                                   _block_rowblock(fmt[:2], rows, K, -(-n // 4) * 4 if n < 16 else 16)):
+    chunk = -(-n // 4) * 4 if n < 16 else 16
+    if ((fmt == "iq4nl" and n < 12) or (fmt == "w4a16" and _w4a16_rowblock(rows, K, chunk)) or
+            (fmt in ("q4", "q4_f16", "q8") and _block_rowblock(fmt[:2], rows, K, chunk))):
         # chunks of 4 or 8 columns run the row-block GEMM on the batch-1 upload
         assert getattr(s, "_gpu_tiled", None) is None
     else:
