@@ -242,7 +242,8 @@ struct RbFmtInfo {
     static constexpr bool IQ = F == RbFmt::IQ4NL;                                // codebook table, no offset
     static constexpr bool Q4 = F == RbFmt::Q4_0 || IQ, RAW = F == RbFmt::Q8_RAW;  // 16-byte blocks
     static constexpr int WD = Q4 ? 4 : 8;                                        // weight dwords a block
-    static constexpr int WL = Q4 ? 1 : RAW ? 4 : 2;                             // weight loads a block
+    static constexpr int WL = Q4 ? 1 : 2;                                       // weight loads a block (not RAW)
+    static constexpr int LPB = RAW ? 3 : WL + 1;                                  // loads a block, scale included
     static constexpr int BB = Q4 ? 16 : RAW ? 36 : 32;                           // data bytes a block
     static constexpr int SBY = RAW ? 36 : (Q4 || F == RbFmt::Q8_SEP16) ? 2 : 4;  // scale stride
     static constexpr int TBL = IQ ? 2048 : 0;                                    // LDS table bytes
@@ -307,12 +308,15 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
             const uint32_t b = brow + r * bstep + (uint32_t)c;
             const uint32_t wo = ok ? b * (uint32_t)Info::BB : 0x80000000u;
             if constexpr (Info::RAW) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) {  // 8 bytes at block offsets 4 + 8i (dword aligned)
-                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, wo + 4 + 8 * i, 0, 2));
-                    w[t][r][2 * i] = v.x;
-                    w[t][r][2 * i + 1] = v.y;
-                }
+                // the block's 9 dwords as three 12-byte loads: the scale, then the 8 data dwords
+                typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+                const u32x3 v0 = __builtin_amdgcn_raw_buffer_load_b96(rw, wo, 0, 2);
+                const u32x3 v1 = __builtin_amdgcn_raw_buffer_load_b96(rw, wo + 12, 0, 2);
+                const u32x3 v2 = __builtin_amdgcn_raw_buffer_load_b96(rw, wo + 24, 0, 2);
+                sc[t][r] = v0.x;
+                w[t][r][0] = v0.y; w[t][r][1] = v0.z;
+                w[t][r][2] = v1.x; w[t][r][3] = v1.y; w[t][r][4] = v1.z;
+                w[t][r][5] = v2.x; w[t][r][6] = v2.y; w[t][r][7] = v2.z;
             } else {
 #pragma unroll
                 for (int i = 0; i < Info::WL; i++) {
@@ -323,9 +327,11 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
                     w[t][r][4 * i + 3] = v.w;
                 }
             }
-            const uint32_t so = ok ? b * (uint32_t)Info::SBY : 0x80000000u;
-            sc[t][r] = Info::SBY == 2 ? __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0)
-                                      : __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+            if constexpr (!Info::RAW) {
+                const uint32_t so = ok ? b * (uint32_t)Info::SBY : 0x80000000u;
+                sc[t][r] = Info::SBY == 2 ? __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0)
+                                          : __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -348,7 +354,7 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this step's activations, issued a step ahead
         } else {
             // the activations only: the weight and scale loads after them may be outstanding
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S * R * (Info::WL + 1)) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S * R * Info::LPB) : "memory");
         }
         // the step's normalisation c = 2^sh
         float m = 0.0f;
