@@ -82,6 +82,8 @@ INT4_CASES = [  # M, K, N, group_size
     (1, 16, 1, 16), (4096, 4096, 2, 32), (100, 4112, 4, 16), (33, 8208, 2, 48),
     # batches 2-4 on 8192 rows: 4 rows a wave of the LDS-staged kernel, a partial last 4096-K chunk
     (8192, 4112, 2, 16), (8192, 4112, 3, 16), (8192, 4112, 4, 16),
+    # batch 1 on the fixed-step kernel: two steps a wave past K = 16384, K = 32768, the loop kernel beyond
+    (65, 20480, 1, 32), (17, 32768, 1, 128), (7, 33024, 1, 64), (2049, 16, 1, 16),
     # MFMA GEMM: group sizes not a multiple of 16, odd shapes, wider batches
     (1000, 1000, 2, 20), (77, 130, 5, 7), (65, 34, 9, 2), (512, 4096, 16, 128), (100, 2048, 64, 32), (3, 2, 1, 1),
     # bf16 MFMA GEMM (K % 32, group % 32, N even): partial 128 x 128 tiles
@@ -118,6 +120,18 @@ def test_int4_rmul(lib, orc, batch, inf, outf, gs):
     assert rel_err(y, orc.gemm_int4_f32_rmul(w.packed, x, w.scales, w.zeros, batch, inf, outf, gs)) <= TOL
 
 
+def test_int4_batch1_large_zero_points(lib, orc):
+    """uint8 zero points up to 255 at batch 1 (the fixed-step kernel takes (8 + zero) sum x off a chunk's
+    sum), against the oracle and the fp64 product."""
+    M, K, gs = 1000, 4096, 32
+    w = synth.int4(M, K, gs, 406, zero_max=255)
+    b = synth.x_f32(K, 407).reshape(K, 1)
+    y = np.asarray(run_int4(lib, w, b, M, K, 1, gs), np.float64).reshape(-1)
+    assert rel_err(y, np.asarray(orc.gemm_int4_f32(w.packed, b, w.scales, w.zeros, M, K, 1, gs)).reshape(-1)) <= TOL
+    exact = synth.int4_dense(w, gs) @ np.asarray(b, np.float64).reshape(-1)
+    assert rel_err(y, exact) <= 1e-6
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_int4_rmul_large_zero_points(lib, orc, batch):
     """uint8 zero points up to 255 (the 16-byte-load kernel takes sum t (8 + zero) off at the end) and
@@ -147,6 +161,7 @@ INT8_CASES = [  # M, K, N
     (4096, 4096, 1), (4096, 14336, 1), (4096, 4096, 4), (1, 16, 1), (333, 1024, 3),
     (7, 33, 1), (1000, 1000, 3), (256, 512, 64), (100, 4096, 17), (65, 1, 65), (64, 4112, 2), (31, 8208, 4),
     (200, 4128, 130), (129, 32, 6),
+    (31, 20496, 1), (9, 33040, 1), (2049, 16, 1), (3, 32768, 1),
     # batches 2-4 on 8192 rows: 4 rows a wave of the LDS-staged kernel, a partial last 4096-K chunk
     (8192, 4112, 2), (8192, 4112, 3), (8192, 4112, 4),
 ]
