@@ -590,6 +590,8 @@ SUITE = {
     "int4_rmul": ("int4_rmul", [(4096, 4096)], [1, 4]),
     "int4_rmul_shapes": ("int4_rmul", [(4096, 4096), (14336, 4096), (4096, 14336)], [1, 2, 3, 4]),
     "int8": ("int8", [(4096, 4096), (4096, 14336)], [1, 4]),
+    "int4_batched": ("int4", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16, 32, 64]),
+    "int8_batched": ("int8", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16, 32, 64]),
     "int4_gemm": ("int4", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int4_rmul_gemm": ("int4_rmul", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int8_gemm": ("int8", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
@@ -878,7 +880,12 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     gbs = nbytes / (us * 1e-6) / 1e9
     r = {"format": fmt, "K": K, "N": rows, "batch": N, "us": round(us, 3), "GB/s": round(gbs, 1),
          "pct_peak": round(100 * gbs / PEAK_GBS, 1), "bytes": nbytes, "rotating_copies": copies}
-    if fmt in ("int4", "int4_rmul", "int8") and N > 4:
+    rowblock = (fmt in ("int4", "int8") and N % 4 == 0 and K % 32 == 0 and K <= 32768
+                and (N <= 16 or (N <= 64 and rows * N <= (1 << 19 if fmt == "int4" else 1 << 18))))
+    if rowblock and N > 4:
+        # the row-block MFMA GEMM (zt_intq.hip's dispatch): one launch per 4 or 8 columns, HBM-bound
+        r["kernel"] = "rowblock"
+    elif fmt in ("int4", "int4_rmul", "int8") and N > 4:
         # useful flops 2 M K N; the MFMA unit the call runs on (zt_intq.hip's dispatch) and its
         # actual MFMA work: bf16 runs 3 MFMAs per product (int4: plus 3 all-ones MFMAs per column
         # tile and step, over TI row tiles), fp32 one

@@ -19,6 +19,12 @@
 //    int4_rmul_v16_kernel, 16-byte
 //    loads, for out % 32 == 0, group_size % 32 == 0 and in <= 8192, else
 //    int4_rmul_valu_kernel for out % 16 == 0 and group_size % 16 == 0);
+//  * batches of 4-64 columns of A B (N % 4 == 0; beyond 16 columns while
+//    M N <= 2^19 for int4, 2^18 for int8) with K % 32 == 0 (int4:
+//    group_size % 32 == 0) and K <= 32768: the row-block MFMA GEMM of
+//    zt_rbmfma.h (formats INT4G and INT8), fp16 encodings of the unsigned
+//    nibble or byte against hi/lo fp16 activations, the offset (8 + z or
+//    128) times the activation sum taken off once per 32-element block;
 //  * wider batches of A B with K % 32 == 0 (int4: group_size % 32 == 0) and
 //    an even N: intq_bf16_kernel, bf16 MFMA on exact three-part activations;
 //  * every other call: intq_mfma_kernel, an LDS-tiled fp32 MFMA GEMM
@@ -29,6 +35,7 @@
 
 #include "zt_common.h"
 #include "zt_mfma.h"
+#include "zt_rbmfma.h"
 
 namespace zt {
 
@@ -1057,12 +1064,26 @@ using namespace zt;
 // Grid limits of the MFMA GEMM: blockIdx.y holds M / 64.
 static bool intq_grid_ok(long M, long N) { return (M + kIqTM - 1) / kIqTM <= 65535 && (N + kIqTN - 1) / kIqTN < 0x7fffffffL; }
 
+// Batches of 4-64 columns (N % 4 == 0) on the row-block MFMA GEMM: one
+// launch per 4 or 8 columns, each streaming the weights once, so its time
+// grows with M N while the bf16 tile GEMM's stays flat up to 128 columns.
+// Measured (us, row-block / bf16): int4 4096 x 4096 batch 8 7.7 / 170,
+// 64 72 / 172; 14336 x 4096 batch 32 91 / 176, 64 183 / 176; int8 4096 x
+// 4096 batch 64 83 / 115, 14336 x 4096 batch 16 58 / 118, 32 139 / 118.  So
+// up to 16 columns always, and to 64 while M N <= 2^19 (int4) or 2^18 (int8).
+static bool intq_rb_ok(int N, int K, long M, long ng, const void* a, const void* B, bool int4) {
+    return N >= 4 && (N <= 16 || (N <= 64 && M * N <= (int4 ? 1L << 19 : 1L << 18))) && K % 32 == 0 && ((uintptr_t)a & 15) == 0 && M * ng * 4 < 0x7fffffffL &&
+           rbf_ok<RbFmt::INT8>(N, K / 32, M, B);
+}
+
 ZT_EXPORT int zt_gemm_int8_f32(const void* A, const float* B, float* C, int M, int K, int N, hipStream_t stream) {
     if (M < 0 || K < 0 || N < 0) return (int)hipErrorInvalidValue;
     if (M == 0 || N == 0) return (int)hipSuccess;
     if (A == nullptr || C == nullptr || (K > 0 && B == nullptr) || !intq_grid_ok(M, N)) return (int)hipErrorInvalidValue;
     const uint8_t* a = static_cast<const uint8_t*>(A);
-    if (N <= 4 && K > 0 && K % 16 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)B & 15) == 0)
+    if (K > 0 && intq_rb_ok(N, K, M, 1, a, B, false))
+        launch_rbf<RbFmt::INT8>(nullptr, a, B, C, M, K / 32, N, stream);
+    else if (N <= 4 && K > 0 && K % 16 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)B & 15) == 0)
         launch_intq_gemv<false>(stream, a, B, C, nullptr, nullptr, M, K, N, 1, 1);
     else if (K > 0 && K % 32 == 0 && N % 2 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 7) == 0)
         launch_intq_bf16<false>(stream, a, B, C, nullptr, nullptr, M, N, K, 1, 1);
@@ -1081,7 +1102,9 @@ ZT_EXPORT int zt_gemm_int4_f32(const void* A, const float* B, float* C, const fl
     const int ng = K > 0 ? ceil_div(K, group_size) : 1;
     const uint8_t* a = static_cast<const uint8_t*>(A);
     const uint8_t* z = static_cast<const uint8_t*>(zeros);
-    if (N <= 4 && K > 0 && K % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 15) == 0)
+    if (K > 0 && group_size % 32 == 0 && intq_rb_ok(N, K, M, ng, a, B, true) && ((uintptr_t)scales & 3) == 0)
+        launch_rbf<RbFmt::INT4G>(scales, a, B, C, M, K / 32, N, stream, z, group_size / 32, ng);
+    else if (N <= 4 && K > 0 && K % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)a & 7) == 0 && ((uintptr_t)B & 15) == 0)
         launch_intq_gemv<true>(stream, a, B, C, scales, z, M, K, N, group_size, ng);
     else if (K > 0 && K % 32 == 0 && group_size % 32 == 0 && N % 2 == 0 && ((uintptr_t)a & 3) == 0 &&
              ((uintptr_t)B & 7) == 0)

@@ -235,17 +235,21 @@ __device__ __forceinline__ void rb_finish(float (&acc)[4 * R * NB], const char* 
 // sum(q x) c = 2^-10 (D - 1.5 X) for Q4_0 (q - 8) and 2^-7 (D - 3 X) for
 // Q8_0, and the block's scale d takes it: y += d 2^-e (D/c - o X/c).  Every
 // output is summed in wave and then wave order and stored once (rb_finish).
-enum class RbFmt { Q4_0, Q8_RAW, Q8_SEP, Q8_SEP16, IQ4NL };
+// INT4G: group-quantized int4 (element 2b in the low nibble of byte b,
+// signed, fp32 scale and uint8 zero a group of 32 g elements); INT8: plain
+// int8 rows without scales.
+enum class RbFmt { Q4_0, Q8_RAW, Q8_SEP, Q8_SEP16, IQ4NL, INT4G, INT8 };
 
 template <RbFmt F>
 struct RbFmtInfo {
     static constexpr bool IQ = F == RbFmt::IQ4NL;                                // codebook table, no offset
-    static constexpr bool Q4 = F == RbFmt::Q4_0 || IQ, RAW = F == RbFmt::Q8_RAW;  // 16-byte blocks
+    static constexpr bool ZP = F == RbFmt::INT4G, NOSC = F == RbFmt::INT8;       // group zero; no scale
+    static constexpr bool Q4 = F == RbFmt::Q4_0 || IQ || ZP, RAW = F == RbFmt::Q8_RAW;  // 16-byte blocks
     static constexpr int WD = Q4 ? 4 : 8;                                        // weight dwords a block
     static constexpr int WL = Q4 ? 1 : 2;                                       // weight loads a block (not RAW)
-    static constexpr int LPB = RAW ? 3 : WL + 1;                                  // loads a block, scale included
+    static constexpr int LPB = RAW ? 3 : NOSC ? WL : ZP ? WL + 2 : WL + 1;        // loads a block, scale included
     static constexpr int BB = Q4 ? 16 : RAW ? 36 : 32;                           // data bytes a block
-    static constexpr int SBY = RAW ? 36 : (Q4 || F == RbFmt::Q8_SEP16) ? 2 : 4;  // scale stride
+    static constexpr int SBY = RAW ? 36 : ZP ? 4 : (Q4 || F == RbFmt::Q8_SEP16) ? 2 : 4;  // scale stride
     static constexpr int TBL = IQ ? 2048 : 0;                                    // LDS table bytes
 };
 
@@ -265,6 +269,16 @@ __device__ __forceinline__ void rbf_load_x(__amdgpu_buffer_rsrc_t rx, u32x4 (&xr
     }
 }
 
+// LDS position of element e of a 32-element chunk.  The Q4_0 steps read
+// positions 4 d + {0, 2, 1, 3} (low nibbles of dword d) and 16 + the same
+// (high nibbles); INT4G keeps element 8 d + 2 i in the low nibble of byte
+// i of dword d and 8 d + 2 i + 1 in its high nibble, so its activations are
+// stored at position 16 (e & 1) + 4 (e >> 3) + ((e >> 1) & 3).
+template <bool ZP>
+__device__ __forceinline__ int rbf_kpos(int e) {
+    return ZP ? 16 * (e & 1) + 4 * (e >> 3) + ((e >> 1) & 3) : e;
+}
+
 // scales: fp16 or fp32 scales (Q8_RAW: the 36-byte blocks); data: 16- or
 // 32-byte blocks (Q8_RAW: the 36-byte blocks again).
 // Threads a workgroup may have.  8-column groups run at most 8 waves (their
@@ -277,7 +291,8 @@ constexpr int rbf_bound(int NB, int R, int S) { return NB == 2 ? 512 : R == 4 &&
 template <RbFmt F, int NB, int R, int S, class Tbl = RbNoTable>
 __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t* __restrict__ scales, const uint8_t* __restrict__ data,
                                                    const float* __restrict__ x, float* __restrict__ y, int rows,
-                                                   int kb, int ldx, int n0) {
+                                                   int kb, int ldx, int n0, const uint8_t* __restrict__ zeros, int gsc,
+                                                   int ng) {
     using Info = RbFmtInfo<F>;
     using Lay = RbO4Layout<2 * NB>;
     constexpr int V = 4 * R * NB;
@@ -290,19 +305,22 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
     // rows past M and K read zeros: the buffers end at row M and at K
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void*)data, (short)0, rows * kb * Info::BB, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, rows * kb * Info::SBY, 0x00020000);
+    // INT4G: scales and zeros [rows, ng], group g of a row covering blocks gsc g .. gsc (g + 1) - 1
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)scales, (short)0, Info::ZP ? rows * ng * 4 : rows * kb * Info::SBY, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)zeros, (short)0, rows * ng, 0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, kb * 128 * ldx, 0x00020000);
     const int step0 = wave * S;
     u32x4 xr[8 * NB];
     rbf_load_x<NB>(rx, xr, step0, ldx, n0, lane);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t w[S][R][Info::WD], sc[S][R];
+    uint32_t w[S][R][Info::WD], sc[S][R], zp[S][R];
     const uint32_t brow = (uint32_t)(row0 + j) * (uint32_t)kb, bstep = 4u * (uint32_t)kb;
 #pragma unroll
     for (int t = 0; t < S; t++) {
         const int c = (step0 + t) * 16 + blk;
         const bool ok = c < kb;
+        const int gq = Info::ZP ? c / gsc : 0;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t b = brow + r * bstep + (uint32_t)c;
@@ -327,7 +345,13 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
                     w[t][r][4 * i + 3] = v.w;
                 }
             }
-            if constexpr (!Info::RAW) {
+            if constexpr (Info::NOSC) {
+                sc[t][r] = 0x3f800000u;  // 1.0f
+            } else if constexpr (Info::ZP) {
+                const uint32_t gi = (uint32_t)(row0 + j + 4 * r) * (uint32_t)ng + (uint32_t)gq;
+                sc[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? 4u * gi : 0x80000000u, 0, 0);
+                zp[t][r] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? gi : 0x80000000u, 0, 0);
+            } else if constexpr (!Info::RAW) {
                 const uint32_t so = ok ? b * (uint32_t)Info::SBY : 0x80000000u;
                 sc[t][r] = Info::SBY == 2 ? __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0)
                                           : __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
@@ -387,12 +411,12 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
             }
             if constexpr (NB == 1) {
                 // K row k: one 16-byte piece (hi columns, then lo columns)
-                const int k = 64 * i + lane, c = k >> 5, p = ((k & 31) + Lay::sig(c)) & 31;
+                const int k = 64 * i + lane, c = k >> 5, p = (rbf_kpos<Info::ZP>(k & 31) + Lay::sig(c)) & 31;
                 *reinterpret_cast<uint4*>(xs + (c * 32 + p) * 16) = make_uint4(hv[0], hv[1], lv[0], lv[1]);
             } else {
                 // K row k: pieces 2k (hi) and 2k + 1 (lo), this lane's 4 columns at byte 8 (lane & 1)
-                const int k = 32 * i + (lane >> 1), c = k >> 5, hf = 8 * (lane & 1);
-                const int ph = (2 * (k & 31) + Lay::sig(c)) & 63, pl = (2 * (k & 31) + 1 + Lay::sig(c)) & 63;
+                const int k = 32 * i + (lane >> 1), c = k >> 5, hf = 8 * (lane & 1), kp = rbf_kpos<Info::ZP>(k & 31);
+                const int ph = (2 * kp + Lay::sig(c)) & 63, pl = (2 * kp + 1 + Lay::sig(c)) & 63;
                 *reinterpret_cast<uint2*>(xs + (c * 64 + ph) * 16 + hf) = make_uint2(hv[0], hv[1]);
                 *reinterpret_cast<uint2*>(xs + (c * 64 + pl) * 16 + hf) = make_uint2(lv[0], lv[1]);
             }
@@ -445,7 +469,7 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
                 for (int r = 0; r < R; r++) {
                     uint32_t a, b;
                     if constexpr (Info::Q4) {
-                        const uint32_t q = w[t][r][s >> 1];
+                        const uint32_t q = w[t][r][s >> 1] ^ (Info::ZP ? 0x88888888u : 0u);  // INT4G: u = v + 8
                         a = (s & 1) ? q << 2 : q << 6;  // bytes 0, 2: low or high nibbles
                         b = (s & 1) ? q >> 6 : q >> 2;  // bytes 1, 3
                     } else {
@@ -472,6 +496,8 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float dv = (Info::SBY == 2 ? h2f((uint16_t)sc[t][r]) : __uint_as_float(sc[t][r])) * kSm;
+            // INT4G: w = (u - 8 - z) s, so the offset is (16 + 8 + z) / 16 where Q4_0's is 24 / 16
+            const float ko = Info::ZP ? __builtin_fmaf((float)(zp[t][r] & 0xffu), 0.0625f, kOff) : kOff;
 #pragma unroll
             for (int js = 0; js < NB; js++)
 #pragma unroll
@@ -480,7 +506,7 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
                     if constexpr (Info::IQ)
                         a = __builtin_fmaf(dv, d[r][js][v] * ic, a);
                     else
-                        a = __builtin_fmaf(dv, __builtin_fmaf(d[r][js][v], ic, -kOff * dx[js][v] * ic), a);
+                        a = __builtin_fmaf(dv, __builtin_fmaf(d[r][js][v], ic, -ko * dx[js][v] * ic), a);
                 }
         }
     }
@@ -491,7 +517,7 @@ __global__ void __launch_bounds__(rbf_bound(NB, R, S)) rbf_kernel(const uint8_t*
 
 template <RbFmt F, int NB, int R, int S, class Tbl>
 static void launch_rbf_t(dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data, const float* x,
-                         float* y, int rows, int kb, int ldx, int n0) {
+                         float* y, int rows, int kb, int ldx, int n0, const uint8_t* zs, int gsc, int ng) {
     const size_t lds = RbFmtInfo<F>::TBL + (size_t)nw * RbO4Layout<2 * NB>::STEP;
     if (lds > 65536) {  // past the default dynamic LDS limit (gfx950 has 160 KB a CU)
         static const bool raised = [] {
@@ -500,17 +526,19 @@ static void launch_rbf_t(dim3 g, int nw, hipStream_t st, const uint8_t* sc, cons
         }();
         (void)raised;
     }
-    rbf_kernel<F, NB, R, S, Tbl><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0);
+    rbf_kernel<F, NB, R, S, Tbl><<<g, nw * kWave, lds, st>>>(sc, data, x, y, rows, kb, ldx, n0, zs, gsc, ng);
 }
 
 template <RbFmt F, int NB, class Tbl>
 static void launch_rbf_n(int R, int S, dim3 g, int nw, hipStream_t st, const uint8_t* sc, const uint8_t* data,
-                         const float* x, float* y, int rows, int kb, int ldx, int n0) {
-#define ZT_RB(RR, SS) \
-    if (R == RR && S == SS) return launch_rbf_t<F, NB, RR, SS, Tbl>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0);
+                         const float* x, float* y, int rows, int kb, int ldx, int n0, const uint8_t* zs, int gsc,
+                         int ng) {
+#define ZT_RB(RR, SS)                                                                                    \
+    if (R == RR && S == SS)                                                                              \
+        return launch_rbf_t<F, NB, RR, SS, Tbl>(g, nw, st, sc, data, x, y, rows, kb, ldx, n0, zs, gsc, ng);
     ZT_RB(1, 1) ZT_RB(2, 1) ZT_RB(4, 1) ZT_RB(1, 2) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4)
     if constexpr (RbFmtInfo<F>::Q4) { ZT_RB(8, 1) ZT_RB(4, 2) }
-    if constexpr (RbFmtInfo<F>::Q4 && NB == 1) { ZT_RB(4, 4) }
+    if constexpr (RbFmtInfo<F>::Q4 && !RbFmtInfo<F>::ZP && NB == 1) { ZT_RB(4, 4) }
 #undef ZT_RB
 }
 
@@ -538,7 +566,8 @@ static bool rbf_ok(int N, int kb, long M, const void* B) {
 // (29.8 against 31.6), for Q8_0 the 8-column launch wins (38.5 against 55.0).
 template <RbFmt F, class Tbl = RbNoTable>
 static void launch_rbf(const void* scales, const void* data, const void* B, float* C, int M, int kb, int N,
-                       hipStream_t st) {
+                       hipStream_t st, const void* zeros = nullptr, int gsc = 1, int ng = 0) {
+    const uint8_t* zs = static_cast<const uint8_t*>(zeros);
     const uint8_t* sc = static_cast<const uint8_t*>(scales);
     const uint8_t* dt = static_cast<const uint8_t*>(data);
     const float* x = static_cast<const float*>(B);
@@ -548,12 +577,13 @@ static void launch_rbf(const void* scales, const void* data, const void* B, floa
         const int steps = ceil_div(kb, 16), wmax = nc == 8 ? 8 : 16;
         const int S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
         const int nw = ceil_div(steps, S);
-        const int rmax = S == 4 ? (Q4 && nc == 4 && nw <= 10 ? 4 : 2) : (S == 2 && !Q4) ? 2 : (S == 1 && Q4) ? 8 : 4;
+        // (INT4G's zero bytes push 4 row sets at four steps past the 640-thread budget)
+        const int rmax = S == 4 ? (Q4 && !RbFmtInfo<F>::ZP && nc == 4 && nw <= 10 ? 4 : 2) : (S == 2 && !Q4) ? 2 : (S == 1 && Q4) ? 8 : 4;
         int R = 1;
         while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
         const dim3 g(ceil_div(M, 4 * R));
-        if (nc == 8) launch_rbf_n<F, 2, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
-        else launch_rbf_n<F, 1, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0);
+        if (nc == 8) launch_rbf_n<F, 2, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0, zs, gsc, ng);
+        else launch_rbf_n<F, 1, Tbl>(R, S, g, nw, st, sc, dt, x, C, M, kb, N, n0, zs, gsc, ng);
         n0 += nc;
     }
 }
