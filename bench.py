@@ -589,6 +589,7 @@ SUITE = {
     "int4": ("int4", [(4096, 4096), (14336, 4096)], [1, 4]),
     "int4_rmul": ("int4_rmul", [(4096, 4096)], [1, 4]),
     "int4_rmul_shapes": ("int4_rmul", [(4096, 4096), (14336, 4096), (4096, 14336)], [1, 2, 3, 4]),
+    "int4_rmul_batched": ("int4_rmul", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16, 32]),
     "int8": ("int8", [(4096, 4096), (4096, 14336)], [1, 4]),
     "int4_batched": ("int4", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16, 32, 64]),
     "int8_batched": ("int8", [(4096, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16, 32, 64]),
@@ -885,6 +886,9 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
     if rowblock and N > 4:
         # the row-block MFMA GEMM (zt_intq.hip's dispatch): one launch per 4 or 8 columns, HBM-bound
         r["kernel"] = "rowblock"
+    elif fmt == "int4_rmul" and N > 4 and ((K <= 8192 and rows % 32 == 0 and N <= 64) or N <= 16):
+        # X W past batch 4: the batch-4 kernels once per group of up to 4 rows of X (zt_intq.hip's dispatch)
+        r["kernel"] = "rmul_groups_of_4"
     elif fmt in ("int4", "int4_rmul", "int8") and N > 4:
         # useful flops 2 M K N; the MFMA unit the call runs on (zt_intq.hip's dispatch) and its
         # actual MFMA work: bf16 runs 3 MFMAs per product (int4: plus 3 all-ones MFMAs per column

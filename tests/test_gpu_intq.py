@@ -108,6 +108,11 @@ RMUL_CASES = [  # batch, in, out, group_size
     # multiple of the 8 waves' rows, batches 1-4
     (2, 1000, 4160, 64), (3, 2048, 96, 32), (1, 8191, 1024, 256), (4, 64, 4096, 32), (1, 14336, 4096, 32),
     (2, 4096, 14336, 128),
+    # past batch 4, groups of up to 4 rows of X on the same kernels: the 16-byte-load kernel up to
+    # batch 64 (ragged last groups), the 8-byte one up to batch 16 (in > 8192 or out % 32 != 0),
+    # the fp32 MFMA GEMM beyond
+    (8, 4096, 4096, 128), (13, 1000, 4160, 64), (32, 512, 2048, 32), (64, 256, 512, 32), (16, 9000, 1040, 16),
+    (6, 300, 4112, 16), (65, 256, 512, 32), (17, 9000, 1024, 32),
 ]
 
 

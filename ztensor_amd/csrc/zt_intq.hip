@@ -1128,22 +1128,36 @@ ZT_EXPORT int zt_gemm_int4_f32_rmul(const void* W, const float* B, float* C, con
     // the 16-byte-load kernel up to K = 8192; beyond, its half as many
     // workgroups each walk too long a K (us, batch 1 / 4: in x out 4096 x 4096
     // 19.2 / 22.1 against 19.1 / 27.3, 4096 x 14336 41.1 / 45.5 against
-    // 64.1 / 102.6, 14336 x 4096 68.8 / 68.5 against 53.2 / 57.4)
-    if (batch <= 4 && in_features > 0 && in_features <= 8192 && out_features % 32 == 0 && group_size % 32 == 0 &&
-        ((uintptr_t)w & 15) == 0 && (long)in_features * (out_features / 2) < 0x7fffffffL &&
-        (long)in_features * ng * 4 < 0x7fffffffL) {
-        switch (batch) {
-            case 1: launch_int4_rmul_v16<1>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 2: launch_int4_rmul_v16<2>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 3: launch_int4_rmul_v16<3>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            default: launch_int4_rmul_v16<4>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-        }
-    } else if (batch <= 4 && in_features > 0 && out_features % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)w & 7) == 0) {
-        switch (batch) {
-            case 1: launch_int4_rmul_valu<1>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 2: launch_int4_rmul_valu<2>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            case 3: launch_int4_rmul_valu<3>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
-            default: launch_int4_rmul_valu<4>(stream, w, B, C, scales, z, in_features, out_features, group_size, ng); break;
+    // 64.1 / 102.6, 14336 x 4096 68.8 / 68.5 against 53.2 / 57.4).  Past
+    // batch 4 the same kernels run once per group of up to 4 rows of X: the
+    // fp32 MFMA GEMM's out / 64 workgroups each walk all of K whatever the
+    // batch (376 us at 4096 x 4096 for batches 8-32, 1310 at 4096 x 14336),
+    // so groups of 4 win up to batch 64 on the 16-byte kernel (about 22 us a
+    // group) and batch 16 on the 8-byte one (about 57 us a group at 14336 x 4096).
+    const bool v16 = in_features > 0 && in_features <= 8192 && out_features % 32 == 0 && group_size % 32 == 0 &&
+                     ((uintptr_t)w & 15) == 0 && (long)in_features * (out_features / 2) < 0x7fffffffL &&
+                     (long)in_features * ng * 4 < 0x7fffffffL;
+    const bool valu = in_features > 0 && out_features % 16 == 0 && group_size % 16 == 0 && ((uintptr_t)w & 7) == 0;
+    if ((v16 && batch <= 64) || (valu && batch <= 16)) {
+        for (int b0 = 0; b0 < batch; b0 += 4) {
+            const float* xb = B + (long)b0 * in_features;
+            float* cb = C + (long)b0 * out_features;
+            const int nb = min(4, batch - b0);
+            if (v16) {
+                switch (nb) {
+                    case 1: launch_int4_rmul_v16<1>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    case 2: launch_int4_rmul_v16<2>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    case 3: launch_int4_rmul_v16<3>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    default: launch_int4_rmul_v16<4>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                }
+            } else {
+                switch (nb) {
+                    case 1: launch_int4_rmul_valu<1>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    case 2: launch_int4_rmul_valu<2>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    case 3: launch_int4_rmul_valu<3>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                    default: launch_int4_rmul_valu<4>(stream, w, xb, cb, scales, z, in_features, out_features, group_size, ng); break;
+                }
+            }
         }
     } else {
         launch_intq_mfma<2>(stream, B, W, C, scales, z, batch, out_features, in_features, group_size, ng);
