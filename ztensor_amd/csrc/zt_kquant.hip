@@ -267,16 +267,20 @@ __global__ void __launch_bounds__(1024) kq_steps_kernel(const uint8_t* __restric
     const uint32_t vq = ok ? (uint32_t)(sb * BB + 16 + byte0) : 0x80000000u;
     const uint32_t vqh = ok ? (uint32_t)(sb * BB + 144 + o) : 0x80000000u;
     const uint32_t vh = ok ? (uint32_t)(sb * BB) : 0x80000000u;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     uint32_t q0[R], q1[R], h0[R], h1[R];
     u32x4 hdr[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint32_t ro = (uint32_t)min(row0 + r, rows - 1) * (uint32_t)(nsb * BB);
-        q0[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vq, ro, 2);  // nontemporal
-        q1[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vq + 4, ro, 2);
+        // one 8-byte load each (super-blocks of 144 / 176 bytes keep both fields 8-byte aligned)
+        const u32x2 qv = __builtin_amdgcn_raw_buffer_load_b64(rw, vq, ro, 2);  // nontemporal
+        q0[r] = qv.x;
+        q1[r] = qv.y;
         if constexpr (FMT == 5) {
-            h0[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vqh, ro, 2);
-            h1[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, vqh + 4, ro, 2);
+            const u32x2 hv = __builtin_amdgcn_raw_buffer_load_b64(rw, vqh, ro, 2);
+            h0[r] = hv.x;
+            h1[r] = hv.y;
         }
         hdr[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, vh, ro, 0);
     }
