@@ -860,7 +860,7 @@ __device__ __forceinline__ uint32_t hi16_pack(float a, float b) {
     return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
 }
 
-template <bool INT4, int TI>
+template <bool INT4, int TI, int PF>
 __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, const float* __restrict__ scales,
                                                         const uint8_t* __restrict__ zeros, int M, int N, int K, int gs,
@@ -889,32 +889,39 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
     const int bn = n0 + 2 * cp;
     const bool bok = stager && bn < N;
 
-    uint2 araw8[TI];
-    uint32_t araw4[TI];
-    float2 braw[8];
-    float sreg = 0.0f, zreg = 0.0f;
-    auto load_step = [&](int k0) {
+    // two register sets, step t in set t & 1.  PF = 2: step t + 2's loads are
+    // issued during step t, so they have two steps of MFMAs to return (for
+    // 64 x 64 tiles; with 128 x 128 tiles the second set's registers would
+    // halve the waves a SIMD holds).  PF = 1: one set and a rolled loop, step
+    // t + 1's loads issued during step t.
+    uint2 araw8[2][TI];
+    uint32_t araw4[2][TI];
+    float2 braw[2][8];
+    float sreg[2] = {0.0f, 0.0f}, zreg[2] = {0.0f, 0.0f};
+    auto load_step = [&](auto parc, int k0) {
+        constexpr int P = decltype(parc)::value;
 #pragma unroll
         for (int i = 0; i < TI; i++) {
             const long off = (long)arow[i] * rowbytes + (INT4 ? (k0 + 8 * lg) / 2 : k0 + 8 * lg);
             if constexpr (INT4)
-                araw4[i] = aok[i] ? *reinterpret_cast<const uint32_t*>(A + off) : 0x88888888u;  // u' = 0
+                araw4[P][i] = aok[i] ? *reinterpret_cast<const uint32_t*>(A + off) : 0x88888888u;  // u' = 0
             else
-                araw8[i] = aok[i] ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
+                araw8[P][i] = aok[i] ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
         }
 #pragma unroll
         for (int r = 0; r < 8; r++)
-            braw[r] = bok ? *reinterpret_cast<const float2*>(B + (long)(k0 + 8 * ko + r) * N + bn) : make_float2(0.f, 0.f);
+            braw[P][r] = bok ? *reinterpret_cast<const float2*>(B + (long)(k0 + 8 * ko + r) * N + bn) : make_float2(0.f, 0.f);
         if constexpr (INT4) {
-            if (tid < TM && k0 % gs == 0) {
+            if (tid < TM) {  // every step: each set holds its own step's group
                 const int m = m0 + tid;
                 const long gi = (long)(m < M ? m : 0) * ng + k0 / gs;
-                sreg = m < M ? scales[gi] : 0.0f;
-                zreg = 136.0f + (float)zeros[gi];
+                sreg[P] = m < M ? scales[gi] : 0.0f;
+                zreg[P] = 136.0f + (float)zeros[gi];
             }
         }
     };
-    auto stage = [&](int buf, int k0) {
+    auto stage = [&](auto parc, int buf) {
+        constexpr int P = decltype(parc)::value;
         // B parts: for each of the 2 columns, 8 K values in slot order
 #pragma unroll
         for (int c = 0; c < 2 && stager; c++) {
@@ -922,7 +929,7 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int r = INT4 ? ((j & 1) ? 4 + (j >> 1) : (j >> 1)) : j;  // slot j holds K offset r
-                v[j] = c == 0 ? braw[r].x : braw[r].y;
+                v[j] = c == 0 ? braw[P][r].x : braw[P][r].y;
             }
             uint32_t p1[4], p2[4], p3[4];
 #pragma unroll
@@ -944,12 +951,10 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
         }
         if constexpr (INT4) {
             if (tid < TM) {
-                // the group changes only at a multiple of gs; otherwise carry the last one
-                scs[buf][tid] = sreg;
-                zzs[buf][tid] = zreg;
+                scs[buf][tid] = sreg[P];
+                zzs[buf][tid] = zreg[P];
             }
         }
-        (void)k0;
     };
 
     float4v acc[TI][TI];
@@ -958,21 +963,28 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
 #pragma unroll
         for (int j = 0; j < TI; j++) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
     const int nsteps = K / 32;
-    load_step(0);
-    stage(0, 0);
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    load_step(P0{}, 0);
+    if (PF == 2 && nsteps > 1) load_step(P1{}, 32);
+    stage(P0{}, 0);
     __syncthreads();
-    for (int t = 0; t < nsteps; t++) {
+    // step t: Bs[t & 1] holds its activations, set t & 1 its weights; set
+    // (t + 1) & 1 has step t + 1's loads in flight
+    auto body = [&](auto parc, int t) {
+        constexpr int P = decltype(parc)::value;
+        using Q = std::integral_constant<int, PF == 2 ? 1 - P : P>;
         const int buf = t & 1;
-        // decode this step's A operands before the next step's loads overwrite the registers
+        // decode this step's A operands, then reuse the set for step t + 2
         u32x4 av[TI];
 #pragma unroll
         for (int i = 0; i < TI; i++) {
             if constexpr (INT4) {
-                const uint32_t d = araw4[i] ^ 0x88888888u;
+                const uint32_t d = araw4[P][i] ^ 0x88888888u;
                 av[i] = (u32x4){(d & 0x000F000Fu) | 0x43004300u, ((d >> 4) & 0x000F000Fu) | 0x43004300u,
                                 ((d >> 8) & 0x000F000Fu) | 0x43004300u, ((d >> 12) & 0x000F000Fu) | 0x43004300u};
             } else {
-                const uint32_t w2[2] = {araw8[i].x, araw8[i].y};
+                const uint32_t w2[2] = {araw8[P][i].x, araw8[P][i].y};
                 uint32_t q[4];
 #pragma unroll
                 for (int h = 0; h < 4; h++) {
@@ -983,7 +995,11 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
                 av[i] = (u32x4){q[0], q[1], q[2], q[3]};
             }
         }
-        if (t + 1 < nsteps) load_step(32 * (t + 1));
+        if constexpr (PF == 2) {
+            if (t + 2 < nsteps) load_step(parc, 32 * (t + 2));
+        } else {
+            if (t + 1 < nsteps) load_step(Q{}, 32 * (t + 1));
+        }
         float4v sc4[TI], zz4[TI];
         if constexpr (INT4) {
 #pragma unroll
@@ -1025,8 +1041,16 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
             }
         }
         // the other buffer was last read in step t - 1, before the barrier that ended it
-        if (t + 1 < nsteps) stage(buf ^ 1, 32 * (t + 1));
+        if (t + 1 < nsteps) stage(Q{}, buf ^ 1);
         __syncthreads();
+    };
+    if constexpr (PF == 2) {
+        for (int t = 0; t < nsteps; t += 2) {
+            body(P0{}, t);
+            if (t + 1 < nsteps) body(P1{}, t + 1);
+        }
+    } else {
+        for (int t = 0; t < nsteps; t++) body(P0{}, t);
     }
 #pragma unroll
     for (int i = 0; i < TI; i++)
@@ -1045,9 +1069,9 @@ template <bool INT4>
 static void launch_intq_bf16(hipStream_t st, const uint8_t* A, const float* B, float* C, const float* s,
                              const uint8_t* z, int M, int N, int K, int gs, int ng) {
     if ((long)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
-        intq_bf16_kernel<INT4, 4><<<dim3(ceil_div(N, 128), ceil_div(M, 128)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+        intq_bf16_kernel<INT4, 4, 1><<<dim3(ceil_div(N, 128), ceil_div(M, 128)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
     else
-        intq_bf16_kernel<INT4, 2><<<dim3(ceil_div(N, 64), ceil_div(M, 64)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+        intq_bf16_kernel<INT4, 2, 2><<<dim3(ceil_div(N, 64), ceil_div(M, 64)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
 }
 
 template <int V>
