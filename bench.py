@@ -561,6 +561,7 @@ SUITE = {
     "w4a16sz_70b_k28672": ("w4a16sz", [(8192, 28672)], [1]),
     "w4a16sz_70b_batched": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [4, 8]),
     "w4a16sz_70b_wide": ("w4a16sz", [(8192, 8192), (1024, 8192), (28672, 8192)], [12, 16]),
+    "w4a16sz_8b_wide": ("w4a16sz", [(4096, 4096), (1024, 4096), (14336, 4096)], [12, 16]),
     "w4a16sz_8b_batched": ("w4a16sz", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8]),
     "w4a16_8b_batched": ("w4a16", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [12, 16]),
     "w4a16t_8b": ("w4a16t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 12, 16]),
@@ -573,6 +574,8 @@ SUITE = {
     "w4a16_70b_engine": ("w4a16_engine", [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)], [1, 4, 8, 16]),
     "iq4nl_engine": ("iq4nl_engine", [(3584, 3584), (18944, 3584), (3584, 18944)], [1, 4, 8]),
     "iq4nl_batched": ("iq4nl", [(3584, 3584), (18944, 3584), (3584, 18944)], [4, 8]),
+    "iq4nl_wide": ("iq4nl", [(3584, 3584), (18944, 3584), (1024, 4096), (4096, 4096)], [12, 16]),
+    "iq4nlt_wide": ("iq4nlt", [(3584, 3584), (1024, 4096), (4096, 4096)], [12, 16]),
     # zt_gemm_iq4nl_f32: fp32 activations (the reference's IQ4_NL matmul input type)
     # zt_gemm_q4_f16: Q4_0 with fp16 activations (Float16Storage activations on the Q4_0 path)
     "q4_0h": ("q4_0h", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),

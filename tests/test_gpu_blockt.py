@@ -374,9 +374,10 @@ def test_engine_other_batch_sizes_on_tiled_kernels(lib, orc, fmt, n):
     assert y.shape == (rows, n)
     assert rel_err(y, ref) <= TOL
     chunk = -(-n // 4) * 4 if n < 16 else 16
-    if ((fmt == "iq4nl" and n < 12) or (fmt == "w4a16" and _w4a16_rowblock(rows, K, chunk)) or
+    if ((fmt == "iq4nl" and K <= 8192 and (chunk <= 8 or rows <= 4096)) or
+            (fmt == "w4a16" and _w4a16_rowblock(rows, K, chunk)) or
             (fmt in ("q4", "q4_f16", "q8") and _block_rowblock(fmt[:2], rows, K, chunk))):
-        # chunks of 4 or 8 columns run the row-block GEMM on the batch-1 upload
+        # chunks the row-block GEMM takes run on the batch-1 upload
         assert getattr(s, "_gpu_tiled", None) is None
     else:
         assert getattr(s, "_gpu_tiled", None) is not None

@@ -1,6 +1,6 @@
 """GPU parity of the single-launch batched IQ4_NL GEMM on the separated
 upload layout (zt_gemm_iq4nl_f16 with fp16 activations and N = 4, 8, 12 or
-16, the row-block kernel; past 2048 rows, N = 12 and 16 run the 16x16x32 MFMA
+16, the row-block kernel; past 4096 rows, N = 12 and 16 run the 16x16x32 MFMA
 kernel without a K split).
 
 The reference has no IQ4_NL matmul: CPUEngine.MatMul falls back to
@@ -59,11 +59,12 @@ def run(lib, raw, x16, rows, K, N):
 
 @pytest.mark.parametrize("N", [4, 8, 12, 16])
 @pytest.mark.parametrize("rows,K", [(1, 32), (3, 96), (5, 544), (17, 4128), (100, 8192), (64, 12288), (9, 32768),
-                                    (2049, 1024), (2100, 1024)])
+                                    (2049, 1024), (2100, 1024), (3000, 2080), (4096, 8192), (4097, 1024)])
 def test_iq4nl_rb_ragged(lib, orc, rows, K, N):
     """Partial row sets and workgroups, K not a multiple of a step (16
-    blocks), one to four steps a wave, and the 16x16x32 path past 2048
-    rows at N = 12 and 16."""
+    blocks), one to four steps a wave; at N = 12 and 16 two row sets (2049
+    to 3000 rows), four (4096, two steps a wave at K = 8192), and the
+    16x16x32 path past 4096 rows."""
     print(f"iq4nl rb rows={rows} K={K} N={N}", flush=True)
     w = synth.iq4nl(rows, K, 81)
     x16 = synth.x_f16(K * N, 81 + N)

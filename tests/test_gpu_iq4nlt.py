@@ -144,15 +144,17 @@ def test_iq4nlt_invalid_arguments(lib):
     assert lib.zt_iq4nl_tile(p, 2, 128, 8, p, p, stream()) == 1  # data not 16-byte aligned
 
 
+@pytest.mark.parametrize("rows", [512, 8192])
 @pytest.mark.parametrize("N", [8, 16])
 @pytest.mark.parametrize("side", ["A", "B"])
-def test_engine_batched_iq4nl_dispatch(lib, orc, side, N):
-    """16 columns build the tiled copy; 8 columns at K <= 8192 run the
-    row-block GEMM on the separated upload and build none."""
+def test_engine_batched_iq4nl_dispatch(lib, orc, side, N, rows):
+    """16 columns of the 8192-row matrix build the tiled copy; 8 columns
+    at K <= 8192, and 16 up to 4096 rows, run the row-block GEMM on the
+    separated upload and build none."""
     from ztensor_amd.engine import ROCmEngine
     from ztensor_amd.storage import IQ4NLStorage, Tensor
 
-    rows, K = 512, 1024
+    K = 1024
     w = synth.iq4nl(rows, K, 73)
     s = IQ4NLStorage.from_raw(w.raw, rows * K)
     eng = ROCmEngine()
@@ -166,7 +168,7 @@ def test_engine_batched_iq4nl_dispatch(lib, orc, side, N):
         y = eng.matmul(xk.t().contiguous(), Tensor((K, rows), s)).cpu().numpy()
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
-    assert (getattr(s, "_gpu_tiled", None) is not None) == (N == 16)
+    assert (getattr(s, "_gpu_tiled", None) is not None) == (N == 16 and rows > 4096)
 
 
 def test_iq4nlt_repeated_calls_bit_identical(lib):

@@ -79,12 +79,14 @@ def run_rm(lib, w, x16, N, zeros=True):
 @pytest.mark.parametrize("N", [4, 8, 12, 16])
 @pytest.mark.parametrize("rows,K,g", [(1, 32, 32), (3, 96, 32), (5, 128, 128), (17, 544, 32), (100, 4128, 32),
                                       (300, 8192, 256), (64, 12288, 128), (33, 16896, 64), (9, 32768, 128),
-                                      (2049, 1024, 128), (4100, 12320, 32)])
+                                      (2049, 1024, 128), (4100, 12320, 32), (3000, 2080, 32), (4100, 8192, 128),
+                                      (9000, 4096, 128)])
 def test_rb_ragged(lib, orc, rows, K, g, N):
     """Partial row sets and workgroups, K not a multiple of a step (512) or of
     16 waves' steps, group sizes 32-256, one to four steps a wave (K up to
     32768; 4100 x 12320: 4 row sets at four steps on 7 waves at N = 8, at two
-    steps on 13 waves at N = 4, a partial last workgroup), on both entry
+    steps on 13 waves at N = 4, a partial last workgroup; at N = 12 and 16,
+    3000 rows take 2 row sets, 4100 and 9000 rows 4), on both entry
     points."""
     if N >= 12 and K > 8192:
         pytest.skip("N >= 12 takes K <= 8192 on zt_gemm_w4a16sz_f32")
@@ -95,9 +97,9 @@ def test_rb_ragged(lib, orc, rows, K, g, N):
     a = run_sz(lib, w, x16, N)
     assert rel_err(a, ref) <= TOL
     b = run_rm(lib, w, x16, N)
-    if N <= 8 or rows <= 2048:  # the row-major entry runs the same kernel
+    if N <= 8 or rows <= 4096:  # the row-major entry runs the same kernel
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    else:  # past 2048 rows it runs batches of 12 and 16 on the 16x16x32 MFMA kernel
+    else:  # past 4096 rows it runs batches of 12 and 16 on the 16x16x32 MFMA kernel
         assert rel_err(b, ref) <= TOL
 
 

@@ -200,12 +200,12 @@ def test_w4t_invalid_arguments(lib):
     assert lib.zt_w4a16_tile(p + 8, p, 0, 2, 128, 32, p, p, stream()) == 1  # W_packed alignment
 
 
-@pytest.mark.parametrize("rows", [512, 4096])
+@pytest.mark.parametrize("rows", [512, 8192])
 @pytest.mark.parametrize("N", [8, 16])
 @pytest.mark.parametrize("side", ["A", "B"])
 def test_engine_batched_w4a16_dispatch(lib, orc, side, N, rows):
     """ROCmEngine.matmul_w4a16 with 8 or 16 activation columns (A side) or
-    rows (B side) matches the oracle.  16 columns of the 4096-row matrix
+    rows (B side) matches the oracle.  16 columns of the 8192-row matrix
     build the tiled copy once; 8 columns, and 16 of the 512-row matrix, run
     the row-block GEMM on the row-major upload and build none."""
     from ztensor_amd.engine import ROCmEngine
@@ -228,7 +228,7 @@ def test_engine_batched_w4a16_dispatch(lib, orc, side, N, rows):
         y = eng.matmul_w4a16(act, Tensor((K, rows), st)).cpu().numpy()
         want = ref.T
     assert rel_err(y.reshape(-1), want.reshape(-1)) <= TOL
-    assert (getattr(st, "_gpu_tiled", None) is not None) == (N == 16 and rows > 2048)
+    assert (getattr(st, "_gpu_tiled", None) is not None) == (N == 16 and rows > 4096)
 
 
 def _w4t_call(lib, wt, sz, xd, c, rows, K, N, s, ws):

@@ -940,7 +940,7 @@ __global__ void __launch_bounds__(512) iq4nl_mfma_kernel(const uint16_t* __restr
 //    within 2^-22 per entry, with every product exact;
 //  * the block's sum then takes the block's fp16 scale: y += d D.
 template <int NB, int R, int S>
-__global__ void __launch_bounds__(1024) iq4nl_rb_kernel(const uint16_t* __restrict__ scales,
+__global__ void __launch_bounds__(NB > 2 && R > 1 ? 512 : 1024) iq4nl_rb_kernel(const uint16_t* __restrict__ scales,
                                                         const uint32_t* __restrict__ data,
                                                         const uint16_t* __restrict__ x, float* __restrict__ y,
                                                         int rows, int kb) {
@@ -1057,6 +1057,7 @@ static void launch_iq4nl_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, cons
     if (R == RR && S == SS) return launch_iq4nl_rb_t<NB, RR, SS>(g, nw, st, sc, data, x, y, rows, kb);
     ZT_RB(1, 1) ZT_RB(1, 2)
     if constexpr (NB <= 2) { ZT_RB(2, 1) ZT_RB(2, 2) ZT_RB(1, 4) ZT_RB(2, 4) ZT_RB(4, 1) }
+    if constexpr (NB > 2) { ZT_RB(2, 1) ZT_RB(2, 2) ZT_RB(4, 1) ZT_RB(4, 2) }  // at most 8 waves: 512 threads
 #undef ZT_RB
 }
 
@@ -1078,8 +1079,10 @@ static int launch_iq4nl_rb(const uint16_t* sc, const uint32_t* data, const uint1
     // 8.13 / 6.10 / 6.00; at 18944 x 3584, batch 8: 32.4 / 21.4 / 17.4 us (fewer activation bytes
     // staged per weight byte).  A sweep of 1-8 row sets x 1, 2 or 4 steps a wave (4 row sets past
     // one step and 8 under a 512-thread bound) at the Qwen2-7B shapes, batches 4 and 8, found
-    // nothing more than 2% faster than this choice.
-    const int rmax = N >= 12 ? 1 : S == 1 ? 4 : 2;
+    // nothing more than 2% faster than this choice.  N >= 12 (at most 8 waves, the 512-thread
+    // bound for more than one row set) takes up to 4: batch 16 at 3584 x 3584 19.3 / 12.0 / 8.0 us
+    // with 1 / 2 / 4 row sets.
+    const int rmax = N >= 12 ? 4 : S == 1 ? 4 : 2;
     int R = 1;
     while (R < rmax && ceil_div(M, 8 * R) >= 200) R *= 2;
     const dim3 g(ceil_div(M, 4 * R));
@@ -1309,8 +1312,9 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
             return (int)hipGetLastError();
     }
     if constexpr (F == Fmt::IQ4NL && sizeof(XT) == 2) {
-        // N = 4, 8 (12, 16 on up to 2048 rows): the row-block GEMM, one launch
-        if (iq4nl_rb_ok(N, kb, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 2048))
+        // N = 4, 8 (12, 16 on up to 4096 rows; past that the 16x16x32 kernel below is as fast or
+        // faster: 31.1 against 31.3 us at 18944 x 3584, batch 12): the row-block GEMM, one launch
+        if (iq4nl_rb_ok(N, kb, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 4096))
             return launch_iq4nl_rb(sc, reinterpret_cast<const uint32_t*>(data), reinterpret_cast<const uint16_t*>(B),
                                    C, M, kb, N, st);
         if (mfma_shape_ok(N, K, B)) {

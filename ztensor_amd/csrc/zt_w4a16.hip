@@ -443,7 +443,7 @@ __device__ __forceinline__ half4v rb_w4_operand(uint32_t q, int odd, uint32_t ma
 // a wave run at most 8 waves (the launch shape keeps them there), so 512
 // threads leave them up to 256 VGPRs (the 1024-thread bound spills the
 // two-step form); everything else may take 16 waves.
-constexpr int w4rb_bound(int NB, int R, int S) { return NB == 2 && R == 4 && S >= 2 ? 512 : 1024; }
+constexpr int w4rb_bound(int NB, int R, int S) { return (NB == 2 && R == 4 && S >= 2) || (NB > 2 && R > 1) ? 512 : 1024; }
 
 template <int NB, int R, int S, bool SZ>
 __global__ void __launch_bounds__(w4rb_bound(NB, R, S)) w4a16_rb_kernel(const uint32_t* __restrict__ packed,
@@ -597,7 +597,7 @@ static void launch_w4a16_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, cons
     if constexpr (NB == 2) {
         ZT_RB(4, 4)
     } else if constexpr (NB > 2) {
-        ZT_RB(1, 1) ZT_RB(1, 2)
+        ZT_RB(1, 1) ZT_RB(1, 2) ZT_RB(2, 1) ZT_RB(2, 2) ZT_RB(4, 1) ZT_RB(4, 2)
     }
 #undef ZT_RB
 }
@@ -606,7 +606,7 @@ static void launch_w4a16_rb_n(int R, int S, dim3 g, int nw, hipStream_t st, cons
 // splitting K (8 for N >= 8: 8-column activation blocks take 8 KB of LDS a
 // wave, so 8 waves let two or more workgroups share a CU; N >= 12 also caps
 // VGPRs), and R row sets a workgroup (up to 4) doubled while about 256
-// workgroups remain; N >= 12: one row set.  Measured on the packed-scale
+// workgroups remain.  Measured on the packed-scale
 // kernel (us, default against the former >= 512 workgroups and 16 waves at
 // N = 8): batch 8 4096 x 14336 (rows x K) 12.18 against 15.20, 28672 x
 // 8192 37.97 against 42.83, 8192 x 8192 13.16 against 13.68, 4096 x 4096
@@ -617,8 +617,11 @@ static void w4a16_rb_shape(int M, int N, int nchunk, int& R, int& S, int& nw) {
     S = steps <= wmax ? 1 : steps <= 2 * wmax ? 2 : 4;
     nw = ceil_div(steps, S);
     // four steps a wave on more than 8 waves (N = 8: K > 16384) keeps 2 row
-    // sets: 4 need the 512-thread bound
-    const int rmax = N >= 12 ? 1 : (S == 4 && (nw > 8 || N == 4)) ? 2 : 4;
+    // sets: 4 need the 512-thread bound.  N >= 12 runs at most 8 waves, so its
+    // 2 and 4 row sets take the 512-thread bound too (us, batch 16, 1 / 2 / 4
+    // row sets: 4096 x 4096 12.9 / 8.4 / 6.4, 14336 x 4096 42.1 / 26.0 / 20.6,
+    // 28672 x 8192 123.7 / 84.9 / 63.4)
+    const int rmax = (S == 4 && (nw > 8 || N == 4)) ? 2 : 4;
     R = 1;
     while (R < rmax && ceil_div(M, 8 * R) >= 256) R *= 2;
     // few rows (one row set a workgroup) and K of 16 steps or more: two steps a
@@ -826,10 +829,10 @@ ZT_EXPORT int zt_gemm_w4a16_f32(const void* W_packed, const uint16_t* scales, co
     if (((uintptr_t)W_packed & 15) || ((uintptr_t)scales & 1) || ((uintptr_t)zeros & 1))
         return (int)hipErrorInvalidValue;
     if (N == 1 && ((uintptr_t)B & 15)) return (int)hipErrorInvalidValue;
-    // N = 4, 8 (and 12, 16 on up to 2048 rows, where the 32-row workgroups below would leave most
-    // CUs idle: 4.3 against 9.7 us at 1024 x 4096, batch 16; from 4096 rows the 16x16x32 kernel is
-    // faster, 10.2 against 13.3 us at 4096 x 4096)
-    if (w4a16_rb_ok(N, K / 32, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 2048))
+    // N = 4, 8 (and 12, 16 on up to 4096 rows, where the 32-row workgroups below would leave most
+    // CUs idle: 4.3 against 9.7 us at 1024 x 4096, batch 16, and 6.4 against 9.9 at 4096 x 4096;
+    // past that the 16x16x32 kernel is faster, 15.2 against 20.6 us at 14336 x 4096)
+    if (w4a16_rb_ok(N, K / 32, M) && ((uintptr_t)B & 15) == 0 && (N <= 8 || M <= 4096))
         return launch_w4a16_rb<false>(static_cast<const uint32_t*>(W_packed), scales, zeros, B, C, M, K, N,
                                       group_size, stream);
     if (mfma_shape_ok(N, K, B) && group_size % 128 == 0) {

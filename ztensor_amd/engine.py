@@ -461,10 +461,12 @@ class ROCmEngine:
         elif isinstance(s, IQ4NLStorage):
             if x.dtype == torch.float32:
                 self.gemm_iq4nl_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
-            elif x.dtype == torch.float16 and n in (4, 8) and k <= 8192 and _p(x) % 16 == 0:
+            elif (x.dtype == torch.float16 and k <= 8192 and _p(x) % 16 == 0
+                  and (n in (4, 8) or (n in (12, 16) and rows <= 4096))):
                 # one launch on the separated upload (the row-block GEMM): no tiled copy, no workspace;
                 # faster than the tiled layout at K <= 8192 (3584 x 3584: 5.0 / 6.0 against 7.3 / 7.5 us at
-                # batch 4 / 8), slower past it (K = 18944, batch 8: 23.8 against 15.7 us)
+                # batch 4 / 8), slower past it (K = 18944, batch 8: 23.8 against 15.7 us); batches of 12
+                # and 16 up to 4096 rows (4096 x 4096: 7.5 / 8.4 against 9.0 / 8.9 us)
                 self.gemm_iq4nl_f16(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
             elif x.dtype == torch.float16 and n in _TILED_BATCHES and k % 128 == 0:
                 wt, st = self._iq4nl_tiled(s, buf, rows, k)
@@ -775,16 +777,16 @@ def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
     10.0 / 11.3, 8192 x 28672 37.1 / 29.7; batch 8 at 14336 x 4096
     11.8 / 12.8, 4096 x 4096 4.9 / 6.8, 1024 x 8192 4.1 / 6.0, 8192 x 8192
     13.2 / 12.5, 4096 x 14336 12.3 / 11.6, 28672 x 8192 37.7 / 29.0; batch
-    16 at 1024 x 8192 5.98 / 6.22, 8192 x 8192 37.3 / 13.5.  A batch-8
-    workgroup re-reads more activation bytes than weight bytes once the rows
-    are many and K is long; batches of 12 and 16 take one row set a
-    workgroup, which only few-row matrices afford."""
+    16 at 1024 x 8192 5.98 / 6.22, 4096 x 4096 6.4 / 7.0, 8192 x 8192
+    20.4 / 12.9, 14336 x 4096 20.6 / 13.7.  A row-block workgroup re-reads
+    more activation bytes than weight bytes once the rows are many and K is
+    long, more so at 12 and 16 columns."""
     if k > 32768:
         return False
     if n == 4:
         return k <= 16384
     if n in (12, 16):
-        return k <= 8192 and rows <= 2048
+        return k <= 8192 and rows <= 4096
     return k <= 4096 or rows <= 2048
 
 
