@@ -553,6 +553,7 @@ SUITE = {
     "q4_0": ("q4_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "q4_0_merged": ("q4_0", [(6144, 4096), (28672, 4096)], [1]),
     "q8_0": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
+    "rbf8": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
     "q8_0_raw": ("q8_0_raw", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "ternary_f32": ("ternary_f32", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
