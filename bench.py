@@ -1143,6 +1143,24 @@ def cpu_configs(budget_s: float = 2.0) -> dict:
     return out
 
 
+def summarize_trace(path: str) -> None:
+    """Per-launch-shape durations from a rocprofv3 kernel-trace CSV, as a
+    markdown table: kernel, grid and block size, calls, median and mean us.
+    The --stats averages mix every shape a kernel runs; this splits them."""
+    import csv
+    import statistics
+
+    groups: dict = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            key = (r["Kernel_Name"][:60], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| kernel | grid (threads) | block | calls | median us | mean us |")
+    print("|---|---|---|---|---|---|")
+    for (name, grid, block), v in sorted(groups.items()):
+        print(f"| `{name}` | {grid} | {block} | {len(v)} | {statistics.median(v):.3f} | {statistics.fmean(v):.3f} |")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1164,7 +1182,12 @@ def main() -> None:
                          "format at that shape (e.g. iq4nlt:3584:3584:8)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="run 64 MiB device copies first (reference kernel for rocprofv3 byte counters)")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print per-launch-shape durations of a rocprofv3 kernel-trace CSV and exit (no GPU)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this path runs on one GPU; multi-GPU runs are not part of this build. "
               "Sharded, each GPU would run the same kernels on its slice: output rows for q/k/v/gate/up, "
