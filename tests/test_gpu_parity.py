@@ -500,10 +500,11 @@ def test_ternary_f32_reference_known_answers(lib, orc):
 
 @pytest.mark.parametrize("rows,K", BITNET + [(7, 33), (128, 256), (65, 2560), (6, 65536), (4, 65600), (1501, 256),
                                               (16397, 128), (3, 4096), (2049, 64),
-                                              # activations staged in LDS: 8 row groups of 4 rows at one wave
-                                              # a row group, 4 at two; partial last workgroups, K not a
-                                              # multiple of a wave's 4096
-                                              (6405, 2560), (8191, 64), (2053, 6912), (4099, 8192)])
+                                              # the quad mapping (K <= 16384, K % 64 == 0): partial row groups,
+                                              # lanes past the row's last dword, 1 to 16 waves, 1, 2 or 4 rows
+                                              # a wave; past K = 16384 one lane a chunk
+                                              (6405, 2560), (8191, 64), (2053, 6912), (4099, 8192), (1, 64),
+                                              (131, 1088), (9, 16384), (5, 16448), (300, 4160)])
 def test_ternary_f32_matches_oracle(lib, orc, rows, K):
     t = synth.ternary(rows, K, 77)
     x = synth.x_f32(K, 77)

@@ -23,7 +23,9 @@
 // a workgroup split K and combine through LDS.  With K % 64 == 0 (every
 // BitNet shape) both activation types take a fixed-step form of the same
 // split (ternary_i8_steps_kernel, ternary_f32_steps_kernel) with every load
-// issued first.
+// issued first; f32 activations up to K = 16384 take the quad mapping
+// instead (ternary_f32_quad_kernel: four lanes a 16-byte chunk, a dword of
+// codes and 16 activations a lane).
 #include "zt_common.h"
 
 namespace zt {
@@ -341,71 +343,57 @@ __global__ void __launch_bounds__(1024) ternary_f32_steps_kernel(const uint8_t* 
 }
 
 
-// The same with the activations staged once per workgroup in LDS: G row
-// groups of R rows, each on nw waves that split K as above, share one copy of
-// x, so global activation reads drop by G (fp32 activations are 16 times the
-// bytes of the 2-bit codes they meet; the int8 kernel's activations, 4).  The 16-byte pieces of x are stored
-// rotated inside each 256-byte chunk (piece j of chunk c at slot (j + c) mod
-// 16), so the 64 lanes of a wave, each reading piece j of its own chunk,
-// address 16 distinct slots.
+// fp32 x on the quad mapping: four lanes a 16-byte chunk, lane 4c + q taking
+// dword q (the codes of elements 64c + 16q .. +15) of R rows and those 16
+// activations (four 16-byte loads), waves splitting the row's chunks 16 a
+// wave.  A quarter of the per-lane work of the kernel above and four times the
+// lanes, for rows whose K leaves that kernel's single wave mostly idle or
+// short of parallelism.
 template <int R>
-__global__ void __launch_bounds__(1024) ternary_f32_lds_kernel(const uint8_t* __restrict__ W,
-                                                               const float* __restrict__ x, float* __restrict__ y,
-                                                               int rows, int bpr, int nw, int G) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    u32x4* xs = reinterpret_cast<u32x4*>(smem);            // bpr / 16 chunks of 16 pieces
-    float* red = reinterpret_cast<float*>(smem + bpr * 16);  // [waves][R]
+__global__ void __launch_bounds__(1024) ternary_f32_quad_kernel(const uint8_t* __restrict__ W,
+                                                                const float* __restrict__ x, float* __restrict__ y,
+                                                                int rows, int bpr, int nw) {
+    __shared__ float red[16 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int grp = wave / nw, wg = wave % nw;                // row group, wave within it
-    const int row0 = (blockIdx.x * G + grp) * R;
-    const int nchunk = bpr / 16;
-    // stage x: piece f = 16 c + j (floats 4f .. 4f + 3) to slot 16 c + ((j + c) & 15)
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, bpr * 16, 0x00020000);
-    for (int f = threadIdx.x; f < nchunk * 16; f += blockDim.x) {
-        const int c = f >> 4, j = f & 15;
-        xs[c * 16 + ((j + c) & 15)] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)f * 16u, 0, 0);
-    }
-    const int c = wg * 64 + lane;  // 16-byte chunk of the row: codes of elements 64c .. 64c+63
-    const bool ok = c < nchunk;
-    const uint32_t voff = ok ? (uint32_t)c * 16u : 0x80000000u;
+    const int row0 = blockIdx.x * R;
+    const int e = wave * 64 + lane;  // dword of the row: codes of elements 16e .. 16e+15
+    const bool ok = e * 4 < bpr;
+    const uint32_t voff = ok ? (uint32_t)e * 4u : 0x80000000u;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, 0x00020000);
-    u32x4 w[R];
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, bpr * 16, 0x00020000);
+    uint32_t w[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
-        w[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff, row * (uint32_t)bpr, 2);  // nontemporal
+        w[r] = __builtin_amdgcn_raw_buffer_load_b32(rw, voff, row * (uint32_t)bpr, 2);  // nontemporal
     }
-    __syncthreads();
-    float xv[64];
-    const int cc = ok ? c : 0;
+    u32x4 xv[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const u32x4 v = xs[cc * 16 + ((i + cc) & 15)];
-        const bool z = !ok;
-        xv[4 * i] = z ? 0.0f : __uint_as_float(v.x);
-        xv[4 * i + 1] = z ? 0.0f : __uint_as_float(v.y);
-        xv[4 * i + 2] = z ? 0.0f : __uint_as_float(v.z);
-        xv[4 * i + 3] = z ? 0.0f : __uint_as_float(v.w);
+    for (int i = 0; i < 4; i++)
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (uint32_t)e * 64u + 16u * i : 0x80000000u, 0, 0);
+    float xs[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        xs[4 * i] = __uint_as_float(xv[i].x);
+        xs[4 * i + 1] = __uint_as_float(xv[i].y);
+        xs[4 * i + 2] = __uint_as_float(xv[i].z);
+        xs[4 * i + 3] = __uint_as_float(xv[i].w);
     }
-    float xsum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 64; e += 4) xsum += (xv[e] + xv[e + 1]) + (xv[e + 2] + xv[e + 3]);
+    const float xsum = ((xs[0] + xs[1]) + (xs[2] + xs[3])) + ((xs[4] + xs[5]) + (xs[6] + xs[7])) +
+                       (((xs[8] + xs[9]) + (xs[10] + xs[11])) + ((xs[12] + xs[13]) + (xs[14] + xs[15])));
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int s2 = 0; s2 < 4; s2++) {
-                // codes of elements 16i + 4j + s2, j = 0..3, one per byte
-                const uint32_t cds = (wd[i] >> (2 * s2)) & 0x03030303u;
-                s0 = fmaf((float)(cds & 0xffu), xv[16 * i + s2], s0);
-                s1 = fmaf((float)((cds >> 8) & 0xffu), xv[16 * i + 4 + s2], s1);
-                s0 = fmaf((float)((cds >> 16) & 0xffu), xv[16 * i + 8 + s2], s0);
-                s1 = fmaf((float)(cds >> 24), xv[16 * i + 12 + s2], s1);
-            }
+        for (int s = 0; s < 4; s++) {
+            // codes of elements 4j + s, j = 0..3, one per byte
+            const uint32_t cds = (w[r] >> (2 * s)) & 0x03030303u;
+            s0 = fmaf((float)(cds & 0xffu), xs[s], s0);
+            s1 = fmaf((float)((cds >> 8) & 0xffu), xs[4 + s], s1);
+            s0 = fmaf((float)((cds >> 16) & 0xffu), xs[8 + s], s0);
+            s1 = fmaf((float)(cds >> 24), xs[12 + s], s1);
+        }
         acc[r] = (s0 + s1) - xsum;
     }
     wave_reduce_rows<R>(acc);
@@ -418,13 +406,14 @@ __global__ void __launch_bounds__(1024) ternary_f32_lds_kernel(const uint8_t* __
     }
     if (is_row_writer<R>(lane)) red[wave * R + row_of_lane<R>(lane)] = acc[0];
     __syncthreads();
-    if (lane < R && wg == 0) {
+    if ((int)threadIdx.x < R) {
         float sm = 0.0f;
-        for (int w2 = 0; w2 < nw; w2++) sm += red[(grp * nw + w2) * R + lane];
-        const int r = row0 + lane;
+        for (int w2 = 0; w2 < nw; w2++) sm += red[w2 * R + threadIdx.x];
+        const int r = row0 + threadIdx.x;
         if (r < rows) y[r] = sm;
     }
 }
+
 
 template <int CB, int R>
 __global__ void __launch_bounds__(512) ternary_f32_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
@@ -524,29 +513,29 @@ static int ternary_gemv(bool i8, const void* Wv, const void* x, const float* xs,
     const int bpr = (K + 3) / 4;
     if (!i8 && K % 64 == 0 && K <= 65536 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
         (long)M * bpr < 0x7fffffffL) {
-        // 4 rows a wave, as for int8 (at the BitNet shapes R = 1 / 2 / 4 / 8
-        // measured 5.33 / 3.87 / 3.77 / 3.77, 10.7 / 6.75 / 5.52 / 6.30 and
-        // 11.4 / 7.71 / 6.18 / 7.74 us)
-        const int nw = (K + 4095) / 4096;
-        int R = 4;
-        while (R > 1 && (long)ceil_div(M, R) * nw < 512) R >>= 1;
         const float* xf = static_cast<const float*>(x);
-        // x staged in LDS for G row groups a workgroup while enough workgroups
-        // remain: 8 at one wave a row group, 4 at two (us, old against staged:
-        // 6912 x 2560 5.54 / 4.75 with G = 8, 2560 x 6912 6.18 / 5.08 with
-        // G = 4; at 2560 x 2560, 160 workgroups of G = 4 took 3.94 against
-        // 3.77, so few rows keep one wave group per workgroup)
-        const int G = nw == 1 ? 8 : nw == 2 ? 4 : 0;
-        if (G > 0 && ceil_div(M, G * R) >= (nw == 1 ? 200 : 128)) {
-            const size_t lds = (size_t)bpr * 16 + (size_t)G * nw * R * 4;  // K <= 8192: <= 32 KB
-            const dim3 g(ceil_div(M, G * R)), b(G * nw * kWave);
-            switch (R) {
-                case 4: ternary_f32_lds_kernel<4><<<g, b, lds, st>>>(W, xf, y, M, bpr, nw, G); break;
-                case 2: ternary_f32_lds_kernel<2><<<g, b, lds, st>>>(W, xf, y, M, bpr, nw, G); break;
-                default: ternary_f32_lds_kernel<1><<<g, b, lds, st>>>(W, xf, y, M, bpr, nw, G); break;
+        if (K <= 16384) {
+            // the quad mapping, 4 rows a wave (measured, us, against one lane a chunk of 64 codes,
+            // with x staged in LDS for several row groups where that was faster: 2560 x 2560
+            // 2.97 / 3.79, 6912 x 2560 3.85 / 4.75, 2560 x 6912 4.73 / 5.10; 2 / 8 rows a wave:
+            // 3.25 / 3.23, 5.12 / 4.06, 6.16 / 4.95)
+            const int nq = ceil_div(bpr / 4, 64);  // waves: 64 dwords of codes each
+            int Rq = 4;
+            while (Rq > 1 && (long)ceil_div(M, Rq) * nq < 512) Rq >>= 1;
+            const dim3 g(ceil_div(M, Rq)), b(nq * kWave);
+            switch (Rq) {
+                case 4: ternary_f32_quad_kernel<4><<<g, b, 0, st>>>(W, xf, y, M, bpr, nq); break;
+                case 2: ternary_f32_quad_kernel<2><<<g, b, 0, st>>>(W, xf, y, M, bpr, nq); break;
+                default: ternary_f32_quad_kernel<1><<<g, b, 0, st>>>(W, xf, y, M, bpr, nq); break;
             }
             return (int)hipGetLastError();
         }
+        // past K = 16384: one lane a chunk, 4 rows a wave (at the BitNet shapes R = 1 / 2 / 4 / 8
+        // measured 5.33 / 3.87 / 3.77 / 3.77, 10.7 / 6.75 / 5.52 / 6.30 and 11.4 / 7.71 / 6.18 /
+        // 7.74 us)
+        const int nw = (K + 4095) / 4096;
+        int R = 4;
+        while (R > 1 && (long)ceil_div(M, R) * nw < 512) R >>= 1;
         const dim3 g(ceil_div(M, R)), b(nw * kWave);
         switch (R) {
             case 4: ternary_f32_steps_kernel<4><<<g, b, 0, st>>>(W, xf, y, M, bpr, nw); break;
