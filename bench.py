@@ -600,7 +600,8 @@ SUITE = {
     "int4_gemm": ("int4", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int4_rmul_gemm": ("int4_rmul", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
     "int8_gemm": ("int8", [(1024, 1024), (2048, 2048), (4096, 4096)], ["square"]),
-    "intq_mid": ("int4", [(4096, 4096)], [32, 64, 128, 256]),
+    "intq_mid": ("int4", [(4096, 4096), (14336, 4096)], [96, 128, 256]),
+    "int8_mid": ("int8", [(4096, 4096), (4096, 14336)], [96, 128, 256]),
     "q8_0_batched": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
     "q8_0_raw_batched": ("q8_0_raw", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8]),
     "q4_0t": ("q4_0t", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [4, 8, 16]),
