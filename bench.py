@@ -903,7 +903,7 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         r["TFLOP/s"] = round(tf, 2)
         bf16 = fmt != "int4_rmul" and K % 32 == 0 and N % 2 == 0
         if bf16:
-            ti = 4 if -(-rows // 128) * -(-N // 128) >= 256 else 2
+            ti = 4 if -(-rows // 128) * -(-N // 128) >= 256 else 1 if -(-rows // 64) * -(-N // 64) < 256 else 2
             work = 3.0 if fmt == "int8" else 3.0 + 3.0 / ti
             r["mfma"] = "bf16"
             r["mfma_TFLOP/s"] = round(tf * work, 1)
