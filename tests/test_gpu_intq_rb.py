@@ -78,6 +78,8 @@ INT4_CASES = [  # M, K, N, group_size
     (515, 10240, 4, 128), (515, 10240, 8, 128), (259, 20480, 4, 64), (130, 32768, 4, 128), (130, 32768, 16, 256),
     # 20-64 columns while M N <= 2^19
     (4096, 4096, 64, 128), (1000, 2048, 36, 64), (8191, 1024, 60, 32),
+    # 8 row sets at one step (4-column groups), 2 row sets at four steps on 10 waves
+    (14336, 4096, 4, 32), (4096, 20480, 4, 128), (4096, 20480, 8, 64),
 ]
 
 
@@ -96,6 +98,8 @@ INT8_CASES = [  # M, K, N
     (130, 32768, 4), (130, 32768, 8),
     # 20-64 columns while M N <= 2^18
     (4096, 4096, 64), (1000, 2048, 36), (2047, 1024, 60),
+    # 4 row sets at one step, 2 at two and four steps
+    (14336, 4096, 4), (4096, 12288, 4), (4096, 20480, 4),
 ]
 
 
