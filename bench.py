@@ -554,6 +554,9 @@ SUITE = {
     "q4_0_merged": ("q4_0", [(6144, 4096), (28672, 4096)], [1]),
     "q8_0": ("q8_0", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "rbf8": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [8, 16]),
+    "q4_0_prefill": ("q4_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [32, 64, 128, 512]),
+    "q8_0_prefill": ("q8_0", [(4096, 4096), (14336, 4096), (4096, 14336)], [32, 64, 128, 512]),
+    "q8_0_raw_prefill": ("q8_0_raw", [(4096, 4096), (14336, 4096), (4096, 14336)], [32, 64, 128, 512]),
     "q8_0_raw": ("q8_0_raw", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)], [1]),
     "ternary": ("ternary_i8", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
     "ternary_f32": ("ternary_f32", [(2560, 2560), (6912, 2560), (2560, 6912)], [1]),
@@ -903,7 +906,8 @@ def _suite_case(torch, lib, fmt: str, rows: int, K: int, N: int, seed: int, eage
         r["TFLOP/s"] = round(tf, 2)
         bf16 = fmt != "int4_rmul" and K % 32 == 0 and N % 2 == 0
         if bf16:
-            ti = 4 if -(-rows // 128) * -(-N // 128) >= 256 else 1 if -(-rows // 64) * -(-N // 64) < 256 else 2
+            ti = (4 if -(-rows // 128) * -(-N // 128) >= 256
+                  else 1 if -(-rows // 64) * -(-N // 64) < (192 if fmt == "int4" else 256) else 2)
             work = 3.0 if fmt == "int8" else 3.0 + 3.0 / ti
             r["mfma"] = "bf16"
             r["mfma_TFLOP/s"] = round(tf * work, 1)

@@ -35,6 +35,7 @@
 
 #include "zt_common.h"
 #include "zt_mfma.h"
+#include "zt_bf16gemm.h"
 #include "zt_rbmfma.h"
 
 namespace zt {
@@ -860,11 +861,25 @@ __device__ __forceinline__ uint32_t hi16_pack(float a, float b) {
     return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
 }
 
-template <bool INT4, int TI, int PF>
-__global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restrict__ A, const float* __restrict__ B,
-                                                        float* __restrict__ C, const float* __restrict__ scales,
+// Weight formats of the bf16 MFMA GEMM (one 32-K step is one block or group
+// of 32 elements):
+//   I4: group-quantized int4 (A [M, K/2], fp32 scales and uint8 zeros [M, ng]);
+//   I8: plain int8 (A [M, K]);
+//   Q4_0: the separated Q4_0 upload's data region (16 bytes a block, element j
+//     the low nibble of byte j and j + 16 the high) with fp16 scales [M, K/32];
+//     the operand is 128 + u for the nibble u and the offset 136 (w = u - 8);
+//   Q8_F32 / Q8_F16: separated Q8_0 (32 int8 a block), fp32 or fp16 scales;
+//   Q8_RAW: the 36-byte blocks [fp32 scale][32 x int8].
+enum class BfFmt { I4, I8, Q4_0, Q8_F32, Q8_F16, Q8_RAW };
+
+template <BfFmt F, int TI, int PF>
+__global__ void __launch_bounds__(256) bf16_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ B,
+                                                        float* __restrict__ C, const void* __restrict__ scales,
                                                         const uint8_t* __restrict__ zeros, int M, int N, int K, int gs,
                                                         int ng) {
+    constexpr bool INT4 = F == BfFmt::I4;                  // nibbles in the 0 4 1 5 2 6 3 7 slot order
+    constexpr bool OFF = INT4 || F == BfFmt::Q4_0;          // an offset times sum x per step and row
+    constexpr bool SCALED = F != BfFmt::I8;                 // a scale per step and row
     constexpr int TM = 32 * TI, TN = 32 * TI, CP = 16 * TI;  // tile, column pairs
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][3][TN][kBfLP];
     __shared__ float scs[2][TM], zzs[2][TM];
@@ -873,7 +888,7 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
     int byi = blockIdx.y, bxi = blockIdx.x;
     const int m0 = byi * TM, n0 = bxi * TN;
     const int wm = (wave & 1) * 16 * TI, wn = (wave >> 1) * 16 * TI;
-    const long rowbytes = INT4 ? K / 2 : K;
+    const long rowbytes = (INT4 || F == BfFmt::Q4_0) ? K / 2 : F == BfFmt::Q8_RAW ? (long)(K / 32) * 36 : K;
     // this lane's A rows (one per row tile), clamped; rows past M load zeros
     int arow[TI];
     bool aok[TI];
@@ -902,21 +917,47 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
         constexpr int P = decltype(parc)::value;
 #pragma unroll
         for (int i = 0; i < TI; i++) {
-            const long off = (long)arow[i] * rowbytes + (INT4 ? (k0 + 8 * lg) / 2 : k0 + 8 * lg);
-            if constexpr (INT4)
+            if constexpr (INT4) {
+                const long off = (long)arow[i] * rowbytes + (k0 + 8 * lg) / 2;
                 araw4[P][i] = aok[i] ? *reinterpret_cast<const uint32_t*>(A + off) : 0x88888888u;  // u' = 0
-            else
+            } else if constexpr (F == BfFmt::Q4_0) {
+                // elements 8 lg .. 8 lg + 7 of block k0 / 32: the low (lg < 2) or high nibbles of bytes
+                // 8 (lg & 1) .. +7
+                const long off = (long)arow[i] * rowbytes + (k0 / 32) * 16 + 8 * (lg & 1);
                 araw8[P][i] = aok[i] ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
+            } else if constexpr (F == BfFmt::Q8_RAW) {
+                // 4-byte aligned only: two dword loads
+                const long off = (long)arow[i] * rowbytes + (k0 / 32) * 36 + 4 + 8 * lg;
+                araw8[P][i] = aok[i] ? make_uint2(*reinterpret_cast<const uint32_t*>(A + off),
+                                                  *reinterpret_cast<const uint32_t*>(A + off + 4))
+                                     : make_uint2(0u, 0u);
+            } else {
+                const long off = (long)arow[i] * rowbytes + k0 + 8 * lg;
+                araw8[P][i] = aok[i] ? *reinterpret_cast<const uint2*>(A + off) : make_uint2(0u, 0u);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 8; r++)
             braw[P][r] = bok ? *reinterpret_cast<const float2*>(B + (long)(k0 + 8 * ko + r) * N + bn) : make_float2(0.f, 0.f);
-        if constexpr (INT4) {
-            if (tid < TM) {  // every step: each set holds its own step's group
+        if constexpr (SCALED) {
+            if (tid < TM) {  // every step: each set holds its own step's scale (and offset)
                 const int m = m0 + tid;
-                const long gi = (long)(m < M ? m : 0) * ng + k0 / gs;
-                sreg[P] = m < M ? scales[gi] : 0.0f;
-                zreg[P] = 136.0f + (float)zeros[gi];
+                const bool mok = m < M;
+                const long mr = mok ? m : 0, bi = mr * (K / 32) + k0 / 32;
+                if constexpr (INT4) {
+                    const long gi = mr * ng + k0 / gs;
+                    sreg[P] = mok ? static_cast<const float*>(scales)[gi] : 0.0f;
+                    zreg[P] = 136.0f + (float)zeros[gi];
+                } else if constexpr (F == BfFmt::Q4_0) {
+                    sreg[P] = mok ? h2f(static_cast<const uint16_t*>(scales)[bi]) : 0.0f;
+                    zreg[P] = 136.0f;
+                } else if constexpr (F == BfFmt::Q8_F32) {
+                    sreg[P] = mok ? static_cast<const float*>(scales)[bi] : 0.0f;
+                } else if constexpr (F == BfFmt::Q8_F16) {
+                    sreg[P] = mok ? h2f(static_cast<const uint16_t*>(scales)[bi]) : 0.0f;
+                } else {  // Q8_RAW: the block's first 4 bytes
+                    sreg[P] = mok ? *reinterpret_cast<const float*>(A + mr * rowbytes + (k0 / 32) * 36) : 0.0f;
+                }
             }
         }
     };
@@ -949,10 +990,10 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
             *reinterpret_cast<u32x4*>(&Bs[buf][1][n][8 * ko]) = (u32x4){p2[0], p2[1], p2[2], p2[3]};
             *reinterpret_cast<u32x4*>(&Bs[buf][2][n][8 * ko]) = (u32x4){p3[0], p3[1], p3[2], p3[3]};
         }
-        if constexpr (INT4) {
+        if constexpr (SCALED) {
             if (tid < TM) {
                 scs[buf][tid] = sreg[P];
-                zzs[buf][tid] = zreg[P];
+                if constexpr (OFF) zzs[buf][tid] = zreg[P];
             }
         }
     };
@@ -983,6 +1024,18 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
                 const uint32_t d = araw4[P][i] ^ 0x88888888u;
                 av[i] = (u32x4){(d & 0x000F000Fu) | 0x43004300u, ((d >> 4) & 0x000F000Fu) | 0x43004300u,
                                 ((d >> 8) & 0x000F000Fu) | 0x43004300u, ((d >> 12) & 0x000F000Fu) | 0x43004300u};
+            } else if constexpr (F == BfFmt::Q4_0) {
+                // elements in order, pairs (2h, 2h + 1) from bytes 2h, 2h + 1 moved to bytes 0 and 2, then
+                // their low or high nibbles as the bf16 128 + u
+                const uint32_t sh = 4u * (uint32_t)(lg >> 1);
+                const uint32_t w2[2] = {araw8[P][i].x, araw8[P][i].y};
+                uint32_t q[4];
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const uint32_t t2 = __builtin_amdgcn_perm(0u, w2[h >> 1], (h & 1) ? 0x0c030c02u : 0x0c010c00u);
+                    q[h] = ((t2 >> sh) & 0x000F000Fu) | 0x43004300u;
+                }
+                av[i] = (u32x4){q[0], q[1], q[2], q[3]};
             } else {
                 const uint32_t w2[2] = {araw8[P][i].x, araw8[P][i].y};
                 uint32_t q[4];
@@ -1001,11 +1054,11 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
             if (t + 1 < nsteps) load_step(Q{}, 32 * (t + 1));
         }
         float4v sc4[TI], zz4[TI];
-        if constexpr (INT4) {
+        if constexpr (SCALED) {
 #pragma unroll
             for (int i = 0; i < TI; i++) {
                 sc4[i] = *reinterpret_cast<const float4v*>(&scs[buf][wm + 16 * i + 4 * lg]);
-                zz4[i] = *reinterpret_cast<const float4v*>(&zzs[buf][wm + 16 * i + 4 * lg]);
+                if constexpr (OFF) zz4[i] = *reinterpret_cast<const float4v*>(&zzs[buf][wm + 16 * i + 4 * lg]);
             }
         }
 #pragma unroll
@@ -1015,7 +1068,7 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
 #pragma unroll
             for (int p = 0; p < 3; p++)
                 bp[p] = __builtin_bit_cast(bf16x8v, *reinterpret_cast<const u32x4*>(&Bs[buf][p][n][8 * lg]));
-            if constexpr (INT4) {
+            if constexpr (OFF) {
                 const bf16x8v ones = __builtin_bit_cast(bf16x8v, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
                 float4v dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[1], dx, 0, 0, 0);
@@ -1029,6 +1082,16 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
 #pragma unroll
                     for (int r = 0; r < 4; r++)
                         acc[i][j][r] = __builtin_fmaf(sc4[i][r], __builtin_fmaf(-zz4[i][r], dx[r], d[r]), acc[i][j][r]);
+                }
+            } else if constexpr (SCALED) {
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const bf16x8v a = __builtin_bit_cast(bf16x8v, av[i]);
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[0], (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[2], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(sc4[i][r], d[r], acc[i][j][r]);
                 }
             } else {
 #pragma unroll
@@ -1065,17 +1128,42 @@ __global__ void __launch_bounds__(256) intq_bf16_kernel(const uint8_t* __restric
         }
 }
 
+template <BfFmt F>
+static void launch_bf16_gemm(hipStream_t st, const uint8_t* A, const float* B, float* C, const void* s,
+                             const uint8_t* z, int M, int N, int K, int gs, int ng) {
+    // 128 x 128 tiles while they give 256 workgroups, else 64 x 64, else 32 x 32 (one 16 x 16 tile a
+    // wave) where fewer than 256 tiles of 64 remain, 192 for the formats with an offset, whose
+    // all-ones MFMAs weigh most in the smallest tiles (us, 64 x 64 against 32 x 32: 4096 x 4096 at
+    // 128 columns, 128 tiles of 64, int4 159.7 / 136.2, int8 106.7 / 94.0; 14336 x 4096 at 32 and 64
+    // columns, 224 tiles of 64, Q8_0 133 / 100 and 136 / 126, Q4_0 at 64 columns 167 / 269)
+    constexpr bool OFF = F == BfFmt::I4 || F == BfFmt::Q4_0;
+    if ((long)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
+        bf16_gemm_kernel<F, 4, 1><<<dim3(ceil_div(N, 128), ceil_div(M, 128)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+    else if ((long)ceil_div(M, 64) * ceil_div(N, 64) < (OFF ? 192 : 256))
+        bf16_gemm_kernel<F, 1, 2><<<dim3(ceil_div(N, 32), ceil_div(M, 32)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+    else
+        bf16_gemm_kernel<F, 2, 2><<<dim3(ceil_div(N, 64), ceil_div(M, 64)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+}
+
+void bf16_gemm_q4_0(hipStream_t st, const uint8_t* data, const uint16_t* scales, const float* B, float* C, int M,
+                    int N, int K) {
+    launch_bf16_gemm<BfFmt::Q4_0>(st, data, B, C, scales, nullptr, M, N, K, 32, K / 32);
+}
+
+void bf16_gemm_q8_0(hipStream_t st, int layout, const uint8_t* data, const void* scales, const float* B, float* C,
+                    int M, int N, int K) {
+    if (layout == 0)
+        launch_bf16_gemm<BfFmt::Q8_RAW>(st, data, B, C, nullptr, nullptr, M, N, K, 32, K / 32);
+    else if (layout == 1)
+        launch_bf16_gemm<BfFmt::Q8_F32>(st, data, B, C, scales, nullptr, M, N, K, 32, K / 32);
+    else
+        launch_bf16_gemm<BfFmt::Q8_F16>(st, data, B, C, scales, nullptr, M, N, K, 32, K / 32);
+}
+
 template <bool INT4>
 static void launch_intq_bf16(hipStream_t st, const uint8_t* A, const float* B, float* C, const float* s,
                              const uint8_t* z, int M, int N, int K, int gs, int ng) {
-    // 128 x 128 tiles while they give 256 workgroups, else 64 x 64, else (fewer than 256 of those)
-    // 32 x 32: 4096 x 4096 at 128 columns 159.7 -> 136.2 us (int4), 106.7 -> 94.0 (int8)
-    if ((long)ceil_div(M, 128) * ceil_div(N, 128) >= 256)
-        intq_bf16_kernel<INT4, 4, 1><<<dim3(ceil_div(N, 128), ceil_div(M, 128)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
-    else if ((long)ceil_div(M, 64) * ceil_div(N, 64) < 256)
-        intq_bf16_kernel<INT4, 1, 2><<<dim3(ceil_div(N, 32), ceil_div(M, 32)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
-    else
-        intq_bf16_kernel<INT4, 2, 2><<<dim3(ceil_div(N, 64), ceil_div(M, 64)), 256, 0, st>>>(A, B, C, s, z, M, N, K, gs, ng);
+    launch_bf16_gemm<INT4 ? BfFmt::I4 : BfFmt::I8>(st, A, B, C, s, z, M, N, K, gs, ng);
 }
 
 template <int V>

@@ -31,6 +31,7 @@
 // row-block MFMA GEMM further down (12 and 16 past 2048 rows the 16x16x32
 // MFMA GEMM); other batched calls (N > 1, column-strided activations) use
 // the block-per-lane kernel with one grid row per column.
+#include "zt_bf16gemm.h"
 #include "zt_rbmfma.h"
 
 namespace zt {
@@ -1304,6 +1305,15 @@ static int gemm_blk18(const void* A, const XT* B, float* C, int M, int K, int N,
         }
     }
     if constexpr (F == Fmt::Q4_0 && sizeof(XT) == 4) {
+        // 128 columns and more (prefill widths): the bf16 MFMA tile GEMM of zt_intq.hip, where the
+        // row-block GEMM's launches of 8 columns each would re-run its per-column work (us, row-block
+        // against tile GEMM, 4096 x 4096 / 14336 x 4096 / 4096 x 14336 rows x K: 64 columns 68.7 /
+        // 160 / 360 against 106 / 269 / 402; 128 columns 136 / 321 / 715 against 127 / 185 / 465;
+        // 512 columns 560 / 1283 / 2841 against 182 / 309 / 640)
+        if (N >= 128 && N % 2 == 0 && ((uintptr_t)B & 7) == 0 && (long)ceil_div(M, 32) <= 65535) {
+            bf16_gemm_q4_0(st, data, sc, reinterpret_cast<const float*>(B), C, M, N, K);
+            return (int)hipGetLastError();
+        }
         if (rbf_ok<RbFmt::Q4_0>(N, kb, M, B)) {
             launch_rbf<RbFmt::Q4_0>(sc, data, B, C, M, kb, N, st);
             return (int)hipGetLastError();

@@ -20,6 +20,7 @@
 // column per grid row, split-K across the waves of a workgroup.  Decode: q XOR 0x80 is q+128 as an unsigned byte,
 // which v_cvt_f32_ubyte converts directly; sum (q+128) x - 128 sum x
 // recovers the signed dot product.
+#include "zt_bf16gemm.h"
 #include "zt_common.h"
 #include "zt_rbmfma.h"
 
@@ -342,6 +343,17 @@ static int gemm_q8(const void* A, const float* B, float* C, int M, int K, int N,
         const int nw = min(8, ceil_div(kb, 16));
         const int R = pick_rows_per_wave(M, nw, 1, 2048);
         launch_q8_quad<L>(R, dim3(ceil_div(M, R)), dim3(nw * kWave), st, base, data_offset, B, C, M, kb);
+        return (int)hipGetLastError();
+    }
+    // Wide batches (prefill widths): the bf16 MFMA tile GEMM of zt_intq.hip from 128 columns, from 32
+    // at 8192 rows and more, from 64 past K = 8192 (us, separated layout, row-block against tile
+    // GEMM, 4096 x 4096 / 14336 x 4096 / 4096 x 14336 rows x K: 32 columns 43 / 147 / 189 against
+    // 88 / 100 / 310; 64 columns 86 / 292 / 380 against 90 / 126 / 312; 128 columns 173 / 589 / 760
+    // against 99 / 161 / 344; 512 columns 695 / 2333 / 3039 against 154 / 256 / 520; the raw blocks
+    // alike)
+    const bool wide = N >= 128 || (N >= 32 && M >= 8192) || (N >= 64 && K > 8192);
+    if (wide && N % 2 == 0 && ((uintptr_t)B & 7) == 0 && (long)ceil_div(M, 32) <= 65535) {
+        bf16_gemm_q8_0(st, L, L == kRaw36 ? base : base + data_offset, base, B, C, M, N, K);
         return (int)hipGetLastError();
     }
     // N = 4, 8, 12, ...: the row-block MFMA GEMM, every weight read once per

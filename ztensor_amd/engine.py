@@ -423,7 +423,9 @@ class ROCmEngine:
         n = 1 if x.dim() == 1 else x.shape[1]
         if x.device != self.device:
             raise ValueError("activations must be on the engine's device")
-        if n > 1 and n not in _TILED_BATCHES and self._tiled_ok(s, rows, k, x):
+        wide = ((isinstance(s, Q4Storage) and x.dtype in (torch.float32, torch.float16) and _block_wide("q4", rows, k, n))
+                or (isinstance(s, Q8Storage) and x.dtype == torch.float32 and _block_wide("q8", rows, k, n)))
+        if n > 1 and n not in _TILED_BATCHES and not wide and self._tiled_ok(s, rows, k, x):
             # other batch sizes on the tiled MFMA kernels: columns in chunks of
             # 16, the last one zero-padded to a multiple of 4
             xs = x.reshape(k, n)
@@ -441,7 +443,12 @@ class ROCmEngine:
         if isinstance(s, MmapStorage):
             return self._mmap_times(s, buf, rows, k, x, n, c)
         if isinstance(s, Q4Storage):
-            if x.dtype in (torch.float32, torch.float16) and _block_rowblock("q4", rows, k, n):
+            if wide:
+                # the bf16 MFMA tile GEMM behind the entry point (fp16 activations widen exactly)
+                x = x.float() if x.dtype == torch.float16 else x
+                x = x if _p(x) % 8 == 0 else x.clone()
+                self.gemm_q4_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+            elif x.dtype in (torch.float32, torch.float16) and _block_rowblock("q4", rows, k, n):
                 # one launch on the separated upload (the row-block GEMM): no tiled copy, no workspace
                 x = x.float() if x.dtype == torch.float16 else x
                 x = x if _p(x) % 16 == 0 else x.clone()
@@ -479,6 +486,11 @@ class ROCmEngine:
         elif isinstance(s, Q8Storage):
             if x.dtype != torch.float32:
                 raise TypeError("Q8_0 matmul takes fp32 activations")
+            if wide:
+                # the bf16 MFMA tile GEMM behind the entry point
+                x = x if _p(x) % 8 == 0 else x.clone()
+                self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
+                return c
             if _block_rowblock("q8", rows, k, n) and _p(x) % 16 == 0:
                 # one launch on the separated upload (the row-block GEMM)
                 self.gemm_q8sep_f32(_p(buf.tensor), _p(x), _p(c), rows, k, n, buf.data_offset)
@@ -788,6 +800,21 @@ def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
     if n in (12, 16):
         return k <= 8192 and rows <= 4096
     return k <= 4096 or rows <= 2048
+
+
+def _block_wide(fmt: str, rows: int, k: int, n: int) -> bool:
+    """Whether zt_gemm_q4_f32 / zt_gemm_q8sep_f32 run a batch of n fp32
+    columns (even n, 8-byte aligned) on the bf16 MFMA tile GEMM: from 128
+    columns, and for Q8_0 also from 32 at 8192 rows and more and from 64
+    past K = 8192 (the rules of zt_q4.hip and zt_q8.hip).  Such batches go
+    to the entry point as they are, with no tiled copy and no 16-column
+    chunks: 512 columns of 14336 x 4096 (rows x K) take 309 us (Q4_0) and
+    256 us (Q8_0) on it."""
+    if n % 2:
+        return False
+    if fmt == "q4":
+        return n >= 128
+    return n >= 128 or (n >= 32 and rows >= 8192) or (n >= 64 and k > 8192)
 
 
 _TILED_BATCHES = (4, 8, 12, 16)  # batch sizes on the tiled layouts (W4A16, IQ4_NL, Q4_0, Q8_0, Q4_K, Q5_K, Q5_0)
