@@ -380,10 +380,13 @@ int zt_gemm_q4t_f32(const void* W_tiled, const void* S_tiled, const float* B, fl
  * forbid allocation).  The K-split partials go to a static device array of
  * ZT_NOALLOC_SCRATCH_BYTES that every GPU holds one copy of from the first
  * call on it until the process ends; C is bit-identical to
- * zt_gemm_q4t_f32's.  A call that needs more scratch than that
+ * zt_gemm_q4t_f32's.  A call whose partials exceed the array
  * (zt_gemm_q4t_workspace_bytes(M, K, N) > ZT_NOALLOC_SCRATCH_BYTES, e.g. the
- * 28672 x 8192 matrices of Llama-3-70B) returns hipErrorOutOfMemory (2)
- * without launching; other argument errors return InvalidValue as
+ * 28672 x 8192 matrices of Llama-3-70B) runs as slices of whole 128-row
+ * groups, one after another on the stream, each with the whole call's K
+ * split, so C is still bit-identical; only a call whose single 128-row slice
+ * needs more (K > 2^19 at 128 or more rows) returns hipErrorOutOfMemory (2)
+ * without launching.  Other argument errors return InvalidValue as
  * zt_gemm_q4t_f32 does.  Calls on one GPU share the array: calls that
  * overlap on one GPU (on different streams) race, calls on one stream do
  * not.  The current device must be the stream's device. */

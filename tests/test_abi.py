@@ -280,12 +280,15 @@ def test_q4_group_rejects_bad_arguments_without_launching():
 
 def test_q4t_noalloc_rejects_oversized_and_bad_calls_without_launching():
     """zt_gemm_q4t_f32_noalloc checks the scratch size and the shape before
-    touching the GPU: a call needing more than ZT_NOALLOC_SCRATCH_BYTES of
-    K-split scratch returns hipErrorOutOfMemory, a bad shape InvalidValue."""
+    touching the GPU: a call whose partials exceed ZT_NOALLOC_SCRATCH_BYTES
+    runs in row slices, so only one whose single 128-row slice needs more
+    (K past 2^19: 2048 splits x 8 tiles x 1 KB = 16 MiB) returns
+    hipErrorOutOfMemory; a bad shape returns InvalidValue."""
     lib = _lib.load()
-    assert lib.zt_gemm_q4t_workspace_bytes(28672, 8192, 8) > _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.zt_gemm_q4t_workspace_bytes(28672, 8192, 8) > _lib.NOALLOC_SCRATCH_BYTES  # sliced, not refused
     p = 0x10000
-    assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 28672, 8192, 8, None) == _lib.HIP_ERROR_OUT_OF_MEMORY
+    assert lib.zt_gemm_q4t_workspace_bytes(128, 1 << 20, 8) == 16 << 20
+    assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 128, 1 << 20, 8, None) == _lib.HIP_ERROR_OUT_OF_MEMORY
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 64, 96, 8, None) == _lib.HIP_ERROR_INVALID_VALUE  # K % 128
     assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 64, 128, 5, None) == _lib.HIP_ERROR_INVALID_VALUE  # N
 

@@ -86,4 +86,44 @@ def test_noalloc_unsplit_call_and_oversized_request(lib, orc):
     ref = orc.gemm_f32_q4_nt(xt, w.raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
     assert rel_err(c.cpu().numpy().reshape(rows, N), ref) <= 1e-5
     p = wt.data_ptr()
-    assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 28672, 8192, 8, s) == _lib.HIP_ERROR_OUT_OF_MEMORY
+    assert lib.zt_gemm_q4t_f32_noalloc(p, p, p, p, 128, 1 << 20, 8, s) == _lib.HIP_ERROR_OUT_OF_MEMORY
+
+
+@pytest.mark.parametrize("rows,K,N", [(28672, 8192, 8), (8200, 28672, 4)])
+def test_noalloc_past_the_scratch_runs_in_row_slices(lib, orc, rows, K, N):
+    """Partials larger than the scratch (29 MB and 16 MB here): the call runs
+    in slices of whole 128-row workgroup rows with the full call's K split,
+    bit-identical to the workspace entry point, then a small call reuses the
+    scratch as before.  8200 rows end in a partial slice and a partial tile."""
+    s = torch.cuda.current_stream().cuda_stream
+    need = lib.zt_gemm_q4t_workspace_bytes(rows, K, N)
+    print(f"noalloc sliced rows={rows} K={K} N={N} partials={need}", flush=True)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    w, wt, st = tiled(lib, rows, K, 104)
+    x = synth.x_f32(K * N, 104)
+    xd = torch.from_numpy(x).cuda()
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    c_ws = torch.empty(rows * N, dtype=torch.float32, device="cuda")
+    c_na = torch.full((rows * N,), float("nan"), dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_q4t_f32", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c_ws.data_ptr(), rows, K, N,
+             ws.data_ptr(), need, s)
+    lib.call("zt_gemm_q4t_f32_noalloc", wt.data_ptr(), st.data_ptr(), xd.data_ptr(), c_na.data_ptr(), rows, K, N, s)
+    torch.cuda.synchronize()
+    a, b = c_ws.cpu().numpy(), c_na.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    xt = np.ascontiguousarray(x.reshape(K, N).T)
+    ref = orc.gemm_f32_q4_nt(xt, w.raw, N, rows, K, threads=orc.nthreads()).reshape(N, rows).T
+    assert rel_err(b.reshape(rows, N), ref) <= 1e-5
+    # a smaller call after it, on the scratch the sliced call left filled
+    rows2, K2 = 1024, 2048
+    w2, wt2, st2 = tiled(lib, rows2, K2, 105)
+    x2 = torch.from_numpy(synth.x_f32(K2 * 4, 105)).cuda()
+    need2 = lib.zt_gemm_q4t_workspace_bytes(rows2, K2, 4)
+    ws2 = torch.empty(max(need2, 16), dtype=torch.uint8, device="cuda")
+    c1 = torch.empty(rows2 * 4, dtype=torch.float32, device="cuda")
+    c2 = torch.empty(rows2 * 4, dtype=torch.float32, device="cuda")
+    lib.call("zt_gemm_q4t_f32", wt2.data_ptr(), st2.data_ptr(), x2.data_ptr(), c1.data_ptr(), rows2, K2, 4,
+             ws2.data_ptr(), need2, s)
+    lib.call("zt_gemm_q4t_f32_noalloc", wt2.data_ptr(), st2.data_ptr(), x2.data_ptr(), c2.data_ptr(), rows2, K2, 4, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(c1.cpu().numpy().view(np.uint32), c2.cpu().numpy().view(np.uint32))

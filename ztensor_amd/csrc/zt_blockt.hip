@@ -62,6 +62,7 @@
 //    half of the A and B operands, with its own offset MFMA and scale (an
 //    earlier form zeroed the other group's lane groups in two copies of B
 //    for 16x16x32 MFMAs: 3.5-8% slower).
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -648,7 +649,7 @@ static long blkt_ws_bytes(int M, int K, int N) {
 
 template <BlkFmt F>
 static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, float* C, int M, int K, int N,
-                     void* ws, long ws_bytes, hipStream_t stream, const void* aux = nullptr) {
+                     void* ws, long ws_bytes, hipStream_t stream, const void* aux = nullptr, int force_upw = 0) {
     constexpr int KQ = (F == BlkFmt::Q4_K || F == BlkFmt::Q5_K || F == BlkFmt::Q6_K) ? 256 : 128;  // K-quants: whole super-blocks
     if (M < 0 || K < 0 || K % KQ != 0) return (int)hipErrorInvalidValue;
     if (N != 4 && N != 8 && N != 12 && N != 16) return (int)hipErrorInvalidValue;
@@ -661,7 +662,11 @@ static int gemm_blkt(const void* W_tiled, const void* S_tiled, const float* B, f
     constexpr long SB = F == BlkFmt::Q8_0 ? 4 : F == BlkFmt::Q6_K ? 8 : 2;  // global scale bytes per (row, block); Q4_K: 16 per 8 blocks
     if ((long)((M + 15) / 16) * (K / 128) * 64 * SB >= 0x7fffffffL) return (int)hipErrorInvalidValue;  // 32-bit scale offsets
     int upw;
-    const dim3 g = blkt_grid<F>(M, K, upw);
+    dim3 g = blkt_grid<F>(M, K, upw);
+    if (force_upw == 2 || force_upw == 4) {  // a row slice of a larger call: that call's K split
+        upw = force_upw;
+        g.y = ceil_div(K / 128, upw);
+    }
     const long need = tiled_ws_bytes(M, (int)g.y);
     if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 15))) return (int)hipErrorInvalidValue;
     const uint4* wt = static_cast<const uint4*>(W_tiled);
@@ -746,13 +751,39 @@ ZT_EXPORT int zt_gemm_q4t_f32_noalloc(const void* W_tiled, const void* S_tiled, 
                                       int N, hipStream_t stream) {
     const long need = blkt_ws_bytes<BlkFmt::Q4_0>(M, K, N);
     if (need < 0) return (int)hipErrorInvalidValue;
-    if (need > ZT_NOALLOC_SCRATCH_BYTES) return (int)hipErrorOutOfMemory;
+    if (need <= ZT_NOALLOC_SCRATCH_BYTES) {
+        void* ws = nullptr;
+        if (need > 0) {
+            const int rc = scratch_on_current_device(&ws);
+            if (rc != 0) return rc;
+        }
+        return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, ws, need, stream);
+    }
+    // Partials past the scratch: run the call as slices of whole 128-row
+    // workgroup rows, each with the full call's K split, one after another on
+    // the stream, so every output is the workspace entry point's to the bit.
+    // A slice's tiles are contiguous in both tiled arrays (tile (rt, u) at
+    // (rt * K/128 + u) * 1024 data bytes and * 128 scale bytes).
+    int upw;
+    const int splits = (int)blkt_grid<BlkFmt::Q4_0>(M, K, upw).y;
+    const long per_group = tiled_ws_bytes(128, splits);  // 8 row tiles
+    const long groups = ZT_NOALLOC_SCRATCH_BYTES / per_group;
+    if (groups < 1) return (int)hipErrorOutOfMemory;
+    if (W_tiled == nullptr || S_tiled == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     void* ws = nullptr;
-    if (need > 0) {
-        const int rc = scratch_on_current_device(&ws);
+    const int rc0 = scratch_on_current_device(&ws);
+    if (rc0 != 0) return rc0;
+    const long slice = groups * 128, units = K / 128;
+    for (long r0 = 0; r0 < M; r0 += slice) {
+        const int rows = (int)std::min<long>(slice, M - r0);
+        const long rt0 = r0 / 16;
+        const int rc = gemm_blkt<BlkFmt::Q4_0>(static_cast<const uint8_t*>(W_tiled) + rt0 * units * 1024,
+                                               static_cast<const uint8_t*>(S_tiled) + rt0 * units * 128, B,
+                                               C + r0 * N, rows, K, N, ws, ZT_NOALLOC_SCRATCH_BYTES, stream, nullptr,
+                                               upw);
         if (rc != 0) return rc;
     }
-    return gemm_blkt<BlkFmt::Q4_0>(W_tiled, S_tiled, B, C, M, K, N, ws, need, stream);
+    return (int)hipSuccess;
 }
 
 ZT_EXPORT long zt_q8_tiled_bytes(int M, int K) {
