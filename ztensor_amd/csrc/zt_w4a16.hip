@@ -1264,15 +1264,20 @@ static void launch_w4t_n(int upw, int nch, dim3 g, hipStream_t st, const uint4* 
         launch_w4t<2, N>(g, st, wt, sz, x, y, ws, M, K, gs, nch);
 }
 
-// Grid of the tiled W4A16 GEMM: 128 rows a workgroup, and the largest K range
-// (up to 8 units) that still gives >= 256 workgroups.  K ranges are split
+// Grid of the tiled W4A16 GEMM: 128 rows a workgroup, and a K range of 8, 4
+// or 2 units (the rule below).  K ranges are split
 // across blockIdx.y; when that leaves more than 8 splits, each workgroup
 // walks nch chunks of upw units in turn, as long as >= 256 workgroups
 // remain, so fewer partial tiles go through the workspace.
 static dim3 w4t_grid(int M, int K, int& upw, int& nch) {
     const int nunits = K / 128;
     const int gx = ceil_div(M, 128);
-    upw = 8;
+    // 8 units a workgroup only while that still gives >= 1024 workgroups: 4
+    // units measured faster below that (batch 8, us, 8 units against 4:
+    // 8192 x 8192 12.35 / 11.13, 14336 x 4096 12.82 / 11.36, 4096 x 14336
+    // rows x K 11.48 / 10.87); then down to 2 while < 256 workgroups (4096 x
+    // 4096 keeps 4: 6.84 against 7.45 us with 2)
+    upw = (long)gx * ceil_div(nunits, 8) >= 1024 ? 8 : 4;
     while (upw > 2 && (long)gx * ceil_div(nunits, upw) < 256) upw >>= 1;
     // (28672 x 8192, batch 16: 33.2 us with 28 splits, 31.6 with 2 chunks, 30.2 with 4)
     nch = 1;

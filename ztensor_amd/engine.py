@@ -785,12 +785,13 @@ def _w4a16_rowblock(rows: int, k: int, n: int) -> bool:
     """Whether a batch of 4-16 W4A16 columns runs faster on the single-launch
     row-block GEMM over the row-major upload (zt_gemm_w4a16sz_f32) than on the
     tiled layout with its split-K reduction.  Measured (us, row-block against
-    tiled): batch 4 at 8192 x 8192 10.1 / 12.2, 4096 x 14336 (rows x K)
-    10.0 / 11.3, 8192 x 28672 37.1 / 29.7; batch 8 at 14336 x 4096
-    11.8 / 12.8, 4096 x 4096 4.9 / 6.8, 1024 x 8192 4.1 / 6.0, 8192 x 8192
-    13.2 / 12.5, 4096 x 14336 12.3 / 11.6, 28672 x 8192 37.7 / 29.0; batch
-    16 at 1024 x 8192 5.98 / 6.22, 4096 x 4096 6.4 / 7.0, 8192 x 8192
-    20.4 / 12.9, 14336 x 4096 20.6 / 13.7.  A row-block workgroup re-reads
+    tiled): batch 4 at 8192 x 8192 10.1 / 11.2, 4096 x 14336 (rows x K)
+    10.0 / 10.7, 14336 x 4096 10.8 / 11.0, 8192 x 28672 37.1 / 29.7; batch
+    8 at 14336 x 4096 11.8 / 11.4, 4096 x 4096 4.9 / 6.8, 1024 x 8192
+    4.1 / 6.0, 8192 x 8192 13.2 / 11.1, 4096 x 14336 12.3 / 10.9, 28672 x
+    8192 37.7 / 29.0; batch 16 at 1024 x 8192 5.98 / 6.22, 4096 x 4096
+    6.4 / 7.1, 8192 x 8192 20.4 / 11.8, 14336 x 4096 20.6 / 12.6.
+    A row-block workgroup re-reads
     more activation bytes than weight bytes once the rows are many and K is
     long, more so at 12 and 16 columns."""
     if k > 32768:
